@@ -1,0 +1,91 @@
+"""ctypes binding of ``libmpq_amd.so`` (the C-ABI in ``include/mpq_amd.h``).
+
+The library is loaded from the package directory only.  There is no CPU or
+PyTorch fallback: if the library is missing or a call fails, the caller gets an
+exception.  Pointers are raw device addresses (``tensor.data_ptr()``); every
+call is asynchronous on the given HIP stream (default: torch's current stream).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmpq_amd.so")
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+c_i64 = ctypes.c_int64
+c_int = ctypes.c_int
+c_float = ctypes.c_float
+c_double = ctypes.c_double
+c_ptr = ctypes.c_void_p
+
+# name -> (restype, argtypes); every entry point returns an int status.
+SIGNATURES = {
+    "mpq_last_error": (ctypes.c_char_p, []),
+    "mpq_last_error_code": (c_int, []),
+    "mpq_clear_error": (None, []),
+    "mpq_e8p12_map": (c_int, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_float,
+                              c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+}
+
+
+class MPQLibraryError(RuntimeError):
+    """Raised when the HIP library is missing or a C-ABI call reports an error."""
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise MPQLibraryError(
+                f"mpq_amd HIP library not found at {LIB_PATH}; build it with "
+                "`python -m mpq_amd.build` (or __graft_entry__.build())."
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+        return lib
+
+
+def exported_symbols() -> list:
+    return sorted(SIGNATURES)
+
+
+def check(status: int, name: str) -> None:
+    if status != 0:
+        lib = load()
+        msg = lib.mpq_last_error()
+        text = msg.decode("utf-8", "replace") if msg else ""
+        if status == -1:
+            raise ValueError(f"{name}: {text}")
+        raise MPQLibraryError(f"{name} failed (status {status}): {text}")
+
+
+def call(name: str, *args) -> None:
+    fn = getattr(load(), name)
+    check(fn(*args), name)
+
+
+def ptr(t) -> Optional[int]:
+    """Device pointer of a tensor, or None (NULL) for None."""
+    if t is None:
+        return None
+    return int(t.data_ptr())
+
+
+def stream_handle(device=None) -> int:
+    import torch
+
+    return int(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,162 @@
+"""E8P12 lattice prior: MAP search and posterior on the HIP kernels.
+
+Drop-in for ``mpq/priors/e8p12.py``:
+
+* ``vamp_vector_map_e8p12``  -> ``mpq_e8p12_map``  (reference ``:541-631``)
+* ``e8p12_nearest``          -> ``mpq_e8p12_map`` with unit precision, no prior
+  (the codebook's exact nearest-codeword quantizer)
+* ``prior_scale_from_center``  (reference ``:45-61``)
+
+Tensors must live on a ROCm device; there is no CPU path in the product.
+"""
+from __future__ import annotations
+
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from .. import _lib
+
+
+def _require_device(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be on a ROCm device (got {t.device}); mpq_amd has no CPU path.")
+
+
+@torch.inference_mode()
+def prior_scale_from_center(prior_center_blocks: Optional[torch.Tensor], mode: str) -> Optional[torch.Tensor]:
+    """Per-block prior scale (reference ``mpq/priors/e8p12.py:45-61``)."""
+    if prior_center_blocks is None:
+        return None
+    mode = str(mode or "absmax").strip().lower()
+    if mode in ("none", "unit", "legacy"):
+        shape = prior_center_blocks.shape[:-1] + (1,)
+        return torch.ones(shape, dtype=torch.float32, device=prior_center_blocks.device)
+    if mode in ("absmax", "exact_full", "exact_full_absmax"):
+        scale = prior_center_blocks.abs().amax(dim=-1, keepdim=True)
+    elif mode in ("rms", "std"):
+        scale = prior_center_blocks.square().mean(dim=-1, keepdim=True).sqrt()
+    elif mode in ("mean_abs", "l1"):
+        scale = prior_center_blocks.abs().mean(dim=-1, keepdim=True)
+    else:
+        raise ValueError(f"unsupported prior_tau_scale_mode={mode!r}; supported: none|absmax|rms|mean_abs")
+    return scale.to(dtype=torch.float32).clamp_min_(1e-12)
+
+
+@torch.inference_mode()
+def e8p12_map_flat(
+    r: torch.Tensor,  # (N, 8) fp32
+    gamma: torch.Tensor,  # (N // gamma_div,) fp32
+    *,
+    gamma_div: int = 1,
+    center: Optional[torch.Tensor] = None,  # (N, 8)
+    scale: Optional[torch.Tensor] = None,  # (N,) or None for in-kernel absmax
+    tau: float = 0.0,
+    want_idx64: bool = True,
+    want_idx16: bool = False,
+    want_vals: bool = False,
+    want_err: bool = False,
+    want_score: bool = False,
+) -> Dict[str, torch.Tensor]:
+    """Low-level launcher of ``mpq_e8p12_map`` on flat (N, 8) blocks."""
+    _require_device(r, "r")
+    if r.dim() != 2 or int(r.shape[1]) != 8:
+        raise ValueError(f"expected r with shape (N, 8), got {tuple(r.shape)}")
+    r = r.to(dtype=torch.float32).contiguous()
+    n = int(r.shape[0])
+    gamma = gamma.to(device=r.device, dtype=torch.float32).contiguous().reshape(-1)
+    if n and int(gamma.numel()) * int(gamma_div) < n:
+        raise ValueError(f"gamma has {gamma.numel()} entries for {n} vectors with gamma_div={gamma_div}")
+    use_prior = center is not None and float(tau) > 0.0
+    if use_prior:
+        center = center.to(device=r.device, dtype=torch.float32).contiguous()
+        if tuple(center.shape) != tuple(r.shape):
+            raise ValueError("prior center must match r in shape")
+        if scale is not None:
+            scale = scale.to(device=r.device, dtype=torch.float32).contiguous().reshape(-1)
+            if int(scale.numel()) != n:
+                raise ValueError("prior scale must have one entry per vector")
+    else:
+        center = None
+        scale = None
+    out: Dict[str, torch.Tensor] = {}
+    dev = r.device
+    if want_idx64:
+        out["idx"] = torch.empty(n, dtype=torch.int64, device=dev)
+    if want_idx16:
+        out["idx16"] = torch.empty(n, dtype=torch.uint16, device=dev)
+    if want_vals:
+        out["vals"] = torch.empty(n, 8, dtype=torch.float32, device=dev)
+    if want_err:
+        out["err"] = torch.empty(n, dtype=torch.float32, device=dev)
+    if want_score:
+        out["score"] = torch.empty(n, dtype=torch.float32, device=dev)
+    if n == 0:
+        return out
+    _lib.call(
+        "mpq_e8p12_map",
+        _lib.ptr(r), n, _lib.ptr(gamma), int(gamma_div),
+        _lib.ptr(center), _lib.ptr(scale), float(tau) if use_prior else 0.0,
+        _lib.ptr(out.get("idx")), _lib.ptr(out.get("idx16")), _lib.ptr(out.get("vals")),
+        _lib.ptr(out.get("err")), _lib.ptr(out.get("score")),
+        _lib.stream_handle(dev),
+    )
+    return out
+
+
+@torch.inference_mode()
+def e8p12_nearest(x: torch.Tensor, *, return_vals: bool = False) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Exact nearest E8P12 codeword of each row of ``x`` (N, 8); first index on ties."""
+    _require_device(x, "x")
+    one = torch.ones(1, dtype=torch.float32, device=x.device)
+    out = e8p12_map_flat(x, one, gamma_div=max(int(x.shape[0]), 1), want_vals=return_vals)
+    return out["idx"], out.get("vals")
+
+
+@torch.inference_mode()
+def vamp_vector_map_e8p12(
+    *,
+    r1_blocks: torch.Tensor,  # (B, n_blocks, 8)
+    gamma1: torch.Tensor,  # (B, 1)
+    cb: object,
+    blocks_per_chunk: int = 64,
+    need_stats: bool = False,
+    prior_center_blocks: Optional[torch.Tensor] = None,
+    prior_scale_blocks: Optional[torch.Tensor] = None,
+    prior_tau: float = 0.0,
+    prior_tau_scale_mode: str = "absmax",
+) -> Dict[str, torch.Tensor | float]:
+    """Factorized E8P12 MAP per 8-block (reference ``mpq/priors/e8p12.py:541-631``).
+
+    ``blocks_per_chunk`` is accepted for signature compatibility; the kernel has
+    no chunking.  ``need_stats`` (margin diagnostics) is not provided by the HIP
+    backend and raises, as the reference's Triton backend does for diagnostics
+    (``mpq/priors/uniform.py:119-120``).
+    """
+    del blocks_per_chunk, cb
+    if need_stats:
+        raise ValueError("HIP E8P12 MAP backend does not support posterior diagnostics (need_stats=True).")
+    batch, n_blocks, codesz = r1_blocks.shape
+    if int(codesz) != 8:
+        raise ValueError(f"E8P12 MAP expects codesz=8, got {codesz}.")
+    if gamma1.ndim != 2 or int(gamma1.shape[-1]) != 1 or int(gamma1.shape[0]) != int(batch):
+        raise ValueError(f"expected scalar gamma1 with shape (B,1), got {tuple(gamma1.shape)}")
+    center = None
+    scale = None
+    tau = 0.0
+    if float(prior_tau) > 0.0 and prior_center_blocks is not None:
+        center = prior_center_blocks.reshape(-1, 8)
+        tau = float(prior_tau)
+        mode = str(prior_tau_scale_mode or "absmax").strip().lower()
+        if prior_scale_blocks is not None:
+            scale = prior_scale_blocks.reshape(-1)
+        elif mode not in ("absmax", "exact_full", "exact_full_absmax"):
+            scale = prior_scale_from_center(prior_center_blocks, mode).reshape(-1)
+    out = e8p12_map_flat(
+        r1_blocks.reshape(-1, 8), gamma1.reshape(-1), gamma_div=max(int(n_blocks), 1),
+        center=center, scale=scale, tau=tau, want_vals=True,
+    )
+    return {
+        "map_idxs": out["idx"].view(batch, n_blocks),
+        "map_vals": out["vals"].view(batch, n_blocks, 8).to(dtype=r1_blocks.dtype),
+    }

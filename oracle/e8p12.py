@@ -1,0 +1,262 @@
+"""ORACLE (test infrastructure only) — E8P12 prior restated on the CPU.
+
+* ``factor_cache``        follows mpq/priors/e8p12.py:83-151 (get_e8p12_factor_cache),
+                          including its structural invariants (:121-130).
+* ``map_search``          wraps the C restatement oracle/e8p12_map.c of
+                          mpq/priors/e8p12.py:367-449 + :541-631.
+* ``bruteforce_nearest``  exhaustive fp64 search over all 65536 codewords (the
+                          mathematical definition the factorized search must equal).
+* ``posterior``           follows mpq/priors/e8p12.py:154-308 + :815-968
+                          (vamp_vector_discrete_mmse_e8p12) with torch CPU ops in the
+                          reference's order.
+* ``posterior_bruteforce``  fp64 softmax over all 65536 codewords (pins ``posterior``).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from typing import Dict, Optional
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(HERE, "liboracle.so")
+_lib = None
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            import subprocess
+
+            subprocess.run(["make", "-C", HERE, "-s"], check=True)
+        lib = ctypes.CDLL(_LIB_PATH)
+        p = ctypes.c_void_p
+        lib.oracle_e8p12_map.argtypes = [p, ctypes.c_int64, p, ctypes.c_int64, p, p, ctypes.c_float,
+                                         p, p, p, p, p, p]
+        lib.oracle_e8p12_map.restype = None
+        lib.oracle_e8p12_sqerr.argtypes = [p, p, ctypes.c_int64, p, p]
+        lib.oracle_e8p12_bruteforce.argtypes = [p, ctypes.c_int64, p, p, p]
+        _lib = lib
+    return _lib
+
+
+def _sign_parity(ids: torch.Tensor) -> torch.Tensor:
+    bits = (ids.unsqueeze(-1) >> torch.arange(8)) & 1
+    return bits.sum(dim=-1) & 1
+
+
+def factor_cache(grid: torch.Tensor) -> Dict[str, torch.Tensor]:
+    """Factor tables of a 65536x8 grid; mpq/priors/e8p12.py:83-151."""
+    grid = grid.to(dtype=torch.float32, device="cpu")
+    if tuple(grid.shape) != (65536, 8):
+        raise ValueError("expected a 65536x8 grid")
+    seed = torch.arange(256, dtype=torch.long) << 8
+    template = grid.index_select(0, seed) - 0.25
+    base_parity = ((template < 0).long().sum(dim=-1) & 1)
+    base_abs = template.abs()
+    base_sqnorm = base_abs.square().sum(dim=-1)
+    full = torch.arange(65536, dtype=torch.long)
+    abs_idx = full >> 8
+    branch = _sign_parity(full & 255)
+    offsets = torch.tensor([0.25, -0.25], dtype=torch.float32)
+    residual = grid - offsets.index_select(0, branch).unsqueeze(-1)
+    sign_id = ((residual < 0).long() * (1 << torch.arange(8))).sum(dim=-1)
+    lut = torch.full((2, 256, 256), -1, dtype=torch.long)
+    lut[branch, abs_idx, sign_id] = full
+    if not torch.allclose(residual.abs(), base_abs.index_select(0, abs_idx), atol=1e-6, rtol=1e-6):
+        raise RuntimeError("grid does not factor into 256 abs patterns")
+    valid = _sign_parity(torch.arange(256)).view(1, 1, -1) == base_parity.view(1, 256, 1)
+    if not torch.all(lut[valid.expand(2, -1, -1)] >= 0):
+        raise RuntimeError("missing valid sign entries")
+    if not torch.all(lut[~valid.expand(2, -1, -1)] < 0):
+        raise RuntimeError("unexpected invalid sign entries")
+    return {
+        "base_abs": base_abs.contiguous(),
+        "base_sqnorm": base_sqnorm.contiguous(),
+        "base_parity": base_parity.to(torch.int32).contiguous(),
+        "idx_lut": lut.contiguous(),
+        "branch_offsets": offsets,
+    }
+
+
+def map_search(r: np.ndarray, gamma: np.ndarray, gamma_div: int, cache: Dict[str, torch.Tensor],
+               center: Optional[np.ndarray] = None, scale: Optional[np.ndarray] = None,
+               tau: float = 0.0):
+    """(idx int64, best score fp32) of the factorized MAP; oracle/e8p12_map.c."""
+    lib = _load()
+    r = np.ascontiguousarray(r, dtype=np.float32).reshape(-1, 8)
+    n = r.shape[0]
+    gamma = np.ascontiguousarray(gamma, dtype=np.float32).reshape(-1)
+    idx = np.empty(n, dtype=np.int64)
+    score = np.empty(n, dtype=np.float32)
+    babs = cache["base_abs"].numpy()
+    bsq = cache["base_sqnorm"].numpy()
+    bpar = cache["base_parity"].numpy()
+    lut = cache["idx_lut"].numpy()
+    c_arr = s_arr = None
+    if center is not None and tau > 0.0:
+        c_arr = np.ascontiguousarray(center, dtype=np.float32).reshape(-1, 8)
+        if scale is None:
+            scale = np.abs(c_arr).max(axis=1)
+        s_arr = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    P = lambda a: None if a is None else a.ctypes.data  # noqa: E731
+    lib.oracle_e8p12_map(P(r), n, P(gamma), int(gamma_div), P(c_arr), P(s_arr), float(tau),
+                         P(babs), P(bsq), P(bpar), P(lut), P(idx), P(score))
+    return idx, score
+
+
+def sqerr(x: np.ndarray, idx: np.ndarray, grid: np.ndarray) -> np.ndarray:
+    lib = _load()
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, 8)
+    idx = np.ascontiguousarray(idx, dtype=np.int64)
+    grid = np.ascontiguousarray(grid, dtype=np.float32)
+    out = np.empty(x.shape[0], dtype=np.float32)
+    lib.oracle_e8p12_sqerr(x.ctypes.data, idx.ctypes.data, x.shape[0], grid.ctypes.data, out.ctypes.data)
+    return out
+
+
+def bruteforce_nearest(x: np.ndarray, grid: np.ndarray):
+    lib = _load()
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, 8)
+    grid = np.ascontiguousarray(grid, dtype=np.float32)
+    idx = np.empty(x.shape[0], dtype=np.int64)
+    dist = np.empty(x.shape[0], dtype=np.float64)
+    lib.oracle_e8p12_bruteforce(x.ctypes.data, x.shape[0], grid.ctypes.data, idx.ctypes.data, dist.ctypes.data)
+    return idx, dist
+
+
+# ---------------------------------------------------------------------------
+# Posterior (denoiser) restatement, torch CPU, reference op order.
+# ---------------------------------------------------------------------------
+
+def _log1mexp(x: torch.Tensor) -> torch.Tensor:
+    cutoff = -math.log(2.0)
+    return torch.where(x < cutoff, torch.log1p(-torch.exp(x)), torch.log(-torch.expm1(x)))
+
+
+def _branch_stats(y: torch.Tensor, g: torch.Tensor, offset: float, branch: int, cache) -> Dict[str, torch.Tensor]:
+    """mpq/priors/e8p12.py:169-308 (_branch_factorized_stats_impl), need_stats=False."""
+    base_abs = cache["base_abs"].view(1, 256, 8)
+    sq = cache["base_sqnorm"].view(1, 256)
+    parity_even = (cache["base_parity"] == 0).view(1, 256)
+    bits = (1 << torch.arange(8)).view(1, 1, 8)
+    n = y.shape[0]
+    a = g.view(n, 1, 1) * y.view(n, 1, 8) * base_abs
+    y_norm = y.square().sum(dim=-1, keepdim=True)
+    const = -0.5 * g[:, :1] * (y_norm + sq)
+    logC = torch.logaddexp(a, -a).sum(dim=-1)
+    t = torch.tanh(a)
+    t_safe = t.clamp(min=-1.0 + 1e-7, max=1.0 - 1e-7)
+    log_abs_prod = torch.log(t_safe.abs().clamp_min(1e-7)).sum(dim=-1)
+    neg = ((t_safe < 0).sum(dim=-1) & 1).bool()
+    prod_abs = torch.exp(log_abs_prod)
+    prod = torch.where(neg, -prod_abs, prod_abs)
+    one = torch.ones_like(prod)
+    zeros = torch.zeros_like(log_abs_prod)
+    lp1 = torch.where(neg, _log1mexp(log_abs_prod), torch.logaddexp(zeros, log_abs_prod))
+    lm1 = torch.where(neg, torch.logaddexp(zeros, log_abs_prod), _log1mexp(log_abs_prod))
+    logZ_even = logC + lp1 - math.log(2.0)
+    logZ_odd = logC + lm1 - math.log(2.0)
+    logZ_sign = torch.where(parity_even, logZ_even, logZ_odd)
+    prefix = []
+    acc = one
+    for c in range(8):
+        prefix.append(acc)
+        acc = acc * t_safe[:, :, c]
+    sign_mean = torch.empty((n, 256, 8), dtype=torch.float32)
+    suffix = one
+    de = one + prod
+    do = one - prod
+    de_s = torch.where(de.abs() > 1e-12, de, torch.ones_like(de))
+    do_s = torch.where(do.abs() > 1e-12, do, torch.ones_like(do))
+    for c in reversed(range(8)):
+        tc = t_safe[:, :, c]
+        excl = prefix[c] * suffix
+        sign_mean[:, :, c] = torch.where(parity_even, (tc + excl) / de_s, (tc - excl) / do_s)
+        suffix = suffix * tc
+    sign_mean = torch.nan_to_num(sign_mean, nan=0.0, posinf=0.0, neginf=0.0)
+    mu_core = sign_mean * base_abs
+    mu = mu_core + float(offset)
+    second = sq + 8 * float(offset) * float(offset) + 2.0 * float(offset) * mu_core.sum(dim=-1)
+    del bits
+    return {"log_component": const + logZ_sign, "mu_component": mu, "second_component": second}
+
+
+def posterior(r1_blocks: torch.Tensor, gamma1: torch.Tensor, cache, *, prior_center_blocks=None,
+              prior_scale_blocks=None, prior_tau: float = 0.0, map_idx: Optional[np.ndarray] = None):
+    """mpq/priors/e8p12.py:815-968 without diagnostics: x1 blocks, var1, alpha1.
+
+    MAP (idx/vals) comes from ``map_search`` (same arithmetic as the reference's
+    per-branch MAP, :411-412 and :933-936).  High-precision snap at gamma >= 1e3
+    (:923-926) is applied.
+    """
+    r1_blocks = r1_blocks.to(dtype=torch.float32, device="cpu")
+    B, nb, _ = r1_blocks.shape
+    g_base = gamma1.to(torch.float32).view(B, 1, 1).expand(B, nb, 1)
+    r_work, g_work = r1_blocks, g_base
+    if prior_tau > 0.0 and prior_center_blocks is not None:
+        c = prior_center_blocks.to(torch.float32)
+        s = prior_scale_blocks
+        if s is None:
+            s = c.abs().amax(dim=-1, keepdim=True).clamp_min(1e-12)
+        s = s.to(torch.float32).clamp_min(1e-12)
+        tau2 = (max(float(prior_tau), 1e-12) * s).square()
+        pp = 1.0 / tau2
+        g_work = g_base + pp
+        r_work = (g_base * r1_blocks + pp * c) / g_work
+    r_flat = r_work.reshape(B * nb, 8)
+    g_flat = g_work.reshape(B * nb, 1)
+    outs = []
+    for bi, off in enumerate((0.25, -0.25)):
+        outs.append(_branch_stats(r_flat - off, g_flat, off, bi, cache))
+    log_comp = torch.stack([o["log_component"] for o in outs], dim=1)
+    logZ = torch.logsumexp(log_comp.reshape(B * nb, -1), dim=-1)
+    w = torch.exp(log_comp - logZ.view(-1, 1, 1))
+    mu = torch.zeros((B * nb, 8), dtype=torch.float32)
+    second = torch.zeros((B * nb,), dtype=torch.float32)
+    for bi in range(2):
+        mu += (w[:, bi, :].unsqueeze(-1) * outs[bi]["mu_component"]).sum(dim=1)
+        second += (w[:, bi, :] * outs[bi]["second_component"]).sum(dim=1)
+    var = ((second - mu.square().sum(dim=-1)) / 8.0).clamp_min_(0.0)
+    if map_idx is None:
+        center = None if prior_center_blocks is None else prior_center_blocks.reshape(-1, 8).numpy()
+        scale = None if prior_scale_blocks is None else prior_scale_blocks.reshape(-1).numpy()
+        map_idx, _ = map_search(r1_blocks.reshape(-1, 8).numpy(), gamma1.reshape(-1).numpy(), nb, cache,
+                                center=center, scale=scale, tau=prior_tau)
+    hi = g_flat.squeeze(-1) >= 1e3
+    if bool(hi.any()):
+        from mpq_amd.codebook import grid_numpy
+
+        mv = torch.from_numpy(grid_numpy()[np.asarray(map_idx)])
+        mu[hi] = mv[hi]
+        var[hi] = 0.0
+    var1 = var.view(B, nb)
+    alpha1 = gamma1.to(torch.float32) * var1.mean(dim=1, keepdim=True)
+    return {"x1_blocks": mu.view(B, nb, 8), "var1": var1, "alpha1": alpha1,
+            "map_idxs": torch.as_tensor(np.asarray(map_idx)).view(B, nb), "logZ": logZ.view(B, nb)}
+
+
+def posterior_bruteforce(r: np.ndarray, g: np.ndarray, grid: np.ndarray):
+    """fp64 posterior over all codewords: p(c) ∝ exp(-g/2 ||c - r||^2).  Returns mean, var (trace/8), logZ."""
+    r = np.asarray(r, dtype=np.float64).reshape(-1, 8)
+    g = np.asarray(g, dtype=np.float64).reshape(-1)
+    G = np.asarray(grid, dtype=np.float64)
+    gn = (G * G).sum(axis=1)
+    means = np.empty_like(r)
+    var = np.empty(r.shape[0])
+    logz = np.empty(r.shape[0])
+    for i in range(r.shape[0]):
+        d = gn - 2.0 * G @ r[i] + r[i] @ r[i]
+        s = -0.5 * g[i] * d
+        m = s.max()
+        w = np.exp(s - m)
+        Z = w.sum()
+        p = w / Z
+        means[i] = p @ G
+        var[i] = ((p * gn).sum() - means[i] @ means[i]) / 8.0
+        logz[i] = m + math.log(Z)
+    return means, var, logz
