@@ -2,12 +2,17 @@
  * mpq_amd — C-ABI of the MI355X (gfx950) per-layer quantization hot path.
  *
  * Conventions (all entry points):
- *  - every buffer is caller-allocated device memory, row-major and contiguous,
- *    fp32 unless stated; no entry point allocates unless documented;
- *  - work is enqueued on `stream` (a hipStream_t; NULL = default stream) and is
- *    asynchronous: nothing synchronises the host;
+ *  - every buffer is caller-allocated device memory, row-major and contiguous
+ *    unless a leading dimension is given, fp32 unless stated;
+ *  - work is enqueued on `stream` (a hipStream_t; NULL = default stream);
+ *    entry points are asynchronous except the two solver drivers
+ *    (mpq_uniform_vamp_solve), which read small status blocks back to run the
+ *    reference's host-side control flow;
+ *  - scratch memory comes from the caller (`workspace`, sized by the matching
+ *    *_workspace_size query); no entry point allocates device memory;
  *  - the return value is 0 on success, MPQ_INVALID_ARGUMENT (-1) for a bad
- *    shape/argument (nothing launched), MPQ_HIP_ERROR (-2) for a HIP failure;
+ *    shape/argument (nothing launched), MPQ_HIP_ERROR (-2) for a HIP failure,
+ *    MPQ_NUMERICAL_ERROR (-4) for the reference's numerical fail-closed checks;
  *    mpq_last_error() returns a thread-local message;
  *  - no C++ exception crosses this boundary.
  */
@@ -25,11 +30,16 @@ typedef struct ihipStream_t* mpq_stream_t; /* == hipStream_t */
 #define MPQ_OK 0
 #define MPQ_INVALID_ARGUMENT (-1)
 #define MPQ_HIP_ERROR (-2)
+#define MPQ_NUMERICAL_ERROR (-4)
 
 /* Thread-local description of the last failed call ("" if none). */
 const char* mpq_last_error(void);
 int mpq_last_error_code(void);
 void mpq_clear_error(void);
+
+/* ------------------------------------------------------------------------ */
+/* E8P12 lattice codebook                                                   */
+/* ------------------------------------------------------------------------ */
 
 /*
  * E8P12 MAP / nearest-codeword search over n 8-dim blocks.
@@ -51,6 +61,171 @@ void mpq_clear_error(void);
 int mpq_e8p12_map(const float* r, int64_t n, const float* gamma, int64_t gamma_div,
                   const float* center, const float* scale, float tau, int64_t* idx64,
                   uint16_t* idx16, float* vals, float* err, float* score, mpq_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Dense algebra                                                            */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * C = alpha * A op(B) + beta * C, fp32 MFMA (v_mfma_f32_32x32x2_f32), split-K
+ * with a fixed reduction order (bit-reproducible).  op(B) = B (K x N, ldb),
+ * B^T (B stored N x K, trans_b = 1) or gathered rows B[b_rows[k], :].
+ * Replaces the torch matmuls of mpq/linear.py:48-51, :94, mpq/solver.py:485,
+ * mpq/polish/triton_scalar_cd.py:195-196.  workspace (optional) holds split-K
+ * partials; with workspace_floats < 2*M*N the product runs unsplit.
+ */
+int mpq_gemm_f32(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B,
+                 int64_t ldb, int trans_b, const int32_t* b_rows, float* C, int64_t ldc,
+                 float alpha, float beta, float* workspace, int64_t workspace_floats,
+                 mpq_stream_t stream);
+
+/* out = in^T (rows x cols -> cols x rows). */
+int mpq_transpose(const float* in, int64_t rows, int64_t cols, int64_t ld_in, float* out,
+                  int64_t ld_out, mpq_stream_t stream);
+
+/*
+ * Post-processing of an ascending eigendecomposition (lam_asc, V_asc columns):
+ * eigenvalues floored at floor_v and put in descending order with their
+ * vectors, S = sqrt(lam), Vs = V * S.  Replaces
+ * mpq/adapters/gptqmodel.py:302-310 and :887-890 (eigh itself is rocSOLVER via
+ * torch.linalg.eigh).  Any output may be NULL.
+ */
+int mpq_eigh_postprocess(const float* lam_asc, const float* V_asc, int64_t n, float floor_v,
+                         float* lam, float* S, float* V, float* Vs, mpq_stream_t stream);
+
+/* out[i][j] = in[i][j] * scale[j] (Vs = V * S, mpq/adapters/gptqmodel.py:890). */
+int mpq_scale_columns(const float* in, int64_t rows, int64_t cols, const float* scale, float* out,
+                      mpq_stream_t stream);
+
+/*
+ * Signed block Walsh-Hadamard along rows: forward out = H_b(in * signs) /
+ * sqrt(b), inverse out = H_b(in) / sqrt(b) * signs, b = had_dim (power of two,
+ * width % b == 0), Sylvester order with butterfly strides 1, 2, 4, ...
+ * Replaces mpq/rotation.py:404-438 (apply_right_block_hadamard[_inverse]) and
+ * its torch butterfly mpq/rotation.py:135-156.  signs may be NULL.
+ */
+int mpq_block_hadamard(const float* in, int64_t ld_in, float* out, int64_t ld_out, int64_t rows,
+                       int64_t width, int64_t had_dim, const float* signs, int inverse,
+                       mpq_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Uniform (scalar) grid                                                    */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * GPTQ asymmetric min-max parameters per (row, group of group_size columns):
+ * xmin = min(min(w), 0), xmax = max(max(w), 0) (+-1 if both 0),
+ * scale = (xmax - xmin)/maxq, zero = round(-xmin/scale).  Replaces the
+ * GPTQModel quantizer.find_params calls of mpq/adapters/gptqmodel.py:899-909.
+ * scale, zero: rows x ceil(n/group_size).
+ */
+int mpq_gptq_find_params(const float* W, int64_t rows, int64_t n, int64_t ldw, int64_t group_size,
+                         int maxq, float* scale, float* zero, mpq_stream_t stream);
+
+/*
+ * RTN decision q = clamp(round(W/s) + z, 0, maxq) (uint8), x = s(q - z).
+ * Replaces mpq/adapters/gptqmodel.py:966-969.  q or x may be NULL.
+ */
+int mpq_uniform_rtn(const float* W, int64_t rows, int64_t n, int64_t ldw, const float* scale,
+                    const float* zero, int64_t group_size, int maxq, uint8_t* q, float* x,
+                    mpq_stream_t stream);
+
+/* x = s(q - z) from uint8 codes.  Replaces mpq/priors/uniform.py:302-309. */
+int mpq_dequant(const uint8_t* q, int64_t rows, int64_t n, const float* scale, const float* zero,
+                int64_t group_size, float* x, mpq_stream_t stream);
+
+/*
+ * Posterior of each entry over the uniform grid a_q = s(q - z), q = 0..maxq,
+ * under channel N(r1, 1/gamma_row) and prior N(center, (tau*s)^2):
+ * mean, var, MAP index (int64, first max) and value, alpha1 = gamma*mean(var)
+ * (rows, optional).  Replaces mpq/priors/uniform.py:99-213
+ * (discrete_uniform_mmse without diagnostics).
+ */
+int mpq_uniform_denoise(int64_t rows, int64_t n, int maxq, const float* r1, const float* gamma,
+                        const float* center, int64_t ld_center, const float* scale,
+                        const float* zero, int64_t group_size, float tau, float* mean, float* var,
+                        int64_t* map_idx, float* map_value, float* alpha1, mpq_stream_t stream);
+
+/* Mirrors UniformVampConfig (mpq/solver.py:35-55). */
+typedef struct MpqUniformVampConfig {
+  int iters;
+  float damping;
+  int final_decision; /* 0 = "map", 1 = "round_mean" */
+  int init_from;      /* 0 = "rtn", 1 = "float", 2 = "zero" */
+  float gamma_start;
+  float gamma_retry_factor;
+  int gamma_retry_steps;
+  float prior_tau;
+  double obs_precision; /* > 0: fixed observation precision (EM off) */
+  int em_obs_precision;
+  double em_obs_precision_damping;
+  double em_obs_precision_min;
+  double em_obs_precision_max;
+} MpqUniformVampConfig;
+
+/* Per-solve statistics (subset of mpq/solver.py:783-829). */
+typedef struct MpqUniformVampStats {
+  int iters;
+  int best_iter;
+  int stop_iter;
+  int alpha1_retry_count;
+  int alpha2_clip_count;
+  int gamma2_invalid_count;
+  double obs_precision_initial;
+  double obs_precision_final;
+  double obs_precision_mean;
+  double alpha1_mean;
+  double alpha2_mean;
+  double best_rankspace_error_mean;
+  double rtn_rankspace_error_mean;
+} MpqUniformVampStats;
+
+/* Workspace bytes needed by mpq_uniform_vamp_solve for a rows x n block. */
+int64_t mpq_uniform_vamp_workspace_size(int64_t rows, int64_t n);
+
+/*
+ * Uniform-grid VAMP on one row block, without the polish: replaces
+ * mpq/solver.py:426-703 (solve_uniform_rankspace_vamp up to the polish) with
+ * its denoiser mpq/priors/uniform.py:99-213, LMMSE mpq/linear.py:10-56, EM
+ * mpq/linear.py:59-82 and rank-space error mpq/linear.py:85-94.
+ *   W (ldw), x_init: rows x n (x_init = RTN decision, also the gamma1 init)
+ *   scale/zero: rows x ceil(n/group_size) group parameters
+ *   V, Vs: n x n (full rank), S: n
+ *   obs_init > 0 overrides the warm start of the observation precision
+ *   q_out (rows x n uint8), x_out (optional), err_out (rows), rtn_err_out (rows, optional)
+ * Synchronises `stream` twice per iteration to read small status blocks.
+ */
+int mpq_uniform_vamp_solve(int64_t rows, int64_t n, int maxq, const float* W, int64_t ldw,
+                           const float* x_init, const float* scale, const float* zero,
+                           int64_t group_size, const float* V, const float* S, const float* Vs,
+                           const MpqUniformVampConfig* cfg, double obs_init, uint8_t* q_out,
+                           float* x_out, float* err_out, float* rtn_err_out,
+                           MpqUniformVampStats* stats, void* workspace, int64_t workspace_bytes,
+                           mpq_stream_t stream);
+
+/* Workspace bytes needed by mpq_uniform_cd_polish. */
+int64_t mpq_uniform_cd_workspace_size(int64_t rows, int64_t n, int64_t block_rows);
+
+/*
+ * Greedy scalar coordinate-descent polish over all rows, each block of
+ * block_rows rows with its own greedy column order: replaces
+ * mpq/polish/triton_scalar_cd.py:164-307 (uniform_scalar_diag_greedy_cd, the
+ * CUDA dispatch of mpq/solver.py:299-333) and, with select != 0, the
+ * keep-if-better selection of mpq/solver.py:749-754.
+ *   targets: W (ldw) rows x n (Yu = W Vs is formed) or Yu rows x n (W = NULL);
+ *   q_in rows x n uint8 initial codes; x_in (optional) rows x n initial values
+ *   (default: dequantised q_in); Vs, H (gram_full) n x n; outputs q_out,
+ *   err_before/err_after (rows), improved (rows int32), accepted_per_row
+ *   (rows int32); every output but q_out may be NULL.  n <= 16384.
+ */
+int mpq_uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                          float accept_tol, const float* W, int64_t ldw, const float* Yu,
+                          const uint8_t* q_in, const float* x_in, const float* scale,
+                          const float* zero, int64_t group_size,
+                          const float* Vs, const float* H, int select, uint8_t* q_out,
+                          float* err_before, float* err_after, int32_t* improved,
+                          int32_t* accepted_per_row, void* workspace, int64_t workspace_bytes,
+                          mpq_stream_t stream);
 
 #ifdef __cplusplus
 }

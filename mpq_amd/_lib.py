@@ -31,7 +31,67 @@ SIGNATURES = {
     "mpq_clear_error": (None, []),
     "mpq_e8p12_map": (c_int, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_float,
                               c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "mpq_gemm_f32": (c_int, [c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_int, c_ptr,
+                             c_ptr, c_i64, c_float, c_float, c_ptr, c_i64, c_ptr]),
+    "mpq_gptq_find_params": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_ptr, c_ptr]),
+    "mpq_uniform_rtn": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_int, c_ptr, c_ptr,
+                                c_ptr]),
+    "mpq_dequant": (c_int, [c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_ptr, c_ptr]),
+    "mpq_block_hadamard": (c_int, [c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr, c_int, c_ptr]),
+    "mpq_transpose": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr]),
+    "mpq_scale_columns": (c_int, [c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_ptr]),
+    "mpq_eigh_postprocess": (c_int, [c_ptr, c_ptr, c_i64, c_float, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "mpq_uniform_denoise": (c_int, [c_i64, c_i64, c_int, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_i64,
+                                    c_float, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "mpq_uniform_vamp_workspace_size": (c_i64, [c_i64, c_i64]),
+    "mpq_uniform_vamp_solve": (c_int, [c_i64, c_i64, c_int, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64,
+                                       c_ptr, c_ptr, c_ptr, c_ptr, c_double, c_ptr, c_ptr, c_ptr, c_ptr,
+                                       c_ptr, c_ptr, c_i64, c_ptr]),
+    "mpq_uniform_cd_workspace_size": (c_i64, [c_i64, c_i64, c_i64]),
+    "mpq_uniform_cd_polish": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_float, c_ptr, c_i64, c_ptr,
+                                      c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_int, c_ptr,
+                                      c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
 }
+
+
+class UniformVampConfigC(ctypes.Structure):
+    """Mirror of MpqUniformVampConfig (include/mpq_amd.h)."""
+
+    _fields_ = [
+        ("iters", ctypes.c_int),
+        ("damping", ctypes.c_float),
+        ("final_decision", ctypes.c_int),
+        ("init_from", ctypes.c_int),
+        ("gamma_start", ctypes.c_float),
+        ("gamma_retry_factor", ctypes.c_float),
+        ("gamma_retry_steps", ctypes.c_int),
+        ("prior_tau", ctypes.c_float),
+        ("obs_precision", ctypes.c_double),
+        ("em_obs_precision", ctypes.c_int),
+        ("em_obs_precision_damping", ctypes.c_double),
+        ("em_obs_precision_min", ctypes.c_double),
+        ("em_obs_precision_max", ctypes.c_double),
+    ]
+
+
+class UniformVampStatsC(ctypes.Structure):
+    """Mirror of MpqUniformVampStats (include/mpq_amd.h)."""
+
+    _fields_ = [
+        ("iters", ctypes.c_int),
+        ("best_iter", ctypes.c_int),
+        ("stop_iter", ctypes.c_int),
+        ("alpha1_retry_count", ctypes.c_int),
+        ("alpha2_clip_count", ctypes.c_int),
+        ("gamma2_invalid_count", ctypes.c_int),
+        ("obs_precision_initial", ctypes.c_double),
+        ("obs_precision_final", ctypes.c_double),
+        ("obs_precision_mean", ctypes.c_double),
+        ("alpha1_mean", ctypes.c_double),
+        ("alpha2_mean", ctypes.c_double),
+        ("best_rankspace_error_mean", ctypes.c_double),
+        ("rtn_rankspace_error_mean", ctypes.c_double),
+    ]
 
 
 class MPQLibraryError(RuntimeError):
@@ -70,6 +130,8 @@ def check(status: int, name: str) -> None:
         text = msg.decode("utf-8", "replace") if msg else ""
         if status == -1:
             raise ValueError(f"{name}: {text}")
+        if status == -4:  # numerical failure, reported as the reference does (RuntimeError)
+            raise RuntimeError(text)
         raise MPQLibraryError(f"{name} failed (status {status}): {text}")
 
 

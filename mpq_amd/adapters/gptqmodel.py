@@ -1,0 +1,306 @@
+"""GPTQModel adapter: per-linear uniform-grid MPQ solve on MI355X.
+
+Drop-in for the reference's ``mpq/adapters/gptqmodel.py``:
+
+* ``GPTQAdapterConfig``          reference :37-43
+* ``run_mpq_quantization``       reference :650-1163 (``solver="vamp"`` path)
+
+Pipeline (all on the ROCm device):
+  H <- hessian_scale * H; eigh of the unrotated H (rocSOLVER through
+  ``torch.linalg.eigh``) -> ``mpq_eigh_postprocess`` (floor, descending order,
+  S, Vs); internal block-Hadamard rotation of W, H (both sides) and V
+  (``mpq_block_hadamard``); GPTQ group parameters (``quantizer.find_params`` if a
+  quantizer is given, else ``mpq_gptq_find_params``); RTN (``mpq_uniform_rtn``);
+  observation-precision warm start; the sequential row-block VAMP chain
+  (``mpq_uniform_vamp_solve``, EM precision carried block to block); one batched
+  greedy CD polish over all rows (``mpq_uniform_cd_polish``, greedy order per row
+  block, identical to polishing block by block); proxy-loss audit
+  ``(W-Q) H (W-Q)^T``; inverse rotation of Q.
+
+Row blocks use exactly ``adapter_cfg.block_rows`` rows (the reference enlarges
+them from free memory on CUDA, mpq/adapters/gptqmodel.py:313-327, which changes
+results; pass ``auto_block_rows=True`` for that behaviour).
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass
+from typing import Any, Dict, List, Optional, Tuple
+
+import torch
+
+from .. import ops
+from ..rotation import (
+    apply_left_block_hadamard,
+    apply_right_block_hadamard,
+    apply_right_block_hadamard_inverse,
+    resolve_block_hadamard_plan,
+    sample_rademacher_signs,
+)
+from ..solver import UniformVampConfig, _resolve_polish_mode
+
+
+@dataclass(frozen=True)
+class GPTQAdapterConfig:
+    hessian_scale: float = 0.5  # GPTQModel stores H = 2/m X^T X
+    block_rows: int = 128
+    jitter_base: float = 1e-6
+    eigen_floor_scale: float = 1e-6
+    rotation_seed: int = 0
+    auto_block_rows: bool = False
+
+
+class MinMaxQuantizer:
+    """GPTQ asymmetric min-max quantizer with the ``find_params`` protocol, on the HIP kernel."""
+
+    def __init__(self, bits: int):
+        self.maxq = torch.tensor(2 ** int(bits) - 1)
+        self.scale = None
+        self.zero = None
+
+    def find_params(self, x: torch.Tensor, weight: bool = True) -> None:
+        s, z = ops.gptq_find_params(x, int(x.shape[1]), int(self.maxq))
+        self.scale, self.zero = s, z
+
+
+def resolve_internal_rotation(*, requested: str, cols: int, module_name: str, seed: int,
+                              device: torch.device) -> Dict[str, Any]:
+    """reference :46-118."""
+    req = str(requested or "none").strip().lower()
+    if req in {"", "none"}:
+        return {"requested": "none", "effective": "none", "mode": "none", "signs": None, "block_dim": 1,
+                "fallback_reason": "", "internal": False}
+    if req in {"model_random", "model_hadamard"}:
+        return {"requested": req, "effective": req, "mode": "none", "signs": None, "block_dim": 1,
+                "fallback_reason": "", "internal": False}
+    if req != "internal_hadamard":
+        raise ValueError("mpq only supports rotation in {none, model_hadamard, model_random, internal_hadamard}; "
+                         f"got rotation={requested!r}.")
+    mode, block_dim = resolve_block_hadamard_plan(int(cols))
+    if mode == "none":
+        return {"requested": "internal_hadamard", "effective": "none", "mode": "none", "signs": None,
+                "block_dim": 1, "fallback_reason": f"unsupported_block_hadamard_width:{int(cols)}",
+                "internal": False}
+    signs = sample_rademacher_signs(width=int(cols), key=f"{module_name}:full", seed=int(seed), device=device)
+    return {"requested": "internal_hadamard", "effective": "internal_block_hadamard", "mode": "block",
+            "signs": signs, "block_dim": int(block_dim), "fallback_reason": "", "internal": True}
+
+
+@torch.inference_mode()
+def vamp_hessian_eigen(H: torch.Tensor, *, jitter_base: float = 1e-6, floor_scale: float = 1e-6):
+    """Floored descending eigendecomposition (reference :276-310).  Returns (lam, S, V, Vs, floor)."""
+    Hs = 0.5 * (H + H.T)
+    if not bool(torch.isfinite(Hs).all()):
+        Hs = torch.nan_to_num(Hs, nan=0.0, posinf=0.0, neginf=0.0)
+    lam_asc, V_asc = torch.linalg.eigh(Hs)
+    max_lam = float(lam_asc[-1].item()) if lam_asc.numel() else 0.0
+    diag_mean = float(torch.diagonal(Hs).mean().abs().item()) if Hs.numel() else 0.0
+    floor = max(float(jitter_base), float(floor_scale) * max(diag_mean, max_lam, 1e-12))
+    lam, S, V, Vs = ops.eigh_postprocess(lam_asc, V_asc, floor)
+    del V_asc
+    return lam, S, V, Vs, float(floor)
+
+
+def _resolve_block_rows(rows: int, cols: int, maxq: int, requested: int, device: torch.device, auto: bool) -> int:
+    block_rows = min(int(rows), max(int(requested), 1))
+    if not auto:
+        return block_rows
+    free_bytes, _ = torch.cuda.mem_get_info(device)
+    bytes_per_row = 4 * (8 * int(cols) + 4 * int(cols) * (int(maxq) + 1))
+    budget = min(4 * 1024 ** 3, int(free_bytes) // 2)
+    automatic = max(8, min(int(rows), int(budget // max(bytes_per_row, 1))))
+    return min(int(rows), max(block_rows, int(automatic)))
+
+
+@torch.inference_mode()
+def run_mpq_quantization(
+    *,
+    W: torch.Tensor,
+    H: torch.Tensor,
+    quantizer: Any,
+    qcfg: Any,
+    module_name: str,
+    vamp_cfg: UniformVampConfig,
+    adapter_cfg: GPTQAdapterConfig = GPTQAdapterConfig(),
+) -> Tuple[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor], Optional[torch.Tensor],
+           Optional[torch.Tensor], float, Dict[str, Any]]:
+    """Per-linear MPQ (uniform grid) on one GPU.
+
+    Returns (Q fp32 rows x cols in the original basis, q_int uint8 (solver basis),
+    scale_groups, zero_groups, g_idx int32, quant_time_s, stats) as the reference.
+    """
+    start = time.time()
+    device = W.device
+    if device.type != "cuda":
+        raise ValueError("run_mpq_quantization: W must be on a ROCm device (mpq_amd has no CPU path).")
+    W = W.to(torch.float32)
+    H = H.to(device=device, dtype=torch.float32)
+    rows, cols = W.shape
+    bits = int(getattr(qcfg, "bits"))
+    maxq = int(2 ** bits - 1)
+    group_size = int(getattr(qcfg, "group_size", cols))
+    if group_size == -1:
+        group_size = cols
+    mpq_cfg = getattr(qcfg, "mpq", None)
+    solver_name = str(getattr(mpq_cfg, "dispatch_solver", getattr(mpq_cfg, "solver", "vamp")) or "vamp").strip().lower()
+    if solver_name != "vamp":
+        raise ValueError(f"mpq_amd implements solver='vamp'; got {solver_name!r}.")
+    if bool(getattr(qcfg, "desc_act", False)):
+        raise ValueError("mpq_amd implements desc_act=False (the recipe default).")
+    rotation = resolve_internal_rotation(
+        requested=str(getattr(mpq_cfg, "rotation_mode", getattr(qcfg, "rotation", None) or "none")),
+        cols=int(cols), module_name=str(module_name), seed=int(adapter_cfg.rotation_seed), device=device)
+    timings: Dict[str, float] = {}
+
+    H_work = float(adapter_cfg.hessian_scale) * H
+    t0 = time.time()
+    lam, S, V, Vs, eigen_floor = vamp_hessian_eigen(H_work, jitter_base=adapter_cfg.jitter_base,
+                                                    floor_scale=adapter_cfg.eigen_floor_scale)
+    torch.cuda.synchronize(device)
+    timings["eigh_s"] = time.time() - t0
+    signs = rotation["signs"]
+    had = int(rotation["block_dim"])
+    if rotation["mode"] == "block":
+        W_work = apply_right_block_hadamard(W, signs=signs, had_dim=had)
+        H_metric = apply_right_block_hadamard(apply_left_block_hadamard(H_work, signs=signs, had_dim=had),
+                                              signs=signs, had_dim=had)
+        V = apply_left_block_hadamard(V, signs=signs, had_dim=had)
+        Vs = ops.scale_columns(V, S)  # Vs = V * S after the rotation (reference :887-890)
+    else:
+        W_work = W.contiguous()
+        H_metric = H_work.contiguous()
+    dead = torch.diagonal(H_metric) == 0
+    has_dead = bool(dead.any().item())
+    if has_dead:
+        H_metric = H_metric.clone()
+        W_work = W_work.clone()
+        H_metric[dead, dead] = 1
+        W_work[:, dead] = 0
+        lam, S, V, Vs, eigen_floor = vamp_hessian_eigen(H_metric, jitter_base=adapter_cfg.jitter_base,
+                                                        floor_scale=adapter_cfg.eigen_floor_scale)
+
+    # group parameters in the solver basis
+    if quantizer is not None and hasattr(quantizer, "find_params") and not isinstance(quantizer, MinMaxQuantizer):
+        sc, zc = [], []
+        for g0 in range(0, cols, group_size):
+            quantizer.find_params(W_work[:, g0:g0 + group_size].contiguous(), weight=True)
+            sc.append(quantizer.scale.to(device=device, dtype=torch.float32).reshape(rows, -1)[:, :1].clone())
+            zc.append(quantizer.zero.to(device=device, dtype=torch.float32).reshape(rows, -1)[:, :1].clone())
+        scale_groups = torch.cat(sc, 1).contiguous()
+        zero_groups = torch.cat(zc, 1).contiguous()
+    else:
+        scale_groups, zero_groups = ops.gptq_find_params(W_work, group_size, maxq)
+    block_rows = _resolve_block_rows(rows, cols, maxq, int(adapter_cfg.block_rows), device,
+                                     bool(adapter_cfg.auto_block_rows))
+    _, x_rtn = ops.uniform_rtn(W_work, scale_groups, zero_groups, group_size, maxq, want_q=False)
+
+    # observation-precision warm start (reference :920-941): per block sums accumulated in double
+    if float(getattr(vamp_cfg, "obs_precision", 0.0)) > 0.0:
+        obs_precision = float(vamp_cfg.obs_precision)
+    else:
+        du = ops.gemm(W_work - x_rtn, Vs)
+        sq = du.square().sum(dim=1)
+        sums = [float(sq[r0:r0 + block_rows].sum().item()) for r0 in range(0, rows, block_rows)]
+        mse = max(sum(sums) / max(rows * cols, 1), 1e-12)
+        obs_precision = 1.0 / mse
+
+    torch.cuda.synchronize(device)
+    t_solve = time.time()
+    q_int = torch.empty(rows, cols, dtype=torch.uint8, device=device)
+    err_vamp = torch.empty(rows, dtype=torch.float32, device=device)
+    rtn_err = torch.empty(rows, dtype=torch.float32, device=device)
+    ws = ops.workspace(int(ops._lib.load().mpq_uniform_vamp_workspace_size(block_rows, cols)), device)
+    obs_block = float(obs_precision)
+    block_stats: List[Dict[str, Any]] = []
+    for r0 in range(0, rows, block_rows):
+        r1 = min(rows, r0 + block_rows)
+        q_b, _, e_b, re_b, st = ops.uniform_vamp_solve(
+            W_work[r0:r1], x_rtn[r0:r1], scale_groups[r0:r1], zero_groups[r0:r1], group_size, maxq, V, S, Vs,
+            vamp_cfg, obs_init=obs_block, ws=ws)
+        q_int[r0:r1] = q_b
+        err_vamp[r0:r1] = e_b
+        rtn_err[r0:r1] = re_b
+        if bool(getattr(vamp_cfg, "em_obs_precision", True)):
+            obs_block = float(st["obs_precision_final"])
+        block_stats.append(st)
+    del ws
+    torch.cuda.synchronize(device)
+    timings["vamp_s"] = time.time() - t_solve
+
+    t_pol = time.time()
+    sweeps = max(int(getattr(vamp_cfg, "polish_sweeps", 3)), 0)
+    mode = _resolve_polish_mode(sweeps=sweeps, mode=str(getattr(vamp_cfg, "polish_mode", "block_cd")))
+    if mode == "topk_block_cd":
+        raise ValueError("mpq_amd implements polish_mode='block_cd'.")
+    polish_updates = 0.0
+    changed = 0
+    if mode == "block_cd":
+        q_pol, eb, ea, imp, acc = ops.uniform_cd_polish(W_work, q_int, scale_groups, zero_groups, group_size, maxq,
+                                                        Vs, H_metric, block_rows=block_rows, sweeps=sweeps,
+                                                        select=True)
+        final_err = torch.where(imp.bool(), ea, err_vamp)
+        changed = int((q_pol != q_int).sum().item())
+        q_int = q_pol
+        polish_updates = float(acc.sum().item())
+    else:
+        final_err = err_vamp
+    torch.cuda.synchronize(device)
+    timings["polish_s"] = time.time() - t_pol
+
+    Q_work = ops.dequant(q_int, scale_groups, zero_groups, group_size)
+    delta = W_work - Q_work
+    raw_rows = (ops.gemm(delta, H_metric) * delta).sum(dim=1)
+    g_idx = torch.arange(cols, device=device, dtype=torch.int32) // int(group_size)
+    if rotation["mode"] == "block":
+        Q = apply_right_block_hadamard_inverse(Q_work, signs=signs, had_dim=had)
+    else:
+        Q = Q_work
+    if mpq_cfg is not None:
+        for k, v in (("rotation_requested", rotation["requested"]), ("rotation_effective", rotation["effective"]),
+                     ("rotation_internal", rotation["internal"]), ("rotation_block_dim", rotation["block_dim"]),
+                     ("rotation_fallback_reason", rotation["fallback_reason"])):
+            try:
+                setattr(mpq_cfg, k, v)
+            except Exception:  # frozen configs
+                pass
+    layer_err_sum = float(final_err.sum().item())
+    raw_sum = float(raw_rows.sum().item())
+    torch.cuda.synchronize(device)
+    quant_time = time.time() - start
+    stats: Dict[str, Any] = {
+        "method": "mpq",
+        "solver": "vamp",
+        "polish_mode": mode,
+        "module": str(module_name),
+        "bits": bits,
+        "group_size": group_size,
+        "rotation_requested": str(rotation["requested"]),
+        "rotation_effective": str(rotation["effective"]),
+        "rotation_internal": bool(rotation["internal"]),
+        "rotation_block_dim": had,
+        "rotation_fallback_reason": str(rotation["fallback_reason"]),
+        "desc_act": False,
+        "rows": int(rows),
+        "cols": int(cols),
+        "rank": int(S.numel()),
+        "eigen_floor": float(eigen_floor),
+        "block_rows": int(block_rows),
+        "block_cd_backend": "hip",
+        "obs_precision_initial": float(obs_precision),
+        "obs_precision_final": float(obs_block),
+        "layer_error_sum": layer_err_sum,
+        "stabilized_objective_mean_final": layer_err_sum / max(rows, 1),
+        "raw_objective_mean_final": raw_sum / max(rows, 1),
+        "proxy_loss": raw_sum,
+        "rankspace_raw_abs_diff_mean": float((final_err - raw_rows).abs().sum().item()) / max(rows, 1),
+        "rtn_error_sum": float(rtn_err.sum().item()),
+        "vamp_iters": [int(b["best_iter"]) + 1 for b in block_stats],
+        "vamp_iters_entered": [
+            (int(b["stop_iter"]) + 1 if int(b["stop_iter"]) >= 0 else int(b["iters"])) for b in block_stats],
+        "block_stats": block_stats,
+        "polish_updates": polish_updates,
+        "changed_by_polish": changed,
+        "timings": timings,
+        "quant_time_s": float(quant_time),
+    }
+    return Q, q_int, scale_groups, zero_groups, g_idx, float(quant_time), stats

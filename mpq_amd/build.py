@@ -21,12 +21,17 @@ from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 BUILD_DIR = os.path.join(HERE, "_build")
 LIB_NAME = "libmpq_amd.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
 HIP_SOURCES = [
     "e8p12_map.hip",
+    "gemm.hip",
+    "elementwise.hip",
+    "uniform_vamp.hip",
+    "cd_uniform.hip",
 ]
 CXX_SOURCES = [
     "errors.cpp",
@@ -70,11 +75,11 @@ def build(verbose: bool = False, jobs: int = 8) -> str:
     cmds = []
     for src in HIP_SOURCES:
         obj = os.path.join(BUILD_DIR, src + ".o")
-        cmds.append([HIPCC, *COMMON_FLAGS, *HIP_FLAGS, "-I", CSRC, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([HIPCC, *COMMON_FLAGS, *HIP_FLAGS, "-I", CSRC, "-I", INCLUDE, "-c", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
     for src in CXX_SOURCES:
         obj = os.path.join(BUILD_DIR, src + ".o")
-        cmds.append([HIPCC, *COMMON_FLAGS, "-I", CSRC, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([HIPCC, *COMMON_FLAGS, "-I", CSRC, "-I", INCLUDE, "-c", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
     with ThreadPoolExecutor(max_workers=max(1, int(jobs))) as pool:
         for out in pool.map(_run, cmds):

@@ -1,0 +1,416 @@
+// Greedy scalar coordinate-descent polish of uniform-grid codes (gfx950).
+//
+// Replaces mpq/polish/triton_scalar_cd.py:164-307 (uniform_scalar_diag_greedy_cd
+// with the persistent sweep kernel :28-110) as dispatched from
+// mpq/solver.py:299-333, plus the selection of mpq/solver.py:749-754.
+//
+// Semantics per row block (block_rows rows sharing one greedy order):
+//   residual_u = Yu - x Vs, rhs = residual_u Vs^T, diag_j = |Vs_j|^2 (>= 1e-12)
+//   per sweep: gain_j = mean_rows(rhs_j^2 / diag_j), order = stable argsort(-gain)
+//   per column (in order): target = x + rhs/diag, q = clamp(rint(target/s + z)),
+//     accept iff res + d^2 diag - 2 rhs d + 1e-12 < res (1 + tol),
+//     rhs -= d * H[col, :]
+// Blocking: columns are taken in windows of 128 consecutive positions of the
+// greedy order.  Inside a window one wave64 per row runs the 128 sequential
+// decisions with the window's H sub-block in LDS (rank-1 updates of the window's
+// own rhs entries); after the window the deferred update of every column,
+// rhs -= Delta(rows x 128) H[window, :], is one fp32 MFMA GEMM with a per-block
+// row gather.  Only the rounding order of the rhs updates differs from the
+// column-at-a-time reference.
+#include <algorithm>
+
+#include "gemm.h"
+#include "kernels.h"
+
+namespace mpq {
+namespace {
+
+constexpr int kWin = 128;
+constexpr int kRowsPerWG = 8;  // one wave64 per row
+
+__device__ __forceinline__ float bcast(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// residual_u = Yu - P (sum of split partials), also copies it scaled for the rhs product.
+__global__ __launch_bounds__(256) void residual_kernel(int64_t rows, int64_t n, const float* __restrict__ P,
+                                                       int splits, int64_t split_stride,
+                                                       const float* __restrict__ Yu,
+                                                       float* __restrict__ res,
+                                                       float* __restrict__ part, int nchunks) {
+  __shared__ float red[4];
+  const int64_t b = blockIdx.y;
+  float acc = 0.f;
+  for (int e = 0; e < 4; ++e) {
+    const int64_t j = (int64_t)blockIdx.x * 1024 + e * 256 + threadIdx.x;
+    if (j >= n) continue;
+    const int64_t o = b * n + j;
+    float v = P[o];
+    for (int s = 1; s < splits; ++s) v = v + P[(int64_t)s * split_stride + o];
+    const float r = Yu[o] - v;
+    if (res) res[o] = r;
+    acc += r * r;
+  }
+  const float t = block_sum(acc, red);
+  if (threadIdx.x == 0) part[b * nchunks + blockIdx.x] = t;
+}
+
+__global__ void rows_sum_kernel(int64_t rows, int nchunks, const float* __restrict__ part,
+                                float* __restrict__ out) {
+  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < rows;
+       b += (int64_t)gridDim.x * blockDim.x) {
+    float v = part[b * nchunks];
+    for (int c = 1; c < nchunks; ++c) v = v + part[b * nchunks + c];
+    out[b] = v;
+  }
+}
+
+// gain[blk][j] = sum_{rows of blk} rhs^2 * diag_inv / rows_in_blk
+__global__ __launch_bounds__(256) void gain_kernel(int64_t rows, int64_t n, int64_t block_rows,
+                                                   const float* __restrict__ rhs,
+                                                   const float* __restrict__ diag_inv,
+                                                   float* __restrict__ gain) {
+  const int64_t blk = blockIdx.y;
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const int64_t r0 = blk * block_rows;
+  int64_t r1 = r0 + block_rows;
+  if (r1 > rows) r1 = rows;
+  const float di = diag_inv[j];
+  float acc = 0.f;
+  for (int64_t r = r0; r < r1; ++r) {
+    const float v = rhs[r * n + j];
+    acc += (v * v) * di;
+  }
+  gain[blk * n + j] = acc / (float)(r1 - r0);
+}
+
+// T[blk][p][q] = H[order[blk][w0 + p]][order[blk][w0 + q]] for the window (zero-padded).
+__global__ __launch_bounds__(kWin) void tile_gather_kernel(int64_t n, const float* __restrict__ H,
+                                                           const int32_t* __restrict__ order,
+                                                           int64_t w0, int wn,
+                                                           float* __restrict__ T) {
+  const int64_t blk = blockIdx.y;
+  const int p = blockIdx.x;
+  const int q = threadIdx.x;
+  const int32_t* ord = order + blk * n + w0;
+  float v = 0.f;
+  if (p < wn && q < wn) v = H[(int64_t)ord[p] * n + ord[q]];
+  T[(blk * kWin + p) * kWin + q] = v;
+}
+
+// One window of greedy decisions; one wave per row, lane l owns positions l and l+64.
+__global__ __launch_bounds__(64 * kRowsPerWG) void window_kernel(
+    int64_t rows, int64_t n, int64_t block_rows, int maxq, float accept_tol,
+    const int32_t* __restrict__ order, int64_t w0, int wn, const float* __restrict__ T,
+    const float* __restrict__ scale, const float* __restrict__ zero, int64_t G, int64_t gs,
+    const float* __restrict__ diag, float* __restrict__ rhs, float* __restrict__ x,
+    uint8_t* __restrict__ q, float* __restrict__ res_norm, float* __restrict__ delta,
+    int* __restrict__ accepted) {
+  __shared__ float Ts[kWin * kWin];
+  const int64_t blk = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const float* Tb = T + blk * kWin * kWin;
+  for (int i = threadIdx.x; i < kWin * kWin; i += blockDim.x) Ts[i] = Tb[i];
+  __syncthreads();
+  const int64_t row = blk * block_rows + (int64_t)blockIdx.x * kRowsPerWG + wave;
+  int64_t blk_end = (blk + 1) * block_rows;
+  if (blk_end > rows) blk_end = rows;
+  if (row >= blk_end) return;
+
+  const int32_t* ord = order + blk * n + w0;
+  const bool v0 = lane < wn, v1 = lane + 64 < wn;
+  const int64_t c0 = v0 ? ord[lane] : 0;
+  const int64_t c1 = v1 ? ord[lane + 64] : 0;
+  const int64_t o0 = row * n + c0, o1 = row * n + c1;
+  float rhs0 = v0 ? rhs[o0] : 0.f, rhs1 = v1 ? rhs[o1] : 0.f;
+  float x0 = v0 ? x[o0] : 0.f, x1 = v1 ? x[o1] : 0.f;
+  float s0 = v0 ? scale[row * G + c0 / gs] : 1.f, s1 = v1 ? scale[row * G + c1 / gs] : 1.f;
+  s0 = s0 < 1e-12f ? 1e-12f : s0;
+  s1 = s1 < 1e-12f ? 1e-12f : s1;
+  const float z0 = v0 ? zero[row * G + c0 / gs] : 0.f, z1 = v1 ? zero[row * G + c1 / gs] : 0.f;
+  const float dg0 = v0 ? diag[c0] : 1.f, dg1 = v1 ? diag[c1] : 1.f;
+  int q0 = -1, q1 = -1;
+  float d0 = 0.f, d1 = 0.f;
+  float res = res_norm[row];
+  int acc_count = 0;
+  const float one_tol = 1.0f + accept_tol;
+
+  for (int p = 0; p < wn; ++p) {
+    const int src = p & 63;
+    const bool hi = p >= 64;
+    const float rp = bcast(hi ? rhs1 : rhs0, src);
+    const float xp = bcast(hi ? x1 : x0, src);
+    const float sp = bcast(hi ? s1 : s0, src);
+    const float zp = bcast(hi ? z1 : z0, src);
+    const float dp = bcast(hi ? dg1 : dg0, src);
+    const float target = xp + rp / dp;
+    float qf = rintf(target / sp + zp);
+    qf = fmaxf(fminf(qf, (float)maxq), 0.f);
+    const float xq = sp * (qf - zp);
+    const float dlt = xq - xp;
+    float cand = res + (dlt * dlt) * dp - (2.0f * rp) * dlt;
+    cand = cand < 0.f ? 0.f : cand;
+    if (cand + 1e-12f < res * one_tol) {
+      res = cand;
+      ++acc_count;
+      if (lane == src) {
+        if (hi) { x1 = xq; q1 = (int)qf; d1 = dlt; }
+        else { x0 = xq; q0 = (int)qf; d0 = dlt; }
+      }
+      const float* trow = Ts + p * kWin;
+      rhs0 = rhs0 - dlt * trow[lane];
+      rhs1 = rhs1 - dlt * trow[lane + 64];
+    }
+  }
+  if (v0) {
+    x[o0] = x0;
+    if (q0 >= 0) q[o0] = (uint8_t)q0;
+  }
+  if (v1) {
+    x[o1] = x1;
+    if (q1 >= 0) q[o1] = (uint8_t)q1;
+  }
+  delta[row * kWin + lane] = v0 ? d0 : 0.f;
+  delta[row * kWin + 64 + lane] = v1 ? d1 : 0.f;
+  if (lane == 0) {
+    res_norm[row] = res;
+    accepted[row] += acc_count;
+  }
+}
+
+__global__ void recip_kernel(int64_t n, const float* __restrict__ a, float* __restrict__ out) {
+  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n;
+       j += (int64_t)gridDim.x * blockDim.x)
+    out[j] = 1.0f / a[j];
+}
+
+// q_out = improved ? q_pol : q_in; err_out likewise (mpq/solver.py:749-754).
+__global__ void select_kernel(int64_t rows, int64_t n, const uint8_t* __restrict__ q_in,
+                              const uint8_t* __restrict__ q_pol, const float* __restrict__ err_before,
+                              const float* __restrict__ err_after, uint8_t* __restrict__ q_out,
+                              float* __restrict__ err_out, int32_t* __restrict__ improved) {
+  const int64_t total = rows * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = e / n;
+    const bool imp = err_after[b] + 1e-12f < err_before[b];
+    q_out[e] = imp ? q_pol[e] : q_in[e];
+    if (e % n == 0) {
+      if (err_out) err_out[b] = imp ? err_after[b] : err_before[b];
+      if (improved) improved[b] = imp ? 1 : 0;
+    }
+  }
+}
+
+inline int64_t a64(int64_t v) { return (v + 63) / 64 * 64; }
+
+struct CdPlan {
+  int64_t rows, n, nblocks, nchunks;
+  int splits, bn;
+  int64_t bytes;
+};
+
+CdPlan cd_plan(int64_t rows, int64_t n, int64_t block_rows) {
+  CdPlan c;
+  c.rows = rows;
+  c.n = n;
+  c.nblocks = (rows + block_rows - 1) / block_rows;
+  c.nchunks = (n + 1023) / 1024;
+  int bn = 128;
+  c.splits = choose_splits(rows, n, n, (int64_t)1 << 62, &bn);
+  c.bn = bn;
+  const int64_t mat = a64(rows * n) * 4;
+  int64_t b = 0;
+  b += 4 * mat;                               // Yu, x, res/rhs-scratch, rhs
+  b += (int64_t)c.splits * mat;               // partials
+  b += a64(rows * n);                         // q work (u8)
+  b += 3 * a64(n) * 4;                        // diag, diag_inv, spare
+  b += a64(c.nblocks * n) * 4 * 2;            // gain + order
+  b += a64(c.nblocks * kWin * kWin) * 4;      // window tiles
+  b += a64(rows * kWin) * 4;                  // delta
+  b += 6 * a64(rows) * 4;                     // res_norm, err_before, err_after, accepted, ...
+  b += a64(rows * c.nchunks) * 4;             // chunk partials
+  c.bytes = b;
+  return c;
+}
+
+hipError_t product_splits(const float* A, const float* B, bool trans_b, int64_t rows, int64_t n,
+                          float* P, int splits, int bn, hipStream_t stream) {
+  GemmParams p{};
+  p.M = rows; p.N = n; p.K = n;
+  p.A = A; p.lda = n; p.B = B; p.ldb = n; p.trans_b = trans_b;
+  p.C = P; p.ldc = n; p.split_stride = a64(rows * n);
+  p.alpha = 1.f; p.beta = 0.f; p.mode = kGemmPartials;
+  return gemm_partials(p, splits, bn, stream);
+}
+
+}  // namespace
+
+int64_t uniform_cd_workspace_bytes(int64_t rows, int64_t n, int64_t block_rows) {
+  return cd_plan(rows, n, block_rows).bytes;
+}
+
+int uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                      float accept_tol, const float* W, int64_t ldw, const float* Yu_in,
+                      const uint8_t* q_in, const float* x_in, const float* scale, const float* zero,
+                      int64_t gs, const float* Vs,
+                      const float* H, int select, uint8_t* q_out, float* err_before_out,
+                      float* err_after_out, int32_t* improved, int32_t* accepted_per_row,
+                      void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  const CdPlan pl = cd_plan(rows, n, block_rows);
+  MPQ_CHECK_ARG(workspace_bytes >= pl.bytes, "uniform CD: workspace too small (%lld < %lld bytes)",
+                (long long)workspace_bytes, (long long)pl.bytes);
+  const int64_t G = (n + gs - 1) / gs;
+  const int64_t mat = a64(rows * n) * 4;
+  char* p = static_cast<char*>(workspace);
+  float* Yu = (float*)p; p += mat;
+  float* x = (float*)p; p += mat;
+  float* scratch = (float*)p; p += mat;
+  float* rhs = (float*)p; p += mat;
+  float* P = (float*)p; p += (int64_t)pl.splits * mat;
+  uint8_t* qw = (uint8_t*)p; p += a64(rows * n);
+  float* diag = (float*)p; p += a64(n) * 4;
+  float* diag_inv = (float*)p; p += a64(n) * 4;
+  p += a64(n) * 4;
+  float* gain = (float*)p; p += a64(pl.nblocks * n) * 4;
+  int32_t* order = (int32_t*)p; p += a64(pl.nblocks * n) * 4;
+  float* T = (float*)p; p += a64(pl.nblocks * kWin * kWin) * 4;
+  float* delta = (float*)p; p += a64(rows * kWin) * 4;
+  float* res_norm = (float*)p; p += a64(rows) * 4;
+  float* err_b = (float*)p; p += a64(rows) * 4;
+  float* err_a = (float*)p; p += a64(rows) * 4;
+  int* acc = (int*)p; p += a64(rows) * 4;
+  p += 2 * a64(rows) * 4;
+  float* part = (float*)p;
+  const int nchunks = (int)pl.nchunks;
+  const dim3 eg((unsigned)nchunks, (unsigned)rows);
+  const int64_t sstride = a64(rows * n);
+
+  // Yu = W Vs (or given)
+  if (Yu_in) {
+    MPQ_HIP_TRY(hipMemcpyAsync(Yu, Yu_in, rows * n * 4, hipMemcpyDeviceToDevice, stream));
+  } else {
+    const float* Wc = W;
+    if (ldw != n) {
+      MPQ_HIP_TRY(hipMemcpy2DAsync(scratch, n * 4, W, ldw * 4, n * 4, rows, hipMemcpyDeviceToDevice, stream));
+      Wc = scratch;
+    }
+    MPQ_HIP_TRY(product_splits(Wc, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
+    MPQ_HIP_TRY(splitk_reduce(P, pl.splits, rows, n, Yu, n, 1.f, 0.f, stream));
+  }
+  // x (given, or from the codes); residual and its norm (= error before the polish)
+  if (x_in) {
+    MPQ_HIP_TRY(hipMemcpyAsync(x, x_in, rows * n * 4, hipMemcpyDeviceToDevice, stream));
+  } else {
+    MPQ_HIP_TRY(dequant_groups(q_in, scale, zero, G, gs, rows, n, x, stream));
+  }
+  MPQ_HIP_TRY(hipMemcpyAsync(qw, q_in, rows * n, hipMemcpyDeviceToDevice, stream));
+  MPQ_HIP_TRY(product_splits(x, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
+  hipLaunchKernelGGL(residual_kernel, eg, dim3(256), 0, stream, rows, n, P, pl.splits, sstride, Yu, scratch,
+                     part, nchunks);
+  hipLaunchKernelGGL(rows_sum_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, rows,
+                     nchunks, part, err_b);
+  MPQ_LAUNCH_CHECK();
+  MPQ_HIP_TRY(hipMemcpyAsync(res_norm, err_b, rows * 4, hipMemcpyDeviceToDevice, stream));
+  MPQ_HIP_TRY(hipMemsetAsync(acc, 0, rows * 4, stream));
+  // rhs = residual Vs^T ; diag = |Vs_j|^2
+  MPQ_HIP_TRY(product_splits(scratch, Vs, true, rows, n, P, pl.splits, pl.bn, stream));
+  MPQ_HIP_TRY(splitk_reduce(P, pl.splits, rows, n, rhs, n, 1.f, 0.f, stream));
+  MPQ_HIP_TRY(row_sqnorm(Vs, n, n, 1e-12f, diag, stream));
+  hipLaunchKernelGGL(recip_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, n, diag, diag_inv);
+  MPQ_LAUNCH_CHECK();
+
+  const bool grouped_gemm = (block_rows % 128 == 0) || pl.nblocks == 1;
+  for (int sw = 0; sw < sweeps; ++sw) {
+    hipLaunchKernelGGL(gain_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)pl.nblocks), dim3(256), 0,
+                       stream, rows, n, block_rows, rhs, diag_inv, gain);
+    MPQ_LAUNCH_CHECK();
+    MPQ_HIP_TRY(argsort_desc_rows(gain, pl.nblocks, n, order, stream));
+    for (int64_t w0 = 0; w0 < n; w0 += kWin) {
+      const int wn = (int)std::min<int64_t>(kWin, n - w0);
+      hipLaunchKernelGGL(tile_gather_kernel, dim3(kWin, (unsigned)pl.nblocks), dim3(kWin), 0, stream, n, H,
+                         order, w0, wn, T);
+      hipLaunchKernelGGL(window_kernel, dim3((unsigned)((block_rows + kRowsPerWG - 1) / kRowsPerWG),
+                                             (unsigned)pl.nblocks),
+                         dim3(64 * kRowsPerWG), 0, stream, rows, n, block_rows, maxq, accept_tol, order, w0,
+                         wn, T, scale, zero, G, gs, diag, rhs, x, qw, res_norm, delta, acc);
+      MPQ_LAUNCH_CHECK();
+      // rhs[rows of blk] -= delta[rows of blk] @ H[order[blk][w0:w0+wn], :]
+      if (grouped_gemm) {
+        GemmParams gp{};
+        gp.M = rows; gp.N = n; gp.K = wn;
+        gp.A = delta; gp.lda = kWin;
+        gp.B = H; gp.ldb = n; gp.trans_b = false;
+        gp.b_rows = order + w0; gp.b_rows_group = pl.nblocks == 1 ? 0 : block_rows;
+        gp.b_rows_group_stride = n;
+        gp.C = rhs; gp.ldc = n; gp.alpha = -1.f; gp.beta = 1.f; gp.mode = kGemmAxpby;
+        MPQ_HIP_TRY(gemm_partials(gp, 1, 128, stream));
+      } else {
+        for (int64_t b = 0; b < pl.nblocks; ++b) {
+          const int64_t r0 = b * block_rows;
+          GemmParams gp{};
+          gp.M = std::min<int64_t>(block_rows, rows - r0); gp.N = n; gp.K = wn;
+          gp.A = delta + r0 * kWin; gp.lda = kWin;
+          gp.B = H; gp.ldb = n; gp.trans_b = false;
+          gp.b_rows = order + b * n + w0;
+          gp.C = rhs + r0 * n; gp.ldc = n; gp.alpha = -1.f; gp.beta = 1.f; gp.mode = kGemmAxpby;
+          MPQ_HIP_TRY(gemm_partials(gp, 1, 128, stream));
+        }
+      }
+    }
+  }
+  // error after the polish, from the final codes (mpq/solver.py:323-330)
+  MPQ_HIP_TRY(dequant_groups(qw, scale, zero, G, gs, rows, n, x, stream));
+  MPQ_HIP_TRY(product_splits(x, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
+  hipLaunchKernelGGL(residual_kernel, eg, dim3(256), 0, stream, rows, n, P, pl.splits, sstride, Yu,
+                     (float*)nullptr, part, nchunks);
+  hipLaunchKernelGGL(rows_sum_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, rows,
+                     nchunks, part, err_a);
+  MPQ_LAUNCH_CHECK();
+  if (err_before_out) MPQ_HIP_TRY(hipMemcpyAsync(err_before_out, err_b, rows * 4, hipMemcpyDeviceToDevice, stream));
+  if (err_after_out) MPQ_HIP_TRY(hipMemcpyAsync(err_after_out, err_a, rows * 4, hipMemcpyDeviceToDevice, stream));
+  if (select) {
+    int64_t blocks = (rows * n + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(select_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, rows, n, q_in, qw, err_b,
+                       err_a, q_out, (float*)nullptr, improved);
+    MPQ_LAUNCH_CHECK();
+  } else {
+    MPQ_HIP_TRY(hipMemcpyAsync(q_out, qw, rows * n, hipMemcpyDeviceToDevice, stream));
+  }
+  if (accepted_per_row) {
+    MPQ_HIP_TRY(hipMemcpyAsync(accepted_per_row, acc, rows * 4, hipMemcpyDeviceToDevice, stream));
+  }
+  return kOk;
+}
+
+}  // namespace mpq
+
+extern "C" int64_t mpq_uniform_cd_workspace_size(int64_t rows, int64_t n, int64_t block_rows) {
+  if (rows <= 0 || n <= 0 || block_rows <= 0) return 0;
+  return mpq::uniform_cd_workspace_bytes(rows, n, block_rows);
+}
+
+extern "C" int mpq_uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                                     float accept_tol, const float* W, int64_t ldw, const float* Yu,
+                                     const uint8_t* q_in, const float* x_in, const float* scale,
+                                     const float* zero, int64_t group_size,
+                                     const float* Vs, const float* H, int select, uint8_t* q_out,
+                                     float* err_before, float* err_after, int32_t* improved,
+                                     int32_t* accepted_per_row, void* workspace, int64_t workspace_bytes,
+                                     hipStream_t stream) {
+  MPQ_CHECK_ARG(rows > 0 && n > 0, "mpq_uniform_cd_polish: empty problem");
+  MPQ_CHECK_ARG(maxq >= 1 && maxq <= 255, "mpq_uniform_cd_polish: maxq must be in [1, 255]");
+  MPQ_CHECK_ARG(block_rows >= 1 && sweeps >= 0 && group_size >= 1, "mpq_uniform_cd_polish: bad sizes");
+  MPQ_CHECK_ARG(n <= 16384, "mpq_uniform_cd_polish: n <= 16384 supported (greedy-order sort in LDS)");
+  MPQ_CHECK_ARG(rows <= 65535, "mpq_uniform_cd_polish: at most 65535 rows per call");
+  MPQ_CHECK_ARG((W || Yu) && q_in && scale && zero && Vs && H && q_out && workspace,
+                "mpq_uniform_cd_polish: null argument");
+  MPQ_CHECK_ARG(!W || ldw >= n, "mpq_uniform_cd_polish: ldw < n");
+  return mpq::uniform_cd_polish(rows, n, maxq, block_rows, sweeps, accept_tol, W, ldw, Yu, q_in, x_in, scale, zero,
+                                group_size, Vs, H, select, q_out, err_before, err_after, improved,
+                                accepted_per_row, workspace, workspace_bytes,
+                                stream);
+}

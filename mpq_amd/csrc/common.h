@@ -17,6 +17,7 @@ enum Status : int {
   kInvalidArgument = -1,
   kHipError = -2,
   kUnsupported = -3,
+  kNumerical = -4,
 };
 
 void set_error(const char* fmt, ...);
@@ -49,3 +50,52 @@ void set_error_code(int code);
 #define MPQ_LAUNCH_CHECK() MPQ_HIP_TRY(hipGetLastError())
 
 static inline int64_t mpq_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+namespace mpq {
+
+// Deterministic work-group sum (fixed tree: lane shuffles, then waves in order).
+// All threads must call it; `scratch` holds blockDim.x/64 floats.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = (blockDim.x + 63) >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float total = scratch[0];
+  for (int w = 1; w < nwaves; ++w) total += scratch[w];
+  __syncthreads();
+  return total;
+}
+
+__device__ __forceinline__ double block_sum_f64(double v, double* scratch) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = (blockDim.x + 63) >> 6;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  double total = scratch[0];
+  for (int w = 1; w < nwaves; ++w) total += scratch[w];
+  __syncthreads();
+  return total;
+}
+
+// torch.nan_to_num + clamp_min semantics used by the VAMP precision updates.
+__device__ __forceinline__ float nan_to_num_clamp_min(float x, float nan_v, float posinf_v,
+                                                      float neginf_v, float lo) {
+  if (isnan(x)) x = nan_v;
+  else if (isinf(x)) x = x > 0.f ? posinf_v : neginf_v;
+  return x < lo ? lo : x;
+}
+
+}  // namespace mpq

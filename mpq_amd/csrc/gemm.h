@@ -1,0 +1,50 @@
+// Internal interface of the fp32 MFMA GEMM (gemm.hip).
+#pragma once
+
+#include "common.h"
+
+namespace mpq {
+
+enum GemmMode : int {
+  kGemmPartials = 0,  // C[split] = partial product (C = workspace, split_stride apart)
+  kGemmAxpby = 1,     // single split: C = alpha * A*op(B) + beta * C
+};
+
+struct GemmParams {
+  int64_t M, N, K;
+  const float* A;
+  int64_t lda;
+  const float* B;
+  int64_t ldb;
+  const int32_t* b_rows;  // optional row gather of B (trans_b == false only)
+  int64_t b_rows_group;   // if > 0: M tile at m0 uses b_rows + (m0 / b_rows_group) * b_rows_group_stride
+  int64_t b_rows_group_stride;  //   (b_rows_group must be a multiple of the 128-row M tile)
+  float* C;
+  int64_t ldc;
+  int64_t split_stride;
+  int64_t k_per_split;
+  float alpha, beta;
+  int mode;
+  bool trans_b;
+  bool a_vec4, b_vec4;
+};
+
+// Split-K count and N tile (64 or 128) for an M x N x K product with the given
+// workspace capacity (floats); 1 split when no workspace.
+int choose_splits(int64_t M, int64_t N, int64_t K, int64_t workspace_floats, int* bn_out);
+
+// Launch the partial-product kernel: `splits` K slices written to p.C with
+// p.split_stride apart (mode kGemmPartials), or one slice with mode kGemmAxpby.
+hipError_t gemm_partials(GemmParams p, int splits, int bn, hipStream_t stream);
+
+// C = alpha * sum_s P[s] + beta * C (fixed split order).
+hipError_t splitk_reduce(const float* P, int splits, int64_t M, int64_t N, float* C, int64_t ldc,
+                         float alpha, float beta, hipStream_t stream);
+
+// Full product with the automatic split choice; `workspace` may be null (1 split).
+hipError_t gemm(const float* A, int64_t lda, const float* B, int64_t ldb, bool trans_b,
+                const int32_t* b_rows, float* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                float alpha, float beta, float* workspace, int64_t workspace_floats,
+                hipStream_t stream);
+
+}  // namespace mpq

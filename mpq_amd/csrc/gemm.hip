@@ -1,0 +1,329 @@
+// fp32 MFMA GEMM for the rank-space contractions of the VAMP / CD path.
+//
+//   P[s] = A[:, Ks] * op(B)[Ks, :]        (split-K partials, s = 0..splits-1)
+//   C    = alpha * sum_s P[s] + beta * C  (deterministic split order)
+//
+// A is M x K row-major (lda).  op(B)(k, n) is B[k*ldb + n] (trans_b = 0),
+// B[n*ldb + k] (trans_b = 1, e.g. V^T from V), or B[rows[k]*ldb + n] (row gather,
+// used by the CD Schur update H[order[window], :]).
+//
+// Tiling for gfx950: 256 threads = 4 wave64s; work-group tile BM x BN, wave tile
+// WM x WN built from v_mfma_f32_32x32x2_f32 (full fp32 precision).  Tiles are
+// staged through LDS as [k][m] / [k][n] (each MFMA operand read is 32 consecutive
+// floats), double-buffered with a register prefetch of the next K slab.
+#include "gemm.h"
+
+namespace mpq {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBK = 16;
+constexpr int kThreads = 256;
+
+template <int BM, int BN, int WM, int WN, bool TRANS_B, bool GATHER_B>
+__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
+  constexpr int WAVES_N = BN / WN;
+  constexpr int MI = WM / 32;
+  constexpr int NI = WN / 32;
+  constexpr int PAD = 4;
+  constexpr int LDA_S = BM + PAD;
+  constexpr int LDB_S = BN + PAD;
+  // per-thread loads per K slab
+  constexpr int A_F4 = BM * kBK / 4 / kThreads;
+  constexpr int B_F4 = BN * kBK / 4 / kThreads;
+  static_assert(A_F4 >= 1 && B_F4 >= 1, "tile too small for 256 threads");
+
+  __shared__ float As[2][kBK][LDA_S];
+  __shared__ float Bs[2][kBK][LDB_S];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm0 = (wave / WAVES_N) * WM;
+  const int wn0 = (wave % WAVES_N) * WN;
+
+  const int64_t m0 = (int64_t)blockIdx.y * BM;
+  const int64_t n0 = (int64_t)blockIdx.x * BN;
+  const int split = blockIdx.z;
+  const int32_t* b_rows = p.b_rows;
+  if (GATHER_B && p.b_rows_group > 0) b_rows += (m0 / p.b_rows_group) * p.b_rows_group_stride;
+  const int64_t kbeg = (int64_t)split * p.k_per_split;
+  int64_t kend = kbeg + p.k_per_split;
+  if (kend > p.K) kend = p.K;
+
+  floatx16 acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  float4 ra[A_F4];
+  float4 rb[B_F4];
+
+  // A slab: element (m, k) = A[(m0+m)*lda + k0 + k]; thread t loads float4 along k.
+  auto load_a = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < A_F4; ++i) {
+      const int t = tid + i * kThreads;
+      const int m = t / (kBK / 4);
+      const int kq = (t % (kBK / 4)) * 4;
+      const int64_t gm = m0 + m;
+      const int64_t gk = k0 + kq;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (gm < p.M) {
+        const float* src = p.A + gm * p.lda + gk;
+        if (gk + 3 < kend && p.a_vec4) {
+          v = *reinterpret_cast<const float4*>(src);
+        } else {
+          if (gk + 0 < kend) v.x = src[0];
+          if (gk + 1 < kend) v.y = src[1];
+          if (gk + 2 < kend) v.z = src[2];
+          if (gk + 3 < kend) v.w = src[3];
+        }
+      }
+      ra[i] = v;
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_F4; ++i) {
+      const int t = tid + i * kThreads;
+      const int m = t / (kBK / 4);
+      const int kq = (t % (kBK / 4)) * 4;
+      As[buf][kq + 0][m] = ra[i].x;
+      As[buf][kq + 1][m] = ra[i].y;
+      As[buf][kq + 2][m] = ra[i].z;
+      As[buf][kq + 3][m] = ra[i].w;
+    }
+  };
+  auto load_b = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < B_F4; ++i) {
+      const int t = tid + i * kThreads;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (!TRANS_B) {
+        const int k = t / (BN / 4);
+        const int nq = (t % (BN / 4)) * 4;
+        const int64_t gk = k0 + k;
+        const int64_t gn = n0 + nq;
+        if (gk < kend) {
+          int64_t row = gk;
+          if constexpr (GATHER_B) row = b_rows[gk];
+          const float* src = p.B + row * p.ldb + gn;
+          if (gn + 3 < p.N && p.b_vec4) {
+            v = *reinterpret_cast<const float4*>(src);
+          } else {
+            if (gn + 0 < p.N) v.x = src[0];
+            if (gn + 1 < p.N) v.y = src[1];
+            if (gn + 2 < p.N) v.z = src[2];
+            if (gn + 3 < p.N) v.w = src[3];
+          }
+        }
+      } else {
+        const int n = t / (kBK / 4);
+        const int kq = (t % (kBK / 4)) * 4;
+        const int64_t gn = n0 + n;
+        const int64_t gk = k0 + kq;
+        if (gn < p.N) {
+          const float* src = p.B + gn * p.ldb + gk;
+          if (gk + 3 < kend && p.b_vec4) {
+            v = *reinterpret_cast<const float4*>(src);
+          } else {
+            if (gk + 0 < kend) v.x = src[0];
+            if (gk + 1 < kend) v.y = src[1];
+            if (gk + 2 < kend) v.z = src[2];
+            if (gk + 3 < kend) v.w = src[3];
+          }
+        }
+      }
+      rb[i] = v;
+    }
+  };
+  auto store_b = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < B_F4; ++i) {
+      const int t = tid + i * kThreads;
+      if constexpr (!TRANS_B) {
+        const int k = t / (BN / 4);
+        const int nq = (t % (BN / 4)) * 4;
+        *reinterpret_cast<float4*>(&Bs[buf][k][nq]) = rb[i];
+      } else {
+        const int n = t / (kBK / 4);
+        const int kq = (t % (kBK / 4)) * 4;
+        Bs[buf][kq + 0][n] = rb[i].x;
+        Bs[buf][kq + 1][n] = rb[i].y;
+        Bs[buf][kq + 2][n] = rb[i].z;
+        Bs[buf][kq + 3][n] = rb[i].w;
+      }
+    }
+  };
+
+  const int64_t nslab = (kend - kbeg + kBK - 1) / kBK;
+  if (nslab > 0) {
+    load_a(kbeg);
+    load_b(kbeg);
+    store_a(0);
+    store_b(0);
+    __syncthreads();
+    for (int64_t s = 0; s < nslab; ++s) {
+      const int buf = (int)(s & 1);
+      if (s + 1 < nslab) {
+        load_a(kbeg + (s + 1) * kBK);
+        load_b(kbeg + (s + 1) * kBK);
+      }
+      const int kl = lane >> 5;  // operand k row within a 2-step
+      const int ml = lane & 31;
+#pragma unroll
+      for (int kk = 0; kk < kBK; kk += 2) {
+        float a[MI], b[NI];
+#pragma unroll
+        for (int i = 0; i < MI; ++i) a[i] = As[buf][kk + kl][wm0 + i * 32 + ml];
+#pragma unroll
+        for (int j = 0; j < NI; ++j) b[j] = Bs[buf][kk + kl][wn0 + j * 32 + ml];
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+      }
+      if (s + 1 < nslab) {
+        store_a(buf ^ 1);
+        store_b(buf ^ 1);
+      }
+      __syncthreads();
+    }
+  }
+
+  // Epilogue: lane l, accumulator v -> row 8*(v/4) + 4*(l/32) + v%4, col l%32.
+  const int col = lane & 31;
+  const int rbase = (lane >> 5) * 4;
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int64_t gn = n0 + wn0 + j * 32 + col;
+      if (gn >= p.N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t gm = m0 + wm0 + i * 32 + (v >> 2) * 8 + rbase + (v & 3);
+        if (gm >= p.M) continue;
+        const float val = acc[i][j][v];
+        if (p.mode == kGemmPartials) {
+          p.C[(int64_t)split * p.split_stride + gm * p.ldc + gn] = val;
+        } else {  // kGemmAxpby, single split: C = alpha*acc + beta*C
+          float* dst = p.C + gm * p.ldc + gn;
+          *dst = p.beta == 0.f ? p.alpha * val : p.alpha * val + p.beta * *dst;
+        }
+      }
+    }
+  }
+}
+
+// Deterministic split-K reduction: C = alpha * sum_s P[s] + beta * C.
+__global__ void splitk_reduce_kernel(const float* __restrict__ P, int splits, int64_t split_stride,
+                                     int64_t M, int64_t N, float* __restrict__ C, int64_t ldc,
+                                     float alpha, float beta) {
+  const int64_t total = M * N;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = e / N, n = e % N;
+    float acc = P[m * N + n];
+    for (int s = 1; s < splits; ++s) acc = acc + P[(int64_t)s * split_stride + m * N + n];
+    float* dst = C + m * ldc + n;
+    *dst = beta == 0.f ? alpha * acc : alpha * acc + beta * *dst;
+  }
+}
+
+template <int BM, int BN, int WM, int WN>
+hipError_t launch_cfg(const GemmParams& p, dim3 grid, hipStream_t stream) {
+  if (p.trans_b) {
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM, WN, true, false>), grid, dim3(kThreads), 0, stream, p);
+  } else if (p.b_rows) {
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM, WN, false, true>), grid, dim3(kThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM, WN, false, false>), grid, dim3(kThreads), 0, stream, p);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int choose_splits(int64_t M, int64_t N, int64_t K, int64_t workspace_floats, int* bn_out) {
+  // 128x128 tiles when the N extent alone fills the chip, else 128x64.
+  const int64_t tiles_m = (M + 127) / 128;
+  int bn = 128;
+  if (tiles_m * ((N + 127) / 128) < 512) bn = 64;
+  const int64_t tiles = tiles_m * ((N + bn - 1) / bn);
+  int splits = 1;
+  const int64_t target = 1024;  // ~4 work-groups per CU on 256 CUs
+  while (splits < 32 && tiles * splits * 2 <= target && K / (splits * 2) >= 256 &&
+         (int64_t)(splits * 2) * M * N <= workspace_floats)
+    splits *= 2;
+  *bn_out = bn;
+  return splits;
+}
+
+hipError_t gemm_partials(GemmParams p, int splits, int bn, hipStream_t stream) {
+  p.mode = splits > 1 ? kGemmPartials : p.mode;
+  const int64_t kps = ((p.K + splits - 1) / splits + kBK - 1) / kBK * kBK;
+  p.k_per_split = kps > 0 ? kps : kBK;
+  p.a_vec4 = ((reinterpret_cast<uintptr_t>(p.A) & 15u) == 0) && (p.lda % 4 == 0);
+  p.b_vec4 = ((reinterpret_cast<uintptr_t>(p.B) & 15u) == 0) && (p.ldb % 4 == 0);
+  dim3 grid((unsigned)((p.N + bn - 1) / bn), (unsigned)((p.M + 127) / 128), (unsigned)splits);
+  if (bn == 128) return launch_cfg<128, 128, 64, 64>(p, grid, stream);
+  return launch_cfg<128, 64, 64, 32>(p, grid, stream);
+}
+
+hipError_t splitk_reduce(const float* P, int splits, int64_t M, int64_t N, float* C, int64_t ldc,
+                         float alpha, float beta, hipStream_t stream) {
+  const int64_t total = M * N;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, P, splits,
+                     M * N, M, N, C, ldc, alpha, beta);
+  return hipGetLastError();
+}
+
+hipError_t gemm(const float* A, int64_t lda, const float* B, int64_t ldb, bool trans_b,
+                const int32_t* b_rows, float* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                float alpha, float beta, float* workspace, int64_t workspace_floats,
+                hipStream_t stream) {
+  int bn = 128;
+  int splits = choose_splits(M, N, K, workspace ? workspace_floats : 0, &bn);
+  GemmParams p{};
+  p.M = M; p.N = N; p.K = K;
+  p.A = A; p.lda = lda; p.B = B; p.ldb = ldb; p.trans_b = trans_b; p.b_rows = b_rows;
+  p.alpha = alpha; p.beta = beta;
+  if (splits == 1) {
+    p.mode = kGemmAxpby;
+    p.C = C; p.ldc = ldc;
+    return gemm_partials(p, 1, bn, stream);
+  }
+  p.mode = kGemmPartials;
+  p.C = workspace; p.ldc = N; p.split_stride = M * N;
+  hipError_t e = gemm_partials(p, splits, bn, stream);
+  if (e != hipSuccess) return e;
+  return splitk_reduce(workspace, splits, M, N, C, ldc, alpha, beta, stream);
+}
+
+}  // namespace mpq
+
+extern "C" int mpq_gemm_f32(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
+                            const float* B, int64_t ldb, int trans_b, const int32_t* b_rows,
+                            float* C, int64_t ldc, float alpha, float beta, float* workspace,
+                            int64_t workspace_floats, hipStream_t stream) {
+  MPQ_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "mpq_gemm_f32: negative extent");
+  if (M == 0 || N == 0) return mpq::kOk;
+  MPQ_CHECK_ARG(A && B && C, "mpq_gemm_f32: null operand");
+  MPQ_CHECK_ARG(lda >= K && ldc >= N, "mpq_gemm_f32: leading dimension too small");
+  MPQ_CHECK_ARG(trans_b ? ldb >= K : ldb >= N, "mpq_gemm_f32: ldb too small");
+  MPQ_CHECK_ARG(!(trans_b && b_rows), "mpq_gemm_f32: row gather needs trans_b = 0");
+  MPQ_CHECK_ARG(M <= (int64_t)65535 * 128 && N <= (int64_t)0x7fffffff * 64,
+                "mpq_gemm_f32: extent too large");
+  MPQ_HIP_TRY(mpq::gemm(A, lda, B, ldb, trans_b != 0, b_rows, C, ldc, M, N, K, alpha, beta,
+                        workspace, workspace_floats, stream));
+  return mpq::kOk;
+}

@@ -1,0 +1,23 @@
+// Internal interface of the uniform-grid VAMP solver (uniform_vamp.hip).
+#pragma once
+
+#include "common.h"
+
+#include "mpq_amd.h"
+
+namespace mpq {
+
+struct UniformProblem {
+  int64_t rows, n;
+  int maxq;
+  const float* W;        // rows x n (prior centre and target)
+  const float* x_init;   // rows x n RTN decision (init_from rtn; gamma1 init)
+  const float* scale;    // rows x G (G = ceil(n / group_size))
+  const float* zero;     // rows x G
+  int64_t group_size;
+  const float* V;        // n x n eigenvectors (columns)
+  const float* S;        // n sqrt-eigenvalues
+  int64_t ldw;           // row stride of W / x_init (elements)
+};
+
+}  // namespace mpq

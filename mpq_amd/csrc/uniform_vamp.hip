@@ -1,0 +1,837 @@
+// Uniform-grid VAMP on one row block (gfx950).
+//
+// Replaces mpq/solver.py:426-830 (solve_uniform_rankspace_vamp, without the
+// polish, which is mpq_uniform_cd_polish) together with
+//   mpq/priors/uniform.py:99-213   discrete_uniform_mmse      -> uniform_denoise_kernel
+//   mpq/linear.py:10-56            linear_mmse_exact          -> GEMM + lmmse_epi1/epi2
+//   mpq/linear.py:59-82            em_update_obs_precision    -> rows_lmmse_kernel + host
+//   mpq/linear.py:85-94            vamp_rankspace_error       -> GEMM + err_epi_kernel
+//   mpq/solver.py:833-850          _uniform_hard_decision     -> uniform_denoise_kernel<kHard*>
+//
+// Layout: every per-element array is rows x n row-major fp32 in HBM; codes are
+// uint8.  Quantizer parameters stay in group form (rows x G) and are expanded on
+// the fly.  Per-row reductions are written as fixed-order partial sums per
+// 1024-column chunk, so every result is bit-reproducible run to run.
+//
+// Control flow is the reference's, driven from the host with two small status
+// reads per iteration (after the denoiser: alpha1 / gamma2 validity; after the
+// hard-state error: error mean, EM statistic).  All arithmetic follows the
+// reference's operation order where it matters for decisions (scores, MAP,
+// rounding); the file is compiled with -ffp-contract=off.
+#include <cmath>
+#include <cstring>
+
+#include "gemm.h"
+#include "kernels.h"
+#include "uniform_vamp.h"
+
+namespace mpq {
+namespace {
+
+constexpr int kEW = 256;             // threads per element-wise work-group
+constexpr int kPer = 4;              // elements per thread
+constexpr int kChunk = kEW * kPer;   // columns per work-group
+constexpr float kAlphaEps = 1e-7f;
+constexpr float kPrecEps = 1e-12f;
+
+__device__ __forceinline__ float one_minus_alpha_eps() { return (float)(1.0 - 1e-7); }
+
+struct VampStatus {
+  int a1_invalid;
+  int a1_nonfinite;
+  int g2new_invalid;
+  int g2_invalid;
+  int a2_clip;
+  int g1_invalid;
+  int pad0, pad1;
+  float a1_mean;
+  float a2_mean;
+  float err_mean;
+  float em_mean;
+  float err_sum;
+  float pad2, pad3, pad4;
+};
+
+enum DenoiseMode : int { kPosterior = 0, kHardMap = 1, kHardRoundMean = 2, kFull = 3 };
+
+__device__ __forceinline__ float grp(const float* a, int64_t b, int64_t G, int64_t gs, int64_t j) {
+  return a[b * G + j / gs];
+}
+
+// Per element: posterior of a uniform grid a_q = s(q - z), q = 0..maxq, under the
+// channel N(r1, 1/gamma) and the prior N(W, (tau*s)^2)  (mpq/priors/uniform.py:177-191).
+template <int MODE>
+__global__ __launch_bounds__(kEW) void uniform_denoise_kernel(
+    const float* __restrict__ r1, const float* __restrict__ gamma, const float* __restrict__ W,
+    int64_t ldw, const float* __restrict__ scale, const float* __restrict__ zero, int64_t G,
+    int64_t gs, int64_t n, int maxq, float tau, float* __restrict__ mean_out,
+    float* __restrict__ var_part, uint8_t* __restrict__ q_out, float* __restrict__ x_out) {
+  __shared__ float red[kEW / 64];
+  const int64_t b = blockIdx.y;
+  const int nchunks = gridDim.x;
+  const float g = gamma[b];
+  const float mh = -0.5f * g;
+  float vsum = 0.f;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
+    if (j >= n) continue;
+    const float r = r1[b * n + j];
+    const float c = W[b * ldw + j];
+    const float s = grp(scale, b, G, gs, j);
+    const float z = grp(zero, b, G, gs, j);
+    float st2 = 0.f;
+    if (tau > 0.f) {
+      const float sc = s < 1e-12f ? 1e-12f : s;
+      const float ts = tau * sc;
+      st2 = ts * ts;
+    }
+    // pass 1: scores, max, first argmax
+    float mx = -INFINITY;
+    int arg = 0;
+    for (int q = 0; q <= maxq; ++q) {
+      const float a = s * ((float)q - z);
+      const float d = a - r;
+      float score = mh * (d * d);
+      if (tau > 0.f) {
+        const float dc = a - c;
+        score = score - (0.5f * (dc * dc)) / st2;
+      }
+      if (score > mx) {
+        mx = score;
+        arg = q;
+      }
+    }
+    float mean = 0.f;
+    if (MODE == kPosterior || MODE == kHardRoundMean || MODE == kFull) {
+      // pass 2: softmax moments
+      float zsum = 0.f, m1 = 0.f, m2 = 0.f;
+      for (int q = 0; q <= maxq; ++q) {
+        const float a = s * ((float)q - z);
+        const float d = a - r;
+        float score = mh * (d * d);
+        if (tau > 0.f) {
+          const float dc = a - c;
+          score = score - (0.5f * (dc * dc)) / st2;
+        }
+        const float w = expf(score - mx);
+        zsum += w;
+        m1 += w * a;
+        m2 += w * (a * a);
+      }
+      mean = m1 / zsum;
+      const float second = m2 / zsum;
+      float var = second - mean * mean;
+      var = var < 0.f ? 0.f : var;
+      if (MODE == kPosterior) {
+        mean_out[b * n + j] = mean;
+        vsum += var;
+      }
+      if (MODE == kFull) {
+        mean_out[b * n + j] = mean;
+        var_part[b * n + j] = var;  // per-element variance in this mode
+        reinterpret_cast<int64_t*>(q_out)[b * n + j] = arg;
+        x_out[b * n + j] = s * ((float)arg - z);
+      }
+    }
+    if (MODE == kHardMap || MODE == kHardRoundMean) {
+      int q = arg;
+      if (MODE == kHardRoundMean) {
+        const float sc = s < 1e-12f ? 1e-12f : s;
+        float qf = rintf(mean / sc + z);
+        qf = qf < 0.f ? 0.f : (qf > (float)maxq ? (float)maxq : qf);
+        q = (int)qf;
+      }
+      q_out[b * n + j] = (uint8_t)q;
+      x_out[b * n + j] = s * ((float)q - z);
+    }
+  }
+  if (MODE == kPosterior) {
+    const float tot = block_sum(vsum, red);
+    if (threadIdx.x == 0) var_part[b * nchunks + blockIdx.x] = tot;
+  }
+}
+
+// alpha1 = gamma * mean_j(var) per row (mpq/priors/uniform.py:191), one work-group per row.
+__global__ __launch_bounds__(kEW) void row_alpha_kernel(int64_t n, const float* __restrict__ var,
+                                                        const float* __restrict__ gamma,
+                                                        float* __restrict__ alpha1) {
+  __shared__ float red[kEW / 64];
+  const int64_t b = blockIdx.x;
+  float acc = 0.f;
+  for (int64_t j = threadIdx.x; j < n; j += blockDim.x) acc += var[b * n + j];
+  const float t = block_sum(acc, red);
+  if (threadIdx.x == 0) alpha1[b] = gamma[b] * (t / (float)n);
+}
+
+// Row statistics after the denoiser (mpq/solver.py:575-615): alpha1, eta1,
+// gamma2_new, damped gamma2, validity counts.  One work-group, rows looped.
+__global__ __launch_bounds__(kEW) void rows_alpha1_kernel(
+    int64_t rows, int64_t n, int nchunks, const float* __restrict__ var_part,
+    const float* __restrict__ g1w, int has_prev, float damping, const float* __restrict__ g2prev,
+    float* __restrict__ alpha1_raw, float* __restrict__ alpha1, float* __restrict__ eta1,
+    float* __restrict__ g2new, float* __restrict__ g2, VampStatus* __restrict__ st) {
+  __shared__ float red[kEW / 64];
+  int inval = 0, nonfin = 0, g2n_bad = 0, g2_bad = 0;
+  const float hi = one_minus_alpha_eps();
+  for (int64_t b = threadIdx.x; b < rows; b += blockDim.x) {
+    float vs = var_part[b * nchunks];
+    for (int c = 1; c < nchunks; ++c) vs = vs + var_part[b * nchunks + c];
+    const float a1 = g1w[b] * (vs / (float)n);
+    alpha1_raw[b] = a1;
+    const bool fin = isfinite(a1);
+    const bool valid = fin && a1 > kAlphaEps && a1 < hi;
+    inval += !valid;
+    nonfin += !fin;
+    float a1c = a1;
+    if (isnan(a1c)) a1c = 0.5f;
+    else if (isinf(a1c)) a1c = a1c > 0.f ? hi : kAlphaEps;
+    a1c = a1c < kAlphaEps ? kAlphaEps : (a1c > hi ? hi : a1c);
+    alpha1[b] = a1c;
+    const float e1 = g1w[b] / a1c;
+    eta1[b] = e1;
+    const float gn = nan_to_num_clamp_min(e1 - g1w[b], 1e-12f, 1e12f, 1e-12f, kPrecEps);
+    g2new[b] = gn;
+    g2n_bad += !(isfinite(gn) && gn > kPrecEps);
+    float gd = gn;
+    if (has_prev && damping < 1.f) {
+      if (damping <= 0.f) {
+        gd = g2prev[b];
+      } else {
+        const float p = g2prev[b] < 1e-12f ? 1e-12f : g2prev[b];
+        const float q = gn < 1e-12f ? 1e-12f : gn;
+        gd = expf((1.0f - damping) * logf(p) + damping * logf(q));
+      }
+    }
+    g2[b] = gd;
+    g2_bad += !(isfinite(gd) && gd > kPrecEps);
+  }
+  // counts: exact in fp32 for < 2^24 rows
+  const float s_inval = block_sum((float)inval, red);
+  const float s_nonfin = block_sum((float)nonfin, red);
+  const float s_g2n = block_sum((float)g2n_bad, red);
+  const float s_g2 = block_sum((float)g2_bad, red);
+  float a1sum = 0.f;
+  if (threadIdx.x == 0) {
+    for (int64_t b = 0; b < rows; ++b) a1sum += alpha1[b];
+    st->a1_invalid = (int)s_inval;
+    st->a1_nonfinite = (int)s_nonfin;
+    st->g2new_invalid = (int)s_g2n;
+    st->g2_invalid = (int)s_g2;
+    st->a1_mean = a1sum / (float)rows;
+  }
+}
+
+// gamma retry (mpq/solver.py:594-596).
+__global__ void rows_retry_kernel(int64_t rows, const float* __restrict__ alpha1_raw, float factor,
+                                  float* __restrict__ g1w) {
+  const float hi = one_minus_alpha_eps();
+  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < rows;
+       b += (int64_t)gridDim.x * blockDim.x) {
+    const float a = alpha1_raw[b];
+    float g = g1w[b];
+    if (a <= kAlphaEps) g = g / factor;
+    if (a >= hi) g = g * factor;
+    g1w[b] = g < 1e-12f ? 1e-12f : g;
+  }
+}
+
+// r2 message (mpq/solver.py:605-612).
+__global__ __launch_bounds__(kEW) void msg_r2_kernel(int64_t n, const float* __restrict__ x1,
+                                                     const float* __restrict__ r1,
+                                                     const float* __restrict__ eta1,
+                                                     const float* __restrict__ g1w,
+                                                     const float* __restrict__ g2new, int has_prev,
+                                                     float damping, const float* __restrict__ r2prev,
+                                                     float* __restrict__ r2) {
+  const int64_t b = blockIdx.y;
+  const float e1 = eta1[b], gw = g1w[b], gn = g2new[b];
+  const bool damp = has_prev && damping < 1.f;
+  const float keep = 1.0f - damping;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
+    if (j >= n) continue;
+    const int64_t o = b * n + j;
+    const float rn = (e1 * x1[o] - gw * r1[o]) / gn;
+    r2[o] = damp ? keep * r2prev[o] + damping * rn : rn;
+  }
+}
+
+// LMMSE part 1 (mpq/linear.py:44-55): from P = r2 @ V, per element
+//   residual_before = Yu - P*s, denom = obs*s^2 + g2, coeff = obs*s/denom,
+//   c = residual_before*coeff (input of the second product); row partial sums of
+//   1/denom (alpha2), residual_after^2 and s^2/denom (EM, mpq/linear.py:74-77).
+__global__ __launch_bounds__(kEW) void lmmse_epi1_kernel(
+    int64_t n, const float* __restrict__ P, int splits, int64_t split_stride,
+    const float* __restrict__ Yu, const float* __restrict__ S, const float* __restrict__ g2,
+    float obs, float* __restrict__ c_out, float* __restrict__ part3) {
+  __shared__ float red[kEW / 64];
+  const int64_t b = blockIdx.y;
+  const int nchunks = gridDim.x;
+  const float gb = g2[b];
+  float sinv = 0.f, sres = 0.f, strace = 0.f;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
+    if (j >= n) continue;
+    const int64_t o = b * n + j;
+    float r2v = P[o];
+    for (int s = 1; s < splits; ++s) r2v = r2v + P[(int64_t)s * split_stride + o];
+    const float sj = S[j];
+    const float s2 = sj * sj;
+    const float denom = obs * s2 + gb;
+    const float rb = Yu[o] - r2v * sj;
+    const float coeff = (obs * sj) / denom;
+    c_out[o] = rb * coeff;
+    sinv += 1.0f / denom;
+    const float ra = rb * (gb / denom);
+    sres += ra * ra;
+    strace += s2 / denom;
+  }
+  const float t0 = block_sum(sinv, red);
+  const float t1 = block_sum(sres, red);
+  const float t2 = block_sum(strace, red);
+  if (threadIdx.x == 0) {
+    float* o = part3 + (b * nchunks + blockIdx.x) * 3;
+    o[0] = t0;
+    o[1] = t1;
+    o[2] = t2;
+  }
+}
+
+// Row update after LMMSE part 1 (mpq/solver.py:626-653): alpha2, eta2,
+// gamma1_new, damped gamma1 (written in place), EM row statistic.
+__global__ __launch_bounds__(kEW) void rows_lmmse_kernel(
+    int64_t rows, int64_t n, int64_t rank, int nchunks, const float* __restrict__ part3,
+    const float* __restrict__ g2, float damping, float* __restrict__ eta2,
+    float* __restrict__ g1new, float* __restrict__ g1, VampStatus* __restrict__ st) {
+  __shared__ float red[kEW / 64];
+  const float hi = one_minus_alpha_eps();
+  const float c0 = (float)(1.0 - (double)rank / (double)n);
+  int clip = 0;
+  for (int64_t b = threadIdx.x; b < rows; b += blockDim.x) {
+    const float* pp = part3 + b * nchunks * 3;
+    float sinv = pp[0], sres = pp[1], strace = pp[2];
+    for (int c = 1; c < nchunks; ++c) {
+      sinv = sinv + pp[3 * c + 0];
+      sres = sres + pp[3 * c + 1];
+      strace = strace + pp[3 * c + 2];
+    }
+    const float gb = g2[b];
+    const float a2raw = c0 + (gb / (float)n) * sinv;
+    clip += !(isfinite(a2raw) && a2raw > kAlphaEps && a2raw < hi);
+    float a2 = a2raw;
+    if (isnan(a2)) a2 = 0.5f;
+    else if (isinf(a2)) a2 = a2 > 0.f ? hi : kAlphaEps;
+    a2 = a2 < kAlphaEps ? kAlphaEps : (a2 > hi ? hi : a2);
+    const float e2 = gb / a2;
+    eta2[b] = e2;
+    const float gn = nan_to_num_clamp_min(e2 - gb, 1e-12f, 1e12f, 1e-12f, kPrecEps);
+    g1new[b] = gn;
+    float gd = gn;
+    if (damping < 1.f) {
+      if (damping <= 0.f) {
+        gd = g1[b];
+      } else {
+        const float p = g1[b] < 1e-12f ? 1e-12f : g1[b];
+        const float q = gn < 1e-12f ? 1e-12f : gn;
+        gd = expf((1.0f - damping) * logf(p) + damping * logf(q));
+      }
+    }
+    g1[b] = gd;
+    // EM statistic per row: |residual_after|^2 + trace term; alpha2 kept for stats
+    eta2[rows + b] = sres + strace;
+    eta2[2 * rows + b] = a2;
+  }
+  const float s_clip = block_sum((float)clip, red);
+  if (threadIdx.x == 0) {
+    float em = 0.f, a2s = 0.f;
+    for (int64_t b = 0; b < rows; ++b) {
+      em += eta2[rows + b];
+      a2s += eta2[2 * rows + b];
+    }
+    st->a2_clip = (int)s_clip;
+    st->em_mean = em / (float)rows;
+    st->a2_mean = a2s / (float)rows;
+  }
+}
+
+// LMMSE part 2 + r1 message (mpq/linear.py:51-52, mpq/solver.py:645-653):
+// x2 = r2 + sum_s P[s], r1_new = (eta2*x2 - g2*r2)/g1_new, r1 <- damped.
+__global__ __launch_bounds__(kEW) void lmmse_epi2_kernel(
+    int64_t n, const float* __restrict__ P, int splits, int64_t split_stride,
+    const float* __restrict__ r2, const float* __restrict__ eta2, const float* __restrict__ g2,
+    const float* __restrict__ g1new, float damping, float* __restrict__ r1) {
+  const int64_t b = blockIdx.y;
+  const float e2 = eta2[b], gb = g2[b], gn = g1new[b];
+  const float keep = 1.0f - damping;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
+    if (j >= n) continue;
+    const int64_t o = b * n + j;
+    float d = P[o];
+    for (int s = 1; s < splits; ++s) d = d + P[(int64_t)s * split_stride + o];
+    const float r2v = r2[o];
+    const float x2 = r2v + d;
+    const float rn = (e2 * x2 - gb * r2v) / gn;
+    r1[o] = damping >= 1.f ? rn : keep * r1[o] + damping * rn;
+  }
+}
+
+// Rank-space error partials (mpq/linear.py:94): sum_j (Yu - sum_s P[s])^2.
+__global__ __launch_bounds__(kEW) void err_epi_kernel(int64_t n, const float* __restrict__ P,
+                                                      int splits, int64_t split_stride,
+                                                      const float* __restrict__ Yu,
+                                                      float* __restrict__ part) {
+  __shared__ float red[kEW / 64];
+  const int64_t b = blockIdx.y;
+  float acc = 0.f;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
+    if (j >= n) continue;
+    const int64_t o = b * n + j;
+    float v = P[o];
+    for (int s = 1; s < splits; ++s) v = v + P[(int64_t)s * split_stride + o];
+    const float d = Yu[o] - v;
+    acc += d * d;
+  }
+  const float t = block_sum(acc, red);
+  if (threadIdx.x == 0) part[b * gridDim.x + blockIdx.x] = t;
+}
+
+// Row sums of chunk partials -> out[b]; st->err_mean / err_sum over rows.
+__global__ __launch_bounds__(kEW) void rows_err_kernel(int64_t rows, int nchunks,
+                                                       const float* __restrict__ part,
+                                                       float* __restrict__ out,
+                                                       VampStatus* __restrict__ st) {
+  for (int64_t b = threadIdx.x; b < rows; b += blockDim.x) {
+    float v = part[b * nchunks];
+    for (int c = 1; c < nchunks; ++c) v = v + part[b * nchunks + c];
+    out[b] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.f;
+    for (int64_t b = 0; b < rows; ++b) s += out[b];
+    st->err_sum = s;
+    st->err_mean = s / (float)rows;
+  }
+}
+
+// gamma1 init (mpq/solver.py:481-483, :85-87): gamma_start * 0.25 / clamp(mean((W-x)^2), 1e-12).
+__global__ __launch_bounds__(kEW) void sqdiff_part_kernel(int64_t n, const float* __restrict__ W,
+                                                          int64_t ldw, const float* __restrict__ X,
+                                                          int64_t ldx, float* __restrict__ part) {
+  __shared__ float red[kEW / 64];
+  const int64_t b = blockIdx.y;
+  float acc = 0.f;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
+    if (j >= n) continue;
+    const float d = W[b * ldw + j] - X[b * ldx + j];
+    acc += d * d;
+  }
+  const float t = block_sum(acc, red);
+  if (threadIdx.x == 0) part[b * gridDim.x + blockIdx.x] = t;
+}
+
+__global__ __launch_bounds__(kEW) void rows_gamma_init_kernel(int64_t rows, int64_t n, int nchunks,
+                                                              const float* __restrict__ part,
+                                                              float gamma_start,
+                                                              float* __restrict__ g1,
+                                                              VampStatus* __restrict__ st) {
+  __shared__ float red[kEW / 64];
+  int bad = 0;
+  for (int64_t b = threadIdx.x; b < rows; b += blockDim.x) {
+    float v = part[b * nchunks];
+    for (int c = 1; c < nchunks; ++c) v = v + part[b * nchunks + c];
+    float mse = v / (float)n;
+    mse = mse < 1e-12f ? 1e-12f : mse;
+    const float g = gamma_start * (0.25f / mse);
+    g1[b] = g;
+    bad += !(isfinite(g) && g > kPrecEps);
+  }
+  const float s = block_sum((float)bad, red);
+  if (threadIdx.x == 0) st->g1_invalid = (int)s;
+}
+
+// ---------------------------------------------------------------------------
+// Host driver
+// ---------------------------------------------------------------------------
+
+struct Workspace {
+  float* Yu;
+  float* r1;
+  float* r2;
+  float* r2prev;
+  float* x1;  // denoiser mean; reused as the LMMSE coefficient product
+  float* xs;  // hard-state dequantised values
+  float* P;   // split-K partials
+  float* rowbuf;  // per-row arrays
+  float* part;    // chunk partials (3 per row per chunk)
+  uint8_t* q_cur;
+  uint8_t* q_best;
+  VampStatus* status;
+  int splits;
+  int bn;
+};
+
+inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+struct Sizes {
+  int64_t rows, n, nchunks, splits, bn;
+  int64_t bytes;
+};
+
+Sizes plan(int64_t rows, int64_t n) {
+  Sizes s;
+  s.rows = rows;
+  s.n = n;
+  s.nchunks = (n + kChunk - 1) / kChunk;
+  int bn = 128;
+  s.splits = choose_splits(rows, n, n, (int64_t)1 << 62, &bn);
+  s.bn = bn;
+  const int64_t mat = align_up(rows * n, 64) * 4;
+  int64_t bytes = 0;
+  bytes += 6 * mat;                                   // Yu r1 r2 r2prev x1 xs
+  bytes += s.splits * mat;                            // P
+  bytes += align_up(32 * rows, 64) * 4;               // row arrays
+  bytes += align_up(3 * rows * s.nchunks, 64) * 4;    // chunk partials
+  bytes += 2 * align_up(rows * n, 256);               // q_cur q_best
+  bytes += 256;                                       // status
+  s.bytes = bytes;
+  return s;
+}
+
+Workspace carve(void* base, const Sizes& s) {
+  Workspace w{};
+  char* p = static_cast<char*>(base);
+  const int64_t mat = align_up(s.rows * s.n, 64) * 4;
+  w.Yu = (float*)p; p += mat;
+  w.r1 = (float*)p; p += mat;
+  w.r2 = (float*)p; p += mat;
+  w.r2prev = (float*)p; p += mat;
+  w.x1 = (float*)p; p += mat;
+  w.xs = (float*)p; p += mat;
+  w.P = (float*)p; p += s.splits * mat;
+  w.rowbuf = (float*)p; p += align_up(32 * s.rows, 64) * 4;
+  w.part = (float*)p; p += align_up(3 * s.rows * s.nchunks, 64) * 4;
+  w.q_cur = (uint8_t*)p; p += align_up(s.rows * s.n, 256);
+  w.q_best = (uint8_t*)p; p += align_up(s.rows * s.n, 256);
+  w.status = (VampStatus*)p;
+  w.splits = (int)s.splits;
+  w.bn = (int)s.bn;
+  return w;
+}
+
+// Pinned host mirror of the device status (allocated once per process).
+VampStatus* host_status() {
+  static thread_local VampStatus* h = nullptr;
+  if (!h) {
+    if (hipHostMalloc((void**)&h, sizeof(VampStatus), hipHostMallocDefault) != hipSuccess) h = nullptr;
+  }
+  return h;
+}
+
+}  // namespace
+
+// P = A @ op(B) as split-K partials into w.P (split_stride rows*n).
+static hipError_t product(const Workspace& w, const float* A, const float* B, bool trans_b,
+                          int64_t rows, int64_t n, hipStream_t stream) {
+  GemmParams p{};
+  p.M = rows; p.N = n; p.K = n;
+  p.A = A; p.lda = n; p.B = B; p.ldb = n; p.trans_b = trans_b; p.b_rows = nullptr;
+  p.C = w.P; p.ldc = n; p.split_stride = align_up(rows * n, 64);
+  p.alpha = 1.f; p.beta = 0.f;
+  p.mode = w.splits > 1 ? kGemmPartials : kGemmPartials;
+  return gemm_partials(p, w.splits, w.bn, stream);
+}
+
+int64_t uniform_vamp_workspace_bytes(int64_t rows, int64_t n) { return plan(rows, n).bytes; }
+
+int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUniformVampConfig& cfg,
+                       double obs_init, uint8_t* q_out, float* x_out, float* err_out,
+                       float* rtn_err_out, MpqUniformVampStats* stats, void* workspace,
+                       int64_t workspace_bytes, hipStream_t stream) {
+  const int64_t rows = pr.rows, n = pr.n;
+  const Sizes sz = plan(rows, n);
+  MPQ_CHECK_ARG(workspace_bytes >= sz.bytes, "uniform VAMP: workspace too small (%lld < %lld bytes)",
+                (long long)workspace_bytes, (long long)sz.bytes);
+  Workspace w = carve(workspace, sz);
+  VampStatus* hs = host_status();
+  MPQ_CHECK_ARG(hs != nullptr, "uniform VAMP: pinned status buffer unavailable");
+  const int nchunks = (int)sz.nchunks;
+  const int64_t sstride = align_up(rows * n, 64);
+  const dim3 eg((unsigned)nchunks, (unsigned)rows), eb(kEW);
+  const int64_t G = (n + pr.group_size - 1) / pr.group_size;
+
+  // per-row arrays
+  float* g1 = w.rowbuf + 0 * rows;
+  float* g1w = w.rowbuf + 1 * rows;
+  float* a1raw = w.rowbuf + 2 * rows;
+  float* a1 = w.rowbuf + 3 * rows;
+  float* eta1 = w.rowbuf + 4 * rows;
+  float* g2new = w.rowbuf + 5 * rows;
+  float* g2 = w.rowbuf + 6 * rows;
+  float* g2prev = w.rowbuf + 7 * rows;
+  float* eta2 = w.rowbuf + 8 * rows;  // 3 * rows: eta2, EM row stat, alpha2
+  float* g1new = w.rowbuf + 11 * rows;
+  float* err_cur = w.rowbuf + 12 * rows;
+  float* err_best = w.rowbuf + 13 * rows;
+
+  auto sync_status = [&]() -> int {
+    MPQ_HIP_TRY(hipMemcpyAsync(hs, w.status, sizeof(VampStatus), hipMemcpyDeviceToHost, stream));
+    MPQ_HIP_TRY(hipStreamSynchronize(stream));
+    return kOk;
+  };
+  const float tau = cfg.prior_tau;
+  int rc;
+
+  // hard state + rank-space error of the decision for (r1, g1) -> q_cur, err_cur, status.err_mean
+  auto hard_state = [&](const float* r, const float* g) -> int {
+    if (cfg.final_decision == 1) {
+      hipLaunchKernelGGL(uniform_denoise_kernel<kHardRoundMean>, eg, eb, 0, stream, r, g, pr.W, pr.ldw,
+                         pr.scale, pr.zero, G, pr.group_size, n, pr.maxq, tau, nullptr, nullptr,
+                         w.q_cur, w.xs);
+    } else {
+      hipLaunchKernelGGL(uniform_denoise_kernel<kHardMap>, eg, eb, 0, stream, r, g, pr.W, pr.ldw,
+                         pr.scale, pr.zero, G, pr.group_size, n, pr.maxq, tau, nullptr, nullptr,
+                         w.q_cur, w.xs);
+    }
+    MPQ_LAUNCH_CHECK();
+    MPQ_HIP_TRY(product(w, w.xs, Vs, false, rows, n, stream));
+    hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.Yu, w.part);
+    hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, w.part, err_cur, w.status);
+    MPQ_LAUNCH_CHECK();
+    return kOk;
+  };
+
+  // ---- setup ----------------------------------------------------------
+  // Yu = W @ Vs
+  {
+    // W may be strided (ldw); copy to contiguous r1 first when needed.
+    const float* Wc = pr.W;
+    if (pr.ldw != n) {
+      MPQ_HIP_TRY(hipMemcpy2DAsync(w.r1, n * 4, pr.W, pr.ldw * 4, n * 4, rows, hipMemcpyDeviceToDevice, stream));
+      Wc = w.r1;
+    }
+    MPQ_HIP_TRY(product(w, Wc, Vs, false, rows, n, stream));
+    MPQ_HIP_TRY(splitk_reduce(w.P, w.splits, rows, n, w.Yu, n, 1.f, 0.f, stream));
+  }
+  // RTN error (rtn_err, and the obs warm start when none is given)
+  MPQ_HIP_TRY(hipMemcpy2DAsync(w.xs, n * 4, pr.x_init, pr.ldw * 4, n * 4, rows, hipMemcpyDeviceToDevice, stream));
+  MPQ_HIP_TRY(product(w, w.xs, Vs, false, rows, n, stream));
+  hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.Yu, w.part);
+  hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, w.part,
+                     rtn_err_out ? rtn_err_out : err_cur, w.status);
+  // gamma1 init from the RTN decision
+  hipLaunchKernelGGL(sqdiff_part_kernel, eg, eb, 0, stream, n, pr.W, pr.ldw, pr.x_init, pr.ldw, w.part + 0);
+  hipLaunchKernelGGL(rows_gamma_init_kernel, dim3(1), eb, 0, stream, rows, n, nchunks, w.part,
+                     cfg.gamma_start, g1, w.status);
+  MPQ_LAUNCH_CHECK();
+  if ((rc = sync_status()) != kOk) return rc;
+  if (hs->g1_invalid) {
+    set_error("gamma1_init invalid: expected finite and > 1e-12.");
+    set_error_code(kNumerical);
+    return kNumerical;
+  }
+  const double rtn_err_mean = (double)hs->err_mean;
+  double obs;
+  if (cfg.obs_precision > 0.0) obs = cfg.obs_precision;
+  else if (obs_init > 0.0) obs = obs_init;
+  else {
+    float m = hs->err_sum / (float)(rows * n);  // mean over all rank-space entries
+    obs = 1.0 / (double)(m < 1e-12f ? 1e-12f : m);
+  }
+  const double obs_initial = obs;
+  const bool em_active = cfg.em_obs_precision && cfg.obs_precision <= 0.0;
+
+  // r1 init
+  if (cfg.init_from == 2) {
+    MPQ_HIP_TRY(hipMemsetAsync(w.r1, 0, rows * n * 4, stream));
+  } else {
+    const float* src = cfg.init_from == 1 ? pr.W : pr.x_init;
+    MPQ_HIP_TRY(hipMemcpy2DAsync(w.r1, n * 4, src, pr.ldw * 4, n * 4, rows, hipMemcpyDeviceToDevice, stream));
+  }
+  // initial hard state = best
+  if ((rc = hard_state(w.r1, g1)) != kOk) return rc;
+  if ((rc = sync_status()) != kOk) return rc;
+  double best_err_mean = (double)hs->err_mean;
+  std::swap(w.q_cur, w.q_best);
+  std::swap(err_cur, err_best);
+  double best_obs = obs;
+  int best_iter = -1, stop_iter = -1;
+  int a1_retry = 0, a2_clip = 0, g2_invalid = 0;
+  double obs_sum = 0.0, a1_sum = 0.0, a2_sum = 0.0;
+  int n_logged = 0;
+  bool has_prev = false;
+  const float damping = cfg.damping;
+  const float retry_factor = cfg.gamma_retry_factor > 1.000001f ? cfg.gamma_retry_factor : 1.000001f;
+  const int retry_steps = cfg.gamma_retry_steps > 0 ? cfg.gamma_retry_steps : 0;
+  const int iters = cfg.iters > 0 ? cfg.iters : 0;
+
+  for (int it = 0; it < iters; ++it) {
+    // ---- denoiser with gamma retries (mpq/solver.py:559-596)
+    MPQ_HIP_TRY(hipMemcpyAsync(g1w, g1, rows * 4, hipMemcpyDeviceToDevice, stream));
+    for (int attempt = 0; attempt <= retry_steps; ++attempt) {
+      hipLaunchKernelGGL(uniform_denoise_kernel<kPosterior>, eg, eb, 0, stream, w.r1, g1w, pr.W, pr.ldw,
+                         pr.scale, pr.zero, G, pr.group_size, n, pr.maxq, tau, w.x1, w.part, nullptr,
+                         nullptr);
+      hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, n, nchunks, w.part, g1w,
+                         has_prev ? 1 : 0, damping, g2prev, a1raw, a1, eta1, g2new, g2, w.status);
+      MPQ_LAUNCH_CHECK();
+      if ((rc = sync_status()) != kOk) return rc;
+      if (hs->a1_invalid == 0) break;
+      if (attempt >= retry_steps) {
+        if (hs->a1_nonfinite) {
+          set_error("alpha1 invalid: expected all in (1e-07, 1-1e-07).");
+          set_error_code(kNumerical);
+          return kNumerical;
+        }
+        break;  // clamped alpha1 already in place
+      }
+      a1_retry += hs->a1_invalid;
+      hipLaunchKernelGGL(rows_retry_kernel, dim3(1), eb, 0, stream, rows, a1raw, retry_factor, g1w);
+      MPQ_LAUNCH_CHECK();
+    }
+    if (hs->g2new_invalid || hs->g2_invalid) {  // mpq/solver.py:602-604, 613-615
+      ++g2_invalid;
+      continue;
+    }
+    const float a1_mean_it = hs->a1_mean;
+    // ---- r2 message, LMMSE (obs as used by this iteration)
+    const float obs_f = (float)obs;
+    hipLaunchKernelGGL(msg_r2_kernel, eg, eb, 0, stream, n, w.x1, w.r1, eta1, g1w, g2new,
+                       has_prev ? 1 : 0, damping, w.r2prev, w.r2);
+    MPQ_LAUNCH_CHECK();
+    MPQ_HIP_TRY(product(w, w.r2, pr.V, false, rows, n, stream));
+    hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.Yu, pr.S, g2,
+                       obs_f, w.x1, w.part);
+    hipLaunchKernelGGL(rows_lmmse_kernel, dim3(1), eb, 0, stream, rows, n, n, nchunks, w.part, g2, damping,
+                       eta2, g1new, g1, w.status);
+    MPQ_LAUNCH_CHECK();
+    MPQ_HIP_TRY(product(w, w.x1, pr.V, true, rows, n, stream));
+    hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.r2, eta2, g2,
+                       g1new, damping, w.r1);
+    MPQ_LAUNCH_CHECK();
+    // ---- hard state of the new (r1, g1)
+    if ((rc = hard_state(w.r1, g1)) != kOk) return rc;
+    if ((rc = sync_status()) != kOk) return rc;
+    a2_clip += hs->a2_clip;
+    // EM update of the observation precision (mpq/linear.py:59-82), in double like the reference
+    if (em_active) {
+      float den = hs->em_mean < 1e-12f ? 1e-12f : hs->em_mean;
+      const double beta_new = (double)n / (double)den;
+      const double beta_old = obs > 1e-12 ? obs : 1e-12;
+      const double d = cfg.em_obs_precision_damping;
+      double beta;
+      if (d >= 1.0) beta = beta_new;
+      else if (d <= 0.0) beta = beta_old;
+      else beta = std::exp((1.0 - d) * std::log(beta_old) + d * std::log(beta_new > 1e-12 ? beta_new : 1e-12));
+      beta = std::min(std::max(beta, cfg.em_obs_precision_min), cfg.em_obs_precision_max);
+      obs = beta;
+    }
+    std::swap(w.r2, w.r2prev);  // r2_prev <- r2
+    std::swap(g2, g2prev);      // gamma2_prev <- gamma2
+    has_prev = true;
+    obs_sum += obs;
+    a1_sum += a1_mean_it;
+    a2_sum += hs->a2_mean;
+    ++n_logged;
+    // best iterate (mpq/solver.py:678-699)
+    const double cur = (double)hs->err_mean;
+    const double tol = std::max(1e-10, std::fabs(best_err_mean) * 1e-8);
+    if (cur + tol < best_err_mean) {
+      std::swap(w.q_cur, w.q_best);
+      std::swap(err_cur, err_best);
+      best_err_mean = cur;
+      best_obs = obs;
+      best_iter = it;
+    } else {
+      obs = best_obs;
+      stop_iter = it;
+      break;
+    }
+  }
+
+  // ---- outputs
+  MPQ_HIP_TRY(hipMemcpyAsync(q_out, w.q_best, rows * n, hipMemcpyDeviceToDevice, stream));
+  if (err_out) MPQ_HIP_TRY(hipMemcpyAsync(err_out, err_best, rows * 4, hipMemcpyDeviceToDevice, stream));
+  if (x_out) {
+    MPQ_HIP_TRY(dequant_groups(w.q_best, pr.scale, pr.zero, G, pr.group_size, rows, n, x_out, stream));
+  }
+  if (stats) {
+    stats->iters = iters;
+    stats->best_iter = best_iter;
+    stats->stop_iter = stop_iter;
+    stats->alpha1_retry_count = a1_retry;
+    stats->alpha2_clip_count = a2_clip;
+    stats->gamma2_invalid_count = g2_invalid;
+    stats->obs_precision_initial = obs_initial;
+    stats->obs_precision_final = obs;
+    stats->obs_precision_mean = n_logged ? obs_sum / n_logged : obs;
+    stats->alpha1_mean = n_logged ? a1_sum / n_logged : 0.0;
+    stats->alpha2_mean = n_logged ? a2_sum / n_logged : 0.0;
+    stats->best_rankspace_error_mean = best_err_mean;
+    stats->rtn_rankspace_error_mean = rtn_err_mean;
+  }
+  return kOk;
+}
+
+}  // namespace mpq
+
+extern "C" int64_t mpq_uniform_vamp_workspace_size(int64_t rows, int64_t n) {
+  if (rows <= 0 || n <= 0) return 0;
+  return mpq::uniform_vamp_workspace_bytes(rows, n);
+}
+
+extern "C" int mpq_uniform_vamp_solve(int64_t rows, int64_t n, int maxq, const float* W, int64_t ldw,
+                                      const float* x_init, const float* scale, const float* zero,
+                                      int64_t group_size, const float* V, const float* S,
+                                      const float* Vs, const MpqUniformVampConfig* cfg,
+                                      double obs_init, uint8_t* q_out, float* x_out,
+                                      float* err_out, float* rtn_err_out,
+                                      MpqUniformVampStats* stats, void* workspace,
+                                      int64_t workspace_bytes, hipStream_t stream) {
+  MPQ_CHECK_ARG(rows > 0 && n > 0, "mpq_uniform_vamp_solve: empty problem");
+  MPQ_CHECK_ARG(maxq >= 1 && maxq <= 255, "mpq_uniform_vamp_solve: maxq must be in [1, 255]");
+  MPQ_CHECK_ARG(W && x_init && scale && zero && V && S && Vs && cfg && q_out && workspace,
+                "mpq_uniform_vamp_solve: null argument");
+  MPQ_CHECK_ARG(group_size >= 1, "mpq_uniform_vamp_solve: group_size must be >= 1");
+  MPQ_CHECK_ARG(ldw >= n, "mpq_uniform_vamp_solve: ldw < n");
+  MPQ_CHECK_ARG(rows <= 65535, "mpq_uniform_vamp_solve: at most 65535 rows per block");
+  mpq::UniformProblem pr{};
+  pr.rows = rows; pr.n = n; pr.maxq = maxq; pr.W = W; pr.x_init = x_init; pr.scale = scale;
+  pr.zero = zero; pr.group_size = group_size; pr.V = V; pr.S = S; pr.ldw = ldw;
+  return mpq::uniform_vamp_solve(pr, Vs, *cfg, obs_init, q_out, x_out, err_out, rtn_err_out, stats,
+                                 workspace, workspace_bytes, stream);
+}
+
+extern "C" int mpq_uniform_denoise(int64_t rows, int64_t n, int maxq, const float* r1, const float* gamma,
+                                   const float* center, int64_t ld_center, const float* scale,
+                                   const float* zero, int64_t group_size, float tau, float* mean,
+                                   float* var, int64_t* map_idx, float* map_value, float* alpha1,
+                                   hipStream_t stream) {
+  MPQ_CHECK_ARG(rows >= 0 && n >= 0, "mpq_uniform_denoise: bad shape");
+  if (rows == 0 || n == 0) return mpq::kOk;
+  MPQ_CHECK_ARG(maxq >= 1 && maxq <= 255 && group_size >= 1, "mpq_uniform_denoise: bad maxq/group_size");
+  MPQ_CHECK_ARG(r1 && gamma && center && scale && zero && mean && var && map_idx && map_value,
+                "mpq_uniform_denoise: null argument");
+  MPQ_CHECK_ARG(ld_center >= n && rows <= 65535, "mpq_uniform_denoise: bad ld/rows");
+  const int64_t G = (n + group_size - 1) / group_size;
+  const dim3 eg((unsigned)((n + mpq::kChunk - 1) / mpq::kChunk), (unsigned)rows);
+  hipLaunchKernelGGL(mpq::uniform_denoise_kernel<mpq::kFull>, eg, dim3(mpq::kEW), 0, stream, r1, gamma, center,
+                     ld_center, scale, zero, G, group_size, n, maxq, tau, mean, var,
+                     reinterpret_cast<uint8_t*>(map_idx), map_value);
+  MPQ_LAUNCH_CHECK();
+  if (alpha1) {
+    hipLaunchKernelGGL(mpq::row_alpha_kernel, dim3((unsigned)rows), dim3(mpq::kEW), 0, stream, n, var, gamma,
+                       alpha1);
+    MPQ_LAUNCH_CHECK();
+  }
+  return mpq::kOk;
+}

@@ -1,0 +1,255 @@
+"""Typed wrappers of the C-ABI entry points (one function per ``mpq_*`` symbol).
+
+Every wrapper checks shapes/dtypes on the host, allocates outputs with torch's
+caching allocator (device memory plumbing only), and enqueues the HIP kernels
+on torch's current stream.  No wrapper has a CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+F32 = torch.float32
+
+
+def _dev(*ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(f"mpq_amd operates on ROCm device tensors only (got a tensor on {t.device}).")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError("all tensors must be on the same device")
+    if dev is None:
+        raise ValueError("no device tensor given")
+    return dev
+
+
+def _f32c(t: torch.Tensor) -> torch.Tensor:
+    return t.to(dtype=F32).contiguous()
+
+
+def _stream(dev: torch.device) -> int:
+    return _lib.stream_handle(dev)
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+# ---- GEMM -----------------------------------------------------------------
+
+def gemm(A: torch.Tensor, B: torch.Tensor, *, trans_b: bool = False, b_rows: Optional[torch.Tensor] = None,
+         out: Optional[torch.Tensor] = None, alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
+    """C = alpha * A @ op(B) + beta * C on the fp32 MFMA kernel (deterministic split-K)."""
+    dev = _dev(A, B)
+    A = _f32c(A)
+    B = _f32c(B)
+    M, K = A.shape
+    if b_rows is not None:
+        b_rows = b_rows.to(device=dev, dtype=torch.int32).contiguous()
+        if trans_b or int(b_rows.numel()) != K:
+            raise ValueError("b_rows needs trans_b=False and K entries")
+        N = int(B.shape[1])
+    elif trans_b:
+        N = int(B.shape[0])
+        if int(B.shape[1]) != K:
+            raise ValueError(f"shape mismatch: A {tuple(A.shape)} vs B^T of {tuple(B.shape)}")
+    else:
+        N = int(B.shape[1])
+        if int(B.shape[0]) != K:
+            raise ValueError(f"shape mismatch: A {tuple(A.shape)} vs B {tuple(B.shape)}")
+    if out is None:
+        if beta != 0.0:
+            raise ValueError("beta != 0 needs out")
+        out = torch.empty(M, N, dtype=F32, device=dev)
+    elif out.dtype != F32 or not out.is_contiguous() or tuple(out.shape) != (M, N):
+        raise ValueError("out must be a contiguous fp32 (M, N) tensor")
+    ws_floats = 32 * M * N if K >= 512 else 0
+    ws = torch.empty(max(ws_floats, 1), dtype=F32, device=dev)
+    _lib.call("mpq_gemm_f32", M, N, K, _lib.ptr(A), K, _lib.ptr(B), int(B.shape[1]), int(bool(trans_b)),
+              _lib.ptr(b_rows), _lib.ptr(out), N, float(alpha), float(beta), _lib.ptr(ws), ws_floats,
+              _stream(dev))
+    return out
+
+
+# ---- quantizer helpers ----------------------------------------------------
+
+def gptq_find_params(W: torch.Tensor, group_size: int, maxq: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Asymmetric min-max GPTQ parameters per (row, group): (scale, zero) of shape (rows, G)."""
+    dev = _dev(W)
+    W = _f32c(W)
+    rows, n = W.shape
+    G = (n + group_size - 1) // group_size
+    scale = torch.empty(rows, G, dtype=F32, device=dev)
+    zero = torch.empty(rows, G, dtype=F32, device=dev)
+    for r0 in range(0, rows, 65535):
+        r1 = min(rows, r0 + 65535)
+        _lib.call("mpq_gptq_find_params", _lib.ptr(W[r0:r1]), r1 - r0, n, n, int(group_size), int(maxq),
+                  _lib.ptr(scale[r0:r1]), _lib.ptr(zero[r0:r1]), _stream(dev))
+    return scale, zero
+
+
+def uniform_rtn(W: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor, group_size: int, maxq: int,
+                want_q: bool = True, want_x: bool = True):
+    dev = _dev(W, scale, zero)
+    W = _f32c(W)
+    rows, n = W.shape
+    scale = _f32c(scale)
+    zero = _f32c(zero)
+    q = torch.empty(rows, n, dtype=torch.uint8, device=dev) if want_q else None
+    x = torch.empty(rows, n, dtype=F32, device=dev) if want_x else None
+    _lib.call("mpq_uniform_rtn", _lib.ptr(W), rows, n, n, _lib.ptr(scale), _lib.ptr(zero), int(group_size),
+              int(maxq), _lib.ptr(q), _lib.ptr(x), _stream(dev))
+    return q, x
+
+
+def dequant(q: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor, group_size: int) -> torch.Tensor:
+    dev = _dev(q, scale, zero)
+    q = q.to(torch.uint8).contiguous()
+    rows, n = q.shape
+    x = torch.empty(rows, n, dtype=F32, device=dev)
+    _lib.call("mpq_dequant", _lib.ptr(q), rows, n, _lib.ptr(_f32c(scale)), _lib.ptr(_f32c(zero)),
+              int(group_size), _lib.ptr(x), _stream(dev))
+    return x
+
+
+# ---- rotation -------------------------------------------------------------
+
+def block_hadamard(X: torch.Tensor, had_dim: int, signs: Optional[torch.Tensor] = None,
+                   inverse: bool = False) -> torch.Tensor:
+    """Signed block Walsh-Hadamard along the last dim (forward: X*signs then H; inverse: H then *signs)."""
+    dev = _dev(X, signs)
+    shape = X.shape
+    X2 = _f32c(X).reshape(-1, shape[-1])
+    rows, width = X2.shape
+    out = torch.empty_like(X2)
+    sg = None if signs is None else _f32c(signs)
+    for r0 in range(0, rows, 65535):
+        r1 = min(rows, r0 + 65535)
+        _lib.call("mpq_block_hadamard", _lib.ptr(X2[r0:r1]), width, _lib.ptr(out[r0:r1]), width, r1 - r0, width,
+                  int(had_dim), _lib.ptr(sg), int(bool(inverse)), _stream(dev))
+    return out.reshape(shape)
+
+
+def transpose(X: torch.Tensor) -> torch.Tensor:
+    dev = _dev(X)
+    X = _f32c(X)
+    rows, cols = X.shape
+    out = torch.empty(cols, rows, dtype=F32, device=dev)
+    _lib.call("mpq_transpose", _lib.ptr(X), rows, cols, cols, _lib.ptr(out), rows, _stream(dev))
+    return out
+
+
+def scale_columns(X: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """out = X * scale[None, :]."""
+    dev = _dev(X, scale)
+    X = _f32c(X)
+    rows, cols = X.shape
+    out = torch.empty_like(X)
+    _lib.call("mpq_scale_columns", _lib.ptr(X), rows, cols, _lib.ptr(_f32c(scale)), _lib.ptr(out), _stream(dev))
+    return out
+
+
+def eigh_postprocess(lam_asc: torch.Tensor, V_asc: torch.Tensor, floor: float):
+    """(lam, S, V, Vs): descending order, floored eigenvalues, S = sqrt(lam), Vs = V * S."""
+    dev = _dev(lam_asc, V_asc)
+    lam_asc = _f32c(lam_asc)
+    V_asc = _f32c(V_asc)
+    n = int(lam_asc.numel())
+    lam = torch.empty(n, dtype=F32, device=dev)
+    S = torch.empty(n, dtype=F32, device=dev)
+    V = torch.empty(n, n, dtype=F32, device=dev)
+    Vs = torch.empty(n, n, dtype=F32, device=dev)
+    _lib.call("mpq_eigh_postprocess", _lib.ptr(lam_asc), _lib.ptr(V_asc), n, float(floor), _lib.ptr(lam),
+              _lib.ptr(S), _lib.ptr(V), _lib.ptr(Vs), _stream(dev))
+    return lam, S, V, Vs
+
+
+# ---- uniform VAMP and CD ------------------------------------------------------
+
+def vamp_config_c(cfg) -> "_lib.UniformVampConfigC":
+    fd = str(getattr(cfg, "final_decision", "map") or "map").strip().lower()
+    if fd not in ("map", "round_mean"):
+        raise ValueError(f"unsupported final_decision={fd!r}")
+    init = str(getattr(cfg, "init_from", "rtn") or "rtn").strip().lower()
+    if init not in ("rtn", "float", "zero"):
+        raise ValueError(f"unknown init_from={init!r} (expected 'rtn', 'float', or 'zero').")
+    c = _lib.UniformVampConfigC()
+    c.iters = max(int(cfg.iters), 0)
+    c.damping = float(cfg.damping)
+    c.final_decision = 0 if fd == "map" else 1
+    c.init_from = {"rtn": 0, "float": 1, "zero": 2}[init]
+    c.gamma_start = float(cfg.gamma_start)
+    c.gamma_retry_factor = float(cfg.gamma_retry_factor)
+    c.gamma_retry_steps = int(cfg.gamma_retry_steps)
+    c.prior_tau = float(cfg.prior_tau)
+    c.obs_precision = float(cfg.obs_precision)
+    c.em_obs_precision = int(bool(cfg.em_obs_precision))
+    c.em_obs_precision_damping = float(cfg.em_obs_precision_damping)
+    c.em_obs_precision_min = float(cfg.em_obs_precision_min)
+    c.em_obs_precision_max = float(cfg.em_obs_precision_max)
+    return c
+
+
+def uniform_vamp_solve(W, x_init, scale, zero, group_size, maxq, V, S, Vs, cfg, obs_init: float = 0.0,
+                       want_x: bool = False, ws: Optional[torch.Tensor] = None):
+    """One row block of the uniform VAMP loop.  Returns (q uint8, x|None, err, rtn_err, stats dict)."""
+    dev = _dev(W, x_init, scale, zero, V, S, Vs)
+    W = _f32c(W)
+    x_init = _f32c(x_init)
+    rows, n = W.shape
+    if tuple(V.shape) != (n, n) or int(S.numel()) != n or tuple(Vs.shape) != (n, n):
+        raise ValueError("mpq_amd uniform VAMP needs full rank: V, Vs (n x n) and S (n)")
+    lib = _lib.load()
+    need = int(lib.mpq_uniform_vamp_workspace_size(rows, n))
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    q = torch.empty(rows, n, dtype=torch.uint8, device=dev)
+    x = torch.empty(rows, n, dtype=F32, device=dev) if want_x else None
+    err = torch.empty(rows, dtype=F32, device=dev)
+    rtn_err = torch.empty(rows, dtype=F32, device=dev)
+    st = _lib.UniformVampStatsC()
+    c = vamp_config_c(cfg)
+    _lib.call("mpq_uniform_vamp_solve", rows, n, int(maxq), _lib.ptr(W), n, _lib.ptr(x_init),
+              _lib.ptr(_f32c(scale)), _lib.ptr(_f32c(zero)), int(group_size), _lib.ptr(_f32c(V)),
+              _lib.ptr(_f32c(S)), _lib.ptr(_f32c(Vs)), ctypes.byref(c), float(obs_init or 0.0), _lib.ptr(q),
+              _lib.ptr(x), _lib.ptr(err), _lib.ptr(rtn_err), ctypes.byref(st), _lib.ptr(ws), int(ws.numel()),
+              _stream(dev))
+    stats = {name: getattr(st, name) for name, _ in st._fields_}
+    return q, x, err, rtn_err, stats
+
+
+def uniform_cd_polish(W, q_in, scale, zero, group_size, maxq, Vs, H, *, block_rows: int, sweeps: int,
+                      accept_tol: float = 0.0, select: bool = True, Yu=None, x_in=None,
+                      ws: Optional[torch.Tensor] = None):
+    """Greedy scalar CD over all rows (greedy order per row block).  ``W`` may be None when ``Yu``
+    is given.  Returns (q, err_before, err_after, improved, accepted_per_row)."""
+    dev = _dev(q_in, scale, zero, Vs, H, W, Yu, x_in)
+    W = None if W is None else _f32c(W)
+    Yu = None if Yu is None else _f32c(Yu)
+    x_in = None if x_in is None else _f32c(x_in)
+    rows, n = q_in.shape
+    lib = _lib.load()
+    need = int(lib.mpq_uniform_cd_workspace_size(rows, n, int(block_rows)))
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    q_out = torch.empty(rows, n, dtype=torch.uint8, device=dev)
+    eb = torch.empty(rows, dtype=F32, device=dev)
+    ea = torch.empty(rows, dtype=F32, device=dev)
+    imp = torch.zeros(rows, dtype=torch.int32, device=dev)
+    acc = torch.zeros(rows, dtype=torch.int32, device=dev)
+    _lib.call("mpq_uniform_cd_polish", rows, n, int(maxq), int(block_rows), int(sweeps), float(accept_tol),
+              _lib.ptr(W), n, _lib.ptr(Yu), _lib.ptr(q_in.to(torch.uint8).contiguous()), _lib.ptr(x_in),
+              _lib.ptr(_f32c(scale)),
+              _lib.ptr(_f32c(zero)), int(group_size), _lib.ptr(_f32c(Vs)), _lib.ptr(_f32c(H)), int(bool(select)),
+              _lib.ptr(q_out), _lib.ptr(eb), _lib.ptr(ea), _lib.ptr(imp), _lib.ptr(acc), _lib.ptr(ws),
+              int(ws.numel()), _stream(dev))
+    return q_out, eb, ea, imp, acc

@@ -1,0 +1,173 @@
+"""GPU parity of the uniform-grid path against the CPU oracle (oracle/uniform.py)."""
+import numpy as np
+import pytest
+import torch
+
+from mpq_amd import ops
+from mpq_amd.adapters.gptqmodel import GPTQAdapterConfig, run_mpq_quantization
+from mpq_amd.priors.uniform import discrete_uniform_mmse
+from mpq_amd.solver import UniformVampConfig
+from oracle import uniform as ou
+from tests.uniform_cases import RECIPE, QCfg, make_layer
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(a, b):
+    return float((a.double() - b.double()).norm() / b.double().norm().clamp_min(1e-30))
+
+
+@pytest.mark.parametrize("M,N,K,trans", [(128, 512, 512, False), (128, 512, 512, True), (100, 72, 37, False),
+                                         (100, 72, 37, True), (256, 1024, 2048, False), (384, 640, 1536, True)])
+def test_gemm_matches_fp64(gpu, M, N, K, trans):
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    A = torch.randn(M, K, generator=g)
+    B = torch.randn(N, K, generator=g) if trans else torch.randn(K, N, generator=g)
+    C = ops.gemm(A.to(gpu), B.to(gpu), trans_b=trans).cpu()
+    ref = A.double() @ (B.double().T if trans else B.double())
+    assert _rel(C, ref) < 2e-6
+    # deterministic: bit-identical on a second call
+    C2 = ops.gemm(A.to(gpu), B.to(gpu), trans_b=trans).cpu()
+    assert torch.equal(C, C2)
+
+
+def test_gemm_gather_and_axpby(gpu):
+    g = torch.Generator().manual_seed(5)
+    A = torch.randn(256, 128, generator=g)
+    B = torch.randn(700, 300, generator=g)
+    rows = torch.randperm(700, generator=g)[:128].to(torch.int32)
+    C0 = torch.randn(256, 300, generator=g)
+    out = C0.clone().to(gpu)
+    ops.gemm(A.to(gpu), B.to(gpu), b_rows=rows.to(gpu), out=out, alpha=-1.0, beta=1.0)
+    ref = C0.double() - A.double() @ B.double()[rows.long()]
+    assert _rel(out.cpu(), ref) < 2e-6
+
+
+def test_hadamard_transpose_scale_bit_exact(gpu):
+    g = torch.Generator().manual_seed(6)
+    for had, width in ((128, 512), (2048, 14336 // 4), (4, 12)):
+        X = torch.randn(37, width, generator=g)
+        signs = torch.randint(0, 2, (width,), generator=g).float() * 2 - 1
+        got = ops.block_hadamard(X.to(gpu), had, signs=signs.to(gpu)).cpu()
+        ref = ou.hadamard_rows(X * signs.view(1, -1), had)
+        assert torch.equal(got, ref)
+        inv = ops.block_hadamard(got.to(gpu), had, signs=signs.to(gpu), inverse=True).cpu()
+        assert torch.allclose(inv, X, atol=1e-5)
+    X = torch.randn(77, 130, generator=g)
+    assert torch.equal(ops.transpose(X.to(gpu)).cpu(), X.T)
+    s = torch.randn(130, generator=g)
+    assert torch.equal(ops.scale_columns(X.to(gpu), s.to(gpu)).cpu(), X * s.view(1, -1))
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 128), (3, 128), (2, 64)])
+def test_find_params_and_rtn_exact(gpu, bits, gs):
+    W, _ = make_layer(96, 512, tokens=16, seed_key=f"fp{bits}")
+    W[3, :gs] = 0.0  # all-zero group -> (-1, +1) range
+    maxq = 2 ** bits - 1
+    s, z = ops.gptq_find_params(W.to(gpu), gs, maxq)
+    rs, rz = [], []
+    for g0 in range(0, 512, gs):
+        a, b = ou.gptq_find_params(W[:, g0:g0 + gs], maxq)
+        rs.append(a)
+        rz.append(b)
+    rs, rz = torch.cat(rs, 1), torch.cat(rz, 1)
+    assert torch.equal(s.cpu(), rs) and torch.equal(z.cpu(), rz)
+    q, x = ops.uniform_rtn(W.to(gpu), s, z, gs, maxq)
+    sf = torch.repeat_interleave(rs, gs, dim=1)
+    zf = torch.repeat_interleave(rz, gs, dim=1)
+    qr = torch.clamp(torch.round(W / sf) + zf, 0, maxq)
+    assert torch.equal(q.cpu().long(), qr.long())
+    assert torch.equal(x.cpu(), sf * (qr - zf))
+
+
+def test_denoiser_matches_oracle(gpu):
+    W, _ = make_layer(64, 384, tokens=16, seed_key="dn")
+    s, z = ou.gptq_find_params(W, 15)
+    sf, zf = s.expand(-1, 384).contiguous(), z.expand(-1, 384).contiguous()
+    g = torch.Generator().manual_seed(9)
+    r1 = W + 0.01 * torch.randn(W.shape, generator=g)
+    gam = torch.exp(torch.randn(64, 1, generator=g)) * 3e3
+    ref = ou.discrete_uniform_mmse(r1, gam, sf, zf, 15, W, 0.2)
+    got = discrete_uniform_mmse(r1=r1.to(gpu), gamma1=gam.to(gpu), scale_full=sf.to(gpu), zero_full=zf.to(gpu),
+                                maxq=15, prior_center=W.to(gpu), prior_tau=0.2, need_stats=False)
+    assert torch.equal(got["map_idx"].cpu(), ref["map_idx"])
+    assert torch.equal(got["map_value"].cpu(), ref["map_value"])
+    assert _rel(got["mean"].cpu(), ref["mean"]) < 1e-5
+    assert float(((got["mean"].cpu() - ref["mean"]).abs() / ref["mean"].abs().clamp_min(1e-3)).max()) < 1e-4
+    assert _rel(got["var"].cpu(), ref["var"]) < 1e-3
+    assert _rel(got["alpha1"].cpu(), ref["alpha1"]) < 1e-4
+
+
+def _setup_block(rows, cols, bits, gs, key):
+    W, H = make_layer(rows, cols, tokens=2048, seed_key=key)
+    Hw = 0.5 * (2.0 * H)
+    lam, V, _ = ou.hessian_eigen(Hw)
+    S = torch.sqrt(lam)
+    Vs = V * S.unsqueeze(0)
+    maxq = 2 ** bits - 1
+    sc, zc = [], []
+    for g0 in range(0, cols, gs):
+        a, b = ou.gptq_find_params(W[:, g0:g0 + gs], maxq)
+        sc.append(a)
+        zc.append(b)
+    sg, zg = torch.cat(sc, 1), torch.cat(zc, 1)
+    sf = torch.repeat_interleave(sg, gs, dim=1)
+    zf = torch.repeat_interleave(zg, gs, dim=1)
+    xr = sf * (torch.clamp(torch.round(W / sf) + zf, 0, maxq) - zf)
+    return W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq
+
+
+def test_vamp_block_matches_oracle(gpu):
+    W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq = _setup_block(128, 512, 4, 128, "vb")
+    cfg = dict(RECIPE, polish_sweeps=0)
+    q_ref, x_ref, e_ref, rtn_ref, tr = ou.solve_uniform_rankspace_vamp(W, xr, sf, zf, maxq, V, V.T, S, Vs, cfg)
+    vcfg = UniformVampConfig(**{k: v for k, v in RECIPE.items()})
+    q, x, e, rtn, st = ops.uniform_vamp_solve(W.to(gpu), xr.to(gpu), sg.to(gpu), zg.to(gpu), 128, maxq, V.to(gpu),
+                                              S.to(gpu), Vs.to(gpu), vcfg, want_x=True)
+    agree = float((q.cpu().long() == q_ref.long()).float().mean())
+    print("vamp block agreement", agree, "best_iter", st["best_iter"], tr["best_iter"], "stop", st["stop_iter"],
+          tr["stop_iter"], "obs", st["obs_precision_final"], tr["obs_final"])
+    assert agree >= 0.999
+    assert _rel(rtn.cpu(), rtn_ref) < 1e-4
+    assert abs(float(e.mean()) - float(e_ref.mean())) <= 5e-3 * float(e_ref.mean())
+
+
+def test_cd_polish_matches_oracle(gpu):
+    W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq = _setup_block(256, 512, 4, 128, "cd")
+    q0 = torch.clamp(torch.round(W / sf) + zf, 0, maxq).to(torch.uint8)
+    Y_u = W @ Vs
+    x_pol, acc_ref = ou.scalar_greedy_cd(xr[:128], Y_u[:128], Vs, Hw, sf[:128], zf[:128], maxq, 3)
+    q_ref = ou.nearest_atom_idx(x_pol, sf[:128], zf[:128], maxq)
+    q, eb, ea, imp, acc = ops.uniform_cd_polish(W.to(gpu), q0.to(gpu), sg.to(gpu), zg.to(gpu), 128, maxq, Vs.to(gpu),
+                                                Hw.to(gpu), block_rows=128, sweeps=3, select=False)
+    agree = float((q[:128].cpu().long() == q_ref.long()).float().mean())
+    print("cd agreement", agree, "accepted", int(acc[:128].sum()), acc_ref)
+    assert agree >= 0.999
+    err_ref = ou.rankspace_error(Y_u[:128], ou.dequant_from_q(q_ref, sf[:128], zf[:128]), Vs)
+    assert abs(float(ea[:128].mean()) - float(err_ref.mean())) <= 1e-3 * float(err_ref.mean())
+    # the error never increases, and row blocks are independent (second block polished alone)
+    assert bool((ea <= eb * (1 + 1e-5) + 1e-9).all())
+    q2, _, ea2, _, _ = ops.uniform_cd_polish(W[128:].to(gpu), q0[128:].to(gpu), sg[128:].to(gpu), zg[128:].to(gpu),
+                                            128, maxq, Vs.to(gpu), Hw.to(gpu), block_rows=128, sweeps=3,
+                                            select=False)
+    assert float((q2.cpu() == q[128:].cpu()).float().mean()) >= 0.999
+
+
+@pytest.mark.parametrize("rotation", ["none", "internal_hadamard"])
+def test_adapter_end_to_end_matches_oracle(gpu, rotation):
+    rows, cols, bits, gs = 256, 512, 4, 128
+    W, H = make_layer(rows, cols, tokens=2048, seed_key=f"e2e:{rotation}")
+    Hg = 2.0 * H
+    ref = ou.run_mpq_quantization(W, Hg, bits, gs, "model.layers.0.mlp.up_proj", RECIPE, rotation=rotation)
+    vcfg = UniformVampConfig(**RECIPE)
+    Q, q, s, z, g_idx, t, st = run_mpq_quantization(W=W.to(gpu), H=Hg.to(gpu), quantizer=None,
+                                                    qcfg=QCfg(bits, gs, rotation),
+                                                    module_name="model.layers.0.mlp.up_proj", vamp_cfg=vcfg,
+                                                    adapter_cfg=GPTQAdapterConfig(block_rows=128))
+    agree = float((q.cpu() == ref["q_int"]).float().mean())
+    proxy_ref = float(ref["proxy_rows"].sum())
+    print(rotation, "codes agreement", agree, "proxy", st["proxy_loss"], proxy_ref)
+    assert torch.equal(s.cpu(), ref["scale"]) or _rel(s.cpu(), ref["scale"]) < 1e-6
+    assert agree >= 0.999
+    assert abs(st["proxy_loss"] - proxy_ref) <= 0.005 * proxy_ref
+    assert _rel(Q.cpu(), ref["Q"]) < 0.05
