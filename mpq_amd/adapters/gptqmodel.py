@@ -122,12 +122,16 @@ def run_mpq_quantization(
     module_name: str,
     vamp_cfg: UniformVampConfig,
     adapter_cfg: GPTQAdapterConfig = GPTQAdapterConfig(),
+    precomputed_eigen: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor], Optional[torch.Tensor],
            Optional[torch.Tensor], float, Dict[str, Any]]:
     """Per-linear MPQ (uniform grid) on one GPU.
 
     Returns (Q fp32 rows x cols in the original basis, q_int uint8 (solver basis),
     scale_groups, zero_groups, g_idx int32, quant_time_s, stats) as the reference.
+    ``precomputed_eigen`` = (floored descending eigenvalues, eigenvectors) of the
+    unrotated ``hessian_scale * H`` replaces the device ``eigh`` (used to compare
+    against another eigensolver's output on identical inputs).
     """
     start = time.time()
     device = W.device
@@ -154,8 +158,15 @@ def run_mpq_quantization(
 
     H_work = float(adapter_cfg.hessian_scale) * H
     t0 = time.time()
-    lam, S, V, Vs, eigen_floor = vamp_hessian_eigen(H_work, jitter_base=adapter_cfg.jitter_base,
-                                                    floor_scale=adapter_cfg.eigen_floor_scale)
+    if precomputed_eigen is not None:
+        lam = precomputed_eigen[0].to(device=device, dtype=torch.float32).contiguous()
+        V = precomputed_eigen[1].to(device=device, dtype=torch.float32).contiguous()
+        S = torch.sqrt(lam)
+        Vs = ops.scale_columns(V, S)
+        eigen_floor = float(lam.min().item())
+    else:
+        lam, S, V, Vs, eigen_floor = vamp_hessian_eigen(H_work, jitter_base=adapter_cfg.jitter_base,
+                                                        floor_scale=adapter_cfg.eigen_floor_scale)
     torch.cuda.synchronize(device)
     timings["eigh_s"] = time.time() - t0
     signs = rotation["signs"]

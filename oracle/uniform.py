@@ -120,8 +120,12 @@ def rankspace_error(Y_u, x, Vs):
 
 # ---- polish ----------------------------------------------------------------
 
-def scalar_greedy_cd(x, Y_u, Vs, gram, scale, zero, maxq, sweeps, accept_tol=0.0):
-    """mpq/polish/triton_scalar_cd.py:164-307 with update_backend="torch" (per-column order)."""
+def scalar_greedy_cd(x, Y_u, Vs, gram, scale, zero, maxq, sweeps, accept_tol=0.0, target_div=True):
+    """mpq/polish/triton_scalar_cd.py:164-307 (per-column order, torch ops).
+
+    ``target_div=True`` forms the RTN target as ``x + rhs / diag`` like the GPU sweep kernel the
+    reference dispatches on CUDA (:73); ``False`` uses the torch twin's ``x + rhs * (1/diag)`` (:265).
+    """
     x = x.to(torch.float32).clone()
     res_u = Y_u - x.matmul(Vs)
     rhs = res_u.matmul(Vs.T.contiguous())
@@ -138,7 +142,7 @@ def scalar_greedy_cd(x, Y_u, Vs, gram, scale, zero, maxq, sweeps, accept_tol=0.0
             xc = x[:, col]
             sc = scale[:, col].clamp_min(1e-12)
             zc = zero[:, col]
-            target = xc + r * dinv[col]
+            target = xc + r / diag[col] if target_div else xc + r * dinv[col]
             q = torch.clamp(torch.round(target / sc + zc), 0, maxq).to(torch.int32)
             xq = sc * (q.to(torch.float32) - zc)
             d = xq - xc

@@ -1,0 +1,128 @@
+"""Write golden input/output vectors from the reference implementation (run in the build container only).
+
+Only functions whose results no closed form, brute force or invariant pins bit for bit are
+recorded here: the VAMP loops (discrete control flow: gamma retries, damping, best-iterate stop,
+EM chain), the greedy coordinate-descent sweeps (near-tie accept cascades) and the E8P12
+posterior (torch's reduction orders).  The reference runs on its CPU dispatch (eager denoisers,
+``block_coordinate_descent_rankspace`` / ``uniform_scalar_diag_greedy_cd(update_backend="torch")``).
+The E8P12 functions need a codebook object of class ``E8P12_codebook``; the build's own table
+(mpq_amd/codebook.py) is passed in.
+
+Usage:  python tests/golden/make_golden.py /root/reference
+Output: tests/golden/*.npz (inputs and outputs only; no reference code is stored).
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+
+
+def _np(d):
+    out = {}
+    for k, v in d.items():
+        if isinstance(v, torch.Tensor):
+            out[k] = v.detach().cpu().numpy()
+        elif isinstance(v, (int, float, bool)):
+            out[k] = np.asarray(v)
+    return out
+
+
+def main(ref_root: str) -> None:
+    sys.path.insert(0, ROOT)
+    sys.path.insert(0, ref_root)
+    torch.set_num_threads(1)  # fixed BLAS partition for reproducible vectors
+    from mpq.linear import vamp_rankspace_error  # noqa: F401  (reference)
+    from mpq.polish.triton_scalar_cd import uniform_scalar_diag_greedy_cd  # reference
+    from mpq.priors.e8p12 import vamp_vector_discrete_mmse_e8p12, vamp_vector_map_e8p12  # reference
+    from mpq.solver import (  # reference
+        E8P12VampConfig as RefE8Cfg,
+        UniformVampConfig as RefUCfg,
+        solve_e8p12_rankspace_vamp,
+        solve_uniform_rankspace_vamp,
+    )
+
+    from mpq_amd.codebook import E8P12_codebook, grid_numpy
+    from oracle import uniform as ou
+    from tests.uniform_cases import make_layer
+
+    # ---- uniform VAMP row blocks (CPU dispatch, polish via block_coordinate_descent_rankspace)
+    for name, rotate, bits, rows, cols in (("uvamp_r0_b4", False, 4, 64, 256), ("uvamp_r1_b3", True, 3, 64, 256),
+                                           ("uvamp_r1_b4", True, 4, 64, 256)):
+        W, H = make_layer(rows, cols, tokens=1024, seed_key=f"golden:{name}")
+        lam, V, _ = ou.hessian_eigen(H)
+        if rotate:
+            signs, had = ou.rotation_plan(cols, name)
+            W = ou.hadamard_rows(W * signs.view(1, -1), had)
+            H = ou.hadamard_rows(ou.hadamard_rows(H.T.contiguous() * signs.view(1, -1), had).T.contiguous()
+                                 * signs.view(1, -1), had)
+            V = ou.hadamard_rows(V.T.contiguous() * signs.view(1, -1), had).T.contiguous()
+        S = torch.sqrt(lam)
+        Vs = V * S.unsqueeze(0)
+        maxq = 2 ** bits - 1
+        sc, zc = zip(*[ou.gptq_find_params(W[:, g:g + 128], maxq) for g in range(0, cols, 128)])
+        sf = torch.repeat_interleave(torch.cat(sc, 1), 128, dim=1)
+        zf = torch.repeat_interleave(torch.cat(zc, 1), 128, dim=1)
+        xr = sf * (torch.clamp(torch.round(W / sf) + zf, 0, maxq) - zf)
+        cfg = RefUCfg(iters=16, damping=0.5, prior_tau=0.2, polish_sweeps=3, polish_mode="block_cd",
+                      vamp_backend="eager", block_cd_backend="eager")
+        cfg0 = RefUCfg(iters=16, damping=0.5, prior_tau=0.2, polish_sweeps=0, vamp_backend="eager")
+        q0, x0, e0, r0, st0 = solve_uniform_rankspace_vamp(W=W, x_rtn=xr, scale_full=sf, zero_full=zf, maxq=maxq,
+                                                           V=V, Vh=V.T.contiguous(), S=S, Vs=Vs, cfg=cfg0,
+                                                           gram_full=H, log_stats=False)
+        q, x, e, r, st = solve_uniform_rankspace_vamp(W=W, x_rtn=xr, scale_full=sf, zero_full=zf, maxq=maxq, V=V,
+                                                      Vh=V.T.contiguous(), S=S, Vs=Vs, cfg=cfg, gram_full=H,
+                                                      log_stats=False)
+        Yu = W.matmul(Vs)
+        xt, _ = uniform_scalar_diag_greedy_cd(x=x0, Y_u=Yu, Vs=Vs, gram_full=H, scale=sf, zero=zf, maxq=maxq,
+                                              sweeps=3, update_backend="torch")
+        np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **_np({
+            "W": W, "H": H, "V": V, "S": S, "scale_full": sf, "zero_full": zf, "x_rtn": xr, "maxq": maxq,
+            "q_vamp": q0, "err_vamp": e0, "best_iter": st0["best_iter"], "stop_iter": st0["stop_iter"],
+            "obs_final_vamp": st0["obs_precision_final"], "q_final": q, "err_final": e, "rtn_err": r,
+            "obs_initial": st["obs_precision_initial"], "x_cd_twin": xt}))
+        print(name, "best_iter", st0["best_iter"], "stop", st0["stop_iter"], "polish updates", st["polish_updates"])
+
+    # ---- E8P12: MAP, posterior, VAMP loop with the build's table as the codebook
+    cb = E8P12_codebook()
+    g = torch.Generator().manual_seed(1234)
+    rows, nb = 16, 32
+    r1 = torch.randn(rows, nb, 8, generator=g) * 0.7
+    center = r1 + 0.2 * torch.randn(rows, nb, 8, generator=g)
+    gam = torch.exp(torch.randn(rows, 1, generator=g)) * 2.0
+    mp = vamp_vector_map_e8p12(r1_blocks=r1, gamma1=gam, cb=cb, prior_center_blocks=center, prior_tau=0.25)
+    post = vamp_vector_discrete_mmse_e8p12(r1_blocks=r1, gamma1=gam, cb=cb, prior_center_blocks=center,
+                                           prior_tau=0.25, compile_prior=False, return_logZ_blocks=True)
+    np.savez_compressed(os.path.join(HERE, "e8p12_posterior.npz"), **_np({
+        "r1": r1, "gamma1": gam, "center": center, "map_idxs": mp["map_idxs"], "x1": post["x1_blocks"],
+        "var1": post["var1"], "alpha1": post["alpha1"], "logZ": post["logZ_blocks"],
+        "post_map_idxs": post["map_idxs"]}))
+    print("e8p12 posterior written")
+
+    W, H = make_layer(32, 128, tokens=1024, seed_key="golden:e8vamp", heavy=True)
+    Wr = W / W.square().mean().sqrt()
+    lamq, Vq, _ = ou.hessian_eigen(H)
+    S = torch.sqrt(lamq)
+    Vs = Vq * S.unsqueeze(0)
+    cb_t = torch.from_numpy(grid_numpy())
+    hat0 = cb_t[torch.from_numpy(np.asarray(vamp_vector_map_e8p12(
+        r1_blocks=Wr.view(32, 16, 8), gamma1=torch.ones(32, 1), cb=cb)["map_idxs"]).reshape(-1))].view(32, 128)
+    ecfg = RefE8Cfg(iters=16, polish_sweeps=3, compile_prior=False)
+    hat, idx, err, est = solve_e8p12_rankspace_vamp(Wr=Wr, hatWr_init=hat0, cb=cb, V=Vq, Vh=Vq.T.contiguous(), S=S,
+                                                    Vs=Vs, cfg=ecfg, log_stats=False)
+    ecfg0 = RefE8Cfg(iters=16, polish_sweeps=0, compile_prior=False)
+    hatv, idxv, errv, estv = solve_e8p12_rankspace_vamp(Wr=Wr, hatWr_init=hat0, cb=cb, V=Vq, Vh=Vq.T.contiguous(),
+                                                        S=S, Vs=Vs, cfg=ecfg0, log_stats=False)
+    np.savez_compressed(os.path.join(HERE, "e8p12_vamp.npz"), **_np({
+        "Wr": Wr, "H": H, "V": Vq, "S": S, "hat0": hat0, "idx_vamp": idxv, "err_vamp": errv, "idx_final": idx,
+        "err_final": err, "obs_initial": est["obs_precision_initial"], "obs_final": est["obs_precision_final"]}))
+    print("e8p12 vamp written; polish updates", est["polish_updates"])
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
