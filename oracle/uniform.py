@@ -157,8 +157,11 @@ def scalar_greedy_cd(x, Y_u, Vs, gram, scale, zero, maxq, sweeps, accept_tol=0.0
     return x, accepted
 
 
-def block_cd_scalar(x, Y_u, Vs, scale, zero, maxq, sweeps, accept_tol=0.0):
-    """mpq/polish/block_cd.py:332-625, block_size=1, metric diag, greedy_gain order (CPU dispatch)."""
+def block_cd_scalar(x, Y_u, Vs, scale, zero, maxq, sweeps, accept_tol=0.0, max_cols=0):
+    """mpq/polish/block_cd.py:332-625, block_size=1, metric diag, greedy_gain order (CPU dispatch).
+
+    ``max_cols`` > 0 stops each sweep after that many columns (a bounded sample for timing).
+    """
     B, n = x.shape
     x = x.to(torch.float32).clone()
     Vs_t = Vs.T.contiguous()
@@ -171,6 +174,8 @@ def block_cd_scalar(x, Y_u, Vs, scale, zero, maxq, sweeps, accept_tol=0.0):
         rhs_all = res_u.matmul(Vs_t)
         gain = (rhs_all.square() * dinv_all.unsqueeze(0)).mean(dim=0)
         order = torch.argsort(gain, descending=True, stable=True).tolist()
+        if max_cols > 0:
+            order = order[:max_cols]
         for j in order:
             xb = x[:, j:j + 1]
             rhs = res_u.matmul(Vs_t[:, j:j + 1])
