@@ -62,6 +62,72 @@ int mpq_e8p12_map(const float* r, int64_t n, const float* gamma, int64_t gamma_d
                   const float* center, const float* scale, float tau, int64_t* idx64,
                   uint16_t* idx16, float* vals, float* err, float* score, mpq_stream_t stream);
 
+/*
+ * E8P12 posterior denoiser for rows x nb 8-blocks: posterior mean x1 (rows*nb x 8),
+ * per-block variance var (rows*nb), MAP index (int64, optional) and codeword
+ * map_vals (rows*nb x 8), alpha1 = gamma_row * mean(var) (rows, optional).
+ * Prior folding as mpq_e8p12_map.  Blocks whose folded precision is >= 1e3 snap to
+ * the MAP codeword with zero variance.  Replaces mpq/priors/e8p12.py:815-968
+ * (vamp_vector_discrete_mmse_e8p12, without diagnostics) and its per-branch
+ * statistics mpq/priors/e8p12.py:169-308.
+ */
+int mpq_e8p12_denoise(const float* r, int64_t rows, int64_t nb, const float* gamma,
+                      const float* center, const float* scale, float tau, float* x1, float* var,
+                      int64_t* map_idx, float* map_vals, float* alpha1, mpq_stream_t stream);
+
+/* Mirrors E8P12VampConfig (mpq/solver.py:59-82) without the polish fields. */
+typedef struct MpqE8P12VampConfig {
+  int iters;
+  float damping;
+  float gamma_start;
+  float gamma_retry_factor;
+  int gamma_retry_steps;
+  float prior_tau;
+  double obs_precision; /* > 0: fixed observation precision (EM off) */
+  int em_obs_precision;
+  double em_obs_precision_damping;
+  double em_obs_precision_min;
+  double em_obs_precision_max;
+  int best_iterate;
+} MpqE8P12VampConfig;
+
+/* Per-solve statistics (subset of mpq/solver.py:1236-1276). */
+typedef struct MpqE8P12VampStats {
+  int iters;
+  int best_iter;
+  int stop_iter;
+  int alpha1_retry_count;
+  int alpha2_clip_count;
+  int gamma2_invalid_count;
+  double obs_precision_initial;
+  double obs_precision_final;
+  double obs_precision_mean;
+  double alpha1_mean;
+  double alpha2_mean;
+  double rankspace_error_mean; /* of the final MAP decision */
+} MpqE8P12VampStats;
+
+/* Workspace bytes needed by mpq_e8p12_vamp_solve for a rows x n block. */
+int64_t mpq_e8p12_vamp_workspace_size(int64_t rows, int64_t n);
+
+/*
+ * E8P12-prior VAMP on one row block, without the polish: replaces
+ * mpq/solver.py:853-1138 (solve_e8p12_rankspace_vamp up to the polish) with the
+ * posterior denoiser of mpq_e8p12_denoise, the LMMSE/EM/error steps shared with
+ * mpq_uniform_vamp_solve and the final factorized MAP (mpq/solver.py:1124-1138).
+ *   Wr, hat_init: rows x n (n % 8 == 0); V, Vs: n x n; S: n
+ *   prior_scale: rows*n/8 block scales (NULL: absmax of each Wr block)
+ *   idx_out: rows x n/8 int64 codeword indices, hat_out rows x n codewords,
+ *   err_out (rows), r1_out (rows x n), gamma1_out (rows): optional
+ * Synchronises `stream` twice per iteration to read small status blocks.
+ */
+int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, const float* hat_init,
+                         const float* V, const float* S, const float* Vs, const float* prior_scale,
+                         const MpqE8P12VampConfig* cfg, double obs_init, int64_t* idx_out,
+                         float* hat_out, float* err_out, float* r1_out, float* gamma1_out,
+                         MpqE8P12VampStats* stats, void* workspace, int64_t workspace_bytes,
+                         mpq_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Dense algebra                                                            */
 /* ------------------------------------------------------------------------ */

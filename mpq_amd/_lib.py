@@ -31,6 +31,11 @@ SIGNATURES = {
     "mpq_clear_error": (None, []),
     "mpq_e8p12_map": (c_int, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_float,
                               c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "mpq_e8p12_denoise": (c_int, [c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_float, c_ptr, c_ptr, c_ptr,
+                                  c_ptr, c_ptr, c_ptr]),
+    "mpq_e8p12_vamp_workspace_size": (c_i64, [c_i64, c_i64]),
+    "mpq_e8p12_vamp_solve": (c_int, [c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_double,
+                                     c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
     "mpq_gemm_f32": (c_int, [c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_int, c_ptr,
                              c_ptr, c_i64, c_float, c_float, c_ptr, c_i64, c_ptr]),
     "mpq_gptq_find_params": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_ptr, c_ptr]),
@@ -91,6 +96,44 @@ class UniformVampStatsC(ctypes.Structure):
         ("alpha2_mean", ctypes.c_double),
         ("best_rankspace_error_mean", ctypes.c_double),
         ("rtn_rankspace_error_mean", ctypes.c_double),
+    ]
+
+
+class E8P12VampConfigC(ctypes.Structure):
+    """Mirror of MpqE8P12VampConfig (include/mpq_amd.h)."""
+
+    _fields_ = [
+        ("iters", ctypes.c_int),
+        ("damping", ctypes.c_float),
+        ("gamma_start", ctypes.c_float),
+        ("gamma_retry_factor", ctypes.c_float),
+        ("gamma_retry_steps", ctypes.c_int),
+        ("prior_tau", ctypes.c_float),
+        ("obs_precision", ctypes.c_double),
+        ("em_obs_precision", ctypes.c_int),
+        ("em_obs_precision_damping", ctypes.c_double),
+        ("em_obs_precision_min", ctypes.c_double),
+        ("em_obs_precision_max", ctypes.c_double),
+        ("best_iterate", ctypes.c_int),
+    ]
+
+
+class E8P12VampStatsC(ctypes.Structure):
+    """Mirror of MpqE8P12VampStats (include/mpq_amd.h)."""
+
+    _fields_ = [
+        ("iters", ctypes.c_int),
+        ("best_iter", ctypes.c_int),
+        ("stop_iter", ctypes.c_int),
+        ("alpha1_retry_count", ctypes.c_int),
+        ("alpha2_clip_count", ctypes.c_int),
+        ("gamma2_invalid_count", ctypes.c_int),
+        ("obs_precision_initial", ctypes.c_double),
+        ("obs_precision_final", ctypes.c_double),
+        ("obs_precision_mean", ctypes.c_double),
+        ("alpha1_mean", ctypes.c_double),
+        ("alpha2_mean", ctypes.c_double),
+        ("rankspace_error_mean", ctypes.c_double),
     ]
 
 

@@ -28,9 +28,11 @@ LIB_PATH = os.path.join(HERE, LIB_NAME)
 
 HIP_SOURCES = [
     "e8p12_map.hip",
+    "e8p12_posterior.hip",
     "gemm.hip",
     "elementwise.hip",
     "uniform_vamp.hip",
+    "e8p12_vamp.hip",
     "cd_uniform.hip",
 ]
 CXX_SOURCES = [

@@ -1,0 +1,307 @@
+// E8P12-prior VAMP on one row block (gfx950).
+//
+// Replaces mpq/solver.py:853-1138 (solve_e8p12_rankspace_vamp up to the polish, which
+// is mpq_e8p12_cd_polish): the denoiser is the E8P12 posterior (mpq_e8p12_denoise),
+// the linear module, EM and messages are the kernels shared with the uniform driver
+// (vamp_common.h), the final decision is the factorized MAP of (r1, gamma1)
+// (mpq/solver.py:1124-1138).  best_iterate (off in the recipe) is supported.
+// Host control flow with two small status reads per iteration.
+#include <cmath>
+
+#include "gemm.h"
+#include "kernels.h"
+#include "mpq_amd.h"
+#include "vamp_common.h"
+
+namespace mpq {
+
+hipError_t e8p12_posterior(const float* r, int64_t n, const float* gamma, int64_t gamma_div,
+                           const float* center, const float* scale, float tau, const float* map_vals,
+                           float* x1, float* var, hipStream_t stream);
+
+namespace {
+
+inline int64_t a64(int64_t v) { return (v + 63) / 64 * 64; }
+
+struct E8Plan {
+  int64_t rows, n, nb, nchunks;
+  int splits, bn;
+  int64_t bytes;
+};
+
+E8Plan e8_plan(int64_t rows, int64_t n) {
+  E8Plan p;
+  p.rows = rows;
+  p.n = n;
+  p.nb = n / 8;
+  p.nchunks = (n + kChunk - 1) / kChunk;
+  int bn = 128;
+  p.splits = choose_splits(rows, n, n, (int64_t)1 << 62, &bn);
+  p.bn = bn;
+  const int64_t mat = a64(rows * n) * 4;
+  int64_t b = 7 * mat;                          // Yu r1 r2 r2prev x1 map_vals r1_best
+  b += (int64_t)p.splits * mat;                 // partials
+  b += a64(rows * p.nb) * 4;                    // var1
+  b += a64(rows * p.nb) * 8;                    // map idx
+  b += a64(16 * rows) * 4;                      // row arrays
+  b += a64(3 * rows * p.nchunks) * 4;           // chunk partials
+  b += 256;                                     // status
+  p.bytes = b;
+  return p;
+}
+
+VampStatus* host_status_e8() {
+  static thread_local VampStatus* h = nullptr;
+  if (!h && hipHostMalloc((void**)&h, sizeof(VampStatus), hipHostMallocDefault) != hipSuccess) h = nullptr;
+  return h;
+}
+
+hipError_t product(const float* A, const float* B, bool trans_b, int64_t rows, int64_t n, float* P, int splits,
+                   int bn, hipStream_t stream) {
+  GemmParams p{};
+  p.M = rows; p.N = n; p.K = n;
+  p.A = A; p.lda = n; p.B = B; p.ldb = n; p.trans_b = trans_b;
+  p.C = P; p.ldc = n; p.split_stride = a64(rows * n);
+  p.alpha = 1.f; p.beta = 0.f; p.mode = kGemmPartials;
+  return gemm_partials(p, splits, bn, stream);
+}
+
+}  // namespace
+}  // namespace mpq
+
+extern "C" int mpq_e8p12_map(const float* r, int64_t n, const float* gamma, int64_t gamma_div,
+                             const float* center, const float* scale, float tau, int64_t* idx64,
+                             uint16_t* idx16, float* vals, float* err, float* score, hipStream_t stream);
+
+extern "C" int64_t mpq_e8p12_vamp_workspace_size(int64_t rows, int64_t n) {
+  if (rows <= 0 || n <= 0 || n % 8) return 0;
+  return mpq::e8_plan(rows, n).bytes;
+}
+
+extern "C" int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, const float* hat_init,
+                                    const float* V, const float* S, const float* Vs, const float* prior_scale,
+                                    const MpqE8P12VampConfig* cfg, double obs_init, int64_t* idx_out,
+                                    float* hat_out, float* err_out, float* r1_out, float* gamma1_out,
+                                    MpqE8P12VampStats* stats, void* workspace, int64_t workspace_bytes,
+                                    hipStream_t stream) {
+  using namespace mpq;
+  MPQ_CHECK_ARG(rows > 0 && n > 0 && n % 8 == 0, "E8P12 solver expects n divisible by 8; got n=%lld",
+                (long long)n);
+  MPQ_CHECK_ARG(rows <= 65535, "mpq_e8p12_vamp_solve: at most 65535 rows per block");
+  MPQ_CHECK_ARG(Wr && hat_init && V && S && Vs && cfg && idx_out && hat_out && workspace,
+                "mpq_e8p12_vamp_solve: null argument");
+  const E8Plan pl = e8_plan(rows, n);
+  MPQ_CHECK_ARG(workspace_bytes >= pl.bytes, "mpq_e8p12_vamp_solve: workspace too small (%lld < %lld)",
+                (long long)workspace_bytes, (long long)pl.bytes);
+  VampStatus* hs = host_status_e8();
+  MPQ_CHECK_ARG(hs != nullptr, "mpq_e8p12_vamp_solve: pinned status buffer unavailable");
+  const int64_t nb = pl.nb;
+  const int nchunks = (int)pl.nchunks;
+  const int64_t mat = a64(rows * n) * 4;
+  const int64_t sstride = a64(rows * n);
+  char* p = static_cast<char*>(workspace);
+  float* Yu = (float*)p; p += mat;
+  float* r1 = (float*)p; p += mat;
+  float* r2 = (float*)p; p += mat;
+  float* r2prev = (float*)p; p += mat;
+  float* x1 = (float*)p; p += mat;
+  float* mvals = (float*)p; p += mat;
+  float* r1_best = (float*)p; p += mat;
+  float* P = (float*)p; p += (int64_t)pl.splits * mat;
+  float* var1 = (float*)p; p += a64(rows * nb) * 4;
+  int64_t* midx = (int64_t*)p; p += a64(rows * nb) * 8;
+  float* rowbuf = (float*)p; p += a64(16 * rows) * 4;
+  float* part = (float*)p; p += a64(3 * rows * nchunks) * 4;
+  VampStatus* status = (VampStatus*)p;
+  float* g1 = rowbuf + 0 * rows;
+  float* g1w = rowbuf + 1 * rows;
+  float* a1raw = rowbuf + 2 * rows;
+  float* a1 = rowbuf + 3 * rows;
+  float* eta1 = rowbuf + 4 * rows;
+  float* g2new = rowbuf + 5 * rows;
+  float* g2 = rowbuf + 6 * rows;
+  float* g2prev = rowbuf + 7 * rows;
+  float* eta2 = rowbuf + 8 * rows;  // 3 rows: eta2, EM row stat, alpha2
+  float* g1new = rowbuf + 11 * rows;
+  float* errrow = rowbuf + 12 * rows;
+  float* g1_best = rowbuf + 13 * rows;
+  const dim3 eg((unsigned)nchunks, (unsigned)rows), eb(kEW);
+  const float tau = cfg->prior_tau;
+  const float* center = tau > 0.f ? Wr : nullptr;
+  auto sync_status = [&]() -> int {
+    MPQ_HIP_TRY(hipMemcpyAsync(hs, status, sizeof(VampStatus), hipMemcpyDeviceToHost, stream));
+    MPQ_HIP_TRY(hipStreamSynchronize(stream));
+    return kOk;
+  };
+  int rc;
+  // MAP decision of (r, g) into midx / mvals and its rank-space error into errrow / status.err_mean
+  auto map_state = [&](const float* r, const float* g) -> int {
+    int e = mpq_e8p12_map(r, rows * nb, g, nb, center, prior_scale, tau, midx, nullptr, mvals, nullptr, nullptr,
+                          stream);
+    if (e != kOk) return e;
+    MPQ_HIP_TRY(product(mvals, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
+    hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, pl.splits, sstride, Yu, part);
+    hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, part, errrow, status);
+    MPQ_LAUNCH_CHECK();
+    return kOk;
+  };
+
+  // ---- setup: Yu, gamma1, obs warm start
+  MPQ_HIP_TRY(product(Wr, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
+  MPQ_HIP_TRY(splitk_reduce(P, pl.splits, rows, n, Yu, n, 1.f, 0.f, stream));
+  MPQ_HIP_TRY(product(hat_init, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
+  hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, pl.splits, sstride, Yu, part);
+  hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, part, errrow, status);
+  hipLaunchKernelGGL(sqdiff_part_kernel, eg, eb, 0, stream, n, Wr, n, hat_init, n, part);
+  hipLaunchKernelGGL(rows_gamma_init_kernel, dim3(1), eb, 0, stream, rows, n, nchunks, part, cfg->gamma_start, g1,
+                     status);
+  MPQ_LAUNCH_CHECK();
+  if ((rc = sync_status()) != kOk) return rc;
+  if (hs->g1_invalid) {
+    set_error("gamma1_init invalid: expected finite and > 1e-12.");
+    set_error_code(kNumerical);
+    return kNumerical;
+  }
+  double obs;
+  if (cfg->obs_precision > 0.0) obs = cfg->obs_precision;
+  else if (obs_init > 0.0) obs = obs_init;
+  else {
+    float mm = hs->err_sum / (float)(rows * n);
+    obs = 1.0 / (double)(mm < 1e-12f ? 1e-12f : mm);
+  }
+  const double obs_initial = obs;
+  const bool em_active = cfg->em_obs_precision && cfg->obs_precision <= 0.0;
+  MPQ_HIP_TRY(hipMemcpyAsync(r1, hat_init, rows * n * 4, hipMemcpyDeviceToDevice, stream));
+
+  const bool best_iterate = cfg->best_iterate != 0;
+  double best_err_mean = INFINITY;
+  double best_obs = obs;
+  auto snapshot = [&](float* rd, float* gd, const float* rs, const float* gs) -> int {
+    MPQ_HIP_TRY(hipMemcpyAsync(rd, rs, rows * n * 4, hipMemcpyDeviceToDevice, stream));
+    MPQ_HIP_TRY(hipMemcpyAsync(gd, gs, rows * 4, hipMemcpyDeviceToDevice, stream));
+    return kOk;
+  };
+  if (best_iterate) {
+    // best-iterate bookkeeping (mpq/solver.py:940-958)
+    if ((rc = map_state(r1, g1)) != kOk) return rc;
+    if ((rc = snapshot(r1_best, g1_best, r1, g1)) != kOk) return rc;
+    if ((rc = sync_status()) != kOk) return rc;
+    best_err_mean = (double)hs->err_mean;
+  }
+  int best_iter = -1, stop_iter = -1, a1_retry = 0, a2_clip = 0, g2_invalid = 0, n_logged = 0;
+  int reported_iters = cfg->iters > 0 ? cfg->iters : 0;
+  double obs_sum = 0.0, a1_sum = 0.0, a2_sum = 0.0;
+  bool has_prev = false;
+  const float damping = cfg->damping;
+  const float retry_factor = cfg->gamma_retry_factor > 1.000001f ? cfg->gamma_retry_factor : 1.000001f;
+  const int retry_steps = cfg->gamma_retry_steps > 0 ? cfg->gamma_retry_steps : 0;
+  const int iters = cfg->iters > 0 ? cfg->iters : 0;
+  for (int it = 0; it < iters; ++it) {
+    MPQ_HIP_TRY(hipMemcpyAsync(g1w, g1, rows * 4, hipMemcpyDeviceToDevice, stream));
+    for (int attempt = 0; attempt <= retry_steps; ++attempt) {
+      rc = mpq_e8p12_map(r1, rows * nb, g1w, nb, center, prior_scale, tau, nullptr, nullptr, mvals, nullptr, nullptr,
+                         stream);
+      if (rc != kOk) return rc;
+      MPQ_HIP_TRY(e8p12_posterior(r1, rows * nb, g1w, nb, center, prior_scale, tau, mvals, x1, var1, stream));
+      hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, nb, (int)nb, var1, g1w, has_prev ? 1 : 0,
+                         damping, g2prev, a1raw, a1, eta1, g2new, g2, status);
+      MPQ_LAUNCH_CHECK();
+      if ((rc = sync_status()) != kOk) return rc;
+      if (hs->a1_invalid == 0) break;
+      if (attempt >= retry_steps) {
+        if (hs->a1_nonfinite) {
+          set_error("alpha1 invalid: expected all in (1e-07, 1-1e-07).");
+          set_error_code(kNumerical);
+          return kNumerical;
+        }
+        break;
+      }
+      a1_retry += hs->a1_invalid;
+      hipLaunchKernelGGL(rows_retry_kernel, dim3(1), eb, 0, stream, rows, a1raw, retry_factor, g1w);
+      MPQ_LAUNCH_CHECK();
+    }
+    if (hs->g2new_invalid || hs->g2_invalid) {
+      ++g2_invalid;
+      continue;
+    }
+    const float a1_mean_it = hs->a1_mean;
+    const float obs_f = (float)obs;
+    hipLaunchKernelGGL(msg_r2_kernel, eg, eb, 0, stream, n, x1, r1, eta1, g1w, g2new, has_prev ? 1 : 0, damping,
+                       r2prev, r2);
+    MPQ_LAUNCH_CHECK();
+    MPQ_HIP_TRY(product(r2, V, false, rows, n, P, pl.splits, pl.bn, stream));
+    hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, P, pl.splits, sstride, Yu, S, g2, obs_f, x1, part);
+    hipLaunchKernelGGL(rows_lmmse_kernel, dim3(1), eb, 0, stream, rows, n, n, nchunks, part, g2, damping, eta2,
+                       g1new, g1, status);
+    MPQ_LAUNCH_CHECK();
+    MPQ_HIP_TRY(product(x1, V, true, rows, n, P, pl.splits, pl.bn, stream));
+    hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, P, pl.splits, sstride, r2, eta2, g2, g1new, damping,
+                       r1);
+    MPQ_LAUNCH_CHECK();
+    if (best_iterate) {
+      if ((rc = map_state(r1, g1)) != kOk) return rc;
+    }
+    if ((rc = sync_status()) != kOk) return rc;
+    a2_clip += hs->a2_clip;
+    if (em_active) {
+      const float den = hs->em_mean < 1e-12f ? 1e-12f : hs->em_mean;
+      const double beta_new = (double)n / (double)den;
+      const double beta_old = obs > 1e-12 ? obs : 1e-12;
+      const double d = cfg->em_obs_precision_damping;
+      double beta;
+      if (d >= 1.0) beta = beta_new;
+      else if (d <= 0.0) beta = beta_old;
+      else beta = std::exp((1.0 - d) * std::log(beta_old) + d * std::log(beta_new > 1e-12 ? beta_new : 1e-12));
+      beta = std::min(std::max(beta, cfg->em_obs_precision_min), cfg->em_obs_precision_max);
+      obs = beta;
+    }
+    std::swap(r2, r2prev);
+    std::swap(g2, g2prev);
+    has_prev = true;
+    obs_sum += obs;
+    a1_sum += a1_mean_it;
+    a2_sum += hs->a2_mean;
+    ++n_logged;
+    if (best_iterate) {
+      // keep the iterate whose MAP decision has the smallest rank-space error; stop at the
+      // first iterate that does not improve and restore the best (mpq/solver.py:1083-1121)
+      const double cur = (double)hs->err_mean;
+      const double tol = std::max(1e-10, std::fabs(best_err_mean) * 1e-8);
+      if (cur + tol < best_err_mean) {
+        best_err_mean = cur;
+        best_obs = obs;
+        best_iter = it;
+        if ((rc = snapshot(r1_best, g1_best, r1, g1)) != kOk) return rc;
+      } else {
+        if ((rc = snapshot(r1, g1, r1_best, g1_best)) != kOk) return rc;
+        obs = best_obs;
+        stop_iter = it;
+        reported_iters = it + 1;
+        break;
+      }
+    }
+  }
+  // ---- final MAP decision and its error (mpq/solver.py:1124-1138)
+  if ((rc = map_state(r1, g1)) != kOk) return rc;
+  if ((rc = sync_status()) != kOk) return rc;
+  MPQ_HIP_TRY(hipMemcpyAsync(idx_out, midx, rows * nb * 8, hipMemcpyDeviceToDevice, stream));
+  MPQ_HIP_TRY(hipMemcpyAsync(hat_out, mvals, rows * n * 4, hipMemcpyDeviceToDevice, stream));
+  if (err_out) MPQ_HIP_TRY(hipMemcpyAsync(err_out, errrow, rows * 4, hipMemcpyDeviceToDevice, stream));
+  if (r1_out) MPQ_HIP_TRY(hipMemcpyAsync(r1_out, r1, rows * n * 4, hipMemcpyDeviceToDevice, stream));
+  if (gamma1_out) MPQ_HIP_TRY(hipMemcpyAsync(gamma1_out, g1, rows * 4, hipMemcpyDeviceToDevice, stream));
+  if (stats) {
+    stats->iters = reported_iters;
+    stats->best_iter = best_iter;
+    stats->stop_iter = stop_iter;
+    stats->alpha1_retry_count = a1_retry;
+    stats->alpha2_clip_count = a2_clip;
+    stats->gamma2_invalid_count = g2_invalid;
+    stats->obs_precision_initial = obs_initial;
+    stats->obs_precision_final = obs;
+    stats->obs_precision_mean = n_logged ? obs_sum / n_logged : obs;
+    stats->alpha1_mean = n_logged ? a1_sum / n_logged : 0.0;
+    stats->alpha2_mean = n_logged ? a2_sum / n_logged : 0.0;
+    stats->rankspace_error_mean = (double)hs->err_mean;
+  }
+  return kOk;
+}

@@ -24,39 +24,12 @@
 #include "gemm.h"
 #include "kernels.h"
 #include "uniform_vamp.h"
+#include "vamp_common.h"
 
 namespace mpq {
 namespace {
 
-constexpr int kEW = 256;             // threads per element-wise work-group
-constexpr int kPer = 4;              // elements per thread
-constexpr int kChunk = kEW * kPer;   // columns per work-group
-constexpr float kAlphaEps = 1e-7f;
-constexpr float kPrecEps = 1e-12f;
-
-__device__ __forceinline__ float one_minus_alpha_eps() { return (float)(1.0 - 1e-7); }
-
-struct VampStatus {
-  int a1_invalid;
-  int a1_nonfinite;
-  int g2new_invalid;
-  int g2_invalid;
-  int a2_clip;
-  int g1_invalid;
-  int pad0, pad1;
-  float a1_mean;
-  float a2_mean;
-  float err_mean;
-  float em_mean;
-  float err_sum;
-  float pad2, pad3, pad4;
-};
-
 enum DenoiseMode : int { kPosterior = 0, kHardMap = 1, kHardRoundMean = 2, kFull = 3 };
-
-__device__ __forceinline__ float grp(const float* a, int64_t b, int64_t G, int64_t gs, int64_t j) {
-  return a[b * G + j / gs];
-}
 
 // Per element: posterior of a uniform grid a_q = s(q - z), q = 0..maxq, under the
 // channel N(r1, 1/gamma) and the prior N(W, (tau*s)^2)  (mpq/priors/uniform.py:177-191).
@@ -150,313 +123,6 @@ __global__ __launch_bounds__(kEW) void uniform_denoise_kernel(
     const float tot = block_sum(vsum, red);
     if (threadIdx.x == 0) var_part[b * nchunks + blockIdx.x] = tot;
   }
-}
-
-// alpha1 = gamma * mean_j(var) per row (mpq/priors/uniform.py:191), one work-group per row.
-__global__ __launch_bounds__(kEW) void row_alpha_kernel(int64_t n, const float* __restrict__ var,
-                                                        const float* __restrict__ gamma,
-                                                        float* __restrict__ alpha1) {
-  __shared__ float red[kEW / 64];
-  const int64_t b = blockIdx.x;
-  float acc = 0.f;
-  for (int64_t j = threadIdx.x; j < n; j += blockDim.x) acc += var[b * n + j];
-  const float t = block_sum(acc, red);
-  if (threadIdx.x == 0) alpha1[b] = gamma[b] * (t / (float)n);
-}
-
-// Row statistics after the denoiser (mpq/solver.py:575-615): alpha1, eta1,
-// gamma2_new, damped gamma2, validity counts.  One work-group, rows looped.
-__global__ __launch_bounds__(kEW) void rows_alpha1_kernel(
-    int64_t rows, int64_t n, int nchunks, const float* __restrict__ var_part,
-    const float* __restrict__ g1w, int has_prev, float damping, const float* __restrict__ g2prev,
-    float* __restrict__ alpha1_raw, float* __restrict__ alpha1, float* __restrict__ eta1,
-    float* __restrict__ g2new, float* __restrict__ g2, VampStatus* __restrict__ st) {
-  __shared__ float red[kEW / 64];
-  int inval = 0, nonfin = 0, g2n_bad = 0, g2_bad = 0;
-  const float hi = one_minus_alpha_eps();
-  for (int64_t b = threadIdx.x; b < rows; b += blockDim.x) {
-    float vs = var_part[b * nchunks];
-    for (int c = 1; c < nchunks; ++c) vs = vs + var_part[b * nchunks + c];
-    const float a1 = g1w[b] * (vs / (float)n);
-    alpha1_raw[b] = a1;
-    const bool fin = isfinite(a1);
-    const bool valid = fin && a1 > kAlphaEps && a1 < hi;
-    inval += !valid;
-    nonfin += !fin;
-    float a1c = a1;
-    if (isnan(a1c)) a1c = 0.5f;
-    else if (isinf(a1c)) a1c = a1c > 0.f ? hi : kAlphaEps;
-    a1c = a1c < kAlphaEps ? kAlphaEps : (a1c > hi ? hi : a1c);
-    alpha1[b] = a1c;
-    const float e1 = g1w[b] / a1c;
-    eta1[b] = e1;
-    const float gn = nan_to_num_clamp_min(e1 - g1w[b], 1e-12f, 1e12f, 1e-12f, kPrecEps);
-    g2new[b] = gn;
-    g2n_bad += !(isfinite(gn) && gn > kPrecEps);
-    float gd = gn;
-    if (has_prev && damping < 1.f) {
-      if (damping <= 0.f) {
-        gd = g2prev[b];
-      } else {
-        const float p = g2prev[b] < 1e-12f ? 1e-12f : g2prev[b];
-        const float q = gn < 1e-12f ? 1e-12f : gn;
-        gd = expf((1.0f - damping) * logf(p) + damping * logf(q));
-      }
-    }
-    g2[b] = gd;
-    g2_bad += !(isfinite(gd) && gd > kPrecEps);
-  }
-  // counts: exact in fp32 for < 2^24 rows
-  const float s_inval = block_sum((float)inval, red);
-  const float s_nonfin = block_sum((float)nonfin, red);
-  const float s_g2n = block_sum((float)g2n_bad, red);
-  const float s_g2 = block_sum((float)g2_bad, red);
-  float a1sum = 0.f;
-  if (threadIdx.x == 0) {
-    for (int64_t b = 0; b < rows; ++b) a1sum += alpha1[b];
-    st->a1_invalid = (int)s_inval;
-    st->a1_nonfinite = (int)s_nonfin;
-    st->g2new_invalid = (int)s_g2n;
-    st->g2_invalid = (int)s_g2;
-    st->a1_mean = a1sum / (float)rows;
-  }
-}
-
-// gamma retry (mpq/solver.py:594-596).
-__global__ void rows_retry_kernel(int64_t rows, const float* __restrict__ alpha1_raw, float factor,
-                                  float* __restrict__ g1w) {
-  const float hi = one_minus_alpha_eps();
-  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < rows;
-       b += (int64_t)gridDim.x * blockDim.x) {
-    const float a = alpha1_raw[b];
-    float g = g1w[b];
-    if (a <= kAlphaEps) g = g / factor;
-    if (a >= hi) g = g * factor;
-    g1w[b] = g < 1e-12f ? 1e-12f : g;
-  }
-}
-
-// r2 message (mpq/solver.py:605-612).
-__global__ __launch_bounds__(kEW) void msg_r2_kernel(int64_t n, const float* __restrict__ x1,
-                                                     const float* __restrict__ r1,
-                                                     const float* __restrict__ eta1,
-                                                     const float* __restrict__ g1w,
-                                                     const float* __restrict__ g2new, int has_prev,
-                                                     float damping, const float* __restrict__ r2prev,
-                                                     float* __restrict__ r2) {
-  const int64_t b = blockIdx.y;
-  const float e1 = eta1[b], gw = g1w[b], gn = g2new[b];
-  const bool damp = has_prev && damping < 1.f;
-  const float keep = 1.0f - damping;
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) {
-    const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
-    if (j >= n) continue;
-    const int64_t o = b * n + j;
-    const float rn = (e1 * x1[o] - gw * r1[o]) / gn;
-    r2[o] = damp ? keep * r2prev[o] + damping * rn : rn;
-  }
-}
-
-// LMMSE part 1 (mpq/linear.py:44-55): from P = r2 @ V, per element
-//   residual_before = Yu - P*s, denom = obs*s^2 + g2, coeff = obs*s/denom,
-//   c = residual_before*coeff (input of the second product); row partial sums of
-//   1/denom (alpha2), residual_after^2 and s^2/denom (EM, mpq/linear.py:74-77).
-__global__ __launch_bounds__(kEW) void lmmse_epi1_kernel(
-    int64_t n, const float* __restrict__ P, int splits, int64_t split_stride,
-    const float* __restrict__ Yu, const float* __restrict__ S, const float* __restrict__ g2,
-    float obs, float* __restrict__ c_out, float* __restrict__ part3) {
-  __shared__ float red[kEW / 64];
-  const int64_t b = blockIdx.y;
-  const int nchunks = gridDim.x;
-  const float gb = g2[b];
-  float sinv = 0.f, sres = 0.f, strace = 0.f;
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) {
-    const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
-    if (j >= n) continue;
-    const int64_t o = b * n + j;
-    float r2v = P[o];
-    for (int s = 1; s < splits; ++s) r2v = r2v + P[(int64_t)s * split_stride + o];
-    const float sj = S[j];
-    const float s2 = sj * sj;
-    const float denom = obs * s2 + gb;
-    const float rb = Yu[o] - r2v * sj;
-    const float coeff = (obs * sj) / denom;
-    c_out[o] = rb * coeff;
-    sinv += 1.0f / denom;
-    const float ra = rb * (gb / denom);
-    sres += ra * ra;
-    strace += s2 / denom;
-  }
-  const float t0 = block_sum(sinv, red);
-  const float t1 = block_sum(sres, red);
-  const float t2 = block_sum(strace, red);
-  if (threadIdx.x == 0) {
-    float* o = part3 + (b * nchunks + blockIdx.x) * 3;
-    o[0] = t0;
-    o[1] = t1;
-    o[2] = t2;
-  }
-}
-
-// Row update after LMMSE part 1 (mpq/solver.py:626-653): alpha2, eta2,
-// gamma1_new, damped gamma1 (written in place), EM row statistic.
-__global__ __launch_bounds__(kEW) void rows_lmmse_kernel(
-    int64_t rows, int64_t n, int64_t rank, int nchunks, const float* __restrict__ part3,
-    const float* __restrict__ g2, float damping, float* __restrict__ eta2,
-    float* __restrict__ g1new, float* __restrict__ g1, VampStatus* __restrict__ st) {
-  __shared__ float red[kEW / 64];
-  const float hi = one_minus_alpha_eps();
-  const float c0 = (float)(1.0 - (double)rank / (double)n);
-  int clip = 0;
-  for (int64_t b = threadIdx.x; b < rows; b += blockDim.x) {
-    const float* pp = part3 + b * nchunks * 3;
-    float sinv = pp[0], sres = pp[1], strace = pp[2];
-    for (int c = 1; c < nchunks; ++c) {
-      sinv = sinv + pp[3 * c + 0];
-      sres = sres + pp[3 * c + 1];
-      strace = strace + pp[3 * c + 2];
-    }
-    const float gb = g2[b];
-    const float a2raw = c0 + (gb / (float)n) * sinv;
-    clip += !(isfinite(a2raw) && a2raw > kAlphaEps && a2raw < hi);
-    float a2 = a2raw;
-    if (isnan(a2)) a2 = 0.5f;
-    else if (isinf(a2)) a2 = a2 > 0.f ? hi : kAlphaEps;
-    a2 = a2 < kAlphaEps ? kAlphaEps : (a2 > hi ? hi : a2);
-    const float e2 = gb / a2;
-    eta2[b] = e2;
-    const float gn = nan_to_num_clamp_min(e2 - gb, 1e-12f, 1e12f, 1e-12f, kPrecEps);
-    g1new[b] = gn;
-    float gd = gn;
-    if (damping < 1.f) {
-      if (damping <= 0.f) {
-        gd = g1[b];
-      } else {
-        const float p = g1[b] < 1e-12f ? 1e-12f : g1[b];
-        const float q = gn < 1e-12f ? 1e-12f : gn;
-        gd = expf((1.0f - damping) * logf(p) + damping * logf(q));
-      }
-    }
-    g1[b] = gd;
-    // EM statistic per row: |residual_after|^2 + trace term; alpha2 kept for stats
-    eta2[rows + b] = sres + strace;
-    eta2[2 * rows + b] = a2;
-  }
-  const float s_clip = block_sum((float)clip, red);
-  if (threadIdx.x == 0) {
-    float em = 0.f, a2s = 0.f;
-    for (int64_t b = 0; b < rows; ++b) {
-      em += eta2[rows + b];
-      a2s += eta2[2 * rows + b];
-    }
-    st->a2_clip = (int)s_clip;
-    st->em_mean = em / (float)rows;
-    st->a2_mean = a2s / (float)rows;
-  }
-}
-
-// LMMSE part 2 + r1 message (mpq/linear.py:51-52, mpq/solver.py:645-653):
-// x2 = r2 + sum_s P[s], r1_new = (eta2*x2 - g2*r2)/g1_new, r1 <- damped.
-__global__ __launch_bounds__(kEW) void lmmse_epi2_kernel(
-    int64_t n, const float* __restrict__ P, int splits, int64_t split_stride,
-    const float* __restrict__ r2, const float* __restrict__ eta2, const float* __restrict__ g2,
-    const float* __restrict__ g1new, float damping, float* __restrict__ r1) {
-  const int64_t b = blockIdx.y;
-  const float e2 = eta2[b], gb = g2[b], gn = g1new[b];
-  const float keep = 1.0f - damping;
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) {
-    const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
-    if (j >= n) continue;
-    const int64_t o = b * n + j;
-    float d = P[o];
-    for (int s = 1; s < splits; ++s) d = d + P[(int64_t)s * split_stride + o];
-    const float r2v = r2[o];
-    const float x2 = r2v + d;
-    const float rn = (e2 * x2 - gb * r2v) / gn;
-    r1[o] = damping >= 1.f ? rn : keep * r1[o] + damping * rn;
-  }
-}
-
-// Rank-space error partials (mpq/linear.py:94): sum_j (Yu - sum_s P[s])^2.
-__global__ __launch_bounds__(kEW) void err_epi_kernel(int64_t n, const float* __restrict__ P,
-                                                      int splits, int64_t split_stride,
-                                                      const float* __restrict__ Yu,
-                                                      float* __restrict__ part) {
-  __shared__ float red[kEW / 64];
-  const int64_t b = blockIdx.y;
-  float acc = 0.f;
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) {
-    const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
-    if (j >= n) continue;
-    const int64_t o = b * n + j;
-    float v = P[o];
-    for (int s = 1; s < splits; ++s) v = v + P[(int64_t)s * split_stride + o];
-    const float d = Yu[o] - v;
-    acc += d * d;
-  }
-  const float t = block_sum(acc, red);
-  if (threadIdx.x == 0) part[b * gridDim.x + blockIdx.x] = t;
-}
-
-// Row sums of chunk partials -> out[b]; st->err_mean / err_sum over rows.
-__global__ __launch_bounds__(kEW) void rows_err_kernel(int64_t rows, int nchunks,
-                                                       const float* __restrict__ part,
-                                                       float* __restrict__ out,
-                                                       VampStatus* __restrict__ st) {
-  for (int64_t b = threadIdx.x; b < rows; b += blockDim.x) {
-    float v = part[b * nchunks];
-    for (int c = 1; c < nchunks; ++c) v = v + part[b * nchunks + c];
-    out[b] = v;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float s = 0.f;
-    for (int64_t b = 0; b < rows; ++b) s += out[b];
-    st->err_sum = s;
-    st->err_mean = s / (float)rows;
-  }
-}
-
-// gamma1 init (mpq/solver.py:481-483, :85-87): gamma_start * 0.25 / clamp(mean((W-x)^2), 1e-12).
-__global__ __launch_bounds__(kEW) void sqdiff_part_kernel(int64_t n, const float* __restrict__ W,
-                                                          int64_t ldw, const float* __restrict__ X,
-                                                          int64_t ldx, float* __restrict__ part) {
-  __shared__ float red[kEW / 64];
-  const int64_t b = blockIdx.y;
-  float acc = 0.f;
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) {
-    const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
-    if (j >= n) continue;
-    const float d = W[b * ldw + j] - X[b * ldx + j];
-    acc += d * d;
-  }
-  const float t = block_sum(acc, red);
-  if (threadIdx.x == 0) part[b * gridDim.x + blockIdx.x] = t;
-}
-
-__global__ __launch_bounds__(kEW) void rows_gamma_init_kernel(int64_t rows, int64_t n, int nchunks,
-                                                              const float* __restrict__ part,
-                                                              float gamma_start,
-                                                              float* __restrict__ g1,
-                                                              VampStatus* __restrict__ st) {
-  __shared__ float red[kEW / 64];
-  int bad = 0;
-  for (int64_t b = threadIdx.x; b < rows; b += blockDim.x) {
-    float v = part[b * nchunks];
-    for (int c = 1; c < nchunks; ++c) v = v + part[b * nchunks + c];
-    float mse = v / (float)n;
-    mse = mse < 1e-12f ? 1e-12f : mse;
-    const float g = gamma_start * (0.25f / mse);
-    g1[b] = g;
-    bad += !(isfinite(g) && g > kPrecEps);
-  }
-  const float s = block_sum((float)bad, red);
-  if (threadIdx.x == 0) st->g1_invalid = (int)s;
 }
 
 // ---------------------------------------------------------------------------

@@ -253,3 +253,58 @@ def uniform_cd_polish(W, q_in, scale, zero, group_size, maxq, Vs, H, *, block_ro
               _lib.ptr(q_out), _lib.ptr(eb), _lib.ptr(ea), _lib.ptr(imp), _lib.ptr(acc), _lib.ptr(ws),
               int(ws.numel()), _stream(dev))
     return q_out, eb, ea, imp, acc
+
+
+# ---- E8P12 VAMP ----------------------------------------------------------------
+
+def e8p12_vamp_config_c(cfg) -> "_lib.E8P12VampConfigC":
+    c = _lib.E8P12VampConfigC()
+    c.iters = max(int(cfg.iters), 0)
+    c.damping = float(cfg.damping)
+    c.gamma_start = float(cfg.gamma_start)
+    c.gamma_retry_factor = float(cfg.gamma_retry_factor)
+    c.gamma_retry_steps = int(cfg.gamma_retry_steps)
+    c.prior_tau = float(cfg.prior_tau)
+    c.obs_precision = float(cfg.obs_precision)
+    c.em_obs_precision = int(bool(cfg.em_obs_precision))
+    c.em_obs_precision_damping = float(cfg.em_obs_precision_damping)
+    c.em_obs_precision_min = float(cfg.em_obs_precision_min)
+    c.em_obs_precision_max = float(cfg.em_obs_precision_max)
+    c.best_iterate = int(bool(getattr(cfg, "best_iterate", False)))
+    return c
+
+
+def e8p12_vamp_solve(Wr, hat_init, V, S, Vs, cfg, *, prior_scale: Optional[torch.Tensor] = None,
+                     obs_init: float = 0.0, want_state: bool = False, ws: Optional[torch.Tensor] = None):
+    """One row block of the E8P12 VAMP loop (no polish).
+
+    Returns (idx int64 (rows, n/8), hat (rows, n), err (rows), r1|None, gamma1|None, stats dict)."""
+    dev = _dev(Wr, hat_init, V, S, Vs, prior_scale)
+    Wr = _f32c(Wr)
+    hat_init = _f32c(hat_init)
+    rows, n = Wr.shape
+    if n % 8:
+        raise ValueError(f"E8P12 solver expects n divisible by 8; got n={n}, codesz=8.")
+    if tuple(V.shape) != (n, n) or int(S.numel()) != n or tuple(Vs.shape) != (n, n):
+        raise ValueError("mpq_amd E8P12 VAMP needs full rank: V, Vs (n x n) and S (n)")
+    if prior_scale is not None:
+        prior_scale = _f32c(prior_scale).reshape(-1)
+        if int(prior_scale.numel()) != rows * (n // 8):
+            raise ValueError("prior_scale must hold one entry per 8-block")
+    lib = _lib.load()
+    need = int(lib.mpq_e8p12_vamp_workspace_size(rows, n))
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    idx = torch.empty(rows, n // 8, dtype=torch.int64, device=dev)
+    hat = torch.empty(rows, n, dtype=F32, device=dev)
+    err = torch.empty(rows, dtype=F32, device=dev)
+    r1 = torch.empty(rows, n, dtype=F32, device=dev) if want_state else None
+    g1 = torch.empty(rows, 1, dtype=F32, device=dev) if want_state else None
+    st = _lib.E8P12VampStatsC()
+    c = e8p12_vamp_config_c(cfg)
+    _lib.call("mpq_e8p12_vamp_solve", rows, n, _lib.ptr(Wr), _lib.ptr(hat_init), _lib.ptr(_f32c(V)),
+              _lib.ptr(_f32c(S)), _lib.ptr(_f32c(Vs)), _lib.ptr(prior_scale), ctypes.byref(c),
+              float(obs_init or 0.0), _lib.ptr(idx), _lib.ptr(hat), _lib.ptr(err), _lib.ptr(r1), _lib.ptr(g1),
+              ctypes.byref(st), _lib.ptr(ws), int(ws.numel()), _stream(dev))
+    stats = {name: getattr(st, name) for name, _ in st._fields_}
+    return idx, hat, err, r1, g1, stats

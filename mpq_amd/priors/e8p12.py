@@ -3,6 +3,7 @@
 Drop-in for ``mpq/priors/e8p12.py``:
 
 * ``vamp_vector_map_e8p12``  -> ``mpq_e8p12_map``  (reference ``:541-631``)
+* ``vamp_vector_discrete_mmse_e8p12`` -> ``mpq_e8p12_denoise`` (reference ``:815-968``)
 * ``e8p12_nearest``          -> ``mpq_e8p12_map`` with unit precision, no prior
   (the codebook's exact nearest-codeword quantizer)
 * ``prior_scale_from_center``  (reference ``:45-61``)
@@ -160,3 +161,63 @@ def vamp_vector_map_e8p12(
         "map_idxs": out["idx"].view(batch, n_blocks),
         "map_vals": out["vals"].view(batch, n_blocks, 8).to(dtype=r1_blocks.dtype),
     }
+
+
+@torch.inference_mode()
+def vamp_vector_discrete_mmse_e8p12(
+    *,
+    r1_blocks: torch.Tensor,  # (B, n_blocks, 8)
+    gamma1: torch.Tensor,  # (B, 1)
+    cb: object,
+    blocks_per_chunk: int = 16,
+    need_stats: bool = False,
+    prior_center_blocks: Optional[torch.Tensor] = None,
+    prior_scale_blocks: Optional[torch.Tensor] = None,
+    prior_tau: float = 0.0,
+    prior_tau_scale_mode: str = "absmax",
+    compile_prior: bool = True,
+) -> Dict[str, torch.Tensor | float]:
+    """Posterior mean/variance over the 2^16 codewords (reference ``mpq/priors/e8p12.py:815-968``).
+
+    Returns ``x1_blocks`` (B, n_blocks, 8), ``var1`` (B, n_blocks), ``alpha1`` (B, 1),
+    ``map_idxs`` (B, n_blocks) and ``map_vals`` (B, n_blocks, 8).  ``blocks_per_chunk`` and
+    ``compile_prior`` are accepted for signature compatibility (the kernel streams all
+    blocks in one launch); ``need_stats`` raises as in :func:`vamp_vector_map_e8p12`.
+    """
+    del blocks_per_chunk, cb, compile_prior
+    if need_stats:
+        raise ValueError("HIP E8P12 posterior backend does not support posterior diagnostics (need_stats=True).")
+    _require_device(r1_blocks, "r1_blocks")
+    batch, n_blocks, codesz = r1_blocks.shape
+    if int(codesz) != 8:
+        raise ValueError(f"E8P12 posterior expects codesz=8, got {codesz}.")
+    if gamma1.ndim != 2 or int(gamma1.shape[-1]) != 1 or int(gamma1.shape[0]) != int(batch):
+        raise ValueError(f"expected scalar gamma1 with shape (B,1), got {tuple(gamma1.shape)}")
+    dev = r1_blocks.device
+    r = r1_blocks.to(dtype=torch.float32).contiguous()
+    g = gamma1.to(device=dev, dtype=torch.float32).contiguous()
+    center = None
+    scale = None
+    tau = 0.0
+    if float(prior_tau) > 0.0 and prior_center_blocks is not None:
+        center = prior_center_blocks.to(device=dev, dtype=torch.float32).reshape(-1, 8).contiguous()
+        tau = float(prior_tau)
+        mode = str(prior_tau_scale_mode or "absmax").strip().lower()
+        if prior_scale_blocks is not None:
+            scale = prior_scale_blocks.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+        elif mode not in ("absmax", "exact_full", "exact_full_absmax"):
+            scale = prior_scale_from_center(prior_center_blocks, mode).reshape(-1).contiguous()
+    nblk = int(batch) * int(n_blocks)
+    x1 = torch.empty(batch, n_blocks, 8, dtype=torch.float32, device=dev)
+    var = torch.empty(batch, n_blocks, dtype=torch.float32, device=dev)
+    idx = torch.empty(batch, n_blocks, dtype=torch.int64, device=dev)
+    vals = torch.empty(batch, n_blocks, 8, dtype=torch.float32, device=dev)
+    alpha1 = torch.empty(batch, 1, dtype=torch.float32, device=dev)
+    if nblk:
+        _lib.call(
+            "mpq_e8p12_denoise",
+            _lib.ptr(r), int(batch), int(n_blocks), _lib.ptr(g), _lib.ptr(center), _lib.ptr(scale), float(tau),
+            _lib.ptr(x1), _lib.ptr(var), _lib.ptr(idx), _lib.ptr(vals), _lib.ptr(alpha1),
+            _lib.stream_handle(dev),
+        )
+    return {"x1_blocks": x1, "var1": var, "alpha1": alpha1, "map_idxs": idx, "map_vals": vals}

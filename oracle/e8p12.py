@@ -260,3 +260,157 @@ def posterior_bruteforce(r: np.ndarray, g: np.ndarray, grid: np.ndarray):
         var[i] = ((p * gn).sum() - means[i] @ means[i]) / 8.0
         logz[i] = m + math.log(Z)
     return means, var, logz
+
+
+# ---------------------------------------------------------------------------
+# E8P12 VAMP loop and gram-metric block CD (torch CPU, reference op order)
+# ---------------------------------------------------------------------------
+
+def stabilize_cholesky(gram: torch.Tensor, jitter: float = 1e-6, max_tries: int = 6) -> torch.Tensor:
+    """mpq/linear.py:121-141."""
+    floor = float(torch.diag(gram).abs().max().item()) * jitter + jitter
+    eye = torch.eye(gram.shape[0], dtype=gram.dtype)
+    out = gram
+    for k in range(max_tries):
+        try:
+            return torch.linalg.cholesky(out)
+        except RuntimeError:
+            out = out + (2.0 ** k) * floor * eye
+    return torch.linalg.cholesky(out)
+
+
+def gram_block_cd(x, idxs, Y_u, Vs, grid, sweeps, accept_tol=0.0):
+    """mpq/polish/block_cd.py:332-625 with E8P12Provider, metric "gram", greedy_gain order and the
+    compiled step _cd_gram_step_impl (:212-246): whitened brute-force argmin over all codewords."""
+    B, n = x.shape
+    nb = n // 8
+    x = x.to(torch.float32).clone()
+    idxs = idxs.clone()
+    Vs_t = Vs.T.contiguous()
+    res_u = Y_u - x.matmul(Vs)
+    res = res_u.square().sum(dim=1)
+    meta = []
+    for b in range(nb):
+        Vb = Vs[8 * b:8 * b + 8]
+        G = Vb.matmul(Vb.T).contiguous()
+        L = stabilize_cholesky(G)
+        Gi = torch.cholesky_inverse(L).contiguous()
+        meta.append((Vb.T.contiguous(), Vb.contiguous(), G, L, Gi))
+    gi_stack = torch.stack([m[4] for m in meta], 0)
+    accepted = 0
+    for _ in range(sweeps):
+        rhs_all = res_u.matmul(Vs_t).reshape(B, nb, 8).permute(1, 0, 2).contiguous()
+        gain = (rhs_all * torch.bmm(rhs_all, gi_stack)).sum(dim=2).mean(dim=1)
+        order = torch.argsort(gain, descending=True, stable=True).tolist()
+        for b in order:
+            Vbt, Vb, G, L, Gi = meta[b]
+            xb = x[:, 8 * b:8 * b + 8]
+            rhs = res_u.matmul(Vbt)
+            target = xb + rhs.matmul(Gi)
+            tm = target.matmul(L)
+            mg = grid.matmul(L)
+            scores = tm.square().sum(dim=1, keepdim=True) + mg.square().sum(dim=-1).unsqueeze(0) - 2.0 * tm.matmul(mg.T)
+            best = torch.argmin(scores, dim=1)
+            cand = grid.index_select(0, best)
+            delta = cand - xb
+            cross = (rhs * delta).sum(dim=1)
+            dn = (delta.matmul(G) * delta).sum(dim=1).clamp_min_(0.0)
+            ce = (res + dn - 2.0 * cross).clamp_min_(0.0)
+            acc = ce + 1e-12 < res * (1.0 + accept_tol)
+            m = acc.unsqueeze(1)
+            x[:, 8 * b:8 * b + 8] = torch.where(m, cand, xb)
+            res_u.sub_((delta * m).matmul(Vb))
+            res = torch.where(acc, ce, res)
+            idxs[:, b] = torch.where(acc, best.to(idxs.dtype), idxs[:, b])
+            accepted += int(acc.sum())
+    return x, idxs, accepted
+
+
+def solve_e8p12_rankspace_vamp(Wr, hat_init, V, S, grid, cache, cfg, obs_precision_init=None):
+    """mpq/solver.py:853-1276 (best_iterate off, the recipe default); returns (hat, idx, err, stats)."""
+    from oracle import uniform as ou
+
+    iters = int(cfg.get("iters", 16))
+    damping = float(cfg.get("damping", 0.5))
+    tau = float(cfg.get("prior_tau", 0.25))
+    retry_factor = max(float(cfg.get("gamma_retry_factor", 4.0)), 1.000001)
+    retry_steps = max(int(cfg.get("gamma_retry_steps", 3)), 0)
+    sweeps = int(cfg.get("polish_sweeps", 3))
+    B, n = Wr.shape
+    nb = n // 8
+    R = S.numel()
+    Vs = V * S.unsqueeze(0)
+    Vh = V.T.contiguous()
+    Wb = Wr.reshape(B, nb, 8)
+    pscale = Wb.abs().amax(dim=-1, keepdim=True).clamp_min(1e-12) if tau > 0 else None
+    Y_u = Wr.matmul(Vs)
+    if obs_precision_init is not None and obs_precision_init > 0:
+        obs = float(obs_precision_init)
+    else:
+        obs = 1.0 / float((Y_u - hat_init.matmul(Vs)).square().mean().clamp_min_(1e-12).item())
+    r1 = hat_init.clone()
+    gamma1 = float(cfg.get("gamma_start", 1.0)) * (0.25 / (Wr - hat_init).square().mean(dim=1, keepdim=True).clamp_min_(1e-12))
+    r2_prev = g2_prev = None
+    stats = {"gamma2_invalid": 0, "obs": []}
+    for it in range(iters):
+        g1w = gamma1
+        for attempt in range(retry_steps + 1):
+            post = posterior(r1.reshape(B, nb, 8), g1w, cache, prior_center_blocks=Wb if tau > 0 else None,
+                             prior_scale_blocks=pscale, prior_tau=tau)
+            a1 = post["alpha1"]
+            if bool(ou.alpha_valid(a1).all()):
+                break
+            if attempt >= retry_steps:
+                if not bool(torch.isfinite(a1).all()):
+                    raise RuntimeError("alpha1 invalid")
+                a1 = torch.nan_to_num(a1, nan=0.5, posinf=1.0 - ou.ALPHA_EPS, neginf=ou.ALPHA_EPS).clamp(
+                    min=ou.ALPHA_EPS, max=1.0 - ou.ALPHA_EPS)
+                break
+            g1w = torch.where(a1 <= ou.ALPHA_EPS, g1w / retry_factor, g1w)
+            g1w = torch.where(a1 >= 1.0 - ou.ALPHA_EPS, g1w * retry_factor, g1w).clamp_min_(1e-12)
+        x1 = post["x1_blocks"].reshape(B, n)
+        eta1 = g1w / a1
+        g2n = torch.nan_to_num(eta1 - g1w, nan=1e-12, posinf=1e12, neginf=1e-12).clamp_min_(1e-12)
+        if not bool(ou.prec_valid(g2n).all()):
+            stats["gamma2_invalid"] += 1
+            continue
+        r2n = (eta1 * x1 - g1w * r1) / g2n
+        if r2_prev is None or damping >= 1.0:
+            g2, r2 = g2n, r2n
+        else:
+            g2 = ou.log_damp(g2_prev, g2n, damping)
+            r2 = (1.0 - damping) * r2_prev + damping * r2n
+        if not bool(ou.prec_valid(g2).all()):
+            stats["gamma2_invalid"] += 1
+            continue
+        x2, a2, res_u = ou.linear_mmse_exact(r2, g2, Y_u, V, Vh, S, obs)
+        a2 = torch.nan_to_num(a2, nan=0.5, posinf=1.0 - ou.ALPHA_EPS, neginf=ou.ALPHA_EPS).clamp(
+            min=ou.ALPHA_EPS, max=1.0 - ou.ALPHA_EPS)
+        if bool(cfg.get("em_obs_precision", True)) and float(cfg.get("obs_precision", 0.0)) <= 0.0:
+            obs = ou.em_update_obs_precision(res_u, g2, S, obs, R)
+        eta2 = g2 / a2
+        g1n = torch.nan_to_num(eta2 - g2, nan=1e-12, posinf=1e12, neginf=1e-12).clamp_min_(1e-12)
+        r1n = (eta2 * x2 - g2 * r2) / g1n
+        if damping >= 1.0:
+            gamma1, r1 = g1n, r1n
+        else:
+            gamma1 = ou.log_damp(gamma1, g1n, damping)
+            r1 = (1.0 - damping) * r1 + damping * r1n
+        r2_prev, g2_prev = r2, g2
+        stats["obs"].append(obs)
+    center = Wb.reshape(-1, 8).numpy() if tau > 0 else None
+    scl = pscale.reshape(-1).numpy() if pscale is not None else None
+    idx, _ = map_search(r1.reshape(-1, 8).numpy(), gamma1.reshape(-1).numpy(), nb, cache, center=center,
+                        scale=scl, tau=tau)
+    idx_t = torch.from_numpy(idx).view(B, nb)
+    hat = grid.index_select(0, idx_t.reshape(-1)).view(B, n)
+    stats["idx_vamp"] = idx_t.clone()
+    stats["err_vamp"] = ou.rankspace_error(Y_u, hat, Vs)
+    if sweeps > 0:
+        hat, idx_t, acc = gram_block_cd(hat, idx_t, Y_u, Vs, grid, sweeps)
+        stats["polish_accepted"] = acc
+    err = ou.rankspace_error(Y_u, hat, Vs)
+    stats["obs_final"] = obs
+    stats["r1"] = r1
+    stats["gamma1"] = gamma1
+    return hat, idx_t, err, stats

@@ -1,0 +1,157 @@
+"""GPU parity of the E8P12 posterior denoiser and the E8P12 VAMP loop against the CPU oracle
+(oracle/e8p12.py) and the reference's golden vectors (tests/golden/e8p12_*.npz)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from mpq_amd import codebook, ops
+from mpq_amd.priors.e8p12 import vamp_vector_discrete_mmse_e8p12
+from oracle import e8p12 as oe8
+from oracle import uniform as ou
+from tests.uniform_cases import make_layer
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+# posterior means: north-star tolerance 1e-4 relative (per block, against the block's norm)
+POST_RTOL = 1e-4
+
+
+def _load(name):
+    d = np.load(os.path.join(GOLD, name + ".npz"))
+    return {k: torch.from_numpy(d[k]) if d[k].ndim else d[k].item() for k in d.files}
+
+
+def _grid_cache():
+    grid = torch.from_numpy(codebook.grid_numpy())
+    return grid, oe8.factor_cache(grid)
+
+
+class _Cfg:
+    iters = 16
+    damping = 0.5
+    gamma_start = 1.0
+    gamma_retry_factor = 4.0
+    gamma_retry_steps = 3
+    prior_tau = 0.25
+    obs_precision = 0.0
+    em_obs_precision = True
+    em_obs_precision_damping = 0.3
+    em_obs_precision_min = 1e-4
+    em_obs_precision_max = 1e8
+    best_iterate = False
+
+
+def _check_post(got, ref_x1, ref_var, ref_alpha, ref_idx):
+    x1 = got["x1_blocks"].cpu()
+    err = (x1 - ref_x1).norm(dim=-1)
+    scale = ref_x1.norm(dim=-1).clamp_min(1e-3)
+    assert float((err / scale).max()) <= POST_RTOL, float((err / scale).max())
+    assert torch.equal(got["map_idxs"].cpu(), ref_idx)
+    # var = (E|c|^2 - |mu|^2) / 8 cancels in fp32, so its error scales with E|c|^2 / 8.  The kernel
+    # accumulates the 512 mixture components sequentially (the oracle sums each branch pairwise):
+    # measured worst 66 ulps of E|c|^2/8 against the oracle, whose own worst against an fp64 brute
+    # force is 18 ulps.  Bound: 256 ulps (3e-5 relative to E|c|^2/8).
+    v = got["var1"].cpu()
+    second = ref_x1.square().sum(-1) / 8 + ref_var
+    bound = 2e-4 * ref_var + 256 * 2.0 ** -23 * second
+    worst = float(((v - ref_var).abs() / bound).max())
+    assert worst <= 1.0, worst
+    assert torch.allclose(got["alpha1"].cpu(), ref_alpha, rtol=2e-4)
+
+
+def test_posterior_matches_reference_golden(gpu):
+    g = _load("e8p12_posterior")
+    got = vamp_vector_discrete_mmse_e8p12(r1_blocks=g["r1"].to(gpu), gamma1=g["gamma1"].to(gpu), cb=None,
+                                          prior_center_blocks=g["center"].to(gpu), prior_tau=0.25)
+    _check_post(got, g["x1"], g["var1"], g["alpha1"], g["map_idxs"])
+
+
+@pytest.mark.parametrize("prior", [False, True])
+def test_posterior_matches_oracle(gpu, prior):
+    gen = torch.Generator().manual_seed(11 + int(prior))
+    rows, nb = 48, 96
+    r1 = torch.randn(rows, nb, 8, generator=gen) * 0.8
+    center = r1 + 0.3 * torch.randn(rows, nb, 8, generator=gen) if prior else None
+    # spread of precisions, including the snap regime (>= 1e3) and a very flat posterior
+    gam = torch.exp(torch.randn(rows, 1, generator=gen) * 1.5) * 2.0
+    gam[0, 0] = 2e3
+    gam[1, 0] = 0.05
+    _, cache = _grid_cache()
+    ref = oe8.posterior(r1, gam, cache, prior_center_blocks=center, prior_tau=0.25 if prior else 0.0)
+    got = vamp_vector_discrete_mmse_e8p12(r1_blocks=r1.to(gpu), gamma1=gam.to(gpu), cb=None,
+                                          prior_center_blocks=None if center is None else center.to(gpu),
+                                          prior_tau=0.25 if prior else 0.0)
+    _check_post(got, ref["x1_blocks"], ref["var1"], ref["alpha1"], ref["map_idxs"])
+
+
+def _e8_case(rows, n, seed_key):
+    W, H = make_layer(rows, n, tokens=1024, seed_key=seed_key, heavy=True)
+    Wr = W / W.square().mean().sqrt()
+    lam, V, _ = ou.hessian_eigen(H)
+    S = torch.sqrt(lam)
+    grid = torch.from_numpy(codebook.grid_numpy())
+    idx0, _ = oe8.bruteforce_nearest(Wr.reshape(-1, 8).numpy(), grid.numpy())
+    hat0 = grid[torch.from_numpy(np.asarray(idx0))].view(rows, n)
+    return Wr, V, S, hat0
+
+
+def _gpu_vamp(Wr, hat0, V, S, cfg, dev):
+    Vs = V * S.unsqueeze(0)
+    return ops.e8p12_vamp_solve(Wr.to(dev), hat0.to(dev), V.to(dev), S.to(dev), Vs.to(dev), cfg, want_state=True)
+
+
+def test_vamp_matches_reference_golden(gpu):
+    g = _load("e8p12_vamp")
+    idx, hat, err, r1, g1, st = _gpu_vamp(g["Wr"], g["hat0"], g["V"], g["S"], _Cfg, gpu)
+    agree = float((idx.cpu() == g["idx_vamp"]).float().mean())
+    # 512 codes: at most one flip of a near-tie
+    assert agree >= 511 / 512, agree
+    assert abs(st["obs_precision_initial"] - g["obs_initial"]) <= 1e-5 * g["obs_initial"]
+    assert abs(st["obs_precision_final"] - g["obs_final"]) <= 1e-3 * g["obs_final"]
+    assert torch.allclose(err.cpu(), g["err_vamp"], rtol=5e-3)
+    grid = torch.from_numpy(codebook.grid_numpy())
+    assert torch.equal(hat.cpu(), grid[idx.cpu().reshape(-1)].view_as(hat.cpu()))
+
+
+def test_vamp_matches_oracle(gpu):
+    Wr, V, S, hat0 = _e8_case(64, 512, "e8vamp:gpu")
+    grid, cache = _grid_cache()
+    cfg = dict(iters=16, damping=0.5, prior_tau=0.25, polish_sweeps=0)
+    ref_hat, ref_idx, ref_err, ref_st = oe8.solve_e8p12_rankspace_vamp(Wr, hat0, V, S, grid, cache, cfg)
+    idx, hat, err, r1, g1, st = _gpu_vamp(Wr, hat0, V, S, _Cfg, gpu)
+    agree = float((idx.cpu() == ref_idx).float().mean())
+    assert agree >= 0.999, agree
+    assert abs(st["obs_precision_final"] - ref_st["obs_final"]) <= 2e-3 * ref_st["obs_final"]
+    assert abs(float(err.mean()) - float(ref_err.mean())) <= 2e-3 * float(ref_err.mean())
+    # the VAMP state (r1, gamma1) tracks the oracle's
+    r1_rel = float((r1.cpu() - ref_st["r1"]).norm() / ref_st["r1"].norm())
+    assert r1_rel <= 1e-3, r1_rel
+    assert torch.allclose(g1.cpu(), ref_st["gamma1"], rtol=1e-2)
+
+
+def test_vamp_best_iterate_never_worse_than_its_start(gpu):
+    """best_iterate keeps the iterate whose MAP decision has the lowest rank-space error, starting from the
+    MAP of the initial state (mpq/solver.py:940-958, 1083-1121)."""
+    Wr, V, S, hat0 = _e8_case(40, 256, "e8vamp:best")
+    rows, n = Wr.shape
+    _, cache = _grid_cache()
+    grid = torch.from_numpy(codebook.grid_numpy())
+    Vs = V * S.unsqueeze(0)
+    g1 = 0.25 / (Wr - hat0).square().mean(dim=1, keepdim=True).clamp_min(1e-12)
+    idx0, _ = oe8.map_search(hat0.reshape(-1, 8).numpy(), g1.reshape(-1).numpy(), n // 8, cache,
+                             center=Wr.reshape(-1, 8).numpy(), tau=0.25)
+    x0 = grid[torch.from_numpy(idx0)].view(rows, n)
+    e_start = float(ou.rankspace_error(Wr.matmul(Vs), x0, Vs).mean())
+
+    class Cfg(_Cfg):
+        best_iterate = True
+
+    idx, hat, err, r1, g1o, st = _gpu_vamp(Wr, hat0, V, S, Cfg, gpu)
+    assert float(err.mean()) <= e_start * (1 + 1e-4)
+    assert 1 <= st["iters"] <= 16
+    if st["stop_iter"] >= 0:
+        assert st["iters"] == st["stop_iter"] + 1
+        assert st["best_iter"] < st["stop_iter"]

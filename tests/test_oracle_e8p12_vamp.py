@@ -1,0 +1,57 @@
+"""CPU: pin the E8P12 posterior, VAMP loop and gram-metric CD of the oracle against the reference."""
+import os
+
+import numpy as np
+import torch
+
+from mpq_amd import codebook
+from oracle import e8p12 as oe8
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _load(name):
+    d = np.load(os.path.join(GOLD, name + ".npz"))
+    return {k: torch.from_numpy(d[k]) if d[k].ndim else d[k].item() for k in d.files}
+
+
+def test_posterior_matches_reference_golden_and_bruteforce():
+    g = _load("e8p12_posterior")
+    grid = codebook.grid_numpy()
+    cache = oe8.factor_cache(torch.from_numpy(grid))
+    post = oe8.posterior(g["r1"], g["gamma1"], cache, prior_center_blocks=g["center"], prior_tau=0.25)
+    assert torch.equal(post["map_idxs"], g["map_idxs"])
+    assert torch.allclose(post["x1_blocks"], g["x1"], rtol=1e-5, atol=1e-6)
+    assert torch.allclose(post["var1"], g["var1"], rtol=1e-4, atol=1e-7)
+    assert torch.allclose(post["alpha1"], g["alpha1"], rtol=1e-5)
+    assert torch.allclose(post["logZ"], g["logZ"], rtol=1e-5, atol=1e-4)
+    # brute force over all 65536 codewords (prior folded into r, gamma)
+    r, c = g["r1"].reshape(-1, 8), g["center"].reshape(-1, 8)
+    gam = g["gamma1"].repeat_interleave(g["r1"].shape[1], 0).reshape(-1)
+    s = c.abs().amax(-1).clamp_min(1e-12)
+    pp = 1.0 / (0.25 * s) ** 2
+    gw = gam + pp
+    rw = (gam[:, None] * r + pp[:, None] * c) / gw[:, None]
+    sel = slice(0, 64)
+    m, v, _ = oe8.posterior_bruteforce(rw[sel].numpy(), gw[sel].numpy(), grid)
+    hi = gw[sel] >= 1e3
+    got = post["x1_blocks"].reshape(-1, 8)[sel]
+    assert np.allclose(got[~hi].numpy(), m[~hi.numpy()], rtol=1e-4, atol=1e-5)
+    assert np.allclose(post["var1"].reshape(-1)[sel][~hi].numpy(), v[~hi.numpy()], rtol=1e-3, atol=1e-6)
+
+
+def test_e8p12_vamp_loop_matches_reference_golden():
+    g = _load("e8p12_vamp")
+    torch.set_num_threads(1)
+    grid = torch.from_numpy(codebook.grid_numpy())
+    cache = oe8.factor_cache(grid)
+    cfg = dict(iters=16, damping=0.5, prior_tau=0.25, polish_sweeps=0)
+    hat, idx, err, st = oe8.solve_e8p12_rankspace_vamp(g["Wr"], g["hat0"], g["V"], g["S"], grid, cache, cfg)
+    agree = float((idx == g["idx_vamp"]).float().mean())
+    assert agree >= 0.999, agree
+    assert abs(st["obs_final"] - g["obs_final"]) <= 1e-3 * g["obs_final"]
+    hat, idx, err, st = oe8.solve_e8p12_rankspace_vamp(g["Wr"], g["hat0"], g["V"], g["S"], grid, cache,
+                                                       dict(cfg, polish_sweeps=3))
+    agree = float((idx == g["idx_final"]).float().mean())
+    assert agree >= 0.999, agree
+    assert torch.allclose(err, g["err_final"], rtol=1e-3)
