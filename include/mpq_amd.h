@@ -128,6 +128,42 @@ int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, const float* 
                          MpqE8P12VampStats* stats, void* workspace, int64_t workspace_bytes,
                          mpq_stream_t stream);
 
+/*
+ * Per-layer context of the E8P12 gram-metric polish: H = Vs Vs^T, per 8-column
+ * block the gram G_j, its stabilized Cholesky factor L_j and (L_j L_j^T)^-1
+ * (mpq/polish/block_cd.py:385-397, stabilize_cholesky mpq/linear.py:121-141),
+ * the codebook grid and the tables |L_j^T c|^2 over all 65536 codewords
+ * (mpq/polish/block_cd.py:228-230).  ctx: caller-allocated device memory of
+ * mpq_e8p12_cd_context_size(n) bytes.  Returns MPQ_NUMERICAL_ERROR when a
+ * Cholesky still fails after the 6 jitter retries (torch raises there).
+ * Synchronises `stream` once.
+ */
+int64_t mpq_e8p12_cd_context_size(int64_t n);
+int mpq_e8p12_cd_prepare(int64_t n, const float* Vs, void* ctx, int64_t ctx_bytes, mpq_stream_t stream);
+
+/* Workspace bytes needed by mpq_e8p12_cd_polish. */
+int64_t mpq_e8p12_cd_workspace_size(int64_t rows, int64_t n, int64_t block_rows);
+
+/*
+ * Gram-metric block coordinate descent over E8P12 codewords, every row block
+ * of block_rows rows with its own greedy order: replaces mpq/solver.py:369-423
+ * (polish_e8p12_rankspace, "block_cd", metric "gram") ->
+ * mpq/polish/block_cd.py:332-625 with the step _cd_gram_step_impl (:212-246)
+ * and the gains of _batched_greedy_gain (:286-306).
+ *   targets: W (rows x n; Yu = W Vs is formed) or Yu (rows x n, W = NULL)
+ *   x_in rows x n codeword values, idx_in rows x n/8 int64 codeword indices
+ *   Vs n x n, ctx from mpq_e8p12_cd_prepare(n, Vs)
+ *   max_blocks > 0 visits only the first max_blocks blocks of each greedy order
+ *   outputs x_out, idx_out; err_before/err_after (rows, |Yu - x Vs|^2) and
+ *   accepted_per_row (rows int32) may be NULL.  n/8 <= 16384.
+ */
+int mpq_e8p12_cd_polish(int64_t rows, int64_t n, int64_t block_rows, int sweeps, int64_t max_blocks,
+                        float accept_tol, const float* W, const float* Yu, const float* x_in,
+                        const int64_t* idx_in, const float* Vs, const void* ctx, float* x_out,
+                        int64_t* idx_out, float* err_before, float* err_after,
+                        int32_t* accepted_per_row, void* workspace, int64_t workspace_bytes,
+                        mpq_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Dense algebra                                                            */
 /* ------------------------------------------------------------------------ */

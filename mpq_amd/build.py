@@ -34,6 +34,7 @@ HIP_SOURCES = [
     "uniform_vamp.hip",
     "e8p12_vamp.hip",
     "cd_uniform.hip",
+    "e8p12_cd.hip",
 ]
 CXX_SOURCES = [
     "errors.cpp",

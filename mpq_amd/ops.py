@@ -308,3 +308,49 @@ def e8p12_vamp_solve(Wr, hat_init, V, S, Vs, cfg, *, prior_scale: Optional[torch
               ctypes.byref(st), _lib.ptr(ws), int(ws.numel()), _stream(dev))
     stats = {name: getattr(st, name) for name, _ in st._fields_}
     return idx, hat, err, r1, g1, stats
+
+
+# ---- E8P12 gram-metric polish ----------------------------------------------------
+
+def e8p12_cd_prepare(Vs: torch.Tensor) -> torch.Tensor:
+    """Per-layer context (H, per-block G/L/Gi, grid, |L^T c|^2 tables) as an opaque uint8 tensor."""
+    dev = _dev(Vs)
+    Vs = _f32c(Vs)
+    n = int(Vs.shape[0])
+    if tuple(Vs.shape) != (n, n) or n % 8:
+        raise ValueError("E8P12 polish needs a square Vs with n divisible by 8")
+    lib = _lib.load()
+    ctx = workspace(int(lib.mpq_e8p12_cd_context_size(n)), dev)
+    _lib.call("mpq_e8p12_cd_prepare", n, _lib.ptr(Vs), _lib.ptr(ctx), int(ctx.numel()), _stream(dev))
+    return ctx
+
+
+def e8p12_cd_polish(x_in, idx_in, Vs, ctx, *, sweeps: int, block_rows: int, W=None, Yu=None,
+                    max_blocks: int = 0, accept_tol: float = 0.0, ws: Optional[torch.Tensor] = None):
+    """Gram-metric E8P12 block CD over all rows (greedy order per row block).
+
+    Returns (x, idx, err_before, err_after, accepted_per_row)."""
+    dev = _dev(x_in, idx_in, Vs, ctx, W, Yu)
+    if (W is None) == (Yu is None):
+        raise ValueError("give exactly one of W or Yu")
+    x_in = _f32c(x_in)
+    rows, n = x_in.shape
+    idx_in = idx_in.to(dtype=torch.int64).contiguous()
+    if tuple(idx_in.shape) != (rows, n // 8):
+        raise ValueError("idx_in must be (rows, n/8)")
+    W = None if W is None else _f32c(W)
+    Yu = None if Yu is None else _f32c(Yu)
+    lib = _lib.load()
+    need = int(lib.mpq_e8p12_cd_workspace_size(rows, n, int(block_rows)))
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    x = torch.empty_like(x_in)
+    idx = torch.empty_like(idx_in)
+    eb = torch.empty(rows, dtype=F32, device=dev)
+    ea = torch.empty(rows, dtype=F32, device=dev)
+    acc = torch.empty(rows, dtype=torch.int32, device=dev)
+    _lib.call("mpq_e8p12_cd_polish", rows, n, int(block_rows), int(sweeps), int(max_blocks), float(accept_tol),
+              _lib.ptr(W), _lib.ptr(Yu), _lib.ptr(x_in), _lib.ptr(idx_in), _lib.ptr(_f32c(Vs)), _lib.ptr(ctx),
+              _lib.ptr(x), _lib.ptr(idx), _lib.ptr(eb), _lib.ptr(ea), _lib.ptr(acc), _lib.ptr(ws),
+              int(ws.numel()), _stream(dev))
+    return x, idx, eb, ea, acc

@@ -279,7 +279,7 @@ def stabilize_cholesky(gram: torch.Tensor, jitter: float = 1e-6, max_tries: int 
     return torch.linalg.cholesky(out)
 
 
-def gram_block_cd(x, idxs, Y_u, Vs, grid, sweeps, accept_tol=0.0):
+def gram_block_cd(x, idxs, Y_u, Vs, grid, sweeps, accept_tol=0.0, max_blocks=0):
     """mpq/polish/block_cd.py:332-625 with E8P12Provider, metric "gram", greedy_gain order and the
     compiled step _cd_gram_step_impl (:212-246): whitened brute-force argmin over all codewords."""
     B, n = x.shape
@@ -302,6 +302,8 @@ def gram_block_cd(x, idxs, Y_u, Vs, grid, sweeps, accept_tol=0.0):
         rhs_all = res_u.matmul(Vs_t).reshape(B, nb, 8).permute(1, 0, 2).contiguous()
         gain = (rhs_all * torch.bmm(rhs_all, gi_stack)).sum(dim=2).mean(dim=1)
         order = torch.argsort(gain, descending=True, stable=True).tolist()
+        if max_blocks > 0:
+            order = order[:max_blocks]  # mpq/polish/block_cd.py:510-511
         for b in order:
             Vbt, Vb, G, L, Gi = meta[b]
             xb = x[:, 8 * b:8 * b + 8]

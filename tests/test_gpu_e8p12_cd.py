@@ -1,0 +1,111 @@
+"""GPU parity of the E8P12 gram-metric block-CD polish against the CPU oracle (oracle/e8p12.py
+gram_block_cd, which follows mpq/polish/block_cd.py:212-246 and :332-625)."""
+import numpy as np
+import pytest
+import torch
+
+from mpq_amd import codebook, ops
+from oracle import e8p12 as oe8
+from oracle import uniform as ou
+from tests.uniform_cases import make_layer
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(rows, n, seed_key, jitter=0.0):
+    W, H = make_layer(rows, n, tokens=1024, seed_key=seed_key, heavy=True)
+    Wr = W / W.square().mean().sqrt()
+    lam, V, _ = ou.hessian_eigen(H)
+    Vs = V * torch.sqrt(lam).unsqueeze(0)
+    grid = torch.from_numpy(codebook.grid_numpy())
+    # start from the nearest codeword of a perturbed target so that the polish has work to do
+    gen = torch.Generator().manual_seed(rows + n)
+    start = Wr + jitter * torch.randn(Wr.shape, generator=gen)
+    idx0, _ = oe8.bruteforce_nearest(start.reshape(-1, 8).numpy(), grid.numpy())
+    idx0 = torch.from_numpy(np.asarray(idx0)).view(rows, n // 8)
+    x0 = grid[idx0.reshape(-1)].view(rows, n)
+    return Wr, Vs, x0, idx0, grid
+
+
+def _oracle_blocks(Wr, Vs, x0, idx0, grid, block_rows, sweeps, max_blocks=0):
+    Yu = Wr.matmul(Vs)
+    xs, ids = [], []
+    for r0 in range(0, Wr.shape[0], block_rows):
+        sl = slice(r0, r0 + block_rows)
+        x, idx, _ = oe8.gram_block_cd(x0[sl], idx0[sl], Yu[sl], Vs, grid, sweeps, max_blocks=max_blocks)
+        xs.append(x)
+        ids.append(idx)
+    x = torch.cat(xs)
+    return x, torch.cat(ids), ou.rankspace_error(Yu, x, Vs)
+
+
+@pytest.mark.parametrize("rows,n,block_rows,max_blocks", [(64, 256, 64, 0), (200, 128, 64, 0),
+                                                           (256, 256, 128, 0), (96, 512, 96, 7)])
+def test_polish_matches_oracle(gpu, rows, n, block_rows, max_blocks):
+    Wr, Vs, x0, idx0, grid = _case(rows, n, f"e8cd:{rows}:{n}", jitter=0.15)
+    ref_x, ref_idx, ref_err = _oracle_blocks(Wr, Vs, x0, idx0, grid, block_rows, 3, max_blocks)
+    ctx = ops.e8p12_cd_prepare(Vs.to(gpu))
+    x, idx, eb, ea, acc = ops.e8p12_cd_polish(x0.to(gpu), idx0.to(gpu), Vs.to(gpu), ctx, sweeps=3,
+                                              block_rows=block_rows, W=Wr.to(gpu), max_blocks=max_blocks)
+    x, idx, eb, ea = x.cpu(), idx.cpu(), eb.cpu(), ea.cpu()
+    # state consistency: values are the codewords of the indices
+    assert torch.equal(x, grid[idx.reshape(-1)].view_as(x))
+    Yu = Wr.matmul(Vs)
+    e0 = ou.rankspace_error(Yu, x0, Vs)
+    assert torch.allclose(eb, e0, rtol=1e-4)
+    assert torch.allclose(ea, ou.rankspace_error(Yu, x, Vs), rtol=1e-4)
+    # the polish only accepts decreasing moves
+    assert bool((ea <= eb * (1 + 1e-5)).all())
+    agree = float((idx == ref_idx).float().mean())
+    assert agree >= 0.99, agree
+    rel = abs(float(ea.mean()) - float(ref_err.mean())) / float(ref_err.mean())
+    assert rel <= 5e-3, rel
+    assert int(acc.sum()) > 0
+
+
+def test_polish_zero_sweeps_is_identity_and_yu_path(gpu):
+    Wr, Vs, x0, idx0, grid = _case(48, 128, "e8cd:id", jitter=0.1)
+    ctx = ops.e8p12_cd_prepare(Vs.to(gpu))
+    x, idx, eb, ea, acc = ops.e8p12_cd_polish(x0.to(gpu), idx0.to(gpu), Vs.to(gpu), ctx, sweeps=0, block_rows=48,
+                                              W=Wr.to(gpu))
+    assert torch.equal(x.cpu(), x0) and torch.equal(idx.cpu(), idx0)
+    assert torch.equal(eb.cpu(), ea.cpu())
+    # Yu given instead of W: identical results
+    Yu = ops.gemm(Wr.to(gpu), Vs.to(gpu))
+    a = ops.e8p12_cd_polish(x0.to(gpu), idx0.to(gpu), Vs.to(gpu), ctx, sweeps=2, block_rows=48, W=Wr.to(gpu))
+    b = ops.e8p12_cd_polish(x0.to(gpu), idx0.to(gpu), Vs.to(gpu), ctx, sweeps=2, block_rows=48, Yu=Yu)
+    assert torch.equal(a[1].cpu(), b[1].cpu())
+
+
+def test_first_step_is_exact_whitened_argmin(gpu):
+    """One step (max_blocks=1, one sweep): each row's candidate is the fp64 argmin of
+    |L^T (target - c)|^2 over all codewords, up to fp32 near-ties."""
+    Wr, Vs, x0, idx0, grid = _case(64, 64, "e8cd:argmin", jitter=0.3)
+    rows, n = Wr.shape
+    Yu = Wr.matmul(Vs)
+    ctx = ops.e8p12_cd_prepare(Vs.to(gpu))
+    x, idx, eb, ea, acc = ops.e8p12_cd_polish(x0.to(gpu), idx0.to(gpu), Vs.to(gpu), ctx, sweeps=1, block_rows=rows,
+                                              W=Wr.to(gpu), max_blocks=1)
+    x = x.cpu()
+    changed = (x != x0).any(dim=1)
+    blk = int(((x != x0).reshape(rows, n // 8, 8).any(-1).any(0)).nonzero().flatten()[0]) if bool(changed.any()) else None
+    assert blk is not None
+    # recompute the step in fp64
+    R = (Yu - x0.matmul(Vs)).double()
+    Vb = Vs[8 * blk:8 * blk + 8].double()
+    G = Vb @ Vb.T
+    L = torch.linalg.cholesky(G)
+    Gi = torch.cholesky_inverse(L)
+    rhs = R @ Vb.T
+    target = x0[:, 8 * blk:8 * blk + 8].double() + rhs @ Gi
+    g64 = grid.double()
+    d = ((target @ L).unsqueeze(1) - (g64 @ L).unsqueeze(0)).square().sum(-1)  # rows x 65536
+    best = d.argmin(dim=1)
+    dmin = d.min(dim=1).values
+    got = idx.cpu()[:, blk]
+    for r in range(rows):
+        if not bool(changed[r]):
+            continue
+        gi = int(got[r])
+        # the chosen codeword is the fp64 argmin, or within fp32 rounding of it
+        assert gi == int(best[r]) or float(d[r, gi] - dmin[r]) <= 1e-5 * float(dmin[r] + (target[r] @ L).square().sum())
