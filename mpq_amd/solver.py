@@ -4,6 +4,10 @@
 * ``solve_uniform_rankspace_vamp``   reference :426-830 -> ``mpq_uniform_vamp_solve`` +
                                      ``mpq_uniform_cd_polish``
 * ``polish_uniform_rankspace``       reference :260-366 -> ``mpq_uniform_cd_polish``
+* ``E8P12VampConfig``                reference :59-82
+* ``solve_e8p12_rankspace_vamp``     reference :853-1276 -> ``mpq_e8p12_vamp_solve`` +
+                                     ``mpq_e8p12_cd_polish``
+* ``polish_e8p12_rankspace``         reference :369-423 -> ``mpq_e8p12_cd_polish``
 
 All tensors live on the ROCm device.  The rank R must equal n (the adapters
 always floor the eigenvalues, so this holds on the reference's own path).
@@ -16,6 +20,7 @@ from typing import Any, Dict, Optional, Tuple
 import torch
 
 from . import ops
+from .priors.e8p12 import prior_scale_from_center
 from .priors.uniform import dequant_from_q, nearest_atom_idx
 
 
@@ -40,6 +45,43 @@ class UniformVampConfig:
     vamp_backend: str = "auto"  # accepted for compatibility; every value runs the HIP kernels
     compile_block_cd: bool = True
     block_cd_backend: str = "eager"  # accepted for compatibility
+
+
+@dataclass(frozen=True)
+class E8P12VampConfig:
+    """Scalar-precision VAMP config for QUIP E8P12 (reference :59-82)."""
+
+    iters: int = 16
+    damping: float = 0.5
+    gamma_start: float = 1.0
+    gamma_retry_factor: float = 4.0
+    gamma_retry_steps: int = 3
+    prior_tau: float = 0.25
+    prior_tau_scale_mode: str = "absmax"
+    compile_prior: bool = True  # accepted for compatibility
+    obs_precision: float = 0.0
+    em_obs_precision: bool = True
+    em_obs_precision_damping: float = 0.3
+    em_obs_precision_min: float = 1e-4
+    em_obs_precision_max: float = 1e8
+    blocks_per_chunk: int = 16  # accepted for compatibility (the kernels stream all blocks)
+    polish_sweeps: int = 3
+    polish_mode: str = "block_cd"  # "none" | "block_cd" | "topk_block_cd"
+    polish_metric: str = "gram"  # "gram" | "diag"
+    polish_metric_rows_per_chunk: int = 0
+    polish_max_blocks: int = 0
+    topk_k: int = 16
+    best_iterate: bool = False
+
+
+def _resolve_e8p12_polish_metric(metric: str) -> str:
+    """reference :179-185."""
+    m = str(metric or "gram").strip().lower()
+    if m in ("isotropic", "diag"):
+        return "diag"
+    if m == "gram":
+        return "gram"
+    raise ValueError(f"unsupported polish_metric={metric!r}; expected 'gram'|'diag'.")
 
 
 def _resolve_polish_mode(*, sweeps: int, mode: str) -> str:
@@ -202,3 +244,182 @@ def solve_uniform_rankspace_vamp(
         "rtn_rankspace_error_mean": float(rtn_err.mean().item()),
     }
     return q.to(torch.int32), x_final, err, rtn_err, stats
+
+
+# ---- E8P12 -----------------------------------------------------------------------
+
+_CD_CTX: Dict[Any, torch.Tensor] = {}
+
+
+def _e8p12_cd_context(Vs: torch.Tensor) -> torch.Tensor:
+    """Per-layer polish context, cached for the last Vs seen (the solvers call the polish
+    once per row block with the same Vs).  The key holds the storage address, the shape and
+    an fp64 content fingerprint (sum and sum of squares), so reused memory misses."""
+    v64 = Vs.to(torch.float64)
+    key = (Vs.data_ptr(), tuple(Vs.shape), str(Vs.device), float(v64.sum().item()), float(v64.square().sum().item()))
+    ctx = _CD_CTX.get(key)
+    if ctx is None:
+        _CD_CTX.clear()
+        ctx = ops.e8p12_cd_prepare(Vs)
+        _CD_CTX[key] = ctx
+    return ctx
+
+
+@torch.inference_mode()
+def polish_e8p12_rankspace(
+    *,
+    x_init: torch.Tensor,
+    idxs_init: torch.Tensor,
+    Y_u: torch.Tensor,
+    Vs: torch.Tensor,
+    cb: object,
+    sweeps: int,
+    polish_mode: str,
+    polish_metric: str,
+    metric_rows_per_chunk: int = 0,
+    polish_max_blocks: int = 0,
+    topk_idxs: Optional[torch.Tensor] = None,
+    order_mode: str = "greedy_gain",
+    snapshot_budgets: Optional[set] = None,
+    snapshots_out: Optional[Dict[int, torch.Tensor]] = None,
+    block_rows: Optional[int] = None,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, Dict[str, Any]]:
+    """Gram-metric block CD over E8P12 codewords (reference :369-423).
+
+    The rows of ``x_init`` form one greedy-order group unless ``block_rows`` splits them
+    (every group of ``block_rows`` rows then has its own order, as separate calls would).
+    Returns (x, idxs, err, stats).
+    """
+    del cb, metric_rows_per_chunk, topk_idxs
+    mode = _resolve_polish_mode(sweeps=int(sweeps), mode=str(polish_mode))
+    metric = _resolve_e8p12_polish_metric(str(polish_metric))
+    x_work = x_init.to(dtype=torch.float32)
+    if mode == "none" or Vs.numel() == 0:
+        err = (Y_u - ops.gemm(x_work, Vs)).square().sum(dim=1)
+        return x_work, idxs_init, err, {"accepted_updates": 0.0}
+    if mode == "topk_block_cd":
+        raise ValueError("mpq_amd implements polish_mode='block_cd' (the recipe default); topk_block_cd is not provided.")
+    if metric != "gram":
+        raise ValueError("mpq_amd implements polish_metric='gram' (the recipe default); 'diag' is not provided.")
+    if str(order_mode or "greedy_gain").strip().lower() != "greedy_gain":
+        raise ValueError("mpq_amd implements order_mode='greedy_gain' (the recipe default).")
+    if snapshot_budgets:
+        raise ValueError("CD snapshots are not provided by the HIP polish.")
+    del snapshots_out
+    rows = int(x_work.shape[0])
+    ctx = _e8p12_cd_context(Vs.to(dtype=torch.float32).contiguous())
+    x, idx, eb, ea, acc = ops.e8p12_cd_polish(x_work, idxs_init, Vs, ctx, sweeps=int(sweeps),
+                                              block_rows=int(block_rows or rows), Yu=Y_u,
+                                              max_blocks=int(polish_max_blocks))
+    stats = {"accepted_updates": float(acc.sum().item()), "block_cd_backend": "hip",
+             "stabilized_objective_nonincreasing": bool((ea <= eb * (1 + 1e-6) + 1e-8).all().item())}
+    return x, idx, ea, stats
+
+
+@torch.inference_mode()
+def solve_e8p12_rankspace_vamp(
+    *,
+    Wr: torch.Tensor,
+    hatWr_init: torch.Tensor,
+    cb: object,
+    V: torch.Tensor,
+    Vh: torch.Tensor,
+    S: torch.Tensor,
+    Vs: torch.Tensor,
+    cfg: E8P12VampConfig,
+    module_name: str = "",
+    obs_precision_init: Optional[float] = None,
+    log_stats: bool = True,
+    debug_out: Optional[Dict[str, Any]] = None,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, Dict[str, Any]]:
+    """Scalar-precision VAMP for QUIP E8P12 in rank space, with the gram-metric polish
+    (reference :853-1276).  Returns (hatWr, Qidxs int64, err, stats); ``log_stats``
+    diagnostics (entropy/margin) are reported as 0.0."""
+    del Vh, log_stats
+    Wr = Wr.to(dtype=torch.float32)
+    rows, n = Wr.shape
+    codesz = int(getattr(cb, "codesz", 8)) if cb is not None else 8
+    if codesz != 8 or n % codesz:
+        raise ValueError(f"E8P12 solver expects n divisible by 8; got n={n}, codesz={codesz}.")
+    nblocks = n // 8
+    polish_sweeps = max(int(cfg.polish_sweeps), 0)
+    polish_mode = _resolve_polish_mode(sweeps=polish_sweeps, mode=str(getattr(cfg, "polish_mode", "block_cd")))
+    polish_metric = _resolve_e8p12_polish_metric(str(cfg.polish_metric or "gram"))
+    prior_tau = float(cfg.prior_tau)
+    mode = str(cfg.prior_tau_scale_mode or "absmax").strip().lower()
+    prior_scale = None
+    if prior_tau > 0.0 and mode not in ("absmax", "exact_full", "exact_full_absmax"):
+        prior_scale = prior_scale_from_center(Wr.reshape(rows, nblocks, 8), mode).reshape(-1)
+    capture_r1 = debug_out is not None and bool(debug_out.get("capture_r1", False))
+    idx, hat, err, r1, g1, st = ops.e8p12_vamp_solve(Wr, hatWr_init, V, S, Vs, cfg, prior_scale=prior_scale,
+                                                     obs_init=float(obs_precision_init or 0.0), want_state=True)
+    idx_stage1 = idx
+    polish_stats: Dict[str, Any] = {}
+    polish_gain = 0.0
+    polish_updates = 0.0
+    if polish_mode != "none":
+        Y_u = ops.gemm(Wr, Vs)
+        err_before = err
+        hat, idx, err, polish_stats = polish_e8p12_rankspace(
+            x_init=hat, idxs_init=idx, Y_u=Y_u, Vs=Vs, cb=cb, sweeps=polish_sweeps, polish_mode=polish_mode,
+            polish_metric=polish_metric, polish_max_blocks=int(cfg.polish_max_blocks))
+        polish_gain = float((err_before - err).mean().item())
+        polish_updates = float(polish_stats.get("accepted_updates", 0.0))
+    if debug_out is not None:
+        summary_only = bool(debug_out.get("summary_only", False))
+        debug_out["solver"] = "e8p12_exact_vamp"
+        g64 = g1.to(torch.float64)
+        debug_out["gamma1_sum"] = float(g64.sum().item())
+        debug_out["gamma1_count"] = int(g64.numel())
+        debug_out["gamma1_min"] = float(g64.min().item())
+        debug_out["gamma1_max"] = float(g64.max().item())
+        if capture_r1:
+            debug_out["r1"] = r1.detach().to(device="cpu")
+        if summary_only:
+            debug_out["changed_count"] = int((idx_stage1 != idx).sum().item())
+            debug_out["changed_total"] = int(idx.numel())
+        else:
+            debug_out["idxs_pre_polish"] = idx_stage1.detach().to(device="cpu")
+            debug_out["gamma1"] = g1.detach().to(device="cpu")
+            debug_out["idxs_post_polish"] = idx.detach().to(device="cpu")
+            debug_out["changed_mask"] = debug_out["idxs_pre_polish"] != debug_out["idxs_post_polish"]
+        if bool(debug_out.get("capture_weights", False)):
+            debug_out["W"] = Wr.detach().to(device="cpu")
+    stats: Dict[str, Any] = {
+        "solver": "e8p12_exact_vamp",
+        "module": str(module_name),
+        "iters": int(st["iters"]),
+        "rank": int(S.numel()),
+        "nblocks": int(nblocks),
+        "damping": float(cfg.damping),
+        "prior_tau": prior_tau,
+        "prior_tau_scale_mode": mode,
+        "compile_prior": bool(getattr(cfg, "compile_prior", True)),
+        "gamma_start": float(cfg.gamma_start),
+        "gamma_retry_factor": float(max(float(cfg.gamma_retry_factor), 1.000001)),
+        "gamma_retry_steps": int(max(int(cfg.gamma_retry_steps), 0)),
+        "obs_precision_initial": float(st["obs_precision_initial"]),
+        "obs_precision_final": float(st["obs_precision_final"]),
+        "obs_precision_mean": float(st["obs_precision_mean"]),
+        "alpha1_retry_count": int(st["alpha1_retry_count"]),
+        "alpha2_clip_count": int(st["alpha2_clip_count"]),
+        "gamma2_invalid_count": int(st["gamma2_invalid_count"]),
+        "alpha1_mean": float(st["alpha1_mean"]),
+        "alpha2_mean": float(st["alpha2_mean"]),
+        "mean_entropy": 0.0,
+        "mean_margin": 0.0,
+        "blocks_per_chunk": int(cfg.blocks_per_chunk),
+        "polish_sweeps": int(polish_sweeps),
+        "polish_mode": polish_mode,
+        "polish_metric": polish_metric,
+        "topk_k": int(cfg.topk_k),
+        "polish_gain": float(polish_gain),
+        "polish_updates": float(polish_updates),
+        "polish_trace": polish_stats,
+        "best_iterate_enabled": bool(cfg.best_iterate),
+        "best_iter": int(st["best_iter"]),
+        "stop_iter": int(st["stop_iter"]),
+        "best_rankspace_error_mean": float(st["rankspace_error_mean"]) if bool(cfg.best_iterate) else 0.0,
+        "rankspace_error_mean": float(err.mean().item()),
+    }
+    return hat, idx, err, stats

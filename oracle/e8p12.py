@@ -416,3 +416,31 @@ def solve_e8p12_rankspace_vamp(Wr, hat_init, V, S, grid, cache, cfg, obs_precisi
     stats["r1"] = r1
     stats["gamma1"] = gamma1
     return hat, idx_t, err, stats
+
+
+def refine_codebook(Wr, Hr, grid, cache, cfg, block_rows=128):
+    """mpq/adapters/quip_sharp.py:396-878 for solver "vamp", init "rtn": nearest-codeword init,
+    fp64 eigh (:33-67), rank-space warm start (:461-475), per row block VAMP + polish with the
+    observation precision carried (:555-586).  Returns (hat, idx, obs_final)."""
+    m, n = Wr.shape
+    idx0, _ = bruteforce_nearest(Wr.reshape(-1, 8).numpy(), grid.numpy())
+    idx0 = torch.from_numpy(np.asarray(idx0)).view(m, n // 8)
+    hat0 = grid[idx0.reshape(-1)].view(m, n)
+    H64 = 0.5 * (Hr.double() + Hr.double().T)
+    lam, V = torch.linalg.eigh(H64)
+    lam, V = lam.float(), V.float()
+    floor = max(1e-6, 1e-6 * max(float(torch.diagonal(H64).mean().abs()), float(lam.max()), 1e-12))
+    lam = lam.clamp_min(floor).flip(0).contiguous()
+    V = V.flip(1).contiguous()
+    S = torch.sqrt(lam)
+    Vs = V * S.unsqueeze(0)
+    obs = 1.0 / max(float((Wr - hat0).matmul(Vs).square().sum()) / (m * n), 1e-12)
+    hat = hat0.clone()
+    idx = idx0.clone()
+    for r0 in range(0, m, block_rows):
+        sl = slice(r0, min(m, r0 + block_rows))
+        h, i, _, st = solve_e8p12_rankspace_vamp(Wr[sl], hat0[sl], V, S, grid, cache, cfg, obs_precision_init=obs)
+        hat[sl] = h
+        idx[sl] = i
+        obs = float(st["obs_final"])
+    return hat, idx, obs
