@@ -13,7 +13,9 @@ Synthetic data: W ~ 0.02 N(0,1) rounded to bf16; Hessians from 128 x 2048 tokens
 channel scales and 1% x20 outlier channels, H = X^T X / T + 0.01 mean(diag) I (config 4).
 AWQ scaling is not applied (the AWQ search is a preprocessing step outside this path).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gate-up]
+It also times one config-3 decoder layer (Llama-3.2-1B-shaped, 2-bit E8P12 via the QUIP# adapter).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gate-up] [--no-e8p12-layer]
 """
 from __future__ import annotations
 
@@ -175,6 +177,87 @@ def e8p12_bench(device, nvec=1 << 24, reps=10):
             "mean_sqerr": float(out["err"].double().mean().item())}
 
 
+def make_student_hessian(n: int, tokens: int, seed: int, device, chunk: int = 16384):
+    """H = X^T X / T + 0.01 mean(diag) I with Student-t (nu = 4) tokens (config 3)."""
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    H = torch.zeros(n, n, device=device, dtype=torch.float32)
+    done = 0
+    while done < tokens:
+        t = min(chunk, tokens - done)
+        Z = torch.randn(t, n, device=device, generator=g)
+        chi = torch.randn(t, n, 4, device=device, generator=g).square().sum(-1)
+        X = Z / torch.sqrt(chi / 4.0)
+        H.addmm_(X.T, X)
+        done += t
+    H /= float(tokens)
+    H += 0.01 * torch.diagonal(H).mean() * torch.eye(n, device=device)
+    return H
+
+
+def e8p12_layer_bench(device, tokens, reps=1):
+    """Config 3 (Llama-3.2-1B-shaped, 2-bit E8P12): one decoder layer's QUIP# linears (qkv fused 3072x2048,
+    o 2048x2048, up/gate fused 16384x2048, down 2048x8192), randomized Hadamard on both sides, mpq_refine_codebook
+    with VAMP (16 iterations, tau 0.2) + 3 gram-metric CD sweeps, 128-row blocks."""
+    import torch
+
+    from mpq_amd import codebook
+    from mpq_amd.adapters.quip_sharp import mpq_refine_codebook
+    from mpq_amd.rotation import apply_left_block_hadamard, apply_right_block_hadamard
+
+    class Args:
+        mpq_init = "rtn"
+        mpq_iters = 16
+        mpq_prior_tau = 0.2
+        mpq_polish_sweeps = 3
+        mpq_block_rows = 128
+
+    cb = codebook.E8P12_codebook(device)
+    shapes = {"qkv": (3072, 2048), "o": (2048, 2048), "up_gate": (16384, 2048), "down": (2048, 8192)}
+    hess = {}
+    out = {}
+    total = 0.0
+    flop_cd = 0.0
+    for i, (name, (m, n)) in enumerate(shapes.items()):
+        if n not in hess:
+            hess[n] = make_student_hessian(n, tokens, 300 + n, device)
+        H = hess[n]
+        g = torch.Generator(device=device)
+        g.manual_seed(400 + i)
+        W = (0.02 * torch.randn(m, n, device=device, generator=g)).to(torch.bfloat16).to(torch.float32)
+        su = (torch.randint(0, 2, (n,), device=device, generator=g) * 2 - 1).float()
+        sv = (torch.randint(0, 2, (m,), device=device, generator=g) * 2 - 1).float()
+        had_m = m & (-m)
+        Wr = apply_right_block_hadamard(W, signs=su, had_dim=n)
+        Wr = apply_left_block_hadamard(Wr, signs=sv, had_dim=had_m)
+        Wr = Wr / Wr.square().mean().sqrt()
+        Hr = apply_right_block_hadamard(apply_left_block_hadamard(H, signs=su, had_dim=n), signs=su, had_dim=n)
+        idx0 = torch.zeros(m, n // 8, dtype=torch.int64, device=device)
+        if i == 0:
+            mpq_refine_codebook(Wr, Hr, Wr, idx0, cb, Args(), module_name=f"model.layers.0.self_attn.{name}")
+        ts = []
+        st = None
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            _, _, st = mpq_refine_codebook(Wr, Hr, Wr, idx0, cb, Args(), module_name=f"model.layers.0.{name}")
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        ms = 1e3 * sum(ts) / len(ts)
+        total += ms
+        flop_cd += 3.0 * m * n * 131072
+        out[name] = {"ms": round(ms, 2), "shape": f"{m}x{n}", "breakdown_s": st["timings"],
+                     "surrogate_before": st["exact_surrogate_before_mean"],
+                     "surrogate_after": st["exact_surrogate_after_mean"]}
+        del W, Wr, Hr
+    polish_s = sum(v["breakdown_s"]["polish_s"] for v in out.values())
+    return {"layer_ms": round(total, 2), "linears": out,
+            "cd_tflops": round(flop_cd / polish_s / 1e12, 2) if polish_s > 0 else None,
+            "cd_frac": round(flop_cd / polish_s / 1e12 / PEAK_FP32_TFLOPS, 4) if polish_s > 0 else None}
+
+
 def cpu_baseline(layer, device):
     """Oracle (torch CPU restatement of the reference's CPU dispatch) on a bounded sample:
     one 128-row block's VAMP init + 2 iterations, 256 CD columns, eigh at n=4096 scaled by n^3."""
@@ -244,6 +327,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gate-up", action="store_true")
+    ap.add_argument("--no-e8p12-layer", action="store_true")
     ap.add_argument("--tokens", type=int, default=128 * 2048)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -281,6 +365,12 @@ def main():
         log(json.dumps({k: v for k, v in gate.items() if k in ("ms", "times_ms", "flop")}),
             json.dumps(gate["stats"]["timings"]))
         del Wg, Hg2
+
+    e8l = None
+    if not args.no_e8p12_layer:
+        log("== E8P12 layer (config 3)")
+        e8l = e8p12_layer_bench(dev, args.tokens)
+        log(json.dumps(e8l))
 
     rf = gemm_roofline(14336, dev)
     log("gemm roofline", json.dumps(rf))
@@ -347,6 +437,9 @@ def main():
                   "achieved_tflops_conv": round(e8["tflops_conv"], 2), "peak": PEAK_FP32_TFLOPS,
                   "frac": round(e8["tflops_conv"] / PEAK_FP32_TFLOPS, 4), "bound": "valu",
                   "bit_exact_sample_65536": e8["bit_exact_sample"]},
+        "e8p12_layer": None if e8l is None else dict(
+            e8l, workload="BASELINE config 3: Llama-3.2-1B-shaped decoder layer, 2-bit E8P12, RHT both sides, "
+                          "VAMP 16 iterations + 3 gram-metric CD sweeps, 128-row blocks"),
         "cpu_baseline": cpu if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
     }
     if cpu is not None:
