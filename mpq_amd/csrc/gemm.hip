@@ -10,7 +10,9 @@
 // Tiling for gfx950: 256 threads = 4 wave64s; work-group tile BM x BN, wave tile
 // WM x WN built from v_mfma_f32_32x32x2_f32 (full fp32 precision).  Tiles are
 // staged through LDS as [k][m] / [k][n] (each MFMA operand read is 32 consecutive
-// floats), double-buffered with a register prefetch of the next K slab.
+// floats), double-buffered.  Interior tiles (the rank-space products always are) run
+// gemm_f32_full_kernel: no bounds checks and two K slabs of global loads in flight;
+// ragged or gathered products run gemm_f32_kernel with one slab of register prefetch.
 #include "gemm.h"
 
 namespace mpq {
@@ -18,10 +20,10 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBK = 16;
+constexpr int kBK = 16;  // K slab of the default configurations (k_per_split is a multiple of 32)
 constexpr int kThreads = 256;
 
-template <int BM, int BN, int WM, int WN, bool TRANS_B, bool GATHER_B>
+template <int BM, int BN, int WM, int WN, bool TRANS_B, bool GATHER_B, int kBK = 16>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
   constexpr int WAVES_N = BN / WN;
   constexpr int MI = WM / 32;
@@ -237,8 +239,174 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ P, int splits, in
   }
 }
 
+// Interior-tile variant: every M/N tile and K slab is in range and 16-byte aligned (checked by
+// the host), no row gather.  Two K slabs of global loads are kept in flight (register sets R0/R1,
+// the loop is unrolled by two so both sets are static), and a slab's LDS operands are all read
+// before its MFMA chain, so each slab waits once for LDS and once for global memory.
+template <int BM, int BN, int WM, int WN, bool TRANS_B, int HOIST = 8>
+__global__ __launch_bounds__(kThreads) void gemm_f32_full_kernel(GemmParams p) {
+  constexpr int BK = 16;
+  constexpr int WAVES_N = BN / WN;
+  constexpr int MI = WM / 32;
+  constexpr int NI = WN / 32;
+  constexpr int LDA_S = BM + 4;
+  constexpr int LDB_S = BN + 4;
+  constexpr int A_F4 = BM * BK / 4 / kThreads;
+  constexpr int B_F4 = BN * BK / 4 / kThreads;
+  static_assert(A_F4 >= 1 && B_F4 >= 1, "tile too small for 256 threads");
+
+  __shared__ float As[2][BK][LDA_S];
+  __shared__ float Bs[2][BK][LDB_S];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm0 = (wave / WAVES_N) * WM;
+  const int wn0 = (wave % WAVES_N) * WN;
+  const int64_t m0 = (int64_t)blockIdx.y * BM;
+  const int64_t n0 = (int64_t)blockIdx.x * BN;
+  const int split = blockIdx.z;
+  const int64_t kbeg = (int64_t)split * p.k_per_split;
+  const int64_t nslab = p.k_per_split / BK;
+
+  // per-thread global source pointers of the first slab (advanced by BK per slab)
+  const float* asrc[A_F4];
+  const float* bsrc[B_F4];
+#pragma unroll
+  for (int i = 0; i < A_F4; ++i) {
+    const int t = tid + i * kThreads;
+    asrc[i] = p.A + (m0 + t / (BK / 4)) * p.lda + kbeg + (t % (BK / 4)) * 4;
+  }
+#pragma unroll
+  for (int i = 0; i < B_F4; ++i) {
+    const int t = tid + i * kThreads;
+    if constexpr (!TRANS_B) {
+      bsrc[i] = p.B + (kbeg + t / (BN / 4)) * p.ldb + n0 + (t % (BN / 4)) * 4;
+    } else {
+      bsrc[i] = p.B + (n0 + t / (BK / 4)) * p.ldb + kbeg + (t % (BK / 4)) * 4;
+    }
+  }
+  const int64_t b_step = TRANS_B ? BK : BK * p.ldb;
+
+  float4 ra0[A_F4], rb0[B_F4], ra1[A_F4], rb1[B_F4];
+  auto gload = [&](float4 (&ra)[A_F4], float4 (&rb)[B_F4], int64_t s) {
+#pragma unroll
+    for (int i = 0; i < A_F4; ++i) ra[i] = *reinterpret_cast<const float4*>(asrc[i] + s * BK);
+#pragma unroll
+    for (int i = 0; i < B_F4; ++i) rb[i] = *reinterpret_cast<const float4*>(bsrc[i] + s * b_step);
+  };
+  auto lstore = [&](const float4 (&ra)[A_F4], const float4 (&rb)[B_F4], int buf) {
+#pragma unroll
+    for (int i = 0; i < A_F4; ++i) {
+      const int t = tid + i * kThreads;
+      const int m = t / (BK / 4);
+      const int kq = (t % (BK / 4)) * 4;
+      As[buf][kq + 0][m] = ra[i].x;
+      As[buf][kq + 1][m] = ra[i].y;
+      As[buf][kq + 2][m] = ra[i].z;
+      As[buf][kq + 3][m] = ra[i].w;
+    }
+#pragma unroll
+    for (int i = 0; i < B_F4; ++i) {
+      const int t = tid + i * kThreads;
+      if constexpr (!TRANS_B) {
+        *reinterpret_cast<float4*>(&Bs[buf][t / (BN / 4)][(t % (BN / 4)) * 4]) = rb[i];
+      } else {
+        const int n = t / (BK / 4);
+        const int kq = (t % (BK / 4)) * 4;
+        Bs[buf][kq + 0][n] = rb[i].x;
+        Bs[buf][kq + 1][n] = rb[i].y;
+        Bs[buf][kq + 2][n] = rb[i].z;
+        Bs[buf][kq + 3][n] = rb[i].w;
+      }
+    }
+  };
+
+  floatx16 acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int kl = lane >> 5;
+  const int ml = lane & 31;
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int k0 = 0; k0 < BK / 2; k0 += HOIST) {
+      float a[HOIST][MI], b[HOIST][NI];
+#pragma unroll
+      for (int kk = 0; kk < HOIST; ++kk) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i) a[kk][i] = As[buf][2 * (k0 + kk) + kl][wm0 + i * 32 + ml];
+#pragma unroll
+        for (int j = 0; j < NI; ++j) b[kk][j] = Bs[buf][2 * (k0 + kk) + kl][wn0 + j * 32 + ml];
+      }
+#pragma unroll
+      for (int kk = 0; kk < HOIST; ++kk)
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][i], b[kk][j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // prologue: slab 0 -> LDS buffer 0, slab 1 in flight in R1
+  gload(ra0, rb0, 0);
+  if (nslab > 1) gload(ra1, rb1, 1);
+  lstore(ra0, rb0, 0);
+  __syncthreads();
+  // slab s is in LDS buffer s&1; slab s+1 is in flight in R((s+1)&1)
+  for (int64_t s = 0; s < nslab; s += 2) {
+    // even slab s: buffer 0; next slab s+1 in R1
+    if (s + 2 < nslab) gload(ra0, rb0, s + 2);
+    compute(0);
+    if (s + 1 < nslab) lstore(ra1, rb1, 1);
+    __syncthreads();
+    if (s + 1 >= nslab) break;
+    // odd slab s+1: buffer 1; next slab s+2 in R0
+    if (s + 3 < nslab) gload(ra1, rb1, s + 3);
+    compute(1);
+    if (s + 2 < nslab) lstore(ra0, rb0, 0);
+    __syncthreads();
+  }
+
+  const int col = lane & 31;
+  const int rbase = (lane >> 5) * 4;
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int64_t gn = n0 + wn0 + j * 32 + col;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t gm = m0 + wm0 + i * 32 + (v >> 2) * 8 + rbase + (v & 3);
+        const float val = acc[i][j][v];
+        if (p.mode == kGemmPartials) {
+          p.C[(int64_t)split * p.split_stride + gm * p.ldc + gn] = val;
+        } else {
+          float* dst = p.C + gm * p.ldc + gn;
+          *dst = p.beta == 0.f ? p.alpha * val : p.alpha * val + p.beta * *dst;
+        }
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int WM, int WN>
 hipError_t launch_cfg(const GemmParams& p, dim3 grid, hipStream_t stream) {
+  const bool full = !p.b_rows && p.a_vec4 && p.b_vec4 && p.M % BM == 0 && p.N % BN == 0 &&
+                    p.k_per_split % 16 == 0 && (int64_t)grid.z * p.k_per_split == p.K;
+  if (full) {
+    if (p.trans_b) {
+      hipLaunchKernelGGL((gemm_f32_full_kernel<BM, BN, WM, WN, true>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((gemm_f32_full_kernel<BM, BN, WM, WN, false>), grid, dim3(kThreads), 0, stream, p);
+    }
+    return hipGetLastError();
+  }
   if (p.trans_b) {
     hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM, WN, true, false>), grid, dim3(kThreads), 0, stream, p);
   } else if (p.b_rows) {
@@ -258,7 +426,7 @@ int choose_splits(int64_t M, int64_t N, int64_t K, int64_t workspace_floats, int
   if (tiles_m * ((N + 127) / 128) < 512) bn = 64;
   const int64_t tiles = tiles_m * ((N + bn - 1) / bn);
   int splits = 1;
-  const int64_t target = 1024;  // ~4 work-groups per CU on 256 CUs
+  const int64_t target = 2048;  // ~8 work-groups per CU on 256 CUs (latency hiding at small M)
   while (splits < 32 && tiles * splits * 2 <= target && K / (splits * 2) >= 256 &&
          (int64_t)(splits * 2) * M * N <= workspace_floats)
     splits *= 2;
@@ -268,7 +436,7 @@ int choose_splits(int64_t M, int64_t N, int64_t K, int64_t workspace_floats, int
 
 hipError_t gemm_partials(GemmParams p, int splits, int bn, hipStream_t stream) {
   p.mode = splits > 1 ? kGemmPartials : p.mode;
-  const int64_t kps = ((p.K + splits - 1) / splits + kBK - 1) / kBK * kBK;
+  const int64_t kps = ((p.K + splits - 1) / splits + 31) / 32 * 32;
   p.k_per_split = kps > 0 ? kps : kBK;
   p.a_vec4 = ((reinterpret_cast<uintptr_t>(p.A) & 15u) == 0) && (p.lda % 4 == 0);
   p.b_vec4 = ((reinterpret_cast<uintptr_t>(p.B) & 15u) == 0) && (p.ldb % 4 == 0);
