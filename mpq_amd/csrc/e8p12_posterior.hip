@@ -13,20 +13,19 @@
 // with a running maximum), var = (E|c|^2 - |mu|^2) / 8, and when the folded
 // precision is >= 1e3 the mean snaps to the MAP codeword (var = 0).
 //
-// Layout: one lane per 8-block.  Each coordinate's |a| takes only three values
-// (b in {1/2, 3/2, 5/2}), so per branch a lane precomputes 24 values of logaddexp,
-// log|t| and t and keeps them in LDS ([slot][lane], conflict-free); the 256 bases
-// are walked with uniform (scalar) table reads.  Transcendental-bound VALU kernel.
+// Layout: 8 lanes per 8-block.  Each coordinate's |a| takes only three values
+// (b in {1/2, 3/2, 5/2}), so per branch lane c of a block computes logaddexp, log|t| and t
+// for coordinate c at the three levels and stores them in LDS ([slot][block]); the lanes then
+// split the 256 bases (k = c mod 8) with their own online softmax, reading the tables and the
+// packed abs patterns from LDS, and merge the 8 partial states with a butterfly.
+// Transcendental-bound VALU kernel.
 #include "common.h"
 #include "e8p12_tables.inc"
 
 namespace {
 
-constexpr int kThreads = 128;
-
-struct Pattern {
-  unsigned char code[8];  // 2*|b| in {1,3,5}
-};
+constexpr int kThreads = 256;
+constexpr int kLanes = 8;  // lanes per 8-block
 
 __device__ __forceinline__ int slot_of(int abs2) { return abs2 >> 1; }  // 1->0, 3->1, 5->2
 
@@ -36,39 +35,84 @@ __device__ __forceinline__ float log1mexp_f(float x) {
   return x < cutoff ? log1pf(-expf(x)) : logf(-expm1f(x));
 }
 
+// Merge of two partial online-softmax states (running max m, sum Z, first moments mu, second
+// moment sec, offset weight wo).  Symmetric in its arguments, so both lanes of a butterfly pair
+// obtain bit-identical results.
+struct SoftState {
+  float m, Z, sec, wo;
+  float mu[8];
+};
+
+__device__ __forceinline__ void merge_state(SoftState& a, int lane_xor) {
+  const float mo = __shfl_xor(a.m, lane_xor);
+  const float Zo = __shfl_xor(a.Z, lane_xor);
+  const float so = __shfl_xor(a.sec, lane_xor);
+  const float wo = __shfl_xor(a.wo, lane_xor);
+  const float mn = fmaxf(a.m, mo);
+  const float fa = a.m == -INFINITY ? 0.f : expf(a.m - mn);
+  const float fo = mo == -INFINITY ? 0.f : expf(mo - mn);
+  a.Z = a.Z * fa + Zo * fo;
+  a.sec = a.sec * fa + so * fo;
+  a.wo = a.wo * fa + wo * fo;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float uo = __shfl_xor(a.mu[i], lane_xor);
+    a.mu[i] = a.mu[i] * fa + uo * fo;
+  }
+  a.m = mn;
+}
+
+// 8 lanes per 8-block (kLanes), 32 blocks per 256-thread work-group.  Lane c of a block
+// builds the three table slots of coordinate c (logaddexp, log|tanh|, tanh for |b| = 1/2, 3/2,
+// 5/2) and walks the bases k = c, c + 8, ..., c + 248 of each shift branch with its own online
+// softmax; the 8 partial states are merged by a butterfly at the end.
 template <bool kPrior>
 __global__ __launch_bounds__(kThreads) void e8p12_posterior_kernel(
     const float* __restrict__ r, int64_t n, const float* __restrict__ gamma, int64_t gamma_div,
     const float* __restrict__ center, const float* __restrict__ scale, float tau,
     const float* __restrict__ map_vals, float* __restrict__ x1_out, float* __restrict__ var_out) {
-  __shared__ float s_lc[24][kThreads];
-  __shared__ float s_lt[24][kThreads];
-  __shared__ float s_t[24][kThreads];
-  const int lane = threadIdx.x;
-  const int64_t v = (int64_t)blockIdx.x * kThreads + lane;
+  constexpr int kBlocks = kThreads / kLanes;
+  __shared__ float s_lc[24][kBlocks];
+  __shared__ float s_lt[24][kBlocks];
+  __shared__ float s_t[24][kBlocks];
+  __shared__ unsigned s_code[256];  // bits 2i..2i+1: slot of coordinate i; bit 16: odd parity
+  __shared__ float s_sq[256];
+
+  const int tid = threadIdx.x;
+  const int bl = tid / kLanes;
+  const int c = tid % kLanes;
+  const int64_t v = (int64_t)blockIdx.x * kBlocks + bl;
   const bool active = v < n;
   const int64_t vv = active ? v : n - 1;
 
-  float rw[8];
+  for (int k = tid; k < 256; k += kThreads) {
+    unsigned w = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) rw[i] = r[8 * vv + i];
+    for (int i = 0; i < 8; ++i) w |= (unsigned)slot_of(kE8Abs2[k][i]) << (2 * i);
+    w |= (unsigned)(kE8Parity[k] & 1) << 16;
+    s_code[k] = w;
+    s_sq[k] = kE8SqNorm[k];
+  }
+
+  float rc = r[8 * vv + c];
   float g = gamma[vv / gamma_div];
   if constexpr (kPrior) {
-    float s;
+    const float cc = center[8 * vv + c];
+    float sc;
     if (scale != nullptr) {
-      s = scale[vv];
+      sc = scale[vv];
     } else {
-      s = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s = fmaxf(s, fabsf(center[8 * vv + i]));
+      sc = fabsf(cc);
+      sc = fmaxf(sc, __shfl_xor(sc, 1));
+      sc = fmaxf(sc, __shfl_xor(sc, 2));
+      sc = fmaxf(sc, __shfl_xor(sc, 4));
     }
-    s = s < 1e-12f ? 1e-12f : s;
+    sc = sc < 1e-12f ? 1e-12f : sc;
     const float tau_c = tau > 1e-12f ? tau : 1e-12f;
-    const float ts = tau_c * s;
+    const float ts = tau_c * sc;
     const float prec = 1.0f / (ts * ts);
     const float gw = g + prec;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) rw[i] = (g * rw[i] + prec * center[8 * vv + i]) / gw;
+    rc = (g * rc + prec * cc) / gw;
     g = gw;
   }
   const float mhalf_g = -0.5f * g;
@@ -76,84 +120,83 @@ __global__ __launch_bounds__(kThreads) void e8p12_posterior_kernel(
   const float t_lo = (float)(-1.0 + 1e-7);
   const float kLog2 = 0.69314718055994530942f;
 
-  float m = -INFINITY;  // running maximum of the log-components
-  float Z = 0.f;        // sum of exp(lc - m)
-  float mu[8];
+  SoftState st;
+  st.m = -INFINITY;
+  st.Z = 0.f;
+  st.sec = 0.f;
+  st.wo = 0.f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) mu[i] = 0.f;
-  float sec = 0.f;
-  float wsum_off = 0.f;  // sum of w * offset (the constant part of mu)
+  for (int i = 0; i < 8; ++i) st.mu[i] = 0.f;
 
   for (int br = 0; br < 2; ++br) {
     const float off = br == 0 ? 0.25f : -0.25f;
-    float y[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = rw[i] - off;
-    float yn = y[0] * y[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) yn = yn + y[i] * y[i];
+    const float yc = rc - off;
+    float yn = yc * yc;
+    yn = yn + __shfl_xor(yn, 1);
+    yn = yn + __shfl_xor(yn, 2);
+    yn = yn + __shfl_xor(yn, 4);
     unsigned negmask = 0;  // bit (3 i + slot): t < 0
+    const float gy = g * yc;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float gy = g * y[i];
-#pragma unroll
-      for (int sl = 0; sl < 3; ++sl) {
-        const float b = 0.5f + (float)sl;  // 0.5, 1.5, 2.5
-        const float a = gy * b;
-        const float aa = fabsf(a);
-        const float lc = aa + log1pf(expf(-2.0f * aa));  // logaddexp(a, -a)
-        float t = tanhf(a);
-        t = t < t_lo ? t_lo : (t > t_hi ? t_hi : t);
-        float at = fabsf(t);
-        at = at < 1e-7f ? 1e-7f : at;
-        s_lc[3 * i + sl][lane] = lc;
-        s_lt[3 * i + sl][lane] = logf(at);
-        s_t[3 * i + sl][lane] = t;
-        if (t < 0.f) negmask |= 1u << (3 * i + sl);
-      }
+    for (int sl = 0; sl < 3; ++sl) {
+      const float b = 0.5f + (float)sl;
+      const float a = gy * b;
+      const float aa = fabsf(a);
+      const float lc = aa + log1pf(expf(-2.0f * aa));  // logaddexp(a, -a)
+      float t = tanhf(a);
+      t = t < t_lo ? t_lo : (t > t_hi ? t_hi : t);
+      float at = fabsf(t);
+      at = at < 1e-7f ? 1e-7f : at;
+      s_lc[3 * c + sl][bl] = lc;
+      s_lt[3 * c + sl][bl] = logf(at);
+      s_t[3 * c + sl][bl] = t;
+      if (t < 0.f) negmask |= 1u << (3 * c + sl);
     }
+    negmask |= __shfl_xor(negmask, 1);
+    negmask |= __shfl_xor(negmask, 2);
+    negmask |= __shfl_xor(negmask, 4);
     __syncthreads();
 
-    for (int k = 0; k < 256; ++k) {
+    for (int k = c; k < 256; k += kLanes) {
+      const unsigned w = s_code[k];
       int sl[8];
       float bv[8];
       unsigned bm = 0;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int code = kE8Abs2[k][i];
-        sl[i] = 3 * i + slot_of(code);
-        bv[i] = 0.5f * (float)code;
+        const int code = (int)((w >> (2 * i)) & 3u);
+        sl[i] = 3 * i + code;
+        bv[i] = 0.5f + (float)code;
         bm |= 1u << sl[i];
       }
-      const bool even = kE8Parity[k] == 0;
-      float logC = s_lc[sl[0]][lane];
-      float L = s_lt[sl[0]][lane];
+      const bool even = (w >> 16) == 0u;
+      float logC = s_lc[sl[0]][bl];
+      float L = s_lt[sl[0]][bl];
 #pragma unroll
       for (int i = 1; i < 8; ++i) {
-        logC = logC + s_lc[sl[i]][lane];
-        L = L + s_lt[sl[i]][lane];
+        logC = logC + s_lc[sl[i]][bl];
+        L = L + s_lt[sl[i]][bl];
       }
       const bool neg = (__builtin_popcount(negmask & bm) & 1) != 0;
       // log(1 + prod t) for an even base, log(1 - prod t) for an odd base
-      const bool plus_branch = even != neg;  // prod t >= 0 with "+", or prod t < 0 with "-"
+      const bool plus_branch = even != neg;
       const float lz = plus_branch ? log1pf(expf(L)) : log1mexp_f(L);
       const float logZs = (logC + lz) - kLog2;
-      const float cst = mhalf_g * (yn + kE8SqNorm[k]);
-      const float lcomp = cst + logZs;
-      // online softmax update
-      const float mnew = fmaxf(m, lcomp);
-      const float resc = expf(m - mnew);
-      const float w = expf(lcomp - mnew);
-      m = mnew;
+      const float sq = s_sq[k];
+      const float lcomp = mhalf_g * (yn + sq) + logZs;
+      const float mnew = fmaxf(st.m, lcomp);
+      const float resc = expf(st.m - mnew);
+      const float wgt = expf(lcomp - mnew);
+      st.m = mnew;
       // sign means with prefix / suffix products (mpq/priors/e8p12.py:235-255)
       float tt[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) tt[i] = s_t[sl[i]][lane];
+      for (int i = 0; i < 8; ++i) tt[i] = s_t[sl[i]][bl];
       const float pabs = expf(L);
       const float prod = neg ? -pabs : pabs;
       float denom = even ? 1.0f + prod : 1.0f - prod;
       denom = fabsf(denom) > 1e-12f ? denom : 1.0f;
-      const float inv = 1.0f / denom;  // one division per base; the 8 sign means multiply by it
+      const float inv = 1.0f / denom;
       float pre[8];
       float acc = 1.0f;
 #pragma unroll
@@ -162,7 +205,6 @@ __global__ __launch_bounds__(kThreads) void e8p12_posterior_kernel(
         acc = acc * tt[i];
       }
       float suf = 1.0f;
-      float mcsum = 0.f;
       float mc[8];
 #pragma unroll
       for (int i = 7; i >= 0; --i) {
@@ -172,36 +214,38 @@ __global__ __launch_bounds__(kThreads) void e8p12_posterior_kernel(
         mc[i] = smn * bv[i];
         suf = suf * tt[i];
       }
-      mcsum = mc[0];
+      float mcsum = mc[0];
 #pragma unroll
       for (int i = 1; i < 8; ++i) mcsum = mcsum + mc[i];
-      const float second = (kE8SqNorm[k] + 8.0f * (off * off)) + (2.0f * off) * mcsum;
-      Z = Z * resc + w;
+      const float second = (sq + 8.0f * (off * off)) + (2.0f * off) * mcsum;
+      st.Z = st.Z * resc + wgt;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) mu[i] = mu[i] * resc + w * mc[i];
-      sec = sec * resc + w * second;
-      wsum_off = wsum_off * resc + w * off;
+      for (int i = 0; i < 8; ++i) st.mu[i] = st.mu[i] * resc + wgt * mc[i];
+      st.sec = st.sec * resc + wgt * second;
+      st.wo = st.wo * resc + wgt * off;
     }
     __syncthreads();
   }
+  merge_state(st, 1);
+  merge_state(st, 2);
+  merge_state(st, 4);
   if (!active) return;
-  float x1[8];
   float msq = 0.f;
+  float x1c = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    x1[i] = (mu[i] + wsum_off) / Z;
-    msq = i == 0 ? x1[i] * x1[i] : msq + x1[i] * x1[i];
+    const float xi = (st.mu[i] + st.wo) / st.Z;
+    msq = i == 0 ? xi * xi : msq + xi * xi;
+    if (i == c) x1c = xi;
   }
-  float var = ((sec / Z) - msq) / 8.0f;
+  float var = ((st.sec / st.Z) - msq) / 8.0f;
   var = var < 0.f ? 0.f : var;
   if (g >= 1e3f) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x1[i] = map_vals[8 * v + i];
+    x1c = map_vals[8 * v + c];
     var = 0.f;
   }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) x1_out[8 * v + i] = x1[i];
-  var_out[v] = var;
+  x1_out[8 * v + c] = x1c;
+  if (c == 0) var_out[v] = var;
 }
 
 // alpha1 = gamma1_row * mean(var1 over the row's blocks) (mpq/priors/e8p12.py:955).
@@ -223,7 +267,7 @@ namespace mpq {
 hipError_t e8p12_posterior(const float* r, int64_t n, const float* gamma, int64_t gamma_div,
                            const float* center, const float* scale, float tau, const float* map_vals,
                            float* x1, float* var, hipStream_t stream) {
-  const int64_t blocks = (n + kThreads - 1) / kThreads;
+  const int64_t blocks = (n + kThreads / kLanes - 1) / (kThreads / kLanes);
   if (center != nullptr && tau > 0.f) {
     hipLaunchKernelGGL(e8p12_posterior_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, stream, r, n,
                        gamma, gamma_div, center, scale, tau, map_vals, x1, var);

@@ -23,6 +23,17 @@ namespace {
 
 inline int64_t a64(int64_t v) { return (v + 63) / 64 * 64; }
 
+// out[b] = sum_j var[b * nb + j], one work-group per row (fixed reduction order).
+__global__ __launch_bounds__(kEW) void row_sum_kernel(int64_t nb, const float* __restrict__ var,
+                                                      float* __restrict__ out) {
+  __shared__ float red[kEW / 64];
+  const int64_t b = blockIdx.x;
+  float acc = 0.f;
+  for (int64_t j = threadIdx.x; j < nb; j += blockDim.x) acc += var[b * nb + j];
+  const float t = block_sum(acc, red);
+  if (threadIdx.x == 0) out[b] = t;
+}
+
 struct E8Plan {
   int64_t rows, n, nb, nchunks;
   int splits, bn;
@@ -125,6 +136,7 @@ extern "C" int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, co
   float* g1new = rowbuf + 11 * rows;
   float* errrow = rowbuf + 12 * rows;
   float* g1_best = rowbuf + 13 * rows;
+  float* varsum = rowbuf + 14 * rows;
   const dim3 eg((unsigned)nchunks, (unsigned)rows), eb(kEW);
   const float tau = cfg->prior_tau;
   const float* center = tau > 0.f ? Wr : nullptr;
@@ -203,7 +215,8 @@ extern "C" int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, co
                          stream);
       if (rc != kOk) return rc;
       MPQ_HIP_TRY(e8p12_posterior(r1, rows * nb, g1w, nb, center, prior_scale, tau, mvals, x1, var1, stream));
-      hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, nb, (int)nb, var1, g1w, has_prev ? 1 : 0,
+      hipLaunchKernelGGL(row_sum_kernel, dim3((unsigned)rows), eb, 0, stream, nb, var1, varsum);
+      hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, nb, 1, varsum, g1w, has_prev ? 1 : 0,
                          damping, g2prev, a1raw, a1, eta1, g2new, g2, status);
       MPQ_LAUNCH_CHECK();
       if ((rc = sync_status()) != kOk) return rc;

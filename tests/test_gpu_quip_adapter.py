@@ -36,27 +36,55 @@ def _surrogate(Wr, hat, H):
 # synthetic Hessians the reference's own EM drives the observation precision of a later row
 # block to its 1e-4 clamp (a divergent VAMP trajectory); the fp32 rounding of the two
 # implementations then decides the codes, so such cases are not parity cases.
+#
+# Parity is checked stage by stage: the VAMP stage (no polish) against the oracle driver, then
+# the polish from the GPU's own VAMP result against the oracle's polish of that same state.  The
+# end-to-end codes are not compared directly: the greedy order of a row block is shared by all
+# its rows, so one differing VAMP code (a near-tie) can reorder the block's CD and move a large
+# fraction of its codes to an equally good local optimum; the surrogate loss is compared instead.
 @pytest.mark.parametrize("m,n,key,heavy", [(128, 256, "quip:128:256", True), (192, 256, "quip:192:256d", False)])
 def test_refine_codebook_matches_oracle(gpu, m, n, key, heavy):
     Wr, H = _layer(m, n, key, heavy)
     grid = torch.from_numpy(codebook.grid_numpy())
     cache = oe8.factor_cache(grid)
-    cfg = dict(iters=16, damping=0.5, prior_tau=0.25, polish_sweeps=3)
-    ref_hat, ref_idx, ref_obs = oe8.refine_codebook(Wr, H, grid, cache, cfg, block_rows=128)
     cb = codebook.E8P12_codebook(gpu)
-    hat0 = ref_hat.to(gpu)  # LDLQ stand-in, only used by the audit statistics
-    hat, idx, st = mpq_refine_codebook(Wr.to(gpu), H.to(gpu), hat0, ref_idx.to(gpu), cb, Args(),
-                                       module_name="model.layers.3.mlp.up_proj", adapter_cfg=QuipAdapterConfig())
+    cfg = dict(iters=16, damping=0.5, prior_tau=0.25, polish_sweeps=0)
+    # VAMP stage
+    ref_hat0, ref_idx0, ref_obs = oe8.refine_codebook(Wr, H, grid, cache, cfg, block_rows=128)
+
+    class A0(Args):
+        mpq_polish_sweeps = 0
+
+    hat0, idx0, st0 = mpq_refine_codebook(Wr.to(gpu), H.to(gpu), ref_hat0.to(gpu), ref_idx0.to(gpu), cb, A0(),
+                                          module_name="model.layers.3.mlp.up_proj")
+    agree0 = float((idx0.cpu() == ref_idx0).float().mean())
+    assert agree0 >= 0.999, agree0
+    assert abs(st0["obs_precision_final"] - ref_obs) <= 5e-3 * ref_obs
+    assert st0["mechanism"]["layer_index"] == 3
+    # full adapter (VAMP + 3 CD sweeps)
+    hat, idx, st = mpq_refine_codebook(Wr.to(gpu), H.to(gpu), ref_hat0.to(gpu), ref_idx0.to(gpu), cb, Args())
     hat, idx = hat.cpu(), idx.cpu()
     assert idx.dtype == torch.int64 and tuple(idx.shape) == (m, n // 8)
     assert torch.equal(hat, grid[idx.reshape(-1)].view(m, n))
-    agree = float((idx == ref_idx).float().mean())
-    assert agree >= 0.99, agree
-    s_ref, s_got = _surrogate(Wr, ref_hat, H), _surrogate(Wr, hat, H)
-    assert abs(s_got - s_ref) <= 5e-3 * s_ref, (s_got, s_ref)
-    assert abs(st["obs_precision_final"] - ref_obs) <= 5e-3 * ref_obs
-    assert st["mechanism"]["layer_index"] == 3
     assert st["exact_surrogate_after_mean"] <= st["exact_surrogate_before_mean"]
+    # polish stage: the oracle polishes the GPU's VAMP result
+    Hd = 0.5 * (H.double() + H.double().T)
+    lam, V = torch.linalg.eigh(Hd)
+    lam, V = lam.float(), V.float()
+    floor = max(1e-6, 1e-6 * max(float(torch.diagonal(Hd).mean().abs()), float(lam.max()), 1e-12))
+    Vs = V.flip(1) * torch.sqrt(lam.clamp_min(floor).flip(0)).unsqueeze(0)
+    Yu = Wr.matmul(Vs)
+    ref_x, ref_i = [], []
+    for r0 in range(0, m, 128):
+        sl = slice(r0, min(m, r0 + 128))
+        x_b, i_b, _ = oe8.gram_block_cd(hat0.cpu()[sl], idx0.cpu()[sl], Yu[sl], Vs, grid, 3)
+        ref_x.append(x_b)
+        ref_i.append(i_b)
+    ref_x, ref_i = torch.cat(ref_x), torch.cat(ref_i)
+    agree = float((idx == ref_i).float().mean())
+    assert agree >= 0.99, agree
+    s_ref, s_got = _surrogate(Wr, ref_x, H), _surrogate(Wr, hat, H)
+    assert abs(s_got - s_ref) <= 5e-3 * s_ref, (s_got, s_ref)
 
 
 @pytest.mark.parametrize("init", ["zero", "random", "float", "ldlq"])
