@@ -19,8 +19,7 @@ __global__ __launch_bounds__(256) void residual_kernel(int64_t rows, int64_t n, 
     const int64_t j = (int64_t)blockIdx.x * 1024 + e * 256 + threadIdx.x;
     if (j >= n) continue;
     const int64_t o = b * n + j;
-    float v = P[o];
-    for (int s = 1; s < splits; ++s) v = v + P[(int64_t)s * split_stride + o];
+    const float v = sum_splits(P, splits, split_stride, o);
     const float r = Yu[o] - v;
     if (res) res[o] = r;
     acc += r * r;

@@ -75,6 +75,25 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
   return total;
 }
 
+// Sum of split-K partials P[s * stride + o], s = 0..splits-1, added in split order.  The loads
+// are unrolled and predicated in groups of 8 so their latencies overlap.
+constexpr int kMaxSplits = 32;
+__device__ __forceinline__ float sum_splits(const float* __restrict__ P, int splits, int64_t stride,
+                                            int64_t o) {
+  float acc = P[o];
+#pragma unroll
+  for (int s0 = 1; s0 < kMaxSplits; s0 += 8) {
+    if (s0 >= splits) break;
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = (s0 + u < splits) ? P[(int64_t)(s0 + u) * stride + o] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < splits) acc = acc + v[u];
+  }
+  return acc;
+}
+
 __device__ __forceinline__ double block_sum_f64(double v, double* scratch) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;

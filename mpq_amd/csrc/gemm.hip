@@ -232,8 +232,7 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ P, int splits, in
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t m = e / N, n = e % N;
-    float acc = P[m * N + n];
-    for (int s = 1; s < splits; ++s) acc = acc + P[(int64_t)s * split_stride + m * N + n];
+    const float acc = sum_splits(P, splits, split_stride, m * N + n);
     float* dst = C + m * ldc + n;
     *dst = beta == 0.f ? alpha * acc : alpha * acc + beta * *dst;
   }

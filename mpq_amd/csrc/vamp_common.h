@@ -58,6 +58,7 @@ __global__ __launch_bounds__(kEW) void rows_alpha1_kernel(
     float* __restrict__ g2new, float* __restrict__ g2, VampStatus* __restrict__ st) {
   __shared__ float red[kEW / 64];
   int inval = 0, nonfin = 0, g2n_bad = 0, g2_bad = 0;
+  float a1part = 0.f;  // this thread's rows of sum(alpha1), in row order
   const float hi = one_minus_alpha_eps();
   for (int64_t b = threadIdx.x; b < rows; b += blockDim.x) {
     float vs = var_part[b * nchunks];
@@ -73,6 +74,7 @@ __global__ __launch_bounds__(kEW) void rows_alpha1_kernel(
     else if (isinf(a1c)) a1c = a1c > 0.f ? hi : kAlphaEps;
     a1c = a1c < kAlphaEps ? kAlphaEps : (a1c > hi ? hi : a1c);
     alpha1[b] = a1c;
+    a1part += a1c;
     const float e1 = g1w[b] / a1c;
     eta1[b] = e1;
     const float gn = nan_to_num_clamp_min(e1 - g1w[b], 1e-12f, 1e12f, 1e-12f, kPrecEps);
@@ -96,9 +98,8 @@ __global__ __launch_bounds__(kEW) void rows_alpha1_kernel(
   const float s_nonfin = block_sum((float)nonfin, red);
   const float s_g2n = block_sum((float)g2n_bad, red);
   const float s_g2 = block_sum((float)g2_bad, red);
-  float a1sum = 0.f;
+  const float a1sum = block_sum(a1part, red);
   if (threadIdx.x == 0) {
-    for (int64_t b = 0; b < rows; ++b) a1sum += alpha1[b];
     st->a1_invalid = (int)s_inval;
     st->a1_nonfinite = (int)s_nonfin;
     st->g2new_invalid = (int)s_g2n;
@@ -161,8 +162,7 @@ __global__ __launch_bounds__(kEW) void lmmse_epi1_kernel(
     const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
     if (j >= n) continue;
     const int64_t o = b * n + j;
-    float r2v = P[o];
-    for (int s = 1; s < splits; ++s) r2v = r2v + P[(int64_t)s * split_stride + o];
+    const float r2v = sum_splits(P, splits, split_stride, o);
     const float sj = S[j];
     const float s2 = sj * sj;
     const float denom = obs * s2 + gb;
@@ -195,6 +195,7 @@ __global__ __launch_bounds__(kEW) void rows_lmmse_kernel(
   const float hi = one_minus_alpha_eps();
   const float c0 = (float)(1.0 - (double)rank / (double)n);
   int clip = 0;
+  float em_part = 0.f, a2_part = 0.f;  // this thread's rows, in row order
   for (int64_t b = threadIdx.x; b < rows; b += blockDim.x) {
     const float* pp = part3 + b * nchunks * 3;
     float sinv = pp[0], sres = pp[1], strace = pp[2];
@@ -228,14 +229,13 @@ __global__ __launch_bounds__(kEW) void rows_lmmse_kernel(
     // EM statistic per row: |residual_after|^2 + trace term; alpha2 kept for stats
     eta2[rows + b] = sres + strace;
     eta2[2 * rows + b] = a2;
+    em_part += sres + strace;
+    a2_part += a2;
   }
   const float s_clip = block_sum((float)clip, red);
+  const float em = block_sum(em_part, red);
+  const float a2s = block_sum(a2_part, red);
   if (threadIdx.x == 0) {
-    float em = 0.f, a2s = 0.f;
-    for (int64_t b = 0; b < rows; ++b) {
-      em += eta2[rows + b];
-      a2s += eta2[2 * rows + b];
-    }
     st->a2_clip = (int)s_clip;
     st->em_mean = em / (float)rows;
     st->a2_mean = a2s / (float)rows;
@@ -256,8 +256,7 @@ __global__ __launch_bounds__(kEW) void lmmse_epi2_kernel(
     const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
     if (j >= n) continue;
     const int64_t o = b * n + j;
-    float d = P[o];
-    for (int s = 1; s < splits; ++s) d = d + P[(int64_t)s * split_stride + o];
+    const float d = sum_splits(P, splits, split_stride, o);
     const float r2v = r2[o];
     const float x2 = r2v + d;
     const float rn = (e2 * x2 - gb * r2v) / gn;
@@ -278,8 +277,7 @@ __global__ __launch_bounds__(kEW) void err_epi_kernel(int64_t n, const float* __
     const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
     if (j >= n) continue;
     const int64_t o = b * n + j;
-    float v = P[o];
-    for (int s = 1; s < splits; ++s) v = v + P[(int64_t)s * split_stride + o];
+    const float v = sum_splits(P, splits, split_stride, o);
     const float d = Yu[o] - v;
     acc += d * d;
   }
@@ -292,15 +290,16 @@ __global__ __launch_bounds__(kEW) void rows_err_kernel(int64_t rows, int nchunks
                                                        const float* __restrict__ part,
                                                        float* __restrict__ out,
                                                        VampStatus* __restrict__ st) {
+  __shared__ float red[kEW / 64];
+  float part_sum = 0.f;  // this thread's rows, in row order
   for (int64_t b = threadIdx.x; b < rows; b += blockDim.x) {
     float v = part[b * nchunks];
     for (int c = 1; c < nchunks; ++c) v = v + part[b * nchunks + c];
     out[b] = v;
+    part_sum += v;
   }
-  __syncthreads();
+  const float s = block_sum(part_sum, red);
   if (threadIdx.x == 0) {
-    float s = 0.f;
-    for (int64_t b = 0; b < rows; ++b) s += out[b];
     st->err_sum = s;
     st->err_mean = s / (float)rows;
   }
