@@ -35,6 +35,22 @@ PEAK_HBM_GBS = 8000.0
 E8_FLOP_PER_VEC = 12334  # factorized search
 
 
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_splitk_128x14336_pmc.md")
+
+
+def pmc_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter on a 1 GiB copy); None if absent."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -118,25 +134,30 @@ def run_layer(rows, cols, module, H_gptq, W, steps, warmup, bits=3):
 
 
 def gemm_roofline(n, device, reps=20):
-    """Live HIP-event timing of the dominant kernel: the rank-space product (128 x n) @ (n x n)."""
+    """Live HIP-event timing of the dominant kernel: the split-K rank-space product
+    (128 x n) @ (n x n) as the VAMP drivers launch it (gemm_f32_full_kernel, partials only;
+    the drivers' epilogues sum the partials).  Events are recorded on the stream the kernel
+    is launched on (torch's current stream)."""
     import torch
 
     from mpq_amd import ops
 
     A = torch.randn(128, n, device=device)
     B = torch.randn(n, n, device=device)
-    out = torch.empty(128, n, device=device)
-    ops.gemm(A, B, out=out)
+    out, splits = ops.gemm_splitk(A, B)
     torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(device)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
+    s.record(stream)
     for _ in range(reps):
-        ops.gemm(A, B, out=out)
-    e.record()
+        ops.gemm_splitk(A, B, splits=splits, out=out)
+    e.record(stream)
     torch.cuda.synchronize()
     ms = s.elapsed_time(e) / reps
     flop = 2.0 * 128 * n * n
-    return {"shape": f"128x{n}x{n}", "ms": ms, "tflops": flop / ms / 1e9}
+    alg_bytes = 4.0 * (128 * n + n * n) + 4.0 * splits * 128 * n
+    return {"shape": f"128x{n}x{n}", "splits": splits, "ms": ms, "tflops": flop / ms / 1e9,
+            "alg_bytes": alg_bytes}
 
 
 def e8p12_bench(device, nvec=1 << 24, reps=10):
@@ -328,6 +349,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gate-up", action="store_true")
     ap.add_argument("--no-e8p12-layer", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the dominant-kernel timing plus a 1 GiB device copy (the PMC scaling reference)")
     ap.add_argument("--tokens", type=int, default=128 * 2048)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -340,6 +363,15 @@ def main():
 
     _lib.load()
     dev = torch.device("cuda:0")
+    if args.roofline_only:
+        rf = gemm_roofline(14336, dev, reps=3)
+        src = torch.ones(256 * 1024 * 1024, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"gemm_roofline": rf, "copy_bytes": 4 * src.numel()}), flush=True)
+        return
     log("== E8P12 search, 2^24 vectors")
     e8 = e8p12_bench(dev)
     log(json.dumps(e8))
@@ -417,12 +449,13 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_f32_kernel (rank-space product 128x14336 @ 14336x14336, split-K)",
+            "kernel": f"gemm_f32_full_kernel (rank-space product 128x14336 @ 14336x14336, split-K {rf['splits']}, "
+                      "partials only, as the VAMP drivers launch it)",
             "achieved": round(rf["tflops"], 2),
             "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(rf["tflops"] / PEAK_FP32_TFLOPS, 4),
-            "traffic": None,
+            "traffic": pmc_traffic(),
         },
         "layer_fp32_tflops": round(down_tflops, 2),
         "layer_roofline_frac": round(down_tflops / PEAK_FP32_TFLOPS, 4),

@@ -5,9 +5,10 @@
  *  - every buffer is caller-allocated device memory, row-major and contiguous
  *    unless a leading dimension is given, fp32 unless stated;
  *  - work is enqueued on `stream` (a hipStream_t; NULL = default stream);
- *    entry points are asynchronous except the two solver drivers
- *    (mpq_uniform_vamp_solve), which read small status blocks back to run the
- *    reference's host-side control flow;
+ *    entry points are asynchronous except the VAMP drivers
+ *    (mpq_uniform_vamp_solve, mpq_e8p12_vamp_solve), which read small status
+ *    blocks back to run the reference's host-side control flow, and
+ *    mpq_e8p12_cd_prepare, which reads back one failure count;
  *  - scratch memory comes from the caller (`workspace`, sized by the matching
  *    *_workspace_size query); no entry point allocates device memory;
  *  - the return value is 0 on success, MPQ_INVALID_ARGUMENT (-1) for a bad
@@ -180,6 +181,17 @@ int mpq_gemm_f32(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, c
                  int64_t ldb, int trans_b, const int32_t* b_rows, float* C, int64_t ldc,
                  float alpha, float beta, float* workspace, int64_t workspace_floats,
                  mpq_stream_t stream);
+
+/*
+ * Split-K partial products P[s] = A[:, Ks] op(B)[Ks, :], s = 0..splits-1, written to
+ * `partials` (splits x M x N, M*N apart): the kernel the VAMP drivers run for their rank-space
+ * products, whose epilogues sum the partials in split order (callers that fuse their own
+ * reduction use it directly).  mpq_gemm_f32_split_count gives the split count the library
+ * uses for an M x N x K product.  Replaces the same torch matmuls as mpq_gemm_f32.
+ */
+int mpq_gemm_f32_split_count(int64_t M, int64_t N, int64_t K);
+int mpq_gemm_f32_splitk(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B,
+                        int64_t ldb, int trans_b, float* partials, int splits, mpq_stream_t stream);
 
 /* out = in^T (rows x cols -> cols x rows). */
 int mpq_transpose(const float* in, int64_t rows, int64_t cols, int64_t ld_in, float* out,

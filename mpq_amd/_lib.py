@@ -43,6 +43,8 @@ SIGNATURES = {
                                     c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
     "mpq_gemm_f32": (c_int, [c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_int, c_ptr,
                              c_ptr, c_i64, c_float, c_float, c_ptr, c_i64, c_ptr]),
+    "mpq_gemm_f32_split_count": (c_int, [c_i64, c_i64, c_i64]),
+    "mpq_gemm_f32_splitk": (c_int, [c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_int, c_ptr, c_int, c_ptr]),
     "mpq_gptq_find_params": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_ptr, c_ptr]),
     "mpq_uniform_rtn": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_int, c_ptr, c_ptr,
                                 c_ptr]),

@@ -494,3 +494,27 @@ extern "C" int mpq_gemm_f32(int64_t M, int64_t N, int64_t K, const float* A, int
                         workspace, workspace_floats, stream));
   return mpq::kOk;
 }
+
+extern "C" int mpq_gemm_f32_split_count(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 1;
+  int bn = 128;
+  return mpq::choose_splits(M, N, K, (int64_t)1 << 62, &bn);
+}
+
+extern "C" int mpq_gemm_f32_splitk(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B,
+                                   int64_t ldb, int trans_b, float* partials, int splits, hipStream_t stream) {
+  MPQ_CHECK_ARG(M > 0 && N > 0 && K > 0, "mpq_gemm_f32_splitk: empty product");
+  MPQ_CHECK_ARG(splits >= 1 && splits <= 32, "mpq_gemm_f32_splitk: splits must be in [1, 32]");
+  MPQ_CHECK_ARG(A && B && partials, "mpq_gemm_f32_splitk: null operand");
+  MPQ_CHECK_ARG(lda >= K && (trans_b ? ldb >= K : ldb >= N), "mpq_gemm_f32_splitk: leading dimension too small");
+  MPQ_CHECK_ARG(M <= (int64_t)65535 * 128, "mpq_gemm_f32_splitk: M too large");
+  int bn = 128;
+  mpq::choose_splits(M, N, K, (int64_t)1 << 62, &bn);
+  mpq::GemmParams p{};
+  p.M = M; p.N = N; p.K = K;
+  p.A = A; p.lda = lda; p.B = B; p.ldb = ldb; p.trans_b = trans_b != 0;
+  p.C = partials; p.ldc = N; p.split_stride = M * N;
+  p.alpha = 1.f; p.beta = 0.f; p.mode = mpq::kGemmPartials;
+  MPQ_HIP_TRY(mpq::gemm_partials(p, splits, bn, stream));
+  return mpq::kOk;
+}

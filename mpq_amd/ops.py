@@ -82,6 +82,25 @@ def gemm(A: torch.Tensor, B: torch.Tensor, *, trans_b: bool = False, b_rows: Opt
 
 # ---- quantizer helpers ----------------------------------------------------
 
+def gemm_splitk(A: torch.Tensor, B: torch.Tensor, *, trans_b: bool = False, splits: Optional[int] = None,
+                out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, int]:
+    """Split-K partial products (splits, M, N) of A op(B); ``splits`` defaults to the library's choice."""
+    dev = _dev(A, B, out)
+    A = _f32c(A)
+    B = _f32c(B)
+    M, K = A.shape
+    N = int(B.shape[0] if trans_b else B.shape[1])
+    lib = _lib.load()
+    s = int(splits) if splits is not None else int(lib.mpq_gemm_f32_split_count(M, N, K))
+    if out is None:
+        out = torch.empty(s, M, N, dtype=F32, device=dev)
+    elif tuple(out.shape) != (s, M, N) or out.dtype != F32 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous fp32 (splits, M, N) tensor")
+    _lib.call("mpq_gemm_f32_splitk", M, N, K, _lib.ptr(A), K, _lib.ptr(B), int(B.shape[1]), int(bool(trans_b)),
+              _lib.ptr(out), s, _stream(dev))
+    return out, s
+
+
 def gptq_find_params(W: torch.Tensor, group_size: int, maxq: int) -> Tuple[torch.Tensor, torch.Tensor]:
     """Asymmetric min-max GPTQ parameters per (row, group): (scale, zero) of shape (rows, G)."""
     dev = _dev(W)
