@@ -244,7 +244,22 @@ int mpq_uniform_rtn(const float* W, int64_t rows, int64_t n, int64_t ldw, const 
                     const float* zero, int64_t group_size, int maxq, uint8_t* q, float* x,
                     mpq_stream_t stream);
 
-/* x = s(q - z) from uint8 codes.  Replaces mpq/priors/uniform.py:302-309. */
+/*
+ * GPTQModel int32 packing of the codes (the step after the solve on the GPTQModel path,
+ * patches/gptqmodel.patch:359-395, scripts/backend_gptq.py:843 format GPTQ_V2):
+ *   q rows x n uint8 codes (rows = out features, n = in features; both % 32 == 0),
+ *   scale/zero rows x G group parameters (G = ceil(n / group_size)), bits in {2, 3, 4, 8};
+ *   outputs qweight int32 [n*bits/32][rows], qzeros int32 [G][rows*bits/32] (format_v1 != 0
+ *   stores zero - 1, else zero), scales fp16 [G][rows], g_idx int32 [n] = i / group_size.
+ * 3-bit values are packed 32 to 3 words (GPTQModel's layout).  Parity with GPTQModel's packer:
+ * the layout is its published one; the packer itself is upstream and absent.
+ */
+int mpq_gptq_pack(const uint8_t* q, const float* scale, const float* zero, int64_t rows, int64_t n,
+                  int64_t group_size, int bits, int format_v1, int32_t* qweight, int32_t* qzeros,
+                  void* scales_fp16, int32_t* g_idx, mpq_stream_t stream);
+
+/* x = s(q - z) from uint8 codes.  Replaces mpq/priors/uniform.py:302-309 and the packed-basis
+ * weight rebuild scale * (q - zero) of patches/gptqmodel.patch:381-391. */
 int mpq_dequant(const uint8_t* q, int64_t rows, int64_t n, const float* scale, const float* zero,
                 int64_t group_size, float* x, mpq_stream_t stream);
 

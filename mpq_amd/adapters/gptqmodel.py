@@ -315,3 +315,57 @@ def run_mpq_quantization(
         "quant_time_s": float(quant_time),
     }
     return Q, q_int, scale_groups, zero_groups, g_idx, float(quant_time), stats
+
+
+def install_internal_hadamard_input_hooks(model: torch.nn.Module, *, rotation_seed: int = 0) -> int:
+    """Forward pre-hooks that rotate each packed module's input into the solver basis
+    (reference ``mpq/adapters/gptqmodel.py:1166-1247``).
+
+    Packed internal-Hadamard weights stay in the solver basis; applying the module's signed block
+    Hadamard (signs from ``stable_seed(f"{name}:full", rotation_seed)``, block = largest power-of-2
+    factor of the input width) to its input reproduces the dense inverse-rotated weight.  Returns
+    the number of modules hooked.  Inputs must be ROCm tensors (the rotation runs on the HIP kernel).
+    """
+    installed = 0
+    for module_name, module in model.named_modules():
+        if not module_name or getattr(module, "_mpq_internal_hadamard_hook", None) is not None:
+            continue
+        if not all(hasattr(module, attr) for attr in ("qweight", "qzeros", "scales")):
+            continue
+        width = int(getattr(module, "in_features", 0) or getattr(module, "infeatures", 0) or 0)
+        if width <= 0:
+            qweight = getattr(module, "qweight", None)
+            bits = int(getattr(module, "bits", 0) or 0)
+            pack_dtype = getattr(qweight, "dtype", torch.int32)
+            pack_bits = (torch.iinfo(pack_dtype).bits
+                         if isinstance(pack_dtype, torch.dtype) and not pack_dtype.is_floating_point else 32)
+            if isinstance(qweight, torch.Tensor) and bits > 0:
+                width = int(qweight.shape[0]) * int(pack_bits // bits)
+        if width <= 0:
+            raise RuntimeError(f"Cannot determine MPQ input width for quantized module {module_name!r}")
+        mode, block_dim = resolve_block_hadamard_plan(width)
+        if mode == "none":
+            continue
+        signs_by_device: Dict[torch.device, torch.Tensor] = {}
+
+        def _rotate_input(_module, args, *, _name=module_name, _width=width, _block_dim=block_dim,
+                          _cache=signs_by_device):
+            if not args or not isinstance(args[0], torch.Tensor):
+                return args
+            value = args[0]
+            if int(value.shape[-1]) != int(_width):
+                raise RuntimeError(
+                    f"MPQ input width mismatch for {_name!r}: expected {_width}, got {int(value.shape[-1])}")
+            signs = _cache.get(value.device)
+            if signs is None:
+                signs = sample_rademacher_signs(width=int(_width), key=f"{_name}:full", seed=int(rotation_seed),
+                                                device=value.device, dtype=torch.float32)
+                _cache[value.device] = signs
+            flat = value.reshape(-1, int(_width)).to(torch.float32).contiguous()
+            rotated = apply_right_block_hadamard(flat, signs=signs, had_dim=int(_block_dim))
+            return (rotated.reshape(value.shape).to(dtype=value.dtype), *args[1:])
+
+        handle = module.register_forward_pre_hook(_rotate_input)
+        setattr(module, "_mpq_internal_hadamard_hook", handle)
+        installed += 1
+    return installed

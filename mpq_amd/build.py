@@ -35,6 +35,7 @@ HIP_SOURCES = [
     "e8p12_vamp.hip",
     "cd_uniform.hip",
     "e8p12_cd.hip",
+    "gptq_pack.hip",
 ]
 CXX_SOURCES = [
     "errors.cpp",
