@@ -245,6 +245,17 @@ int mpq_uniform_rtn(const float* W, int64_t rows, int64_t n, int64_t ldw, const 
                     mpq_stream_t stream);
 
 /*
+ * Per-linear Hessian accumulation H = beta H + alpha X^T X (both triangles, exactly symmetric)
+ * and optionally colsum += column sums of X: the step before the solve, GPTQModel's add_batch
+ * (H = 2/m sum x x^T, mpq/adapters/gptqmodel.py:39) and QUIP#'s Hessian hooks
+ * (mpq/quip_generic.py:823-921: sum x x^T and sum x, finalised as H/ct - mu mu^T).
+ *   X: T x n activations (ldx >= n, ldx % 4 == 0), fp32 (x_bf16 = 0) or bf16 (x_bf16 = 1);
+ *   n % 128 == 0; H: n x n fp32 (ldh).  fp32 MFMA SYRK (tiles on/above the diagonal).
+ */
+int mpq_hessian_accumulate(const void* X, int x_bf16, int64_t T, int64_t n, int64_t ldx, float alpha,
+                           float beta, float* H, int64_t ldh, float* colsum, mpq_stream_t stream);
+
+/*
  * GPTQModel int32 packing of the codes (the step after the solve on the GPTQModel path,
  * patches/gptqmodel.patch:359-395, scripts/backend_gptq.py:843 format GPTQ_V2):
  *   q rows x n uint8 codes (rows = out features, n = in features; both % 32 == 0),

@@ -36,6 +36,7 @@ HIP_SOURCES = [
     "cd_uniform.hip",
     "e8p12_cd.hip",
     "gptq_pack.hip",
+    "hessian.hip",
 ]
 CXX_SOURCES = [
     "errors.cpp",
