@@ -245,6 +245,26 @@ int mpq_uniform_rtn(const float* W, int64_t rows, int64_t n, int64_t ldw, const 
                     mpq_stream_t stream);
 
 /*
+ * AWQ scale search for one linear (or linears sharing an input), the step before the solve:
+ * mpq/awq_scale.py:491-580 (_search_best_scale) scored, for a single linear layer, by the
+ * output error  sum_rows D H D^T / rows  (D = W - pseudo_quant(W s)/s, H = X^T X / T), with
+ * _compute_w_mean (:49-83), _candidate_scales (:338-348), _pseudo_quantize_tensor_into
+ * (:108-157), 20 ratios k/20, first minimum wins.
+ *   mpq_awq_w_mean: w_sum[j] += sum_rows |W[r][j]| / (group abs-max + 1e-6) (divide by the
+ *     total row count for w_mean); workspace >= rows * n/group_size floats.
+ *   mpq_awq_search: W rows x n, H n x n, x_mean n (mean |x|), w_mean n; outputs best_scales (n,
+ *     device), losses_out (20, device, optional), best_error / best_ratio (host pointers,
+ *     optional).  Synchronises `stream` once.  n % group_size == 0.
+ */
+int64_t mpq_awq_workspace_size(int64_t rows, int64_t n);
+int mpq_awq_w_mean(const float* W, int64_t rows, int64_t n, int64_t group_size, float* w_sum,
+                   void* workspace, int64_t workspace_bytes, mpq_stream_t stream);
+int mpq_awq_search(const float* W, int64_t rows, int64_t n, const float* H, const float* x_mean,
+                   const float* w_mean, int64_t group_size, int bits, int sym, float* best_scales,
+                   float* losses_out, float* best_error, float* best_ratio, void* workspace,
+                   int64_t workspace_bytes, mpq_stream_t stream);
+
+/*
  * Per-linear Hessian accumulation H = beta H + alpha X^T X (both triangles, exactly symmetric)
  * and optionally colsum += column sums of X: the step before the solve, GPTQModel's add_batch
  * (H = 2/m sum x x^T, mpq/adapters/gptqmodel.py:39) and QUIP#'s Hessian hooks

@@ -48,6 +48,10 @@ SIGNATURES = {
     "mpq_gptq_find_params": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_ptr, c_ptr]),
     "mpq_uniform_rtn": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_int, c_ptr, c_ptr,
                                 c_ptr]),
+    "mpq_awq_workspace_size": (c_i64, [c_i64, c_i64]),
+    "mpq_awq_w_mean": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_ptr]),
+    "mpq_awq_search": (c_int, [c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_int, c_int, c_ptr, c_ptr, c_ptr,
+                               c_ptr, c_ptr, c_i64, c_ptr]),
     "mpq_hessian_accumulate": (c_int, [c_ptr, c_int, c_i64, c_i64, c_i64, c_float, c_float, c_ptr, c_i64, c_ptr,
                                        c_ptr]),
     "mpq_gptq_pack": (c_int, [c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_int, c_int, c_ptr, c_ptr, c_ptr, c_ptr,

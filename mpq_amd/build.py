@@ -37,6 +37,7 @@ HIP_SOURCES = [
     "e8p12_cd.hip",
     "gptq_pack.hip",
     "hessian.hip",
+    "awq.hip",
 ]
 CXX_SOURCES = [
     "errors.cpp",
