@@ -369,3 +369,121 @@ def install_internal_hadamard_input_hooks(model: torch.nn.Module, *, rotation_se
         setattr(module, "_mpq_internal_hadamard_hook", handle)
         installed += 1
     return installed
+
+
+@torch.inference_mode()
+def postprocess_gptq_quantization(
+    *,
+    W: torch.Tensor,
+    H: torch.Tensor,
+    Q_init: torch.Tensor,
+    scale_groups: torch.Tensor,
+    zero_groups: torch.Tensor,
+    g_idx: torch.Tensor,
+    qcfg: Any,
+    module_name: str,
+    adapter_cfg: GPTQAdapterConfig = GPTQAdapterConfig(),
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, float, Dict[str, Any]]:
+    """Greedy-CD polish of a finished GPTQ result (reference ``mpq/adapters/gptqmodel.py:1250-1470``).
+
+    The codes ``round(Q_init / s + z)`` are polished in the rank space of ``hessian_scale * H`` with
+    one greedy order over all rows, each row keeps the polished codes only if its error drops, and
+    the module falls back to ``Q_init`` when the mean error would rise (fail-closed).  Only the
+    contiguous group layout (``g_idx[i] = i // group_size``, no act-order) is provided.
+    Returns ``(Q, q_int, scale_groups, zero_groups, g_idx, time_s, stats)``.
+    """
+    start = time.time()
+    if not W.is_cuda:
+        raise ValueError(f"W must be on a ROCm device (got {W.device}); mpq_amd has no CPU path.")
+    device = W.device
+    W = W.to(torch.float32).contiguous()
+    H = H.to(device=device, dtype=torch.float32)
+    Q_init = Q_init.to(device=device, dtype=torch.float32).contiguous()
+    scale_groups = scale_groups.to(device=device, dtype=torch.float32).contiguous()
+    zero_groups = zero_groups.to(device=device, dtype=torch.float32).contiguous()
+    g_idx = g_idx.to(device=device, dtype=torch.int32)
+    bits = int(getattr(qcfg, "bits"))
+    maxq = int(2 ** bits - 1)
+    rows, cols = W.shape
+    group_size = int(getattr(qcfg, "group_size", cols) or cols)
+    if group_size <= 0:
+        group_size = cols
+    expected = torch.arange(cols, device=device, dtype=torch.int32) // group_size
+    if int(g_idx.numel()) != cols or not bool(torch.equal(g_idx, expected)):
+        raise ValueError("mpq_amd postprocess supports the contiguous group layout (g_idx = i // group_size) only.")
+    mpq_cfg = getattr(qcfg, "mpq", None)
+    H_work = float(adapter_cfg.hessian_scale) * H
+    _, S, V, Vs, eigen_floor = vamp_hessian_eigen(H_work, jitter_base=adapter_cfg.jitter_base,
+                                                  floor_scale=adapter_cfg.eigen_floor_scale)
+    q_init, _ = ops.uniform_rtn(Q_init, scale_groups.clamp_min(1e-12), zero_groups, group_size, maxq, want_x=False)
+    polish_mode = str(getattr(mpq_cfg, "polish_mode", "none") or "none").strip().lower()
+    polish_sweeps = int(getattr(mpq_cfg, "polish_sweeps", 0) or 0)
+    mode = _resolve_polish_mode(sweeps=polish_sweeps, mode=polish_mode)
+    if mode == "topk_block_cd":
+        raise ValueError("mpq_amd implements polish_mode='block_cd'; topk_block_cd is not provided.")
+    Yu = ops.gemm(W, Vs)
+
+    def _err(x):
+        return (Yu - ops.gemm(x, Vs)).square().sum(dim=1)
+
+    err_before = _err(Q_init)
+    delta0 = W - Q_init
+    raw_before = (ops.gemm(delta0, H_work) * delta0).sum(dim=1)
+    polish_updates = 0.0
+    if mode == "block_cd":
+        q_pol, eb, ea, imp, acc = ops.uniform_cd_polish(None, q_init, scale_groups, zero_groups, group_size, maxq,
+                                                        Vs, H_work, block_rows=rows, sweeps=polish_sweeps,
+                                                        select=True, Yu=Yu, x_in=Q_init)
+        err_after = ea
+        polish_updates = float(acc.sum().item())
+        q_final = q_pol
+        Q_final = torch.where(imp.bool().unsqueeze(1), ops.dequant(q_pol, scale_groups, zero_groups, group_size),
+                              Q_init)
+    else:
+        err_after = err_before
+        q_final = q_init
+        Q_final = Q_init
+    err_final = _err(Q_final)
+    before_mean = float(err_before.mean().item())
+    final_mean = float(err_final.mean().item())
+    fail_closed = (not bool(torch.isfinite(err_final).all().item())) or (final_mean > before_mean + 1e-9)
+    if fail_closed:
+        Q_final, q_final, err_final, final_mean = Q_init, q_init, err_before, before_mean
+    delta = W - Q_final
+    raw_final = (ops.gemm(delta, H_work) * delta).sum(dim=1)
+    stats: Dict[str, Any] = {
+        "method": "mpq",
+        "solver": "gptq",
+        "polish_mode": mode,
+        "module": str(module_name),
+        "bits": bits,
+        "group_size": group_size,
+        "rows": int(rows),
+        "cols": int(cols),
+        "rank": int(S.numel()),
+        "eigen_floor": float(eigen_floor),
+        "block_rows": int(rows),
+        "polish_sweeps": int(polish_sweeps),
+        "rankspace_error_mean_before": before_mean,
+        "rankspace_error_mean_after": float(err_after.mean().item()),
+        "rankspace_error_mean_final": final_mean,
+        "raw_objective_mean_before": float(raw_before.mean().item()),
+        "raw_objective_mean_final": float(raw_final.mean().item()),
+        "polish_gain": float((err_before - err_after).mean().item()),
+        "polish_updates": polish_updates,
+        "polish_assignment_changes": int((q_final != q_init).sum().item()),
+        "polish_assignments_total": int(q_init.numel()),
+        "block_cd_backend": "hip",
+        "module_fail_closed": bool(fail_closed),
+        "quant_time_s": float(time.time() - start),
+    }
+    if mpq_cfg is not None:
+        bucket = getattr(mpq_cfg, "_layer_stats", None)
+        if not isinstance(bucket, list):
+            bucket = []
+            try:
+                setattr(mpq_cfg, "_layer_stats", bucket)
+            except Exception:  # frozen configs
+                pass
+        bucket.append(stats)
+    return Q_final, q_final.to(torch.int32), scale_groups, zero_groups, g_idx, float(time.time() - start), stats

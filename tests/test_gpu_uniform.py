@@ -217,3 +217,46 @@ def test_adapter_device_eigh(gpu, rotation):
     assert st["proxy_loss"] < 0.9 * proxy_rtn
     # Q is the inverse rotation of the dequantised codes
     assert _rel(Q.cpu(), ref["Q"]) < 0.2
+
+
+def test_postprocess_gptq_polish_matches_oracle(gpu):
+    """postprocess_gptq_quantization (mpq/adapters/gptqmodel.py:1250-1470): one greedy order over all
+    rows, keep-if-better per row, module fail-closed; against the oracle's scalar CD."""
+    from mpq_amd.adapters.gptqmodel import postprocess_gptq_quantization
+
+    rows, n, gs, bits = 96, 256, 128, 3
+    maxq = 2 ** bits - 1
+    W, H = make_layer(rows, n, tokens=1024, seed_key="post:gptq")
+    sg, zg = ou.gptq_find_params(W.reshape(-1, gs), maxq)
+    sg, zg = sg.reshape(rows, n // gs), zg.reshape(rows, n // gs)
+    sf, zf = sg.repeat_interleave(gs, 1), zg.repeat_interleave(gs, 1)
+    Q0 = sf * (torch.clamp(torch.round(W / sf) + zf, 0, maxq) - zf)
+
+    class Q:
+        pass
+
+    qcfg = Q()
+    qcfg.bits, qcfg.group_size = bits, gs
+    qcfg.mpq = Q()
+    qcfg.mpq.polish_mode, qcfg.mpq.polish_sweeps = "block_cd", 3
+    g_idx = torch.arange(n, dtype=torch.int32) // gs
+    Qf, qf, _, _, _, _, st = postprocess_gptq_quantization(W=W.to(gpu), H=(2.0 * H).to(gpu), Q_init=Q0.to(gpu),
+                                                           scale_groups=sg.to(gpu), zero_groups=zg.to(gpu),
+                                                           g_idx=g_idx.to(gpu), qcfg=qcfg, module_name="m")
+    # oracle: same eigenbasis, scalar greedy CD over all rows, keep-if-better
+    lam, V, _ = ou.hessian_eigen(H)
+    Vs = V * torch.sqrt(lam).unsqueeze(0)
+    Yu = W.matmul(Vs)
+    x_pol, _ = ou.scalar_greedy_cd(Q0, Yu, Vs, H, sf, zf, maxq, 3)
+    e0 = ou.rankspace_error(Yu, Q0, Vs)
+    e1 = ou.rankspace_error(Yu, x_pol, Vs)
+    ref = torch.where((e1 + 1e-12 < e0).unsqueeze(1), x_pol, Q0)
+    e_ref = ou.rankspace_error(Yu, ref, Vs)
+    got = Qf.cpu()
+    e_got = ou.rankspace_error(Yu, got, Vs)
+    assert float(e_got.mean()) <= float(e0.mean()) + 1e-6
+    assert abs(float(e_got.mean()) - float(e_ref.mean())) <= 5e-3 * float(e_ref.mean())
+    agree = float((got == ref).float().mean())
+    assert agree >= 0.98, agree
+    assert not st["module_fail_closed"] and st["polish_updates"] > 0
+    assert torch.equal(got, sf * (qf.cpu().float() - zf))
