@@ -207,6 +207,18 @@ int mpq_transpose(const float* in, int64_t rows, int64_t cols, int64_t ld_in, fl
 int mpq_eigh_postprocess(const float* lam_asc, const float* V_asc, int64_t n, float floor_v,
                          float* lam, float* S, float* V, float* Vs, mpq_stream_t stream);
 
+/*
+ * Symmetric eigendecomposition of H (n x n, fp32): lam ascending (n) and V (n x n, row-major,
+ * column k = eigenvector k), the torch.linalg.eigh call of mpq/adapters/gptqmodel.py:276-310.
+ * rocSOLVER ssytrd + sstedc, then the back-transformation V = Q Z as blocked compact-WY
+ * updates on this library's fp32 MFMA GEMM.  workspace: mpq_syevd_workspace_size(n) bytes
+ * (rocSOLVER may also use its handle's own device memory).  Synchronises `stream` once;
+ * MPQ_NUMERICAL_ERROR when the tridiagonal solver does not converge.
+ */
+int64_t mpq_syevd_workspace_size(int64_t n);
+int mpq_syevd(int64_t n, const float* H, float* lam, float* V, void* workspace, int64_t workspace_bytes,
+              mpq_stream_t stream);
+
 /* out[i][j] = in[i][j] * scale[j] (Vs = V * S, mpq/adapters/gptqmodel.py:890). */
 int mpq_scale_columns(const float* in, int64_t rows, int64_t cols, const float* scale, float* out,
                       mpq_stream_t stream);

@@ -6,8 +6,9 @@ Drop-in for the reference's ``mpq/adapters/gptqmodel.py``:
 * ``run_mpq_quantization``       reference :650-1163 (``solver="vamp"`` path)
 
 Pipeline (all on the ROCm device):
-  H <- hessian_scale * H; eigh of the unrotated H (rocSOLVER through
-  ``torch.linalg.eigh``) -> ``mpq_eigh_postprocess`` (floor, descending order,
+  H <- hessian_scale * H; eigh of the unrotated H (``mpq_syevd``: rocSOLVER
+  tridiagonalisation and divide and conquer, compact-WY back-transformation on
+  the library's MFMA GEMM) -> ``mpq_eigh_postprocess`` (floor, descending order,
   S, Vs); internal block-Hadamard rotation of W, H (both sides) and V
   (``mpq_block_hadamard``); GPTQ group parameters (``quantizer.find_params`` if a
   quantizer is given, else ``mpq_gptq_find_params``); RTN (``mpq_uniform_rtn``);
@@ -92,7 +93,7 @@ def vamp_hessian_eigen(H: torch.Tensor, *, jitter_base: float = 1e-6, floor_scal
     Hs = 0.5 * (H + H.T)
     if not bool(torch.isfinite(Hs).all()):
         Hs = torch.nan_to_num(Hs, nan=0.0, posinf=0.0, neginf=0.0)
-    lam_asc, V_asc = torch.linalg.eigh(Hs)
+    lam_asc, V_asc = ops.syevd(Hs)
     max_lam = float(lam_asc[-1].item()) if lam_asc.numel() else 0.0
     diag_mean = float(torch.diagonal(Hs).mean().abs().item()) if Hs.numel() else 0.0
     floor = max(float(jitter_base), float(floor_scale) * max(diag_mean, max_lam, 1e-12))

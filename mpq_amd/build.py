@@ -26,6 +26,8 @@ BUILD_DIR = os.path.join(HERE, "_build")
 LIB_NAME = "libmpq_amd.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
+ROCM_LIB = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
+
 HIP_SOURCES = [
     "e8p12_map.hip",
     "e8p12_posterior.hip",
@@ -38,6 +40,7 @@ HIP_SOURCES = [
     "gptq_pack.hip",
     "hessian.hip",
     "awq.hip",
+    "eigh.hip",
 ]
 CXX_SOURCES = [
     "errors.cpp",
@@ -92,7 +95,8 @@ def build(verbose: bool = False, jobs: int = 8) -> str:
             if verbose and out:
                 print(out)
     tmp = LIB_PATH + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-L", ROCM_LIB,
+          "-Wl,-rpath," + ROCM_LIB, "-lrocsolver", "-lrocblas"])
     shutil.move(tmp, LIB_PATH)
     return LIB_PATH
 

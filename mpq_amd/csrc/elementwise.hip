@@ -256,6 +256,13 @@ hipError_t argsort_desc_rows(const float* keys, int64_t nrows, int64_t n, int32_
   return hipGetLastError();
 }
 
+hipError_t transpose_matrix(const float* in, int64_t rows, int64_t cols, int64_t ld_in, float* out,
+                            int64_t ld_out, hipStream_t stream) {
+  hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32)),
+                     dim3(256), 0, stream, in, rows, cols, ld_in, out, ld_out);
+  return hipGetLastError();
+}
+
 hipError_t row_sqnorm(const float* M, int64_t n, int64_t ld, float floor_v, float* out,
                       hipStream_t stream) {
   hipLaunchKernelGGL(row_sqnorm_kernel, dim3((unsigned)n), dim3(256), 0, stream, M, n, ld, floor_v, out);
@@ -329,9 +336,7 @@ extern "C" int mpq_transpose(const float* in, int64_t rows, int64_t cols, int64_
   if (rows == 0 || cols == 0) return kOk;
   MPQ_CHECK_ARG(in && out && in != out && ld_in >= cols && ld_out >= rows, "mpq_transpose: bad pointer/ld");
   MPQ_CHECK_ARG((rows + 31) / 32 <= 65535, "mpq_transpose: too many rows");
-  hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32)),
-                     dim3(256), 0, stream, in, rows, cols, ld_in, out, ld_out);
-  MPQ_LAUNCH_CHECK();
+  MPQ_HIP_TRY(transpose_matrix(in, rows, cols, ld_in, out, ld_out, stream));
   return kOk;
 }
 

@@ -14,6 +14,10 @@ hipError_t dequant_groups(const uint8_t* q, const float* scale, const float* zer
 hipError_t argsort_desc_rows(const float* keys, int64_t nrows, int64_t n, int32_t* order,
                              hipStream_t stream);
 
+// out = in^T (rows x cols -> cols x rows), tiled through LDS.
+hipError_t transpose_matrix(const float* in, int64_t rows, int64_t cols, int64_t ld_in, float* out,
+                            int64_t ld_out, hipStream_t stream);
+
 // out[j] = max(sum_k M[j][k]^2, floor) for an n x n matrix (row-major).
 hipError_t row_sqnorm(const float* M, int64_t n, int64_t ld, float floor, float* out,
                       hipStream_t stream);

@@ -177,6 +177,21 @@ def scale_columns(X: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def syevd(H: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Eigendecomposition of a symmetric fp32 matrix: (lam ascending, V with eigenvectors as columns)."""
+    dev = _dev(H)
+    H = _f32c(H)
+    n = int(H.shape[0])
+    if tuple(H.shape) != (n, n):
+        raise ValueError("H must be square")
+    lib = _lib.load()
+    ws = workspace(int(lib.mpq_syevd_workspace_size(n)), dev)
+    lam = torch.empty(n, dtype=F32, device=dev)
+    V = torch.empty(n, n, dtype=F32, device=dev)
+    _lib.call("mpq_syevd", n, _lib.ptr(H), _lib.ptr(lam), _lib.ptr(V), _lib.ptr(ws), int(ws.numel()), _stream(dev))
+    return lam, V
+
+
 def eigh_postprocess(lam_asc: torch.Tensor, V_asc: torch.Tensor, floor: float):
     """(lam, S, V, Vs): descending order, floored eigenvalues, S = sqrt(lam), Vs = V * S."""
     dev = _dev(lam_asc, V_asc)
