@@ -1,14 +1,23 @@
 // Symmetric eigendecomposition for the rank-space solvers (gfx950).
 //
-// Replaces the torch.linalg.eigh call of mpq/adapters/gptqmodel.py:276-310 (and the fp32 use of
-// mpq/adapters/quip_sharp.py:33-67) with:
-//   1. rocSOLVER ssytrd (lower): A = Q T Q^T, T tridiagonal, Q = H(0) H(1) ... H(n-2) stored as
-//      LAPACK reflectors (column-major view of the symmetric buffer);
+// Replaces the torch.linalg.eigh call of mpq/adapters/gptqmodel.py:276-310 with:
+//   1. tridiagonalisation A = Q T Q^T (LAPACK sytrd, lower, blocked as latrd + syr2k) written for
+//      this device: per reflector one half-storage symv kernel over the trailing matrix (only
+//      64 x 64 tiles on or below the diagonal are read, each tile contributing A_t v and A_t^T v,
+//      partial sums kept per tile so the result is deterministic) and one kernel that finishes
+//      w = tau (A v - V W^T v - W V^T v) - tau/2 (w.v) v, applies the panel's lazy update to the
+//      next column and forms the partial norms of the next reflector; every 32 reflectors the
+//      trailing matrix takes the rank-64 update A -= V W^T + W V^T on the MFMA GEMM;
 //   2. rocSOLVER sstedc (divide and conquer): T = Z diag(lam) Z^T, eigenvalues ascending;
 //   3. back-transformation V = Q Z on fp32 MFMA GEMMs: the reflectors are applied in blocks of
 //      kNB as compact-WY factors I - Y Tb Y^T (Tb from the block's gram Y^T Y, LAPACK larft
-//      forward/columnwise), last block first: two GEMMs per block instead of rocSOLVER's ormtr.
+//      forward/columnwise), last block first.
 // Output: lam ascending (n), V (n x n, row-major, column k = eigenvector k), as torch.linalg.eigh.
+//
+// Storage: the symmetric matrix is kept in full (both triangles) in a zero-padded row-major
+// buffer with leading dimension lda = n rounded up to 64, so every tile load is 16-byte aligned.
+// Reflector i (LAPACK's H(i) = I - tau_i v_i v_i^T, v_i[0..i] = 0, v_i[i+1] = 1) is stored in
+// row i, entries i+2..n-1 -- by symmetry the same entries LAPACK's lower storage keeps in column i.
 #include <rocblas/rocblas.h>
 #include <rocsolver/rocsolver.h>
 
@@ -21,15 +30,377 @@
 namespace mpq {
 namespace {
 
-constexpr int kNB = 128;  // reflectors per compact-WY block
+constexpr int kNB = 128;  // reflectors per compact-WY block of the back-transformation
+constexpr int kPB = 32;   // reflectors per tridiagonalisation panel (latrd block)
+constexpr int kTB = 64;   // symv tile edge
+constexpr int kCH = 8;    // symv tiles per work-group (one chunk of a column strip)
+constexpr int kThr = 256;
+constexpr int kSub = 8;               // finish_kernel lanes per matrix row
+constexpr int kRowsPB = kThr / kSub;  // finish_kernel rows per work-group
+constexpr int kDotWG = 32;                      // symv work-groups that form the dots p, q
+constexpr int kDotPerWave = (2 * kPB + 3) / 4;  // dots per wave of a dot work-group
 
 inline int64_t a64(int64_t v) { return (v + 63) / 64 * 64; }
 
+// ---- tridiagonalisation ----------------------------------------------------------------------
+
+struct Reflector {
+  float tau, beta, scale;
+};
+
+// LAPACK larfg on (alpha, x): beta = -sign(alpha) sqrt(alpha^2 + |x|^2), tau = (beta - alpha) / beta,
+// v = [1, x / (alpha - beta)]; |x| = 0 gives tau = 0, beta = alpha.  |x|^2 arrives as per-block
+// partial sums, added here in a fixed order (every work-group gets the same bits).
+__device__ Reflector reflector_of(float alpha, const float* __restrict__ Pn, int npn, float* red) {
+  float s = 0.f;
+  for (int k = threadIdx.x; k < npn; k += blockDim.x) s += Pn[k];
+  const float xn2 = block_sum(s, red);
+  Reflector r;
+  if (xn2 == 0.f) {
+    r.tau = 0.f;
+    r.beta = alpha;
+    r.scale = 0.f;
+  } else {
+    const float beta = -copysignf(sqrtf(alpha * alpha + xn2), alpha);
+    r.tau = (beta - alpha) / beta;
+    r.beta = beta;
+    r.scale = 1.f / (alpha - beta);
+  }
+  return r;
+}
+
+// First column c of a panel: D[c] = A[c][c], alpha_c = A[c][c+1] and the partial sums of
+// A[c][g]^2 for g >= c+2 (one per work-group; thread g = c + 256 blockIdx + tid).
+__global__ __launch_bounds__(kThr) void panel_start_kernel(const float* __restrict__ A, int64_t lda, int64_t n,
+                                                          int64_t c, float* __restrict__ D, float* __restrict__ alph,
+                                                          float* __restrict__ Pn) {
+  __shared__ float red[kThr / 64];
+  const int64_t g = c + (int64_t)blockIdx.x * kThr + threadIdx.x;
+  float sq = 0.f;
+  if (g < n) {
+    const float a = A[c * lda + g];
+    if (g == c) D[c] = a;
+    if (g == c + 1) alph[c] = a;
+    if (g >= c + 2) sq = a * a;
+  }
+  const float t = block_sum(sq, red);
+  if (threadIdx.x == 0) Pn[blockIdx.x] = t;
+}
+
+// Half-storage symv over the trailing matrix A[c+1:, c+1:] (as of the panel start) with the
+// reflector v of column c, plus the dots p = W_j^T v and q = V_j^T v of the panel's earlier
+// reflectors j < i (an extra row of kDotWG work-groups).  Tiles are 64 x 64 in global coordinates (rows/cols below c+1 are masked by
+// v = 0).  Work-group (x, y) takes column strip bj = b0 + x and row tiles bi = bj + 8y .. +7:
+//   Pr[bj][rows of bi] = A_(bi,bj) v_bj          (row contributions, one value per tile row)
+//   Pc[bj][y][64]      = sum_{bi > bj} A_(bi,bj)^T v_bi   (column contributions of the chunk)
+//   Pvv[y][bj]         = sum v_bi^T A_(bi,bj) v_bj (x2 off the diagonal)
+//   Ppq[x][64]         = dot work-group x's share of p (slots 0..i-1) and q (slots 32..32+i-1)
+// Thread layout over a tile: column quad cq = tid % 16 (4 columns), rows r0 + 16k, r0 = tid / 16.
+__global__ __launch_bounds__(kThr) void symv_kernel(const float* __restrict__ A, int64_t lda, int64_t n, int64_t c,
+                                                   int64_t i0, int i, const float* __restrict__ alph,
+                                                   const float* __restrict__ Pn, int npn,
+                                                   const float* __restrict__ Wb, float* __restrict__ Pr,
+                                                   float* __restrict__ Pc, float* __restrict__ Pvv,
+                                                   float* __restrict__ Ppq, int ch_alloc) {
+  const int nblk = (int)(lda / kTB);
+  const int b0 = (int)((c + 1) / kTB);
+  if ((int)blockIdx.y == (int)gridDim.y - 1) {
+    // dot work-groups: x < kDotWG takes strips b0 + x, b0 + x + kDotWG, ...; wave w the dots
+    // d = w, w + 4, ... (d < i: p_d = W_d . v; i <= d < 2i: q_{d-i} = V_{d-i} . v), lane = entry
+    if ((int)blockIdx.x >= kDotWG) return;
+    __shared__ float red0[kThr / 64];
+    const Reflector R0 = reflector_of(alph[c], Pn, npn, red0);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    float acc[kDotPerWave];
+#pragma unroll
+    for (int t = 0; t < kDotPerWave; ++t) acc[t] = 0.f;
+    for (int sx = b0 + (int)blockIdx.x; sx < nblk; sx += kDotWG) {
+      const int64_t g = (int64_t)sx * kTB + lane;
+      float v = 0.f;
+      if (g == c + 1) v = 1.f;
+      else if (g > c + 1 && g < n) v = A[c * lda + g] * R0.scale;
+      float x[kDotPerWave];
+#pragma unroll
+      for (int t = 0; t < kDotPerWave; ++t) {
+        const int d = w + 4 * t;
+        const int j = d < i ? d : d - i;
+        x[t] = d < 2 * i ? (d < i ? Wb[(int64_t)j * lda + g] : A[(i0 + j) * lda + g]) : 0.f;
+      }
+#pragma unroll
+      for (int t = 0; t < kDotPerWave; ++t) acc[t] += x[t] * v;
+    }
+#pragma unroll
+    for (int t = 0; t < kDotPerWave; ++t) {
+      const int d = w + 4 * t;
+      const float tot = wave_sum(acc[t]);
+      if (lane == 0 && d < 2 * i) Ppq[(int64_t)blockIdx.x * 64 + (d < i ? d : kPB + d - i)] = tot;
+    }
+    return;
+  }
+  const int bj = b0 + (int)blockIdx.x;
+  const int ch = (int)blockIdx.y;
+  const int bi_first = bj + ch * kCH;
+  if (bi_first >= nblk) return;  // uniform over the work-group, before any barrier
+  const int bi_end = min(bi_first + kCH, nblk);
+  __shared__ float red[kThr / 64];
+  __shared__ float sv[(kCH + 1) * kTB];
+  __shared__ float scol[16][kTB + 1];
+  const Reflector R = reflector_of(alph[c], Pn, npn, red);
+  const int nseg = 1 + bi_end - bi_first;
+  for (int t = threadIdx.x; t < nseg * kTB; t += kThr) {
+    const int seg = t / kTB, off = t % kTB;
+    const int64_t g = (int64_t)(seg == 0 ? bj : bi_first + seg - 1) * kTB + off;
+    float v = 0.f;
+    if (g == c + 1) v = 1.f;
+    else if (g > c + 1 && g < n) v = A[c * lda + g] * R.scale;
+    sv[t] = v;
+  }
+  __syncthreads();
+  const int cq = threadIdx.x & 15, r0 = threadIdx.x >> 4;
+  float vc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) vc[u] = sv[4 * cq + u];
+  float cacc[4] = {0.f, 0.f, 0.f, 0.f};
+  float vav = 0.f;
+  const float* colbase = A + (int64_t)bj * kTB + 4 * cq;
+  float4 cur[4], nxt[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    cur[k] = *reinterpret_cast<const float4*>(colbase + ((int64_t)bi_first * kTB + r0 + 16 * k) * lda);
+  for (int bi = bi_first; bi < bi_end; ++bi) {
+    if (bi + 1 < bi_end) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        nxt[k] = *reinterpret_cast<const float4*>(colbase + ((int64_t)(bi + 1) * kTB + r0 + 16 * k) * lda);
+    }
+    const float* svr = sv + kTB * (1 + bi - bi_first);
+    float rs[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) rs[k] = cur[k].x * vc[0] + cur[k].y * vc[1] + cur[k].z * vc[2] + cur[k].w * vc[3];
+    if (bi != bj) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float vr = svr[r0 + 16 * k];
+        cacc[0] += cur[k].x * vr;
+        cacc[1] += cur[k].y * vr;
+        cacc[2] += cur[k].z * vr;
+        cacc[3] += cur[k].w * vr;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+      for (int off = 8; off >= 1; off >>= 1) rs[k] += __shfl_xor(rs[k], off, 64);
+    }
+    if (cq == 0) {
+      const float wgt = bi == bj ? 1.f : 2.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int rr = r0 + 16 * k;
+        Pr[(int64_t)bj * lda + (int64_t)bi * kTB + rr] = rs[k];
+        vav += wgt * rs[k] * svr[rr];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) cur[k] = nxt[k];
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) scol[r0][4 * cq + u] = cacc[u];
+  const float vtot = block_sum(vav, red);  // contains the barrier that publishes scol
+  if (threadIdx.x < kTB) {
+    float s = 0.f;
+    for (int r = 0; r < 16; ++r) s += scol[r][threadIdx.x];
+    Pc[((int64_t)bj * ch_alloc + ch) * kTB + threadIdx.x] = s;
+  }
+  if (threadIdx.x == 0) Pvv[(int64_t)ch * nblk + bj] = vtot;
+}
+
+// Deterministic work-group sums of three values at once (one set of barriers).
+__device__ __forceinline__ void block_sum3(float& a, float& b, float& c, float (*scratch)[kThr / 64]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  a = wave_sum(a);
+  b = wave_sum(b);
+  c = wave_sum(c);
+  __syncthreads();
+  if (lane == 0) {
+    scratch[0][wave] = a;
+    scratch[1][wave] = b;
+    scratch[2][wave] = c;
+  }
+  __syncthreads();
+  a = scratch[0][0];
+  b = scratch[1][0];
+  c = scratch[2][0];
+  for (int w = 1; w < kThr / 64; ++w) {
+    a += scratch[0][w];
+    b += scratch[1][w];
+    c += scratch[2][w];
+  }
+}
+
+// Finish reflector i (column c = i0 + i) of the panel and, if do_next, update column c+1:
+//   w = tau (A v - V p - W q) + alpha2 v,  alpha2 = -tau/2 (w . v) = -tau^2/2 (v^T A v - 2 p.q)
+//   W[i] = w, row c of A <- v (unit entry at c+1), E[c] = beta, tau[c] = tau
+//   row c+1 of A: a[g] -= sum_{j <= i} V_j[g] W_j[c+1] + W_j[g] V_j[c+1]  (g >= c+1),
+//   D[c+1] = a[c+1], alph[c+1] = a[c+2], Pn_out[blk] = sum_{g >= c+3} a[g]^2.
+// Every work-group reduces the column's scalars (|x|^2 -> tau, p, q, v^T A v, (A v)[c+1]) from
+// the symv partials itself, in a fixed order, so no grid-wide step is needed.  Eight lanes per
+// row g = c + 1 + 32 blockIdx + tid / 8: lane k adds the symv partials of strips b0 + k,
+// b0 + k + 8, ..., chunks k, k + 8, ... and the reflectors j = k, k + 8, ...; a fixed butterfly
+// over the eight lanes completes the sums.
+__global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int64_t lda, int64_t n, int64_t c,
+                                                     int64_t i0, int i, int do_next, float* __restrict__ alph,
+                                                     const float* __restrict__ Pn_in, int npn,
+                                                     float* __restrict__ Pn_out, float* __restrict__ Wb,
+                                                     const float* __restrict__ Pr, const float* __restrict__ Pc,
+                                                     const float* __restrict__ Pvv, const float* __restrict__ Ppq,
+                                                     int ch_alloc, float* __restrict__ D, float* __restrict__ E,
+                                                     float* __restrict__ tau) {
+  __shared__ float red3[3][kThr / 64];
+  __shared__ float spq[4][64];
+  __shared__ float sp[kPB], sq[kPB], svr[kPB], swr[kPB];
+  const int tid = threadIdx.x, k = tid & (kSub - 1);
+  const int64_t r = c + 1;
+  const int64_t g = r + (int64_t)blockIdx.x * kRowsPB + (tid / kSub);
+  const bool active = g < n;
+  const int nblk = (int)(lda / kTB);
+  const int b0 = (int)((c + 1) / kTB);
+  const int ns = nblk - b0;
+  const int chy = (ns + kCH - 1) / kCH;
+
+  // column scalars: partial loads
+  float xn2 = 0.f;
+  for (int t = tid; t < npn; t += kThr) xn2 += Pn_in[t];
+  float pqp = 0.f;
+  {
+    const int slot = tid & 63, part = tid >> 6;
+    float v[kDotWG / 4];
+#pragma unroll
+    for (int u = 0; u < kDotWG / 4; ++u) v[u] = Ppq[(int64_t)(part * (kDotWG / 4) + u) * 64 + slot];
+#pragma unroll
+    for (int u = 0; u < kDotWG / 4; ++u) pqp += v[u];
+  }
+  float vav = 0.f;
+  for (int base = tid; base < chy * ns; base += kThr * 16) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int idx = base + u * kThr;
+      const int chx = idx / ns, sx = idx % ns;
+      v[u] = (idx < chy * ns && sx < ns - kCH * chx) ? Pvv[(int64_t)chx * nblk + b0 + sx] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) vav += v[u];
+  }
+  float yr = 0.f;
+  if (tid < chy) yr = Pc[((int64_t)b0 * ch_alloc + tid) * kTB + (r % kTB)];
+  if (tid == kThr - 1) yr = Pr[(int64_t)b0 * lda + r];  // chy <= ch_alloc < kThr - 1
+  if (tid >= 64 && tid < 64 + i) {
+    svr[tid - 64] = A[(i0 + tid - 64) * lda + r];
+    swr[tid - 64] = Wb[(int64_t)(tid - 64) * lda + r];
+  }
+
+  // own row: symv partials and the earlier reflectors' entries
+  float y = 0.f;
+  float vj[kPB / kSub], wj[kPB / kSub];
+#pragma unroll
+  for (int t = 0; t < kPB / kSub; ++t) vj[t] = wj[t] = 0.f;
+  float a_c = 0.f, a_r = 0.f;
+  if (active) {
+    const int s = (int)(g / kTB);
+    for (int bj0 = b0 + k; bj0 <= s; bj0 += 8 * kSub) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = (bj0 + kSub * u <= s) ? Pr[(int64_t)(bj0 + kSub * u) * lda + g] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (bj0 + kSub * u <= s) y += v[u];
+    }
+    const int nch = (nblk - s + kCH - 1) / kCH;
+    for (int ch = k; ch < nch; ch += kSub) y += Pc[((int64_t)s * ch_alloc + ch) * kTB + (g % kTB)];
+#pragma unroll
+    for (int t = 0; t < kPB / kSub; ++t) {
+      const int j = k + kSub * t;
+      if (j < i) {
+        vj[t] = A[(i0 + j) * lda + g];
+        wj[t] = Wb[(int64_t)j * lda + g];
+      }
+    }
+    if (k == 0) {
+      a_c = A[c * lda + g];
+      if (do_next) a_r = A[r * lda + g];
+    }
+  }
+
+  // column scalars: reductions (fixed order)
+  spq[tid >> 6][tid & 63] = pqp;
+  block_sum3(xn2, vav, yr, red3);  // its barriers also publish spq, svr, swr
+  if (tid < i) {
+    sp[tid] = spq[0][tid] + spq[1][tid] + spq[2][tid] + spq[3][tid];
+    sq[tid] = spq[0][kPB + tid] + spq[1][kPB + tid] + spq[2][kPB + tid] + spq[3][kPB + tid];
+  }
+  __syncthreads();
+  const float alpha = alph[c];
+  float tau_c = 0.f, beta = alpha, scale = 0.f;
+  if (xn2 != 0.f) {
+    beta = -copysignf(sqrtf(alpha * alpha + xn2), alpha);
+    tau_c = (beta - alpha) / beta;
+    scale = 1.f / (alpha - beta);
+  }
+  float pq = 0.f, yr_c = yr;
+  for (int j = 0; j < i; ++j) {
+    pq += sp[j] * sq[j];
+    yr_c -= svr[j] * sp[j] + swr[j] * sq[j];
+  }
+  const float alpha2 = -0.5f * tau_c * (tau_c * (vav - 2.f * pq));
+  const float w0 = tau_c * yr_c + alpha2;
+
+  float sw = 0.f, su = 0.f;
+#pragma unroll
+  for (int t = 0; t < kPB / kSub; ++t) {
+    const int j = k + kSub * t;
+    if (j < i) {
+      sw += vj[t] * sp[j] + wj[t] * sq[j];
+      su += vj[t] * swr[j] + wj[t] * svr[j];
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < kSub; off <<= 1) {
+    y += __shfl_xor(y, off, 64);
+    sw += __shfl_xor(sw, off, 64);
+    su += __shfl_xor(su, off, 64);
+  }
+  float sqv = 0.f;
+  if (active && k == 0) {
+    const float vg = g == r ? 1.f : a_c * scale;
+    const float wg = tau_c * (y - sw) + alpha2 * vg;
+    Wb[(int64_t)i * lda + g] = wg;
+    A[c * lda + g] = vg;
+    if (do_next) {
+      const float a = a_r - (su + (vg * w0 + wg));
+      A[r * lda + g] = a;
+      if (g == r) D[r] = a;
+      if (g == r + 1) alph[r] = a;
+      if (g >= r + 2) sqv = a * a;
+    }
+  }
+  if (blockIdx.x == 0 && tid == 0) {
+    E[c] = beta;
+    tau[c] = tau_c;
+  }
+  if (!do_next) return;  // uniform
+  float z1 = 0.f, z2 = 0.f;
+  block_sum3(sqv, z1, z2, red3);
+  if (tid == 0) Pn_out[blockIdx.x] = sqv;
+}
+
+// ---- back-transformation ---------------------------------------------------------------------
+
 // Y (m x nb, row-major, m = n - i0) of reflectors i0 .. i0+nb-1: Y[r'][c] = v_{i0+c}[i0+r'], with
-// v_i[i+1] = 1, v_i[r] = A_col[i * n + r] for r > i+1, 0 for r <= i (A column-major).  Starting
-// the rows at i0 (a multiple of the block size) keeps the GEMM operands 16-byte aligned.
-__global__ __launch_bounds__(256) void extract_y_kernel(const float* __restrict__ A, int64_t n, int64_t i0, int nb,
-                                                        float* __restrict__ Y) {
+// v_i[i+1] = 1, v_i[r] = A[i][r] for r > i+1, 0 for r <= i.  Starting the rows at i0 (a multiple
+// of the block size) keeps the GEMM operands 16-byte aligned.
+__global__ __launch_bounds__(256) void extract_y_kernel(const float* __restrict__ A, int64_t lda, int64_t n,
+                                                        int64_t i0, int nb, float* __restrict__ Y) {
   const int64_t m = n - i0;
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= m * nb) return;
@@ -39,7 +410,7 @@ __global__ __launch_bounds__(256) void extract_y_kernel(const float* __restrict_
   const int64_t i = i0 + c;
   float v = 0.f;
   if (r == i + 1) v = 1.f;
-  else if (r > i + 1) v = A[i * n + r];
+  else if (r > i + 1) v = A[i * lda + r];
   Y[e] = v;
 }
 
@@ -68,96 +439,197 @@ __global__ __launch_bounds__(256) void larft_kernel(const float* __restrict__ G,
   for (int e = threadIdx.x; e < nb * nb; e += blockDim.x) Tb[e] = sT[e / nb][e % nb];
 }
 
-struct Handle {
-  rocblas_handle h = nullptr;
-  int device = -1;
-};
-
-rocblas_handle get_handle(hipStream_t stream) {
-  static thread_local Handle hs[16];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return nullptr;
-  if (!hs[dev].h) {
-    if (rocblas_create_handle(&hs[dev].h) != rocblas_status_success) return nullptr;
-    hs[dev].device = dev;
-  }
-  if (rocblas_set_stream(hs[dev].h, stream) != rocblas_status_success) return nullptr;
-  return hs[dev].h;
-}
-
 }  // namespace
 }  // namespace mpq
 
+namespace {
+
+// Workspace layout of mpq_syevd (float offsets, each region 64-float aligned).
+struct SyevdLayout {
+  int64_t lda, nblk, ch_alloc, pn_stride, splits;
+  int64_t A, Z, Y, Yt, W, W2, G, Tb, P, D, E, tau, alph, Pn, Wb, X, Yb, Pr, Pc, Pvv, Ppq, info, total;
+};
+
+SyevdLayout syevd_layout(int64_t n) {
+  using namespace mpq;
+  SyevdLayout L{};
+  L.lda = a64(n);
+  L.nblk = L.lda / kTB;
+  L.ch_alloc = (L.nblk + kCH - 1) / kCH;
+  L.pn_stride = a64(L.lda / kRowsPB + 2);
+  int bn = 128;
+  L.splits = std::max(choose_splits(n, kNB, n, (int64_t)1 << 62, &bn), 1);
+  int64_t o = 0;
+  auto take = [&](int64_t floats) {
+    const int64_t at = o;
+    o += a64(floats);
+    return at;
+  };
+  L.A = take(L.lda * L.lda);
+  L.Z = take(n * n);
+  L.Y = take(n * kNB);
+  L.Yt = take(n * kNB);
+  L.W = take(n * kNB);
+  L.W2 = take(n * kNB);
+  L.G = take(kNB * kNB);
+  L.Tb = take(kNB * kNB);
+  L.P = take(a64(n * kNB) * L.splits);
+  L.D = take(n);
+  L.E = take(n);
+  L.tau = take(n);
+  L.alph = take(n);
+  L.Pn = take(2 * L.pn_stride);
+  L.Wb = take(kPB * L.lda);
+  L.X = take(L.lda * 2 * kPB);
+  L.Yb = take(L.lda * 2 * kPB);
+  L.Pr = take(L.nblk * L.lda);
+  L.Pc = take(L.nblk * L.ch_alloc * kTB);
+  L.Pvv = take(L.nblk * L.ch_alloc);
+  L.Ppq = take(kDotWG * 64);
+  L.info = take(64);
+  L.total = o;
+  return L;
+}
+
+// A = Q T Q^T for the symmetric A (lda x lda buffer, zero padded, full storage): D, E, tau and
+// the reflectors in the rows of A.  n >= 2.
+int sytrd(int64_t n, const SyevdLayout& L, float* base, hipStream_t stream) {
+  using namespace mpq;
+  const int64_t lda = L.lda;
+  float* A = base + L.A;
+  float* D = base + L.D;
+  float* E = base + L.E;
+  float* tau = base + L.tau;
+  float* alph = base + L.alph;
+  float* Pn = base + L.Pn;
+  float* Wb = base + L.Wb;
+  float* X = base + L.X;
+  float* Yb = base + L.Yb;
+  float* Pr = base + L.Pr;
+  float* Pc = base + L.Pc;
+  float* Pvv = base + L.Pvv;
+  float* Ppq = base + L.Ppq;
+  const int ch_alloc = (int)L.ch_alloc;
+  MPQ_HIP_TRY(hipMemsetAsync(Wb, 0, (size_t)kPB * lda * 4, stream));
+  for (int64_t i0 = 0; i0 < n - 1; i0 += kPB) {
+    const int nbl = (int)std::min<int64_t>(kPB, n - 1 - i0);
+    int npn = (int)((n - i0 + kThr - 1) / kThr);  // partial norms of the current column
+    hipLaunchKernelGGL(panel_start_kernel, dim3((unsigned)npn), dim3(kThr), 0, stream, A, lda, n, i0, D, alph,
+                       Pn + (i0 & 1) * L.pn_stride);
+    MPQ_LAUNCH_CHECK();
+    for (int i = 0; i < nbl; ++i) {
+      const int64_t c = i0 + i;
+      const int ns = (int)L.nblk - (int)((c + 1) / kTB);
+      const int chy = (ns + kCH - 1) / kCH;
+      // one extra row of work-groups forms the dots p, q
+      const dim3 sgrid((unsigned)std::max(ns, kDotWG), (unsigned)(chy + 1));
+      float* pn_in = Pn + (c & 1) * L.pn_stride;
+      float* pn_out = Pn + ((c + 1) & 1) * L.pn_stride;
+      hipLaunchKernelGGL(symv_kernel, sgrid, dim3(kThr), 0, stream, A, lda, n, c, i0, i, alph, pn_in, npn, Wb, Pr,
+                         Pc, Pvv, Ppq, ch_alloc);
+      MPQ_LAUNCH_CHECK();
+      const int do_next = (i + 1 < nbl) || (c + 1 == n - 1);
+      const int fblocks = (int)((n - c - 1 + kRowsPB - 1) / kRowsPB);
+      hipLaunchKernelGGL(finish_kernel, dim3((unsigned)fblocks), dim3(kThr), 0, stream, A, lda, n, c, i0, i, do_next,
+                         alph, pn_in, npn, pn_out, Wb, Pr, Pc, Pvv, Ppq, ch_alloc, D, E, tau);
+      MPQ_LAUNCH_CHECK();
+      npn = fblocks;
+    }
+    const int64_t s0 = i0 + nbl;
+    if (s0 < n - 1) {
+      // trailing update A[s0:, s0:] -= V W^T + W V^T = [V W] [W V]^T (nbl == kPB here)
+      const int64_t m = n - s0;
+      const float* Vp = A + i0 * lda + s0;
+      const float* Wp = Wb + s0;
+      MPQ_HIP_TRY(transpose_matrix(Vp, kPB, m, lda, X, 2 * kPB, stream));
+      MPQ_HIP_TRY(transpose_matrix(Wp, kPB, m, lda, X + kPB, 2 * kPB, stream));
+      MPQ_HIP_TRY(transpose_matrix(Wp, kPB, m, lda, Yb, 2 * kPB, stream));
+      MPQ_HIP_TRY(transpose_matrix(Vp, kPB, m, lda, Yb + kPB, 2 * kPB, stream));
+      MPQ_HIP_TRY(gemm(X, 2 * kPB, Yb, 2 * kPB, true, nullptr, A + s0 * lda + s0, lda, m, m, 2 * kPB, -1.f, 1.f,
+                       nullptr, 0, stream));
+    }
+  }
+  return kOk;
+}
+
+rocblas_handle get_handle(hipStream_t stream) {
+  static thread_local rocblas_handle hs[16] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return nullptr;
+  if (!hs[dev] && rocblas_create_handle(&hs[dev]) != rocblas_status_success) return nullptr;
+  if (rocblas_set_stream(hs[dev], stream) != rocblas_status_success) return nullptr;
+  return hs[dev];
+}
+
+}  // namespace
+
 extern "C" int64_t mpq_syevd_workspace_size(int64_t n) {
   if (n <= 0) return 0;
-  const int64_t nb = mpq::kNB;
-  int bn = 128;
-  const int splits = mpq::choose_splits(n, nb, n, (int64_t)1 << 62, &bn);
-  // A copy, Z, Y, Y^T, W (n x nb), W2 (n x nb), gram, Tb, split partials, D, E, tau, info
-  return (mpq::a64(n * n) * 2 + mpq::a64(n * nb) * 4 + mpq::a64(nb * nb) * 2 +
-          mpq::a64(n * nb) * std::max(splits, 1) + mpq::a64(n) * 3 + 64) * 4;
+  return syevd_layout(n).total * 4;
 }
 
 extern "C" int mpq_syevd(int64_t n, const float* H, float* lam, float* V, void* workspace, int64_t workspace_bytes,
                          hipStream_t stream) {
   using namespace mpq;
-  MPQ_CHECK_ARG(n > 0 && n <= 46340, "mpq_syevd: n must be in [1, 46340]");
+  MPQ_CHECK_ARG(n > 0 && n <= 46336, "mpq_syevd: n must be in [1, 46336]");
+  static_assert(kDotWG % 4 == 0 && 2 * kPB <= 64 && kPB % kSub == 0, "tridiagonalisation constants");
   MPQ_CHECK_ARG(H && lam && V && workspace, "mpq_syevd: null pointer");
+  MPQ_CHECK_ARG((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "mpq_syevd: workspace must be 256-byte aligned");
   MPQ_CHECK_ARG(workspace_bytes >= mpq_syevd_workspace_size(n), "mpq_syevd: workspace too small (%lld < %lld)",
                 (long long)workspace_bytes, (long long)mpq_syevd_workspace_size(n));
   rocblas_handle h = get_handle(stream);
   MPQ_CHECK_ARG(h != nullptr, "mpq_syevd: rocBLAS handle unavailable");
-  const int nb_max = kNB;
-  char* p = static_cast<char*>(workspace);
-  float* A = (float*)p; p += a64(n * n) * 4;
-  float* Z = (float*)p; p += a64(n * n) * 4;
-  float* Y = (float*)p; p += a64(n * nb_max) * 4;
-  float* Yt = (float*)p; p += a64(n * nb_max) * 4;
-  float* W = (float*)p; p += a64(n * nb_max) * 4;
-  float* W2 = (float*)p; p += a64(n * nb_max) * 4;
-  float* G = (float*)p; p += a64(nb_max * nb_max) * 4;
-  float* Tb = (float*)p; p += a64(nb_max * nb_max) * 4;
-  int bn = 128;
-  const int splits = choose_splits(n, nb_max, n, (int64_t)1 << 62, &bn);
-  float* P = (float*)p; p += a64(n * nb_max) * std::max(splits, 1) * 4;
-  float* D = (float*)p; p += a64(n) * 4;
-  float* E = (float*)p; p += a64(n) * 4;
-  float* tau = (float*)p; p += a64(n) * 4;
-  rocblas_int* info = (rocblas_int*)p;
-  const int ni = (int)n;
+  const SyevdLayout L = syevd_layout(n);
+  float* base = static_cast<float*>(workspace);
+  float* A = base + L.A;
+  float* Z = base + L.Z;
+  float* Y = base + L.Y;
+  float* Yt = base + L.Yt;
+  float* W = base + L.W;
+  float* W2 = base + L.W2;
+  float* G = base + L.G;
+  float* Tb = base + L.Tb;
+  float* P = base + L.P;
+  float* D = base + L.D;
+  float* E = base + L.E;
+  float* tau = base + L.tau;
+  rocblas_int* info = reinterpret_cast<rocblas_int*>(base + L.info);
+  const int64_t lda = L.lda;
+  const int64_t pstride = a64(n * kNB);
 
-  // 1-2: tridiagonalise (the symmetric buffer read column-major) and solve the tridiagonal problem
-  MPQ_HIP_TRY(hipMemcpyAsync(A, H, n * n * 4, hipMemcpyDeviceToDevice, stream));
-  if (rocsolver_ssytrd(h, rocblas_fill_lower, ni, A, ni, D, E, tau) != rocblas_status_success) {
-    set_error("rocsolver_ssytrd failed");
-    set_error_code(kHipError);
-    return kHipError;
+  // 1. tridiagonalise (zero-padded copy, leading dimension lda)
+  MPQ_HIP_TRY(hipMemsetAsync(A, 0, (size_t)(lda * lda) * 4, stream));
+  MPQ_HIP_TRY(hipMemcpy2DAsync(A, lda * 4, H, n * 4, n * 4, n, hipMemcpyDeviceToDevice, stream));
+  MPQ_HIP_TRY(hipMemsetAsync(info, 0, sizeof(rocblas_int), stream));
+  if (n == 1) {
+    MPQ_HIP_TRY(hipMemcpyAsync(D, A, 4, hipMemcpyDeviceToDevice, stream));
+  } else {
+    const int rc = sytrd(n, L, base, stream);
+    if (rc != kOk) return rc;
   }
-  if (rocsolver_sstedc(h, rocblas_evect_tridiagonal, ni, D, E, Z, ni, info) != rocblas_status_success) {
+  // 2. tridiagonal eigenproblem
+  if (rocsolver_sstedc(h, rocblas_evect_tridiagonal, (rocblas_int)n, D, E, Z, (rocblas_int)n, info) !=
+      rocblas_status_success) {
     set_error("rocsolver_sstedc failed");
     set_error_code(kHipError);
     return kHipError;
   }
-  // Z column-major = row-major Zb with Zb = Z^T.  V^T = Zb Q^T, applied block by block:
-  //   Zb[:, i0:] <- Zb[:, i0:] - ((Zb[:, i0:] Y) Tb^T) Y^T
+  // 3. Z column-major = row-major Zb with Zb = Z^T.  V^T = Zb Q^T, applied block by block:
+  //    Zb[:, i0:] <- Zb[:, i0:] - ((Zb[:, i0:] Y) Tb^T) Y^T
   const int64_t nrefl = n - 1;
   for (int64_t i0 = ((nrefl - 1) / kNB) * kNB; i0 >= 0 && nrefl > 0; i0 -= kNB) {
     const int nb = (int)std::min<int64_t>(kNB, nrefl - i0);
     const int64_t m = n - i0;
     const int64_t cnt = m * nb;
-    hipLaunchKernelGGL(extract_y_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, stream, A, n, i0, nb, Y);
+    hipLaunchKernelGGL(extract_y_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, stream, A, lda, n, i0, nb,
+                       Y);
     MPQ_LAUNCH_CHECK();
-    // G = Y^T Y (nb x nb)
     MPQ_HIP_TRY(transpose_matrix(Y, m, nb, nb, Yt, m, stream));
-    MPQ_HIP_TRY(gemm(Yt, m, Y, nb, false, nullptr, G, nb, nb, nb, m, 1.f, 0.f, P, a64(n * nb_max) * splits, stream));
+    MPQ_HIP_TRY(gemm(Yt, m, Y, nb, false, nullptr, G, nb, nb, nb, m, 1.f, 0.f, P, pstride * L.splits, stream));
     hipLaunchKernelGGL(larft_kernel, dim3(1), dim3(256), 0, stream, G, tau + i0, nb, Tb);
     MPQ_LAUNCH_CHECK();
-    // W = Zb[:, i0:] Y  (n x nb)
-    MPQ_HIP_TRY(gemm(Z + i0, n, Y, nb, false, nullptr, W, nb, n, nb, m, 1.f, 0.f, P, a64(n * nb_max) * splits,
-                     stream));
-    // W2 = W Tb^T  (n x nb)
+    MPQ_HIP_TRY(gemm(Z + i0, n, Y, nb, false, nullptr, W, nb, n, nb, m, 1.f, 0.f, P, pstride * L.splits, stream));
     MPQ_HIP_TRY(gemm(W, nb, Tb, nb, true, nullptr, W2, nb, n, nb, nb, 1.f, 0.f, nullptr, 0, stream));
-    // Zb[:, i0:] -= W2 Y^T
     MPQ_HIP_TRY(gemm(W2, nb, Y, nb, true, nullptr, Z + i0, n, n, m, nb, -1.f, 1.f, nullptr, 0, stream));
   }
   // V (row-major, columns = eigenvectors) = (Zb)^T
