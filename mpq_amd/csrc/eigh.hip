@@ -14,8 +14,10 @@
 //      forward/columnwise), last block first.
 // Output: lam ascending (n), V (n x n, row-major, column k = eigenvector k), as torch.linalg.eigh.
 //
-// Storage: the symmetric matrix is kept in full (both triangles) in a zero-padded row-major
-// buffer with leading dimension lda = n rounded up to 64, so every tile load is 16-byte aligned.
+// Storage: the symmetric matrix sits in a zero-padded row-major buffer with leading dimension
+// lda = n rounded up to 64, so every tile load is 16-byte aligned.  Only the lower triangle and
+// the 64 x 64 diagonal tiles are kept current; column c is copied into row c when its reflector
+// is formed.
 // Reflector i (LAPACK's H(i) = I - tau_i v_i v_i^T, v_i[0..i] = 0, v_i[i+1] = 1) is stored in
 // row i, entries i+2..n-1 -- by symmetry the same entries LAPACK's lower storage keeps in column i.
 #include <rocblas/rocblas.h>
@@ -69,16 +71,19 @@ __device__ Reflector reflector_of(float alpha, const float* __restrict__ Pn, int
   return r;
 }
 
-// First column c of a panel: D[c] = A[c][c], alpha_c = A[c][c+1] and the partial sums of
-// A[c][g]^2 for g >= c+2 (one per work-group; thread g = c + 256 blockIdx + tid).
-__global__ __launch_bounds__(kThr) void panel_start_kernel(const float* __restrict__ A, int64_t lda, int64_t n,
+// First column c of a panel, read from the lower triangle (the trailing update keeps only that
+// part current) and copied into row c, where the reflector is formed: D[c] = A[c][c],
+// alpha_c = A[c+1][c] and the partial sums of A[g][c]^2 for g >= c+2 (one per work-group;
+// thread g = c + 256 blockIdx + tid).
+__global__ __launch_bounds__(kThr) void panel_start_kernel(float* __restrict__ A, int64_t lda, int64_t n,
                                                           int64_t c, float* __restrict__ D, float* __restrict__ alph,
                                                           float* __restrict__ Pn) {
   __shared__ float red[kThr / 64];
   const int64_t g = c + (int64_t)blockIdx.x * kThr + threadIdx.x;
   float sq = 0.f;
   if (g < n) {
-    const float a = A[c * lda + g];
+    const float a = A[g * lda + c];
+    A[c * lda + g] = a;
     if (g == c) D[c] = a;
     if (g == c + 1) alph[c] = a;
     if (g >= c + 2) sq = a * a;
@@ -328,7 +333,7 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
     }
     if (k == 0) {
       a_c = A[c * lda + g];
-      if (do_next) a_r = A[r * lda + g];
+      if (do_next) a_r = A[g * lda + r];  // column r, lower triangle
     }
   }
 
@@ -537,7 +542,8 @@ int sytrd(int64_t n, const SyevdLayout& L, float* base, hipStream_t stream) {
     }
     const int64_t s0 = i0 + nbl;
     if (s0 < n - 1) {
-      // trailing update A[s0:, s0:] -= V W^T + W V^T = [V W] [W V]^T (nbl == kPB here)
+      // trailing update A[s0:, s0:] -= V W^T + W V^T = [V W] [W V]^T (nbl == kPB here), on the
+      // tiles on or below the diagonal: symv reads only those, and the columns are read there
       const int64_t m = n - s0;
       const float* Vp = A + i0 * lda + s0;
       const float* Wp = Wb + s0;
@@ -545,8 +551,9 @@ int sytrd(int64_t n, const SyevdLayout& L, float* base, hipStream_t stream) {
       MPQ_HIP_TRY(transpose_matrix(Wp, kPB, m, lda, X + kPB, 2 * kPB, stream));
       MPQ_HIP_TRY(transpose_matrix(Wp, kPB, m, lda, Yb, 2 * kPB, stream));
       MPQ_HIP_TRY(transpose_matrix(Vp, kPB, m, lda, Yb + kPB, 2 * kPB, stream));
-      MPQ_HIP_TRY(gemm(X, 2 * kPB, Yb, 2 * kPB, true, nullptr, A + s0 * lda + s0, lda, m, m, 2 * kPB, -1.f, 1.f,
-                       nullptr, 0, stream));
+      // (band kTB - 1 above the diagonal: the 64 x 64 diagonal tiles of symv are read whole)
+      MPQ_HIP_TRY(gemm_lower(X, 2 * kPB, Yb, 2 * kPB, true, A + s0 * lda + s0, lda, m, 2 * kPB, -1.f, 1.f, kTB - 1,
+                             stream));
     }
   }
   return kOk;

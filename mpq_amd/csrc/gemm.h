@@ -27,6 +27,8 @@ struct GemmParams {
   int mode;
   bool trans_b;
   bool a_vec4, b_vec4;
+  bool lower_only;  // square C: skip tiles whose first column is >= last row + 1 + upper_band
+  int upper_band;
 };
 
 // Split-K count and N tile (64 or 128) for an M x N x K product with the given
@@ -46,5 +48,11 @@ hipError_t gemm(const float* A, int64_t lda, const float* B, int64_t ldb, bool t
                 const int32_t* b_rows, float* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
                 float alpha, float beta, float* workspace, int64_t workspace_floats,
                 hipStream_t stream);
+
+// Lower part of a square product: C = alpha * A*op(B) + beta * C on every 128 x 64 tile holding
+// an entry (i, j) with j <= i + upper_band (such tiles are computed whole).
+hipError_t gemm_lower(const float* A, int64_t lda, const float* B, int64_t ldb, bool trans_b, float* C,
+                      int64_t ldc, int64_t M, int64_t K, float alpha, float beta, int upper_band,
+                      hipStream_t stream);
 
 }  // namespace mpq

@@ -47,6 +47,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
 
   const int64_t m0 = (int64_t)blockIdx.y * BM;
   const int64_t n0 = (int64_t)blockIdx.x * BN;
+  if (p.lower_only && n0 >= m0 + BM + p.upper_band) return;  // uniform, before any barrier
   const int split = blockIdx.z;
   const int32_t* b_rows = p.b_rows;
   if (GATHER_B && p.b_rows_group > 0) b_rows += (m0 / p.b_rows_group) * p.b_rows_group_stride;
@@ -264,6 +265,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_full_kernel(GemmParams p) {
   const int wn0 = (wave % WAVES_N) * WN;
   const int64_t m0 = (int64_t)blockIdx.y * BM;
   const int64_t n0 = (int64_t)blockIdx.x * BN;
+  if (p.lower_only && n0 >= m0 + BM + p.upper_band) return;  // uniform, before any barrier
   const int split = blockIdx.z;
   const int64_t kbeg = (int64_t)split * p.k_per_split;
   const int64_t nslab = p.k_per_split / BK;
@@ -419,10 +421,10 @@ hipError_t launch_cfg(const GemmParams& p, dim3 grid, hipStream_t stream) {
 }  // namespace
 
 int choose_splits(int64_t M, int64_t N, int64_t K, int64_t workspace_floats, int* bn_out) {
-  // 128x128 tiles when the N extent alone fills the chip, else 128x64.
+  // 128x64 tiles: the 128x128 variant needs 154 VGPRs + 128 AGPRs (one work-group per SIMD set),
+  // which measured slower on every shape tried.
   const int64_t tiles_m = (M + 127) / 128;
-  int bn = 128;
-  if (tiles_m * ((N + 127) / 128) < 512) bn = 64;
+  const int bn = 64;
   const int64_t tiles = tiles_m * ((N + bn - 1) / bn);
   int splits = 1;
   const int64_t target = 2048;  // ~8 work-groups per CU on 256 CUs (latency hiding at small M)
@@ -452,6 +454,20 @@ hipError_t splitk_reduce(const float* P, int splits, int64_t M, int64_t N, float
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, P, splits,
                      M * N, M, N, C, ldc, alpha, beta);
   return hipGetLastError();
+}
+
+hipError_t gemm_lower(const float* A, int64_t lda, const float* B, int64_t ldb, bool trans_b, float* C,
+                      int64_t ldc, int64_t M, int64_t K, float alpha, float beta, int upper_band,
+                      hipStream_t stream) {
+  GemmParams p{};
+  p.M = M; p.N = M; p.K = K;
+  p.A = A; p.lda = lda; p.B = B; p.ldb = ldb; p.trans_b = trans_b;
+  p.alpha = alpha; p.beta = beta;
+  p.mode = kGemmAxpby;
+  p.C = C; p.ldc = ldc;
+  p.lower_only = true;
+  p.upper_band = upper_band;
+  return gemm_partials(p, 1, 64, stream);
 }
 
 hipError_t gemm(const float* A, int64_t lda, const float* B, int64_t ldb, bool trans_b,
