@@ -35,7 +35,7 @@ namespace {
 constexpr int kNB = 128;  // reflectors per compact-WY block of the back-transformation
 constexpr int kPB = 32;   // reflectors per tridiagonalisation panel (latrd block)
 constexpr int kTB = 64;   // symv tile edge
-constexpr int kCH = 8;    // symv tiles per work-group (one chunk of a column strip)
+constexpr int kCH = 8;    // most symv tiles per work-group (one chunk of a column strip)
 constexpr int kThr = 256;
 constexpr int kSub = 8;               // finish_kernel lanes per matrix row
 constexpr int kRowsPB = kThr / kSub;  // finish_kernel rows per work-group
@@ -45,31 +45,6 @@ constexpr int kDotPerWave = (2 * kPB + 3) / 4;  // dots per wave of a dot work-g
 inline int64_t a64(int64_t v) { return (v + 63) / 64 * 64; }
 
 // ---- tridiagonalisation ----------------------------------------------------------------------
-
-struct Reflector {
-  float tau, beta, scale;
-};
-
-// LAPACK larfg on (alpha, x): beta = -sign(alpha) sqrt(alpha^2 + |x|^2), tau = (beta - alpha) / beta,
-// v = [1, x / (alpha - beta)]; |x| = 0 gives tau = 0, beta = alpha.  |x|^2 arrives as per-block
-// partial sums, added here in a fixed order (every work-group gets the same bits).
-__device__ Reflector reflector_of(float alpha, const float* __restrict__ Pn, int npn, float* red) {
-  float s = 0.f;
-  for (int k = threadIdx.x; k < npn; k += blockDim.x) s += Pn[k];
-  const float xn2 = block_sum(s, red);
-  Reflector r;
-  if (xn2 == 0.f) {
-    r.tau = 0.f;
-    r.beta = alpha;
-    r.scale = 0.f;
-  } else {
-    const float beta = -copysignf(sqrtf(alpha * alpha + xn2), alpha);
-    r.tau = (beta - alpha) / beta;
-    r.beta = beta;
-    r.scale = 1.f / (alpha - beta);
-  }
-  return r;
-}
 
 // First column c of a panel, read from the lower triangle (the trailing update keeps only that
 // part current) and copied into row c, where the reflector is formed: D[c] = A[c][c],
@@ -93,37 +68,35 @@ __global__ __launch_bounds__(kThr) void panel_start_kernel(float* __restrict__ A
 }
 
 // Half-storage symv over the trailing matrix A[c+1:, c+1:] (as of the panel start) with the
-// reflector v of column c, plus the dots p = W_j^T v and q = V_j^T v of the panel's earlier
-// reflectors j < i (an extra row of kDotWG work-groups).  Tiles are 64 x 64 in global coordinates (rows/cols below c+1 are masked by
-// v = 0).  Work-group (x, y) takes column strip bj = b0 + x and row tiles bi = bj + 8y .. +7:
-//   Pr[bj][rows of bi] = A_(bi,bj) v_bj          (row contributions, one value per tile row)
-//   Pc[bj][y][64]      = sum_{bi > bj} A_(bi,bj)^T v_bi   (column contributions of the chunk)
-//   Pvv[y][bj]         = sum v_bi^T A_(bi,bj) v_bj (x2 off the diagonal)
-//   Ppq[x][64]         = dot work-group x's share of p (slots 0..i-1) and q (slots 32..32+i-1)
+// unscaled tail x of column c's reflector (x[g] = row c entry g for g >= c+2, else 0; the reflector
+// is v = e_{c+1} + scale x, and the finishing kernel combines the pieces once scale is known),
+// plus the dots W_j . x and V_j . x of the panel's earlier reflectors j < i (an extra row of
+// kDotWG work-groups).  Tiles are 64 x 64 in global coordinates.  Work-group (x, y) takes column
+// strip bj = b0 + x and row tiles bi = bj + 8y .. +7:
+//   Pr[bj][rows of bi] = A_(bi,bj) x_bj          (row contributions, one value per tile row)
+//   Pc[bj][y][64]      = sum_{bi > bj} A_(bi,bj)^T x_bi   (column contributions of the chunk)
+//   Pvv[y][bj]         = sum x_bi^T A_(bi,bj) x_bj (x2 off the diagonal)
+//   Ppq[x][64]         = dot work-group x's share of W_j . x (slots 0..i-1), V_j . x (32..32+i-1)
+// No work-group waits for anything before its first tile load.
 // Thread layout over a tile: column quad cq = tid % 16 (4 columns), rows r0 + 16k, r0 = tid / 16.
 __global__ __launch_bounds__(kThr) void symv_kernel(const float* __restrict__ A, int64_t lda, int64_t n, int64_t c,
-                                                   int64_t i0, int i, const float* __restrict__ alph,
-                                                   const float* __restrict__ Pn, int npn,
-                                                   const float* __restrict__ Wb, float* __restrict__ Pr,
-                                                   float* __restrict__ Pc, float* __restrict__ Pvv,
-                                                   float* __restrict__ Ppq, int ch_alloc) {
+                                                   int64_t i0, int i, const float* __restrict__ Wb,
+                                                   float* __restrict__ Pr, float* __restrict__ Pc,
+                                                   float* __restrict__ Pvv, float* __restrict__ Ppq, int ch_alloc,
+                                                   int chl) {
   const int nblk = (int)(lda / kTB);
   const int b0 = (int)((c + 1) / kTB);
   if ((int)blockIdx.y == (int)gridDim.y - 1) {
     // dot work-groups: x < kDotWG takes strips b0 + x, b0 + x + kDotWG, ...; wave w the dots
-    // d = w, w + 4, ... (d < i: p_d = W_d . v; i <= d < 2i: q_{d-i} = V_{d-i} . v), lane = entry
+    // d = w, w + 4, ... (d < i: W_d . x; i <= d < 2i: V_{d-i} . x), lane = entry
     if ((int)blockIdx.x >= kDotWG) return;
-    __shared__ float red0[kThr / 64];
-    const Reflector R0 = reflector_of(alph[c], Pn, npn, red0);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     float acc[kDotPerWave];
 #pragma unroll
     for (int t = 0; t < kDotPerWave; ++t) acc[t] = 0.f;
     for (int sx = b0 + (int)blockIdx.x; sx < nblk; sx += kDotWG) {
       const int64_t g = (int64_t)sx * kTB + lane;
-      float v = 0.f;
-      if (g == c + 1) v = 1.f;
-      else if (g > c + 1 && g < n) v = A[c * lda + g] * R0.scale;
+      const float v = (g > c + 1 && g < n) ? A[c * lda + g] : 0.f;
       float x[kDotPerWave];
 #pragma unroll
       for (int t = 0; t < kDotPerWave; ++t) {
@@ -142,36 +115,35 @@ __global__ __launch_bounds__(kThr) void symv_kernel(const float* __restrict__ A,
     }
     return;
   }
-  const int bj = b0 + (int)blockIdx.x;
-  const int ch = (int)blockIdx.y;
-  const int bi_first = bj + ch * kCH;
+  // odd columns walk the tiles in reverse dispatch order, so the tiles the previous column read
+  // last (still in the memory-side cache) are read first
+  const bool rev = (c & 1) != 0;
+  const int bj = b0 + (rev ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x);
+  const int ch = rev ? (int)gridDim.y - 2 - (int)blockIdx.y : (int)blockIdx.y;
+  const int bi_first = bj + ch * chl;
   if (bi_first >= nblk) return;  // uniform over the work-group, before any barrier
-  const int bi_end = min(bi_first + kCH, nblk);
+  const int bi_end = min(bi_first + chl, nblk);
   __shared__ float red[kThr / 64];
   __shared__ float sv[(kCH + 1) * kTB];
   __shared__ float scol[16][kTB + 1];
-  const Reflector R = reflector_of(alph[c], Pn, npn, red);
-  const int nseg = 1 + bi_end - bi_first;
-  for (int t = threadIdx.x; t < nseg * kTB; t += kThr) {
-    const int seg = t / kTB, off = t % kTB;
-    const int64_t g = (int64_t)(seg == 0 ? bj : bi_first + seg - 1) * kTB + off;
-    float v = 0.f;
-    if (g == c + 1) v = 1.f;
-    else if (g > c + 1 && g < n) v = A[c * lda + g] * R.scale;
-    sv[t] = v;
-  }
-  __syncthreads();
   const int cq = threadIdx.x & 15, r0 = threadIdx.x >> 4;
-  float vc[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) vc[u] = sv[4 * cq + u];
-  float cacc[4] = {0.f, 0.f, 0.f, 0.f};
-  float vav = 0.f;
   const float* colbase = A + (int64_t)bj * kTB + 4 * cq;
   float4 cur[4], nxt[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k)
     cur[k] = *reinterpret_cast<const float4*>(colbase + ((int64_t)bi_first * kTB + r0 + 16 * k) * lda);
+  const int nseg = 1 + bi_end - bi_first;
+  for (int t = threadIdx.x; t < nseg * kTB; t += kThr) {
+    const int seg = t / kTB, off = t % kTB;
+    const int64_t g = (int64_t)(seg == 0 ? bj : bi_first + seg - 1) * kTB + off;
+    sv[t] = (g > c + 1 && g < n) ? A[c * lda + g] : 0.f;
+  }
+  __syncthreads();
+  float vc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) vc[u] = sv[4 * cq + u];
+  float cacc[4] = {0.f, 0.f, 0.f, 0.f};
+  float vav = 0.f;
   for (int bi = bi_first; bi < bi_end; ++bi) {
     if (bi + 1 < bi_end) {
 #pragma unroll
@@ -243,24 +215,27 @@ __device__ __forceinline__ void block_sum3(float& a, float& b, float& c, float (
   }
 }
 
-// Finish reflector i (column c = i0 + i) of the panel and, if do_next, update column c+1:
+// Finish reflector i (column c = i0 + i) of the panel and, if do_next, update column c+1.  With
+// r = c+1, x the unscaled tail (row c, entries >= c+2), v = e_r + scale x and u = A x (the symv):
+//   A v = A[:, r] + scale u,  v^T A v = A_rr + 2 scale u_r + scale^2 x^T u,
+//   p_j = W_j . v = W_j[r] + scale W_j . x,  q_j = V_j . v = V_j[r] + scale V_j . x,
 //   w = tau (A v - V p - W q) + alpha2 v,  alpha2 = -tau/2 (w . v) = -tau^2/2 (v^T A v - 2 p.q)
-//   W[i] = w, row c of A <- v (unit entry at c+1), E[c] = beta, tau[c] = tau
-//   row c+1 of A: a[g] -= sum_{j <= i} V_j[g] W_j[c+1] + W_j[g] V_j[c+1]  (g >= c+1),
-//   D[c+1] = a[c+1], alph[c+1] = a[c+2], Pn_out[blk] = sum_{g >= c+3} a[g]^2.
-// Every work-group reduces the column's scalars (|x|^2 -> tau, p, q, v^T A v, (A v)[c+1]) from
-// the symv partials itself, in a fixed order, so no grid-wide step is needed.  Eight lanes per
-// row g = c + 1 + 32 blockIdx + tid / 8: lane k adds the symv partials of strips b0 + k,
-// b0 + k + 8, ..., chunks k, k + 8, ... and the reflectors j = k, k + 8, ...; a fixed butterfly
-// over the eight lanes completes the sums.
+//   W[i] = w, row c of A <- v (unit entry at r), E[c] = beta, tau[c] = tau
+//   row r of A: a[g] = A[g][r] - sum_{j <= i} V_j[g] W_j[r] + W_j[g] V_j[r]  (g >= r),
+//   D[r] = a[r], alph[r] = a[r+1], Pn_out[blk] = sum_{g >= r+2} a[g]^2.
+// Every work-group reduces the column's scalars (|x|^2 -> tau, the dots, x^T A x, u_r) from the
+// partials itself, in a fixed order, so no grid-wide step is needed.  Eight lanes per row
+// g = r + 32 blockIdx + tid / 8: lane k adds the symv partials of strips b0 + k, b0 + k + 8, ...,
+// chunks k, k + 8, ... and the reflectors j = k, k + 8, ...; a fixed butterfly over the eight
+// lanes completes the sums.
 __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int64_t lda, int64_t n, int64_t c,
                                                      int64_t i0, int i, int do_next, float* __restrict__ alph,
                                                      const float* __restrict__ Pn_in, int npn,
                                                      float* __restrict__ Pn_out, float* __restrict__ Wb,
                                                      const float* __restrict__ Pr, const float* __restrict__ Pc,
                                                      const float* __restrict__ Pvv, const float* __restrict__ Ppq,
-                                                     int ch_alloc, float* __restrict__ D, float* __restrict__ E,
-                                                     float* __restrict__ tau) {
+                                                     int ch_alloc, int chl, float* __restrict__ D,
+                                                     float* __restrict__ E, float* __restrict__ tau) {
   __shared__ float red3[3][kThr / 64];
   __shared__ float spq[4][64];
   __shared__ float sp[kPB], sq[kPB], svr[kPB], swr[kPB];
@@ -271,7 +246,7 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
   const int nblk = (int)(lda / kTB);
   const int b0 = (int)((c + 1) / kTB);
   const int ns = nblk - b0;
-  const int chy = (ns + kCH - 1) / kCH;
+  const int chy = (ns + chl - 1) / chl;
 
   // column scalars: partial loads
   float xn2 = 0.f;
@@ -285,28 +260,29 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
 #pragma unroll
     for (int u = 0; u < kDotWG / 4; ++u) pqp += v[u];
   }
-  float vav = 0.f;
+  float xux = 0.f;
   for (int base = tid; base < chy * ns; base += kThr * 16) {
     float v[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const int idx = base + u * kThr;
       const int chx = idx / ns, sx = idx % ns;
-      v[u] = (idx < chy * ns && sx < ns - kCH * chx) ? Pvv[(int64_t)chx * nblk + b0 + sx] : 0.f;
+      v[u] = (idx < chy * ns && sx < ns - chl * chx) ? Pvv[(int64_t)chx * nblk + b0 + sx] : 0.f;
     }
 #pragma unroll
-    for (int u = 0; u < 16; ++u) vav += v[u];
+    for (int u = 0; u < 16; ++u) xux += v[u];
   }
-  float yr = 0.f;
-  if (tid < chy) yr = Pc[((int64_t)b0 * ch_alloc + tid) * kTB + (r % kTB)];
-  if (tid == kThr - 1) yr = Pr[(int64_t)b0 * lda + r];  // chy <= ch_alloc < kThr - 1
+  float ur = 0.f;
+  if (tid < chy) ur = Pc[((int64_t)b0 * ch_alloc + tid) * kTB + (r % kTB)];
+  if (tid == kThr - 1) ur = Pr[(int64_t)b0 * lda + r];  // chy < kThr - 1 (checked by the host)
   if (tid >= 64 && tid < 64 + i) {
     svr[tid - 64] = A[(i0 + tid - 64) * lda + r];
     swr[tid - 64] = Wb[(int64_t)(tid - 64) * lda + r];
   }
+  const float arr = A[r * lda + r];
 
-  // own row: symv partials and the earlier reflectors' entries
-  float y = 0.f;
+  // own row: symv partials, the earlier reflectors' entries, column r and row c
+  float u = 0.f;
   float vj[kPB / kSub], wj[kPB / kSub];
 #pragma unroll
   for (int t = 0; t < kPB / kSub; ++t) vj[t] = wj[t] = 0.f;
@@ -316,13 +292,21 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
     for (int bj0 = b0 + k; bj0 <= s; bj0 += 8 * kSub) {
       float v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = (bj0 + kSub * u <= s) ? Pr[(int64_t)(bj0 + kSub * u) * lda + g] : 0.f;
+      for (int q = 0; q < 8; ++q) v[q] = (bj0 + kSub * q <= s) ? Pr[(int64_t)(bj0 + kSub * q) * lda + g] : 0.f;
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (bj0 + kSub * u <= s) y += v[u];
+      for (int q = 0; q < 8; ++q)
+        if (bj0 + kSub * q <= s) u += v[q];
     }
-    const int nch = (nblk - s + kCH - 1) / kCH;
-    for (int ch = k; ch < nch; ch += kSub) y += Pc[((int64_t)s * ch_alloc + ch) * kTB + (g % kTB)];
+    const int nch = (nblk - s + chl - 1) / chl;
+    for (int ch0 = k; ch0 < nch; ch0 += 4 * kSub) {
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        v[q] = (ch0 + kSub * q < nch) ? Pc[((int64_t)s * ch_alloc + ch0 + kSub * q) * kTB + (g % kTB)] : 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (ch0 + kSub * q < nch) u += v[q];
+    }
 #pragma unroll
     for (int t = 0; t < kPB / kSub; ++t) {
       const int j = k + kSub * t;
@@ -333,18 +317,13 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
     }
     if (k == 0) {
       a_c = A[c * lda + g];
-      if (do_next) a_r = A[g * lda + r];  // column r, lower triangle
+      a_r = A[g * lda + r];  // column r, lower triangle
     }
   }
 
   // column scalars: reductions (fixed order)
   spq[tid >> 6][tid & 63] = pqp;
-  block_sum3(xn2, vav, yr, red3);  // its barriers also publish spq, svr, swr
-  if (tid < i) {
-    sp[tid] = spq[0][tid] + spq[1][tid] + spq[2][tid] + spq[3][tid];
-    sq[tid] = spq[0][kPB + tid] + spq[1][kPB + tid] + spq[2][kPB + tid] + spq[3][kPB + tid];
-  }
-  __syncthreads();
+  block_sum3(xn2, xux, ur, red3);  // its barriers also publish spq, svr, swr
   const float alpha = alph[c];
   float tau_c = 0.f, beta = alpha, scale = 0.f;
   if (xn2 != 0.f) {
@@ -352,12 +331,19 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
     tau_c = (beta - alpha) / beta;
     scale = 1.f / (alpha - beta);
   }
+  if (tid < i) {
+    sp[tid] = swr[tid] + scale * (spq[0][tid] + spq[1][tid] + spq[2][tid] + spq[3][tid]);
+    sq[tid] = svr[tid] + scale * (spq[0][kPB + tid] + spq[1][kPB + tid] + spq[2][kPB + tid] + spq[3][kPB + tid]);
+  }
+  __syncthreads();
+  const float yr = arr + scale * ur;
+  const float vAv = arr + scale * (2.f * ur + scale * xux);
   float pq = 0.f, yr_c = yr;
   for (int j = 0; j < i; ++j) {
     pq += sp[j] * sq[j];
     yr_c -= svr[j] * sp[j] + swr[j] * sq[j];
   }
-  const float alpha2 = -0.5f * tau_c * (tau_c * (vav - 2.f * pq));
+  const float alpha2 = -0.5f * tau_c * (tau_c * (vAv - 2.f * pq));
   const float w0 = tau_c * yr_c + alpha2;
 
   float sw = 0.f, su = 0.f;
@@ -371,19 +357,20 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
   }
 #pragma unroll
   for (int off = 1; off < kSub; off <<= 1) {
-    y += __shfl_xor(y, off, 64);
+    u += __shfl_xor(u, off, 64);
     sw += __shfl_xor(sw, off, 64);
     su += __shfl_xor(su, off, 64);
   }
   float sqv = 0.f;
   if (active && k == 0) {
     const float vg = g == r ? 1.f : a_c * scale;
-    const float wg = tau_c * (y - sw) + alpha2 * vg;
+    const float wg = tau_c * ((a_r + scale * u) - sw) + alpha2 * vg;
     Wb[(int64_t)i * lda + g] = wg;
     A[c * lda + g] = vg;
     if (do_next) {
       const float a = a_r - (su + (vg * w0 + wg));
-      A[r * lda + g] = a;
+      // A[r][r] is read by every work-group above (arr): the updated diagonal goes to D only
+      if (g != r) A[r * lda + g] = a;
       if (g == r) D[r] = a;
       if (g == r + 1) alph[r] = a;
       if (g >= r + 2) sqv = a * a;
@@ -419,29 +406,35 @@ __global__ __launch_bounds__(256) void extract_y_kernel(const float* __restrict_
   Y[e] = v;
 }
 
-// Tb (nb x nb, row-major, upper) from the gram G = Y^T Y and tau (LAPACK larft, forward,
-// columnwise): Tb[i][i] = tau_i, Tb[0:i, i] = -tau_i Tb[0:i, 0:i] G[0:i, i].  One work-group.
+// Tb (nb x nb, row-major, upper) of the compact-WY form H_0 ... H_{nb-1} = I - Y Tb Y^T from the
+// gram G = Y^T Y and tau (LAPACK larft, forward, columnwise).  Tb^{-1} = diag(1/tau) + striu(G),
+// so Tb = (I + N)^{-1} D with D = diag(tau), N = D striu(G) (strictly upper, nilpotent); the form
+// needs no 1/tau, so tau = 0 (H = I) gives zero row and column as larft does.  Thread j < nb
+// solves column j of X = (I + N)^{-1} by back substitution, x_k = -sum_{l=k+1..j} N[k][l] x_l,
+// x_j = 1; Tb[k][j] = X[k][j] tau_j.  One work-group, N and X in LDS (2 x 66 KB).
 __global__ __launch_bounds__(256) void larft_kernel(const float* __restrict__ G, const float* __restrict__ tau,
                                                     int nb, float* __restrict__ Tb) {
-  __shared__ float sT[kNB][kNB + 1];
-  __shared__ float w[kNB];
-  for (int e = threadIdx.x; e < nb * nb; e += blockDim.x) sT[e / nb][e % nb] = 0.f;
-  __syncthreads();
-  for (int i = 0; i < nb; ++i) {
-    const float ti = tau[i];
-    // w[0:i] = -tau_i G[0:i, i]
-    for (int r = threadIdx.x; r < i; r += blockDim.x) w[r] = -ti * G[r * nb + i];
-    __syncthreads();
-    // T[0:i, i] = T[0:i, 0:i] w (upper triangular)
-    for (int r = threadIdx.x; r < i; r += blockDim.x) {
-      float acc = 0.f;
-      for (int k = r; k < i; ++k) acc += sT[r][k] * w[k];
-      sT[r][i] = acc;
-    }
-    if (threadIdx.x == 0) sT[i][i] = ti;
-    __syncthreads();
+  __shared__ float sN[kNB][kNB + 1];
+  __shared__ float sX[kNB][kNB + 1];
+  for (int e = threadIdx.x; e < nb * nb; e += blockDim.x) {
+    const int k = e / nb, l = e % nb;
+    sN[k][l] = k < l ? tau[k] * G[e] : 0.f;
   }
-  for (int e = threadIdx.x; e < nb * nb; e += blockDim.x) Tb[e] = sT[e / nb][e % nb];
+  __syncthreads();
+  const int j = threadIdx.x;
+  if (j < nb) {
+    sX[j][j] = 1.f;
+    for (int k = j - 1; k >= 0; --k) {
+      float acc = 0.f;
+      for (int l = k + 1; l <= j; ++l) acc += sN[k][l] * sX[l][j];
+      sX[k][j] = -acc;
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < nb * nb; e += blockDim.x) {
+    const int k = e / nb, l = e % nb;
+    Tb[e] = k <= l ? sX[k][l] * tau[l] : 0.f;
+  }
 }
 
 }  // namespace
@@ -460,7 +453,7 @@ SyevdLayout syevd_layout(int64_t n) {
   SyevdLayout L{};
   L.lda = a64(n);
   L.nblk = L.lda / kTB;
-  L.ch_alloc = (L.nblk + kCH - 1) / kCH;
+  L.ch_alloc = L.nblk;  // chunks of one tile at the smallest chunk length
   L.pn_stride = a64(L.lda / kRowsPB + 2);
   int bn = 128;
   L.splits = std::max(choose_splits(n, kNB, n, (int64_t)1 << 62, &bn), 1);
@@ -525,18 +518,26 @@ int sytrd(int64_t n, const SyevdLayout& L, float* base, hipStream_t stream) {
     for (int i = 0; i < nbl; ++i) {
       const int64_t c = i0 + i;
       const int ns = (int)L.nblk - (int)((c + 1) / kTB);
-      const int chy = (ns + kCH - 1) / kCH;
+      // chunk length: kCH tiles (fewest partials) except on small trailing matrices, where more
+      // and shorter work-groups shorten the kernel
+      const int chl = ns > 32 ? kCH : 1;
+      const int chy = (ns + chl - 1) / chl;
+      if (chy >= kThr - 1) {
+        set_error("mpq_syevd: internal chunk count %d too large", chy);
+        set_error_code(kInvalidArgument);
+        return kInvalidArgument;
+      }
       // one extra row of work-groups forms the dots p, q
       const dim3 sgrid((unsigned)std::max(ns, kDotWG), (unsigned)(chy + 1));
       float* pn_in = Pn + (c & 1) * L.pn_stride;
       float* pn_out = Pn + ((c + 1) & 1) * L.pn_stride;
-      hipLaunchKernelGGL(symv_kernel, sgrid, dim3(kThr), 0, stream, A, lda, n, c, i0, i, alph, pn_in, npn, Wb, Pr,
-                         Pc, Pvv, Ppq, ch_alloc);
+      hipLaunchKernelGGL(symv_kernel, sgrid, dim3(kThr), 0, stream, A, lda, n, c, i0, i, Wb, Pr, Pc, Pvv, Ppq,
+                         ch_alloc, chl);
       MPQ_LAUNCH_CHECK();
       const int do_next = (i + 1 < nbl) || (c + 1 == n - 1);
       const int fblocks = (int)((n - c - 1 + kRowsPB - 1) / kRowsPB);
       hipLaunchKernelGGL(finish_kernel, dim3((unsigned)fblocks), dim3(kThr), 0, stream, A, lda, n, c, i0, i, do_next,
-                         alph, pn_in, npn, pn_out, Wb, Pr, Pc, Pvv, Ppq, ch_alloc, D, E, tau);
+                         alph, pn_in, npn, pn_out, Wb, Pr, Pc, Pvv, Ppq, ch_alloc, chl, D, E, tau);
       MPQ_LAUNCH_CHECK();
       npn = fblocks;
     }
