@@ -119,17 +119,21 @@ __global__ __launch_bounds__(kThreads) void syrk_kernel(const void* __restrict__
   if (nslab > 1) gload(ra1, rb1, 1);
   lstore(ra0, rb0, 0);
   __syncthreads();
-  for (int64_t s = 0; s < nslab; s += 2) {
+  // Pairs of slabs with no exit inside the body (an exit between the halves makes the compiler
+  // copy every accumulator through VGPRs each iteration, draining the MFMA pipeline); an odd last
+  // slab, already in LDS buffer 0, is computed after the loop.
+  int64_t s = 0;
+  for (; s + 1 < nslab; s += 2) {
     if (s + 2 < nslab) gload(ra0, rb0, s + 2);
     compute(0);
-    if (s + 1 < nslab) lstore(ra1, rb1, 1);
+    lstore(ra1, rb1, 1);
     __syncthreads();
-    if (s + 1 >= nslab) break;
     if (s + 3 < nslab) gload(ra1, rb1, s + 3);
     compute(1);
     if (s + 2 < nslab) lstore(ra0, rb0, 0);
     __syncthreads();
   }
+  if (s < nslab) compute(0);
 
   // epilogue: elements on or above the diagonal, value written to (m, n) and (n, m)
   const int col = lane & 31;
