@@ -314,7 +314,7 @@ int uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows, int
         gp.b_rows = order + w0; gp.b_rows_group = pl.nblocks == 1 ? 0 : block_rows;
         gp.b_rows_group_stride = n;
         gp.C = rhs; gp.ldc = n; gp.alpha = -1.f; gp.beta = 1.f; gp.mode = kGemmAxpby;
-        MPQ_HIP_TRY(gemm_partials(gp, 1, 128, stream));
+        MPQ_HIP_TRY(gemm_partials(gp, 1, 64, stream));
       } else {
         for (int64_t b = 0; b < pl.nblocks; ++b) {
           const int64_t r0 = b * block_rows;
@@ -324,7 +324,7 @@ int uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows, int
           gp.B = H; gp.ldb = n; gp.trans_b = false;
           gp.b_rows = order + b * n + w0;
           gp.C = rhs + r0 * n; gp.ldc = n; gp.alpha = -1.f; gp.beta = 1.f; gp.mode = kGemmAxpby;
-          MPQ_HIP_TRY(gemm_partials(gp, 1, 128, stream));
+          MPQ_HIP_TRY(gemm_partials(gp, 1, 64, stream));
         }
       }
     }

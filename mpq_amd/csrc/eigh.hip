@@ -416,18 +416,41 @@ __global__ __launch_bounds__(256) void larft_kernel(const float* __restrict__ G,
                                                     int nb, float* __restrict__ Tb) {
   __shared__ float sN[kNB][kNB + 1];
   __shared__ float sX[kNB][kNB + 1];
-  for (int e = threadIdx.x; e < nb * nb; e += blockDim.x) {
-    const int k = e / nb, l = e % nb;
-    sN[k][l] = k < l ? tau[k] * G[e] : 0.f;
+  // 16 global loads in flight per thread (a loop of single loads waits a full memory round trip
+  // per element and dominated the kernel)
+  for (int e0 = threadIdx.x; e0 < kNB * kNB; e0 += 256 * 16) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      // unconditional loads from clamped in-range indices (a guarded load becomes a branch that
+      // waits for each load in turn), then a select
+      const int e = e0 + 256 * u, k = e / kNB, l = e % kNB;
+      const bool use = e < kNB * kNB && k < l && l < nb;
+      const int kc = min(k, nb - 1), lc = min(l, nb - 1);
+      const float g = G[kc * nb + lc] * tau[kc];
+      v[u] = use ? g : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int e = e0 + 256 * u;
+      if (e < kNB * kNB) sN[e / kNB][e % kNB] = v[u];
+    }
   }
   __syncthreads();
+  // Uniform loop bounds for every thread: sN[k][l] is then one broadcast LDS read per step and
+  // sX[l][j] is conflict-free across j; x_l = 0 for l > j makes the extra terms vanish.
+  // The l range starts at a multiple of 8 below k+1 (N[k][l] = 0 for l <= k, and for l >= nb)
+  // and is unrolled by 8 with four partial sums, so the LDS reads of a chunk overlap.
   const int j = threadIdx.x;
   if (j < nb) {
-    sX[j][j] = 1.f;
-    for (int k = j - 1; k >= 0; --k) {
-      float acc = 0.f;
-      for (int l = k + 1; l <= j; ++l) acc += sN[k][l] * sX[l][j];
-      sX[k][j] = -acc;
+    for (int l = 0; l < kNB; ++l) sX[l][j] = l == j ? 1.f : 0.f;
+    for (int k = nb - 2; k >= 0; --k) {
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int l = (k + 1) & ~7; l < nb; l += 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[u & 3] += sN[k][l + u] * sX[l + u][j];
+      }
+      if (k < j) sX[k][j] = -((acc[0] + acc[1]) + (acc[2] + acc[3]));
     }
   }
   __syncthreads();
