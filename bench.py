@@ -133,11 +133,13 @@ def run_layer(rows, cols, module, H_gptq, W, steps, warmup, bits=3):
             "flop": layer_flops(rows, cols, blocks), "result": res}
 
 
-def gemm_roofline(n, device, reps=20):
+def gemm_roofline(n, device, reps=20, warmup=100):
     """Live HIP-event timing of the dominant kernel: the split-K rank-space product
     (128 x n) @ (n x n) as the VAMP drivers launch it (gemm_f32_full_kernel, partials only;
     the drivers' epilogues sum the partials).  Events are recorded on the stream the kernel
-    is launched on (torch's current stream)."""
+    is launched on (torch's current stream).  `warmup` untimed launches (~50 ms of work) come
+    first: after the host-side phases the GPU has idled down, and the timed launches should run at
+    the clock the layer solve runs at, not during the ramp-up."""
     import torch
 
     from mpq_amd import ops
@@ -145,6 +147,8 @@ def gemm_roofline(n, device, reps=20):
     A = torch.randn(128, n, device=device)
     B = torch.randn(n, n, device=device)
     out, splits = ops.gemm_splitk(A, B)
+    for _ in range(warmup - 1):
+        ops.gemm_splitk(A, B, splits=splits, out=out)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(device)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
