@@ -289,20 +289,26 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
   float a_c = 0.f, a_r = 0.f;
   if (active) {
     const int s = (int)(g / kTB);
-    for (int bj0 = b0 + k; bj0 <= s; bj0 += 8 * kSub) {
-      float v[8];
+    // up to 32 partials per lane in one batch of loads (one memory round trip up to 256 strips)
+    for (int bj0 = b0 + k; bj0 <= s; bj0 += 32 * kSub) {
+      float v[32];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = (bj0 + kSub * q <= s) ? Pr[(int64_t)(bj0 + kSub * q) * lda + g] : 0.f;
+      for (int q = 0; q < 32; ++q) {
+        const int bj = min(bj0 + kSub * q, s);  // clamped: unconditional loads, then a select
+        v[q] = Pr[(int64_t)bj * lda + g];
+      }
 #pragma unroll
-      for (int q = 0; q < 8; ++q)
+      for (int q = 0; q < 32; ++q)
         if (bj0 + kSub * q <= s) u += v[q];
     }
     const int nch = (nblk - s + chl - 1) / chl;
     for (int ch0 = k; ch0 < nch; ch0 += 4 * kSub) {
       float v[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        v[q] = (ch0 + kSub * q < nch) ? Pc[((int64_t)s * ch_alloc + ch0 + kSub * q) * kTB + (g % kTB)] : 0.f;
+      for (int q = 0; q < 4; ++q) {
+        const int ch = min(ch0 + kSub * q, nch - 1);
+        v[q] = Pc[((int64_t)s * ch_alloc + ch) * kTB + (g % kTB)];
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         if (ch0 + kSub * q < nch) u += v[q];

@@ -30,6 +30,7 @@ namespace mpq {
 namespace {
 
 enum DenoiseMode : int { kPosterior = 0, kHardMap = 1, kHardRoundMean = 2, kFull = 3 };
+constexpr int kRegAtoms = 16;  // grids up to 4 bits keep their scores in registers
 
 // Per element: posterior of a uniform grid a_q = s(q - z), q = 0..maxq, under the
 // channel N(r1, 1/gamma) and the prior N(W, (tau*s)^2)  (mpq/priors/uniform.py:177-191).
@@ -59,10 +60,8 @@ __global__ __launch_bounds__(kEW) void uniform_denoise_kernel(
       const float ts = tau * sc;
       st2 = ts * ts;
     }
-    // pass 1: scores, max, first argmax
-    float mx = -INFINITY;
-    int arg = 0;
-    for (int q = 0; q <= maxq; ++q) {
+    // score of atom q (the division is kept as a division: MAP decisions are bit-exact)
+    auto score_of = [&](int q) {
       const float a = s * ((float)q - z);
       const float d = a - r;
       float score = mh * (d * d);
@@ -70,27 +69,54 @@ __global__ __launch_bounds__(kEW) void uniform_denoise_kernel(
         const float dc = a - c;
         score = score - (0.5f * (dc * dc)) / st2;
       }
-      if (score > mx) {
-        mx = score;
-        arg = q;
+      return score;
+    };
+    // pass 1: scores, max, first argmax.  Grids of up to kRegAtoms levels (4-bit) keep the scores
+    // in registers for pass 2, so each score is computed once.
+    float sc_reg[kRegAtoms];
+    const bool in_regs = maxq < kRegAtoms;
+    float mx = -INFINITY;
+    int arg = 0;
+    if (in_regs) {
+#pragma unroll
+      for (int q = 0; q < kRegAtoms; ++q) {
+        sc_reg[q] = q <= maxq ? score_of(q) : -INFINITY;
+        if (q <= maxq && sc_reg[q] > mx) {
+          mx = sc_reg[q];
+          arg = q;
+        }
+      }
+    } else {
+      for (int q = 0; q <= maxq; ++q) {
+        const float score = score_of(q);
+        if (score > mx) {
+          mx = score;
+          arg = q;
+        }
       }
     }
     float mean = 0.f;
     if (MODE == kPosterior || MODE == kHardRoundMean || MODE == kFull) {
       // pass 2: softmax moments
       float zsum = 0.f, m1 = 0.f, m2 = 0.f;
-      for (int q = 0; q <= maxq; ++q) {
-        const float a = s * ((float)q - z);
-        const float d = a - r;
-        float score = mh * (d * d);
-        if (tau > 0.f) {
-          const float dc = a - c;
-          score = score - (0.5f * (dc * dc)) / st2;
+      if (in_regs) {
+#pragma unroll
+        for (int q = 0; q < kRegAtoms; ++q) {
+          if (q > maxq) break;
+          const float a = s * ((float)q - z);
+          const float w = expf(sc_reg[q] - mx);
+          zsum += w;
+          m1 += w * a;
+          m2 += w * (a * a);
         }
-        const float w = expf(score - mx);
-        zsum += w;
-        m1 += w * a;
-        m2 += w * (a * a);
+      } else {
+        for (int q = 0; q <= maxq; ++q) {
+          const float a = s * ((float)q - z);
+          const float w = expf(score_of(q) - mx);
+          zsum += w;
+          m1 += w * a;
+          m2 += w * (a * a);
+        }
       }
       mean = m1 / zsum;
       const float second = m2 / zsum;
