@@ -31,7 +31,7 @@ struct GemmParams {
   int upper_band;
 };
 
-// Split-K count and N tile (64 or 128) for an M x N x K product with the given
+// Split-K count and N tile (always 64) for an M x N x K product with the given
 // workspace capacity (floats); 1 split when no workspace.
 int choose_splits(int64_t M, int64_t N, int64_t K, int64_t workspace_floats, int* bn_out);
 

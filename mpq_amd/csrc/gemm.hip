@@ -23,7 +23,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr int kBK = 16;  // K slab of the default configurations (k_per_split is a multiple of 32)
 constexpr int kThreads = 256;
 
-template <int BM, int BN, int WM, int WN, bool TRANS_B, bool GATHER_B, int kBK = 16>
+template <int BM, int BN, int WM, int WN, bool TRANS_B, bool GATHER_B, int kBK = 16, bool PRE_C = false>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
   constexpr int WAVES_N = BN / WN;
   constexpr int MI = WM / 32;
@@ -62,6 +62,26 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
     for (int j = 0; j < NI; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // PRE_C (axpby epilogue with beta != 0): this lane's C entries are loaded before the K loop, so
+  // their latency overlaps the MFMAs instead of stalling the epilogue.  Rows/columns outside C
+  // read a clamped in-range entry (never used) so the loads need no branches.
+  float cpre[PRE_C ? MI : 1][PRE_C ? NI : 1][PRE_C ? 16 : 1];
+  if constexpr (PRE_C) {
+    const int col = lane & 31;
+    const int rbase = (lane >> 5) * 4;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int64_t gn = min(n0 + wn0 + j * 32 + col, p.N - 1);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t gm = min(m0 + wm0 + i * 32 + (v >> 2) * 8 + rbase + (v & 3), p.M - 1);
+          cpre[i][j][v] = p.C[gm * p.ldc + gn];
+        }
+      }
+  }
 
   float4 ra[A_F4];
   float4 rb[B_F4];
@@ -218,7 +238,11 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
           p.C[(int64_t)split * p.split_stride + gm * p.ldc + gn] = val;
         } else {  // kGemmAxpby, single split: C = alpha*acc + beta*C
           float* dst = p.C + gm * p.ldc + gn;
-          *dst = p.beta == 0.f ? p.alpha * val : p.alpha * val + p.beta * *dst;
+          if constexpr (PRE_C) {
+            *dst = p.alpha * val + p.beta * cpre[i][j][v];
+          } else {
+            *dst = p.beta == 0.f ? p.alpha * val : p.alpha * val + p.beta * *dst;
+          }
         }
       }
     }
@@ -243,8 +267,9 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ P, int splits, in
 // the host), no row gather.  Two K slabs of global loads are kept in flight (register sets R0/R1,
 // the loop is unrolled by two so both sets are static), and a slab's LDS operands are all read
 // before its MFMA chain, so each slab waits once for LDS and once for global memory.
-template <int BM, int BN, int WM, int WN, bool TRANS_B, int HOIST = 8>
+template <int BM, int BN, int WM, int WN, bool TRANS_B, int HOIST = 8, bool PRE_C = false, bool GATHER_B = false>
 __global__ __launch_bounds__(kThreads) void gemm_f32_full_kernel(GemmParams p) {
+  static_assert(!(GATHER_B && TRANS_B), "row gather needs a row-major K x N B");
   constexpr int BK = 16;
   constexpr int WAVES_N = BN / WN;
   constexpr int MI = WM / 32;
@@ -288,13 +313,25 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_full_kernel(GemmParams p) {
     }
   }
   const int64_t b_step = TRANS_B ? BK : BK * p.ldb;
+  // GATHER_B: K row k of B is B[b_rows[k]] (per M tile group as in gemm_f32_kernel); each thread
+  // reads its slab row index in the same two-slabs-ahead prefetch as the data
+  const int32_t* b_rows = p.b_rows;
+  if (GATHER_B && p.b_rows_group > 0) b_rows += (m0 / p.b_rows_group) * p.b_rows_group_stride;
 
   float4 ra0[A_F4], rb0[B_F4], ra1[A_F4], rb1[B_F4];
   auto gload = [&](float4 (&ra)[A_F4], float4 (&rb)[B_F4], int64_t s) {
 #pragma unroll
     for (int i = 0; i < A_F4; ++i) ra[i] = *reinterpret_cast<const float4*>(asrc[i] + s * BK);
 #pragma unroll
-    for (int i = 0; i < B_F4; ++i) rb[i] = *reinterpret_cast<const float4*>(bsrc[i] + s * b_step);
+    for (int i = 0; i < B_F4; ++i) {
+      if constexpr (GATHER_B) {
+        const int t = tid + i * kThreads;
+        const int64_t row = b_rows[kbeg + s * BK + t / (BN / 4)];
+        rb[i] = *reinterpret_cast<const float4*>(p.B + row * p.ldb + n0 + (t % (BN / 4)) * 4);
+      } else {
+        rb[i] = *reinterpret_cast<const float4*>(bsrc[i] + s * b_step);
+      }
+    }
   };
   auto lstore = [&](const float4 (&ra)[A_F4], const float4 (&rb)[B_F4], int buf) {
 #pragma unroll
@@ -330,6 +367,24 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_full_kernel(GemmParams p) {
     for (int j = 0; j < NI; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // PRE_C: this lane's C entries of an axpby epilogue with beta != 0, loaded before the K loop
+  float cpre[PRE_C ? MI : 1][PRE_C ? NI : 1][PRE_C ? 16 : 1];
+  if constexpr (PRE_C) {
+    const int col = lane & 31;
+    const int rbase = (lane >> 5) * 4;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int64_t gn = n0 + wn0 + j * 32 + col;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t gm = m0 + wm0 + i * 32 + (v >> 2) * 8 + rbase + (v & 3);
+          cpre[i][j][v] = p.C[gm * p.ldc + gn];
+        }
+      }
+  }
 
   const int kl = lane >> 5;
   const int ml = lane & 31;
@@ -389,7 +444,11 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_full_kernel(GemmParams p) {
           p.C[(int64_t)split * p.split_stride + gm * p.ldc + gn] = val;
         } else {
           float* dst = p.C + gm * p.ldc + gn;
-          *dst = p.beta == 0.f ? p.alpha * val : p.alpha * val + p.beta * *dst;
+          if constexpr (PRE_C) {
+            *dst = p.alpha * val + p.beta * cpre[i][j][v];
+          } else {
+            *dst = p.beta == 0.f ? p.alpha * val : p.alpha * val + p.beta * *dst;
+          }
         }
       }
     }
@@ -398,17 +457,29 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_full_kernel(GemmParams p) {
 
 template <int BM, int BN, int WM, int WN>
 hipError_t launch_cfg(const GemmParams& p, dim3 grid, hipStream_t stream) {
-  // interior-tile kernel: whole tiles, an even number of 16-wide K slabs per split
-  const bool full = !p.b_rows && p.a_vec4 && p.b_vec4 && p.M % BM == 0 && p.N % BN == 0 &&
+  // interior-tile kernel: whole tiles, an even number of 16-wide K slabs per split; a row gather
+  // also needs its groups aligned to the 128-row M tile
+  const bool gather_ok = !p.b_rows || (!p.trans_b && (p.b_rows_group == 0 || p.b_rows_group % BM == 0));
+  const bool full = gather_ok && p.a_vec4 && p.b_vec4 && p.M % BM == 0 && p.N % BN == 0 &&
                     p.k_per_split % 32 == 0 && (int64_t)grid.z * p.k_per_split == p.K;
+  const bool pre_c = p.mode == kGemmAxpby && p.beta != 0.f;
+  if (full && p.b_rows) {
+    if (pre_c) hipLaunchKernelGGL((gemm_f32_full_kernel<BM, BN, WM, WN, false, 8, true, true>), grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((gemm_f32_full_kernel<BM, BN, WM, WN, false, 8, false, true>), grid, dim3(kThreads), 0, stream, p);
+    return hipGetLastError();
+  }
   if (full) {
     if (p.trans_b) {
-      hipLaunchKernelGGL((gemm_f32_full_kernel<BM, BN, WM, WN, true>), grid, dim3(kThreads), 0, stream, p);
+      if (pre_c) hipLaunchKernelGGL((gemm_f32_full_kernel<BM, BN, WM, WN, true, 8, true>), grid, dim3(kThreads), 0, stream, p);
+      else hipLaunchKernelGGL((gemm_f32_full_kernel<BM, BN, WM, WN, true>), grid, dim3(kThreads), 0, stream, p);
     } else {
-      hipLaunchKernelGGL((gemm_f32_full_kernel<BM, BN, WM, WN, false>), grid, dim3(kThreads), 0, stream, p);
+      if (pre_c) hipLaunchKernelGGL((gemm_f32_full_kernel<BM, BN, WM, WN, false, 8, true>), grid, dim3(kThreads), 0, stream, p);
+      else hipLaunchKernelGGL((gemm_f32_full_kernel<BM, BN, WM, WN, false>), grid, dim3(kThreads), 0, stream, p);
     }
     return hipGetLastError();
   }
+  // (the general kernel does not prefetch C: that costs it 96 VGPRs, occupancy 6 -> 2, and measured
+  // slower on the CD Schur update)
   if (p.trans_b) {
     hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM, WN, true, false>), grid, dim3(kThreads), 0, stream, p);
   } else if (p.b_rows) {
@@ -442,8 +513,8 @@ hipError_t gemm_partials(GemmParams p, int splits, int bn, hipStream_t stream) {
   p.k_per_split = kps > 0 ? kps : kBK;
   p.a_vec4 = ((reinterpret_cast<uintptr_t>(p.A) & 15u) == 0) && (p.lda % 4 == 0);
   p.b_vec4 = ((reinterpret_cast<uintptr_t>(p.B) & 15u) == 0) && (p.ldb % 4 == 0);
-  dim3 grid((unsigned)((p.N + bn - 1) / bn), (unsigned)((p.M + 127) / 128), (unsigned)splits);
-  if (bn == 128) return launch_cfg<128, 128, 64, 64>(p, grid, stream);
+  (void)bn;  // one tile shape: 128 x 64 (4 waves of 64 x 32)
+  dim3 grid((unsigned)((p.N + 63) / 64), (unsigned)((p.M + 127) / 128), (unsigned)splits);
   return launch_cfg<128, 64, 64, 32>(p, grid, stream);
 }
 
