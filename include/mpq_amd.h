@@ -210,14 +210,25 @@ int mpq_eigh_postprocess(const float* lam_asc, const float* V_asc, int64_t n, fl
 /*
  * Symmetric eigendecomposition of H (n x n, fp32): lam ascending (n) and V (n x n, row-major,
  * column k = eigenvector k), the torch.linalg.eigh call of mpq/adapters/gptqmodel.py:276-310.
- * rocSOLVER ssytrd + sstedc, then the back-transformation V = Q Z as blocked compact-WY
- * updates on this library's fp32 MFMA GEMM.  workspace: mpq_syevd_workspace_size(n) bytes
- * (rocSOLVER may also use its handle's own device memory).  Synchronises `stream` once;
+ * Blocked Householder tridiagonalisation on this library's kernels, rocSOLVER sstedc, then the
+ * back-transformation V = Q Z as blocked compact-WY updates on this library's fp32 MFMA GEMM.
+ * workspace: mpq_syevd_workspace_size(n) bytes (rocSOLVER and rocBLAS may also use their
+ * handle's own device memory).  Synchronises `stream` once;
  * MPQ_NUMERICAL_ERROR when the tridiagonal solver does not converge.
  */
 int64_t mpq_syevd_workspace_size(int64_t n);
 int mpq_syevd(int64_t n, const float* H, float* lam, float* V, void* workspace, int64_t workspace_bytes,
               mpq_stream_t stream);
+
+/*
+ * The same decomposition in fp64 (the torch.linalg.eigh of the float64 Hessian in
+ * mpq/adapters/quip_sharp.py:33-67): the tridiagonalisation kernels in double, rocSOLVER
+ * dstedc, and the trailing updates and back-transformation on rocBLAS dgemm.
+ * workspace: mpq_syevd_f64_workspace_size(n) bytes.
+ */
+int64_t mpq_syevd_f64_workspace_size(int64_t n);
+int mpq_syevd_f64(int64_t n, const double* H, double* lam, double* V, void* workspace, int64_t workspace_bytes,
+                  mpq_stream_t stream);
 
 /* out[i][j] = in[i][j] * scale[j] (Vs = V * S, mpq/adapters/gptqmodel.py:890). */
 int mpq_scale_columns(const float* in, int64_t rows, int64_t cols, const float* scale, float* out,

@@ -55,7 +55,7 @@ def _vamp_hessian_eigen(H: torch.Tensor, *, jitter_base: float = 1e-6, floor_sca
     H64 = 0.5 * (H64 + H64.T)
     if not bool(torch.isfinite(H64).all()):
         H64 = torch.nan_to_num(H64, nan=0.0, posinf=0.0, neginf=0.0)
-    lam64, V64 = torch.linalg.eigh(H64)
+    lam64, V64 = ops.syevd(H64)
     lam32 = lam64.to(torch.float32)
     V32 = V64.to(torch.float32).contiguous()
     del V64

@@ -44,26 +44,86 @@ constexpr int kDotPerWave = (2 * kPB + 3) / 4;  // dots per wave of a dot work-g
 
 inline int64_t a64(int64_t v) { return (v + 63) / 64 * 64; }
 
+// ---- element-type helpers (fp32 and fp64 share every kernel) ------------------------------------
+
+template <typename T>
+struct Vec4 {
+  T x, y, z, w;
+};
+template <typename T>
+__device__ __forceinline__ Vec4<T> load_v4(const T* p);
+template <>
+__device__ __forceinline__ Vec4<float> load_v4<float>(const float* p) {
+  const float4 f = *reinterpret_cast<const float4*>(p);
+  return {f.x, f.y, f.z, f.w};
+}
+template <>
+__device__ __forceinline__ Vec4<double> load_v4<double>(const double* p) {
+  const double2 a = *reinterpret_cast<const double2*>(p);
+  const double2 b = *reinterpret_cast<const double2*>(p + 2);
+  return {a.x, a.y, b.x, b.y};
+}
+template <typename T>
+__device__ __forceinline__ T wave_sum_t(T v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float block_sum_t(float v, float* scratch) { return block_sum(v, scratch); }
+__device__ __forceinline__ double block_sum_t(double v, double* scratch) { return block_sum_f64(v, scratch); }
+
+// reflectors per compact-WY block of the back-transformation (the T factor's two LDS arrays:
+// 2 x 128 x 129 x 4 bytes in fp32, 2 x 64 x 65 x 8 in fp64)
+template <typename T>
+struct NbOf;
+template <>
+struct NbOf<float> {
+  static constexpr int value = kNB;
+};
+template <>
+struct NbOf<double> {
+  static constexpr int value = kNB / 2;
+};
+
+// out = in^T (rows x cols -> cols x rows), 32 x 32 tiles through LDS
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_t_kernel(const T* __restrict__ in, int64_t rows, int64_t cols,
+                                                          int64_t ld_in, T* __restrict__ out, int64_t ld_out) {
+  __shared__ T tile[32][33];
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = r0 + k, c = c0 + tx;
+    if (r < rows && c < cols) tile[k][tx] = in[r * ld_in + c];
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t c = c0 + k, r = r0 + tx;
+    if (r < rows && c < cols) out[c * ld_out + r] = tile[tx][k];
+  }
+}
+
 // ---- tridiagonalisation ----------------------------------------------------------------------
 
 // First column c of a panel, read from the lower triangle (the trailing update keeps only that
 // part current) and copied into row c, where the reflector is formed: D[c] = A[c][c],
 // alpha_c = A[c+1][c] and the partial sums of A[g][c]^2 for g >= c+2 (one per work-group;
 // thread g = c + 256 blockIdx + tid).
-__global__ __launch_bounds__(kThr) void panel_start_kernel(float* __restrict__ A, int64_t lda, int64_t n,
-                                                          int64_t c, float* __restrict__ D, float* __restrict__ alph,
-                                                          float* __restrict__ Pn) {
-  __shared__ float red[kThr / 64];
+template <typename T>
+__global__ __launch_bounds__(kThr) void panel_start_kernel(T* __restrict__ A, int64_t lda, int64_t n,
+                                                          int64_t c, T* __restrict__ D, T* __restrict__ alph,
+                                                          T* __restrict__ Pn) {
+  __shared__ T red[kThr / 64];
   const int64_t g = c + (int64_t)blockIdx.x * kThr + threadIdx.x;
-  float sq = 0.f;
+  T sq = 0.f;
   if (g < n) {
-    const float a = A[g * lda + c];
+    const T a = A[g * lda + c];
     A[c * lda + g] = a;
     if (g == c) D[c] = a;
     if (g == c + 1) alph[c] = a;
     if (g >= c + 2) sq = a * a;
   }
-  const float t = block_sum(sq, red);
+  const T t = block_sum_t(sq, red);
   if (threadIdx.x == 0) Pn[blockIdx.x] = t;
 }
 
@@ -79,10 +139,11 @@ __global__ __launch_bounds__(kThr) void panel_start_kernel(float* __restrict__ A
 //   Ppq[x][64]         = dot work-group x's share of W_j . x (slots 0..i-1), V_j . x (32..32+i-1)
 // No work-group waits for anything before its first tile load.
 // Thread layout over a tile: column quad cq = tid % 16 (4 columns), rows r0 + 16k, r0 = tid / 16.
-__global__ __launch_bounds__(kThr) void symv_kernel(const float* __restrict__ A, int64_t lda, int64_t n, int64_t c,
-                                                   int64_t i0, int i, const float* __restrict__ Wb,
-                                                   float* __restrict__ Pr, float* __restrict__ Pc,
-                                                   float* __restrict__ Pvv, float* __restrict__ Ppq, int ch_alloc,
+template <typename T>
+__global__ __launch_bounds__(kThr) void symv_kernel(const T* __restrict__ A, int64_t lda, int64_t n, int64_t c,
+                                                   int64_t i0, int i, const T* __restrict__ Wb,
+                                                   T* __restrict__ Pr, T* __restrict__ Pc,
+                                                   T* __restrict__ Pvv, T* __restrict__ Ppq, int ch_alloc,
                                                    int chl) {
   const int nblk = (int)(lda / kTB);
   const int b0 = (int)((c + 1) / kTB);
@@ -91,13 +152,13 @@ __global__ __launch_bounds__(kThr) void symv_kernel(const float* __restrict__ A,
     // d = w, w + 4, ... (d < i: W_d . x; i <= d < 2i: V_{d-i} . x), lane = entry
     if ((int)blockIdx.x >= kDotWG) return;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    float acc[kDotPerWave];
+    T acc[kDotPerWave];
 #pragma unroll
     for (int t = 0; t < kDotPerWave; ++t) acc[t] = 0.f;
     for (int sx = b0 + (int)blockIdx.x; sx < nblk; sx += kDotWG) {
       const int64_t g = (int64_t)sx * kTB + lane;
-      const float v = (g > c + 1 && g < n) ? A[c * lda + g] : 0.f;
-      float x[kDotPerWave];
+      const T v = (g > c + 1 && g < n) ? A[c * lda + g] : 0.f;
+      T x[kDotPerWave];
 #pragma unroll
       for (int t = 0; t < kDotPerWave; ++t) {
         const int d = w + 4 * t;
@@ -110,7 +171,7 @@ __global__ __launch_bounds__(kThr) void symv_kernel(const float* __restrict__ A,
 #pragma unroll
     for (int t = 0; t < kDotPerWave; ++t) {
       const int d = w + 4 * t;
-      const float tot = wave_sum(acc[t]);
+      const T tot = wave_sum_t(acc[t]);
       if (lane == 0 && d < 2 * i) Ppq[(int64_t)blockIdx.x * 64 + (d < i ? d : kPB + d - i)] = tot;
     }
     return;
@@ -123,15 +184,15 @@ __global__ __launch_bounds__(kThr) void symv_kernel(const float* __restrict__ A,
   const int bi_first = bj + ch * chl;
   if (bi_first >= nblk) return;  // uniform over the work-group, before any barrier
   const int bi_end = min(bi_first + chl, nblk);
-  __shared__ float red[kThr / 64];
-  __shared__ float sv[(kCH + 1) * kTB];
-  __shared__ float scol[16][kTB + 1];
+  __shared__ T red[kThr / 64];
+  __shared__ T sv[(kCH + 1) * kTB];
+  __shared__ T scol[16][kTB + 1];
   const int cq = threadIdx.x & 15, r0 = threadIdx.x >> 4;
-  const float* colbase = A + (int64_t)bj * kTB + 4 * cq;
-  float4 cur[4], nxt[4];
+  const T* colbase = A + (int64_t)bj * kTB + 4 * cq;
+  Vec4<T> cur[4], nxt[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k)
-    cur[k] = *reinterpret_cast<const float4*>(colbase + ((int64_t)bi_first * kTB + r0 + 16 * k) * lda);
+    cur[k] = load_v4(colbase + ((int64_t)bi_first * kTB + r0 + 16 * k) * lda);
   const int nseg = 1 + bi_end - bi_first;
   for (int t = threadIdx.x; t < nseg * kTB; t += kThr) {
     const int seg = t / kTB, off = t % kTB;
@@ -139,25 +200,25 @@ __global__ __launch_bounds__(kThr) void symv_kernel(const float* __restrict__ A,
     sv[t] = (g > c + 1 && g < n) ? A[c * lda + g] : 0.f;
   }
   __syncthreads();
-  float vc[4];
+  T vc[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) vc[u] = sv[4 * cq + u];
-  float cacc[4] = {0.f, 0.f, 0.f, 0.f};
-  float vav = 0.f;
+  T cacc[4] = {0.f, 0.f, 0.f, 0.f};
+  T vav = 0.f;
   for (int bi = bi_first; bi < bi_end; ++bi) {
     if (bi + 1 < bi_end) {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        nxt[k] = *reinterpret_cast<const float4*>(colbase + ((int64_t)(bi + 1) * kTB + r0 + 16 * k) * lda);
+        nxt[k] = load_v4(colbase + ((int64_t)(bi + 1) * kTB + r0 + 16 * k) * lda);
     }
-    const float* svr = sv + kTB * (1 + bi - bi_first);
-    float rs[4];
+    const T* svr = sv + kTB * (1 + bi - bi_first);
+    T rs[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) rs[k] = cur[k].x * vc[0] + cur[k].y * vc[1] + cur[k].z * vc[2] + cur[k].w * vc[3];
     if (bi != bj) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const float vr = svr[r0 + 16 * k];
+        const T vr = svr[r0 + 16 * k];
         cacc[0] += cur[k].x * vr;
         cacc[1] += cur[k].y * vr;
         cacc[2] += cur[k].z * vr;
@@ -170,7 +231,7 @@ __global__ __launch_bounds__(kThr) void symv_kernel(const float* __restrict__ A,
       for (int off = 8; off >= 1; off >>= 1) rs[k] += __shfl_xor(rs[k], off, 64);
     }
     if (cq == 0) {
-      const float wgt = bi == bj ? 1.f : 2.f;
+      const T wgt = bi == bj ? 1.f : 2.f;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int rr = r0 + 16 * k;
@@ -183,9 +244,9 @@ __global__ __launch_bounds__(kThr) void symv_kernel(const float* __restrict__ A,
   }
 #pragma unroll
   for (int u = 0; u < 4; ++u) scol[r0][4 * cq + u] = cacc[u];
-  const float vtot = block_sum(vav, red);  // contains the barrier that publishes scol
+  const T vtot = block_sum_t(vav, red);  // contains the barrier that publishes scol
   if (threadIdx.x < kTB) {
-    float s = 0.f;
+    T s = 0.f;
     for (int r = 0; r < 16; ++r) s += scol[r][threadIdx.x];
     Pc[((int64_t)bj * ch_alloc + ch) * kTB + threadIdx.x] = s;
   }
@@ -193,11 +254,12 @@ __global__ __launch_bounds__(kThr) void symv_kernel(const float* __restrict__ A,
 }
 
 // Deterministic work-group sums of three values at once (one set of barriers).
-__device__ __forceinline__ void block_sum3(float& a, float& b, float& c, float (*scratch)[kThr / 64]) {
+template <typename T>
+__device__ __forceinline__ void block_sum3(T& a, T& b, T& c, T (*scratch)[kThr / 64]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  a = wave_sum(a);
-  b = wave_sum(b);
-  c = wave_sum(c);
+  a = wave_sum_t(a);
+  b = wave_sum_t(b);
+  c = wave_sum_t(c);
   __syncthreads();
   if (lane == 0) {
     scratch[0][wave] = a;
@@ -228,17 +290,18 @@ __device__ __forceinline__ void block_sum3(float& a, float& b, float& c, float (
 // g = r + 32 blockIdx + tid / 8: lane k adds the symv partials of strips b0 + k, b0 + k + 8, ...,
 // chunks k, k + 8, ... and the reflectors j = k, k + 8, ...; a fixed butterfly over the eight
 // lanes completes the sums.
-__global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int64_t lda, int64_t n, int64_t c,
-                                                     int64_t i0, int i, int do_next, float* __restrict__ alph,
-                                                     const float* __restrict__ Pn_in, int npn,
-                                                     float* __restrict__ Pn_out, float* __restrict__ Wb,
-                                                     const float* __restrict__ Pr, const float* __restrict__ Pc,
-                                                     const float* __restrict__ Pvv, const float* __restrict__ Ppq,
-                                                     int ch_alloc, int chl, float* __restrict__ D,
-                                                     float* __restrict__ E, float* __restrict__ tau) {
-  __shared__ float red3[3][kThr / 64];
-  __shared__ float spq[4][64];
-  __shared__ float sp[kPB], sq[kPB], svr[kPB], swr[kPB];
+template <typename T>
+__global__ __launch_bounds__(kThr) void finish_kernel(T* __restrict__ A, int64_t lda, int64_t n, int64_t c,
+                                                     int64_t i0, int i, int do_next, T* __restrict__ alph,
+                                                     const T* __restrict__ Pn_in, int npn,
+                                                     T* __restrict__ Pn_out, T* __restrict__ Wb,
+                                                     const T* __restrict__ Pr, const T* __restrict__ Pc,
+                                                     const T* __restrict__ Pvv, const T* __restrict__ Ppq,
+                                                     int ch_alloc, int chl, T* __restrict__ D,
+                                                     T* __restrict__ E, T* __restrict__ tau) {
+  __shared__ T red3[3][kThr / 64];
+  __shared__ T spq[4][64];
+  __shared__ T sp[kPB], sq[kPB], svr[kPB], swr[kPB];
   const int tid = threadIdx.x, k = tid & (kSub - 1);
   const int64_t r = c + 1;
   const int64_t g = r + (int64_t)blockIdx.x * kRowsPB + (tid / kSub);
@@ -249,20 +312,20 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
   const int chy = (ns + chl - 1) / chl;
 
   // column scalars: partial loads
-  float xn2 = 0.f;
+  T xn2 = 0.f;
   for (int t = tid; t < npn; t += kThr) xn2 += Pn_in[t];
-  float pqp = 0.f;
+  T pqp = 0.f;
   {
     const int slot = tid & 63, part = tid >> 6;
-    float v[kDotWG / 4];
+    T v[kDotWG / 4];
 #pragma unroll
     for (int u = 0; u < kDotWG / 4; ++u) v[u] = Ppq[(int64_t)(part * (kDotWG / 4) + u) * 64 + slot];
 #pragma unroll
     for (int u = 0; u < kDotWG / 4; ++u) pqp += v[u];
   }
-  float xux = 0.f;
+  T xux = 0.f;
   for (int base = tid; base < chy * ns; base += kThr * 16) {
-    float v[16];
+    T v[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const int idx = base + u * kThr;
@@ -272,26 +335,26 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
 #pragma unroll
     for (int u = 0; u < 16; ++u) xux += v[u];
   }
-  float ur = 0.f;
+  T ur = 0.f;
   if (tid < chy) ur = Pc[((int64_t)b0 * ch_alloc + tid) * kTB + (r % kTB)];
   if (tid == kThr - 1) ur = Pr[(int64_t)b0 * lda + r];  // chy < kThr - 1 (checked by the host)
   if (tid >= 64 && tid < 64 + i) {
     svr[tid - 64] = A[(i0 + tid - 64) * lda + r];
     swr[tid - 64] = Wb[(int64_t)(tid - 64) * lda + r];
   }
-  const float arr = A[r * lda + r];
+  const T arr = A[r * lda + r];
 
   // own row: symv partials, the earlier reflectors' entries, column r and row c
-  float u = 0.f;
-  float vj[kPB / kSub], wj[kPB / kSub];
+  T u = 0.f;
+  T vj[kPB / kSub], wj[kPB / kSub];
 #pragma unroll
   for (int t = 0; t < kPB / kSub; ++t) vj[t] = wj[t] = 0.f;
-  float a_c = 0.f, a_r = 0.f;
+  T a_c = 0.f, a_r = 0.f;
   if (active) {
     const int s = (int)(g / kTB);
     // up to 32 partials per lane in one batch of loads (one memory round trip up to 256 strips)
     for (int bj0 = b0 + k; bj0 <= s; bj0 += 32 * kSub) {
-      float v[32];
+      T v[32];
 #pragma unroll
       for (int q = 0; q < 32; ++q) {
         const int bj = min(bj0 + kSub * q, s);  // clamped: unconditional loads, then a select
@@ -303,7 +366,7 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
     }
     const int nch = (nblk - s + chl - 1) / chl;
     for (int ch0 = k; ch0 < nch; ch0 += 4 * kSub) {
-      float v[4];
+      T v[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int ch = min(ch0 + kSub * q, nch - 1);
@@ -330,10 +393,10 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
   // column scalars: reductions (fixed order)
   spq[tid >> 6][tid & 63] = pqp;
   block_sum3(xn2, xux, ur, red3);  // its barriers also publish spq, svr, swr
-  const float alpha = alph[c];
-  float tau_c = 0.f, beta = alpha, scale = 0.f;
+  const T alpha = alph[c];
+  T tau_c = 0.f, beta = alpha, scale = 0.f;
   if (xn2 != 0.f) {
-    beta = -copysignf(sqrtf(alpha * alpha + xn2), alpha);
+    beta = -copysign(sqrt(alpha * alpha + xn2), alpha);
     tau_c = (beta - alpha) / beta;
     scale = 1.f / (alpha - beta);
   }
@@ -342,17 +405,17 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
     sq[tid] = svr[tid] + scale * (spq[0][kPB + tid] + spq[1][kPB + tid] + spq[2][kPB + tid] + spq[3][kPB + tid]);
   }
   __syncthreads();
-  const float yr = arr + scale * ur;
-  const float vAv = arr + scale * (2.f * ur + scale * xux);
-  float pq = 0.f, yr_c = yr;
+  const T yr = arr + scale * ur;
+  const T vAv = arr + scale * (2.f * ur + scale * xux);
+  T pq = 0.f, yr_c = yr;
   for (int j = 0; j < i; ++j) {
     pq += sp[j] * sq[j];
     yr_c -= svr[j] * sp[j] + swr[j] * sq[j];
   }
-  const float alpha2 = -0.5f * tau_c * (tau_c * (vAv - 2.f * pq));
-  const float w0 = tau_c * yr_c + alpha2;
+  const T alpha2 = -0.5f * tau_c * (tau_c * (vAv - 2.f * pq));
+  const T w0 = tau_c * yr_c + alpha2;
 
-  float sw = 0.f, su = 0.f;
+  T sw = 0.f, su = 0.f;
 #pragma unroll
   for (int t = 0; t < kPB / kSub; ++t) {
     const int j = k + kSub * t;
@@ -367,14 +430,14 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
     sw += __shfl_xor(sw, off, 64);
     su += __shfl_xor(su, off, 64);
   }
-  float sqv = 0.f;
+  T sqv = 0.f;
   if (active && k == 0) {
-    const float vg = g == r ? 1.f : a_c * scale;
-    const float wg = tau_c * ((a_r + scale * u) - sw) + alpha2 * vg;
+    const T vg = g == r ? 1.f : a_c * scale;
+    const T wg = tau_c * ((a_r + scale * u) - sw) + alpha2 * vg;
     Wb[(int64_t)i * lda + g] = wg;
     A[c * lda + g] = vg;
     if (do_next) {
-      const float a = a_r - (su + (vg * w0 + wg));
+      const T a = a_r - (su + (vg * w0 + wg));
       // A[r][r] is read by every work-group above (arr): the updated diagonal goes to D only
       if (g != r) A[r * lda + g] = a;
       if (g == r) D[r] = a;
@@ -387,7 +450,7 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
     tau[c] = tau_c;
   }
   if (!do_next) return;  // uniform
-  float z1 = 0.f, z2 = 0.f;
+  T z1 = 0.f, z2 = 0.f;
   block_sum3(sqv, z1, z2, red3);
   if (tid == 0) Pn_out[blockIdx.x] = sqv;
 }
@@ -397,8 +460,9 @@ __global__ __launch_bounds__(kThr) void finish_kernel(float* __restrict__ A, int
 // Y (m x nb, row-major, m = n - i0) of reflectors i0 .. i0+nb-1: Y[r'][c] = v_{i0+c}[i0+r'], with
 // v_i[i+1] = 1, v_i[r] = A[i][r] for r > i+1, 0 for r <= i.  Starting the rows at i0 (a multiple
 // of the block size) keeps the GEMM operands 16-byte aligned.
-__global__ __launch_bounds__(256) void extract_y_kernel(const float* __restrict__ A, int64_t lda, int64_t n,
-                                                        int64_t i0, int nb, float* __restrict__ Y) {
+template <typename T>
+__global__ __launch_bounds__(256) void extract_y_kernel(const T* __restrict__ A, int64_t lda, int64_t n,
+                                                        int64_t i0, int nb, T* __restrict__ Y) {
   const int64_t m = n - i0;
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= m * nb) return;
@@ -406,7 +470,7 @@ __global__ __launch_bounds__(256) void extract_y_kernel(const float* __restrict_
   const int c = (int)(e % nb);
   const int64_t r = i0 + rp;
   const int64_t i = i0 + c;
-  float v = 0.f;
+  T v = 0.f;
   if (r == i + 1) v = 1.f;
   else if (r > i + 1) v = A[i * lda + r];
   Y[e] = v;
@@ -418,28 +482,30 @@ __global__ __launch_bounds__(256) void extract_y_kernel(const float* __restrict_
 // needs no 1/tau, so tau = 0 (H = I) gives zero row and column as larft does.  Thread j < nb
 // solves column j of X = (I + N)^{-1} by back substitution, x_k = -sum_{l=k+1..j} N[k][l] x_l,
 // x_j = 1; Tb[k][j] = X[k][j] tau_j.  One work-group, N and X in LDS (2 x 66 KB).
-__global__ __launch_bounds__(256) void larft_kernel(const float* __restrict__ G, const float* __restrict__ tau,
-                                                    int nb, float* __restrict__ Tb) {
-  __shared__ float sN[kNB][kNB + 1];
-  __shared__ float sX[kNB][kNB + 1];
+template <typename T>
+__global__ __launch_bounds__(256) void larft_kernel(const T* __restrict__ G, const T* __restrict__ tau,
+                                                    int nb, T* __restrict__ Tb) {
+  constexpr int NBT = NbOf<T>::value;
+  __shared__ T sN[NBT][NBT + 1];
+  __shared__ T sX[NBT][NBT + 1];
   // 16 global loads in flight per thread (a loop of single loads waits a full memory round trip
   // per element and dominated the kernel)
-  for (int e0 = threadIdx.x; e0 < kNB * kNB; e0 += 256 * 16) {
-    float v[16];
+  for (int e0 = threadIdx.x; e0 < NBT * NBT; e0 += 256 * 16) {
+    T v[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       // unconditional loads from clamped in-range indices (a guarded load becomes a branch that
       // waits for each load in turn), then a select
-      const int e = e0 + 256 * u, k = e / kNB, l = e % kNB;
-      const bool use = e < kNB * kNB && k < l && l < nb;
+      const int e = e0 + 256 * u, k = e / NBT, l = e % NBT;
+      const bool use = e < NBT * NBT && k < l && l < nb;
       const int kc = min(k, nb - 1), lc = min(l, nb - 1);
-      const float g = G[kc * nb + lc] * tau[kc];
+      const T g = G[kc * nb + lc] * tau[kc];
       v[u] = use ? g : 0.f;
     }
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const int e = e0 + 256 * u;
-      if (e < kNB * kNB) sN[e / kNB][e % kNB] = v[u];
+      if (e < NBT * NBT) sN[e / NBT][e % NBT] = v[u];
     }
   }
   __syncthreads();
@@ -449,9 +515,9 @@ __global__ __launch_bounds__(256) void larft_kernel(const float* __restrict__ G,
   // and is unrolled by 8 with four partial sums, so the LDS reads of a chunk overlap.
   const int j = threadIdx.x;
   if (j < nb) {
-    for (int l = 0; l < kNB; ++l) sX[l][j] = l == j ? 1.f : 0.f;
+    for (int l = 0; l < NBT; ++l) sX[l][j] = l == j ? 1.f : 0.f;
     for (int k = nb - 2; k >= 0; --k) {
-      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      T acc[4] = {0.f, 0.f, 0.f, 0.f};
       for (int l = (k + 1) & ~7; l < nb; l += 8) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc[u & 3] += sN[k][l + u] * sX[l + u][j];
@@ -471,12 +537,80 @@ __global__ __launch_bounds__(256) void larft_kernel(const float* __restrict__ G,
 
 namespace {
 
-// Workspace layout of mpq_syevd (float offsets, each region 64-float aligned).
+using mpq::a64;
+
+rocblas_handle get_handle(hipStream_t stream) {
+  static thread_local rocblas_handle hs[16] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return nullptr;
+  if (!hs[dev] && rocblas_create_handle(&hs[dev]) != rocblas_status_success) return nullptr;
+  if (rocblas_set_stream(hs[dev], stream) != rocblas_status_success) return nullptr;
+  return hs[dev];
+}
+
+int rocblas_fail(const char* what) {
+  mpq::set_error("mpq_syevd: %s failed", what);
+  mpq::set_error_code(mpq::kHipError);
+  return mpq::kHipError;
+}
+
+// Row-major C (M x N) = alpha A (M x K) op(B) + beta C, op(B) = B (K x N) or B^T (B: N x K).
+// fp32: this library's MFMA GEMM (split-K partials in P when given); fp64: rocBLAS dgemm on the
+// column-major view, C^T = op(B)^T A^T.
+int gemm_rm(rocblas_handle, const float* A, int64_t lda, const float* B, int64_t ldb, bool trans_b, float* C,
+            int64_t ldc, int64_t M, int64_t N, int64_t K, float alpha, float beta, float* P, int64_t p_floats,
+            hipStream_t stream) {
+  MPQ_HIP_TRY(mpq::gemm(A, lda, B, ldb, trans_b, nullptr, C, ldc, M, N, K, alpha, beta, P, p_floats, stream));
+  return mpq::kOk;
+}
+int gemm_rm(rocblas_handle h, const double* A, int64_t lda, const double* B, int64_t ldb, bool trans_b, double* C,
+            int64_t ldc, int64_t M, int64_t N, int64_t K, double alpha, double beta, double*, int64_t, hipStream_t) {
+  if (rocblas_dgemm(h, trans_b ? rocblas_operation_transpose : rocblas_operation_none, rocblas_operation_none,
+                    (rocblas_int)N, (rocblas_int)M, (rocblas_int)K, &alpha, B, (rocblas_int)ldb, A,
+                    (rocblas_int)lda, &beta, C, (rocblas_int)ldc) != rocblas_status_success)
+    return rocblas_fail("rocblas_dgemm");
+  return mpq::kOk;
+}
+
+// Trailing update A[s0:, s0:] -= [V W] [W V]^T (m x m, K = 2 kPB).  fp32: only the tiles that
+// symv and the column reads use (lower triangle plus a band of kTB - 1 above the diagonal, so the
+// 64 x 64 diagonal tiles are whole); fp64: the whole square on rocBLAS.
+int trailing_update(rocblas_handle, const float* X, const float* Yb, float* C, int64_t ldc, int64_t m,
+                    hipStream_t stream) {
+  using namespace mpq;
+  MPQ_HIP_TRY(gemm_lower(X, 2 * kPB, Yb, 2 * kPB, true, C, ldc, m, 2 * kPB, -1.f, 1.f, kTB - 1, stream));
+  return kOk;
+}
+int trailing_update(rocblas_handle h, const double* X, const double* Yb, double* C, int64_t ldc, int64_t m,
+                    hipStream_t stream) {
+  using namespace mpq;
+  return gemm_rm(h, X, 2 * kPB, Yb, 2 * kPB, true, C, ldc, m, m, 2 * kPB, -1.0, 1.0, nullptr, 0, stream);
+}
+
+rocblas_status stedc(rocblas_handle h, rocblas_int n, float* D, float* E, float* Z, rocblas_int ldz,
+                     rocblas_int* info) {
+  return rocsolver_sstedc(h, rocblas_evect_tridiagonal, n, D, E, Z, ldz, info);
+}
+rocblas_status stedc(rocblas_handle h, rocblas_int n, double* D, double* E, double* Z, rocblas_int ldz,
+                     rocblas_int* info) {
+  return rocsolver_dstedc(h, rocblas_evect_tridiagonal, n, D, E, Z, ldz, info);
+}
+
+template <typename T>
+hipError_t transpose_t(const T* in, int64_t rows, int64_t cols, int64_t ld_in, T* out, int64_t ld_out,
+                       hipStream_t stream) {
+  hipLaunchKernelGGL(mpq::transpose_t_kernel<T>, dim3((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32)),
+                     dim3(256), 0, stream, in, rows, cols, ld_in, out, ld_out);
+  return hipGetLastError();
+}
+
+// Workspace layout of mpq_syevd / mpq_syevd_f64 (element offsets, each region 64 elements aligned).
 struct SyevdLayout {
-  int64_t lda, nblk, ch_alloc, pn_stride, splits;
+  int64_t lda, nblk, ch_alloc, pn_stride, splits, nb;
   int64_t A, Z, Y, Yt, W, W2, G, Tb, P, D, E, tau, alph, Pn, Wb, X, Yb, Pr, Pc, Pvv, Ppq, info, total;
 };
 
+template <typename T>
 SyevdLayout syevd_layout(int64_t n) {
   using namespace mpq;
   SyevdLayout L{};
@@ -484,23 +618,25 @@ SyevdLayout syevd_layout(int64_t n) {
   L.nblk = L.lda / kTB;
   L.ch_alloc = L.nblk;  // chunks of one tile at the smallest chunk length
   L.pn_stride = a64(L.lda / kRowsPB + 2);
-  int bn = 128;
-  L.splits = std::max(choose_splits(n, kNB, n, (int64_t)1 << 62, &bn), 1);
+  L.nb = NbOf<T>::value;
+  int bn = 64;
+  // split-K partials of the fp32 back-transformation GEMMs (rocBLAS needs none)
+  L.splits = sizeof(T) == 4 ? std::max(choose_splits(n, L.nb, n, (int64_t)1 << 62, &bn), 1) : 1;
   int64_t o = 0;
-  auto take = [&](int64_t floats) {
+  auto take = [&](int64_t elems) {
     const int64_t at = o;
-    o += a64(floats);
+    o += a64(elems);
     return at;
   };
   L.A = take(L.lda * L.lda);
   L.Z = take(n * n);
-  L.Y = take(n * kNB);
-  L.Yt = take(n * kNB);
-  L.W = take(n * kNB);
-  L.W2 = take(n * kNB);
-  L.G = take(kNB * kNB);
-  L.Tb = take(kNB * kNB);
-  L.P = take(a64(n * kNB) * L.splits);
+  L.Y = take(n * L.nb);
+  L.Yt = take(n * L.nb);
+  L.W = take(n * L.nb);
+  L.W2 = take(n * L.nb);
+  L.G = take(L.nb * L.nb);
+  L.Tb = take(L.nb * L.nb);
+  L.P = take(sizeof(T) == 4 ? a64(n * L.nb) * L.splits : 64);
   L.D = take(n);
   L.E = take(n);
   L.tau = take(n);
@@ -518,30 +654,31 @@ SyevdLayout syevd_layout(int64_t n) {
   return L;
 }
 
-// A = Q T Q^T for the symmetric A (lda x lda buffer, zero padded, full storage): D, E, tau and
-// the reflectors in the rows of A.  n >= 2.
-int sytrd(int64_t n, const SyevdLayout& L, float* base, hipStream_t stream) {
+// A = Q T Q^T for the symmetric A (lda x lda buffer, zero padded): D, E, tau and the reflectors
+// in the rows of A.  n >= 2.
+template <typename T>
+int sytrd(int64_t n, const SyevdLayout& L, T* base, rocblas_handle h, hipStream_t stream) {
   using namespace mpq;
   const int64_t lda = L.lda;
-  float* A = base + L.A;
-  float* D = base + L.D;
-  float* E = base + L.E;
-  float* tau = base + L.tau;
-  float* alph = base + L.alph;
-  float* Pn = base + L.Pn;
-  float* Wb = base + L.Wb;
-  float* X = base + L.X;
-  float* Yb = base + L.Yb;
-  float* Pr = base + L.Pr;
-  float* Pc = base + L.Pc;
-  float* Pvv = base + L.Pvv;
-  float* Ppq = base + L.Ppq;
+  T* A = base + L.A;
+  T* D = base + L.D;
+  T* E = base + L.E;
+  T* tau = base + L.tau;
+  T* alph = base + L.alph;
+  T* Pn = base + L.Pn;
+  T* Wb = base + L.Wb;
+  T* X = base + L.X;
+  T* Yb = base + L.Yb;
+  T* Pr = base + L.Pr;
+  T* Pc = base + L.Pc;
+  T* Pvv = base + L.Pvv;
+  T* Ppq = base + L.Ppq;
   const int ch_alloc = (int)L.ch_alloc;
-  MPQ_HIP_TRY(hipMemsetAsync(Wb, 0, (size_t)kPB * lda * 4, stream));
+  MPQ_HIP_TRY(hipMemsetAsync(Wb, 0, (size_t)kPB * lda * sizeof(T), stream));
   for (int64_t i0 = 0; i0 < n - 1; i0 += kPB) {
     const int nbl = (int)std::min<int64_t>(kPB, n - 1 - i0);
     int npn = (int)((n - i0 + kThr - 1) / kThr);  // partial norms of the current column
-    hipLaunchKernelGGL(panel_start_kernel, dim3((unsigned)npn), dim3(kThr), 0, stream, A, lda, n, i0, D, alph,
+    hipLaunchKernelGGL(panel_start_kernel<T>, dim3((unsigned)npn), dim3(kThr), 0, stream, A, lda, n, i0, D, alph,
                        Pn + (i0 & 1) * L.pn_stride);
     MPQ_LAUNCH_CHECK();
     for (int i = 0; i < nbl; ++i) {
@@ -558,127 +695,131 @@ int sytrd(int64_t n, const SyevdLayout& L, float* base, hipStream_t stream) {
       }
       // one extra row of work-groups forms the dots p, q
       const dim3 sgrid((unsigned)std::max(ns, kDotWG), (unsigned)(chy + 1));
-      float* pn_in = Pn + (c & 1) * L.pn_stride;
-      float* pn_out = Pn + ((c + 1) & 1) * L.pn_stride;
-      hipLaunchKernelGGL(symv_kernel, sgrid, dim3(kThr), 0, stream, A, lda, n, c, i0, i, Wb, Pr, Pc, Pvv, Ppq,
+      T* pn_in = Pn + (c & 1) * L.pn_stride;
+      T* pn_out = Pn + ((c + 1) & 1) * L.pn_stride;
+      hipLaunchKernelGGL(symv_kernel<T>, sgrid, dim3(kThr), 0, stream, A, lda, n, c, i0, i, Wb, Pr, Pc, Pvv, Ppq,
                          ch_alloc, chl);
       MPQ_LAUNCH_CHECK();
       const int do_next = (i + 1 < nbl) || (c + 1 == n - 1);
       const int fblocks = (int)((n - c - 1 + kRowsPB - 1) / kRowsPB);
-      hipLaunchKernelGGL(finish_kernel, dim3((unsigned)fblocks), dim3(kThr), 0, stream, A, lda, n, c, i0, i, do_next,
-                         alph, pn_in, npn, pn_out, Wb, Pr, Pc, Pvv, Ppq, ch_alloc, chl, D, E, tau);
+      hipLaunchKernelGGL(finish_kernel<T>, dim3((unsigned)fblocks), dim3(kThr), 0, stream, A, lda, n, c, i0, i,
+                         do_next, alph, pn_in, npn, pn_out, Wb, Pr, Pc, Pvv, Ppq, ch_alloc, chl, D, E, tau);
       MPQ_LAUNCH_CHECK();
       npn = fblocks;
     }
     const int64_t s0 = i0 + nbl;
     if (s0 < n - 1) {
-      // trailing update A[s0:, s0:] -= V W^T + W V^T = [V W] [W V]^T (nbl == kPB here), on the
-      // tiles on or below the diagonal: symv reads only those, and the columns are read there
+      // trailing update A[s0:, s0:] -= V W^T + W V^T = [V W] [W V]^T (nbl == kPB here)
       const int64_t m = n - s0;
-      const float* Vp = A + i0 * lda + s0;
-      const float* Wp = Wb + s0;
-      MPQ_HIP_TRY(transpose_matrix(Vp, kPB, m, lda, X, 2 * kPB, stream));
-      MPQ_HIP_TRY(transpose_matrix(Wp, kPB, m, lda, X + kPB, 2 * kPB, stream));
-      MPQ_HIP_TRY(transpose_matrix(Wp, kPB, m, lda, Yb, 2 * kPB, stream));
-      MPQ_HIP_TRY(transpose_matrix(Vp, kPB, m, lda, Yb + kPB, 2 * kPB, stream));
-      // (band kTB - 1 above the diagonal: the 64 x 64 diagonal tiles of symv are read whole)
-      MPQ_HIP_TRY(gemm_lower(X, 2 * kPB, Yb, 2 * kPB, true, A + s0 * lda + s0, lda, m, 2 * kPB, -1.f, 1.f, kTB - 1,
-                             stream));
+      const T* Vp = A + i0 * lda + s0;
+      const T* Wp = Wb + s0;
+      MPQ_HIP_TRY(transpose_t(Vp, kPB, m, lda, X, 2 * kPB, stream));
+      MPQ_HIP_TRY(transpose_t(Wp, kPB, m, lda, X + kPB, 2 * kPB, stream));
+      MPQ_HIP_TRY(transpose_t(Wp, kPB, m, lda, Yb, 2 * kPB, stream));
+      MPQ_HIP_TRY(transpose_t(Vp, kPB, m, lda, Yb + kPB, 2 * kPB, stream));
+      const int rc = trailing_update(h, X, Yb, A + s0 * lda + s0, lda, m, stream);
+      if (rc != kOk) return rc;
     }
   }
   return kOk;
 }
 
-rocblas_handle get_handle(hipStream_t stream) {
-  static thread_local rocblas_handle hs[16] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return nullptr;
-  if (!hs[dev] && rocblas_create_handle(&hs[dev]) != rocblas_status_success) return nullptr;
-  if (rocblas_set_stream(hs[dev], stream) != rocblas_status_success) return nullptr;
-  return hs[dev];
+template <typename T>
+int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  using namespace mpq;
+  MPQ_CHECK_ARG(n > 0 && n <= 46336, "mpq_syevd: n must be in [1, 46336]");
+  static_assert(kDotWG % 4 == 0 && 2 * kPB <= 64 && kPB % kSub == 0, "tridiagonalisation constants");
+  MPQ_CHECK_ARG(H && lam && V && workspace, "mpq_syevd: null pointer");
+  MPQ_CHECK_ARG((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "mpq_syevd: workspace must be 256-byte aligned");
+  const SyevdLayout L = syevd_layout<T>(n);
+  MPQ_CHECK_ARG(workspace_bytes >= L.total * (int64_t)sizeof(T), "mpq_syevd: workspace too small (%lld < %lld)",
+                (long long)workspace_bytes, (long long)(L.total * (int64_t)sizeof(T)));
+  rocblas_handle h = get_handle(stream);
+  MPQ_CHECK_ARG(h != nullptr, "mpq_syevd: rocBLAS handle unavailable");
+  T* base = static_cast<T*>(workspace);
+  T* A = base + L.A;
+  T* Z = base + L.Z;
+  T* Y = base + L.Y;
+  T* Yt = base + L.Yt;
+  T* W = base + L.W;
+  T* W2 = base + L.W2;
+  T* G = base + L.G;
+  T* Tb = base + L.Tb;
+  T* P = base + L.P;
+  T* D = base + L.D;
+  T* E = base + L.E;
+  T* tau = base + L.tau;
+  rocblas_int* info = reinterpret_cast<rocblas_int*>(base + L.info);
+  const int64_t lda = L.lda;
+  const int64_t pfl = L.splits > 1 ? a64(n * L.nb) * L.splits : 0;
+  const int NB = (int)L.nb;
+
+  // 1. tridiagonalise (zero-padded copy, leading dimension lda)
+  MPQ_HIP_TRY(hipMemsetAsync(A, 0, (size_t)(lda * lda) * sizeof(T), stream));
+  MPQ_HIP_TRY(hipMemcpy2DAsync(A, lda * sizeof(T), H, n * sizeof(T), n * sizeof(T), n, hipMemcpyDeviceToDevice,
+                               stream));
+  MPQ_HIP_TRY(hipMemsetAsync(info, 0, sizeof(rocblas_int), stream));
+  if (n == 1) {
+    MPQ_HIP_TRY(hipMemcpyAsync(D, A, sizeof(T), hipMemcpyDeviceToDevice, stream));
+  } else {
+    const int rc = sytrd<T>(n, L, base, h, stream);
+    if (rc != kOk) return rc;
+  }
+  // 2. tridiagonal eigenproblem
+  if (stedc(h, (rocblas_int)n, D, E, Z, (rocblas_int)n, info) != rocblas_status_success)
+    return rocblas_fail("rocsolver stedc");
+  // 3. Z column-major = row-major Zb with Zb = Z^T.  V^T = Zb Q^T, applied block by block:
+  //    Zb[:, i0:] <- Zb[:, i0:] - ((Zb[:, i0:] Y) Tb^T) Y^T
+  const int64_t nrefl = n - 1;
+  for (int64_t i0 = ((nrefl - 1) / NB) * NB; i0 >= 0 && nrefl > 0; i0 -= NB) {
+    const int nb = (int)std::min<int64_t>(NB, nrefl - i0);
+    const int64_t m = n - i0;
+    const int64_t cnt = m * nb;
+    hipLaunchKernelGGL(extract_y_kernel<T>, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, stream, A, lda, n,
+                       i0, nb, Y);
+    MPQ_LAUNCH_CHECK();
+    int rc;
+    MPQ_HIP_TRY(transpose_t(Y, m, nb, nb, Yt, m, stream));
+    if ((rc = gemm_rm(h, Yt, m, Y, nb, false, G, nb, nb, nb, m, T(1), T(0), P, pfl, stream)) != kOk) return rc;
+    hipLaunchKernelGGL(larft_kernel<T>, dim3(1), dim3(256), 0, stream, G, tau + i0, nb, Tb);
+    MPQ_LAUNCH_CHECK();
+    if ((rc = gemm_rm(h, Z + i0, n, Y, nb, false, W, nb, n, nb, m, T(1), T(0), P, pfl, stream)) != kOk) return rc;
+    if ((rc = gemm_rm(h, W, nb, Tb, nb, true, W2, nb, n, nb, nb, T(1), T(0), nullptr, 0, stream)) != kOk) return rc;
+    if ((rc = gemm_rm(h, W2, nb, Y, nb, true, Z + i0, n, n, m, nb, T(-1), T(1), nullptr, 0, stream)) != kOk)
+      return rc;
+  }
+  // V (row-major, columns = eigenvectors) = (Zb)^T
+  MPQ_HIP_TRY(transpose_t(Z, n, n, n, V, n, stream));
+  MPQ_HIP_TRY(hipMemcpyAsync(lam, D, n * sizeof(T), hipMemcpyDeviceToDevice, stream));
+  rocblas_int hinfo = 0;
+  MPQ_HIP_TRY(hipMemcpyAsync(&hinfo, info, sizeof(hinfo), hipMemcpyDeviceToHost, stream));
+  MPQ_HIP_TRY(hipStreamSynchronize(stream));
+  if (hinfo != 0) {
+    set_error("rocsolver stedc did not converge (info = %d)", (int)hinfo);
+    set_error_code(kNumerical);
+    return kNumerical;
+  }
+  return kOk;
 }
 
 }  // namespace
 
 extern "C" int64_t mpq_syevd_workspace_size(int64_t n) {
   if (n <= 0) return 0;
-  return syevd_layout(n).total * 4;
+  return syevd_layout<float>(n).total * 4;
 }
 
 extern "C" int mpq_syevd(int64_t n, const float* H, float* lam, float* V, void* workspace, int64_t workspace_bytes,
                          hipStream_t stream) {
-  using namespace mpq;
-  MPQ_CHECK_ARG(n > 0 && n <= 46336, "mpq_syevd: n must be in [1, 46336]");
-  static_assert(kDotWG % 4 == 0 && 2 * kPB <= 64 && kPB % kSub == 0, "tridiagonalisation constants");
-  MPQ_CHECK_ARG(H && lam && V && workspace, "mpq_syevd: null pointer");
-  MPQ_CHECK_ARG((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "mpq_syevd: workspace must be 256-byte aligned");
-  MPQ_CHECK_ARG(workspace_bytes >= mpq_syevd_workspace_size(n), "mpq_syevd: workspace too small (%lld < %lld)",
-                (long long)workspace_bytes, (long long)mpq_syevd_workspace_size(n));
-  rocblas_handle h = get_handle(stream);
-  MPQ_CHECK_ARG(h != nullptr, "mpq_syevd: rocBLAS handle unavailable");
-  const SyevdLayout L = syevd_layout(n);
-  float* base = static_cast<float*>(workspace);
-  float* A = base + L.A;
-  float* Z = base + L.Z;
-  float* Y = base + L.Y;
-  float* Yt = base + L.Yt;
-  float* W = base + L.W;
-  float* W2 = base + L.W2;
-  float* G = base + L.G;
-  float* Tb = base + L.Tb;
-  float* P = base + L.P;
-  float* D = base + L.D;
-  float* E = base + L.E;
-  float* tau = base + L.tau;
-  rocblas_int* info = reinterpret_cast<rocblas_int*>(base + L.info);
-  const int64_t lda = L.lda;
-  const int64_t pstride = a64(n * kNB);
+  return syevd_impl<float>(n, H, lam, V, workspace, workspace_bytes, stream);
+}
 
-  // 1. tridiagonalise (zero-padded copy, leading dimension lda)
-  MPQ_HIP_TRY(hipMemsetAsync(A, 0, (size_t)(lda * lda) * 4, stream));
-  MPQ_HIP_TRY(hipMemcpy2DAsync(A, lda * 4, H, n * 4, n * 4, n, hipMemcpyDeviceToDevice, stream));
-  MPQ_HIP_TRY(hipMemsetAsync(info, 0, sizeof(rocblas_int), stream));
-  if (n == 1) {
-    MPQ_HIP_TRY(hipMemcpyAsync(D, A, 4, hipMemcpyDeviceToDevice, stream));
-  } else {
-    const int rc = sytrd(n, L, base, stream);
-    if (rc != kOk) return rc;
-  }
-  // 2. tridiagonal eigenproblem
-  if (rocsolver_sstedc(h, rocblas_evect_tridiagonal, (rocblas_int)n, D, E, Z, (rocblas_int)n, info) !=
-      rocblas_status_success) {
-    set_error("rocsolver_sstedc failed");
-    set_error_code(kHipError);
-    return kHipError;
-  }
-  // 3. Z column-major = row-major Zb with Zb = Z^T.  V^T = Zb Q^T, applied block by block:
-  //    Zb[:, i0:] <- Zb[:, i0:] - ((Zb[:, i0:] Y) Tb^T) Y^T
-  const int64_t nrefl = n - 1;
-  for (int64_t i0 = ((nrefl - 1) / kNB) * kNB; i0 >= 0 && nrefl > 0; i0 -= kNB) {
-    const int nb = (int)std::min<int64_t>(kNB, nrefl - i0);
-    const int64_t m = n - i0;
-    const int64_t cnt = m * nb;
-    hipLaunchKernelGGL(extract_y_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, stream, A, lda, n, i0, nb,
-                       Y);
-    MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(transpose_matrix(Y, m, nb, nb, Yt, m, stream));
-    MPQ_HIP_TRY(gemm(Yt, m, Y, nb, false, nullptr, G, nb, nb, nb, m, 1.f, 0.f, P, pstride * L.splits, stream));
-    hipLaunchKernelGGL(larft_kernel, dim3(1), dim3(256), 0, stream, G, tau + i0, nb, Tb);
-    MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(gemm(Z + i0, n, Y, nb, false, nullptr, W, nb, n, nb, m, 1.f, 0.f, P, pstride * L.splits, stream));
-    MPQ_HIP_TRY(gemm(W, nb, Tb, nb, true, nullptr, W2, nb, n, nb, nb, 1.f, 0.f, nullptr, 0, stream));
-    MPQ_HIP_TRY(gemm(W2, nb, Y, nb, true, nullptr, Z + i0, n, n, m, nb, -1.f, 1.f, nullptr, 0, stream));
-  }
-  // V (row-major, columns = eigenvectors) = (Zb)^T
-  MPQ_HIP_TRY(transpose_matrix(Z, n, n, n, V, n, stream));
-  MPQ_HIP_TRY(hipMemcpyAsync(lam, D, n * 4, hipMemcpyDeviceToDevice, stream));
-  rocblas_int hinfo = 0;
-  MPQ_HIP_TRY(hipMemcpyAsync(&hinfo, info, sizeof(hinfo), hipMemcpyDeviceToHost, stream));
-  MPQ_HIP_TRY(hipStreamSynchronize(stream));
-  if (hinfo != 0) {
-    set_error("rocsolver_sstedc did not converge (info = %d)", (int)hinfo);
-    set_error_code(kNumerical);
-    return kNumerical;
-  }
-  return kOk;
+extern "C" int64_t mpq_syevd_f64_workspace_size(int64_t n) {
+  if (n <= 0) return 0;
+  return syevd_layout<double>(n).total * 8;
+}
+
+extern "C" int mpq_syevd_f64(int64_t n, const double* H, double* lam, double* V, void* workspace,
+                             int64_t workspace_bytes, hipStream_t stream) {
+  return syevd_impl<double>(n, H, lam, V, workspace, workspace_bytes, stream);
 }

@@ -178,17 +178,20 @@ def scale_columns(X: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
 
 
 def syevd(H: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Eigendecomposition of a symmetric fp32 matrix: (lam ascending, V with eigenvectors as columns)."""
+    """Eigendecomposition of a symmetric matrix: (lam ascending, V with eigenvectors as columns).
+    float64 input runs in fp64 (mpq_syevd_f64), anything else in fp32 (mpq_syevd)."""
     dev = _dev(H)
-    H = _f32c(H)
+    f64 = H.dtype == torch.float64
+    H = H.contiguous() if f64 else _f32c(H)
     n = int(H.shape[0])
     if tuple(H.shape) != (n, n):
         raise ValueError("H must be square")
     lib = _lib.load()
-    ws = workspace(int(lib.mpq_syevd_workspace_size(n)), dev)
-    lam = torch.empty(n, dtype=F32, device=dev)
-    V = torch.empty(n, n, dtype=F32, device=dev)
-    _lib.call("mpq_syevd", n, _lib.ptr(H), _lib.ptr(lam), _lib.ptr(V), _lib.ptr(ws), int(ws.numel()), _stream(dev))
+    name = "mpq_syevd_f64" if f64 else "mpq_syevd"
+    ws = workspace(int(getattr(lib, name + "_workspace_size")(n)), dev)
+    lam = torch.empty(n, dtype=H.dtype, device=dev)
+    V = torch.empty(n, n, dtype=H.dtype, device=dev)
+    _lib.call(name, n, _lib.ptr(H), _lib.ptr(lam), _lib.ptr(V), _lib.ptr(ws), int(ws.numel()), _stream(dev))
     return lam, V
 
 

@@ -43,3 +43,32 @@ def test_syevd_small_and_diagonal(gpu):
         assert float((lam.cpu().double() - ref).abs().max()) <= 1e-5 * max(1.0, float(ref.abs().max()))
         resid, orth = _quality(H, lam, V)
         assert resid < 1e-5 and orth < 1e-5, (H.shape, resid, orth)
+
+
+@pytest.mark.parametrize("n", [200, 1000, 2048])
+def test_syevd_f64_matches_lapack(gpu, n):
+    # fp64 path (the QUIP# adapter's float64 Hessian): eigenvalues, residual and orthogonality at
+    # fp64 accuracy against LAPACK on the CPU
+    _, H = make_layer(8, n, tokens=2 * n, seed_key=f"eigh64:{n}")
+    H = H.double()
+    H = 0.5 * (H + H.T)  # exactly symmetric in fp64, as the adapter passes it (both solvers read one triangle)
+    lam, V = ops.syevd(H.to(gpu))
+    assert lam.dtype == torch.float64 and V.dtype == torch.float64
+    lam, V = lam.cpu(), V.cpu()
+    ref = torch.linalg.eigvalsh(H)
+    scale = float(ref.abs().max())
+    assert float((lam - ref).abs().max()) <= 1e-11 * scale
+    assert bool((lam[1:] >= lam[:-1]).all())
+    resid = float((H @ V - V * lam.unsqueeze(0)).norm() / H.norm())
+    orth = float((V.T @ V - torch.eye(n, dtype=torch.float64)).abs().max())
+    assert resid < 1e-12 and orth < 1e-12, (resid, orth)
+
+
+def test_syevd_f64_small(gpu):
+    for H in (torch.tensor([[3.0]], dtype=torch.float64), torch.diag(torch.arange(70, dtype=torch.float64)),
+              torch.eye(65, dtype=torch.float64) * 2.0):
+        lam, V = ops.syevd(H.to(gpu))
+        ref = torch.linalg.eigvalsh(H)
+        assert float((lam.cpu() - ref).abs().max()) <= 1e-12 * max(1.0, float(ref.abs().max()))
+        Vc = V.cpu()
+        assert float((Vc.T @ Vc - torch.eye(H.shape[0], dtype=torch.float64)).abs().max()) < 1e-12
