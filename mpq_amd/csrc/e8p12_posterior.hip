@@ -29,11 +29,18 @@ constexpr int kLanes = 8;  // lanes per 8-block
 
 __device__ __forceinline__ int slot_of(int abs2) { return abs2 >> 1; }  // 1->0, 3->1, 5->2
 
-__device__ __forceinline__ float log1mexp_f(float x) {
-  // log(1 - exp(x)), x <= 0 (mpq/priors/e8p12.py:213-219)
-  const float cutoff = -0.69314718055994530942f;
-  return x < cutoff ? log1pf(-expf(x)) : logf(-expm1f(x));
-}
+// log(1 - exp(x)) for x <= 0 switches from log1p(-exp(x)) to log(-expm1(x)) at -log 2
+// (mpq/priors/e8p12.py:213-219)
+constexpr float kLog1mexpCut = -0.69314718055994530942f;
+
+// Hardware exp2 / log2 (v_exp_f32, v_log_f32: 1 ulp on the base-2 result) with the base change
+// folded in.  exp(x) then has a relative error of about |x| * 2^-24 (6e-6 at the largest mixture
+// exponents, |x| < 88, beyond which the weight underflows anyway); log(1 + y), y in [0, 1], an
+// absolute error of about 1e-7.  Used for the mixture log-weights and weights, where the
+// tolerance is 1e-4 relative on the posterior means; the cancelling log(-expm1(x)) near x = 0
+// keeps the accurate library functions.
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f); }
+__device__ __forceinline__ float fast_log(float y) { return __builtin_amdgcn_logf(y) * 0.69314718055994530942f; }
 
 // Merge of two partial online-softmax states (running max m, sum Z, first moments mu, second
 // moment sec, offset weight wo).  Symmetric in its arguments, so both lanes of a butterfly pair
@@ -178,21 +185,26 @@ __global__ __launch_bounds__(kThreads) void e8p12_posterior_kernel(
         L = L + s_lt[sl[i]][bl];
       }
       const bool neg = (__builtin_popcount(negmask & bm) & 1) != 0;
-      // log(1 + prod t) for an even base, log(1 - prod t) for an odd base
+      // log(1 + prod t) for an even base, log(1 - prod t) for an odd base; |prod t| = exp(L) is
+      // evaluated once and shared with the sign means below
       const bool plus_branch = even != neg;
-      const float lz = plus_branch ? log1pf(expf(L)) : log1mexp_f(L);
+      const float pabs = fast_exp(L);
+      const float lz = plus_branch ? fast_log(1.0f + pabs)
+                                   : (L < kLog1mexpCut ? fast_log(1.0f - pabs) : logf(-expm1f(L)));
       const float logZs = (logC + lz) - kLog2;
       const float sq = s_sq[k];
       const float lcomp = mhalf_g * (yn + sq) + logZs;
-      const float mnew = fmaxf(st.m, lcomp);
-      const float resc = expf(st.m - mnew);
-      const float wgt = expf(lcomp - mnew);
-      st.m = mnew;
+      // online softmax: the larger of (running max, new log-weight) contributes exp(0) = 1, so one
+      // exponential per component gives the same bits as exp(m - max) and exp(lcomp - max)
+      const bool up = lcomp > st.m;
+      const float e = fast_exp(up ? st.m - lcomp : lcomp - st.m);
+      const float resc = up ? e : 1.0f;
+      const float wgt = up ? 1.0f : e;
+      st.m = up ? lcomp : st.m;
       // sign means with prefix / suffix products (mpq/priors/e8p12.py:235-255)
       float tt[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) tt[i] = s_t[sl[i]][bl];
-      const float pabs = expf(L);
       const float prod = neg ? -pabs : pabs;
       float denom = even ? 1.0f + prod : 1.0f - prod;
       denom = fabsf(denom) > 1e-12f ? denom : 1.0f;
