@@ -111,16 +111,20 @@ def run_layer(rows, cols, module, H_gptq, W, steps, warmup, bits=3):
     from mpq_amd.adapters.gptqmodel import GPTQAdapterConfig, run_mpq_quantization
     from mpq_amd.solver import UniformVampConfig
 
+    from mpq_amd.adapters.gptqmodel import clear_eigen_cache
+
     vcfg = UniformVampConfig(iters=16, damping=0.5, prior_tau=0.2, polish_sweeps=3, polish_mode="block_cd")
     qcfg = QCfg(bits, 128, "internal_hadamard")
     acfg = GPTQAdapterConfig(block_rows=128)
     res = None
     for _ in range(warmup):
+        clear_eigen_cache()
         res = run_mpq_quantization(W=W, H=H_gptq, quantizer=None, qcfg=qcfg, module_name=module, vamp_cfg=vcfg,
                                    adapter_cfg=acfg)
     torch.cuda.synchronize()
     times = []
     for _ in range(steps):
+        clear_eigen_cache()  # every timed solve computes its own eigendecomposition
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         res = run_mpq_quantization(W=W, H=H_gptq, quantizer=None, qcfg=qcfg, module_name=module, vamp_cfg=vcfg,
@@ -131,6 +135,39 @@ def run_layer(rows, cols, module, H_gptq, W, steps, warmup, bits=3):
     blocks = [(min(128, rows - r0), it) for r0, it in zip(range(0, rows, 128), stats["vamp_iters_entered"])]
     return {"ms": 1e3 * sum(times) / len(times), "times_ms": [1e3 * t for t in times], "stats": stats,
             "flop": layer_flops(rows, cols, blocks), "result": res}
+
+
+def set_pass(specs, weights, device, warmup):
+    """One pass over a layer's linears in pipeline order, each through the whole adapter, from an
+    empty eigendecomposition cache: linears that share their input (q/k/v, gate/up) reuse the
+    decomposition of the identical Hessian, as a real quantization pass does."""
+    import torch
+
+    from mpq_amd.adapters.gptqmodel import GPTQAdapterConfig, clear_eigen_cache, run_mpq_quantization
+    from mpq_amd.solver import UniformVampConfig
+
+    vcfg = UniformVampConfig(iters=16, damping=0.5, prior_tau=0.2, polish_sweeps=3, polish_mode="block_cd")
+    qcfg = QCfg(3, 128, "internal_hadamard")
+    acfg = GPTQAdapterConfig(block_rows=128)
+    clear_eigen_cache()
+    linears = {}
+    gate_run = None
+    t_all = 0.0
+    for (name, block, rows, cols, Hx), Wx in zip(specs, weights):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        res = run_mpq_quantization(W=Wx, H=Hx, quantizer=None, qcfg=qcfg, module_name=f"model.layers.0.{block}.{name}",
+                                   vamp_cfg=vcfg, adapter_cfg=acfg)
+        torch.cuda.synchronize()
+        dt = 1e3 * (time.perf_counter() - t0)
+        t_all += dt
+        st = res[6]
+        linears[name] = {"ms": round(dt, 3), "shape": f"{rows}x{cols}", "breakdown_s": st["timings"]}
+        if name == "gate_proj":
+            blocks = [(min(128, rows - r0), it) for r0, it in zip(range(0, rows, 128), st["vamp_iters_entered"])]
+            gate_run = {"ms": dt, "stats": st, "flop": layer_flops(rows, cols, blocks)}
+    clear_eigen_cache()
+    return {"ms": round(t_all, 3), "linears": linears, "gate_run": gate_run, "warmup": warmup}
 
 
 def gemm_roofline(n, device, reps=20, warmup=100):
@@ -442,14 +479,25 @@ def main():
     from mpq_amd.adapters.gptqmodel import resolve_internal_rotation, vamp_hessian_eigen  # noqa: F401
 
     gate = None
+    layer_set = None
     if not args.no_gate_up:
-        log("== timing gate/up (14336 x 4096)")
-        Wg = make_weight(14336, 4096, 21, dev)
-        Hg2 = 2.0 * make_hessian(4096, args.tokens, 22, dev)
-        gate = run_layer(14336, 4096, "model.layers.0.mlp.gate_proj", Hg2, Wg, args.steps, args.warmup)
-        log(json.dumps({k: v for k, v in gate.items() if k in ("ms", "times_ms", "flop")}),
-            json.dumps(gate["stats"]["timings"]))
-        del Wg, Hg2
+        # The rest of one Llama-3-8B layer's linears (config 4's "full per-layer set"): q/k/v share
+        # the attention-input Hessian, gate/up the MLP-input one, o has its own; down is the
+        # headline measurement above.  Every linear runs the whole adapter (its own eigh included).
+        log("== timing the layer set (q, k, v, o, gate, up, down)")
+        H_attn = 2.0 * make_hessian(4096, args.tokens, 22, dev)
+        H_o = 2.0 * make_hessian(4096, args.tokens, 23, dev)
+        H_mlp = 2.0 * make_hessian(4096, args.tokens, 24, dev)
+        specs = [("q_proj", "self_attn", 4096, 4096, H_attn), ("k_proj", "self_attn", 1024, 4096, H_attn),
+                 ("v_proj", "self_attn", 1024, 4096, H_attn), ("o_proj", "self_attn", 4096, 4096, H_o),
+                 ("gate_proj", "mlp", 14336, 4096, H_mlp), ("up_proj", "mlp", 14336, 4096, H_mlp),
+                 ("down_proj", "mlp", 4096, 14336, Hg)]
+        weights = [make_weight(rows, cols, 31 + i, dev) for i, (_, _, rows, cols, _) in enumerate(specs)]
+        layer_set = set_pass(specs, weights, dev, warmup=True)
+        layer_set = set_pass(specs, weights, dev, warmup=False)
+        gate = layer_set.pop("gate_run")
+        log("layer set", json.dumps({k: v["ms"] for k, v in layer_set["linears"].items()}), layer_set["ms"])
+        del H_attn, H_o, H_mlp, weights
 
     e8l = None
     if not args.no_e8p12_layer:
@@ -517,6 +565,11 @@ def main():
         "layer_breakdown_s": down["stats"]["timings"],
         "proxy_loss": down["stats"]["proxy_loss"],
         "vamp_iters_entered": down["stats"]["vamp_iters_entered"],
+        "layer_set": None if layer_set is None else dict(
+            {k: v for k, v in layer_set.items() if k != "warmup"},
+            workload="BASELINE config 4: one Llama-3-8B layer's q, k, v, o, gate, up, down, 3-bit, group 128, "
+                     "internal Hadamard, VAMP + 3 CD sweeps, one timed pass in pipeline order after a warm-up "
+                     "pass; k/v reuse q's eigendecomposition and up reuses gate's (identical Hessians)"),
         "gate_up": None if gate is None else {"ms": round(gate["ms"], 3), "rows": 14336, "cols": 4096,
                                               "breakdown_s": gate["stats"]["timings"],
                                               "fp32_tflops": round(gate["flop"] / (gate["ms"] / 1e3) / 1e12, 2)},

@@ -49,6 +49,7 @@ class GPTQAdapterConfig:
     eigen_floor_scale: float = 1e-6
     rotation_seed: int = 0
     auto_block_rows: bool = False
+    eigen_cache: bool = True  # reuse the decomposition of an identical Hessian (q/k/v, gate/up)
 
 
 class MinMaxQuantizer:
@@ -87,19 +88,42 @@ def resolve_internal_rotation(*, requested: str, cols: int, module_name: str, se
             "signs": signs, "block_dim": int(block_dim), "fallback_reason": "", "internal": True}
 
 
+# The most recent eigendecomposition per device.  The linears of one block that read the same
+# input (q/k/v, gate/up) carry identical Hessians; their decomposition is reused when the
+# symmetrized matrix is element-for-element equal, which returns exactly the bits a fresh
+# computation would (the solver is deterministic).  The entries are read-only to callers.
+_EIGEN_CACHE: Dict[Any, Tuple[torch.Tensor, Tuple[float, float], tuple]] = {}
+
+
+def clear_eigen_cache() -> None:
+    """Drop the cached eigendecompositions (and the Hessian copies they are keyed on)."""
+    _EIGEN_CACHE.clear()
+
+
 @torch.inference_mode()
-def vamp_hessian_eigen(H: torch.Tensor, *, jitter_base: float = 1e-6, floor_scale: float = 1e-6):
+def vamp_hessian_eigen(H: torch.Tensor, *, jitter_base: float = 1e-6, floor_scale: float = 1e-6,
+                       use_cache: bool = True):
     """Floored descending eigendecomposition (reference :276-310).  Returns (lam, S, V, Vs, floor)."""
     Hs = 0.5 * (H + H.T)
     if not bool(torch.isfinite(Hs).all()):
         Hs = torch.nan_to_num(Hs, nan=0.0, posinf=0.0, neginf=0.0)
+    key = (Hs.device, tuple(Hs.shape))
+    params = (float(jitter_base), float(floor_scale))
+    if use_cache:
+        hit = _EIGEN_CACHE.get(key)
+        if hit is not None and hit[1] == params and hit[0].dtype == Hs.dtype and torch.equal(hit[0], Hs):
+            return hit[2]
     lam_asc, V_asc = ops.syevd(Hs)
     max_lam = float(lam_asc[-1].item()) if lam_asc.numel() else 0.0
     diag_mean = float(torch.diagonal(Hs).mean().abs().item()) if Hs.numel() else 0.0
     floor = max(float(jitter_base), float(floor_scale) * max(diag_mean, max_lam, 1e-12))
     lam, S, V, Vs = ops.eigh_postprocess(lam_asc, V_asc, floor)
     del V_asc
-    return lam, S, V, Vs, float(floor)
+    out = (lam, S, V, Vs, float(floor))
+    if use_cache:
+        _EIGEN_CACHE.clear()  # one entry: the newest decomposition
+        _EIGEN_CACHE[key] = (Hs, params, out)
+    return out
 
 
 def _resolve_block_rows(rows: int, cols: int, maxq: int, requested: int, device: torch.device, auto: bool) -> int:
@@ -167,7 +191,8 @@ def run_mpq_quantization(
         eigen_floor = float(lam.min().item())
     else:
         lam, S, V, Vs, eigen_floor = vamp_hessian_eigen(H_work, jitter_base=adapter_cfg.jitter_base,
-                                                        floor_scale=adapter_cfg.eigen_floor_scale)
+                                                        floor_scale=adapter_cfg.eigen_floor_scale,
+                                                        use_cache=bool(adapter_cfg.eigen_cache))
     torch.cuda.synchronize(device)
     timings["eigh_s"] = time.time() - t0
     signs = rotation["signs"]
@@ -189,7 +214,8 @@ def run_mpq_quantization(
         H_metric[dead, dead] = 1
         W_work[:, dead] = 0
         lam, S, V, Vs, eigen_floor = vamp_hessian_eigen(H_metric, jitter_base=adapter_cfg.jitter_base,
-                                                        floor_scale=adapter_cfg.eigen_floor_scale)
+                                                        floor_scale=adapter_cfg.eigen_floor_scale,
+                                                        use_cache=bool(adapter_cfg.eigen_cache))
 
     # group parameters in the solver basis
     if quantizer is not None and hasattr(quantizer, "find_params") and not isinstance(quantizer, MinMaxQuantizer):

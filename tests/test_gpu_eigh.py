@@ -72,3 +72,28 @@ def test_syevd_f64_small(gpu):
         assert float((lam.cpu() - ref).abs().max()) <= 1e-12 * max(1.0, float(ref.abs().max()))
         Vc = V.cpu()
         assert float((Vc.T @ Vc - torch.eye(H.shape[0], dtype=torch.float64)).abs().max()) < 1e-12
+
+
+def test_eigen_cache_exact_match_only(gpu):
+    # the adapter reuses the decomposition of an element-for-element identical Hessian (q/k/v,
+    # gate/up) and recomputes for any other input or floor parameters
+    from mpq_amd.adapters.gptqmodel import clear_eigen_cache, vamp_hessian_eigen
+
+    _, H = make_layer(8, 256, tokens=512, seed_key="eigen-cache")
+    H = H.to(gpu)
+    clear_eigen_cache()
+    a = vamp_hessian_eigen(H)
+    b = vamp_hessian_eigen(H.clone())
+    assert all(x is y for x, y in zip(a[:4], b[:4])) and a[4] == b[4]
+    H2 = H.clone()
+    H2[3, 5] += 1e-3
+    H2[5, 3] += 1e-3
+    c = vamp_hessian_eigen(H2)
+    assert c[2] is not a[2]
+    assert float((c[0] - a[0]).abs().max()) > 0.0
+    d = vamp_hessian_eigen(H2, floor_scale=1e-3)
+    assert d[2] is not c[2]
+    e = vamp_hessian_eigen(H2, floor_scale=1e-3, use_cache=False)
+    assert e[2] is not d[2]
+    assert torch.equal(e[2], d[2]) and torch.equal(e[0], d[0])  # deterministic: same bits either way
+    clear_eigen_cache()
