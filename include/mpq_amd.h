@@ -120,7 +120,10 @@ int64_t mpq_e8p12_vamp_workspace_size(int64_t rows, int64_t n);
  *   prior_scale: rows*n/8 block scales (NULL: absmax of each Wr block)
  *   idx_out: rows x n/8 int64 codeword indices, hat_out rows x n codewords,
  *   err_out (rows), r1_out (rows x n), gamma1_out (rows): optional
- * Synchronises `stream` twice per iteration to read small status blocks.
+ * Waits twice per iteration for `stream` to drain up to a small status block, which a
+ * one-thread kernel publishes into mapped pinned host memory (the host spins on a sequence
+ * number; after 20 s it falls back to hipStreamSynchronize).  Output copies issued after
+ * the last wait stay asynchronous on `stream`.
  */
 int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, const float* hat_init,
                          const float* V, const float* S, const float* Vs, const float* prior_scale,
@@ -376,7 +379,10 @@ int64_t mpq_uniform_vamp_workspace_size(int64_t rows, int64_t n);
  *   V, Vs: n x n (full rank), S: n
  *   obs_init > 0 overrides the warm start of the observation precision
  *   q_out (rows x n uint8), x_out (optional), err_out (rows), rtn_err_out (rows, optional)
- * Synchronises `stream` twice per iteration to read small status blocks.
+ * Waits twice per iteration for `stream` to drain up to a small status block, which a
+ * one-thread kernel publishes into mapped pinned host memory (the host spins on a sequence
+ * number; after 20 s it falls back to hipStreamSynchronize).  Output copies issued after
+ * the last wait stay asynchronous on `stream`.
  */
 int mpq_uniform_vamp_solve(int64_t rows, int64_t n, int maxq, const float* W, int64_t ldw,
                            const float* x_init, const float* scale, const float* zero,

@@ -140,11 +140,9 @@ extern "C" int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, co
   const dim3 eg((unsigned)nchunks, (unsigned)rows), eb(kEW);
   const float tau = cfg->prior_tau;
   const float* center = tau > 0.f ? Wr : nullptr;
-  auto sync_status = [&]() -> int {
-    MPQ_HIP_TRY(hipMemcpyAsync(hs, status, sizeof(VampStatus), hipMemcpyDeviceToHost, stream));
-    MPQ_HIP_TRY(hipStreamSynchronize(stream));
-    return kOk;
-  };
+  HostMailbox* mb = host_mailbox();
+  MPQ_CHECK_ARG(mb != nullptr, "E8P12 VAMP: mapped status mailbox unavailable");
+  auto sync_status = [&]() -> int { return read_status(mb, status, hs, stream); };
   int rc;
   // MAP decision of (r, g) into midx / mvals and its rank-space error into errrow / status.err_mean
   auto map_state = [&](const float* r, const float* g) -> int {

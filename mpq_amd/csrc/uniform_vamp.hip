@@ -275,11 +275,9 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
   float* err_cur = w.rowbuf + 12 * rows;
   float* err_best = w.rowbuf + 13 * rows;
 
-  auto sync_status = [&]() -> int {
-    MPQ_HIP_TRY(hipMemcpyAsync(hs, w.status, sizeof(VampStatus), hipMemcpyDeviceToHost, stream));
-    MPQ_HIP_TRY(hipStreamSynchronize(stream));
-    return kOk;
-  };
+  HostMailbox* mb = host_mailbox();
+  MPQ_CHECK_ARG(mb != nullptr, "uniform VAMP: mapped status mailbox unavailable");
+  auto sync_status = [&]() -> int { return read_status(mb, w.status, hs, stream); };
   const float tau = cfg.prior_tau;
   int rc;
 

@@ -4,6 +4,9 @@
 // reference's operation order (mpq/solver.py:426-703, :961-1122; mpq/linear.py).
 #pragma once
 
+#include <chrono>
+#include <cstring>
+
 #include "common.h"
 
 namespace mpq {
@@ -32,6 +35,75 @@ struct VampStatus {
   float err_sum;
   float pad2, pad3, pad4;
 };
+
+// Status handshake with the host.  The drivers read the status twice per iteration; instead of a
+// device-to-host copy plus a stream synchronisation, a one-thread kernel copies the status into
+// mapped, coherent pinned host memory and then publishes a sequence number behind a system-scope
+// fence, and the host spins on that number.  The wait is bounded: past a time limit the host falls
+// back to hipStreamSynchronize, which returns any error of the stream's earlier work.
+struct StatusMailbox {
+  VampStatus st;
+  unsigned seq;
+  unsigned pad[15];
+};
+
+__global__ __launch_bounds__(64) void publish_status_kernel(const VampStatus* __restrict__ src,
+                                                            StatusMailbox* __restrict__ box, unsigned seq) {
+  if (threadIdx.x == 0) {
+    box->st = *src;
+    __threadfence_system();
+    __hip_atomic_store(&box->seq, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
+struct HostMailbox {
+  StatusMailbox* h = nullptr;  // host view
+  StatusMailbox* d = nullptr;  // device view of the same pages
+  unsigned seq = 0;
+};
+
+// One mailbox per host thread (allocated once, kept for the thread's lifetime).
+inline HostMailbox* host_mailbox() {
+  static thread_local HostMailbox mb;
+  if (mb.h == nullptr) {
+    StatusMailbox* h = nullptr;
+    if (hipHostMalloc((void**)&h, sizeof(StatusMailbox),
+                      hipHostMallocMapped | hipHostMallocCoherent | hipHostMallocPortable) != hipSuccess)
+      return nullptr;
+    std::memset(h, 0, sizeof(StatusMailbox));
+    StatusMailbox* d = nullptr;
+    if (hipHostGetDevicePointer((void**)&d, h, 0) != hipSuccess) {
+      (void)hipHostFree(h);
+      return nullptr;
+    }
+    mb.h = h;
+    mb.d = d;
+  }
+  return &mb;
+}
+
+// Copy the device status to *out once every earlier operation on `stream` has completed.
+inline int read_status(HostMailbox* mb, const VampStatus* dstatus, VampStatus* out, hipStream_t stream) {
+  const unsigned seq = ++mb->seq;
+  hipLaunchKernelGGL(publish_status_kernel, dim3(1), dim3(64), 0, stream, dstatus, mb->d, seq);
+  MPQ_LAUNCH_CHECK();
+  const auto t0 = std::chrono::steady_clock::now();
+  unsigned spins = 0;
+  while (__atomic_load_n(&mb->h->seq, __ATOMIC_ACQUIRE) != seq) {
+    __builtin_ia32_pause();
+    if ((++spins & 4095u) == 0 && std::chrono::steady_clock::now() - t0 > std::chrono::seconds(20)) {
+      MPQ_HIP_TRY(hipStreamSynchronize(stream));
+      if (__atomic_load_n(&mb->h->seq, __ATOMIC_ACQUIRE) != seq) {
+        set_error("VAMP status handshake: the status kernel completed but its sequence number did not arrive");
+        set_error_code(kHipError);
+        return kHipError;
+      }
+      break;
+    }
+  }
+  std::memcpy(out, &mb->h->st, sizeof(VampStatus));
+  return kOk;
+}
 
 __device__ __forceinline__ float grp(const float* a, int64_t b, int64_t G, int64_t gs, int64_t j) {
   return a[b * G + j / gs];
