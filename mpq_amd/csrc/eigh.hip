@@ -103,6 +103,34 @@ __global__ __launch_bounds__(256) void transpose_t_kernel(const T* __restrict__ 
   }
 }
 
+// Operands of the rank-2 kPB panel update from the panel's reflectors V (kPB x m, rows of A) and
+// W (kPB x m): X = [V^T W^T] and Yb = [W^T V^T] (m x 2 kPB each), so A -= X Yb^T.  One launch
+// per panel, 32 source columns per work-group.
+template <typename T>
+__global__ __launch_bounds__(256) void panel_operands_kernel(const T* __restrict__ Vp, const T* __restrict__ Wp,
+                                                             int64_t m, int64_t ld, T* __restrict__ X,
+                                                             T* __restrict__ Yb) {
+  __shared__ T tv[kPB][33], tw[kPB][33];
+  const int64_t c0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int k = ty; k < kPB; k += 8) {
+    const int64_t c = c0 + tx;
+    tv[k][tx] = c < m ? Vp[k * ld + c] : T(0);
+    tw[k][tx] = c < m ? Wp[k * ld + c] : T(0);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 32 * kPB; e += 256) {
+    const int rr = e / kPB, k = e % kPB;
+    const int64_t r = c0 + rr;
+    if (r < m) {
+      X[r * 2 * kPB + k] = tv[k][rr];
+      X[r * 2 * kPB + kPB + k] = tw[k][rr];
+      Yb[r * 2 * kPB + k] = tw[k][rr];
+      Yb[r * 2 * kPB + kPB + k] = tv[k][rr];
+    }
+  }
+}
+
 // ---- tridiagonalisation ----------------------------------------------------------------------
 
 // First column c of a panel, read from the lower triangle (the trailing update keeps only that
@@ -481,11 +509,19 @@ __global__ __launch_bounds__(256) void extract_y_kernel(const T* __restrict__ A,
 // so Tb = (I + N)^{-1} D with D = diag(tau), N = D striu(G) (strictly upper, nilpotent); the form
 // needs no 1/tau, so tau = 0 (H = I) gives zero row and column as larft does.  Thread j < nb
 // solves column j of X = (I + N)^{-1} by back substitution, x_k = -sum_{l=k+1..j} N[k][l] x_l,
-// x_j = 1; Tb[k][j] = X[k][j] tau_j.  One work-group, N and X in LDS (2 x 66 KB).
+// x_j = 1; Tb[k][j] = X[k][j] tau_j.  One work-group per block of reflectors: block b holds
+// reflectors b NB .. b NB + nb - 1 (nb = NB except for the last, partial block), its gram at
+// Gall + b NB^2 and its Tb at Tball + b NB^2 (both nb x nb, leading dimension nb); N and X in LDS
+// (2 x 66 KB).
 template <typename T>
-__global__ __launch_bounds__(256) void larft_kernel(const T* __restrict__ G, const T* __restrict__ tau,
-                                                    int nb, T* __restrict__ Tb) {
+__global__ __launch_bounds__(256) void larft_kernel(const T* __restrict__ Gall, const T* __restrict__ tau_all,
+                                                    int64_t nrefl, T* __restrict__ Tball) {
   constexpr int NBT = NbOf<T>::value;
+  const int64_t i0 = (int64_t)blockIdx.x * NBT;
+  const int nb = (int)min((int64_t)NBT, nrefl - i0);
+  const T* __restrict__ G = Gall + (int64_t)blockIdx.x * NBT * NBT;
+  const T* __restrict__ tau = tau_all + i0;
+  T* __restrict__ Tb = Tball + (int64_t)blockIdx.x * NBT * NBT;
   __shared__ T sN[NBT][NBT + 1];
   __shared__ T sX[NBT][NBT + 1];
   // 16 global loads in flight per thread (a loop of single loads waits a full memory round trip
@@ -634,8 +670,10 @@ SyevdLayout syevd_layout(int64_t n) {
   L.Yt = take(n * L.nb);
   L.W = take(n * L.nb);
   L.W2 = take(n * L.nb);
-  L.G = take(L.nb * L.nb);
-  L.Tb = take(L.nb * L.nb);
+  // grams and compact-WY factors of every block of reflectors
+  const int64_t nblocks = std::max<int64_t>((n - 1 + L.nb - 1) / L.nb, 1);
+  L.G = take(nblocks * L.nb * L.nb);
+  L.Tb = take(nblocks * L.nb * L.nb);
   L.P = take(sizeof(T) == 4 ? a64(n * L.nb) * L.splits : 64);
   L.D = take(n);
   L.E = take(n);
@@ -713,10 +751,9 @@ int sytrd(int64_t n, const SyevdLayout& L, T* base, rocblas_handle h, hipStream_
       const int64_t m = n - s0;
       const T* Vp = A + i0 * lda + s0;
       const T* Wp = Wb + s0;
-      MPQ_HIP_TRY(transpose_t(Vp, kPB, m, lda, X, 2 * kPB, stream));
-      MPQ_HIP_TRY(transpose_t(Wp, kPB, m, lda, X + kPB, 2 * kPB, stream));
-      MPQ_HIP_TRY(transpose_t(Wp, kPB, m, lda, Yb, 2 * kPB, stream));
-      MPQ_HIP_TRY(transpose_t(Vp, kPB, m, lda, Yb + kPB, 2 * kPB, stream));
+      hipLaunchKernelGGL(panel_operands_kernel<T>, dim3((unsigned)((m + 31) / 32)), dim3(256), 0, stream, Vp, Wp,
+                         m, lda, X, Yb);
+      MPQ_LAUNCH_CHECK();
       const int rc = trailing_update(h, X, Yb, A + s0 * lda + s0, lda, m, stream);
       if (rc != kOk) return rc;
     }
@@ -770,21 +807,37 @@ int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t wor
     return rocblas_fail("rocsolver stedc");
   // 3. Z column-major = row-major Zb with Zb = Z^T.  V^T = Zb Q^T, applied block by block:
   //    Zb[:, i0:] <- Zb[:, i0:] - ((Zb[:, i0:] Y) Tb^T) Y^T
+  //    The grams Y^T Y of all blocks come first, then one larft launch forms every Tb.
   const int64_t nrefl = n - 1;
-  for (int64_t i0 = ((nrefl - 1) / NB) * NB; i0 >= 0 && nrefl > 0; i0 -= NB) {
+  const int64_t nblocks = nrefl > 0 ? (nrefl + NB - 1) / NB : 0;
+  int rc;
+  for (int64_t b = 0; b < nblocks; ++b) {
+    const int64_t i0 = b * NB;
     const int nb = (int)std::min<int64_t>(NB, nrefl - i0);
     const int64_t m = n - i0;
     const int64_t cnt = m * nb;
     hipLaunchKernelGGL(extract_y_kernel<T>, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, stream, A, lda, n,
                        i0, nb, Y);
     MPQ_LAUNCH_CHECK();
-    int rc;
     MPQ_HIP_TRY(transpose_t(Y, m, nb, nb, Yt, m, stream));
-    if ((rc = gemm_rm(h, Yt, m, Y, nb, false, G, nb, nb, nb, m, T(1), T(0), P, pfl, stream)) != kOk) return rc;
-    hipLaunchKernelGGL(larft_kernel<T>, dim3(1), dim3(256), 0, stream, G, tau + i0, nb, Tb);
+    if ((rc = gemm_rm(h, Yt, m, Y, nb, false, G + b * NB * NB, nb, nb, nb, m, T(1), T(0), P, pfl, stream)) != kOk)
+      return rc;
+  }
+  if (nblocks > 0) {
+    hipLaunchKernelGGL(larft_kernel<T>, dim3((unsigned)nblocks), dim3(256), 0, stream, G, tau, nrefl, Tb);
+    MPQ_LAUNCH_CHECK();
+  }
+  for (int64_t b = nblocks - 1; b >= 0; --b) {
+    const int64_t i0 = b * NB;
+    const int nb = (int)std::min<int64_t>(NB, nrefl - i0);
+    const int64_t m = n - i0;
+    const int64_t cnt = m * nb;
+    const T* Tbb = Tb + b * NB * NB;
+    hipLaunchKernelGGL(extract_y_kernel<T>, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, stream, A, lda, n,
+                       i0, nb, Y);
     MPQ_LAUNCH_CHECK();
     if ((rc = gemm_rm(h, Z + i0, n, Y, nb, false, W, nb, n, nb, m, T(1), T(0), P, pfl, stream)) != kOk) return rc;
-    if ((rc = gemm_rm(h, W, nb, Tb, nb, true, W2, nb, n, nb, nb, T(1), T(0), nullptr, 0, stream)) != kOk) return rc;
+    if ((rc = gemm_rm(h, W, nb, Tbb, nb, true, W2, nb, n, nb, nb, T(1), T(0), nullptr, 0, stream)) != kOk) return rc;
     if ((rc = gemm_rm(h, W2, nb, Y, nb, true, Z + i0, n, n, m, nb, T(-1), T(1), nullptr, 0, stream)) != kOk)
       return rc;
   }
