@@ -339,84 +339,111 @@ __global__ __launch_bounds__(kThr) void finish_kernel(T* __restrict__ A, int64_t
   const int ns = nblk - b0;
   const int chy = (ns + chl - 1) / chl;
 
-  // column scalars: partial loads
-  T xn2 = 0.f;
-  for (int t = tid; t < npn; t += kThr) xn2 += Pn_in[t];
-  T pqp = 0.f;
+  // Every global load of the kernel is issued in one batch before any of them is used: fixed-size,
+  // unrolled batches from clamped in-range addresses whose values are selected afterwards.  (A
+  // guarded load, or a loop that accumulates while it loads, costs a memory round trip each.)
+  // Only trailing matrices above 2 kThr norm partials, kPvBatch kThr symv partials or 32 kSub
+  // strips take the remainder loops below.
+  constexpr int kPvBatch = 32;
+  const int npv = chy * ns;  // x^T A x partials (chunk, strip); some slots hold no chunk
+  const int gl = (int)min(g, n - 1);  // in-range row for the loads of inactive threads
+  const int s_row = gl / kTB;
+  const int nch = (nblk - s_row + chl - 1) / chl;
+  const T pn_v0 = Pn_in[min(tid, npn - 1)];
+  const T pn_v1 = Pn_in[min(tid + kThr, npn - 1)];
+  T pq_v[kDotWG / 4];
   {
     const int slot = tid & 63, part = tid >> 6;
-    T v[kDotWG / 4];
 #pragma unroll
-    for (int u = 0; u < kDotWG / 4; ++u) v[u] = Ppq[(int64_t)(part * (kDotWG / 4) + u) * 64 + slot];
-#pragma unroll
-    for (int u = 0; u < kDotWG / 4; ++u) pqp += v[u];
+    for (int u = 0; u < kDotWG / 4; ++u) pq_v[u] = Ppq[(int64_t)(part * (kDotWG / 4) + u) * 64 + slot];
   }
-  T xux = 0.f;
-  for (int base = tid; base < chy * ns; base += kThr * 16) {
-    T v[16];
+  // partial idx = tid + kThr u sits at (chunk idx / ns, strip b0 + idx % ns); both indices step
+  // by a fixed quotient and remainder (no division per element).  pv_ok bit u: the slot holds a
+  // chunk (strip sx has a chunk chx when sx < ns - chl chx).
+  T pv_v[kPvBatch];
+  unsigned pv_ok = 0u;
+  {
+    const int q_step = kThr / ns, r_step = kThr % ns;
+    int chx = tid / ns, sx = tid % ns;
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int idx = base + u * kThr;
-      const int chx = idx / ns, sx = idx % ns;
-      v[u] = (idx < chy * ns && sx < ns - chl * chx) ? Pvv[(int64_t)chx * nblk + b0 + sx] : 0.f;
+    for (int u = 0; u < kPvBatch; ++u) {
+      const int idx = tid + kThr * u;
+      pv_v[u] = 0.f;
+      if (idx < npv) {
+        pv_v[u] = Pvv[(int64_t)chx * nblk + b0 + sx];
+        if (sx < ns - chl * chx) pv_ok |= 1u << u;
+      }
+      sx += r_step;
+      chx += q_step;
+      if (sx >= ns) {
+        sx -= ns;
+        ++chx;
+      }
     }
-#pragma unroll
-    for (int u = 0; u < 16; ++u) xux += v[u];
   }
-  T ur = 0.f;
-  if (tid < chy) ur = Pc[((int64_t)b0 * ch_alloc + tid) * kTB + (r % kTB)];
-  if (tid == kThr - 1) ur = Pr[(int64_t)b0 * lda + r];  // chy < kThr - 1 (checked by the host)
-  if (tid >= 64 && tid < 64 + i) {
-    svr[tid - 64] = A[(i0 + tid - 64) * lda + r];
-    swr[tid - 64] = Wb[(int64_t)(tid - 64) * lda + r];
-  }
+  const T ur_c = Pc[((int64_t)b0 * ch_alloc + min(tid, chy - 1)) * kTB + (r % kTB)];
+  const T ur_r = Pr[(int64_t)b0 * lda + r];
+  const int jr = min(max(tid - 64, 0), max(i - 1, 0));
+  const T svr_v = A[(i0 + jr) * lda + r];
+  const T swr_v = Wb[(int64_t)jr * lda + r];
   const T arr = A[r * lda + r];
-
-  // own row: symv partials, the earlier reflectors' entries, column r and row c
-  T u = 0.f;
+  T pr_v[32];
+#pragma unroll
+  for (int q = 0; q < 32; ++q) pr_v[q] = Pr[(int64_t)min(b0 + k + kSub * q, s_row) * lda + gl];
+  T pc_v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    pc_v[q] = Pc[((int64_t)s_row * ch_alloc + min(k + kSub * q, nch - 1)) * kTB + (gl % kTB)];
   T vj[kPB / kSub], wj[kPB / kSub];
 #pragma unroll
-  for (int t = 0; t < kPB / kSub; ++t) vj[t] = wj[t] = 0.f;
-  T a_c = 0.f, a_r = 0.f;
-  if (active) {
-    const int s = (int)(g / kTB);
-    // up to 32 partials per lane in one batch of loads (one memory round trip up to 256 strips)
-    for (int bj0 = b0 + k; bj0 <= s; bj0 += 32 * kSub) {
-      T v[32];
-#pragma unroll
-      for (int q = 0; q < 32; ++q) {
-        const int bj = min(bj0 + kSub * q, s);  // clamped: unconditional loads, then a select
-        v[q] = Pr[(int64_t)bj * lda + g];
-      }
-#pragma unroll
-      for (int q = 0; q < 32; ++q)
-        if (bj0 + kSub * q <= s) u += v[q];
-    }
-    const int nch = (nblk - s + chl - 1) / chl;
-    for (int ch0 = k; ch0 < nch; ch0 += 4 * kSub) {
-      T v[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int ch = min(ch0 + kSub * q, nch - 1);
-        v[q] = Pc[((int64_t)s * ch_alloc + ch) * kTB + (g % kTB)];
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (ch0 + kSub * q < nch) u += v[q];
-    }
-#pragma unroll
-    for (int t = 0; t < kPB / kSub; ++t) {
-      const int j = k + kSub * t;
-      if (j < i) {
-        vj[t] = A[(i0 + j) * lda + g];
-        wj[t] = Wb[(int64_t)j * lda + g];
-      }
-    }
-    if (k == 0) {
-      a_c = A[c * lda + g];
-      a_r = A[g * lda + r];  // column r, lower triangle
-    }
+  for (int t = 0; t < kPB / kSub; ++t) {
+    const int j = min(k + kSub * t, max(i - 1, 0));
+    vj[t] = A[(i0 + j) * lda + gl];
+    wj[t] = Wb[(int64_t)j * lda + gl];
   }
+  T a_c = A[c * lda + gl];
+  T a_r = A[(int64_t)gl * lda + r];  // column r, lower triangle
+
+  // column scalars
+  T xn2 = tid < npn ? pn_v0 : T(0);
+  if (tid + kThr < npn) xn2 += pn_v1;
+  for (int t = tid + 2 * kThr; t < npn; t += kThr) xn2 += Pn_in[t];
+  T pqp = 0.f;
+#pragma unroll
+  for (int u = 0; u < kDotWG / 4; ++u) pqp += pq_v[u];
+  T xux = 0.f;
+#pragma unroll
+  for (int u = 0; u < kPvBatch; ++u)
+    if (pv_ok & (1u << u)) xux += pv_v[u];
+  for (int idx = tid + kThr * kPvBatch; idx < npv; idx += kThr) {
+    const int chx = idx / ns, sx = idx % ns;
+    if (sx < ns - chl * chx) xux += Pvv[(int64_t)chx * nblk + b0 + sx];
+  }
+  T ur = tid < chy ? ur_c : T(0);
+  if (tid == kThr - 1) ur = ur_r;  // chy < kThr - 1 (checked by the host)
+  if (tid >= 64 && tid < 64 + i) {
+    svr[tid - 64] = svr_v;
+    swr[tid - 64] = swr_v;
+  }
+
+  // own row: symv partials (strips b0 .. s_row, chunks 0 .. nch-1 of strip s_row), the earlier
+  // reflectors' entries, column r and row c
+  T u = 0.f;
+  if (active) {
+#pragma unroll
+    for (int q = 0; q < 32; ++q)
+      if (b0 + k + kSub * q <= s_row) u += pr_v[q];
+    for (int bj = b0 + k + 32 * kSub; bj <= s_row; bj += kSub) u += Pr[(int64_t)bj * lda + g];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (k + kSub * q < nch) u += pc_v[q];
+    for (int ch = k + 4 * kSub; ch < nch; ch += kSub) u += Pc[((int64_t)s_row * ch_alloc + ch) * kTB + (g % kTB)];
+  }
+#pragma unroll
+  for (int t = 0; t < kPB / kSub; ++t) {
+    if (!(active && k + kSub * t < i)) vj[t] = wj[t] = 0.f;
+  }
+  if (!(active && k == 0)) a_c = a_r = 0.f;
 
   // column scalars: reductions (fixed order)
   spq[tid >> 6][tid & 63] = pqp;

@@ -34,6 +34,28 @@ def test_syevd_matches_fp64(gpu, n):
     assert orth <= max(2.0 * orth_t, 2e-5), (orth, orth_t)
 
 
+def test_syevd_large_remainder_paths(gpu):
+    # n = 17000: the first trailing matrices exceed the tridiagonalisation kernels' fixed load
+    # batches (over 512 norm partials, 8192 symv partials and 256 column strips), so their
+    # remainder loops run.  Yardstick: torch's fp32 eigh on the same GPU; residual and
+    # orthogonality in fp64 on the GPU.
+    n = 17000
+    g = torch.Generator(device=gpu).manual_seed(17000)
+    X = torch.randn(2 * n, n, generator=g, device=gpu) * torch.exp(torch.randn(n, generator=g, device=gpu))
+    Hg = X.T @ X / (2 * n)
+    del X
+    Hg = 0.5 * (Hg + Hg.T)
+    lam, V = ops.syevd(Hg)
+    lt = torch.linalg.eigvalsh(Hg)
+    scale = float(lt.abs().max())
+    assert float((lam - lt).abs().max()) <= 2e-5 * scale
+    assert bool((lam[1:] >= lam[:-1]).all())
+    Hd, Vd = Hg.double(), V.double()
+    resid = float((Hd @ Vd - Vd * lam.double().unsqueeze(0)).norm() / Hd.norm())
+    orth = float((Vd.T @ Vd - torch.eye(n, dtype=torch.float64, device=gpu)).abs().max())
+    assert resid < 1e-4 and orth < 1e-4, (resid, orth)
+
+
 def test_syevd_small_and_diagonal(gpu):
     # n = 1, 2 (no or one reflector), a diagonal matrix (all reflectors trivial), repeated eigenvalues
     for H in (torch.tensor([[3.0]]), torch.tensor([[2.0, 1.0], [1.0, 2.0]]),
