@@ -41,6 +41,7 @@ HIP_SOURCES = [
     "hessian.hip",
     "awq.hip",
     "eigh.hip",
+    "stedc.hip",
 ]
 CXX_SOURCES = [
     "errors.cpp",
@@ -104,7 +105,7 @@ def build(verbose: bool = False, jobs: int = 8) -> str:
                 print(out)
     tmp = LIB_PATH + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-L", ROCM_LIB,
-          "-Wl,-rpath," + ROCM_LIB, "-lrocsolver", "-lrocblas"])
+          "-Wl,-rpath," + ROCM_LIB, "-lrocblas"])
     shutil.move(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -8,7 +8,8 @@
 //      w = tau (A v - V W^T v - W V^T v) - tau/2 (w.v) v, applies the panel's lazy update to the
 //      next column and forms the partial norms of the next reflector; every 32 reflectors the
 //      trailing matrix takes the rank-64 update A -= V W^T + W V^T on the MFMA GEMM;
-//   2. rocSOLVER sstedc (divide and conquer): T = Z diag(lam) Z^T, eigenvalues ascending;
+//   2. divide and conquer on the tridiagonal matrix (stedc.hip): T = Z^T diag(lam) Z, eigenvalues
+//      ascending, Z row-major with row k = eigenvector k;
 //   3. back-transformation V = Q Z on fp32 MFMA GEMMs: the reflectors are applied in blocks of
 //      kNB as compact-WY factors I - Y Tb Y^T (Tb from the block's gram Y^T Y, LAPACK larft
 //      forward/columnwise), last block first.
@@ -21,13 +22,13 @@
 // Reflector i (LAPACK's H(i) = I - tau_i v_i v_i^T, v_i[0..i] = 0, v_i[i+1] = 1) is stored in
 // row i, entries i+2..n-1 -- by symmetry the same entries LAPACK's lower storage keeps in column i.
 #include <rocblas/rocblas.h>
-#include <rocsolver/rocsolver.h>
 
 #include <algorithm>
 
 #include "common.h"
 #include "gemm.h"
 #include "kernels.h"
+#include "stedc.h"
 
 namespace mpq {
 namespace {
@@ -650,15 +651,6 @@ int trailing_update(rocblas_handle h, const double* X, const double* Yb, double*
   return gemm_rm(h, X, 2 * kPB, Yb, 2 * kPB, true, C, ldc, m, m, 2 * kPB, -1.0, 1.0, nullptr, 0, stream);
 }
 
-rocblas_status stedc(rocblas_handle h, rocblas_int n, float* D, float* E, float* Z, rocblas_int ldz,
-                     rocblas_int* info) {
-  return rocsolver_sstedc(h, rocblas_evect_tridiagonal, n, D, E, Z, ldz, info);
-}
-rocblas_status stedc(rocblas_handle h, rocblas_int n, double* D, double* E, double* Z, rocblas_int ldz,
-                     rocblas_int* info) {
-  return rocsolver_dstedc(h, rocblas_evect_tridiagonal, n, D, E, Z, ldz, info);
-}
-
 template <typename T>
 hipError_t transpose_t(const T* in, int64_t rows, int64_t cols, int64_t ld_in, T* out, int64_t ld_out,
                        hipStream_t stream) {
@@ -670,7 +662,7 @@ hipError_t transpose_t(const T* in, int64_t rows, int64_t cols, int64_t ld_in, T
 // Workspace layout of mpq_syevd / mpq_syevd_f64 (element offsets, each region 64 elements aligned).
 struct SyevdLayout {
   int64_t lda, nblk, ch_alloc, pn_stride, splits, nb;
-  int64_t A, Z, Y, Yt, W, W2, G, Tb, P, D, E, tau, alph, Pn, Wb, X, Yb, Pr, Pc, Pvv, Ppq, info, total;
+  int64_t A, Z, Y, Yt, W, W2, G, Tb, P, D, E, tau, alph, Pn, Wb, X, Yb, Pr, Pc, Pvv, Ppq, dc, total;
 };
 
 template <typename T>
@@ -714,7 +706,7 @@ SyevdLayout syevd_layout(int64_t n) {
   L.Pc = take(L.nblk * L.ch_alloc * kTB);
   L.Pvv = take(L.nblk * L.ch_alloc);
   L.Ppq = take(kDotWG * 64);
-  L.info = take(64);
+  L.dc = take((tridiag_dc_workspace_bytes(n, (int)sizeof(T)) + (int64_t)sizeof(T) - 1) / (int64_t)sizeof(T));
   L.total = o;
   return L;
 }
@@ -813,7 +805,6 @@ int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t wor
   T* D = base + L.D;
   T* E = base + L.E;
   T* tau = base + L.tau;
-  rocblas_int* info = reinterpret_cast<rocblas_int*>(base + L.info);
   const int64_t lda = L.lda;
   const int64_t pfl = L.splits > 1 ? a64(n * L.nb) * L.splits : 0;
   const int NB = (int)L.nb;
@@ -822,7 +813,6 @@ int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t wor
   MPQ_HIP_TRY(hipMemsetAsync(A, 0, (size_t)(lda * lda) * sizeof(T), stream));
   MPQ_HIP_TRY(hipMemcpy2DAsync(A, lda * sizeof(T), H, n * sizeof(T), n * sizeof(T), n, hipMemcpyDeviceToDevice,
                                stream));
-  MPQ_HIP_TRY(hipMemsetAsync(info, 0, sizeof(rocblas_int), stream));
   if (n == 1) {
     MPQ_HIP_TRY(hipMemcpyAsync(D, A, sizeof(T), hipMemcpyDeviceToDevice, stream));
   } else {
@@ -830,8 +820,10 @@ int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t wor
     if (rc != kOk) return rc;
   }
   // 2. tridiagonal eigenproblem
-  if (stedc(h, (rocblas_int)n, D, E, Z, (rocblas_int)n, info) != rocblas_status_success)
-    return rocblas_fail("rocsolver stedc");
+  {
+    const int rc = tridiag_dc(n, D, E, lam, Z, base + L.dc, (L.total - L.dc) * (int64_t)sizeof(T), h, stream);
+    if (rc != kOk) return rc;
+  }
   // 3. Z column-major = row-major Zb with Zb = Z^T.  V^T = Zb Q^T, applied block by block:
   //    Zb[:, i0:] <- Zb[:, i0:] - ((Zb[:, i0:] Y) Tb^T) Y^T
   //    The grams Y^T Y of all blocks come first, then one larft launch forms every Tb.
@@ -870,15 +862,7 @@ int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t wor
   }
   // V (row-major, columns = eigenvectors) = (Zb)^T
   MPQ_HIP_TRY(transpose_t(Z, n, n, n, V, n, stream));
-  MPQ_HIP_TRY(hipMemcpyAsync(lam, D, n * sizeof(T), hipMemcpyDeviceToDevice, stream));
-  rocblas_int hinfo = 0;
-  MPQ_HIP_TRY(hipMemcpyAsync(&hinfo, info, sizeof(hinfo), hipMemcpyDeviceToHost, stream));
   MPQ_HIP_TRY(hipStreamSynchronize(stream));
-  if (hinfo != 0) {
-    set_error("rocsolver stedc did not converge (info = %d)", (int)hinfo);
-    set_error_code(kNumerical);
-    return kNumerical;
-  }
   return kOk;
 }
 
