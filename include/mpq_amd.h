@@ -204,8 +204,8 @@ int mpq_transpose(const float* in, int64_t rows, int64_t cols, int64_t ld_in, fl
  * Post-processing of an ascending eigendecomposition (lam_asc, V_asc columns):
  * eigenvalues floored at floor_v and put in descending order with their
  * vectors, S = sqrt(lam), Vs = V * S.  Replaces
- * mpq/adapters/gptqmodel.py:302-310 and :887-890 (eigh itself is rocSOLVER via
- * torch.linalg.eigh).  Any output may be NULL.
+ * mpq/adapters/gptqmodel.py:302-310 and :887-890 (the reference's eigh itself is
+ * torch.linalg.eigh; here mpq_syevd).  Any output may be NULL.
  */
 int mpq_eigh_postprocess(const float* lam_asc, const float* V_asc, int64_t n, float floor_v,
                          float* lam, float* S, float* V, float* Vs, mpq_stream_t stream);
@@ -213,11 +213,12 @@ int mpq_eigh_postprocess(const float* lam_asc, const float* V_asc, int64_t n, fl
 /*
  * Symmetric eigendecomposition of H (n x n, fp32): lam ascending (n) and V (n x n, row-major,
  * column k = eigenvector k), the torch.linalg.eigh call of mpq/adapters/gptqmodel.py:276-310.
- * Blocked Householder tridiagonalisation on this library's kernels, rocSOLVER sstedc, then the
- * back-transformation V = Q Z as blocked compact-WY updates on this library's fp32 MFMA GEMM.
- * workspace: mpq_syevd_workspace_size(n) bytes (rocSOLVER and rocBLAS may also use their
- * handle's own device memory).  Synchronises `stream` once;
- * MPQ_NUMERICAL_ERROR when the tridiagonal solver does not converge.
+ * Blocked Householder tridiagonalisation, divide and conquer on the tridiagonal matrix (fp64
+ * secular equations and Loewner vectors, merge products on the fp32 MFMA GEMM), then the
+ * back-transformation V = Q Z as blocked compact-WY updates on the same GEMM; all on this
+ * library's kernels.  workspace: mpq_syevd_workspace_size(n) bytes (about 24 n^2; rocBLAS may
+ * also use its handle's device memory).  Synchronises `stream` once per tridiagonal merge of more
+ * than 512 rows and once at the end.
  */
 int64_t mpq_syevd_workspace_size(int64_t n);
 int mpq_syevd(int64_t n, const float* H, float* lam, float* V, void* workspace, int64_t workspace_bytes,
@@ -225,8 +226,9 @@ int mpq_syevd(int64_t n, const float* H, float* lam, float* V, void* workspace, 
 
 /*
  * The same decomposition in fp64 (the torch.linalg.eigh of the float64 Hessian in
- * mpq/adapters/quip_sharp.py:33-67): the tridiagonalisation kernels in double, rocSOLVER
- * dstedc, and the trailing updates and back-transformation on rocBLAS dgemm.
+ * mpq/adapters/quip_sharp.py:33-67): the same kernels in double (divide-and-conquer tolerances
+ * at fp64 unit roundoff), with the trailing updates, merge products and back-transformation on
+ * rocBLAS dgemm.
  * workspace: mpq_syevd_f64_workspace_size(n) bytes.
  */
 int64_t mpq_syevd_f64_workspace_size(int64_t n);

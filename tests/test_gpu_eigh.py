@@ -1,5 +1,5 @@
-"""GPU: symmetric eigendecomposition (mpq_syevd: rocSOLVER tridiagonalisation + D&C, back-transformation
-on this library's MFMA GEMM) against fp64 LAPACK on the CPU, with the fp32 accuracy of
+"""GPU: symmetric eigendecomposition (mpq_syevd: tridiagonalisation, divide and conquer on the
+tridiagonal matrix, back-transformation on this library's MFMA GEMM) against fp64 LAPACK on the CPU, with the fp32 accuracy of
 torch.linalg.eigh on the same GPU as the yardstick for residual and orthogonality."""
 import pytest
 import torch

@@ -194,7 +194,7 @@ def test_adapter_end_to_end_matches_oracle(gpu, rotation, bits):
 
 @pytest.mark.parametrize("rotation", ["none", "internal_hadamard"])
 def test_adapter_device_eigh(gpu, rotation):
-    """With the device eigh (rocSOLVER) the discrete decisions may move; the proxy loss stays close
+    """With the device eigh (mpq_syevd) the discrete decisions may move; the proxy loss stays close
     to the CPU path's and well below RTN's."""
     rows, cols, bits, gs = 256, 512, 4, 128
     W, H = make_layer(rows, cols, tokens=2048, seed_key=f"e2e:{rotation}:4")
