@@ -394,6 +394,22 @@ int mpq_uniform_vamp_solve(int64_t rows, int64_t n, int maxq, const float* W, in
                            MpqUniformVampStats* stats, void* workspace, int64_t workspace_bytes,
                            mpq_stream_t stream);
 
+/*
+ * mpq_uniform_vamp_solve with products the caller formed for all rows at once (one GEMM over
+ * every row block instead of one per block; the reference forms the same products per block in
+ * mpq/solver.py:467-480 and the warm start in mpq/adapters/gptqmodel.py:920-941):
+ *   Yu_in (optional) rows x n = W Vs, xr_in (optional) rows x n = x_init Vs;
+ *   xprod_out (optional) rows x n receives x_best Vs of the returned codes (the polish's start).
+ * All three are contiguous (leading dimension n).
+ */
+int mpq_uniform_vamp_solve_ex(int64_t rows, int64_t n, int maxq, const float* W, int64_t ldw,
+                              const float* x_init, const float* scale, const float* zero,
+                              int64_t group_size, const float* V, const float* S, const float* Vs,
+                              const MpqUniformVampConfig* cfg, double obs_init, const float* Yu_in,
+                              const float* xr_in, uint8_t* q_out, float* x_out, float* err_out,
+                              float* rtn_err_out, float* xprod_out, MpqUniformVampStats* stats,
+                              void* workspace, int64_t workspace_bytes, mpq_stream_t stream);
+
 /* Workspace bytes needed by mpq_uniform_cd_polish. */
 int64_t mpq_uniform_cd_workspace_size(int64_t rows, int64_t n, int64_t block_rows);
 
@@ -417,6 +433,20 @@ int mpq_uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows,
                           float* err_before, float* err_after, int32_t* improved,
                           int32_t* accepted_per_row, void* workspace, int64_t workspace_bytes,
                           mpq_stream_t stream);
+
+/*
+ * mpq_uniform_cd_polish with the start's product x Vs from the caller (xprod_in, rows x n,
+ * contiguous; optional): mpq_uniform_vamp_solve_ex returns it for its codes, so the polish skips
+ * that product (the reference recomputes it, mpq/solver.py:283-290).
+ */
+int mpq_uniform_cd_polish_ex(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                             float accept_tol, const float* W, int64_t ldw, const float* Yu,
+                             const uint8_t* q_in, const float* x_in, const float* xprod_in,
+                             const float* scale, const float* zero, int64_t group_size,
+                             const float* Vs, const float* H, int select, uint8_t* q_out,
+                             float* err_before, float* err_after, int32_t* improved,
+                             int32_t* accepted_per_row, void* workspace, int64_t workspace_bytes,
+                             mpq_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -75,6 +75,12 @@ SIGNATURES = {
     "mpq_uniform_cd_polish": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_float, c_ptr, c_i64, c_ptr,
                                       c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_int, c_ptr,
                                       c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
+    "mpq_uniform_vamp_solve_ex": (c_int, [c_i64, c_i64, c_int, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64,
+                                          c_ptr, c_ptr, c_ptr, c_ptr, c_double, c_ptr, c_ptr, c_ptr, c_ptr,
+                                          c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
+    "mpq_uniform_cd_polish_ex": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_float, c_ptr, c_i64, c_ptr,
+                                         c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_int, c_ptr,
+                                         c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
 }
 
 

@@ -232,12 +232,16 @@ def run_mpq_quantization(
                                      bool(adapter_cfg.auto_block_rows))
     _, x_rtn = ops.uniform_rtn(W_work, scale_groups, zero_groups, group_size, maxq, want_q=False)
 
+    # Rank-space targets W Vs and the RTN decision's x_rtn Vs, formed once for all rows (the
+    # reference forms them per row block inside the solver, mpq/solver.py:467-480); the row blocks
+    # and the polish take slices, and each block returns its best decision's x Vs for the polish.
+    Yu_all = ops.gemm(W_work, Vs)
+    XR_all = ops.gemm(x_rtn, Vs)
     # observation-precision warm start (reference :920-941): per block sums accumulated in double
     if float(getattr(vamp_cfg, "obs_precision", 0.0)) > 0.0:
         obs_precision = float(vamp_cfg.obs_precision)
     else:
-        du = ops.gemm(W_work - x_rtn, Vs)
-        sq = du.square().sum(dim=1)
+        sq = (Yu_all - XR_all).square().sum(dim=1)
         sums = [float(sq[r0:r0 + block_rows].sum().item()) for r0 in range(0, rows, block_rows)]
         mse = max(sum(sums) / max(rows * cols, 1), 1e-12)
         obs_precision = 1.0 / mse
@@ -247,6 +251,7 @@ def run_mpq_quantization(
     q_int = torch.empty(rows, cols, dtype=torch.uint8, device=device)
     err_vamp = torch.empty(rows, dtype=torch.float32, device=device)
     rtn_err = torch.empty(rows, dtype=torch.float32, device=device)
+    XP_all = torch.empty(rows, cols, dtype=torch.float32, device=device)
     ws = ops.workspace(int(ops._lib.load().mpq_uniform_vamp_workspace_size(block_rows, cols)), device)
     obs_block = float(obs_precision)
     block_stats: List[Dict[str, Any]] = []
@@ -254,14 +259,14 @@ def run_mpq_quantization(
         r1 = min(rows, r0 + block_rows)
         q_b, _, e_b, re_b, st = ops.uniform_vamp_solve(
             W_work[r0:r1], x_rtn[r0:r1], scale_groups[r0:r1], zero_groups[r0:r1], group_size, maxq, V, S, Vs,
-            vamp_cfg, obs_init=obs_block, ws=ws)
+            vamp_cfg, obs_init=obs_block, ws=ws, Yu=Yu_all[r0:r1], xr=XR_all[r0:r1], xprod_out=XP_all[r0:r1])
         q_int[r0:r1] = q_b
         err_vamp[r0:r1] = e_b
         rtn_err[r0:r1] = re_b
         if bool(getattr(vamp_cfg, "em_obs_precision", True)):
             obs_block = float(st["obs_precision_final"])
         block_stats.append(st)
-    del ws
+    del ws, XR_all
     torch.cuda.synchronize(device)
     timings["vamp_s"] = time.time() - t_solve
 
@@ -273,9 +278,9 @@ def run_mpq_quantization(
     polish_updates = 0.0
     changed = 0
     if mode == "block_cd":
-        q_pol, eb, ea, imp, acc = ops.uniform_cd_polish(W_work, q_int, scale_groups, zero_groups, group_size, maxq,
+        q_pol, eb, ea, imp, acc = ops.uniform_cd_polish(None, q_int, scale_groups, zero_groups, group_size, maxq,
                                                         Vs, H_metric, block_rows=block_rows, sweeps=sweeps,
-                                                        select=True)
+                                                        select=True, Yu=Yu_all, xprod=XP_all)
         final_err = torch.where(imp.bool(), ea, err_vamp)
         changed = int((q_pol != q_int).sum().item())
         q_int = q_pol

@@ -20,6 +20,7 @@
 #include <algorithm>
 
 #include "cd_common.h"
+#include "mpq_amd.h"
 #include "gemm.h"
 #include "kernels.h"
 
@@ -226,7 +227,8 @@ int uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows, int
                       int64_t gs, const float* Vs,
                       const float* H, int select, uint8_t* q_out, float* err_before_out,
                       float* err_after_out, int32_t* improved, int32_t* accepted_per_row,
-                      void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+                      void* workspace, int64_t workspace_bytes, hipStream_t stream,
+                      const float* xprod_in = nullptr) {
   const CdPlan pl = cd_plan(rows, n, block_rows);
   MPQ_CHECK_ARG(workspace_bytes >= pl.bytes, "uniform CD: workspace too small (%lld < %lld bytes)",
                 (long long)workspace_bytes, (long long)pl.bytes);
@@ -275,9 +277,14 @@ int uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows, int
     MPQ_HIP_TRY(dequant_groups(q_in, scale, zero, G, gs, rows, n, x, stream));
   }
   MPQ_HIP_TRY(hipMemcpyAsync(qw, q_in, rows * n, hipMemcpyDeviceToDevice, stream));
-  MPQ_HIP_TRY(product_splits(x, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
-  hipLaunchKernelGGL(residual_kernel, eg, dim3(256), 0, stream, rows, n, P, pl.splits, sstride, Yu, scratch,
-                     part, nchunks);
+  if (xprod_in) {  // x Vs from the caller
+    hipLaunchKernelGGL(residual_kernel, eg, dim3(256), 0, stream, rows, n, xprod_in, 1, (int64_t)0, Yu, scratch,
+                       part, nchunks);
+  } else {
+    MPQ_HIP_TRY(product_splits(x, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
+    hipLaunchKernelGGL(residual_kernel, eg, dim3(256), 0, stream, rows, n, P, pl.splits, sstride, Yu, scratch,
+                       part, nchunks);
+  }
   hipLaunchKernelGGL(rows_sum_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, rows,
                      nchunks, part, err_b);
   MPQ_LAUNCH_CHECK();
@@ -369,6 +376,19 @@ extern "C" int mpq_uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t 
                                      float* err_before, float* err_after, int32_t* improved,
                                      int32_t* accepted_per_row, void* workspace, int64_t workspace_bytes,
                                      hipStream_t stream) {
+  return mpq_uniform_cd_polish_ex(rows, n, maxq, block_rows, sweeps, accept_tol, W, ldw, Yu, q_in, x_in, nullptr,
+                                  scale, zero, group_size, Vs, H, select, q_out, err_before, err_after, improved,
+                                  accepted_per_row, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mpq_uniform_cd_polish_ex(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                                        float accept_tol, const float* W, int64_t ldw, const float* Yu,
+                                        const uint8_t* q_in, const float* x_in, const float* xprod_in,
+                                        const float* scale, const float* zero, int64_t group_size,
+                                        const float* Vs, const float* H, int select, uint8_t* q_out,
+                                        float* err_before, float* err_after, int32_t* improved,
+                                        int32_t* accepted_per_row, void* workspace, int64_t workspace_bytes,
+                                        hipStream_t stream) {
   MPQ_CHECK_ARG(rows > 0 && n > 0, "mpq_uniform_cd_polish: empty problem");
   MPQ_CHECK_ARG(maxq >= 1 && maxq <= 255, "mpq_uniform_cd_polish: maxq must be in [1, 255]");
   MPQ_CHECK_ARG(block_rows >= 1 && sweeps >= 0 && group_size >= 1, "mpq_uniform_cd_polish: bad sizes");
@@ -379,6 +399,5 @@ extern "C" int mpq_uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t 
   MPQ_CHECK_ARG(!W || ldw >= n, "mpq_uniform_cd_polish: ldw < n");
   return mpq::uniform_cd_polish(rows, n, maxq, block_rows, sweeps, accept_tol, W, ldw, Yu, q_in, x_in, scale, zero,
                                 group_size, Vs, H, select, q_out, err_before, err_after, improved,
-                                accepted_per_row, workspace, workspace_bytes,
-                                stream);
+                                accepted_per_row, workspace, workspace_bytes, stream, xprod_in);
 }

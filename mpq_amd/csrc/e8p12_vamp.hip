@@ -150,7 +150,7 @@ extern "C" int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, co
                           stream);
     if (e != kOk) return e;
     MPQ_HIP_TRY(product(mvals, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
-    hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, pl.splits, sstride, Yu, part);
+    hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, pl.splits, sstride, Yu, part, nullptr);
     hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, part, errrow, status);
     MPQ_LAUNCH_CHECK();
     return kOk;
@@ -160,7 +160,7 @@ extern "C" int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, co
   MPQ_HIP_TRY(product(Wr, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
   MPQ_HIP_TRY(splitk_reduce(P, pl.splits, rows, n, Yu, n, 1.f, 0.f, stream));
   MPQ_HIP_TRY(product(hat_init, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
-  hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, pl.splits, sstride, Yu, part);
+  hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, pl.splits, sstride, Yu, part, nullptr);
   hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, part, errrow, status);
   hipLaunchKernelGGL(sqdiff_part_kernel, eg, eb, 0, stream, n, Wr, n, hat_init, n, part);
   hipLaunchKernelGGL(rows_gamma_init_kernel, dim3(1), eb, 0, stream, rows, n, nchunks, part, cfg->gamma_start, g1,

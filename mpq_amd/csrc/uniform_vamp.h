@@ -18,6 +18,10 @@ struct UniformProblem {
   const float* V;        // n x n eigenvectors (columns)
   const float* S;        // n sqrt-eigenvalues
   int64_t ldw;           // row stride of W / x_init (elements)
+  // optional products computed by the caller for all rows at once (rows x n, contiguous)
+  const float* Yu_in = nullptr;   // W Vs
+  const float* xr_in = nullptr;   // x_init Vs
+  float* xprod_out = nullptr;     // receives x_best Vs of the returned decision
 };
 
 }  // namespace mpq

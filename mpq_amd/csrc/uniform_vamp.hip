@@ -162,6 +162,8 @@ struct Workspace {
   float* r2prev;
   float* x1;  // denoiser mean; reused as the LMMSE coefficient product
   float* xs;  // hard-state dequantised values
+  float* prod_cur;   // xs Vs of the current / best hard state (kept when the caller asks for it)
+  float* prod_best;
   float* P;   // split-K partials
   float* rowbuf;  // per-row arrays
   float* part;    // chunk partials (3 per row per chunk)
@@ -189,7 +191,7 @@ Sizes plan(int64_t rows, int64_t n) {
   s.bn = bn;
   const int64_t mat = align_up(rows * n, 64) * 4;
   int64_t bytes = 0;
-  bytes += 6 * mat;                                   // Yu r1 r2 r2prev x1 xs
+  bytes += 8 * mat;                                   // Yu r1 r2 r2prev x1 xs prod_cur prod_best
   bytes += s.splits * mat;                            // P
   bytes += align_up(32 * rows, 64) * 4;               // row arrays
   bytes += align_up(3 * rows * s.nchunks, 64) * 4;    // chunk partials
@@ -209,6 +211,8 @@ Workspace carve(void* base, const Sizes& s) {
   w.r2prev = (float*)p; p += mat;
   w.x1 = (float*)p; p += mat;
   w.xs = (float*)p; p += mat;
+  w.prod_cur = (float*)p; p += mat;
+  w.prod_best = (float*)p; p += mat;
   w.P = (float*)p; p += s.splits * mat;
   w.rowbuf = (float*)p; p += align_up(32 * s.rows, 64) * 4;
   w.part = (float*)p; p += align_up(3 * s.rows * s.nchunks, 64) * 4;
@@ -254,6 +258,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
   MPQ_CHECK_ARG(workspace_bytes >= sz.bytes, "uniform VAMP: workspace too small (%lld < %lld bytes)",
                 (long long)workspace_bytes, (long long)sz.bytes);
   Workspace w = carve(workspace, sz);
+  const float* Yu = pr.Yu_in ? pr.Yu_in : w.Yu;
   VampStatus* hs = host_status();
   MPQ_CHECK_ARG(hs != nullptr, "uniform VAMP: pinned status buffer unavailable");
   const int nchunks = (int)sz.nchunks;
@@ -294,15 +299,16 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     }
     MPQ_LAUNCH_CHECK();
     MPQ_HIP_TRY(product(w, w.xs, Vs, false, rows, n, stream));
-    hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.Yu, w.part);
+    hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, w.part,
+                       pr.xprod_out ? w.prod_cur : nullptr);
     hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, w.part, err_cur, w.status);
     MPQ_LAUNCH_CHECK();
     return kOk;
   };
 
   // ---- setup ----------------------------------------------------------
-  // Yu = W @ Vs
-  {
+  // Yu = W @ Vs (or the caller's)
+  if (!pr.Yu_in) {
     // W may be strided (ldw); copy to contiguous r1 first when needed.
     const float* Wc = pr.W;
     if (pr.ldw != n) {
@@ -312,10 +318,14 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     MPQ_HIP_TRY(product(w, Wc, Vs, false, rows, n, stream));
     MPQ_HIP_TRY(splitk_reduce(w.P, w.splits, rows, n, w.Yu, n, 1.f, 0.f, stream));
   }
-  // RTN error (rtn_err, and the obs warm start when none is given)
-  MPQ_HIP_TRY(hipMemcpy2DAsync(w.xs, n * 4, pr.x_init, pr.ldw * 4, n * 4, rows, hipMemcpyDeviceToDevice, stream));
-  MPQ_HIP_TRY(product(w, w.xs, Vs, false, rows, n, stream));
-  hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.Yu, w.part);
+  // RTN error (rtn_err, and the obs warm start when none is given), from x_init Vs (or the caller's)
+  if (pr.xr_in) {
+    hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, pr.xr_in, 1, (int64_t)0, Yu, w.part, nullptr);
+  } else {
+    MPQ_HIP_TRY(hipMemcpy2DAsync(w.xs, n * 4, pr.x_init, pr.ldw * 4, n * 4, rows, hipMemcpyDeviceToDevice, stream));
+    MPQ_HIP_TRY(product(w, w.xs, Vs, false, rows, n, stream));
+    hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, w.part, nullptr);
+  }
   hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, w.part,
                      rtn_err_out ? rtn_err_out : err_cur, w.status);
   // gamma1 init from the RTN decision
@@ -353,6 +363,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
   double best_err_mean = (double)hs->err_mean;
   std::swap(w.q_cur, w.q_best);
   std::swap(err_cur, err_best);
+  std::swap(w.prod_cur, w.prod_best);
   double best_obs = obs;
   int best_iter = -1, stop_iter = -1;
   int a1_retry = 0, a2_clip = 0, g2_invalid = 0;
@@ -399,7 +410,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
                        has_prev ? 1 : 0, damping, w.r2prev, w.r2);
     MPQ_LAUNCH_CHECK();
     MPQ_HIP_TRY(product(w, w.r2, pr.V, false, rows, n, stream));
-    hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.Yu, pr.S, g2,
+    hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, pr.S, g2,
                        obs_f, w.x1, w.part);
     hipLaunchKernelGGL(rows_lmmse_kernel, dim3(1), eb, 0, stream, rows, n, n, nchunks, w.part, g2, damping,
                        eta2, g1new, g1, w.status);
@@ -438,6 +449,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     if (cur + tol < best_err_mean) {
       std::swap(w.q_cur, w.q_best);
       std::swap(err_cur, err_best);
+      std::swap(w.prod_cur, w.prod_best);
       best_err_mean = cur;
       best_obs = obs;
       best_iter = it;
@@ -451,6 +463,8 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
   // ---- outputs
   MPQ_HIP_TRY(hipMemcpyAsync(q_out, w.q_best, rows * n, hipMemcpyDeviceToDevice, stream));
   if (err_out) MPQ_HIP_TRY(hipMemcpyAsync(err_out, err_best, rows * 4, hipMemcpyDeviceToDevice, stream));
+  if (pr.xprod_out)
+    MPQ_HIP_TRY(hipMemcpyAsync(pr.xprod_out, w.prod_best, rows * n * 4, hipMemcpyDeviceToDevice, stream));
   if (x_out) {
     MPQ_HIP_TRY(dequant_groups(w.q_best, pr.scale, pr.zero, G, pr.group_size, rows, n, x_out, stream));
   }
@@ -487,6 +501,19 @@ extern "C" int mpq_uniform_vamp_solve(int64_t rows, int64_t n, int maxq, const f
                                       float* err_out, float* rtn_err_out,
                                       MpqUniformVampStats* stats, void* workspace,
                                       int64_t workspace_bytes, hipStream_t stream) {
+  return mpq_uniform_vamp_solve_ex(rows, n, maxq, W, ldw, x_init, scale, zero, group_size, V, S, Vs, cfg, obs_init,
+                                   nullptr, nullptr, q_out, x_out, err_out, rtn_err_out, nullptr, stats, workspace,
+                                   workspace_bytes, stream);
+}
+
+extern "C" int mpq_uniform_vamp_solve_ex(int64_t rows, int64_t n, int maxq, const float* W, int64_t ldw,
+                                         const float* x_init, const float* scale, const float* zero,
+                                         int64_t group_size, const float* V, const float* S,
+                                         const float* Vs, const MpqUniformVampConfig* cfg,
+                                         double obs_init, const float* Yu_in, const float* xr_in,
+                                         uint8_t* q_out, float* x_out, float* err_out, float* rtn_err_out,
+                                         float* xprod_out, MpqUniformVampStats* stats, void* workspace,
+                                         int64_t workspace_bytes, hipStream_t stream) {
   MPQ_CHECK_ARG(rows > 0 && n > 0, "mpq_uniform_vamp_solve: empty problem");
   MPQ_CHECK_ARG(maxq >= 1 && maxq <= 255, "mpq_uniform_vamp_solve: maxq must be in [1, 255]");
   MPQ_CHECK_ARG(W && x_init && scale && zero && V && S && Vs && cfg && q_out && workspace,
@@ -497,6 +524,7 @@ extern "C" int mpq_uniform_vamp_solve(int64_t rows, int64_t n, int maxq, const f
   mpq::UniformProblem pr{};
   pr.rows = rows; pr.n = n; pr.maxq = maxq; pr.W = W; pr.x_init = x_init; pr.scale = scale;
   pr.zero = zero; pr.group_size = group_size; pr.V = V; pr.S = S; pr.ldw = ldw;
+  pr.Yu_in = Yu_in; pr.xr_in = xr_in; pr.xprod_out = xprod_out;
   return mpq::uniform_vamp_solve(pr, Vs, *cfg, obs_init, q_out, x_out, err_out, rtn_err_out, stats,
                                  workspace, workspace_bytes, stream);
 }

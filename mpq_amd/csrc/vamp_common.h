@@ -337,10 +337,11 @@ __global__ __launch_bounds__(kEW) void lmmse_epi2_kernel(
 }
 
 // Rank-space error partials (mpq/linear.py:94): sum_j (Yu - sum_s P[s])^2.
+// prod (optional, rows x n) receives the summed product x Vs.
 __global__ __launch_bounds__(kEW) void err_epi_kernel(int64_t n, const float* __restrict__ P,
                                                       int splits, int64_t split_stride,
                                                       const float* __restrict__ Yu,
-                                                      float* __restrict__ part) {
+                                                      float* __restrict__ part, float* __restrict__ prod) {
   __shared__ float red[kEW / 64];
   const int64_t b = blockIdx.y;
   float acc = 0.f;
@@ -350,6 +351,7 @@ __global__ __launch_bounds__(kEW) void err_epi_kernel(int64_t n, const float* __
     if (j >= n) continue;
     const int64_t o = b * n + j;
     const float v = sum_splits(P, splits, split_stride, o);
+    if (prod) prod[o] = v;
     const float d = Yu[o] - v;
     acc += d * d;
   }

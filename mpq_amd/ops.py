@@ -237,9 +237,12 @@ def vamp_config_c(cfg) -> "_lib.UniformVampConfigC":
 
 
 def uniform_vamp_solve(W, x_init, scale, zero, group_size, maxq, V, S, Vs, cfg, obs_init: float = 0.0,
-                       want_x: bool = False, ws: Optional[torch.Tensor] = None):
-    """One row block of the uniform VAMP loop.  Returns (q uint8, x|None, err, rtn_err, stats dict)."""
-    dev = _dev(W, x_init, scale, zero, V, S, Vs)
+                       want_x: bool = False, ws: Optional[torch.Tensor] = None, Yu=None, xr=None,
+                       xprod_out: Optional[torch.Tensor] = None):
+    """One row block of the uniform VAMP loop.  Returns (q uint8, x|None, err, rtn_err, stats dict).
+    ``Yu`` = W Vs and ``xr`` = x_init Vs may come from the caller (formed once for all row blocks);
+    ``xprod_out`` (rows x n, contiguous fp32) then receives x_best Vs of the returned codes."""
+    dev = _dev(W, x_init, scale, zero, V, S, Vs, Yu, xr, xprod_out)
     W = _f32c(W)
     x_init = _f32c(x_init)
     rows, n = W.shape
@@ -255,21 +258,25 @@ def uniform_vamp_solve(W, x_init, scale, zero, group_size, maxq, V, S, Vs, cfg, 
     rtn_err = torch.empty(rows, dtype=F32, device=dev)
     st = _lib.UniformVampStatsC()
     c = vamp_config_c(cfg)
-    _lib.call("mpq_uniform_vamp_solve", rows, n, int(maxq), _lib.ptr(W), n, _lib.ptr(x_init),
+    for name, t in (("Yu", Yu), ("xr", xr), ("xprod_out", xprod_out)):
+        if t is not None and (tuple(t.shape) != (rows, n) or t.dtype != F32 or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous float32 tensor of shape {(rows, n)}")
+    _lib.call("mpq_uniform_vamp_solve_ex", rows, n, int(maxq), _lib.ptr(W), n, _lib.ptr(x_init),
               _lib.ptr(_f32c(scale)), _lib.ptr(_f32c(zero)), int(group_size), _lib.ptr(_f32c(V)),
-              _lib.ptr(_f32c(S)), _lib.ptr(_f32c(Vs)), ctypes.byref(c), float(obs_init or 0.0), _lib.ptr(q),
-              _lib.ptr(x), _lib.ptr(err), _lib.ptr(rtn_err), ctypes.byref(st), _lib.ptr(ws), int(ws.numel()),
-              _stream(dev))
+              _lib.ptr(_f32c(S)), _lib.ptr(_f32c(Vs)), ctypes.byref(c), float(obs_init or 0.0), _lib.ptr(Yu),
+              _lib.ptr(xr), _lib.ptr(q), _lib.ptr(x), _lib.ptr(err), _lib.ptr(rtn_err), _lib.ptr(xprod_out),
+              ctypes.byref(st), _lib.ptr(ws), int(ws.numel()), _stream(dev))
     stats = {name: getattr(st, name) for name, _ in st._fields_}
     return q, x, err, rtn_err, stats
 
 
 def uniform_cd_polish(W, q_in, scale, zero, group_size, maxq, Vs, H, *, block_rows: int, sweeps: int,
-                      accept_tol: float = 0.0, select: bool = True, Yu=None, x_in=None,
+                      accept_tol: float = 0.0, select: bool = True, Yu=None, x_in=None, xprod=None,
                       ws: Optional[torch.Tensor] = None):
     """Greedy scalar CD over all rows (greedy order per row block).  ``W`` may be None when ``Yu``
-    is given.  Returns (q, err_before, err_after, improved, accepted_per_row)."""
-    dev = _dev(q_in, scale, zero, Vs, H, W, Yu, x_in)
+    is given; ``xprod`` (optional) is the start's x Vs.  Returns (q, err_before, err_after, improved,
+    accepted_per_row)."""
+    dev = _dev(q_in, scale, zero, Vs, H, W, Yu, x_in, xprod)
     W = None if W is None else _f32c(W)
     Yu = None if Yu is None else _f32c(Yu)
     x_in = None if x_in is None else _f32c(x_in)
@@ -283,9 +290,10 @@ def uniform_cd_polish(W, q_in, scale, zero, group_size, maxq, Vs, H, *, block_ro
     ea = torch.empty(rows, dtype=F32, device=dev)
     imp = torch.zeros(rows, dtype=torch.int32, device=dev)
     acc = torch.zeros(rows, dtype=torch.int32, device=dev)
-    _lib.call("mpq_uniform_cd_polish", rows, n, int(maxq), int(block_rows), int(sweeps), float(accept_tol),
+    xprod = None if xprod is None else _f32c(xprod)
+    _lib.call("mpq_uniform_cd_polish_ex", rows, n, int(maxq), int(block_rows), int(sweeps), float(accept_tol),
               _lib.ptr(W), n, _lib.ptr(Yu), _lib.ptr(q_in.to(torch.uint8).contiguous()), _lib.ptr(x_in),
-              _lib.ptr(_f32c(scale)),
+              _lib.ptr(xprod), _lib.ptr(_f32c(scale)),
               _lib.ptr(_f32c(zero)), int(group_size), _lib.ptr(_f32c(Vs)), _lib.ptr(_f32c(H)), int(bool(select)),
               _lib.ptr(q_out), _lib.ptr(eb), _lib.ptr(ea), _lib.ptr(imp), _lib.ptr(acc), _lib.ptr(ws),
               int(ws.numel()), _stream(dev))

@@ -141,6 +141,34 @@ def test_vamp_block_matches_oracle(gpu, rotate, bits):
     assert abs(float(e.mean()) - float(e_ref.mean())) <= 5e-3 * float(e_ref.mean())
 
 
+def test_vamp_block_with_caller_products(gpu):
+    # mpq_uniform_vamp_solve_ex: W Vs and x_init Vs from the caller (one product over all rows), and
+    # the returned x_best Vs; matches the oracle like the per-block path, and x_best Vs is the
+    # product of the returned codes
+    W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq = _setup_block(128, 512, 4, 128, "vbx", rotate=True)
+    cfg = dict(RECIPE, polish_sweeps=0)
+    q_ref, x_ref, e_ref, rtn_ref, tr = ou.solve_uniform_rankspace_vamp(W, xr, sf, zf, maxq, V, V.T, S, Vs, cfg)
+    vcfg = UniformVampConfig(**{k: v for k, v in RECIPE.items()})
+    Wg, xg, Vsg = W.to(gpu), xr.to(gpu), Vs.to(gpu)
+    Yu, XR = ops.gemm(Wg, Vsg), ops.gemm(xg, Vsg)
+    xp = torch.empty_like(Yu)
+    q, x, e, rtn, st = ops.uniform_vamp_solve(Wg, xg, sg.to(gpu), zg.to(gpu), 128, maxq, V.to(gpu), S.to(gpu), Vsg,
+                                              vcfg, want_x=True, Yu=Yu, xr=XR, xprod_out=xp)
+    assert float((q.cpu().long() == q_ref.long()).float().mean()) >= 0.999
+    assert st["best_iter"] == tr["best_iter"] and st["stop_iter"] == tr["stop_iter"]
+    assert _rel(rtn.cpu(), rtn_ref) < 1e-4
+    assert abs(float(e.mean()) - float(e_ref.mean())) <= 5e-3 * float(e_ref.mean())
+    xp_ref = x.double().cpu() @ Vs.double()
+    assert float((xp.double().cpu() - xp_ref).abs().max()) <= 1e-5 * float(xp_ref.abs().max())
+    # the polish started from that product equals the polish that forms it
+    a = ops.uniform_cd_polish(None, q, sg.to(gpu), zg.to(gpu), 128, maxq, Vsg, Hw.to(gpu), block_rows=128,
+                              sweeps=3, select=True, Yu=Yu, xprod=xp)
+    b = ops.uniform_cd_polish(None, q, sg.to(gpu), zg.to(gpu), 128, maxq, Vsg, Hw.to(gpu), block_rows=128,
+                              sweeps=3, select=True, Yu=Yu)
+    assert float((a[0] == b[0]).float().mean()) >= 0.999
+    assert _rel(a[1].cpu(), b[1].cpu()) < 1e-4 and _rel(a[2].cpu(), b[2].cpu()) < 1e-4
+
+
 def test_cd_polish_matches_oracle(gpu):
     W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq = _setup_block(256, 512, 4, 128, "cd")
     q0 = torch.clamp(torch.round(W / sf) + zf, 0, maxq).to(torch.uint8)
