@@ -31,11 +31,12 @@ if ROOT not in sys.path:
 
 METRIC = "per-layer quantize ms (VAMP+3 CD) at 4096×14336; E8P12 Gvec/s; roofline %"
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 (matrix and packed vector)
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 E8_FLOP_PER_VEC = 12334  # factorized search
 
 
-PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_splitk_128x14336_pmc.md")
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_x6_128x14336_pmc.md")
 
 
 def pmc_traffic():
@@ -171,34 +172,40 @@ def set_pass(specs, weights, device, warmup):
 
 
 def gemm_roofline(n, device, reps=20, warmup=100):
-    """Live HIP-event timing of the dominant kernel: the split-K rank-space product
-    (128 x n) @ (n x n) as the VAMP drivers launch it (gemm_f32_full_kernel, partials only;
-    the drivers' epilogues sum the partials).  Events are recorded on the stream the kernel
-    is launched on (torch's current stream).  `warmup` untimed launches (~50 ms of work) come
-    first: after the host-side phases the GPU has idled down, and the timed launches should run at
-    the clock the layer solve runs at, not during the ramp-up."""
+    """Live HIP-event timing of the dominant VAMP kernel: the split-K rank-space product
+    (128 x n) @ (n x n) as the VAMP drivers launch it (gemm_x6_kernel on the packed rank-space
+    operator and the bf16 planes of A, partials only; the drivers' epilogues sum the partials).
+    Each fp32 multiply-add is six bf16 MFMA products, so the kernel executes 12 * 128 * n^2 bf16
+    flops per launch (2 * 128 * n^2 fp32-equivalent).  Events are recorded on the stream the kernel
+    is launched on (torch's current stream).  `warmup` untimed launches come first: after the
+    host-side phases the GPU has idled down, and the timed launches should run at the clock the
+    layer solve runs at, not during the ramp-up."""
     import torch
 
     from mpq_amd import ops
 
     A = torch.randn(128, n, device=device)
     B = torch.randn(n, n, device=device)
-    out, splits = ops.gemm_splitk(A, B)
+    Bp = ops.gemm_x6_pack_b(B)
+    Ap = ops.gemm_x6_pack_a(A)
+    out, splits = ops.gemm_x6_splitk(Ap, Bp, 128, n, n)
     for _ in range(warmup - 1):
-        ops.gemm_splitk(A, B, splits=splits, out=out)
+        ops.gemm_x6_splitk(Ap, Bp, 128, n, n, splits=splits, out=out)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(device)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record(stream)
     for _ in range(reps):
-        ops.gemm_splitk(A, B, splits=splits, out=out)
+        ops.gemm_x6_splitk(Ap, Bp, 128, n, n, splits=splits, out=out)
     e.record(stream)
     torch.cuda.synchronize()
     ms = s.elapsed_time(e) / reps
     flop = 2.0 * 128 * n * n
-    alg_bytes = 4.0 * (128 * n + n * n) + 4.0 * splits * 128 * n
+    # packed B (fp32), A planes (3 x bf16), split partials (fp32)
+    alg_bytes = 4.0 * n * n + 6.0 * 128 * n + 4.0 * splits * 128 * n
     return {"shape": f"128x{n}x{n}", "splits": splits, "ms": ms, "tflops": flop / ms / 1e9,
-            "alg_bytes": alg_bytes}
+            "bf16_tflops": 6.0 * flop / ms / 1e9, "alg_bytes": alg_bytes,
+            "hbm_GBps": alg_bytes / ms / 1e6}
 
 
 def denoise_roofline(device, rows=4096, n=14336, maxq=7, group=128, reps=20, warmup=20):
@@ -552,13 +559,16 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": f"gemm_f32_full_kernel (rank-space product 128x14336 @ 14336x14336, split-K {rf['splits']}, "
-                      "partials only, as the VAMP drivers launch it)",
-            "achieved": round(rf["tflops"], 2),
-            "peak": PEAK_FP32_TFLOPS,
+            "kernel": f"gemm_x6_kernel (rank-space product 128x14336 @ 14336x14336 as six bf16-plane MFMA "
+                      f"products per fp32 multiply-add, split-K {rf['splits']}, partials only, as the VAMP "
+                      "drivers launch it)",
+            "achieved": round(rf["bf16_tflops"], 2),
+            "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(rf["tflops"] / PEAK_FP32_TFLOPS, 4),
+            "frac": round(rf["bf16_tflops"] / PEAK_BF16_TFLOPS, 4),
             "traffic": pmc_traffic(),
+            "fp32_equivalent_tflops": round(rf["tflops"], 2),
+            "hbm_GBps_algorithmic": round(rf["hbm_GBps"], 1),
         },
         "layer_fp32_tflops": round(down_tflops, 2),
         "layer_roofline_frac": round(down_tflops / PEAK_FP32_TFLOPS, 4),

@@ -196,6 +196,43 @@ int mpq_gemm_f32_split_count(int64_t M, int64_t N, int64_t K);
 int mpq_gemm_f32_splitk(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B,
                         int64_t ldb, int trans_b, float* partials, int splits, mpq_stream_t stream);
 
+/*
+ * fp32 products on the bf16 matrix cores ("x6"): each operand is split exactly into three bf16
+ * planes and the six plane products of order >= 2^-16 |a||b| are accumulated in fp32
+ * (v_mfma_f32_32x32x16_bf16), which keeps the accuracy of an fp32 product (the dropped terms are
+ * below ~2^-22.4 |a||b| per multiply) at 8/3 the matrix-core rate of v_mfma_f32_32x32x2_f32.
+ * The large operand op(B) (K x N, N % 128 == 0, K % 32 == 0) is packed once into fragment-ordered
+ * tiles (K * N floats, mpq_gemm_x6_pack_b); mpq_gemm_x6 then forms C = A op(B) for any M, splitting
+ * and packing A in `workspace` (mpq_gemm_x6_workspace_size bytes) and reducing split-K partials in
+ * a fixed order.  Same products as mpq_gemm_f32 (no reference counterpart beyond those matmuls).
+ */
+int mpq_gemm_x6_pack_b(int64_t K, int64_t N, const float* B, int64_t ldb, int trans_b, float* packed,
+                       mpq_stream_t stream);
+int64_t mpq_gemm_x6_workspace_size(int64_t M, int64_t N, int64_t K);
+int mpq_gemm_x6(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B_packed,
+                float* C, int64_t ldc, void* workspace, int64_t workspace_bytes, mpq_stream_t stream);
+
+/*
+ * The two launches inside mpq_gemm_x6, as the VAMP solvers issue them: mpq_gemm_x6_pack_a splits
+ * and packs A (mpq_gemm_x6_packed_a_size bytes, 16-byte aligned); mpq_gemm_x6_splitk writes the
+ * split-K partials P[s] = A[:, Ks] op(B)[Ks, :] (splits x M x N, M*N apart; the library's split
+ * count is mpq_gemm_x6_split_count, 0 when the shape has no x6 path).
+ */
+int mpq_gemm_x6_split_count(int64_t M, int64_t N, int64_t K);
+int64_t mpq_gemm_x6_packed_a_size(int64_t M, int64_t K);
+int mpq_gemm_x6_pack_a(int64_t M, int64_t K, const float* A, int64_t lda, void* packed, mpq_stream_t stream);
+int mpq_gemm_x6_splitk(int64_t M, int64_t N, int64_t K, const void* A_packed, const float* B_packed,
+                       float* partials, int splits, mpq_stream_t stream);
+
+/*
+ * The rank-space operator of one linear packed for the x6 products of the VAMP solvers:
+ * 3 n^2 floats = [V packed for r V | V packed for x V^T | Vs packed for x Vs].
+ * mpq_rankspace_pack_floats returns 0 when n has no x6 path (n % 128 != 0).  Formed once per
+ * eigendecomposition and passed to mpq_uniform_vamp_solve_ex (`packed`).
+ */
+int64_t mpq_rankspace_pack_floats(int64_t n);
+int mpq_rankspace_pack(int64_t n, const float* V, const float* Vs, float* packed, mpq_stream_t stream);
+
 /* out = in^T (rows x cols -> cols x rows). */
 int mpq_transpose(const float* in, int64_t rows, int64_t cols, int64_t ld_in, float* out,
                   int64_t ld_out, mpq_stream_t stream);
@@ -400,15 +437,18 @@ int mpq_uniform_vamp_solve(int64_t rows, int64_t n, int maxq, const float* W, in
  * mpq/solver.py:467-480 and the warm start in mpq/adapters/gptqmodel.py:920-941):
  *   Yu_in (optional) rows x n = W Vs, xr_in (optional) rows x n = x_init Vs;
  *   xprod_out (optional) rows x n receives x_best Vs of the returned codes (the polish's start).
- * All three are contiguous (leading dimension n).
+ * All three are contiguous (leading dimension n).  `packed` (optional): the rank-space operator
+ * from mpq_rankspace_pack; the solver's products then run as x6 products (same accuracy class
+ * as the fp32 MFMA path).
  */
 int mpq_uniform_vamp_solve_ex(int64_t rows, int64_t n, int maxq, const float* W, int64_t ldw,
                               const float* x_init, const float* scale, const float* zero,
                               int64_t group_size, const float* V, const float* S, const float* Vs,
                               const MpqUniformVampConfig* cfg, double obs_init, const float* Yu_in,
-                              const float* xr_in, uint8_t* q_out, float* x_out, float* err_out,
-                              float* rtn_err_out, float* xprod_out, MpqUniformVampStats* stats,
-                              void* workspace, int64_t workspace_bytes, mpq_stream_t stream);
+                              const float* xr_in, const float* packed, uint8_t* q_out, float* x_out,
+                              float* err_out, float* rtn_err_out, float* xprod_out,
+                              MpqUniformVampStats* stats, void* workspace, int64_t workspace_bytes,
+                              mpq_stream_t stream);
 
 /* Workspace bytes needed by mpq_uniform_cd_polish. */
 int64_t mpq_uniform_cd_workspace_size(int64_t rows, int64_t n, int64_t block_rows);

@@ -77,7 +77,16 @@ SIGNATURES = {
                                       c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
     "mpq_uniform_vamp_solve_ex": (c_int, [c_i64, c_i64, c_int, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64,
                                           c_ptr, c_ptr, c_ptr, c_ptr, c_double, c_ptr, c_ptr, c_ptr, c_ptr,
-                                          c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
+                                          c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
+    "mpq_gemm_x6_pack_b": (c_int, [c_i64, c_i64, c_ptr, c_i64, c_int, c_ptr, c_ptr]),
+    "mpq_gemm_x6_workspace_size": (c_i64, [c_i64, c_i64, c_i64]),
+    "mpq_gemm_x6": (c_int, [c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_ptr]),
+    "mpq_gemm_x6_split_count": (c_int, [c_i64, c_i64, c_i64]),
+    "mpq_gemm_x6_packed_a_size": (c_i64, [c_i64, c_i64]),
+    "mpq_gemm_x6_pack_a": (c_int, [c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr]),
+    "mpq_gemm_x6_splitk": (c_int, [c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_int, c_ptr]),
+    "mpq_rankspace_pack_floats": (c_i64, [c_i64]),
+    "mpq_rankspace_pack": (c_int, [c_i64, c_ptr, c_ptr, c_ptr, c_ptr]),
     "mpq_uniform_cd_polish_ex": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_float, c_ptr, c_i64, c_ptr,
                                          c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_int, c_ptr,
                                          c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
@@ -203,15 +212,30 @@ def check(status: int, name: str) -> None:
         raise MPQLibraryError(f"{name} failed (status {status}): {text}")
 
 
+# Tensors whose pointers were taken for the next call(): an argument such as ptr(x.contiguous())
+# would otherwise free its temporary as soon as the address is read, and a later argument's
+# temporary could take the same block before the library reads it.  Kept until the call returns;
+# after that the work is enqueued on torch's current stream, whose allocator reuses a freed block
+# only for work ordered after it.
+_keep = threading.local()
+
+
 def call(name: str, *args) -> None:
     fn = getattr(load(), name)
-    check(fn(*args), name)
+    try:
+        check(fn(*args), name)
+    finally:
+        _keep.tensors = []
 
 
 def ptr(t) -> Optional[int]:
-    """Device pointer of a tensor, or None (NULL) for None."""
+    """Device pointer of a tensor, or None (NULL) for None; `t` stays alive until the next call()."""
     if t is None:
         return None
+    held = getattr(_keep, "tensors", None)
+    if held is None:
+        held = _keep.tensors = []
+    held.append(t)
     return int(t.data_ptr())
 
 

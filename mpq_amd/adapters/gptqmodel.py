@@ -50,6 +50,9 @@ class GPTQAdapterConfig:
     rotation_seed: int = 0
     auto_block_rows: bool = False
     eigen_cache: bool = True  # reuse the decomposition of an identical Hessian (q/k/v, gate/up)
+    # rank-space products as fp32-accurate bf16-plane products on the matrix cores (ops.gemm_x6)
+    # when cols % 128 == 0; False keeps every product on the fp32 MFMA kernel
+    x6_products: bool = True
 
 
 class MinMaxQuantizer:
@@ -235,8 +238,15 @@ def run_mpq_quantization(
     # Rank-space targets W Vs and the RTN decision's x_rtn Vs, formed once for all rows (the
     # reference forms them per row block inside the solver, mpq/solver.py:467-480); the row blocks
     # and the polish take slices, and each block returns its best decision's x Vs for the polish.
-    Yu_all = ops.gemm(W_work, Vs)
-    XR_all = ops.gemm(x_rtn, Vs)
+    # The rank-space operator packed once per linear for the bf16-plane products (None: fp32 path).
+    packed = ops.rankspace_pack(V, Vs) if bool(adapter_cfg.x6_products) else None
+    if packed is not None:
+        Vs_packed = packed[2 * cols * cols:]
+        Yu_all = ops.gemm_x6(W_work, Vs_packed, cols)
+        XR_all = ops.gemm_x6(x_rtn, Vs_packed, cols)
+    else:
+        Yu_all = ops.gemm(W_work, Vs)
+        XR_all = ops.gemm(x_rtn, Vs)
     # observation-precision warm start (reference :920-941): per block sums accumulated in double
     if float(getattr(vamp_cfg, "obs_precision", 0.0)) > 0.0:
         obs_precision = float(vamp_cfg.obs_precision)
@@ -259,14 +269,15 @@ def run_mpq_quantization(
         r1 = min(rows, r0 + block_rows)
         q_b, _, e_b, re_b, st = ops.uniform_vamp_solve(
             W_work[r0:r1], x_rtn[r0:r1], scale_groups[r0:r1], zero_groups[r0:r1], group_size, maxq, V, S, Vs,
-            vamp_cfg, obs_init=obs_block, ws=ws, Yu=Yu_all[r0:r1], xr=XR_all[r0:r1], xprod_out=XP_all[r0:r1])
+            vamp_cfg, obs_init=obs_block, ws=ws, Yu=Yu_all[r0:r1], xr=XR_all[r0:r1], xprod_out=XP_all[r0:r1],
+            packed=packed)
         q_int[r0:r1] = q_b
         err_vamp[r0:r1] = e_b
         rtn_err[r0:r1] = re_b
         if bool(getattr(vamp_cfg, "em_obs_precision", True)):
             obs_block = float(st["obs_precision_final"])
         block_stats.append(st)
-    del ws, XR_all
+    del ws, XR_all, packed
     torch.cuda.synchronize(device)
     timings["vamp_s"] = time.time() - t_solve
 

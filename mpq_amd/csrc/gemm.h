@@ -55,4 +55,18 @@ hipError_t gemm_lower(const float* A, int64_t lda, const float* B, int64_t ldb, 
                       int64_t ldc, int64_t M, int64_t K, float alpha, float beta, int upper_band,
                       hipStream_t stream);
 
+// fp32 products on the bf16 matrix cores (each operand split exactly into three bf16 planes, six
+// plane products; accuracy of an fp32 product, see gemm.hip).  B is packed once into fp32 tiles of
+// 128 columns x 16 k (K * N floats); A is split and packed per product (x6_packed_a_bytes).
+// Shapes: N % 128 == 0, K % 32 == 0; any M (rows past M are zero in the packed A).
+bool x6_shape_ok(int64_t N, int64_t K);
+int x6_choose_splits(int64_t M, int64_t N, int64_t K);
+int64_t x6_packed_a_bytes(int64_t M, int64_t K);
+hipError_t x6_pack_b(const float* B, int64_t ldb, bool trans_b, int64_t K, int64_t N, float* Bt, hipStream_t stream);
+hipError_t x6_pack_a(const float* A, int64_t lda, int64_t M, int64_t K, void* At, hipStream_t stream);
+// C[s] = A[:, K slice s] * op(B)[K slice s, :] for s < splits (K / splits a multiple of 32),
+// C[s] at C + s * split_stride with row stride ldc.
+hipError_t x6_gemm_partials(const void* At, const float* Bt, int64_t M, int64_t N, int64_t K, float* C, int64_t ldc,
+                            int64_t split_stride, int splits, hipStream_t stream);
+
 }  // namespace mpq

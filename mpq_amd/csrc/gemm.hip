@@ -455,6 +455,206 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_full_kernel(GemmParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// fp32 product on the bf16 matrix cores ("x6").  Every fp32 operand x is split into three bf16
+// planes,
+//   x0 = rn(x), x1 = rn(x - x0), x2 = rn(x - x0 - x1)   (rn: round to nearest bf16)
+// with |x1| <= 2^-8 |x|, |x2| <= 2^-16 |x| and |x - x0 - x1 - x2| <= 2^-24 |x|, and the product keeps
+// the six plane products of order >= 2^-16 |a||b|:
+//   a b = a0 b0 + (a0 b1 + a1 b0) + (a0 b2 + a1 b1 + a2 b0) + e,   |e| <= ~2^-22.4 |a||b|
+// (a1 b2 + a2 b1 + a2 b2 and the residues below the third planes), the size of one or two fp32
+// roundings of the product; a product of two bf16 values is exact in the fp32 accumulator.
+// v_mfma_f32_32x32x16_bf16 has 16x the flop rate of v_mfma_f32_32x32x2_f32, so the six products
+// of a 32x32x16 step take 3/8 of the fp32 instruction time.
+//
+// Operands are packed into 128-row x 16-k tiles in MFMA fragment order: chunk c = (blk*2 + h)*32 + r
+// of a tile holds row blk*32 + r at k = 16 ks + 8 h + (0..7).  B (the large, reused operand) is
+// packed once as fp32 [N/128][K/16][256 chunks][8]; A (small, re-formed per product) is split and
+// packed as bf16 planes [ceil(M/128)][K/16][3][256][8].  A work-group (128 x 128 tile, one K slice)
+// then reads each K slab as contiguous 12 KB (A, L2-resident) + 8 KB (B), splits B into planes on
+// its way to LDS, and runs 24 MFMAs per wave per slab.  Split s of tile t is block t * splits + s,
+// so with 8 or 16 splits every XCD (blocks are dispatched round-robin over 8) works on one or two
+// K slices and its L2 holds those slices of A.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t pk_bf16(float x, float y) {
+  const f32x2 v = {x, y};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));  // v_cvt_pk_bf16_f32 (RNE)
+}
+
+// Three bf16 planes of the pair (x, y), each packed low = x, high = y.
+__device__ __forceinline__ void split3(float x, float y, uint32_t& h, uint32_t& m, uint32_t& l) {
+  h = pk_bf16(x, y);
+  const float rx = x - __builtin_bit_cast(float, h << 16);
+  const float ry = y - __builtin_bit_cast(float, h & 0xffff0000u);
+  m = pk_bf16(rx, ry);
+  const float sx = rx - __builtin_bit_cast(float, m << 16);
+  const float sy = ry - __builtin_bit_cast(float, m & 0xffff0000u);
+  l = pk_bf16(sx, sy);
+}
+
+// B tiles: thread per chunk (8 floats).  trans_b: op(B)(k, n) = B[n*ldb + k] (32 contiguous bytes
+// per thread), else B[k*ldb + n] (lanes along n).
+template <bool TRANS_B>
+__global__ void x6_pack_b_kernel(const float* __restrict__ B, int64_t ldb, int64_t K, int64_t N, float* __restrict__ Bt) {
+  const int64_t KS = K / 16;
+  const int64_t nchunks = (N / 128) * KS * 256;
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < nchunks; q += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(q & 255);
+    const int64_t tk = q >> 8;  // nt * KS + ks
+    const int64_t nt = tk / KS, ks = tk - nt * KS;
+    const int64_t n = nt * 128 + (c >> 6) * 32 + (c & 31), k0 = ks * 16 + ((c >> 5) & 1) * 8;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = TRANS_B ? B[n * ldb + k0 + e] : B[(k0 + e) * ldb + n];
+    float4* d = reinterpret_cast<float4*>(Bt + q * 8);
+    d[0] = make_float4(v[0], v[1], v[2], v[3]);
+    d[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+// A planes: thread per chunk; rows >= M are zero.
+__global__ void x6_pack_a_kernel(const float* __restrict__ A, int64_t lda, int64_t M, int64_t K, uint4* __restrict__ At) {
+  const int64_t KS = K / 16;
+  const int64_t nchunks = ((M + 127) / 128) * KS * 256;
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < nchunks; q += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(q & 255);
+    const int64_t tk = q >> 8;  // mt * KS + ks
+    const int64_t mt = tk / KS, ks = tk - mt * KS;
+    const int64_t m = mt * 128 + (c >> 6) * 32 + (c & 31), k0 = ks * 16 + ((c >> 5) & 1) * 8;
+    float v[8];
+    if (m < M) {
+      const float* src = A + m * lda + k0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = src[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = 0.f;
+    }
+    uint4 h, mm, l;
+    split3(v[0], v[1], h.x, mm.x, l.x);
+    split3(v[2], v[3], h.y, mm.y, l.y);
+    split3(v[4], v[5], h.z, mm.z, l.z);
+    split3(v[6], v[7], h.w, mm.w, l.w);
+    uint4* d = At + tk * 768 + c;
+    d[0] = h;
+    d[256] = mm;
+    d[512] = l;
+  }
+}
+
+// C[split] (rows < M) = A[:, K slice] * op(B)[K slice, :] from the packed operands.  Every K slice
+// is an even number of 16-k slabs.
+__global__ __launch_bounds__(kThreads) void gemm_x6_kernel(int64_t M, int64_t N, int64_t K, const uint4* __restrict__ At,
+                                                           const float* __restrict__ Bt, float* __restrict__ C,
+                                                           int64_t ldc, int64_t split_stride, int64_t k_per_split,
+                                                           int splits) {
+  __shared__ uint4 As[2][3][256];
+  __shared__ uint4 Bs[2][3][256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wmb = (wave >> 1) * 2, wnb = (wave & 1) * 2;  // 2 x 2 waves of 64 x 64
+  const int64_t bid = blockIdx.x;
+  const int split = (int)(bid % splits);
+  const int64_t tile = bid / splits;
+  const int64_t ntn = N / 128;
+  const int64_t mt = tile / ntn, nt = tile - mt * ntn;
+  const int64_t KS = K / 16;
+  const int nslab = (int)(k_per_split / 16);
+  const int64_t ks0 = (int64_t)split * nslab;
+  // A slab: 768 chunks (3 planes), thread -> chunks tid + 256 j; B slab: 512 float4, thread -> float4
+  // tid + 256 j = half tid%2 of chunk 128 j + tid/2
+  const u32x4v* asrc = reinterpret_cast<const u32x4v*>(At) + (mt * KS + ks0) * 768 + tid;
+  const f32x4v* bsrc = reinterpret_cast<const f32x4v*>(Bt) + (nt * KS + ks0) * 512 + tid;
+  const int bc = tid >> 1, bh = tid & 1;
+
+  u32x4v qa0[3], qa1[3];
+  f32x4v qb0[2], qb1[2];
+  auto gload = [&](u32x4v (&qa)[3], f32x4v (&qb)[2], int64_t s) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) qa[j] = asrc[s * 768 + j * 256];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) qb[j] = bsrc[s * 512 + j * 256];
+  };
+  auto lstore = [&](const u32x4v (&qa)[3], const f32x4v (&qb)[2], int buf) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) As[buf][j][tid] = __builtin_bit_cast(uint4, qa[j]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uint2 h, m, l;
+      split3(qb[j].x, qb[j].y, h.x, m.x, l.x);
+      split3(qb[j].z, qb[j].w, h.y, m.y, l.y);
+      const int c = j * 128 + bc;
+      reinterpret_cast<uint2*>(&Bs[buf][0][c])[bh] = h;
+      reinterpret_cast<uint2*>(&Bs[buf][1][c])[bh] = m;
+      reinterpret_cast<uint2*>(&Bs[buf][2][c])[bh] = l;
+    }
+  };
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  auto compute = [&](int buf) {
+    bf16x8 a[3][2], b[3][2];
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[pl][i] = __builtin_bit_cast(bf16x8, As[buf][pl][(wmb + i) * 64 + lane]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[pl][j] = __builtin_bit_cast(bf16x8, Bs[buf][pl][(wnb + j) * 64 + lane]);
+    }
+    // smallest terms first; the (i, j) loop innermost keeps four independent accumulator chains
+    constexpr int pa[6] = {2, 1, 0, 1, 0, 0};
+    constexpr int pb[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+    for (int t = 0; t < 6; ++t)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[pa[t]][i], b[pb[t]][j], acc[i][j], 0, 0, 0);
+  };
+
+  // same two-slabs-in-flight schedule as gemm_f32_full_kernel
+  gload(qa0, qb0, 0);
+  gload(qa1, qb1, 1);
+  lstore(qa0, qb0, 0);
+  __syncthreads();
+  for (int s = 0; s < nslab; s += 2) {
+    if (s + 2 < nslab) gload(qa0, qb0, s + 2);
+    compute(0);
+    lstore(qa1, qb1, 1);
+    __syncthreads();
+    if (s + 3 < nslab) gload(qa1, qb1, s + 3);
+    compute(1);
+    if (s + 2 < nslab) lstore(qa0, qb0, 0);
+    __syncthreads();
+  }
+
+  // lane l, accumulator v -> row 8*(v/4) + 4*(l/32) + v%4, column l%32 of the 32 x 32 block
+  const int col = lane & 31, rbase = (lane >> 5) * 4;
+  float* Cs = C + (int64_t)split * split_stride;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t gn = nt * 128 + (wnb + j) * 32 + col;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t gm = mt * 128 + (wmb + i) * 32 + (v >> 2) * 8 + rbase + (v & 3);
+        if (gm < M) Cs[gm * ldc + gn] = acc[i][j][v];
+      }
+    }
+}
+
 template <int BM, int BN, int WM, int WN>
 hipError_t launch_cfg(const GemmParams& p, dim3 grid, hipStream_t stream) {
   // interior-tile kernel: whole tiles, an even number of 16-wide K slabs per split; a row gather
@@ -525,6 +725,47 @@ hipError_t splitk_reduce(const float* P, int splits, int64_t M, int64_t N, float
   if (blocks > 8192) blocks = 8192;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, P, splits,
                      M * N, M, N, C, ldc, alpha, beta);
+  return hipGetLastError();
+}
+
+bool x6_shape_ok(int64_t N, int64_t K) { return N > 0 && K > 0 && N % 128 == 0 && K % 32 == 0; }
+
+int x6_choose_splits(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = ((M + 127) / 128) * (N / 128);
+  int splits = 1;
+  while (splits < 16 && tiles * splits * 2 <= 2048 && K % (splits * 2 * 32) == 0 && K / (splits * 2) >= 256)
+    splits *= 2;
+  return splits;
+}
+
+int64_t x6_packed_a_bytes(int64_t M, int64_t K) { return ((M + 127) / 128) * 128 * K * 6; }
+
+static unsigned grid_for(int64_t items) {
+  int64_t b = (items + 255) / 256;
+  return (unsigned)(b < 1 ? 1 : b > 16384 ? 16384 : b);
+}
+
+hipError_t x6_pack_b(const float* B, int64_t ldb, bool trans_b, int64_t K, int64_t N, float* Bt, hipStream_t stream) {
+  const unsigned g = grid_for((N / 128) * (K / 16) * 256);
+  if (trans_b) hipLaunchKernelGGL(x6_pack_b_kernel<true>, dim3(g), dim3(256), 0, stream, B, ldb, K, N, Bt);
+  else hipLaunchKernelGGL(x6_pack_b_kernel<false>, dim3(g), dim3(256), 0, stream, B, ldb, K, N, Bt);
+  return hipGetLastError();
+}
+
+hipError_t x6_pack_a(const float* A, int64_t lda, int64_t M, int64_t K, void* At, hipStream_t stream) {
+  const unsigned g = grid_for(((M + 127) / 128) * (K / 16) * 256);
+  hipLaunchKernelGGL(x6_pack_a_kernel, dim3(g), dim3(256), 0, stream, A, lda, M, K, static_cast<uint4*>(At));
+  return hipGetLastError();
+}
+
+hipError_t x6_gemm_partials(const void* At, const float* Bt, int64_t M, int64_t N, int64_t K, float* C, int64_t ldc,
+                            int64_t split_stride, int splits, hipStream_t stream) {
+  const int64_t kps = K / splits;
+  if (!x6_shape_ok(N, K) || splits < 1 || K % splits != 0 || kps % 32 != 0) return hipErrorInvalidValue;
+  const int64_t blocks = ((M + 127) / 128) * (N / 128) * splits;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gemm_x6_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, M, N, K,
+                     static_cast<const uint4*>(At), Bt, C, ldc, split_stride, kps, splits);
   return hipGetLastError();
 }
 
@@ -604,5 +845,84 @@ extern "C" int mpq_gemm_f32_splitk(int64_t M, int64_t N, int64_t K, const float*
   p.C = partials; p.ldc = N; p.split_stride = M * N;
   p.alpha = 1.f; p.beta = 0.f; p.mode = mpq::kGemmPartials;
   MPQ_HIP_TRY(mpq::gemm_partials(p, splits, bn, stream));
+  return mpq::kOk;
+}
+
+extern "C" int mpq_gemm_x6_pack_b(int64_t K, int64_t N, const float* B, int64_t ldb, int trans_b, float* packed,
+                                  hipStream_t stream) {
+  MPQ_CHECK_ARG(mpq::x6_shape_ok(N, K), "mpq_gemm_x6_pack_b: needs N %% 128 == 0 and K %% 32 == 0 (N=%lld K=%lld)",
+                (long long)N, (long long)K);
+  MPQ_CHECK_ARG(B && packed, "mpq_gemm_x6_pack_b: null operand");
+  MPQ_CHECK_ARG(trans_b ? ldb >= K : ldb >= N, "mpq_gemm_x6_pack_b: ldb too small");
+  MPQ_HIP_TRY(mpq::x6_pack_b(B, ldb, trans_b != 0, K, N, packed, stream));
+  return mpq::kOk;
+}
+
+extern "C" int64_t mpq_gemm_x6_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || !mpq::x6_shape_ok(N, K)) return 0;
+  const int splits = mpq::x6_choose_splits(M, N, K);
+  return (mpq::x6_packed_a_bytes(M, K) + 255) / 256 * 256 + (int64_t)splits * M * N * 4;
+}
+
+extern "C" int mpq_gemm_x6(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B_packed,
+                           float* C, int64_t ldc, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  MPQ_CHECK_ARG(M >= 0, "mpq_gemm_x6: negative M");
+  if (M == 0) return mpq::kOk;
+  MPQ_CHECK_ARG(mpq::x6_shape_ok(N, K), "mpq_gemm_x6: needs N %% 128 == 0 and K %% 32 == 0 (N=%lld K=%lld)",
+                (long long)N, (long long)K);
+  MPQ_CHECK_ARG(A && B_packed && C && workspace, "mpq_gemm_x6: null operand");
+  MPQ_CHECK_ARG(lda >= K && ldc >= N, "mpq_gemm_x6: leading dimension too small");
+  MPQ_CHECK_ARG((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "mpq_gemm_x6: workspace must be 256-byte aligned");
+  const int64_t need = mpq_gemm_x6_workspace_size(M, N, K);
+  MPQ_CHECK_ARG(workspace_bytes >= need, "mpq_gemm_x6: workspace too small (%lld < %lld bytes)",
+                (long long)workspace_bytes, (long long)need);
+  const int splits = mpq::x6_choose_splits(M, N, K);
+  char* ws = static_cast<char*>(workspace);
+  float* P = reinterpret_cast<float*>(ws + (mpq::x6_packed_a_bytes(M, K) + 255) / 256 * 256);
+  MPQ_HIP_TRY(mpq::x6_pack_a(A, lda, M, K, ws, stream));
+  MPQ_HIP_TRY(mpq::x6_gemm_partials(ws, B_packed, M, N, K, P, N, M * N, splits, stream));
+  MPQ_HIP_TRY(mpq::splitk_reduce(P, splits, M, N, C, ldc, 1.f, 0.f, stream));
+  return mpq::kOk;
+}
+
+extern "C" int64_t mpq_rankspace_pack_floats(int64_t n) {
+  return (n > 0 && mpq::x6_shape_ok(n, n)) ? 3 * n * n : 0;
+}
+
+extern "C" int mpq_rankspace_pack(int64_t n, const float* V, const float* Vs, float* packed, hipStream_t stream) {
+  MPQ_CHECK_ARG(n > 0 && mpq::x6_shape_ok(n, n), "mpq_rankspace_pack: n must be a positive multiple of 128 (n=%lld)",
+                (long long)n);
+  MPQ_CHECK_ARG(V && Vs && packed, "mpq_rankspace_pack: null operand");
+  MPQ_HIP_TRY(mpq::x6_pack_b(V, n, false, n, n, packed, stream));
+  MPQ_HIP_TRY(mpq::x6_pack_b(V, n, true, n, n, packed + n * n, stream));
+  MPQ_HIP_TRY(mpq::x6_pack_b(Vs, n, false, n, n, packed + 2 * n * n, stream));
+  return mpq::kOk;
+}
+
+extern "C" int mpq_gemm_x6_split_count(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || !mpq::x6_shape_ok(N, K)) return 0;
+  return mpq::x6_choose_splits(M, N, K);
+}
+
+extern "C" int64_t mpq_gemm_x6_packed_a_size(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0 || K % 32 != 0) return 0;
+  return mpq::x6_packed_a_bytes(M, K);
+}
+
+extern "C" int mpq_gemm_x6_pack_a(int64_t M, int64_t K, const float* A, int64_t lda, void* packed, hipStream_t stream) {
+  MPQ_CHECK_ARG(M > 0 && K > 0 && K % 32 == 0, "mpq_gemm_x6_pack_a: needs M > 0 and K %% 32 == 0");
+  MPQ_CHECK_ARG(A && packed && lda >= K, "mpq_gemm_x6_pack_a: null operand or lda < K");
+  MPQ_CHECK_ARG((reinterpret_cast<uintptr_t>(packed) & 15u) == 0, "mpq_gemm_x6_pack_a: packed must be 16-byte aligned");
+  MPQ_HIP_TRY(mpq::x6_pack_a(A, lda, M, K, packed, stream));
+  return mpq::kOk;
+}
+
+extern "C" int mpq_gemm_x6_splitk(int64_t M, int64_t N, int64_t K, const void* A_packed, const float* B_packed,
+                                  float* partials, int splits, hipStream_t stream) {
+  MPQ_CHECK_ARG(M > 0 && mpq::x6_shape_ok(N, K), "mpq_gemm_x6_splitk: needs M > 0, N %% 128 == 0, K %% 32 == 0");
+  MPQ_CHECK_ARG(splits >= 1 && K % splits == 0 && (K / splits) % 32 == 0,
+                "mpq_gemm_x6_splitk: K / splits must be a whole multiple of 32");
+  MPQ_CHECK_ARG(A_packed && B_packed && partials, "mpq_gemm_x6_splitk: null operand");
+  MPQ_HIP_TRY(mpq::x6_gemm_partials(A_packed, B_packed, M, N, K, partials, N, M * N, splits, stream));
   return mpq::kOk;
 }

@@ -22,6 +22,9 @@ struct UniformProblem {
   const float* Yu_in = nullptr;   // W Vs
   const float* xr_in = nullptr;   // x_init Vs
   float* xprod_out = nullptr;     // receives x_best Vs of the returned decision
+  // optional packed rank-space operator (mpq_rankspace_pack: V for r V, V for x V^T, Vs for x Vs);
+  // when given, the products run on the bf16 matrix cores (x6_gemm_partials)
+  const float* packed = nullptr;
 };
 
 }  // namespace mpq

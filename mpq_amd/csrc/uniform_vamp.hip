@@ -18,6 +18,7 @@
 // hard-state error: error mean, EM statistic).  All arithmetic follows the
 // reference's operation order where it matters for decisions (scores, MAP,
 // rounding); the file is compiled with -ffp-contract=off.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -165,19 +166,23 @@ struct Workspace {
   float* prod_cur;   // xs Vs of the current / best hard state (kept when the caller asks for it)
   float* prod_best;
   float* P;   // split-K partials
+  void* Ap;   // packed bf16 planes of the left operand (x6 products)
   float* rowbuf;  // per-row arrays
   float* part;    // chunk partials (3 per row per chunk)
   uint8_t* q_cur;
   uint8_t* q_best;
   VampStatus* status;
-  int splits;
+  int splits;      // of the active product path
+  int splits_f32;
+  int splits_x6;   // 0 if the shape has no x6 path
   int bn;
+  const float* packed;  // rank-space operator of the x6 path, or null (fp32 path)
 };
 
 inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 struct Sizes {
-  int64_t rows, n, nchunks, splits, bn;
+  int64_t rows, n, nchunks, splits, splits_x6, bn;
   int64_t bytes;
 };
 
@@ -188,11 +193,13 @@ Sizes plan(int64_t rows, int64_t n) {
   s.nchunks = (n + kChunk - 1) / kChunk;
   int bn = 128;
   s.splits = choose_splits(rows, n, n, (int64_t)1 << 62, &bn);
+  s.splits_x6 = x6_shape_ok(n, n) ? x6_choose_splits(rows, n, n) : 0;
   s.bn = bn;
   const int64_t mat = align_up(rows * n, 64) * 4;
   int64_t bytes = 0;
   bytes += 8 * mat;                                   // Yu r1 r2 r2prev x1 xs prod_cur prod_best
-  bytes += s.splits * mat;                            // P
+  bytes += std::max(s.splits, s.splits_x6) * mat;     // P
+  bytes += s.splits_x6 ? align_up(x6_packed_a_bytes(rows, n), 256) : 0;  // Ap
   bytes += align_up(32 * rows, 64) * 4;               // row arrays
   bytes += align_up(3 * rows * s.nchunks, 64) * 4;    // chunk partials
   bytes += 2 * align_up(rows * n, 256);               // q_cur q_best
@@ -213,14 +220,18 @@ Workspace carve(void* base, const Sizes& s) {
   w.xs = (float*)p; p += mat;
   w.prod_cur = (float*)p; p += mat;
   w.prod_best = (float*)p; p += mat;
-  w.P = (float*)p; p += s.splits * mat;
+  w.P = (float*)p; p += std::max(s.splits, s.splits_x6) * mat;
+  w.Ap = s.splits_x6 ? (void*)p : nullptr;
+  p += s.splits_x6 ? align_up(x6_packed_a_bytes(s.rows, s.n), 256) : 0;
   w.rowbuf = (float*)p; p += align_up(32 * s.rows, 64) * 4;
   w.part = (float*)p; p += align_up(3 * s.rows * s.nchunks, 64) * 4;
   w.q_cur = (uint8_t*)p; p += align_up(s.rows * s.n, 256);
   w.q_best = (uint8_t*)p; p += align_up(s.rows * s.n, 256);
   w.status = (VampStatus*)p;
-  w.splits = (int)s.splits;
+  w.splits = w.splits_f32 = (int)s.splits;
+  w.splits_x6 = (int)s.splits_x6;
   w.bn = (int)s.bn;
+  w.packed = nullptr;
   return w;
 }
 
@@ -235,9 +246,20 @@ VampStatus* host_status() {
 
 }  // namespace
 
-// P = A @ op(B) as split-K partials into w.P (split_stride rows*n).
-static hipError_t product(const Workspace& w, const float* A, const float* B, bool trans_b,
+// Rank-space operands of the products (index into the packed operator).
+enum RankOperand : int { kOpV = 0, kOpVt = 1, kOpVs = 2 };
+
+// P = A @ op(B) as split-K partials into w.P (split_stride rows*n, w.splits of them).  With a packed
+// operator the product runs on the bf16 matrix cores (A split into planes first), else on the
+// fp32 MFMA kernel.
+static hipError_t product(const Workspace& w, const float* A, const float* B, bool trans_b, RankOperand op,
                           int64_t rows, int64_t n, hipStream_t stream) {
+  if (w.packed) {
+    hipError_t e = x6_pack_a(A, n, rows, n, w.Ap, stream);
+    if (e != hipSuccess) return e;
+    return x6_gemm_partials(w.Ap, w.packed + (int64_t)op * n * n, rows, n, n, w.P, n, align_up(rows * n, 64),
+                            w.splits, stream);
+  }
   GemmParams p{};
   p.M = rows; p.N = n; p.K = n;
   p.A = A; p.lda = n; p.B = B; p.ldb = n; p.trans_b = trans_b; p.b_rows = nullptr;
@@ -258,6 +280,10 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
   MPQ_CHECK_ARG(workspace_bytes >= sz.bytes, "uniform VAMP: workspace too small (%lld < %lld bytes)",
                 (long long)workspace_bytes, (long long)sz.bytes);
   Workspace w = carve(workspace, sz);
+  if (pr.packed && w.splits_x6 > 0) {
+    w.packed = pr.packed;
+    w.splits = w.splits_x6;
+  }
   const float* Yu = pr.Yu_in ? pr.Yu_in : w.Yu;
   VampStatus* hs = host_status();
   MPQ_CHECK_ARG(hs != nullptr, "uniform VAMP: pinned status buffer unavailable");
@@ -298,7 +324,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
                          w.q_cur, w.xs);
     }
     MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(product(w, w.xs, Vs, false, rows, n, stream));
+    MPQ_HIP_TRY(product(w, w.xs, Vs, false, kOpVs, rows, n, stream));
     hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, w.part,
                        pr.xprod_out ? w.prod_cur : nullptr);
     hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, w.part, err_cur, w.status);
@@ -315,7 +341,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
       MPQ_HIP_TRY(hipMemcpy2DAsync(w.r1, n * 4, pr.W, pr.ldw * 4, n * 4, rows, hipMemcpyDeviceToDevice, stream));
       Wc = w.r1;
     }
-    MPQ_HIP_TRY(product(w, Wc, Vs, false, rows, n, stream));
+    MPQ_HIP_TRY(product(w, Wc, Vs, false, kOpVs, rows, n, stream));
     MPQ_HIP_TRY(splitk_reduce(w.P, w.splits, rows, n, w.Yu, n, 1.f, 0.f, stream));
   }
   // RTN error (rtn_err, and the obs warm start when none is given), from x_init Vs (or the caller's)
@@ -323,7 +349,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, pr.xr_in, 1, (int64_t)0, Yu, w.part, nullptr);
   } else {
     MPQ_HIP_TRY(hipMemcpy2DAsync(w.xs, n * 4, pr.x_init, pr.ldw * 4, n * 4, rows, hipMemcpyDeviceToDevice, stream));
-    MPQ_HIP_TRY(product(w, w.xs, Vs, false, rows, n, stream));
+    MPQ_HIP_TRY(product(w, w.xs, Vs, false, kOpVs, rows, n, stream));
     hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, w.part, nullptr);
   }
   hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, w.part,
@@ -409,13 +435,13 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     hipLaunchKernelGGL(msg_r2_kernel, eg, eb, 0, stream, n, w.x1, w.r1, eta1, g1w, g2new,
                        has_prev ? 1 : 0, damping, w.r2prev, w.r2);
     MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(product(w, w.r2, pr.V, false, rows, n, stream));
+    MPQ_HIP_TRY(product(w, w.r2, pr.V, false, kOpV, rows, n, stream));
     hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, pr.S, g2,
                        obs_f, w.x1, w.part);
     hipLaunchKernelGGL(rows_lmmse_kernel, dim3(1), eb, 0, stream, rows, n, n, nchunks, w.part, g2, damping,
                        eta2, g1new, g1, w.status);
     MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(product(w, w.x1, pr.V, true, rows, n, stream));
+    MPQ_HIP_TRY(product(w, w.x1, pr.V, true, kOpVt, rows, n, stream));
     hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.r2, eta2, g2,
                        g1new, damping, w.r1);
     MPQ_LAUNCH_CHECK();
@@ -502,7 +528,7 @@ extern "C" int mpq_uniform_vamp_solve(int64_t rows, int64_t n, int maxq, const f
                                       MpqUniformVampStats* stats, void* workspace,
                                       int64_t workspace_bytes, hipStream_t stream) {
   return mpq_uniform_vamp_solve_ex(rows, n, maxq, W, ldw, x_init, scale, zero, group_size, V, S, Vs, cfg, obs_init,
-                                   nullptr, nullptr, q_out, x_out, err_out, rtn_err_out, nullptr, stats, workspace,
+                                   nullptr, nullptr, nullptr, q_out, x_out, err_out, rtn_err_out, nullptr, stats, workspace,
                                    workspace_bytes, stream);
 }
 
@@ -511,7 +537,8 @@ extern "C" int mpq_uniform_vamp_solve_ex(int64_t rows, int64_t n, int maxq, cons
                                          int64_t group_size, const float* V, const float* S,
                                          const float* Vs, const MpqUniformVampConfig* cfg,
                                          double obs_init, const float* Yu_in, const float* xr_in,
-                                         uint8_t* q_out, float* x_out, float* err_out, float* rtn_err_out,
+                                         const float* packed, uint8_t* q_out, float* x_out, float* err_out,
+                                         float* rtn_err_out,
                                          float* xprod_out, MpqUniformVampStats* stats, void* workspace,
                                          int64_t workspace_bytes, hipStream_t stream) {
   MPQ_CHECK_ARG(rows > 0 && n > 0, "mpq_uniform_vamp_solve: empty problem");
@@ -524,7 +551,7 @@ extern "C" int mpq_uniform_vamp_solve_ex(int64_t rows, int64_t n, int maxq, cons
   mpq::UniformProblem pr{};
   pr.rows = rows; pr.n = n; pr.maxq = maxq; pr.W = W; pr.x_init = x_init; pr.scale = scale;
   pr.zero = zero; pr.group_size = group_size; pr.V = V; pr.S = S; pr.ldw = ldw;
-  pr.Yu_in = Yu_in; pr.xr_in = xr_in; pr.xprod_out = xprod_out;
+  pr.Yu_in = Yu_in; pr.xr_in = xr_in; pr.xprod_out = xprod_out; pr.packed = packed;
   return mpq::uniform_vamp_solve(pr, Vs, *cfg, obs_init, q_out, x_out, err_out, rtn_err_out, stats,
                                  workspace, workspace_bytes, stream);
 }

@@ -80,6 +80,78 @@ def gemm(A: torch.Tensor, B: torch.Tensor, *, trans_b: bool = False, b_rows: Opt
     return out
 
 
+def gemm_x6_pack_b(B: torch.Tensor, *, trans_b: bool = False) -> torch.Tensor:
+    """op(B) (K x N; N % 128 == 0, K % 32 == 0) packed for :func:`gemm_x6` (K * N floats)."""
+    dev = _dev(B)
+    B = _f32c(B)
+    K, N = (int(B.shape[1]), int(B.shape[0])) if trans_b else (int(B.shape[0]), int(B.shape[1]))
+    out = torch.empty(K * N, dtype=F32, device=dev)
+    _lib.call("mpq_gemm_x6_pack_b", K, N, _lib.ptr(B), int(B.shape[1]), int(bool(trans_b)), _lib.ptr(out),
+              _stream(dev))
+    return out
+
+
+def gemm_x6(A: torch.Tensor, B_packed: torch.Tensor, N: int, *, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """C = A @ op(B) with op(B) packed by :func:`gemm_x6_pack_b`: fp32 product on the bf16 matrix
+    cores (three bf16 planes per operand, six plane products)."""
+    dev = _dev(A, B_packed)
+    A = _f32c(A)
+    M, K = A.shape
+    if int(B_packed.numel()) != K * int(N) or B_packed.dtype != F32:
+        raise ValueError("B_packed must hold K * N float32 values from gemm_x6_pack_b")
+    if out is None:
+        out = torch.empty(M, int(N), dtype=F32, device=dev)
+    elif out.dtype != F32 or not out.is_contiguous() or tuple(out.shape) != (M, int(N)):
+        raise ValueError("out must be a contiguous fp32 (M, N) tensor")
+    lib = _lib.load()
+    need = int(lib.mpq_gemm_x6_workspace_size(M, int(N), K))
+    ws = workspace(need, dev)
+    _lib.call("mpq_gemm_x6", M, int(N), K, _lib.ptr(A), K, _lib.ptr(B_packed), _lib.ptr(out), int(N), _lib.ptr(ws),
+              int(ws.numel()), _stream(dev))
+    return out
+
+
+def gemm_x6_pack_a(A: torch.Tensor) -> torch.Tensor:
+    """A (M x K, K % 32 == 0) split into bf16 planes and packed for :func:`gemm_x6_splitk` (uint8 buffer)."""
+    dev = _dev(A)
+    A = _f32c(A)
+    M, K = A.shape
+    lib = _lib.load()
+    out = torch.empty(int(lib.mpq_gemm_x6_packed_a_size(M, K)), dtype=torch.uint8, device=dev)
+    _lib.call("mpq_gemm_x6_pack_a", M, K, _lib.ptr(A), K, _lib.ptr(out), _stream(dev))
+    return out
+
+
+def gemm_x6_splitk(A_packed: torch.Tensor, B_packed: torch.Tensor, M: int, N: int, K: int, *,
+                   splits: Optional[int] = None, out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, int]:
+    """Split-K partials (splits, M, N) of the x6 product from packed operands (the VAMP solvers' launch)."""
+    dev = _dev(A_packed, B_packed, out)
+    lib = _lib.load()
+    s = int(splits) if splits is not None else int(lib.mpq_gemm_x6_split_count(M, N, K))
+    if out is None:
+        out = torch.empty(s, M, N, dtype=F32, device=dev)
+    elif tuple(out.shape) != (s, M, N) or out.dtype != F32 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous fp32 (splits, M, N) tensor")
+    _lib.call("mpq_gemm_x6_splitk", M, N, K, _lib.ptr(A_packed), _lib.ptr(B_packed), _lib.ptr(out), s, _stream(dev))
+    return out, s
+
+
+def rankspace_pack(V: torch.Tensor, Vs: torch.Tensor) -> Optional[torch.Tensor]:
+    """The packed rank-space operator (V for r V, V for x V^T, Vs for x Vs) of the VAMP solvers' x6
+    products, or None when n has no x6 path (n % 128 != 0)."""
+    dev = _dev(V, Vs)
+    n = int(V.shape[0])
+    if tuple(V.shape) != (n, n) or tuple(Vs.shape) != (n, n):
+        raise ValueError("rankspace_pack needs square V and Vs of the same order")
+    lib = _lib.load()
+    floats = int(lib.mpq_rankspace_pack_floats(n))
+    if floats == 0:
+        return None
+    out = torch.empty(floats, dtype=F32, device=dev)
+    _lib.call("mpq_rankspace_pack", n, _lib.ptr(_f32c(V)), _lib.ptr(_f32c(Vs)), _lib.ptr(out), _stream(dev))
+    return out
+
+
 # ---- quantizer helpers ----------------------------------------------------
 
 def gemm_splitk(A: torch.Tensor, B: torch.Tensor, *, trans_b: bool = False, splits: Optional[int] = None,
@@ -238,17 +310,21 @@ def vamp_config_c(cfg) -> "_lib.UniformVampConfigC":
 
 def uniform_vamp_solve(W, x_init, scale, zero, group_size, maxq, V, S, Vs, cfg, obs_init: float = 0.0,
                        want_x: bool = False, ws: Optional[torch.Tensor] = None, Yu=None, xr=None,
-                       xprod_out: Optional[torch.Tensor] = None):
+                       xprod_out: Optional[torch.Tensor] = None, packed: Optional[torch.Tensor] = None):
     """One row block of the uniform VAMP loop.  Returns (q uint8, x|None, err, rtn_err, stats dict).
     ``Yu`` = W Vs and ``xr`` = x_init Vs may come from the caller (formed once for all row blocks);
-    ``xprod_out`` (rows x n, contiguous fp32) then receives x_best Vs of the returned codes."""
-    dev = _dev(W, x_init, scale, zero, V, S, Vs, Yu, xr, xprod_out)
+    ``xprod_out`` (rows x n, contiguous fp32) then receives x_best Vs of the returned codes.
+    ``packed`` (from :func:`rankspace_pack`) runs the solver's products on the bf16 matrix cores."""
+    dev = _dev(W, x_init, scale, zero, V, S, Vs, Yu, xr, xprod_out, packed)
     W = _f32c(W)
     x_init = _f32c(x_init)
     rows, n = W.shape
     if tuple(V.shape) != (n, n) or int(S.numel()) != n or tuple(Vs.shape) != (n, n):
         raise ValueError("mpq_amd uniform VAMP needs full rank: V, Vs (n x n) and S (n)")
     lib = _lib.load()
+    if packed is not None and (packed.dtype != F32 or not packed.is_contiguous()
+                               or int(packed.numel()) != int(lib.mpq_rankspace_pack_floats(n)) or n % 128):
+        raise ValueError("packed must be the float32 rank-space operator from rankspace_pack for this n")
     need = int(lib.mpq_uniform_vamp_workspace_size(rows, n))
     if ws is None or ws.numel() < need:
         ws = workspace(need, dev)
@@ -264,7 +340,8 @@ def uniform_vamp_solve(W, x_init, scale, zero, group_size, maxq, V, S, Vs, cfg, 
     _lib.call("mpq_uniform_vamp_solve_ex", rows, n, int(maxq), _lib.ptr(W), n, _lib.ptr(x_init),
               _lib.ptr(_f32c(scale)), _lib.ptr(_f32c(zero)), int(group_size), _lib.ptr(_f32c(V)),
               _lib.ptr(_f32c(S)), _lib.ptr(_f32c(Vs)), ctypes.byref(c), float(obs_init or 0.0), _lib.ptr(Yu),
-              _lib.ptr(xr), _lib.ptr(q), _lib.ptr(x), _lib.ptr(err), _lib.ptr(rtn_err), _lib.ptr(xprod_out),
+              _lib.ptr(xr), _lib.ptr(packed), _lib.ptr(q), _lib.ptr(x), _lib.ptr(err), _lib.ptr(rtn_err),
+              _lib.ptr(xprod_out),
               ctypes.byref(st), _lib.ptr(ws), int(ws.numel()), _stream(dev))
     stats = {name: getattr(st, name) for name, _ in st._fields_}
     return q, x, err, rtn_err, stats

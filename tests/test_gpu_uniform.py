@@ -123,14 +123,18 @@ def _setup_block(rows, cols, bits, gs, key, rotate=False):
     return W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq
 
 
+@pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("rotate,bits", [(False, 4), (True, 4), (True, 3)])
-def test_vamp_block_matches_oracle(gpu, rotate, bits):
+def test_vamp_block_matches_oracle(gpu, rotate, bits, packed):
+    """fp32 MFMA products, and (packed) the bf16-plane products on the packed rank-space operator."""
     W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq = _setup_block(128, 512, bits, 128, f"vb{bits}", rotate=rotate)
     cfg = dict(RECIPE, polish_sweeps=0)
     q_ref, x_ref, e_ref, rtn_ref, tr = ou.solve_uniform_rankspace_vamp(W, xr, sf, zf, maxq, V, V.T, S, Vs, cfg)
     vcfg = UniformVampConfig(**{k: v for k, v in RECIPE.items()})
+    pk = ops.rankspace_pack(V.to(gpu), Vs.to(gpu)) if packed else None
+    assert (pk is not None) == packed
     q, x, e, rtn, st = ops.uniform_vamp_solve(W.to(gpu), xr.to(gpu), sg.to(gpu), zg.to(gpu), 128, maxq, V.to(gpu),
-                                              S.to(gpu), Vs.to(gpu), vcfg, want_x=True)
+                                              S.to(gpu), Vs.to(gpu), vcfg, want_x=True, packed=pk)
     agree = float((q.cpu().long() == q_ref.long()).float().mean())
     print("vamp block agreement", agree, "best_iter", st["best_iter"], tr["best_iter"], "stop", st["stop_iter"],
           tr["stop_iter"], "obs", st["obs_precision_final"], tr["obs_final"])

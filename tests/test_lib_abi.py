@@ -44,3 +44,24 @@ def test_invalid_argument_reported_without_gpu():
     assert b"n must be" in lib.mpq_last_error()
     lib.mpq_clear_error()
     assert lib.mpq_last_error() == b""
+
+
+def test_pointer_arguments_stay_alive_until_the_call_returns():
+    """_lib.ptr(x.contiguous()) must not free the temporary before the library reads it: a later
+    argument's temporary could otherwise take the same block."""
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libmpq_amd.so not built")
+    import gc
+    import weakref
+
+    import torch
+
+    t = torch.empty(4)
+    ref = weakref.ref(t)
+    _lib.ptr(t)
+    del t
+    gc.collect()
+    assert ref() is not None
+    _lib.call("mpq_last_error_code")
+    gc.collect()
+    assert ref() is None
