@@ -133,6 +133,18 @@ int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, const float* 
                          mpq_stream_t stream);
 
 /*
+ * mpq_e8p12_vamp_solve with the packed rank-space operator of mpq_rankspace_pack (`packed`,
+ * nullable): the solver's products then run as x6 products on the bf16 matrix cores (fp32
+ * accuracy).  Same products as the reference's solver (mpq/solver.py:853-1138).
+ */
+int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr, const float* hat_init,
+                            const float* V, const float* S, const float* Vs, const float* prior_scale,
+                            const MpqE8P12VampConfig* cfg, double obs_init, const float* packed,
+                            int64_t* idx_out, float* hat_out, float* err_out, float* r1_out,
+                            float* gamma1_out, MpqE8P12VampStats* stats, void* workspace,
+                            int64_t workspace_bytes, mpq_stream_t stream);
+
+/*
  * Per-layer context of the E8P12 gram-metric polish: H = Vs Vs^T, per 8-column
  * block the gram G_j, its stabilized Cholesky factor L_j and (L_j L_j^T)^-1
  * (mpq/polish/block_cd.py:385-397, stabilize_cholesky mpq/linear.py:121-141),

@@ -36,6 +36,8 @@ SIGNATURES = {
     "mpq_e8p12_vamp_workspace_size": (c_i64, [c_i64, c_i64]),
     "mpq_e8p12_vamp_solve": (c_int, [c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_double,
                                      c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
+    "mpq_e8p12_vamp_solve_ex": (c_int, [c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_double,
+                                        c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
     "mpq_e8p12_cd_context_size": (c_i64, [c_i64]),
     "mpq_e8p12_cd_prepare": (c_int, [c_i64, c_ptr, c_ptr, c_i64, c_ptr]),
     "mpq_e8p12_cd_workspace_size": (c_i64, [c_i64, c_i64, c_i64]),

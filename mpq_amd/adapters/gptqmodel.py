@@ -51,7 +51,7 @@ class GPTQAdapterConfig:
     auto_block_rows: bool = False
     eigen_cache: bool = True  # reuse the decomposition of an identical Hessian (q/k/v, gate/up)
     # rank-space products as fp32-accurate bf16-plane products on the matrix cores (ops.gemm_x6)
-    # when cols % 128 == 0; False keeps every product on the fp32 MFMA kernel
+    # when cols % 128 == 0 and cols >= ops.X6_MIN_N; False keeps every product on the fp32 MFMA kernel
     x6_products: bool = True
 
 
@@ -239,7 +239,7 @@ def run_mpq_quantization(
     # reference forms them per row block inside the solver, mpq/solver.py:467-480); the row blocks
     # and the polish take slices, and each block returns its best decision's x Vs for the polish.
     # The rank-space operator packed once per linear for the bf16-plane products (None: fp32 path).
-    packed = ops.rankspace_pack(V, Vs) if bool(adapter_cfg.x6_products) else None
+    packed = ops.rankspace_pack(V, Vs) if bool(adapter_cfg.x6_products) and cols >= ops.X6_MIN_N else None
     if packed is not None:
         Vs_packed = packed[2 * cols * cols:]
         Yu_all = ops.gemm_x6(W_work, Vs_packed, cols)

@@ -40,6 +40,9 @@ class QuipAdapterConfig:
     block_rows: int = 128
     jitter_base: float = 1e-6
     eigen_floor_scale: float = 1e-6
+    # rank-space products as fp32-accurate bf16-plane products on the matrix cores (ops.gemm_x6)
+    # when n % 128 == 0 and n >= ops.X6_MIN_N; False keeps every product on the fp32 MFMA kernel
+    x6_products: bool = True
 
 
 def _resolve_block_rows(rows: int, requested: int) -> int:
@@ -228,9 +231,17 @@ def mpq_refine_codebook(
 
     block_rows = _resolve_block_rows(m, int(getattr(args, "mpq_block_rows", adapter_cfg.block_rows)
                                             or adapter_cfg.block_rows))
+    # the rank-space operator packed once for the bf16-plane products (None: fp32 path)
+    packed = (ops.rankspace_pack(V, Vs) if bool(getattr(adapter_cfg, "x6_products", True)) and n >= ops.X6_MIN_N
+              else None)
     requested_obs = float(getattr(args, "mpq_obs_precision", 0.0) or 0.0)
     if requested_obs > 0.0:
         obs_precision = requested_obs
+    elif packed is not None:
+        du = ops.gemm_x6((Wr - hat_init).contiguous(), packed[2 * n * n:], n)
+        sq = du.square().sum(dim=1).double()
+        mse = max(float(sq.sum().item()) / max(m * n, 1), 1e-12)
+        obs_precision = 1.0 / mse
     else:
         du = ops.gemm((Wr - hat_init).contiguous(), Vs)
         sq = du.square().sum(dim=1).double()
@@ -264,7 +275,7 @@ def mpq_refine_codebook(
                 pscale = prior_scale_from_center(Wr[r0:r1].reshape(r1 - r0, nblocks, 8), mode).reshape(-1)
             idx_b, hat_b, _, _, g1_b, st = ops.e8p12_vamp_solve(Wr[r0:r1], final_hat[r0:r1], V, S, Vs, vamp_cfg,
                                                                 prior_scale=pscale, obs_init=obs_block,
-                                                                want_state=True, ws=ws)
+                                                                want_state=True, ws=ws, packed=packed)
             final_hat[r0:r1] = hat_b
             final_idx[r0:r1] = idx_b
             if bool(vamp_cfg.em_obs_precision) and float(vamp_cfg.obs_precision) <= 0.0:
@@ -276,6 +287,7 @@ def mpq_refine_codebook(
             gamma_max = max(gamma_max, float(g64.max().item()))
             block_stats.append(st)
         del ws
+    del packed
     torch.cuda.synchronize(device)
     timings["vamp_s"] = time.time() - t0
 

@@ -6,6 +6,7 @@
 // (vamp_common.h), the final decision is the factorized MAP of (r1, gamma1)
 // (mpq/solver.py:1124-1138).  best_iterate (off in the recipe) is supported.
 // Host control flow with two small status reads per iteration.
+#include <algorithm>
 #include <cmath>
 
 #include "gemm.h"
@@ -37,6 +38,8 @@ __global__ __launch_bounds__(kEW) void row_sum_kernel(int64_t nb, const float* _
 struct E8Plan {
   int64_t rows, n, nb, nchunks;
   int splits, bn;
+  int splits_x6;     // 0 if the shape has no x6 path
+  int64_t ap_bytes;  // packed bf16 planes of a product's left operand (x6 path)
   int64_t bytes;
 };
 
@@ -49,9 +52,12 @@ E8Plan e8_plan(int64_t rows, int64_t n) {
   int bn = 128;
   p.splits = choose_splits(rows, n, n, (int64_t)1 << 62, &bn);
   p.bn = bn;
+  p.splits_x6 = x6_shape_ok(n, n) ? x6_choose_splits(rows, n, n) : 0;
+  p.ap_bytes = p.splits_x6 ? (x6_packed_a_bytes(rows, n) + 255) / 256 * 256 : 0;
   const int64_t mat = a64(rows * n) * 4;
   int64_t b = 7 * mat;                          // Yu r1 r2 r2prev x1 map_vals r1_best
-  b += (int64_t)p.splits * mat;                 // partials
+  b += (int64_t)std::max(p.splits, p.splits_x6) * mat;  // partials
+  b += p.ap_bytes;                              // packed left operand (x6 path)
   b += a64(rows * p.nb) * 4;                    // var1
   b += a64(rows * p.nb) * 8;                    // map idx
   b += a64(16 * rows) * 4;                      // row arrays
@@ -95,6 +101,16 @@ extern "C" int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, co
                                     float* hat_out, float* err_out, float* r1_out, float* gamma1_out,
                                     MpqE8P12VampStats* stats, void* workspace, int64_t workspace_bytes,
                                     hipStream_t stream) {
+  return mpq_e8p12_vamp_solve_ex(rows, n, Wr, hat_init, V, S, Vs, prior_scale, cfg, obs_init, nullptr, idx_out,
+                                 hat_out, err_out, r1_out, gamma1_out, stats, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr, const float* hat_init,
+                                       const float* V, const float* S, const float* Vs, const float* prior_scale,
+                                       const MpqE8P12VampConfig* cfg, double obs_init, const float* packed,
+                                       int64_t* idx_out, float* hat_out, float* err_out, float* r1_out,
+                                       float* gamma1_out, MpqE8P12VampStats* stats, void* workspace,
+                                       int64_t workspace_bytes, hipStream_t stream) {
   using namespace mpq;
   MPQ_CHECK_ARG(rows > 0 && n > 0 && n % 8 == 0, "E8P12 solver expects n divisible by 8; got n=%lld",
                 (long long)n);
@@ -118,7 +134,8 @@ extern "C" int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, co
   float* x1 = (float*)p; p += mat;
   float* mvals = (float*)p; p += mat;
   float* r1_best = (float*)p; p += mat;
-  float* P = (float*)p; p += (int64_t)pl.splits * mat;
+  float* P = (float*)p; p += (int64_t)std::max(pl.splits, pl.splits_x6) * mat;
+  void* Ap = p; p += pl.ap_bytes;
   float* var1 = (float*)p; p += a64(rows * nb) * 4;
   int64_t* midx = (int64_t*)p; p += a64(rows * nb) * 8;
   float* rowbuf = (float*)p; p += a64(16 * rows) * 4;
@@ -143,24 +160,36 @@ extern "C" int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, co
   HostMailbox* mb = host_mailbox();
   MPQ_CHECK_ARG(mb != nullptr, "E8P12 VAMP: mapped status mailbox unavailable");
   auto sync_status = [&]() -> int { return read_status(mb, status, hs, stream); };
+  // rank-space products: on the packed operator (x6, bf16 matrix cores) when given, else fp32 MFMA;
+  // `op` indexes the packed operator (0: V for r V, 1: V for x V^T, 2: Vs for x Vs)
+  const bool x6 = packed != nullptr && pl.splits_x6 > 0;
+  const int nsplit = x6 ? pl.splits_x6 : pl.splits;
+  auto prod = [&](const float* A, const float* B, bool trans_b, int op) -> hipError_t {
+    if (x6) {
+      hipError_t e = x6_pack_a(A, n, rows, n, Ap, stream);
+      if (e != hipSuccess) return e;
+      return x6_gemm_partials(Ap, packed + (int64_t)op * n * n, rows, n, n, P, n, sstride, nsplit, stream);
+    }
+    return product(A, B, trans_b, rows, n, P, pl.splits, pl.bn, stream);
+  };
   int rc;
   // MAP decision of (r, g) into midx / mvals and its rank-space error into errrow / status.err_mean
   auto map_state = [&](const float* r, const float* g) -> int {
     int e = mpq_e8p12_map(r, rows * nb, g, nb, center, prior_scale, tau, midx, nullptr, mvals, nullptr, nullptr,
                           stream);
     if (e != kOk) return e;
-    MPQ_HIP_TRY(product(mvals, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
-    hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, pl.splits, sstride, Yu, part, nullptr);
+    MPQ_HIP_TRY(prod(mvals, Vs, false, 2));
+    hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, Yu, part, nullptr);
     hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, part, errrow, status);
     MPQ_LAUNCH_CHECK();
     return kOk;
   };
 
   // ---- setup: Yu, gamma1, obs warm start
-  MPQ_HIP_TRY(product(Wr, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
-  MPQ_HIP_TRY(splitk_reduce(P, pl.splits, rows, n, Yu, n, 1.f, 0.f, stream));
-  MPQ_HIP_TRY(product(hat_init, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
-  hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, pl.splits, sstride, Yu, part, nullptr);
+  MPQ_HIP_TRY(prod(Wr, Vs, false, 2));
+  MPQ_HIP_TRY(splitk_reduce(P, nsplit, rows, n, Yu, n, 1.f, 0.f, stream));
+  MPQ_HIP_TRY(prod(hat_init, Vs, false, 2));
+  hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, Yu, part, nullptr);
   hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, part, errrow, status);
   hipLaunchKernelGGL(sqdiff_part_kernel, eg, eb, 0, stream, n, Wr, n, hat_init, n, part);
   hipLaunchKernelGGL(rows_gamma_init_kernel, dim3(1), eb, 0, stream, rows, n, nchunks, part, cfg->gamma_start, g1,
@@ -240,13 +269,13 @@ extern "C" int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, co
     hipLaunchKernelGGL(msg_r2_kernel, eg, eb, 0, stream, n, x1, r1, eta1, g1w, g2new, has_prev ? 1 : 0, damping,
                        r2prev, r2);
     MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(product(r2, V, false, rows, n, P, pl.splits, pl.bn, stream));
-    hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, P, pl.splits, sstride, Yu, S, g2, obs_f, x1, part);
+    MPQ_HIP_TRY(prod(r2, V, false, 0));
+    hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, Yu, S, g2, obs_f, x1, part);
     hipLaunchKernelGGL(rows_lmmse_kernel, dim3(1), eb, 0, stream, rows, n, n, nchunks, part, g2, damping, eta2,
                        g1new, g1, status);
     MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(product(x1, V, true, rows, n, P, pl.splits, pl.bn, stream));
-    hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, P, pl.splits, sstride, r2, eta2, g2, g1new, damping,
+    MPQ_HIP_TRY(prod(x1, V, true, 1));
+    hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, r2, eta2, g2, g1new, damping,
                        r1);
     MPQ_LAUNCH_CHECK();
     if (best_iterate) {

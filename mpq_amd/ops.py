@@ -136,6 +136,13 @@ def gemm_x6_splitk(A_packed: torch.Tensor, B_packed: torch.Tensor, M: int, N: in
     return out, s
 
 
+# Smallest n for which the adapters run the rank-space products as x6 products: a 128 x n x n
+# product at n = 2048 is launch-latency bound, and the extra pack of A made the E8P12 solver slower
+# there (up/gate VAMP 428 -> 451 ms on a Llama-3.2-1B layer), while n = 4096 (Llama-3-8B q/k/v/o,
+# gate/up: 405 -> 380 ms) and larger gain.
+X6_MIN_N = 4096
+
+
 def rankspace_pack(V: torch.Tensor, Vs: torch.Tensor) -> Optional[torch.Tensor]:
     """The packed rank-space operator (V for r V, V for x V^T, Vs for x Vs) of the VAMP solvers' x6
     products, or None when n has no x6 path (n % 128 != 0)."""
@@ -397,11 +404,13 @@ def e8p12_vamp_config_c(cfg) -> "_lib.E8P12VampConfigC":
 
 
 def e8p12_vamp_solve(Wr, hat_init, V, S, Vs, cfg, *, prior_scale: Optional[torch.Tensor] = None,
-                     obs_init: float = 0.0, want_state: bool = False, ws: Optional[torch.Tensor] = None):
-    """One row block of the E8P12 VAMP loop (no polish).
+                     obs_init: float = 0.0, want_state: bool = False, ws: Optional[torch.Tensor] = None,
+                     packed: Optional[torch.Tensor] = None):
+    """One row block of the E8P12 VAMP loop (no polish).  ``packed`` (from :func:`rankspace_pack`)
+    runs the solver's products on the bf16 matrix cores.
 
     Returns (idx int64 (rows, n/8), hat (rows, n), err (rows), r1|None, gamma1|None, stats dict)."""
-    dev = _dev(Wr, hat_init, V, S, Vs, prior_scale)
+    dev = _dev(Wr, hat_init, V, S, Vs, prior_scale, packed)
     Wr = _f32c(Wr)
     hat_init = _f32c(hat_init)
     rows, n = Wr.shape
@@ -414,6 +423,9 @@ def e8p12_vamp_solve(Wr, hat_init, V, S, Vs, cfg, *, prior_scale: Optional[torch
         if int(prior_scale.numel()) != rows * (n // 8):
             raise ValueError("prior_scale must hold one entry per 8-block")
     lib = _lib.load()
+    if packed is not None and (packed.dtype != F32 or not packed.is_contiguous()
+                               or int(packed.numel()) != int(lib.mpq_rankspace_pack_floats(n)) or n % 128):
+        raise ValueError("packed must be the float32 rank-space operator from rankspace_pack for this n")
     need = int(lib.mpq_e8p12_vamp_workspace_size(rows, n))
     if ws is None or ws.numel() < need:
         ws = workspace(need, dev)
@@ -424,9 +436,10 @@ def e8p12_vamp_solve(Wr, hat_init, V, S, Vs, cfg, *, prior_scale: Optional[torch
     g1 = torch.empty(rows, 1, dtype=F32, device=dev) if want_state else None
     st = _lib.E8P12VampStatsC()
     c = e8p12_vamp_config_c(cfg)
-    _lib.call("mpq_e8p12_vamp_solve", rows, n, _lib.ptr(Wr), _lib.ptr(hat_init), _lib.ptr(_f32c(V)),
+    _lib.call("mpq_e8p12_vamp_solve_ex", rows, n, _lib.ptr(Wr), _lib.ptr(hat_init), _lib.ptr(_f32c(V)),
               _lib.ptr(_f32c(S)), _lib.ptr(_f32c(Vs)), _lib.ptr(prior_scale), ctypes.byref(c),
-              float(obs_init or 0.0), _lib.ptr(idx), _lib.ptr(hat), _lib.ptr(err), _lib.ptr(r1), _lib.ptr(g1),
+              float(obs_init or 0.0), _lib.ptr(packed), _lib.ptr(idx), _lib.ptr(hat), _lib.ptr(err), _lib.ptr(r1),
+              _lib.ptr(g1),
               ctypes.byref(st), _lib.ptr(ws), int(ws.numel()), _stream(dev))
     stats = {name: getattr(st, name) for name, _ in st._fields_}
     return idx, hat, err, r1, g1, stats

@@ -98,9 +98,12 @@ def _e8_case(rows, n, seed_key):
     return Wr, V, S, hat0
 
 
-def _gpu_vamp(Wr, hat0, V, S, cfg, dev):
+def _gpu_vamp(Wr, hat0, V, S, cfg, dev, packed=False):
     Vs = V * S.unsqueeze(0)
-    return ops.e8p12_vamp_solve(Wr.to(dev), hat0.to(dev), V.to(dev), S.to(dev), Vs.to(dev), cfg, want_state=True)
+    pk = ops.rankspace_pack(V.to(dev), Vs.to(dev)) if packed else None
+    assert (pk is not None) == packed
+    return ops.e8p12_vamp_solve(Wr.to(dev), hat0.to(dev), V.to(dev), S.to(dev), Vs.to(dev), cfg, want_state=True,
+                                packed=pk)
 
 
 def test_vamp_matches_reference_golden(gpu):
@@ -116,12 +119,14 @@ def test_vamp_matches_reference_golden(gpu):
     assert torch.equal(hat.cpu(), grid[idx.cpu().reshape(-1)].view_as(hat.cpu()))
 
 
-def test_vamp_matches_oracle(gpu):
+@pytest.mark.parametrize("packed", [False, True])
+def test_vamp_matches_oracle(gpu, packed):
+    """fp32 MFMA products, and (packed) the bf16-plane products on the packed rank-space operator."""
     Wr, V, S, hat0 = _e8_case(64, 512, "e8vamp:gpu")
     grid, cache = _grid_cache()
     cfg = dict(iters=16, damping=0.5, prior_tau=0.25, polish_sweeps=0)
     ref_hat, ref_idx, ref_err, ref_st = oe8.solve_e8p12_rankspace_vamp(Wr, hat0, V, S, grid, cache, cfg)
-    idx, hat, err, r1, g1, st = _gpu_vamp(Wr, hat0, V, S, _Cfg, gpu)
+    idx, hat, err, r1, g1, st = _gpu_vamp(Wr, hat0, V, S, _Cfg, gpu, packed=packed)
     agree = float((idx.cpu() == ref_idx).float().mean())
     assert agree >= 0.999, agree
     assert abs(st["obs_precision_final"] - ref_st["obs_final"]) <= 2e-3 * ref_st["obs_final"]

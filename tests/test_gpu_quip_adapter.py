@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from mpq_amd import codebook
+from mpq_amd import codebook, ops
 from mpq_amd.adapters.quip_sharp import QuipAdapterConfig, mpq_refine_codebook
 from mpq_amd.solver import E8P12VampConfig, polish_e8p12_rankspace, solve_e8p12_rankspace_vamp
 from oracle import e8p12 as oe8
@@ -42,8 +42,13 @@ def _surrogate(Wr, hat, H):
 # end-to-end codes are not compared directly: the greedy order of a row block is shared by all
 # its rows, so one differing VAMP code (a near-tie) can reorder the block's CD and move a large
 # fraction of its codes to an equally good local optimum; the surrogate loss is compared instead.
-@pytest.mark.parametrize("m,n,key,heavy", [(128, 256, "quip:128:256", True), (192, 256, "quip:192:256d", False)])
-def test_refine_codebook_matches_oracle(gpu, m, n, key, heavy):
+@pytest.mark.parametrize("m,n,key,heavy,x6", [(128, 256, "quip:128:256", True, False),
+                                              (192, 256, "quip:192:256d", False, False),
+                                              (192, 256, "quip:192:256d", False, True)])
+def test_refine_codebook_matches_oracle(gpu, m, n, key, heavy, x6, monkeypatch):
+    """x6: the VAMP products on the packed rank-space operator (the adapter uses them from
+    ops.X6_MIN_N columns; lowered here so the 256-column case takes that path)."""
+    monkeypatch.setattr(ops, "X6_MIN_N", 128 if x6 else 1 << 30)
     Wr, H = _layer(m, n, key, heavy)
     grid = torch.from_numpy(codebook.grid_numpy())
     cache = oe8.factor_cache(grid)

@@ -194,10 +194,13 @@ def test_cd_polish_matches_oracle(gpu):
     assert float((q2.cpu() == q[128:].cpu()).float().mean()) >= 0.999
 
 
-@pytest.mark.parametrize("rotation", ["none", "internal_hadamard"])
-@pytest.mark.parametrize("bits", [4, 3])
-def test_adapter_end_to_end_matches_oracle(gpu, rotation, bits):
-    """Same eigendecomposition on both sides: proxy loss within 0.5%, codes >= 99% equal.
+@pytest.mark.parametrize("rotation,bits,x6", [("none", 4, False), ("internal_hadamard", 4, False), ("none", 3, False),
+                                              ("internal_hadamard", 3, False), ("internal_hadamard", 4, True),
+                                              ("none", 3, True)])
+def test_adapter_end_to_end_matches_oracle(gpu, rotation, bits, x6, monkeypatch):
+    """Same eigendecomposition on both sides: proxy loss within 0.5%, codes >= 99% equal; x6: the
+    rank-space products on the packed operator (the adapters use them from ops.X6_MIN_N columns;
+    lowered here so the 512-column case takes that path).
 
     VAMP alone is code-identical (test_vamp_block_matches_oracle); the greedy CD amplifies
     rounding-order differences through near-tie accept decisions and the shared greedy order, so
@@ -205,6 +208,7 @@ def test_adapter_end_to_end_matches_oracle(gpu, rotation, bits):
     disagree with each other (tests/test_oracle_uniform.py::test_reference_cd_dispatches_disagree).
     """
     rows, cols, gs = 256, 512, 128
+    monkeypatch.setattr(ops, "X6_MIN_N", 128 if x6 else 1 << 30)
     W, H = make_layer(rows, cols, tokens=2048, seed_key=f"e2e:{rotation}:{bits}")
     Hg = 2.0 * H
     ref = ou.run_mpq_quantization(W, Hg, bits, gs, "model.layers.0.mlp.up_proj", RECIPE, rotation=rotation)
