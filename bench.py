@@ -173,7 +173,7 @@ def set_pass(specs, weights, device, warmup):
 
 def gemm_roofline(n, device, reps=20, warmup=100):
     """Live HIP-event timing of the dominant VAMP kernel: the split-K rank-space product
-    (128 x n) @ (n x n) as the VAMP drivers launch it (gemm_x6_kernel on the packed rank-space
+    (128 x n) @ (n x n) as the VAMP drivers launch it (gemm_x6_ring_kernel on the packed rank-space
     operator and the bf16 planes of A, partials only; the drivers' epilogues sum the partials).
     Each fp32 multiply-add is six bf16 MFMA products, so the kernel executes 12 * 128 * n^2 bf16
     flops per launch (2 * 128 * n^2 fp32-equivalent).  Events are recorded on the stream the kernel
@@ -559,7 +559,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": f"gemm_x6_kernel (rank-space product 128x14336 @ 14336x14336 as six bf16-plane MFMA "
+            "kernel": f"gemm_x6_ring_kernel (rank-space product 128x14336 @ 14336x14336 as six bf16-plane MFMA "
                       f"products per fp32 multiply-add, split-K {rf['splits']}, partials only, as the VAMP "
                       "drivers launch it)",
             "achieved": round(rf["bf16_tflops"], 2),

@@ -469,12 +469,16 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_full_kernel(GemmParams p) {
 //
 // Operands are packed into 128-row x 16-k tiles in MFMA fragment order: chunk c = (blk*2 + h)*32 + r
 // of a tile holds row blk*32 + r at k = 16 ks + 8 h + (0..7).  B (the large, reused operand) is
-// packed once as fp32 [N/128][K/16][256 chunks][8]; A (small, re-formed per product) is split and
-// packed as bf16 planes [ceil(M/128)][K/16][3][256][8].  A work-group (128 x 128 tile, one K slice)
-// then reads each K slab as contiguous 12 KB (A, L2-resident) + 8 KB (B), splits B into planes on
-// its way to LDS, and runs 24 MFMAs per wave per slab.  Split s of tile t is block t * splits + s,
-// so with 8 or 16 splits every XCD (blocks are dispatched round-robin over 8) works on one or two
-// K slices and its L2 holds those slices of A.
+// packed once as fp32 [N/128][K/16][2][256 chunks][4] (first and second four k of every chunk in two
+// 4 KB halves, so a fragment is two conflict-free 16-byte LDS reads); A (small, re-formed per
+// product) is split and packed as bf16 planes [ceil(M/128)][K/16][3][256][8].  A work-group
+// (128 x 128 tile, one K slice, 2 x 2 waves of 64 x 64) reads each K slab as contiguous 12 KB (A,
+// L2-resident) + 8 KB (B) and runs 24 MFMAs per wave per slab.  gemm_x6_ring_kernel moves the slabs
+// with global_load_lds into a 4-stage LDS ring (three slabs in flight, no register staging) and each
+// wave splits its own B fragments; gemm_x6_kernel (K slices of an even slab count) stages through
+// registers and splits B once on its way to LDS.  Split s of tile t is block t * splits + s, so with
+// 8 or 16 splits every XCD (blocks are dispatched round-robin over 8) works on one or two K slices
+// and its L2 holds those slices of A.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -511,9 +515,9 @@ __global__ void x6_pack_b_kernel(const float* __restrict__ B, int64_t ldb, int64
     float v[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = TRANS_B ? B[n * ldb + k0 + e] : B[(k0 + e) * ldb + n];
-    float4* d = reinterpret_cast<float4*>(Bt + q * 8);
+    float4* d = reinterpret_cast<float4*>(Bt) + tk * 512 + c;
     d[0] = make_float4(v[0], v[1], v[2], v[3]);
-    d[1] = make_float4(v[4], v[5], v[6], v[7]);
+    d[256] = make_float4(v[4], v[5], v[6], v[7]);
   }
 }
 
@@ -565,11 +569,10 @@ __global__ __launch_bounds__(kThreads) void gemm_x6_kernel(int64_t M, int64_t N,
   const int64_t KS = K / 16;
   const int nslab = (int)(k_per_split / 16);
   const int64_t ks0 = (int64_t)split * nslab;
-  // A slab: 768 chunks (3 planes), thread -> chunks tid + 256 j; B slab: 512 float4, thread -> float4
-  // tid + 256 j = half tid%2 of chunk 128 j + tid/2
+  // A slab: 768 chunks (3 planes), thread -> chunks tid + 256 j; B slab: 2 x 256 float4, thread ->
+  // both halves of chunk tid
   const u32x4v* asrc = reinterpret_cast<const u32x4v*>(At) + (mt * KS + ks0) * 768 + tid;
   const f32x4v* bsrc = reinterpret_cast<const f32x4v*>(Bt) + (nt * KS + ks0) * 512 + tid;
-  const int bc = tid >> 1, bh = tid & 1;
 
   u32x4v qa0[3], qa1[3];
   f32x4v qb0[2], qb1[2];
@@ -582,16 +585,14 @@ __global__ __launch_bounds__(kThreads) void gemm_x6_kernel(int64_t M, int64_t N,
   auto lstore = [&](const u32x4v (&qa)[3], const f32x4v (&qb)[2], int buf) {
 #pragma unroll
     for (int j = 0; j < 3; ++j) As[buf][j][tid] = __builtin_bit_cast(uint4, qa[j]);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      uint2 h, m, l;
-      split3(qb[j].x, qb[j].y, h.x, m.x, l.x);
-      split3(qb[j].z, qb[j].w, h.y, m.y, l.y);
-      const int c = j * 128 + bc;
-      reinterpret_cast<uint2*>(&Bs[buf][0][c])[bh] = h;
-      reinterpret_cast<uint2*>(&Bs[buf][1][c])[bh] = m;
-      reinterpret_cast<uint2*>(&Bs[buf][2][c])[bh] = l;
-    }
+    uint4 h, m, l;
+    split3(qb[0].x, qb[0].y, h.x, m.x, l.x);
+    split3(qb[0].z, qb[0].w, h.y, m.y, l.y);
+    split3(qb[1].x, qb[1].y, h.z, m.z, l.z);
+    split3(qb[1].z, qb[1].w, h.w, m.w, l.w);
+    Bs[buf][0][tid] = h;
+    Bs[buf][1][tid] = m;
+    Bs[buf][2][tid] = l;
   };
 
   floatx16 acc[2][2];
@@ -640,6 +641,138 @@ __global__ __launch_bounds__(kThreads) void gemm_x6_kernel(int64_t M, int64_t N,
   }
 
   // lane l, accumulator v -> row 8*(v/4) + 4*(l/32) + v%4, column l%32 of the 32 x 32 block
+  const int col = lane & 31, rbase = (lane >> 5) * 4;
+  float* Cs = C + (int64_t)split * split_stride;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t gn = nt * 128 + (wnb + j) * 32 + col;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t gm = mt * 128 + (wmb + i) * 32 + (v >> 2) * 8 + rbase + (v & 3);
+        if (gm < M) Cs[gm * ldc + gn] = acc[i][j][v];
+      }
+    }
+}
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt bits 3:0 and 15:14).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Same product as gemm_x6_kernel with the slabs moved by global_load_lds into a ring of four LDS
+// stages (three slabs in flight, no register staging).  Each stage is its own __shared__ array and
+// the loops are unrolled by four, so every stage index is a constant: the compiler then tells the
+// stages apart and waits only where this code waits (s_waitcnt vmcnt(n) before each barrier: all
+// but the n most recent loads of this wave done, i.e. the slab about to be read).  The barrier is
+// s_barrier without a fence (the fence of __syncthreads would wait for every load in flight).
+// Every K slice is a positive multiple of four slabs.
+__global__ __launch_bounds__(kThreads) void gemm_x6_ring_kernel(int64_t M, int64_t N, int64_t K,
+                                                                const uint4* __restrict__ At,
+                                                                const float* __restrict__ Bt, float* __restrict__ C,
+                                                                int64_t ldc, int64_t split_stride,
+                                                                int64_t k_per_split, int splits) {
+  constexpr int S = 4;
+  constexpr int STAGE = 768 + 512;  // 16-byte slots: A planes, then the two halves of B
+  constexpr int LOADS = 5;          // global_load_lds per wave per slab: 3 (A) + 2 (B)
+  __shared__ uint4 st0[STAGE];
+  __shared__ uint4 st1[STAGE];
+  __shared__ uint4 st2[STAGE];
+  __shared__ uint4 st3[STAGE];
+  auto stage = [&](int slot) -> uint4* { return slot == 0 ? st0 : slot == 1 ? st1 : slot == 2 ? st2 : st3; };
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wmb = (wave >> 1) * 2, wnb = (wave & 1) * 2;
+  const int64_t bid = blockIdx.x;
+  const int split = (int)(bid % splits);
+  const int64_t tile = bid / splits;
+  const int64_t ntn = N / 128;
+  const int64_t mt = tile / ntn, nt = tile - mt * ntn;
+  const int64_t KS = K / 16;
+  const int nslab = (int)(k_per_split / 16);
+  const int64_t ks0 = (int64_t)split * nslab;
+  // wave w moves A slots w*192 + 64 q (q < 3) and B slots w*128 + 64 q (q < 2); lane l adds 16 l bytes
+  const uint4* asrc = At + (mt * KS + ks0) * 768 + wave * 192 + lane;
+  const uint4* bsrc = reinterpret_cast<const uint4*>(Bt) + (nt * KS + ks0) * 512 + wave * 128 + lane;
+  auto issue = [&](int s, int slot) {
+    uint4* d = stage(slot);
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+      __builtin_amdgcn_global_load_lds(asrc + (int64_t)s * 768 + q * 64, d + wave * 192 + q * 64, 16, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      __builtin_amdgcn_global_load_lds(bsrc + (int64_t)s * 512 + q * 64, d + 768 + wave * 128 + q * 64, 16, 0, 0);
+  };
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+  auto compute = [&](int slot) {
+    const uint4* d = stage(slot);
+    bf16x8 a[3][2], b[3][2];
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[pl][i] = __builtin_bit_cast(bf16x8, d[pl * 256 + (wmb + i) * 64 + lane]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float4 x = __builtin_bit_cast(float4, d[768 + (wnb + j) * 64 + lane]);
+      const float4 y = __builtin_bit_cast(float4, d[768 + 256 + (wnb + j) * 64 + lane]);
+      uint4 h, m, l;
+      split3(x.x, x.y, h.x, m.x, l.x);
+      split3(x.z, x.w, h.y, m.y, l.y);
+      split3(y.x, y.y, h.z, m.z, l.z);
+      split3(y.z, y.w, h.w, m.w, l.w);
+      b[0][j] = __builtin_bit_cast(bf16x8, h);
+      b[1][j] = __builtin_bit_cast(bf16x8, m);
+      b[2][j] = __builtin_bit_cast(bf16x8, l);
+    }
+    constexpr int pa[6] = {2, 1, 0, 1, 0, 0};
+    constexpr int pb[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+    for (int t = 0; t < 6; ++t)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[pa[t]][i], b[pb[t]][j], acc[i][j], 0, 0, 0);
+  };
+  auto sync = [&]() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // Slab t lives in stage t % 4.  Step t: wait for slab t (loads of slabs t+1, t+2 may stay in
+  // flight), barrier (slab t visible; every wave is done with stage (t-1) % 4), issue slab t+3 into
+  // that stage, compute slab t.
+#pragma unroll
+  for (int t = 0; t < S - 1; ++t) issue(t, t);
+  int t0 = 0;
+  for (; t0 < nslab - S; t0 += S) {
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(LOADS * (S - 2)));
+      sync();
+      issue(t0 + u + S - 1, (u + S - 1) % S);
+      compute(u);
+    }
+  }
+  // last four slabs: slab nslab - 1 is issued in the first step, then the ring drains
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(LOADS * 2));
+  sync();
+  issue(t0 + S - 1, S - 1);
+  compute(0);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(LOADS * 2));
+  sync();
+  compute(1);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(LOADS * 1));
+  sync();
+  compute(2);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  sync();
+  compute(3);
+
   const int col = lane & 31, rbase = (lane >> 5) * 4;
   float* Cs = C + (int64_t)split * split_stride;
 #pragma unroll
@@ -764,8 +897,12 @@ hipError_t x6_gemm_partials(const void* At, const float* Bt, int64_t M, int64_t 
   if (!x6_shape_ok(N, K) || splits < 1 || K % splits != 0 || kps % 32 != 0) return hipErrorInvalidValue;
   const int64_t blocks = ((M + 127) / 128) * (N / 128) * splits;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gemm_x6_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, M, N, K,
-                     static_cast<const uint4*>(At), Bt, C, ldc, split_stride, kps, splits);
+  if ((kps / 16) % 4 == 0)
+    hipLaunchKernelGGL(gemm_x6_ring_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, M, N, K,
+                       static_cast<const uint4*>(At), Bt, C, ldc, split_stride, kps, splits);
+  else
+    hipLaunchKernelGGL(gemm_x6_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, M, N, K,
+                       static_cast<const uint4*>(At), Bt, C, ldc, split_stride, kps, splits);
   return hipGetLastError();
 }
 

@@ -35,10 +35,12 @@ def test_gemm_x6_known_answer_pins_the_plane_products(gpu):
 
 
 @pytest.mark.parametrize("M,N,K,trans", [(128, 512, 512, False), (128, 512, 512, True), (100, 256, 1024, False),
-                                         (384, 1024, 2048, True), (1, 128, 32, False), (257, 384, 4096, False)])
+                                         (384, 1024, 2048, True), (1, 128, 32, False), (257, 384, 4096, False),
+                                         (130, 256, 96, True)])
 def test_gemm_x6_matches_fp64(gpu, M, N, K, trans):
     """Entry-wise error relative to sum_k |a_k b_k| against fp64: within twice the fp32 MFMA kernel's
-    on the same operands, and below 2e-6 (a dropped 2^-16-order plane product shows at K = 32 as
+    on the same operands, and below 2e-6.  K slices of a multiple of four 16-k slabs run the LDS-ring
+    kernel, the others (K = 32, 96 here) the register-staged one (a dropped 2^-16-order plane product shows at K = 32 as
     ~3e-6 and above; the known-answer test pins the plane set exactly)."""
     g = torch.Generator().manual_seed(M * 13 + N + K)
     # columns of A and rows of op(B) with a spread of magnitudes (1e-3 .. 1e3)
