@@ -105,19 +105,21 @@ __global__ __launch_bounds__(256) void transpose_t_kernel(const T* __restrict__ 
 }
 
 // Operands of the rank-2 kPB panel update from the panel's reflectors V (kPB x m, rows of A) and
-// W (kPB x m): X = [V^T W^T] and Yb = [W^T V^T] (m x 2 kPB each), so A -= X Yb^T.  One launch
-// per panel, 32 source columns per work-group.
+// W (kPB x m): X = [V^T W^T] and Yb = [W^T V^T] (m x 2 kPB each), so A -= X Yb^T.  Rows below
+// `zrows` are zero (the update then starts below the panel at an aligned row and leaves the rows
+// in between unchanged).  One launch per panel, 32 source columns per work-group.
 template <typename T>
 __global__ __launch_bounds__(256) void panel_operands_kernel(const T* __restrict__ Vp, const T* __restrict__ Wp,
-                                                             int64_t m, int64_t ld, T* __restrict__ X,
+                                                             int64_t m, int64_t zrows, int64_t ld, T* __restrict__ X,
                                                              T* __restrict__ Yb) {
   __shared__ T tv[kPB][33], tw[kPB][33];
   const int64_t c0 = (int64_t)blockIdx.x * 32;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
   for (int k = ty; k < kPB; k += 8) {
     const int64_t c = c0 + tx;
-    tv[k][tx] = c < m ? Vp[k * ld + c] : T(0);
-    tw[k][tx] = c < m ? Wp[k * ld + c] : T(0);
+    const bool in = c >= zrows && c < m;
+    tv[k][tx] = in ? Vp[k * ld + c] : T(0);
+    tw[k][tx] = in ? Wp[k * ld + c] : T(0);
   }
   __syncthreads();
   for (int e = threadIdx.x; e < 32 * kPB; e += 256) {
@@ -766,14 +768,18 @@ int sytrd(int64_t n, const SyevdLayout& L, T* base, rocblas_handle h, hipStream_
     }
     const int64_t s0 = i0 + nbl;
     if (s0 < n - 1) {
-      // trailing update A[s0:, s0:] -= V W^T + W V^T = [V W] [W V]^T (nbl == kPB here)
-      const int64_t m = n - s0;
-      const T* Vp = A + i0 * lda + s0;
-      const T* Wp = Wb + s0;
+      // trailing update A[s0:, s0:] -= V W^T + W V^T = [V W] [W V]^T (nbl == kPB here).  fp32 with
+      // n % 128 == 0: the update starts at the 128-aligned row sa <= s0 with zero operand rows in
+      // [sa, s0), so its square is whole 128-row tiles (the interior-tile GEMM kernel) and the rows
+      // and columns in [sa, s0) get exact zero updates.
+      const int64_t sa = (sizeof(T) == 4 && n % 128 == 0) ? s0 / 128 * 128 : s0;
+      const int64_t m = n - sa;
+      const T* Vp = A + i0 * lda + sa;
+      const T* Wp = Wb + sa;
       hipLaunchKernelGGL(panel_operands_kernel<T>, dim3((unsigned)((m + 31) / 32)), dim3(256), 0, stream, Vp, Wp,
-                         m, lda, X, Yb);
+                         m, s0 - sa, lda, X, Yb);
       MPQ_LAUNCH_CHECK();
-      const int rc = trailing_update(h, X, Yb, A + s0 * lda + s0, lda, m, stream);
+      const int rc = trailing_update(h, X, Yb, A + sa * lda + sa, lda, m, stream);
       if (rc != kOk) return rc;
     }
   }

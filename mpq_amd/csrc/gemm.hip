@@ -926,6 +926,9 @@ hipError_t gemm(const float* A, int64_t lda, const float* B, int64_t ldb, bool t
                 hipStream_t stream) {
   int bn = 128;
   int splits = choose_splits(M, N, K, workspace ? workspace_floats : 0, &bn);
+  // whole 32-k slices per split let interior tiles run gemm_f32_full_kernel
+  if (K % 32 == 0)
+    while (splits > 1 && K % (splits * 32) != 0) splits /= 2;
   GemmParams p{};
   p.M = M; p.N = N; p.K = K;
   p.A = A; p.lda = lda; p.B = B; p.ldb = ldb; p.trans_b = trans_b; p.b_rows = b_rows;
