@@ -267,13 +267,10 @@ def run_mpq_quantization(
     block_stats: List[Dict[str, Any]] = []
     for r0 in range(0, rows, block_rows):
         r1 = min(rows, r0 + block_rows)
-        q_b, _, e_b, re_b, st = ops.uniform_vamp_solve(
+        _, _, _, _, st = ops.uniform_vamp_solve(
             W_work[r0:r1], x_rtn[r0:r1], scale_groups[r0:r1], zero_groups[r0:r1], group_size, maxq, V, S, Vs,
             vamp_cfg, obs_init=obs_block, ws=ws, Yu=Yu_all[r0:r1], xr=XR_all[r0:r1], xprod_out=XP_all[r0:r1],
-            packed=packed)
-        q_int[r0:r1] = q_b
-        err_vamp[r0:r1] = e_b
-        rtn_err[r0:r1] = re_b
+            packed=packed, q_out=q_int[r0:r1], err_out=err_vamp[r0:r1], rtn_err_out=rtn_err[r0:r1])
         if bool(getattr(vamp_cfg, "em_obs_precision", True)):
             obs_block = float(st["obs_precision_final"])
         block_stats.append(st)

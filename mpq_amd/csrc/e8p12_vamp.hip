@@ -180,7 +180,7 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
     if (e != kOk) return e;
     MPQ_HIP_TRY(prod(mvals, Vs, false, 2));
     hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, Yu, part, nullptr);
-    hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, part, errrow, status);
+    hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, part, errrow, status, nullptr, 0u);
     MPQ_LAUNCH_CHECK();
     return kOk;
   };
@@ -190,9 +190,10 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
   MPQ_HIP_TRY(splitk_reduce(P, nsplit, rows, n, Yu, n, 1.f, 0.f, stream));
   MPQ_HIP_TRY(prod(hat_init, Vs, false, 2));
   hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, Yu, part, nullptr);
-  hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, part, errrow, status);
+  hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, part, errrow, status, nullptr, 0u);
   hipLaunchKernelGGL(sqdiff_part_kernel, eg, eb, 0, stream, n, Wr, n, hat_init, n, part);
   hipLaunchKernelGGL(rows_gamma_init_kernel, dim3(1), eb, 0, stream, rows, n, nchunks, part, cfg->gamma_start, g1,
+                     nullptr,
                      status);
   MPQ_LAUNCH_CHECK();
   if ((rc = sync_status()) != kOk) return rc;
@@ -210,14 +211,14 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
   }
   const double obs_initial = obs;
   const bool em_active = cfg->em_obs_precision && cfg->obs_precision <= 0.0;
-  MPQ_HIP_TRY(hipMemcpyAsync(r1, hat_init, rows * n * 4, hipMemcpyDeviceToDevice, stream));
+  MPQ_HIP_TRY(copy_rows(r1, 0, hat_init, 0, 1, rows * n * 4, stream));
 
   const bool best_iterate = cfg->best_iterate != 0;
   double best_err_mean = INFINITY;
   double best_obs = obs;
   auto snapshot = [&](float* rd, float* gd, const float* rs, const float* gs) -> int {
-    MPQ_HIP_TRY(hipMemcpyAsync(rd, rs, rows * n * 4, hipMemcpyDeviceToDevice, stream));
-    MPQ_HIP_TRY(hipMemcpyAsync(gd, gs, rows * 4, hipMemcpyDeviceToDevice, stream));
+    MPQ_HIP_TRY(copy_rows(rd, 0, rs, 0, 1, rows * n * 4, stream));
+    MPQ_HIP_TRY(copy_rows(gd, 0, gs, 0, 1, rows * 4, stream));
     return kOk;
   };
   if (best_iterate) {
@@ -236,17 +237,18 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
   const int retry_steps = cfg->gamma_retry_steps > 0 ? cfg->gamma_retry_steps : 0;
   const int iters = cfg->iters > 0 ? cfg->iters : 0;
   for (int it = 0; it < iters; ++it) {
-    MPQ_HIP_TRY(hipMemcpyAsync(g1w, g1, rows * 4, hipMemcpyDeviceToDevice, stream));
+    MPQ_HIP_TRY(copy_rows(g1w, 0, g1, 0, 1, rows * 4, stream));
     for (int attempt = 0; attempt <= retry_steps; ++attempt) {
       rc = mpq_e8p12_map(r1, rows * nb, g1w, nb, center, prior_scale, tau, nullptr, nullptr, mvals, nullptr, nullptr,
                          stream);
       if (rc != kOk) return rc;
       MPQ_HIP_TRY(e8p12_posterior(r1, rows * nb, g1w, nb, center, prior_scale, tau, mvals, x1, var1, stream));
       hipLaunchKernelGGL(row_sum_kernel, dim3((unsigned)rows), eb, 0, stream, nb, var1, varsum);
+      const unsigned a1_seq = ++mb->seq;
       hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, nb, 1, varsum, g1w, has_prev ? 1 : 0,
-                         damping, g2prev, a1raw, a1, eta1, g2new, g2, status);
+                         damping, g2prev, a1raw, a1, eta1, g2new, g2, status, mb->d, a1_seq);
       MPQ_LAUNCH_CHECK();
-      if ((rc = sync_status()) != kOk) return rc;
+      if ((rc = wait_status(mb, a1_seq, hs, stream)) != kOk) return rc;
       if (hs->a1_invalid == 0) break;
       if (attempt >= retry_steps) {
         if (hs->a1_nonfinite) {
@@ -272,7 +274,7 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
     MPQ_HIP_TRY(prod(r2, V, false, 0));
     hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, Yu, S, g2, obs_f, x1, part);
     hipLaunchKernelGGL(rows_lmmse_kernel, dim3(1), eb, 0, stream, rows, n, n, nchunks, part, g2, damping, eta2,
-                       g1new, g1, status);
+                       g1new, g1, nullptr, status);
     MPQ_LAUNCH_CHECK();
     MPQ_HIP_TRY(prod(x1, V, true, 1));
     hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, r2, eta2, g2, g1new, damping,
@@ -324,11 +326,11 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
   // ---- final MAP decision and its error (mpq/solver.py:1124-1138)
   if ((rc = map_state(r1, g1)) != kOk) return rc;
   if ((rc = sync_status()) != kOk) return rc;
-  MPQ_HIP_TRY(hipMemcpyAsync(idx_out, midx, rows * nb * 8, hipMemcpyDeviceToDevice, stream));
-  MPQ_HIP_TRY(hipMemcpyAsync(hat_out, mvals, rows * n * 4, hipMemcpyDeviceToDevice, stream));
-  if (err_out) MPQ_HIP_TRY(hipMemcpyAsync(err_out, errrow, rows * 4, hipMemcpyDeviceToDevice, stream));
-  if (r1_out) MPQ_HIP_TRY(hipMemcpyAsync(r1_out, r1, rows * n * 4, hipMemcpyDeviceToDevice, stream));
-  if (gamma1_out) MPQ_HIP_TRY(hipMemcpyAsync(gamma1_out, g1, rows * 4, hipMemcpyDeviceToDevice, stream));
+  MPQ_HIP_TRY(copy_rows(idx_out, 0, midx, 0, 1, rows * nb * 8, stream));
+  MPQ_HIP_TRY(copy_rows(hat_out, 0, mvals, 0, 1, rows * n * 4, stream));
+  if (err_out) MPQ_HIP_TRY(copy_rows(err_out, 0, errrow, 0, 1, rows * 4, stream));
+  if (r1_out) MPQ_HIP_TRY(copy_rows(r1_out, 0, r1, 0, 1, rows * n * 4, stream));
+  if (gamma1_out) MPQ_HIP_TRY(copy_rows(gamma1_out, 0, g1, 0, 1, rows * 4, stream));
   if (stats) {
     stats->iters = reported_iters;
     stats->best_iter = best_iter;

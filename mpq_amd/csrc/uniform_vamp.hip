@@ -309,6 +309,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
   HostMailbox* mb = host_mailbox();
   MPQ_CHECK_ARG(mb != nullptr, "uniform VAMP: mapped status mailbox unavailable");
   auto sync_status = [&]() -> int { return read_status(mb, w.status, hs, stream); };
+  unsigned hard_seq = 0;  // sequence number the last hard state's row kernel published
   const float tau = cfg.prior_tau;
   int rc;
 
@@ -327,7 +328,10 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     MPQ_HIP_TRY(product(w, w.xs, Vs, false, kOpVs, rows, n, stream));
     hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, w.part,
                        pr.xprod_out ? w.prod_cur : nullptr);
-    hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, w.part, err_cur, w.status);
+    // the row kernel publishes the status (hard_seq) for the wait that follows every hard state
+    hard_seq = ++mb->seq;
+    hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, w.part, err_cur, w.status, mb->d,
+                       hard_seq);
     MPQ_LAUNCH_CHECK();
     return kOk;
   };
@@ -338,7 +342,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     // W may be strided (ldw); copy to contiguous r1 first when needed.
     const float* Wc = pr.W;
     if (pr.ldw != n) {
-      MPQ_HIP_TRY(hipMemcpy2DAsync(w.r1, n * 4, pr.W, pr.ldw * 4, n * 4, rows, hipMemcpyDeviceToDevice, stream));
+      MPQ_HIP_TRY(copy_rows(w.r1, n * 4, pr.W, pr.ldw * 4, rows, n * 4, stream));
       Wc = w.r1;
     }
     MPQ_HIP_TRY(product(w, Wc, Vs, false, kOpVs, rows, n, stream));
@@ -348,16 +352,16 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
   if (pr.xr_in) {
     hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, pr.xr_in, 1, (int64_t)0, Yu, w.part, nullptr);
   } else {
-    MPQ_HIP_TRY(hipMemcpy2DAsync(w.xs, n * 4, pr.x_init, pr.ldw * 4, n * 4, rows, hipMemcpyDeviceToDevice, stream));
+    MPQ_HIP_TRY(copy_rows(w.xs, n * 4, pr.x_init, pr.ldw * 4, rows, n * 4, stream));
     MPQ_HIP_TRY(product(w, w.xs, Vs, false, kOpVs, rows, n, stream));
     hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, w.part, nullptr);
   }
   hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, w.part,
-                     rtn_err_out ? rtn_err_out : err_cur, w.status);
+                     rtn_err_out ? rtn_err_out : err_cur, w.status, nullptr, 0u);
   // gamma1 init from the RTN decision
   hipLaunchKernelGGL(sqdiff_part_kernel, eg, eb, 0, stream, n, pr.W, pr.ldw, pr.x_init, pr.ldw, w.part + 0);
   hipLaunchKernelGGL(rows_gamma_init_kernel, dim3(1), eb, 0, stream, rows, n, nchunks, w.part,
-                     cfg.gamma_start, g1, w.status);
+                     cfg.gamma_start, g1, g1w, w.status);
   MPQ_LAUNCH_CHECK();
   if ((rc = sync_status()) != kOk) return rc;
   if (hs->g1_invalid) {
@@ -381,11 +385,11 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     MPQ_HIP_TRY(hipMemsetAsync(w.r1, 0, rows * n * 4, stream));
   } else {
     const float* src = cfg.init_from == 1 ? pr.W : pr.x_init;
-    MPQ_HIP_TRY(hipMemcpy2DAsync(w.r1, n * 4, src, pr.ldw * 4, n * 4, rows, hipMemcpyDeviceToDevice, stream));
+    MPQ_HIP_TRY(copy_rows(w.r1, n * 4, src, pr.ldw * 4, rows, n * 4, stream));
   }
   // initial hard state = best
   if ((rc = hard_state(w.r1, g1)) != kOk) return rc;
-  if ((rc = sync_status()) != kOk) return rc;
+  if ((rc = wait_status(mb, hard_seq, hs, stream)) != kOk) return rc;
   double best_err_mean = (double)hs->err_mean;
   std::swap(w.q_cur, w.q_best);
   std::swap(err_cur, err_best);
@@ -401,17 +405,20 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
   const int retry_steps = cfg.gamma_retry_steps > 0 ? cfg.gamma_retry_steps : 0;
   const int iters = cfg.iters > 0 ? cfg.iters : 0;
 
+  bool g1w_current = true;  // g1w == g1 (the row kernels that write gamma1 also write g1w)
   for (int it = 0; it < iters; ++it) {
-    // ---- denoiser with gamma retries (mpq/solver.py:559-596)
-    MPQ_HIP_TRY(hipMemcpyAsync(g1w, g1, rows * 4, hipMemcpyDeviceToDevice, stream));
+    // ---- denoiser with gamma retries (mpq/solver.py:559-596), from g1w = g1
+    if (!g1w_current) MPQ_HIP_TRY(copy_rows(g1w, 0, g1, 0, 1, rows * 4, stream));
+    g1w_current = true;
     for (int attempt = 0; attempt <= retry_steps; ++attempt) {
       hipLaunchKernelGGL(uniform_denoise_kernel<kPosterior>, eg, eb, 0, stream, w.r1, g1w, pr.W, pr.ldw,
                          pr.scale, pr.zero, G, pr.group_size, n, pr.maxq, tau, w.x1, w.part, nullptr,
                          nullptr);
+      const unsigned a1_seq = ++mb->seq;
       hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, n, nchunks, w.part, g1w,
-                         has_prev ? 1 : 0, damping, g2prev, a1raw, a1, eta1, g2new, g2, w.status);
+                         has_prev ? 1 : 0, damping, g2prev, a1raw, a1, eta1, g2new, g2, w.status, mb->d, a1_seq);
       MPQ_LAUNCH_CHECK();
-      if ((rc = sync_status()) != kOk) return rc;
+      if ((rc = wait_status(mb, a1_seq, hs, stream)) != kOk) return rc;
       if (hs->a1_invalid == 0) break;
       if (attempt >= retry_steps) {
         if (hs->a1_nonfinite) {
@@ -423,6 +430,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
       }
       a1_retry += hs->a1_invalid;
       hipLaunchKernelGGL(rows_retry_kernel, dim3(1), eb, 0, stream, rows, a1raw, retry_factor, g1w);
+      g1w_current = false;
       MPQ_LAUNCH_CHECK();
     }
     if (hs->g2new_invalid || hs->g2_invalid) {  // mpq/solver.py:602-604, 613-615
@@ -439,7 +447,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, pr.S, g2,
                        obs_f, w.x1, w.part);
     hipLaunchKernelGGL(rows_lmmse_kernel, dim3(1), eb, 0, stream, rows, n, n, nchunks, w.part, g2, damping,
-                       eta2, g1new, g1, w.status);
+                       eta2, g1new, g1, g1w, w.status);
     MPQ_LAUNCH_CHECK();
     MPQ_HIP_TRY(product(w, w.x1, pr.V, true, kOpVt, rows, n, stream));
     hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.r2, eta2, g2,
@@ -447,7 +455,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     MPQ_LAUNCH_CHECK();
     // ---- hard state of the new (r1, g1)
     if ((rc = hard_state(w.r1, g1)) != kOk) return rc;
-    if ((rc = sync_status()) != kOk) return rc;
+    if ((rc = wait_status(mb, hard_seq, hs, stream)) != kOk) return rc;
     a2_clip += hs->a2_clip;
     // EM update of the observation precision (mpq/linear.py:59-82), in double like the reference
     if (em_active) {
@@ -487,10 +495,10 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
   }
 
   // ---- outputs
-  MPQ_HIP_TRY(hipMemcpyAsync(q_out, w.q_best, rows * n, hipMemcpyDeviceToDevice, stream));
-  if (err_out) MPQ_HIP_TRY(hipMemcpyAsync(err_out, err_best, rows * 4, hipMemcpyDeviceToDevice, stream));
+  MPQ_HIP_TRY(copy_rows(q_out, 0, w.q_best, 0, 1, rows * n, stream));
+  if (err_out) MPQ_HIP_TRY(copy_rows(err_out, 0, err_best, 0, 1, rows * 4, stream));
   if (pr.xprod_out)
-    MPQ_HIP_TRY(hipMemcpyAsync(pr.xprod_out, w.prod_best, rows * n * 4, hipMemcpyDeviceToDevice, stream));
+    MPQ_HIP_TRY(copy_rows(pr.xprod_out, 0, w.prod_best, 0, 1, rows * n * 4, stream));
   if (x_out) {
     MPQ_HIP_TRY(dequant_groups(w.q_best, pr.scale, pr.zero, G, pr.group_size, rows, n, x_out, stream));
   }

@@ -47,13 +47,17 @@ struct StatusMailbox {
   unsigned pad[15];
 };
 
+// Copy the status to the mapped host mailbox, then publish its sequence number behind a
+// system-scope fence (the host reads the status once it sees `seq`).  One thread.
+__device__ __forceinline__ void publish_to(const VampStatus* st, StatusMailbox* box, unsigned seq) {
+  box->st = *st;
+  __threadfence_system();
+  __hip_atomic_store(&box->seq, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 __global__ __launch_bounds__(64) void publish_status_kernel(const VampStatus* __restrict__ src,
                                                             StatusMailbox* __restrict__ box, unsigned seq) {
-  if (threadIdx.x == 0) {
-    box->st = *src;
-    __threadfence_system();
-    __hip_atomic_store(&box->seq, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-  }
+  if (threadIdx.x == 0) publish_to(src, box, seq);
 }
 
 struct HostMailbox {
@@ -82,11 +86,9 @@ inline HostMailbox* host_mailbox() {
   return &mb;
 }
 
-// Copy the device status to *out once every earlier operation on `stream` has completed.
-inline int read_status(HostMailbox* mb, const VampStatus* dstatus, VampStatus* out, hipStream_t stream) {
-  const unsigned seq = ++mb->seq;
-  hipLaunchKernelGGL(publish_status_kernel, dim3(1), dim3(64), 0, stream, dstatus, mb->d, seq);
-  MPQ_LAUNCH_CHECK();
+// Wait for the status published with sequence number `seq` (by publish_status_kernel or by a
+// row kernel that publishes at its end) and copy it to *out.
+inline int wait_status(HostMailbox* mb, unsigned seq, VampStatus* out, hipStream_t stream) {
   const auto t0 = std::chrono::steady_clock::now();
   unsigned spins = 0;
   while (__atomic_load_n(&mb->h->seq, __ATOMIC_ACQUIRE) != seq) {
@@ -103,6 +105,14 @@ inline int read_status(HostMailbox* mb, const VampStatus* dstatus, VampStatus* o
   }
   std::memcpy(out, &mb->h->st, sizeof(VampStatus));
   return kOk;
+}
+
+// Copy the device status to *out once every earlier operation on `stream` has completed.
+inline int read_status(HostMailbox* mb, const VampStatus* dstatus, VampStatus* out, hipStream_t stream) {
+  const unsigned seq = ++mb->seq;
+  hipLaunchKernelGGL(publish_status_kernel, dim3(1), dim3(64), 0, stream, dstatus, mb->d, seq);
+  MPQ_LAUNCH_CHECK();
+  return wait_status(mb, seq, out, stream);
 }
 
 __device__ __forceinline__ float grp(const float* a, int64_t b, int64_t G, int64_t gs, int64_t j) {
@@ -127,7 +137,8 @@ __global__ __launch_bounds__(kEW) void rows_alpha1_kernel(
     int64_t rows, int64_t n, int nchunks, const float* __restrict__ var_part,
     const float* __restrict__ g1w, int has_prev, float damping, const float* __restrict__ g2prev,
     float* __restrict__ alpha1_raw, float* __restrict__ alpha1, float* __restrict__ eta1,
-    float* __restrict__ g2new, float* __restrict__ g2, VampStatus* __restrict__ st) {
+    float* __restrict__ g2new, float* __restrict__ g2, VampStatus* __restrict__ st, StatusMailbox* box,
+    unsigned seq) {
   __shared__ float red[kEW / 64];
   int inval = 0, nonfin = 0, g2n_bad = 0, g2_bad = 0;
   float a1part = 0.f;  // this thread's rows of sum(alpha1), in row order
@@ -177,6 +188,7 @@ __global__ __launch_bounds__(kEW) void rows_alpha1_kernel(
     st->g2new_invalid = (int)s_g2n;
     st->g2_invalid = (int)s_g2;
     st->a1_mean = a1sum / (float)rows;
+    if (box) publish_to(st, box, seq);  // saves the launch of publish_status_kernel
   }
 }
 
@@ -262,7 +274,7 @@ __global__ __launch_bounds__(kEW) void lmmse_epi1_kernel(
 __global__ __launch_bounds__(kEW) void rows_lmmse_kernel(
     int64_t rows, int64_t n, int64_t rank, int nchunks, const float* __restrict__ part3,
     const float* __restrict__ g2, float damping, float* __restrict__ eta2,
-    float* __restrict__ g1new, float* __restrict__ g1, VampStatus* __restrict__ st) {
+    float* __restrict__ g1new, float* __restrict__ g1, float* __restrict__ g1w, VampStatus* __restrict__ st) {
   __shared__ float red[kEW / 64];
   const float hi = one_minus_alpha_eps();
   const float c0 = (float)(1.0 - (double)rank / (double)n);
@@ -298,6 +310,7 @@ __global__ __launch_bounds__(kEW) void rows_lmmse_kernel(
       }
     }
     g1[b] = gd;
+    if (g1w) g1w[b] = gd;  // the next iteration's working gamma1 (its retries scale the copy)
     // EM statistic per row: |residual_after|^2 + trace term; alpha2 kept for stats
     eta2[rows + b] = sres + strace;
     eta2[2 * rows + b] = a2;
@@ -363,7 +376,8 @@ __global__ __launch_bounds__(kEW) void err_epi_kernel(int64_t n, const float* __
 __global__ __launch_bounds__(kEW) void rows_err_kernel(int64_t rows, int nchunks,
                                                        const float* __restrict__ part,
                                                        float* __restrict__ out,
-                                                       VampStatus* __restrict__ st) {
+                                                       VampStatus* __restrict__ st, StatusMailbox* box,
+                                                       unsigned seq) {
   __shared__ float red[kEW / 64];
   float part_sum = 0.f;  // this thread's rows, in row order
   for (int64_t b = threadIdx.x; b < rows; b += blockDim.x) {
@@ -376,6 +390,7 @@ __global__ __launch_bounds__(kEW) void rows_err_kernel(int64_t rows, int nchunks
   if (threadIdx.x == 0) {
     st->err_sum = s;
     st->err_mean = s / (float)rows;
+    if (box) publish_to(st, box, seq);  // saves the launch of publish_status_kernel
   }
 }
 
@@ -401,6 +416,7 @@ __global__ __launch_bounds__(kEW) void rows_gamma_init_kernel(int64_t rows, int6
                                                               const float* __restrict__ part,
                                                               float gamma_start,
                                                               float* __restrict__ g1,
+                                                              float* __restrict__ g1w,
                                                               VampStatus* __restrict__ st) {
   __shared__ float red[kEW / 64];
   int bad = 0;
@@ -411,10 +427,48 @@ __global__ __launch_bounds__(kEW) void rows_gamma_init_kernel(int64_t rows, int6
     mse = mse < 1e-12f ? 1e-12f : mse;
     const float g = gamma_start * (0.25f / mse);
     g1[b] = g;
+    if (g1w) g1w[b] = g;
     bad += !(isfinite(g) && g > kPrecEps);
   }
   const float s = block_sum((float)bad, red);
   if (threadIdx.x == 0) st->g1_invalid = (int)s;
+}
+
+// dst[r * ldd + c] = src[r * lds + c] (elements of T) for r < rows, c < cols.
+template <typename T>
+__global__ void copy_rows_kernel(T* __restrict__ dst, int64_t ldd, const T* __restrict__ src, int64_t lds,
+                                 int64_t rows, int64_t cols) {
+  const int64_t total = rows * cols;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / cols, c = e - r * cols;
+    dst[r * ldd + c] = src[r * lds + c];
+  }
+}
+
+// Strided device-to-device copy of `rows` rows of `row_bytes` as one kernel (16-, 4- or 1-byte
+// elements by alignment).  The solvers' small per-block copies take this instead of
+// hipMemcpy*Async, whose host-side cost left the GPU idle between their short kernels.
+inline hipError_t copy_rows(void* dst, int64_t ldd_bytes, const void* src, int64_t lds_bytes, int64_t rows,
+                            int64_t row_bytes, hipStream_t stream) {
+  if (rows <= 0 || row_bytes <= 0) return hipSuccess;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) |
+                          (uintptr_t)ldd_bytes | (uintptr_t)lds_bytes | (uintptr_t)row_bytes;
+  const int es = (align & 15u) == 0 ? 16 : (align & 3u) == 0 ? 4 : 1;
+  const int64_t cols = row_bytes / es;
+  int64_t blocks = (rows * cols + 255) / 256;
+  blocks = blocks < 1 ? 1 : blocks > 4096 ? 4096 : blocks;
+  if (es == 16)
+    hipLaunchKernelGGL(copy_rows_kernel<uint4>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<uint4*>(dst), ldd_bytes / 16, static_cast<const uint4*>(src), lds_bytes / 16, rows,
+                       cols);
+  else if (es == 4)
+    hipLaunchKernelGGL(copy_rows_kernel<uint32_t>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<uint32_t*>(dst), ldd_bytes / 4, static_cast<const uint32_t*>(src), lds_bytes / 4,
+                       rows, cols);
+  else
+    hipLaunchKernelGGL(copy_rows_kernel<uint8_t>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<uint8_t*>(dst), ldd_bytes, static_cast<const uint8_t*>(src), lds_bytes, rows, cols);
+  return hipGetLastError();
 }
 
 }  // namespace

@@ -317,11 +317,15 @@ def vamp_config_c(cfg) -> "_lib.UniformVampConfigC":
 
 def uniform_vamp_solve(W, x_init, scale, zero, group_size, maxq, V, S, Vs, cfg, obs_init: float = 0.0,
                        want_x: bool = False, ws: Optional[torch.Tensor] = None, Yu=None, xr=None,
-                       xprod_out: Optional[torch.Tensor] = None, packed: Optional[torch.Tensor] = None):
+                       xprod_out: Optional[torch.Tensor] = None, packed: Optional[torch.Tensor] = None,
+                       q_out: Optional[torch.Tensor] = None, err_out: Optional[torch.Tensor] = None,
+                       rtn_err_out: Optional[torch.Tensor] = None):
     """One row block of the uniform VAMP loop.  Returns (q uint8, x|None, err, rtn_err, stats dict).
     ``Yu`` = W Vs and ``xr`` = x_init Vs may come from the caller (formed once for all row blocks);
     ``xprod_out`` (rows x n, contiguous fp32) then receives x_best Vs of the returned codes.
-    ``packed`` (from :func:`rankspace_pack`) runs the solver's products on the bf16 matrix cores."""
+    ``packed`` (from :func:`rankspace_pack`) runs the solver's products on the bf16 matrix cores.
+    ``q_out`` (uint8 rows x n), ``err_out`` and ``rtn_err_out`` (float32 rows), contiguous, receive the
+    results in place of new tensors."""
     dev = _dev(W, x_init, scale, zero, V, S, Vs, Yu, xr, xprod_out, packed)
     W = _f32c(W)
     x_init = _f32c(x_init)
@@ -335,10 +339,14 @@ def uniform_vamp_solve(W, x_init, scale, zero, group_size, maxq, V, S, Vs, cfg, 
     need = int(lib.mpq_uniform_vamp_workspace_size(rows, n))
     if ws is None or ws.numel() < need:
         ws = workspace(need, dev)
-    q = torch.empty(rows, n, dtype=torch.uint8, device=dev)
+    for name, t, dt, shape in (("q_out", q_out, torch.uint8, (rows, n)), ("err_out", err_out, F32, (rows,)),
+                               ("rtn_err_out", rtn_err_out, F32, (rows,))):
+        if t is not None and (tuple(t.shape) != shape or t.dtype != dt or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous {dt} tensor of shape {shape}")
+    q = q_out if q_out is not None else torch.empty(rows, n, dtype=torch.uint8, device=dev)
     x = torch.empty(rows, n, dtype=F32, device=dev) if want_x else None
-    err = torch.empty(rows, dtype=F32, device=dev)
-    rtn_err = torch.empty(rows, dtype=F32, device=dev)
+    err = err_out if err_out is not None else torch.empty(rows, dtype=F32, device=dev)
+    rtn_err = rtn_err_out if rtn_err_out is not None else torch.empty(rows, dtype=F32, device=dev)
     st = _lib.UniformVampStatsC()
     c = vamp_config_c(cfg)
     for name, t in (("Yu", Yu), ("xr", xr), ("xprod_out", xprod_out)):
