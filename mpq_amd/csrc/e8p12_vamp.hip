@@ -164,10 +164,13 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
   // `op` indexes the packed operator (0: V for r V, 1: V for x V^T, 2: Vs for x Vs)
   const bool x6 = packed != nullptr && pl.splits_x6 > 0;
   const int nsplit = x6 ? pl.splits_x6 : pl.splits;
-  auto prod = [&](const float* A, const float* B, bool trans_b, int op) -> hipError_t {
+  uint4* const planes = x6 ? static_cast<uint4*>(Ap) : nullptr;  // written by msg_r2 / lmmse_epi1
+  auto prod = [&](const float* A, const float* B, bool trans_b, int op, bool a_planes_written = false) -> hipError_t {
     if (x6) {
-      hipError_t e = x6_pack_a(A, n, rows, n, Ap, stream);
-      if (e != hipSuccess) return e;
+      if (!a_planes_written) {  // else the kernel that produced A wrote its planes into Ap
+        hipError_t e = x6_pack_a(A, n, rows, n, Ap, stream);
+        if (e != hipSuccess) return e;
+      }
       return x6_gemm_partials(Ap, packed + (int64_t)op * n * n, rows, n, n, P, n, sstride, nsplit, stream);
     }
     return product(A, B, trans_b, rows, n, P, pl.splits, pl.bn, stream);
@@ -269,14 +272,15 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
     const float a1_mean_it = hs->a1_mean;
     const float obs_f = (float)obs;
     hipLaunchKernelGGL(msg_r2_kernel, eg, eb, 0, stream, n, x1, r1, eta1, g1w, g2new, has_prev ? 1 : 0, damping,
-                       r2prev, r2);
+                       r2prev, r2, planes);
     MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(prod(r2, V, false, 0));
-    hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, Yu, S, g2, obs_f, x1, part);
+    MPQ_HIP_TRY(prod(r2, V, false, 0, planes != nullptr));
+    hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, Yu, S, g2, obs_f, x1, part,
+                       planes);
     hipLaunchKernelGGL(rows_lmmse_kernel, dim3(1), eb, 0, stream, rows, n, n, nchunks, part, g2, damping, eta2,
                        g1new, g1, nullptr, status);
     MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(prod(x1, V, true, 1));
+    MPQ_HIP_TRY(prod(x1, V, true, 1, planes != nullptr));
     hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, r2, eta2, g2, g1new, damping,
                        r1);
     MPQ_LAUNCH_CHECK();

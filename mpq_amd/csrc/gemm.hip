@@ -14,6 +14,7 @@
 // gemm_f32_full_kernel: no bounds checks and two K slabs of global loads in flight;
 // ragged or gathered products run gemm_f32_kernel with one slab of register prefetch.
 #include "gemm.h"
+#include "x6_split.h"
 
 namespace mpq {
 namespace {
@@ -480,26 +481,9 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_full_kernel(GemmParams p) {
 // 8 or 16 splits every XCD (blocks are dispatched round-robin over 8) works on one or two K slices
 // and its L2 holds those slices of A.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint32_t pk_bf16(float x, float y) {
-  const f32x2 v = {x, y};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));  // v_cvt_pk_bf16_f32 (RNE)
-}
-
-// Three bf16 planes of the pair (x, y), each packed low = x, high = y.
-__device__ __forceinline__ void split3(float x, float y, uint32_t& h, uint32_t& m, uint32_t& l) {
-  h = pk_bf16(x, y);
-  const float rx = x - __builtin_bit_cast(float, h << 16);
-  const float ry = y - __builtin_bit_cast(float, h & 0xffff0000u);
-  m = pk_bf16(rx, ry);
-  const float sx = rx - __builtin_bit_cast(float, m << 16);
-  const float sy = ry - __builtin_bit_cast(float, m & 0xffff0000u);
-  l = pk_bf16(sx, sy);
-}
 
 // B tiles: thread per chunk (8 floats).  trans_b: op(B)(k, n) = B[n*ldb + k] (32 contiguous bytes
 // per thread), else B[k*ldb + n] (lanes along n).

@@ -40,8 +40,10 @@ __global__ __launch_bounds__(kEW) void uniform_denoise_kernel(
     const float* __restrict__ r1, const float* __restrict__ gamma, const float* __restrict__ W,
     int64_t ldw, const float* __restrict__ scale, const float* __restrict__ zero, int64_t G,
     int64_t gs, int64_t n, int maxq, float tau, float* __restrict__ mean_out,
-    float* __restrict__ var_part, uint8_t* __restrict__ q_out, float* __restrict__ x_out) {
+    float* __restrict__ var_part, uint8_t* __restrict__ q_out, float* __restrict__ x_out,
+    uint4* __restrict__ planes) {
   __shared__ float red[kEW / 64];
+  __shared__ __attribute__((aligned(16))) float s_v[(MODE == kHardMap || MODE == kHardRoundMean) ? kChunk : 4];
   const int64_t b = blockIdx.y;
   const int nchunks = gridDim.x;
   const float g = gamma[b];
@@ -144,6 +146,13 @@ __global__ __launch_bounds__(kEW) void uniform_denoise_kernel(
       }
       q_out[b * n + j] = (uint8_t)q;
       x_out[b * n + j] = s * ((float)q - z);
+      if (planes) s_v[e * kEW + threadIdx.x] = s * ((float)q - z);
+    }
+  }
+  if (MODE == kHardMap || MODE == kHardRoundMean) {
+    if (planes) {  // uniform: the planes of the hard state for its x6 product
+      __syncthreads();
+      chunk_planes(planes, n, b, s_v);
     }
   }
   if (MODE == kPosterior) {
@@ -253,10 +262,12 @@ enum RankOperand : int { kOpV = 0, kOpVt = 1, kOpVs = 2 };
 // operator the product runs on the bf16 matrix cores (A split into planes first), else on the
 // fp32 MFMA kernel.
 static hipError_t product(const Workspace& w, const float* A, const float* B, bool trans_b, RankOperand op,
-                          int64_t rows, int64_t n, hipStream_t stream) {
+                          int64_t rows, int64_t n, hipStream_t stream, bool a_planes_written = false) {
   if (w.packed) {
-    hipError_t e = x6_pack_a(A, n, rows, n, w.Ap, stream);
-    if (e != hipSuccess) return e;
+    if (!a_planes_written) {  // else the kernel that produced A wrote its planes into w.Ap
+      hipError_t e = x6_pack_a(A, n, rows, n, w.Ap, stream);
+      if (e != hipSuccess) return e;
+    }
     return x6_gemm_partials(w.Ap, w.packed + (int64_t)op * n * n, rows, n, n, w.P, n, align_up(rows * n, 64),
                             w.splits, stream);
   }
@@ -284,6 +295,8 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     w.packed = pr.packed;
     w.splits = w.splits_x6;
   }
+  // x6 path: the kernels producing the left operands of the products write its bf16 planes
+  uint4* const planes = w.packed ? static_cast<uint4*>(w.Ap) : nullptr;
   const float* Yu = pr.Yu_in ? pr.Yu_in : w.Yu;
   VampStatus* hs = host_status();
   MPQ_CHECK_ARG(hs != nullptr, "uniform VAMP: pinned status buffer unavailable");
@@ -318,14 +331,14 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     if (cfg.final_decision == 1) {
       hipLaunchKernelGGL(uniform_denoise_kernel<kHardRoundMean>, eg, eb, 0, stream, r, g, pr.W, pr.ldw,
                          pr.scale, pr.zero, G, pr.group_size, n, pr.maxq, tau, nullptr, nullptr,
-                         w.q_cur, w.xs);
+                         w.q_cur, w.xs, planes);
     } else {
       hipLaunchKernelGGL(uniform_denoise_kernel<kHardMap>, eg, eb, 0, stream, r, g, pr.W, pr.ldw,
                          pr.scale, pr.zero, G, pr.group_size, n, pr.maxq, tau, nullptr, nullptr,
-                         w.q_cur, w.xs);
+                         w.q_cur, w.xs, planes);
     }
     MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(product(w, w.xs, Vs, false, kOpVs, rows, n, stream));
+    MPQ_HIP_TRY(product(w, w.xs, Vs, false, kOpVs, rows, n, stream, planes != nullptr));
     hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, w.part,
                        pr.xprod_out ? w.prod_cur : nullptr);
     // the row kernel publishes the status (hard_seq) for the wait that follows every hard state
@@ -413,7 +426,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     for (int attempt = 0; attempt <= retry_steps; ++attempt) {
       hipLaunchKernelGGL(uniform_denoise_kernel<kPosterior>, eg, eb, 0, stream, w.r1, g1w, pr.W, pr.ldw,
                          pr.scale, pr.zero, G, pr.group_size, n, pr.maxq, tau, w.x1, w.part, nullptr,
-                         nullptr);
+                         nullptr, nullptr);
       const unsigned a1_seq = ++mb->seq;
       hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, n, nchunks, w.part, g1w,
                          has_prev ? 1 : 0, damping, g2prev, a1raw, a1, eta1, g2new, g2, w.status, mb->d, a1_seq);
@@ -441,15 +454,15 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     // ---- r2 message, LMMSE (obs as used by this iteration)
     const float obs_f = (float)obs;
     hipLaunchKernelGGL(msg_r2_kernel, eg, eb, 0, stream, n, w.x1, w.r1, eta1, g1w, g2new,
-                       has_prev ? 1 : 0, damping, w.r2prev, w.r2);
+                       has_prev ? 1 : 0, damping, w.r2prev, w.r2, planes);
     MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(product(w, w.r2, pr.V, false, kOpV, rows, n, stream));
+    MPQ_HIP_TRY(product(w, w.r2, pr.V, false, kOpV, rows, n, stream, planes != nullptr));
     hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, pr.S, g2,
-                       obs_f, w.x1, w.part);
+                       obs_f, w.x1, w.part, planes);
     hipLaunchKernelGGL(rows_lmmse_kernel, dim3(1), eb, 0, stream, rows, n, n, nchunks, w.part, g2, damping,
                        eta2, g1new, g1, g1w, w.status);
     MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(product(w, w.x1, pr.V, true, kOpVt, rows, n, stream));
+    MPQ_HIP_TRY(product(w, w.x1, pr.V, true, kOpVt, rows, n, stream, planes != nullptr));
     hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.r2, eta2, g2,
                        g1new, damping, w.r1);
     MPQ_LAUNCH_CHECK();
@@ -579,7 +592,7 @@ extern "C" int mpq_uniform_denoise(int64_t rows, int64_t n, int maxq, const floa
   const dim3 eg((unsigned)((n + mpq::kChunk - 1) / mpq::kChunk), (unsigned)rows);
   hipLaunchKernelGGL(mpq::uniform_denoise_kernel<mpq::kFull>, eg, dim3(mpq::kEW), 0, stream, r1, gamma, center,
                      ld_center, scale, zero, G, group_size, n, maxq, tau, mean, var,
-                     reinterpret_cast<uint8_t*>(map_idx), map_value);
+                     reinterpret_cast<uint8_t*>(map_idx), map_value, nullptr);
   MPQ_LAUNCH_CHECK();
   if (alpha1) {
     hipLaunchKernelGGL(mpq::row_alpha_kernel, dim3((unsigned)rows), dim3(mpq::kEW), 0, stream, n, var, gamma,

@@ -8,6 +8,7 @@
 #include <cstring>
 
 #include "common.h"
+#include "x6_split.h"
 
 namespace mpq {
 namespace {
@@ -53,6 +54,17 @@ __device__ __forceinline__ void publish_to(const VampStatus* st, StatusMailbox* 
   box->st = *st;
   __threadfence_system();
   __hip_atomic_store(&box->seq, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// bf16 planes of this work-group's column chunk of row b, staged in s_v (column
+// blockIdx.x * kChunk + i at s_v[i]), at their place in the packed left operand At of the next x6
+// product (n % 16 == 0).  The producing kernels write them so the product needs no packing launch.
+__device__ __forceinline__ void chunk_planes(uint4* __restrict__ At, int64_t n, int64_t b, const float* s_v) {
+  const int64_t j0 = (int64_t)blockIdx.x * kChunk + 4 * threadIdx.x;
+  if (j0 < n) {
+    const float4 v = *reinterpret_cast<const float4*>(s_v + 4 * threadIdx.x);
+    store_planes4(At, n, b, j0, v.x, v.y, v.z, v.w);
+  }
 }
 
 __global__ __launch_bounds__(64) void publish_status_kernel(const VampStatus* __restrict__ src,
@@ -213,7 +225,8 @@ __global__ __launch_bounds__(kEW) void msg_r2_kernel(int64_t n, const float* __r
                                                      const float* __restrict__ g1w,
                                                      const float* __restrict__ g2new, int has_prev,
                                                      float damping, const float* __restrict__ r2prev,
-                                                     float* __restrict__ r2) {
+                                                     float* __restrict__ r2, uint4* __restrict__ planes) {
+  __shared__ __attribute__((aligned(16))) float s_v[kChunk];
   const int64_t b = blockIdx.y;
   const float e1 = eta1[b], gw = g1w[b], gn = g2new[b];
   const bool damp = has_prev && damping < 1.f;
@@ -224,7 +237,13 @@ __global__ __launch_bounds__(kEW) void msg_r2_kernel(int64_t n, const float* __r
     if (j >= n) continue;
     const int64_t o = b * n + j;
     const float rn = (e1 * x1[o] - gw * r1[o]) / gn;
-    r2[o] = damp ? keep * r2prev[o] + damping * rn : rn;
+    const float v = damp ? keep * r2prev[o] + damping * rn : rn;
+    r2[o] = v;
+    if (planes) s_v[e * kEW + threadIdx.x] = v;
+  }
+  if (planes) {  // uniform
+    __syncthreads();
+    chunk_planes(planes, n, b, s_v);
   }
 }
 
@@ -235,8 +254,9 @@ __global__ __launch_bounds__(kEW) void msg_r2_kernel(int64_t n, const float* __r
 __global__ __launch_bounds__(kEW) void lmmse_epi1_kernel(
     int64_t n, const float* __restrict__ P, int splits, int64_t split_stride,
     const float* __restrict__ Yu, const float* __restrict__ S, const float* __restrict__ g2,
-    float obs, float* __restrict__ c_out, float* __restrict__ part3) {
+    float obs, float* __restrict__ c_out, float* __restrict__ part3, uint4* __restrict__ planes) {
   __shared__ float red[kEW / 64];
+  __shared__ __attribute__((aligned(16))) float s_v[kChunk];
   const int64_t b = blockIdx.y;
   const int nchunks = gridDim.x;
   const float gb = g2[b];
@@ -253,10 +273,15 @@ __global__ __launch_bounds__(kEW) void lmmse_epi1_kernel(
     const float rb = Yu[o] - r2v * sj;
     const float coeff = (obs * sj) / denom;
     c_out[o] = rb * coeff;
+    if (planes) s_v[e * kEW + threadIdx.x] = rb * coeff;
     sinv += 1.0f / denom;
     const float ra = rb * (gb / denom);
     sres += ra * ra;
     strace += s2 / denom;
+  }
+  if (planes) {  // uniform
+    __syncthreads();
+    chunk_planes(planes, n, b, s_v);
   }
   const float t0 = block_sum(sinv, red);
   const float t1 = block_sum(sres, red);
