@@ -239,18 +239,26 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
   const float retry_factor = cfg->gamma_retry_factor > 1.000001f ? cfg->gamma_retry_factor : 1.000001f;
   const int retry_steps = cfg->gamma_retry_steps > 0 ? cfg->gamma_retry_steps : 0;
   const int iters = cfg->iters > 0 ? cfg->iters : 0;
+  // posterior denoiser of (r1, g1w) + the alpha1 row kernel, which publishes its status under *seq
+  auto launch_alpha1 = [&](unsigned* seq) -> int {
+    int e = mpq_e8p12_map(r1, rows * nb, g1w, nb, center, prior_scale, tau, nullptr, nullptr, mvals, nullptr, nullptr,
+                          stream);
+    if (e != kOk) return e;
+    MPQ_HIP_TRY(e8p12_posterior(r1, rows * nb, g1w, nb, center, prior_scale, tau, mvals, x1, var1, stream));
+    hipLaunchKernelGGL(row_sum_kernel, dim3((unsigned)rows), eb, 0, stream, nb, var1, varsum);
+    *seq = ++mb->seq;
+    hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, nb, 1, varsum, g1w, has_prev ? 1 : 0,
+                       damping, g2prev, a1raw, a1, eta1, g2new, g2, status, mb->dev(*seq), *seq);
+    MPQ_LAUNCH_CHECK();
+    return kOk;
+  };
+  unsigned ahead_seq = 0;  // the iteration's first denoiser pass, launched at the end of the one before
   for (int it = 0; it < iters; ++it) {
-    MPQ_HIP_TRY(copy_rows(g1w, 0, g1, 0, 1, rows * 4, stream));
+    if (ahead_seq == 0) MPQ_HIP_TRY(copy_rows(g1w, 0, g1, 0, 1, rows * 4, stream));
     for (int attempt = 0; attempt <= retry_steps; ++attempt) {
-      rc = mpq_e8p12_map(r1, rows * nb, g1w, nb, center, prior_scale, tau, nullptr, nullptr, mvals, nullptr, nullptr,
-                         stream);
-      if (rc != kOk) return rc;
-      MPQ_HIP_TRY(e8p12_posterior(r1, rows * nb, g1w, nb, center, prior_scale, tau, mvals, x1, var1, stream));
-      hipLaunchKernelGGL(row_sum_kernel, dim3((unsigned)rows), eb, 0, stream, nb, var1, varsum);
-      const unsigned a1_seq = ++mb->seq;
-      hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, nb, 1, varsum, g1w, has_prev ? 1 : 0,
-                         damping, g2prev, a1raw, a1, eta1, g2new, g2, status, mb->d, a1_seq);
-      MPQ_LAUNCH_CHECK();
+      unsigned a1_seq = ahead_seq;
+      ahead_seq = 0;
+      if (a1_seq == 0 && (rc = launch_alpha1(&a1_seq)) != kOk) return rc;
       if ((rc = wait_status(mb, a1_seq, hs, stream)) != kOk) return rc;
       if (hs->a1_invalid == 0) break;
       if (attempt >= retry_steps) {
@@ -287,7 +295,21 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
     if (best_iterate) {
       if ((rc = map_state(r1, g1)) != kOk) return rc;
     }
-    if ((rc = sync_status()) != kOk) return rc;
+    const unsigned st_seq = ++mb->seq;
+    hipLaunchKernelGGL(publish_status_kernel, dim3(1), dim3(64), 0, stream, status, mb->dev(st_seq), st_seq);
+    MPQ_LAUNCH_CHECK();
+    std::swap(r2, r2prev);
+    std::swap(g2, g2prev);
+    has_prev = true;
+    // The next iteration's first denoiser pass reads only device state (r1, gamma1, and gamma2 of
+    // this iteration), so it is queued before this iteration's status is read.  It writes none of
+    // r1, gamma1 or the MAP decision the loop keeps, so a stop (which restores the best r1, gamma1
+    // and decides again) never reads its results.
+    if (it + 1 < iters) {
+      MPQ_HIP_TRY(copy_rows(g1w, 0, g1, 0, 1, rows * 4, stream));
+      if ((rc = launch_alpha1(&ahead_seq)) != kOk) return rc;
+    }
+    if ((rc = wait_status(mb, st_seq, hs, stream)) != kOk) return rc;
     a2_clip += hs->a2_clip;
     if (em_active) {
       const float den = hs->em_mean < 1e-12f ? 1e-12f : hs->em_mean;
@@ -301,9 +323,6 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
       beta = std::min(std::max(beta, cfg->em_obs_precision_min), cfg->em_obs_precision_max);
       obs = beta;
     }
-    std::swap(r2, r2prev);
-    std::swap(g2, g2prev);
-    has_prev = true;
     obs_sum += obs;
     a1_sum += a1_mean_it;
     a2_sum += hs->a2_mean;

@@ -343,7 +343,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
                        pr.xprod_out ? w.prod_cur : nullptr);
     // the row kernel publishes the status (hard_seq) for the wait that follows every hard state
     hard_seq = ++mb->seq;
-    hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, w.part, err_cur, w.status, mb->d,
+    hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, w.part, err_cur, w.status, mb->dev(hard_seq),
                        hard_seq);
     MPQ_LAUNCH_CHECK();
     return kOk;
@@ -419,18 +419,31 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
   const int iters = cfg.iters > 0 ? cfg.iters : 0;
 
   bool g1w_current = true;  // g1w == g1 (the row kernels that write gamma1 also write g1w)
+  // posterior denoiser of (r1, g1w) + the alpha1 row kernel, which publishes its status; returns the
+  // status's sequence number
+  auto launch_alpha1 = [&]() -> unsigned {
+    hipLaunchKernelGGL(uniform_denoise_kernel<kPosterior>, eg, eb, 0, stream, w.r1, g1w, pr.W, pr.ldw,
+                       pr.scale, pr.zero, G, pr.group_size, n, pr.maxq, tau, w.x1, w.part, nullptr,
+                       nullptr, nullptr);
+    const unsigned seq = ++mb->seq;
+    hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, n, nchunks, w.part, g1w,
+                       has_prev ? 1 : 0, damping, g2prev, a1raw, a1, eta1, g2new, g2, w.status, mb->dev(seq), seq);
+    return seq;
+  };
+  unsigned ahead_seq = 0;  // the iteration's first denoiser pass, launched at the end of the one before
   for (int it = 0; it < iters; ++it) {
     // ---- denoiser with gamma retries (mpq/solver.py:559-596), from g1w = g1
-    if (!g1w_current) MPQ_HIP_TRY(copy_rows(g1w, 0, g1, 0, 1, rows * 4, stream));
-    g1w_current = true;
+    if (ahead_seq == 0) {
+      if (!g1w_current) MPQ_HIP_TRY(copy_rows(g1w, 0, g1, 0, 1, rows * 4, stream));
+      g1w_current = true;
+    }
     for (int attempt = 0; attempt <= retry_steps; ++attempt) {
-      hipLaunchKernelGGL(uniform_denoise_kernel<kPosterior>, eg, eb, 0, stream, w.r1, g1w, pr.W, pr.ldw,
-                         pr.scale, pr.zero, G, pr.group_size, n, pr.maxq, tau, w.x1, w.part, nullptr,
-                         nullptr, nullptr);
-      const unsigned a1_seq = ++mb->seq;
-      hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, n, nchunks, w.part, g1w,
-                         has_prev ? 1 : 0, damping, g2prev, a1raw, a1, eta1, g2new, g2, w.status, mb->d, a1_seq);
-      MPQ_LAUNCH_CHECK();
+      unsigned a1_seq = ahead_seq;
+      ahead_seq = 0;
+      if (a1_seq == 0) {
+        a1_seq = launch_alpha1();
+        MPQ_LAUNCH_CHECK();
+      }
       if ((rc = wait_status(mb, a1_seq, hs, stream)) != kOk) return rc;
       if (hs->a1_invalid == 0) break;
       if (attempt >= retry_steps) {
@@ -468,6 +481,18 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     MPQ_LAUNCH_CHECK();
     // ---- hard state of the new (r1, g1)
     if ((rc = hard_state(w.r1, g1)) != kOk) return rc;
+    std::swap(w.r2, w.r2prev);  // r2_prev <- r2
+    std::swap(g2, g2prev);      // gamma2_prev <- gamma2
+    has_prev = true;
+    // The next iteration's first denoiser pass reads only device state (r1, gamma1, and gamma2 of
+    // this iteration), so it is queued before this iteration's status is read and the GPU works
+    // through the host's EM and stopping decision.  After a stop its results are never read.
+    if (it + 1 < iters) {
+      if (!g1w_current) MPQ_HIP_TRY(copy_rows(g1w, 0, g1, 0, 1, rows * 4, stream));
+      g1w_current = true;
+      ahead_seq = launch_alpha1();
+      MPQ_LAUNCH_CHECK();
+    }
     if ((rc = wait_status(mb, hard_seq, hs, stream)) != kOk) return rc;
     a2_clip += hs->a2_clip;
     // EM update of the observation precision (mpq/linear.py:59-82), in double like the reference
@@ -483,9 +508,6 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
       beta = std::min(std::max(beta, cfg.em_obs_precision_min), cfg.em_obs_precision_max);
       obs = beta;
     }
-    std::swap(w.r2, w.r2prev);  // r2_prev <- r2
-    std::swap(g2, g2prev);      // gamma2_prev <- gamma2
-    has_prev = true;
     obs_sum += obs;
     a1_sum += a1_mean_it;
     a2_sum += hs->a2_mean;

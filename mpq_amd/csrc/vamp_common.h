@@ -72,10 +72,15 @@ __global__ __launch_bounds__(64) void publish_status_kernel(const VampStatus* __
   if (threadIdx.x == 0) publish_to(src, box, seq);
 }
 
+// Two mailbox slots, used by alternate sequence numbers: a status may be published (seq + 1) while the
+// host has not yet read the one before it (seq), as when a driver launches the next iteration's first
+// row kernel ahead of reading the current one's status.  Every driver waits for status seq before it
+// launches anything that publishes seq + 2, so a slot is never rewritten before it is read.
 struct HostMailbox {
-  StatusMailbox* h = nullptr;  // host view
+  StatusMailbox* h = nullptr;  // host view of the two slots
   StatusMailbox* d = nullptr;  // device view of the same pages
   unsigned seq = 0;
+  StatusMailbox* dev(unsigned s) const { return d + (s & 1u); }
 };
 
 // One mailbox per host thread (allocated once, kept for the thread's lifetime).
@@ -83,10 +88,10 @@ inline HostMailbox* host_mailbox() {
   static thread_local HostMailbox mb;
   if (mb.h == nullptr) {
     StatusMailbox* h = nullptr;
-    if (hipHostMalloc((void**)&h, sizeof(StatusMailbox),
+    if (hipHostMalloc((void**)&h, 2 * sizeof(StatusMailbox),
                       hipHostMallocMapped | hipHostMallocCoherent | hipHostMallocPortable) != hipSuccess)
       return nullptr;
-    std::memset(h, 0, sizeof(StatusMailbox));
+    std::memset(h, 0, 2 * sizeof(StatusMailbox));
     StatusMailbox* d = nullptr;
     if (hipHostGetDevicePointer((void**)&d, h, 0) != hipSuccess) {
       (void)hipHostFree(h);
@@ -103,11 +108,12 @@ inline HostMailbox* host_mailbox() {
 inline int wait_status(HostMailbox* mb, unsigned seq, VampStatus* out, hipStream_t stream) {
   const auto t0 = std::chrono::steady_clock::now();
   unsigned spins = 0;
-  while (__atomic_load_n(&mb->h->seq, __ATOMIC_ACQUIRE) != seq) {
+  const StatusMailbox* box = mb->h + (seq & 1u);
+  while (__atomic_load_n(&box->seq, __ATOMIC_ACQUIRE) != seq) {
     __builtin_ia32_pause();
     if ((++spins & 4095u) == 0 && std::chrono::steady_clock::now() - t0 > std::chrono::seconds(20)) {
       MPQ_HIP_TRY(hipStreamSynchronize(stream));
-      if (__atomic_load_n(&mb->h->seq, __ATOMIC_ACQUIRE) != seq) {
+      if (__atomic_load_n(&box->seq, __ATOMIC_ACQUIRE) != seq) {
         set_error("VAMP status handshake: the status kernel completed but its sequence number did not arrive");
         set_error_code(kHipError);
         return kHipError;
@@ -115,14 +121,14 @@ inline int wait_status(HostMailbox* mb, unsigned seq, VampStatus* out, hipStream
       break;
     }
   }
-  std::memcpy(out, &mb->h->st, sizeof(VampStatus));
+  std::memcpy(out, &box->st, sizeof(VampStatus));
   return kOk;
 }
 
 // Copy the device status to *out once every earlier operation on `stream` has completed.
 inline int read_status(HostMailbox* mb, const VampStatus* dstatus, VampStatus* out, hipStream_t stream) {
   const unsigned seq = ++mb->seq;
-  hipLaunchKernelGGL(publish_status_kernel, dim3(1), dim3(64), 0, stream, dstatus, mb->d, seq);
+  hipLaunchKernelGGL(publish_status_kernel, dim3(1), dim3(64), 0, stream, dstatus, mb->dev(seq), seq);
   MPQ_LAUNCH_CHECK();
   return wait_status(mb, seq, out, stream);
 }
