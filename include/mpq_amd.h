@@ -489,13 +489,17 @@ int mpq_uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows,
 /*
  * mpq_uniform_cd_polish with the start's product x Vs from the caller (xprod_in, rows x n,
  * contiguous; optional): mpq_uniform_vamp_solve_ex returns it for its codes, so the polish skips
- * that product (the reference recomputes it, mpq/solver.py:283-290).
+ * that product (the reference recomputes it, mpq/solver.py:283-290).  With S (n singular values,
+ * Vs = V diag(S)) and the packed rank-space operator (mpq_rankspace_pack; both optional, n % 128
+ * == 0) its two full products (rhs = residual Vs^T, final x Vs; mpq/solver.py:291-330) run as
+ * fp32-accurate bf16-plane products on the matrix cores.
  */
 int mpq_uniform_cd_polish_ex(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
                              float accept_tol, const float* W, int64_t ldw, const float* Yu,
                              const uint8_t* q_in, const float* x_in, const float* xprod_in,
                              const float* scale, const float* zero, int64_t group_size,
-                             const float* Vs, const float* H, int select, uint8_t* q_out,
+                             const float* Vs, const float* S, const float* packed, const float* H,
+                             int select, uint8_t* q_out,
                              float* err_before, float* err_after, int32_t* improved,
                              int32_t* accepted_per_row, void* workspace, int64_t workspace_bytes,
                              mpq_stream_t stream);

@@ -90,7 +90,8 @@ SIGNATURES = {
     "mpq_rankspace_pack_floats": (c_i64, [c_i64]),
     "mpq_rankspace_pack": (c_int, [c_i64, c_ptr, c_ptr, c_ptr, c_ptr]),
     "mpq_uniform_cd_polish_ex": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_float, c_ptr, c_i64, c_ptr,
-                                         c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_int, c_ptr,
+                                         c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr,
+                                         c_int, c_ptr,
                                          c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
 }
 

@@ -274,7 +274,7 @@ def run_mpq_quantization(
         if bool(getattr(vamp_cfg, "em_obs_precision", True)):
             obs_block = float(st["obs_precision_final"])
         block_stats.append(st)
-    del ws, XR_all, packed
+    del ws, XR_all
     torch.cuda.synchronize(device)
     timings["vamp_s"] = time.time() - t_solve
 
@@ -288,7 +288,8 @@ def run_mpq_quantization(
     if mode == "block_cd":
         q_pol, eb, ea, imp, acc = ops.uniform_cd_polish(None, q_int, scale_groups, zero_groups, group_size, maxq,
                                                         Vs, H_metric, block_rows=block_rows, sweeps=sweeps,
-                                                        select=True, Yu=Yu_all, xprod=XP_all)
+                                                        select=True, Yu=Yu_all, xprod=XP_all,
+                                                        S=None if packed is None else S, packed=packed)
         final_err = torch.where(imp.bool(), ea, err_vamp)
         changed = int((q_pol != q_int).sum().item())
         q_int = q_pol
@@ -297,6 +298,7 @@ def run_mpq_quantization(
         final_err = err_vamp
     torch.cuda.synchronize(device)
     timings["polish_s"] = time.time() - t_pol
+    del packed
 
     Q_work = ops.dequant(q_int, scale_groups, zero_groups, group_size)
     delta = W_work - Q_work

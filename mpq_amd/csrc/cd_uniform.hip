@@ -178,6 +178,8 @@ inline int64_t a64(int64_t v) { return (v + 63) / 64 * 64; }
 struct CdPlan {
   int64_t rows, n, nblocks, nchunks;
   int splits, bn;
+  int splits_x6;    // split count of the x6 products (0: shape not supported)
+  int64_t ap_bytes;  // packed bf16 planes of their left operand
   int64_t bytes;
 };
 
@@ -190,10 +192,13 @@ CdPlan cd_plan(int64_t rows, int64_t n, int64_t block_rows) {
   int bn = 128;
   c.splits = choose_splits(rows, n, n, (int64_t)1 << 62, &bn);
   c.bn = bn;
+  c.splits_x6 = x6_shape_ok(n, n) ? x6_choose_splits(rows, n, n) : 0;
+  c.ap_bytes = c.splits_x6 > 0 ? (x6_packed_a_bytes(rows, n) + 255) / 256 * 256 : 0;
   const int64_t mat = a64(rows * n) * 4;
   int64_t b = 0;
   b += 4 * mat;                               // Yu, x, res/rhs-scratch, rhs
-  b += (int64_t)c.splits * mat;               // partials
+  b += (int64_t)std::max(c.splits, c.splits_x6) * mat;  // partials
+  b += c.ap_bytes;                            // x6 planes of the left operand
   b += a64(rows * n);                         // q work (u8)
   b += 3 * a64(n) * 4;                        // diag, diag_inv, spare
   b += a64(c.nblocks * n) * 4 * 2;            // gain + order
@@ -228,7 +233,7 @@ int uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows, int
                       const float* H, int select, uint8_t* q_out, float* err_before_out,
                       float* err_after_out, int32_t* improved, int32_t* accepted_per_row,
                       void* workspace, int64_t workspace_bytes, hipStream_t stream,
-                      const float* xprod_in = nullptr) {
+                      const float* xprod_in = nullptr, const float* S = nullptr, const float* packed = nullptr) {
   const CdPlan pl = cd_plan(rows, n, block_rows);
   MPQ_CHECK_ARG(workspace_bytes >= pl.bytes, "uniform CD: workspace too small (%lld < %lld bytes)",
                 (long long)workspace_bytes, (long long)pl.bytes);
@@ -239,7 +244,10 @@ int uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows, int
   float* x = (float*)p; p += mat;
   float* scratch = (float*)p; p += mat;
   float* rhs = (float*)p; p += mat;
-  float* P = (float*)p; p += (int64_t)pl.splits * mat;
+  float* P = (float*)p; p += (int64_t)std::max(pl.splits, pl.splits_x6) * mat;
+  void* Ap = p; p += pl.ap_bytes;
+  // the two full products on the packed rank-space operator (V | V^T | Vs, x6 products) when given
+  const bool x6 = packed != nullptr && S != nullptr && pl.splits_x6 > 0;
   uint8_t* qw = (uint8_t*)p; p += a64(rows * n);
   float* diag = (float*)p; p += a64(n) * 4;
   float* diag_inv = (float*)p; p += a64(n) * 4;
@@ -290,9 +298,15 @@ int uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows, int
   MPQ_LAUNCH_CHECK();
   MPQ_HIP_TRY(hipMemcpyAsync(res_norm, err_b, rows * 4, hipMemcpyDeviceToDevice, stream));
   MPQ_HIP_TRY(hipMemsetAsync(acc, 0, rows * 4, stream));
-  // rhs = residual Vs^T ; diag = |Vs_j|^2
-  MPQ_HIP_TRY(product_splits(scratch, Vs, true, rows, n, P, pl.splits, pl.bn, stream));
-  MPQ_HIP_TRY(splitk_reduce(P, pl.splits, rows, n, rhs, n, 1.f, 0.f, stream));
+  // rhs = residual Vs^T (x6: (residual diag(S)) V^T, Vs = V diag(S)); diag = |Vs_j|^2
+  if (x6) {
+    MPQ_HIP_TRY(x6_pack_a(scratch, n, rows, n, Ap, stream, S));
+    MPQ_HIP_TRY(x6_gemm_partials(Ap, packed + n * n, rows, n, n, P, n, sstride, pl.splits_x6, stream));
+    MPQ_HIP_TRY(splitk_reduce(P, pl.splits_x6, rows, n, rhs, n, 1.f, 0.f, stream));
+  } else {
+    MPQ_HIP_TRY(product_splits(scratch, Vs, true, rows, n, P, pl.splits, pl.bn, stream));
+    MPQ_HIP_TRY(splitk_reduce(P, pl.splits, rows, n, rhs, n, 1.f, 0.f, stream));
+  }
   MPQ_HIP_TRY(row_sqnorm(Vs, n, n, 1e-12f, diag, stream));
   hipLaunchKernelGGL(recip_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, n, diag, diag_inv);
   MPQ_LAUNCH_CHECK();
@@ -338,9 +352,14 @@ int uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows, int
   }
   // error after the polish, from the final codes (mpq/solver.py:323-330)
   MPQ_HIP_TRY(dequant_groups(qw, scale, zero, G, gs, rows, n, x, stream));
-  MPQ_HIP_TRY(product_splits(x, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
-  hipLaunchKernelGGL(residual_kernel, eg, dim3(256), 0, stream, rows, n, P, pl.splits, sstride, Yu,
-                     (float*)nullptr, part, nchunks);
+  if (x6) {
+    MPQ_HIP_TRY(x6_pack_a(x, n, rows, n, Ap, stream));
+    MPQ_HIP_TRY(x6_gemm_partials(Ap, packed + 2 * n * n, rows, n, n, P, n, sstride, pl.splits_x6, stream));
+  } else {
+    MPQ_HIP_TRY(product_splits(x, Vs, false, rows, n, P, pl.splits, pl.bn, stream));
+  }
+  hipLaunchKernelGGL(residual_kernel, eg, dim3(256), 0, stream, rows, n, P, x6 ? pl.splits_x6 : pl.splits, sstride,
+                     Yu, (float*)nullptr, part, nchunks);
   hipLaunchKernelGGL(rows_sum_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, rows,
                      nchunks, part, err_a);
   MPQ_LAUNCH_CHECK();
@@ -377,15 +396,16 @@ extern "C" int mpq_uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t 
                                      int32_t* accepted_per_row, void* workspace, int64_t workspace_bytes,
                                      hipStream_t stream) {
   return mpq_uniform_cd_polish_ex(rows, n, maxq, block_rows, sweeps, accept_tol, W, ldw, Yu, q_in, x_in, nullptr,
-                                  scale, zero, group_size, Vs, H, select, q_out, err_before, err_after, improved,
-                                  accepted_per_row, workspace, workspace_bytes, stream);
+                                  scale, zero, group_size, Vs, nullptr, nullptr, H, select, q_out, err_before,
+                                  err_after, improved, accepted_per_row, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mpq_uniform_cd_polish_ex(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
                                         float accept_tol, const float* W, int64_t ldw, const float* Yu,
                                         const uint8_t* q_in, const float* x_in, const float* xprod_in,
                                         const float* scale, const float* zero, int64_t group_size,
-                                        const float* Vs, const float* H, int select, uint8_t* q_out,
+                                        const float* Vs, const float* S, const float* packed, const float* H,
+                                        int select, uint8_t* q_out,
                                         float* err_before, float* err_after, int32_t* improved,
                                         int32_t* accepted_per_row, void* workspace, int64_t workspace_bytes,
                                         hipStream_t stream) {
@@ -399,5 +419,5 @@ extern "C" int mpq_uniform_cd_polish_ex(int64_t rows, int64_t n, int maxq, int64
   MPQ_CHECK_ARG(!W || ldw >= n, "mpq_uniform_cd_polish: ldw < n");
   return mpq::uniform_cd_polish(rows, n, maxq, block_rows, sweeps, accept_tol, W, ldw, Yu, q_in, x_in, scale, zero,
                                 group_size, Vs, H, select, q_out, err_before, err_after, improved,
-                                accepted_per_row, workspace, workspace_bytes, stream, xprod_in);
+                                accepted_per_row, workspace, workspace_bytes, stream, xprod_in, S, packed);
 }

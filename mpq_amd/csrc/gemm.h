@@ -63,7 +63,9 @@ bool x6_shape_ok(int64_t N, int64_t K);
 int x6_choose_splits(int64_t M, int64_t N, int64_t K);
 int64_t x6_packed_a_bytes(int64_t M, int64_t K);
 hipError_t x6_pack_b(const float* B, int64_t ldb, bool trans_b, int64_t K, int64_t N, float* Bt, hipStream_t stream);
-hipError_t x6_pack_a(const float* A, int64_t lda, int64_t M, int64_t K, void* At, hipStream_t stream);
+// colscale (optional, K floats): pack the planes of A diag(colscale) instead of A.
+hipError_t x6_pack_a(const float* A, int64_t lda, int64_t M, int64_t K, void* At, hipStream_t stream,
+                     const float* colscale = nullptr);
 // C[s] = A[:, K slice s] * op(B)[K slice s, :] for s < splits (K / splits a multiple of 32),
 // C[s] at C + s * split_stride with row stride ldc.
 hipError_t x6_gemm_partials(const void* At, const float* Bt, int64_t M, int64_t N, int64_t K, float* C, int64_t ldc,

@@ -505,8 +505,9 @@ __global__ void x6_pack_b_kernel(const float* __restrict__ B, int64_t ldb, int64
   }
 }
 
-// A planes: thread per chunk; rows >= M are zero.
-__global__ void x6_pack_a_kernel(const float* __restrict__ A, int64_t lda, int64_t M, int64_t K, uint4* __restrict__ At) {
+// A planes (of A diag(colscale) when colscale is given): thread per chunk; rows >= M are zero.
+__global__ void x6_pack_a_kernel(const float* __restrict__ A, int64_t lda, int64_t M, int64_t K, uint4* __restrict__ At,
+                                 const float* __restrict__ colscale) {
   const int64_t KS = K / 16;
   const int64_t nchunks = ((M + 127) / 128) * KS * 256;
   for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < nchunks; q += (int64_t)gridDim.x * blockDim.x) {
@@ -519,6 +520,10 @@ __global__ void x6_pack_a_kernel(const float* __restrict__ A, int64_t lda, int64
       const float* src = A + m * lda + k0;
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = src[e];
+      if (colscale) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] *= colscale[k0 + e];
+      }
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = 0.f;
@@ -869,9 +874,11 @@ hipError_t x6_pack_b(const float* B, int64_t ldb, bool trans_b, int64_t K, int64
   return hipGetLastError();
 }
 
-hipError_t x6_pack_a(const float* A, int64_t lda, int64_t M, int64_t K, void* At, hipStream_t stream) {
+hipError_t x6_pack_a(const float* A, int64_t lda, int64_t M, int64_t K, void* At, hipStream_t stream,
+                     const float* colscale) {
   const unsigned g = grid_for(((M + 127) / 128) * (K / 16) * 256);
-  hipLaunchKernelGGL(x6_pack_a_kernel, dim3(g), dim3(256), 0, stream, A, lda, M, K, static_cast<uint4*>(At));
+  hipLaunchKernelGGL(x6_pack_a_kernel, dim3(g), dim3(256), 0, stream, A, lda, M, K, static_cast<uint4*>(At),
+                     colscale);
   return hipGetLastError();
 }
 

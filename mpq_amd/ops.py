@@ -364,10 +364,15 @@ def uniform_vamp_solve(W, x_init, scale, zero, group_size, maxq, V, S, Vs, cfg, 
 
 def uniform_cd_polish(W, q_in, scale, zero, group_size, maxq, Vs, H, *, block_rows: int, sweeps: int,
                       accept_tol: float = 0.0, select: bool = True, Yu=None, x_in=None, xprod=None,
-                      ws: Optional[torch.Tensor] = None):
+                      S=None, packed=None, ws: Optional[torch.Tensor] = None):
     """Greedy scalar CD over all rows (greedy order per row block).  ``W`` may be None when ``Yu``
-    is given; ``xprod`` (optional) is the start's x Vs.  Returns (q, err_before, err_after, improved,
-    accepted_per_row)."""
+    is given; ``xprod`` (optional) is the start's x Vs.  ``S`` with ``packed`` (``rankspace_pack``,
+    n % 128 == 0) runs the two full products as x6 products.  Returns (q, err_before, err_after,
+    improved, accepted_per_row)."""
+    if (S is None) != (packed is None):
+        raise ValueError("uniform_cd_polish: S and packed go together")
+    if packed is not None and packed.numel() != 3 * Vs.shape[0] * Vs.shape[0]:
+        raise ValueError("uniform_cd_polish: packed must hold 3 n^2 floats (rankspace_pack)")
     dev = _dev(q_in, scale, zero, Vs, H, W, Yu, x_in, xprod)
     W = None if W is None else _f32c(W)
     Yu = None if Yu is None else _f32c(Yu)
@@ -386,7 +391,8 @@ def uniform_cd_polish(W, q_in, scale, zero, group_size, maxq, Vs, H, *, block_ro
     _lib.call("mpq_uniform_cd_polish_ex", rows, n, int(maxq), int(block_rows), int(sweeps), float(accept_tol),
               _lib.ptr(W), n, _lib.ptr(Yu), _lib.ptr(q_in.to(torch.uint8).contiguous()), _lib.ptr(x_in),
               _lib.ptr(xprod), _lib.ptr(_f32c(scale)),
-              _lib.ptr(_f32c(zero)), int(group_size), _lib.ptr(_f32c(Vs)), _lib.ptr(_f32c(H)), int(bool(select)),
+              _lib.ptr(_f32c(zero)), int(group_size), _lib.ptr(_f32c(Vs)),
+              _lib.ptr(None if S is None else _f32c(S)), _lib.ptr(packed), _lib.ptr(_f32c(H)), int(bool(select)),
               _lib.ptr(q_out), _lib.ptr(eb), _lib.ptr(ea), _lib.ptr(imp), _lib.ptr(acc), _lib.ptr(ws),
               int(ws.numel()), _stream(dev))
     return q_out, eb, ea, imp, acc

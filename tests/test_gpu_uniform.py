@@ -194,6 +194,28 @@ def test_cd_polish_matches_oracle(gpu):
     assert float((q2.cpu() == q[128:].cpu()).float().mean()) >= 0.999
 
 
+def test_cd_polish_x6_products_match_oracle(gpu):
+    # the polish's two full products (rhs = residual Vs^T as (residual diag(S)) V^T, final x Vs) on
+    # the packed rank-space operator: same codes as the oracle and as the fp32-kernel polish
+    W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq = _setup_block(256, 512, 4, 128, "cd6")
+    q0 = torch.clamp(torch.round(W / sf) + zf, 0, maxq).to(torch.uint8)
+    Y_u = W @ Vs
+    x_pol, _ = ou.scalar_greedy_cd(xr[:128], Y_u[:128], Vs, Hw, sf[:128], zf[:128], maxq, 3)
+    q_ref = ou.nearest_atom_idx(x_pol, sf[:128], zf[:128], maxq)
+    Vg, Sg, Vsg = V.to(gpu), S.to(gpu), Vs.to(gpu)
+    pk = ops.rankspace_pack(Vg, Vsg)
+    args = (W.to(gpu), q0.to(gpu), sg.to(gpu), zg.to(gpu), 128, maxq, Vsg, Hw.to(gpu))
+    q, eb, ea, imp, acc = ops.uniform_cd_polish(*args, block_rows=128, sweeps=3, select=False, S=Sg, packed=pk)
+    assert float((q[:128].cpu().long() == q_ref.long()).float().mean()) >= 0.999
+    err_ref = ou.rankspace_error(Y_u[:128], ou.dequant_from_q(q_ref, sf[:128], zf[:128]), Vs)
+    assert abs(float(ea[:128].mean()) - float(err_ref.mean())) <= 1e-3 * float(err_ref.mean())
+    q32, eb32, ea32, _, _ = ops.uniform_cd_polish(*args, block_rows=128, sweeps=3, select=False)
+    assert float((q == q32).float().mean()) >= 0.999
+    assert _rel(eb.cpu(), eb32.cpu()) < 1e-4 and _rel(ea.cpu(), ea32.cpu()) < 1e-4
+    with pytest.raises(ValueError):
+        ops.uniform_cd_polish(*args, block_rows=128, sweeps=3, select=False, S=Sg)
+
+
 @pytest.mark.parametrize("rotation,bits,x6", [("none", 4, False), ("internal_hadamard", 4, False), ("none", 3, False),
                                               ("internal_hadamard", 3, False), ("internal_hadamard", 4, True),
                                               ("none", 3, True)])
