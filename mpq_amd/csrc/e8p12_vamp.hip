@@ -177,13 +177,16 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
   };
   int rc;
   // MAP decision of (r, g) into midx / mvals and its rank-space error into errrow / status.err_mean
-  auto map_state = [&](const float* r, const float* g) -> int {
+  // MAP decision of (r, g) and its rank-space error; with pub_seq != 0 the error row kernel also
+  // publishes the status under that sequence number
+  auto map_state = [&](const float* r, const float* g, unsigned pub_seq = 0u) -> int {
     int e = mpq_e8p12_map(r, rows * nb, g, nb, center, prior_scale, tau, midx, nullptr, mvals, nullptr, nullptr,
                           stream);
     if (e != kOk) return e;
     MPQ_HIP_TRY(prod(mvals, Vs, false, 2));
     hipLaunchKernelGGL(err_epi_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, Yu, part, nullptr);
-    hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, part, errrow, status, nullptr, 0u);
+    hipLaunchKernelGGL(rows_err_kernel, dim3(1), eb, 0, stream, rows, nchunks, part, errrow, status,
+                       pub_seq ? mb->dev(pub_seq) : nullptr, pub_seq);
     MPQ_LAUNCH_CHECK();
     return kOk;
   };
@@ -292,12 +295,13 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
     hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, r2, eta2, g2, g1new, damping,
                        r1);
     MPQ_LAUNCH_CHECK();
-    if (best_iterate) {
-      if ((rc = map_state(r1, g1)) != kOk) return rc;
-    }
     const unsigned st_seq = ++mb->seq;
-    hipLaunchKernelGGL(publish_status_kernel, dim3(1), dim3(64), 0, stream, status, mb->dev(st_seq), st_seq);
-    MPQ_LAUNCH_CHECK();
+    if (best_iterate) {
+      if ((rc = map_state(r1, g1, st_seq)) != kOk) return rc;
+    } else {
+      hipLaunchKernelGGL(publish_status_kernel, dim3(1), dim3(64), 0, stream, status, mb->dev(st_seq), st_seq);
+      MPQ_LAUNCH_CHECK();
+    }
     std::swap(r2, r2prev);
     std::swap(g2, g2prev);
     has_prev = true;
