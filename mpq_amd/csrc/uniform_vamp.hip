@@ -529,6 +529,12 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     }
   }
 
+  // a stop leaves the look-ahead pass queued: wait for its status, so that no publish to the
+  // mailbox is outstanding when this call returns (a later call may run on another stream)
+  if (ahead_seq != 0) {
+    VampStatus unused;
+    if ((rc = wait_status(mb, ahead_seq, &unused, stream)) != kOk) return rc;
+  }
   // ---- outputs
   MPQ_HIP_TRY(copy_rows(q_out, 0, w.q_best, 0, 1, rows * n, stream));
   if (err_out) MPQ_HIP_TRY(copy_rows(err_out, 0, err_best, 0, 1, rows * 4, stream));
