@@ -487,6 +487,28 @@ int mpq_uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows,
                           mpq_stream_t stream);
 
 /*
+ * The greedy sweeps alone, in place on caller state: replaces the persistent
+ * sweep launch of mpq/polish/triton_scalar_cd.py:113-161
+ * (_launch_persistent_scalar_cd_sweep, which takes rhs_all, x_work,
+ * residual_norm, order, gram and diag) together with the per-sweep greedy
+ * order of :241-243.  Per row block of block_rows rows: gain_j = (sum over the
+ * block's rows, in row order, of rhs^2 * (1/diag_j)) / rows_in_block, stable
+ * descending order, then the column-at-a-time decisions and rank-1 updates
+ * rhs -= delta * H[col, :] (product rounded, then difference rounded).
+ *   rhs, x: rows x n fp32 (in/out); q: rows x n uint8 codes (in/out);
+ *   res_norm: rows (in/out); accepted: rows int32, incremented by the number
+ *   of accepted moves; scale/zero: rows x ceil(n/group_size); diag: n
+ *   (|Vs_j|^2, already floored); H: n x n.
+ * workspace: mpq_uniform_cd_sweeps_workspace_size(rows, n, block_rows) bytes.
+ */
+int64_t mpq_uniform_cd_sweeps_workspace_size(int64_t rows, int64_t n, int64_t block_rows);
+int mpq_uniform_cd_sweeps(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                          float accept_tol, float* rhs, float* x, uint8_t* q, float* res_norm,
+                          int32_t* accepted, const float* scale, const float* zero,
+                          int64_t group_size, const float* diag, const float* H, void* workspace,
+                          int64_t workspace_bytes, mpq_stream_t stream);
+
+/*
  * mpq_uniform_cd_polish with the start's product x Vs from the caller (xprod_in, rows x n,
  * contiguous; optional): mpq_uniform_vamp_solve_ex returns it for its codes, so the polish skips
  * that product (the reference recomputes it, mpq/solver.py:283-290).  With S (n singular values,

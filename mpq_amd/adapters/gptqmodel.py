@@ -359,6 +359,53 @@ def run_mpq_quantization(
     return Q, q_int, scale_groups, zero_groups, g_idx, float(quant_time), stats
 
 
+@torch.inference_mode()
+def prepare_gptq_internal_hadamard(
+    *,
+    W: torch.Tensor,
+    H: torch.Tensor,
+    qcfg: Any,
+    module_name: str,
+    adapter_cfg: GPTQAdapterConfig = GPTQAdapterConfig(),
+) -> Tuple[torch.Tensor, torch.Tensor, Dict[str, Any]]:
+    """Rotate a linear into the internal block-Hadamard basis before GPTQModel's own solver (reference
+    mpq/adapters/gptqmodel.py:593-632, called from the GPTQ hook when ``solver="gptq"`` runs with
+    ``rotation_mode="internal_hadamard"``): ``W_work = W diag(signs) Had``, ``H_work`` rotated on both
+    sides, and the rotation plan for ``finalize_gptq_internal_hadamard``.  Without an internal
+    rotation W and H are returned as fp32.  The reference's optional file-backed paired (W, H) cache
+    (``qcfg.mpq.paired_matrix_cache_dir``) is not provided: setting it raises ValueError."""
+    mpq_cfg = getattr(qcfg, "mpq", None)
+    if getattr(mpq_cfg, "paired_matrix_cache_dir", None):
+        raise ValueError("mpq_amd does not provide the file-backed paired matrix cache (paired_matrix_cache_dir).")
+    if float(adapter_cfg.hessian_scale) <= 0.0:
+        raise ValueError(f"hessian_scale must be positive, got {float(adapter_cfg.hessian_scale)}")
+    requested = getattr(mpq_cfg, "rotation_mode", getattr(qcfg, "rotation", None) or "none")
+    plan = resolve_internal_rotation(requested=str(requested), cols=int(W.shape[1]), module_name=str(module_name),
+                                     seed=int(adapter_cfg.rotation_seed), device=W.device)
+    W32 = W.to(dtype=torch.float32).contiguous()
+    H32 = H.to(dtype=torch.float32).contiguous()
+    if not bool(plan["internal"]):
+        return W32, H32, plan
+    had, signs = int(plan["block_dim"]), plan["signs"]
+    W_work = apply_right_block_hadamard(W32, signs=signs, had_dim=had)
+    H_work = apply_right_block_hadamard(apply_left_block_hadamard(H32, signs=signs, had_dim=had), signs=signs,
+                                        had_dim=had)
+    # the reference stores the scaled Hessian and divides the scale back out (exact for the default 0.5)
+    hs = float(adapter_cfg.hessian_scale)
+    H_work = (hs * H_work) / hs
+    return W_work.contiguous(), H_work.contiguous(), plan
+
+
+@torch.inference_mode()
+def finalize_gptq_internal_hadamard(*, Q_work: torch.Tensor, rotation_plan: Dict[str, Any]) -> torch.Tensor:
+    """Rotate a result back to the original basis (reference mpq/adapters/gptqmodel.py:635-647)."""
+    if not bool(rotation_plan.get("internal", False)):
+        return Q_work.to(dtype=torch.float32).contiguous()
+    return apply_right_block_hadamard_inverse(Q_work.to(dtype=torch.float32).contiguous(),
+                                              signs=rotation_plan["signs"],
+                                              had_dim=int(rotation_plan["block_dim"])).contiguous()
+
+
 def install_internal_hadamard_input_hooks(model: torch.nn.Module, *, rotation_seed: int = 0) -> int:
     """Forward pre-hooks that rotate each packed module's input into the solver basis
     (reference ``mpq/adapters/gptqmodel.py:1166-1247``).

@@ -30,6 +30,7 @@ from typing import Any, Dict, Optional, Tuple
 import torch
 
 from .. import ops
+from ..codebook import require_standin_table
 from ..solver import E8P12VampConfig, _resolve_e8p12_polish_metric, _resolve_polish_mode
 from ..priors.e8p12 import prior_scale_from_center
 from ..utils import stable_seed
@@ -203,6 +204,7 @@ def mpq_refine_codebook(
     nblocks = n // 8
     if hasattr(cb, "grid") and cb.grid.device != device:
         cb = cb.to(device) if hasattr(cb, "to") else cb
+    require_standin_table(cb, "mpq_refine_codebook")
     timings: Dict[str, float] = {}
 
     init_mode = str(getattr(args, "mpq_init", "rtn") or "rtn").strip().lower()

@@ -99,6 +99,33 @@ def index_of(branch: int, k: int, sign_id: int) -> int:
     return (int(k) << 8) | (int(sign_id) ^ (((int(branch) ^ int(base_parity()[k])) & 1) << 7))
 
 
+_GRID_ON: dict = {}
+
+
+def require_standin_table(cb, where: str) -> None:
+    """Raise ValueError unless ``cb`` is None or its ``grid`` equals, element by element, the table
+    compiled into libmpq_amd (``grid_numpy()``).  The kernels search that table and emit its index
+    layout, so a codebook with another table (quip-sharp's real ``E8P12_codebook``) would mix two
+    layouts: refused until its table is swapped in here and the library is rebuilt."""
+    if cb is None:
+        return
+    import torch
+
+    grid = getattr(cb, "grid", None)
+    if grid is None:
+        raise ValueError(f"{where}: the codebook object has no `grid`")
+    g = torch.as_tensor(grid)
+    key = str(g.device)
+    ref = _GRID_ON.get(key)
+    if ref is None:
+        ref = _GRID_ON[key] = torch.from_numpy(grid_numpy()).to(g.device)
+    if tuple(g.shape) != tuple(ref.shape) or not torch.equal(g.to(torch.float32), ref):
+        raise ValueError(
+            f"{where}: cb.grid differs from the E8P12 table compiled into libmpq_amd (the documented "
+            "stand-in table of mpq_amd/codebook.py; QUIP#'s own table is not available to this build). "
+            "Swap QUIP#'s table into ABS2_TABLE and rebuild before passing this codebook.")
+
+
 class E8P12_codebook:  # noqa: N801 - class name is part of the reference protocol
     """Codebook object with the protocol the reference consumes.
 

@@ -13,10 +13,16 @@
 // Blocking: columns are taken in windows of 128 consecutive positions of the
 // greedy order.  Inside a window one wave64 per row runs the 128 sequential
 // decisions with the window's H sub-block in LDS (rank-1 updates of the window's
-// own rhs entries); after the window the deferred update of every column,
-// rhs -= Delta(rows x 128) H[window, :], is one fp32 MFMA GEMM with a per-block
-// row gather.  Only the rounding order of the rhs updates differs from the
-// column-at-a-time reference.
+// own rhs entries in registers); after the window the deferred update of every
+// column, rhs[r, j] -= delta[r, p] * H[order[p], j] for p = 0 .. 127 in window
+// order, runs on the VALU as a sequential multiply-then-subtract chain per
+// entry (schur_valu_kernel), which is exactly the per-column update order and
+// rounding of the reference's sweep (its torch twin,
+// mpq/polish/triton_scalar_cd.py:258-288).  Steps whose delta is zero for
+// every row of a 16-row tile are skipped (subtracting 0 * h leaves rhs as is).
+// The greedy gain is summed over the block's rows in row order.  From the same
+// rhs, x, codes and residual norms, a sweep here is bit-identical to the
+// column-at-a-time restatement (mpq_uniform_cd_sweeps).
 #include <algorithm>
 
 #include "cd_common.h"
@@ -155,6 +161,131 @@ __global__ void recip_kernel(int64_t n, const float* __restrict__ a, float* __re
     out[j] = 1.0f / a[j];
 }
 
+constexpr int kSRows = 16;    // rows per work-group of the deferred update
+constexpr int kSCols = 1024;  // columns per work-group (4 waves x 64 lanes x 4 columns)
+
+// Deferred update after a window: rhs[r, j] -= delta[r, p] * H[order[p], j], p = 0 .. wn-1 in order,
+// one rounding for the product and one for the difference (as the reference's column-at-a-time
+// update).  Work-group = 16 rows of one row block x 1024 columns; lane = 4 consecutive columns.
+// Work-groups are numbered so that the tiles sharing one block's window rows of H land on one XCD.
+template <bool kVec>
+__device__ __forceinline__ void load4(const float* __restrict__ row, int64_t c, int64_t n, float (&v)[4]) {
+  if (kVec) {  // n % 4 == 0 and c <= n - 4
+    const float4 t = *reinterpret_cast<const float4*>(row + c);
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = row[c + i < n ? c + i : n - 1];
+  }
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(256) void schur_valu_kernel(int64_t rows, int64_t n, int64_t block_rows,
+                                                         int64_t rtiles, int64_t ctiles,
+                                                         const int32_t* __restrict__ order, int64_t w0,
+                                                         int wn, const float* __restrict__ delta,
+                                                         const float* __restrict__ H,
+                                                         float* __restrict__ rhs) {
+  __shared__ float dT[(kWin + 1) * kSRows];  // [p][r]; slot kWin is all zero (padding steps)
+  __shared__ int plist[kWin + 8];
+  __shared__ int64_t hoff[kWin + 8];
+  __shared__ unsigned long long masks[2];
+  // XCD-aware tile numbering: hardware work-group i runs on XCD i % 8
+  const int64_t total = (int64_t)gridDim.x;
+  const int64_t per = total / 8;
+  const int64_t id = blockIdx.x;
+  const int64_t logical = id < per * 8 ? (id % 8) * per + id / 8 : id;
+  const int64_t rt = logical % rtiles;
+  const int64_t ct = (logical / rtiles) % ctiles;
+  const int64_t blk = logical / (rtiles * ctiles);
+  const int64_t r0 = blk * block_rows + rt * kSRows;
+  int64_t rend = (blk + 1) * block_rows;
+  if (rend > rows) rend = rows;
+  const int nr = (int)(rend - r0 < kSRows ? rend - r0 : kSRows);
+  if (nr <= 0) return;  // uniform over the work-group
+
+  const int t = threadIdx.x;
+  for (int e = t; e < (kWin + 1) * kSRows; e += 256) {
+    const int r = e % kSRows, p = e / kSRows;
+    dT[e] = (r < nr && p < wn) ? delta[(r0 + r) * kWin + p] : 0.f;
+  }
+  __syncthreads();
+  bool active = false;
+  if (t < kWin) {
+#pragma unroll
+    for (int r = 0; r < kSRows; ++r) active |= dT[t * kSRows + r] != 0.f;
+  }
+  const unsigned long long m = __ballot(active);
+  if (t < kWin && (t & 63) == 0) masks[t >> 6] = m;
+  __syncthreads();
+  const unsigned long long m0 = masks[0], m1 = masks[1];
+  const int nact = __popcll(m0) + __popcll(m1);
+  if (nact == 0) return;  // uniform
+  const int nact4 = (nact + 3) & ~3;
+  if (t < kWin && active) {
+    const int pos = t < 64 ? __popcll(m0 & ((1ull << t) - 1ull))
+                           : __popcll(m0) + __popcll(m1 & ((1ull << (t - 64)) - 1ull));
+    plist[pos] = t;
+    hoff[pos] = (int64_t)order[blk * n + w0 + t] * n;
+  }
+  if (t >= nact && t < nact4 + 4) {  // padding steps (and the prefetch past the end): zero deltas, row 0 of H
+    plist[t] = kWin;
+    hoff[t] = 0;
+  }
+  __syncthreads();
+
+  const int lane = t & 63, wave = t >> 6;
+  const int64_t c0 = ct * kSCols + wave * 256 + lane * 4;
+  const bool live = c0 < n;
+  const int64_t cl = kVec ? (live ? c0 : n - 4) : (live ? c0 : n - 1);  // in-bounds column for idle lanes
+  float a[kSRows][4];
+#pragma unroll
+  for (int r = 0; r < kSRows; ++r) {
+    if (r < nr) {
+      load4<kVec>(rhs + (r0 + r) * n, cl, n, a[r]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[r][i] = 0.f;
+    }
+  }
+  float hc[4][4], hn[4][4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) load4<kVec>(H + hoff[u], cl, n, hc[u]);
+  for (int k = 0; k < nact4; k += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load4<kVec>(H + hoff[k + 4 + u], cl, n, hn[u]);  // next group (row 0 past the end)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float* dp = dT + plist[k + u] * kSRows;
+#pragma unroll
+      for (int r = 0; r < kSRows; ++r) {
+        const float d = dp[r];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[r][i] = a[r][i] - d * hc[u][i];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hc[u][i] = hn[u][i];
+    }
+  }
+  if (!live) return;
+#pragma unroll
+  for (int r = 0; r < kSRows; ++r) {
+    if (r < nr) {
+      float* dst = rhs + (r0 + r) * n + c0;
+      if (kVec) {
+        *reinterpret_cast<float4*>(dst) = make_float4(a[r][0], a[r][1], a[r][2], a[r][3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (c0 + i < n) dst[i] = a[r][i];
+      }
+    }
+  }
+}
+
 // q_out = improved ? q_pol : q_in; err_out likewise (mpq/solver.py:749-754).
 __global__ void select_kernel(int64_t rows, int64_t n, const uint8_t* __restrict__ q_in,
                               const uint8_t* __restrict__ q_pol, const float* __restrict__ err_before,
@@ -174,6 +305,51 @@ __global__ void select_kernel(int64_t rows, int64_t n, const uint8_t* __restrict
 }
 
 inline int64_t a64(int64_t v) { return (v + 63) / 64 * 64; }
+
+// The greedy sweeps on caller state (rhs, x, codes, residual norms, accept counts), per row block:
+// gain -> stable descending order -> windows of 128 decisions -> deferred rhs update.
+hipError_t run_sweeps(int64_t rows, int64_t n, int maxq, int64_t block_rows, int64_t nblocks, int sweeps,
+                      float accept_tol, const float* scale, const float* zero, int64_t G, int64_t gs,
+                      const float* diag, const float* diag_inv, const float* H, float* rhs, float* x,
+                      uint8_t* qw, float* res_norm, int* acc, float* gain, int32_t* order, float* T,
+                      float* delta, hipStream_t stream) {
+  const int64_t rtiles = (block_rows + kSRows - 1) / kSRows;
+  const int64_t ctiles = (n + kSCols - 1) / kSCols;
+  const int64_t wgs = nblocks * rtiles * ctiles;
+  if (wgs > 0x7fffffffLL) return hipErrorInvalidValue;
+  for (int sw = 0; sw < sweeps; ++sw) {
+    hipLaunchKernelGGL(gain_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)nblocks), dim3(256), 0,
+                       stream, rows, n, block_rows, rhs, diag_inv, gain);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = argsort_desc_rows(gain, nblocks, n, order, stream);
+    if (e != hipSuccess) return e;
+    for (int64_t w0 = 0; w0 < n; w0 += kWin) {
+      const int wn = (int)std::min<int64_t>(kWin, n - w0);
+      hipLaunchKernelGGL(tile_gather_kernel, dim3(kWin, (unsigned)nblocks), dim3(kWin), 0, stream, n, H,
+                         order, w0, wn, T);
+      hipLaunchKernelGGL(window_kernel, dim3((unsigned)((block_rows + kRowsPerWG - 1) / kRowsPerWG),
+                                             (unsigned)nblocks),
+                         dim3(64 * kRowsPerWG), 0, stream, rows, n, block_rows, maxq, accept_tol, order, w0,
+                         wn, T, scale, zero, G, gs, diag, rhs, x, qw, res_norm, delta, acc);
+      if (n % 4 == 0)
+        hipLaunchKernelGGL(schur_valu_kernel<true>, dim3((unsigned)wgs), dim3(256), 0, stream, rows, n, block_rows,
+                           rtiles, ctiles, order, w0, wn, delta, H, rhs);
+      else
+        hipLaunchKernelGGL(schur_valu_kernel<false>, dim3((unsigned)wgs), dim3(256), 0, stream, rows, n,
+                           block_rows, rtiles, ctiles, order, w0, wn, delta, H, rhs);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+  }
+  return hipSuccess;
+}
+
+// Workspace of mpq_uniform_cd_sweeps: diag_inv, gain, order, window tiles, deltas.
+int64_t sweeps_ws_bytes(int64_t rows, int64_t n, int64_t block_rows) {
+  const int64_t nblocks = (rows + block_rows - 1) / block_rows;
+  return a64(n) * 4 + a64(nblocks * n) * 4 * 2 + a64(nblocks * kWin * kWin) * 4 + a64(rows * kWin) * 4;
+}
 
 struct CdPlan {
   int64_t rows, n, nblocks, nchunks;
@@ -311,45 +487,8 @@ int uniform_cd_polish(int64_t rows, int64_t n, int maxq, int64_t block_rows, int
   hipLaunchKernelGGL(recip_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, n, diag, diag_inv);
   MPQ_LAUNCH_CHECK();
 
-  const bool grouped_gemm = (block_rows % 128 == 0) || pl.nblocks == 1;
-  for (int sw = 0; sw < sweeps; ++sw) {
-    hipLaunchKernelGGL(gain_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)pl.nblocks), dim3(256), 0,
-                       stream, rows, n, block_rows, rhs, diag_inv, gain);
-    MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(argsort_desc_rows(gain, pl.nblocks, n, order, stream));
-    for (int64_t w0 = 0; w0 < n; w0 += kWin) {
-      const int wn = (int)std::min<int64_t>(kWin, n - w0);
-      hipLaunchKernelGGL(tile_gather_kernel, dim3(kWin, (unsigned)pl.nblocks), dim3(kWin), 0, stream, n, H,
-                         order, w0, wn, T);
-      hipLaunchKernelGGL(window_kernel, dim3((unsigned)((block_rows + kRowsPerWG - 1) / kRowsPerWG),
-                                             (unsigned)pl.nblocks),
-                         dim3(64 * kRowsPerWG), 0, stream, rows, n, block_rows, maxq, accept_tol, order, w0,
-                         wn, T, scale, zero, G, gs, diag, rhs, x, qw, res_norm, delta, acc);
-      MPQ_LAUNCH_CHECK();
-      // rhs[rows of blk] -= delta[rows of blk] @ H[order[blk][w0:w0+wn], :]
-      if (grouped_gemm) {
-        GemmParams gp{};
-        gp.M = rows; gp.N = n; gp.K = wn;
-        gp.A = delta; gp.lda = kWin;
-        gp.B = H; gp.ldb = n; gp.trans_b = false;
-        gp.b_rows = order + w0; gp.b_rows_group = pl.nblocks == 1 ? 0 : block_rows;
-        gp.b_rows_group_stride = n;
-        gp.C = rhs; gp.ldc = n; gp.alpha = -1.f; gp.beta = 1.f; gp.mode = kGemmAxpby;
-        MPQ_HIP_TRY(gemm_partials(gp, 1, 64, stream));
-      } else {
-        for (int64_t b = 0; b < pl.nblocks; ++b) {
-          const int64_t r0 = b * block_rows;
-          GemmParams gp{};
-          gp.M = std::min<int64_t>(block_rows, rows - r0); gp.N = n; gp.K = wn;
-          gp.A = delta + r0 * kWin; gp.lda = kWin;
-          gp.B = H; gp.ldb = n; gp.trans_b = false;
-          gp.b_rows = order + b * n + w0;
-          gp.C = rhs + r0 * n; gp.ldc = n; gp.alpha = -1.f; gp.beta = 1.f; gp.mode = kGemmAxpby;
-          MPQ_HIP_TRY(gemm_partials(gp, 1, 64, stream));
-        }
-      }
-    }
-  }
+  MPQ_HIP_TRY(run_sweeps(rows, n, maxq, block_rows, pl.nblocks, sweeps, accept_tol, scale, zero, G, gs, diag,
+                         diag_inv, H, rhs, x, qw, res_norm, acc, gain, order, T, delta, stream));
   // error after the polish, from the final codes (mpq/solver.py:323-330)
   MPQ_HIP_TRY(dequant_groups(qw, scale, zero, G, gs, rows, n, x, stream));
   if (x6) {
@@ -420,4 +559,41 @@ extern "C" int mpq_uniform_cd_polish_ex(int64_t rows, int64_t n, int maxq, int64
   return mpq::uniform_cd_polish(rows, n, maxq, block_rows, sweeps, accept_tol, W, ldw, Yu, q_in, x_in, scale, zero,
                                 group_size, Vs, H, select, q_out, err_before, err_after, improved,
                                 accepted_per_row, workspace, workspace_bytes, stream, xprod_in, S, packed);
+}
+
+extern "C" int64_t mpq_uniform_cd_sweeps_workspace_size(int64_t rows, int64_t n, int64_t block_rows) {
+  if (rows <= 0 || n <= 0 || block_rows <= 0) return 0;
+  return mpq::sweeps_ws_bytes(rows, n, block_rows);
+}
+
+extern "C" int mpq_uniform_cd_sweeps(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                                     float accept_tol, float* rhs, float* x, uint8_t* q, float* res_norm,
+                                     int32_t* accepted, const float* scale, const float* zero,
+                                     int64_t group_size, const float* diag, const float* H, void* workspace,
+                                     int64_t workspace_bytes, hipStream_t stream) {
+  using namespace mpq;
+  MPQ_CHECK_ARG(rows > 0 && n > 0, "mpq_uniform_cd_sweeps: empty problem");
+  MPQ_CHECK_ARG(maxq >= 1 && maxq <= 255, "mpq_uniform_cd_sweeps: maxq must be in [1, 255]");
+  MPQ_CHECK_ARG(block_rows >= 1 && sweeps >= 0 && group_size >= 1, "mpq_uniform_cd_sweeps: bad sizes");
+  MPQ_CHECK_ARG(n <= 16384, "mpq_uniform_cd_sweeps: n <= 16384 supported (greedy-order sort in LDS)");
+  MPQ_CHECK_ARG(rows <= 65535 * kRowsPerWG, "mpq_uniform_cd_sweeps: too many rows");
+  MPQ_CHECK_ARG((rows + block_rows - 1) / block_rows <= 65535, "mpq_uniform_cd_sweeps: too many row blocks");
+  MPQ_CHECK_ARG(rhs && x && q && res_norm && accepted && scale && zero && diag && H && workspace,
+                "mpq_uniform_cd_sweeps: null argument");
+  const int64_t need = sweeps_ws_bytes(rows, n, block_rows);
+  MPQ_CHECK_ARG(workspace_bytes >= need, "mpq_uniform_cd_sweeps: workspace too small (%lld < %lld bytes)",
+                (long long)workspace_bytes, (long long)need);
+  const int64_t nblocks = (rows + block_rows - 1) / block_rows;
+  const int64_t G = (n + group_size - 1) / group_size;
+  char* p = static_cast<char*>(workspace);
+  float* diag_inv = (float*)p; p += a64(n) * 4;
+  float* gain = (float*)p; p += a64(nblocks * n) * 4;
+  int32_t* order = (int32_t*)p; p += a64(nblocks * n) * 4;
+  float* T = (float*)p; p += a64(nblocks * kWin * kWin) * 4;
+  float* delta = (float*)p;
+  hipLaunchKernelGGL(recip_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, n, diag, diag_inv);
+  MPQ_LAUNCH_CHECK();
+  MPQ_HIP_TRY(run_sweeps(rows, n, maxq, block_rows, nblocks, sweeps, accept_tol, scale, zero, G, group_size, diag,
+                         diag_inv, H, rhs, x, q, res_norm, accepted, gain, order, T, delta, stream));
+  return kOk;
 }

@@ -398,6 +398,26 @@ def uniform_cd_polish(W, q_in, scale, zero, group_size, maxq, Vs, H, *, block_ro
     return q_out, eb, ea, imp, acc
 
 
+def uniform_cd_sweeps(rhs, x, q, res_norm, accepted, scale, zero, group_size, maxq, diag, H, *,
+                      block_rows: int, sweeps: int, accept_tol: float = 0.0):
+    """The greedy sweeps in place on (rhs, x, q, res_norm, accepted): the state the reference's
+    persistent sweep kernel takes (mpq/polish/triton_scalar_cd.py:113-161)."""
+    dev = _dev(rhs, x, q, res_norm, accepted, scale, zero, diag, H)
+    rows, n = rhs.shape
+    for name, t, dt, shape in (("rhs", rhs, F32, (rows, n)), ("x", x, F32, (rows, n)),
+                               ("q", q, torch.uint8, (rows, n)), ("res_norm", res_norm, F32, (rows,)),
+                               ("accepted", accepted, torch.int32, (rows,))):
+        if tuple(t.shape) != shape or t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {dt} tensor of shape {shape}")
+    lib = _lib.load()
+    need = int(lib.mpq_uniform_cd_sweeps_workspace_size(rows, n, int(block_rows)))
+    ws = workspace(need, dev)
+    _lib.call("mpq_uniform_cd_sweeps", rows, n, int(maxq), int(block_rows), int(sweeps), float(accept_tol),
+              _lib.ptr(rhs), _lib.ptr(x), _lib.ptr(q), _lib.ptr(res_norm), _lib.ptr(accepted),
+              _lib.ptr(_f32c(scale)), _lib.ptr(_f32c(zero)), int(group_size), _lib.ptr(_f32c(diag)),
+              _lib.ptr(_f32c(H)), _lib.ptr(ws), int(ws.numel()), _stream(dev))
+
+
 # ---- E8P12 VAMP ----------------------------------------------------------------
 
 def e8p12_vamp_config_c(cfg) -> "_lib.E8P12VampConfigC":

@@ -20,6 +20,7 @@ from typing import Any, Dict, Optional, Tuple
 import torch
 
 from . import ops
+from .codebook import require_standin_table
 from .priors.e8p12 import prior_scale_from_center
 from .priors.uniform import dequant_from_q, nearest_atom_idx
 
@@ -248,20 +249,20 @@ def solve_uniform_rankspace_vamp(
 
 # ---- E8P12 -----------------------------------------------------------------------
 
-_CD_CTX: Dict[Any, torch.Tensor] = {}
+_CD_CTX: Dict[str, Any] = {}
 
 
 def _e8p12_cd_context(Vs: torch.Tensor) -> torch.Tensor:
-    """Per-layer polish context, cached for the last Vs seen (the solvers call the polish
-    once per row block with the same Vs).  The key holds the storage address, the shape and
-    an fp64 content fingerprint (sum and sum of squares), so reused memory misses."""
-    v64 = Vs.to(torch.float64)
-    key = (Vs.data_ptr(), tuple(Vs.shape), str(Vs.device), float(v64.sum().item()), float(v64.square().sum().item()))
-    ctx = _CD_CTX.get(key)
-    if ctx is None:
-        _CD_CTX.clear()
-        ctx = ops.e8p12_cd_prepare(Vs)
-        _CD_CTX[key] = ctx
+    """Per-layer polish context for the last Vs seen (the reference-signature solvers call the
+    polish once per row block with the same Vs).  A hit requires the same shape and device and
+    every element equal to the stored copy of Vs; anything else rebuilds the context."""
+    held = _CD_CTX.get("Vs")
+    if held is not None and held.shape == Vs.shape and held.device == Vs.device and torch.equal(held, Vs):
+        return _CD_CTX["ctx"]
+    _CD_CTX.clear()
+    ctx = ops.e8p12_cd_prepare(Vs)
+    _CD_CTX["Vs"] = Vs.detach().clone()
+    _CD_CTX["ctx"] = ctx
     return ctx
 
 
@@ -283,13 +284,17 @@ def polish_e8p12_rankspace(
     snapshot_budgets: Optional[set] = None,
     snapshots_out: Optional[Dict[int, torch.Tensor]] = None,
     block_rows: Optional[int] = None,
+    cd_context: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, Dict[str, Any]]:
     """Gram-metric block CD over E8P12 codewords (reference :369-423).
 
     The rows of ``x_init`` form one greedy-order group unless ``block_rows`` splits them
     (every group of ``block_rows`` rows then has its own order, as separate calls would).
+    ``cd_context`` (``ops.e8p12_cd_prepare(Vs)``, optional) is the per-layer context; without
+    it the context of the last Vs is reused when Vs is element-wise identical.
     Returns (x, idxs, err, stats).
     """
+    require_standin_table(cb, "polish_e8p12_rankspace")
     del cb, metric_rows_per_chunk, topk_idxs
     mode = _resolve_polish_mode(sweeps=int(sweeps), mode=str(polish_mode))
     metric = _resolve_e8p12_polish_metric(str(polish_metric))
@@ -307,7 +312,7 @@ def polish_e8p12_rankspace(
         raise ValueError("CD snapshots are not provided by the HIP polish.")
     del snapshots_out
     rows = int(x_work.shape[0])
-    ctx = _e8p12_cd_context(Vs.to(dtype=torch.float32).contiguous())
+    ctx = cd_context if cd_context is not None else _e8p12_cd_context(Vs.to(dtype=torch.float32).contiguous())
     x, idx, eb, ea, acc = ops.e8p12_cd_polish(x_work, idxs_init, Vs, ctx, sweeps=int(sweeps),
                                               block_rows=int(block_rows or rows), Yu=Y_u,
                                               max_blocks=int(polish_max_blocks))
@@ -336,6 +341,7 @@ def solve_e8p12_rankspace_vamp(
     (reference :853-1276).  Returns (hatWr, Qidxs int64, err, stats); ``log_stats``
     diagnostics (entropy/margin) are reported as 0.0."""
     del Vh, log_stats
+    require_standin_table(cb, "solve_e8p12_rankspace_vamp")
     Wr = Wr.to(dtype=torch.float32)
     rows, n = Wr.shape
     codesz = int(getattr(cb, "codesz", 8)) if cb is not None else 8

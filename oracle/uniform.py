@@ -131,11 +131,39 @@ def scalar_greedy_cd(x, Y_u, Vs, gram, scale, zero, maxq, sweeps, accept_tol=0.0
     rhs = res_u.matmul(Vs.T.contiguous())
     res = res_u.square().sum(dim=1)
     diag = Vs.square().sum(dim=1).clamp_min_(1e-12)
+    x, rhs, res, acc_rows = greedy_cd_sweeps(x, rhs, res, gram, diag, scale, zero, maxq, sweeps,
+                                             accept_tol=accept_tol, target_div=target_div)
+    return x, int(acc_rows.sum())
+
+
+def greedy_cd_sweeps(x, rhs, res, gram, diag, scale, zero, maxq, sweeps, accept_tol=0.0, target_div=True,
+                     seq_gain=False):
+    """The sweeps of mpq/polish/triton_scalar_cd.py:240-288 on given state (x, rhs = residual Vs^T,
+    res = |residual|^2 per row, diag = |Vs_j|^2 floored); returns new (x, rhs, res, accepted per row).
+
+    Per sweep: gain = mean over rows of rhs^2 * (1/diag) (:241), stable descending order (:242; the
+    reference's argsort is unstable, ties are broken by index here), then per column in order the RTN
+    target, the accept test ``cand + 1e-12 < res * (1 + tol)`` and the rank-1 update
+    ``rhs -= delta * gram[col, :]`` (:265-288), each operation rounded to fp32 as torch evaluates it.
+    ``seq_gain=True`` sums the gain over rows in row order (one fp32 addition per row, as the GPU
+    sweep does) instead of torch's reduction order; everything else is the same.
+    """
+    x = x.to(torch.float32).clone()
+    rhs = rhs.to(torch.float32).clone()
+    res = res.to(torch.float32).clone()
     dinv = diag.reciprocal()
-    accepted = 0
-    zero_d = torch.zeros(x.shape[0])
+    rows = x.shape[0]
+    acc_rows = torch.zeros(rows, dtype=torch.int64)
+    zero_d = torch.zeros(rows)
     for _ in range(sweeps):
-        gain = (rhs.square() * dinv.unsqueeze(0)).sum(dim=0) / float(max(rhs.shape[0], 1))
+        terms = rhs.square() * dinv.unsqueeze(0)
+        if seq_gain:
+            g = torch.zeros(rhs.shape[1])
+            for r in range(rows):
+                g = g + terms[r]
+            gain = g / float(max(rows, 1))
+        else:
+            gain = terms.sum(dim=0) / float(max(rows, 1))
         order = torch.argsort(gain, descending=True, stable=True)
         for col in order.tolist():
             r = rhs[:, col]
@@ -152,9 +180,9 @@ def scalar_greedy_cd(x, Y_u, Vs, gram, scale, zero, maxq, sweeps, accept_tol=0.0
                 continue
             x[:, col] = torch.where(acc, xq, xc)
             res = torch.where(acc, cand, res)
-            accepted += int(acc.sum())
+            acc_rows += acc.to(torch.int64)
             rhs.sub_(torch.where(acc, d, zero_d).unsqueeze(1) * gram[col].unsqueeze(0))
-    return x, accepted
+    return x, rhs, res, acc_rows
 
 
 def block_cd_scalar(x, Y_u, Vs, scale, zero, maxq, sweeps, accept_tol=0.0, max_cols=0):

@@ -153,3 +153,52 @@ def test_reference_cd_dispatches_disagree():
     ea = float(ou.rankspace_error(Yu, xa, Vs).mean())
     eb = float(ou.rankspace_error(Yu, xb, Vs).mean())
     assert abs(ea - eb) <= 0.005 * eb
+
+
+def test_gptq_find_params_hand_computed():
+    """The asymmetric min-max quantizer (GPTQModel Quantizer.find_params, un-vendored) against values
+    computed by hand from its published formula: xmin = min(min(x), 0), xmax = max(max(x), 0), an
+    all-zero group widened to [-1, 1], scale = (xmax - xmin) / maxq, zero = round(-xmin / scale)."""
+    W = torch.tensor([
+        [0.5, 1.0, 2.0, 3.0],     # all positive: xmin = 0 -> scale 3/3 = 1, zero 0
+        [-1.5, 0.25, 3.0, 1.0],   # 4.5 / 15 rounds to fp32(0.3); 1.5 / fp32(0.3) = 4.99999982 -> zero 5
+        [-2.0, -1.0, -0.5, -4.0],  # all negative: xmax = 0 -> scale fp32(4/7); 4 / fp32(4/7) = 7 -> zero 7
+        [0.0, 0.0, 0.0, 0.0],     # all zero: [-1, 1] -> scale fp32(2/15) = 0.13333334;
+                                  # 1 / 0.13333334 = 7.4999995 in fp32 -> round -> 7 (not 8)
+    ])
+    maxqs = [3, 15, 7, 15]
+    want_scale = [1.0, float(torch.tensor(0.3)), float(torch.tensor(4.0) / 7), 0.13333334028720856]
+    want_zero = [0.0, 5.0, 7.0, 7.0]
+    for r, maxq in enumerate(maxqs):
+        s, z = ou.gptq_find_params(W[r:r + 1], maxq)
+        assert float(s) == want_scale[r], (r, float(s))
+        assert float(z) == want_zero[r], (r, float(z))
+    # the codes of the all-positive row: round(w / 1) + 0 clamped to [0, 3]
+    s, z = ou.gptq_find_params(W[:1], 3)
+    q = torch.clamp(torch.round(W[:1] / s) + z, 0, 3)
+    assert q.tolist() == [[0.0, 1.0, 2.0, 3.0]]
+
+
+def test_greedy_cd_sweeps_gain_order_only_changes_rounding():
+    """With integer-valued data every sum is exact, so the row-order gain (``seq_gain``, the GPU's
+    order) and torch's reduction order give bit-identical sweeps."""
+    g = torch.Generator().manual_seed(11)
+    rows, n = 24, 40
+    Vs = torch.randint(-3, 4, (n, n), generator=g).float()
+    H = Vs @ Vs.T
+    scale = torch.ones(rows, n)
+    zero = torch.full((rows, n), 4.0)
+    x = torch.randint(-4, 4, (rows, n), generator=g).float()
+    target = torch.randint(-40, 40, (rows, n), generator=g).float()
+    Yu = target @ Vs
+    res_u = Yu - x @ Vs
+    rhs = res_u @ Vs.T
+    res = res_u.square().sum(1)
+    diag = Vs.square().sum(1).clamp_min(1e-12)
+    a = ou.greedy_cd_sweeps(x, rhs, res, H, diag, scale, zero, 7, 3, seq_gain=False)
+    b = ou.greedy_cd_sweeps(x, rhs, res, H, diag, scale, zero, 7, 3, seq_gain=True)
+    assert int(a[3].sum()) > 0
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    # every accepted move lowered the exact objective: the tracked residual equals the recomputed one
+    assert torch.equal(a[2], (Yu - a[0] @ Vs).square().sum(1))
