@@ -26,6 +26,30 @@ import torch
 
 ALPHA_EPS = 1e-7
 
+# Product rounding of the solve.  "fp32": torch's fp32 products (the reference's own arithmetic).
+# "fp64": every product of the solve formed in fp64 and rounded to fp32 -- another valid rounding of
+# the same products, used to measure how far last-bit differences move the discrete decisions.
+_PRODUCTS = {"mode": "fp32"}
+
+
+def _mm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    if _PRODUCTS["mode"] == "fp64":
+        return a.double().matmul(b.double()).float()
+    return a.matmul(b)
+
+
+class products_in_fp64:
+    """Context manager: the solve's products rounded from fp64 (see ``_PRODUCTS``)."""
+
+    def __enter__(self):
+        self._prev = _PRODUCTS["mode"]
+        _PRODUCTS["mode"] = "fp64"
+        return self
+
+    def __exit__(self, *exc):
+        _PRODUCTS["mode"] = self._prev
+        return False
+
 
 # ---- utils (mpq/utils.py:18-68) --------------------------------------------
 
@@ -96,10 +120,10 @@ def linear_mmse_exact(r2, gamma2, Y_u, V, Vh, S, obs):
     R = S.numel()
     s = S.unsqueeze(0)
     denom = float(obs) * s.square() + gamma2
-    r2v = r2.matmul(V)
+    r2v = _mm(r2, V)
     rb = Y_u - r2v * s
     coeff = float(obs) * s / denom
-    x2 = r2 + (rb * coeff).matmul(Vh)
+    x2 = r2 + _mm(rb * coeff, Vh)
     alpha2 = 1.0 - (float(R) / float(n)) + (gamma2 / float(n)) * (1.0 / denom).sum(dim=1, keepdim=True)
     return x2, alpha2, rb * (gamma2 / denom)
 
@@ -115,24 +139,35 @@ def em_update_obs_precision(residual_u, gamma2, S, obs, num_obs, damping=0.3, lo
 
 
 def rankspace_error(Y_u, x, Vs):
-    return (Y_u - x.matmul(Vs)).square().sum(dim=1)
+    return (Y_u - _mm(x, Vs)).square().sum(dim=1)
 
 
 # ---- polish ----------------------------------------------------------------
 
-def scalar_greedy_cd(x, Y_u, Vs, gram, scale, zero, maxq, sweeps, accept_tol=0.0, target_div=True):
+def scalar_greedy_cd(x, Y_u, Vs, gram, scale, zero, maxq, sweeps, accept_tol=0.0, target_div=True,
+                     seq_gain=False, f64_products=False):
     """mpq/polish/triton_scalar_cd.py:164-307 (per-column order, torch ops).
 
     ``target_div=True`` forms the RTN target as ``x + rhs / diag`` like the GPU sweep kernel the
     reference dispatches on CUDA (:73); ``False`` uses the torch twin's ``x + rhs * (1/diag)`` (:265).
+    ``seq_gain``: see ``greedy_cd_sweeps``.  ``f64_products`` forms the starting residual, rhs and
+    diagonal in fp64 and rounds them to fp32 (another valid rounding of the same start, used to
+    measure how far last-bit differences of the products move the greedy decisions).
     """
     x = x.to(torch.float32).clone()
-    res_u = Y_u - x.matmul(Vs)
-    rhs = res_u.matmul(Vs.T.contiguous())
-    res = res_u.square().sum(dim=1)
-    diag = Vs.square().sum(dim=1).clamp_min_(1e-12)
+    if f64_products:
+        V64 = Vs.double()
+        ru = Y_u.double() - x.double().matmul(V64)
+        rhs = ru.matmul(V64.T).float()
+        res = ru.square().sum(dim=1).float()
+        diag = V64.square().sum(dim=1).float().clamp_min_(1e-12)
+    else:
+        res_u = Y_u - x.matmul(Vs)
+        rhs = res_u.matmul(Vs.T.contiguous())
+        res = res_u.square().sum(dim=1)
+        diag = Vs.square().sum(dim=1).clamp_min_(1e-12)
     x, rhs, res, acc_rows = greedy_cd_sweeps(x, rhs, res, gram, diag, scale, zero, maxq, sweeps,
-                                             accept_tol=accept_tol, target_div=target_div)
+                                             accept_tol=accept_tol, target_div=target_div, seq_gain=seq_gain)
     return x, int(acc_rows.sum())
 
 
@@ -228,7 +263,9 @@ def block_cd_scalar(x, Y_u, Vs, scale, zero, maxq, sweeps, accept_tol=0.0, max_c
 
 def solve_uniform_rankspace_vamp(W, x_rtn, scale_full, zero_full, maxq, V, Vh, S, Vs, cfg: Dict[str, Any],
                                  gram_full=None, obs_precision_init=None, polish: str = "twin"):
-    """Returns (q int32, x, err, rtn_err, stats).  polish: "twin" (GPU semantics) | "block_cd" (CPU)."""
+    """Returns (q int32, x, err, rtn_err, stats).  polish: "twin" (the CUDA sweep's semantics) |
+    "twin_rowsum" (the same with the greedy gain summed over rows in row order) | "twin_f64prod" (the
+    same with the polish's starting products rounded from fp64) | "block_cd" (CPU)."""
     iters = int(cfg.get("iters", 16))
     damping = float(cfg.get("damping", 0.5))
     tau = float(cfg.get("prior_tau", 0.2))
@@ -240,11 +277,11 @@ def solve_uniform_rankspace_vamp(W, x_rtn, scale_full, zero_full, maxq, V, Vh, S
     R = S.numel()
     r1 = x_rtn.clone()
     gamma1 = gamma_start * (0.25 / (W - x_rtn).square().mean(dim=1, keepdim=True).clamp_min_(1e-12))
-    Y_u = W.matmul(Vs)
+    Y_u = _mm(W, Vs)
     if obs_precision_init is not None and obs_precision_init > 0:
         obs = float(obs_precision_init)
     else:
-        obs = 1.0 / float((Y_u - x_rtn.matmul(Vs)).square().mean().clamp_min_(1e-12).item())
+        obs = 1.0 / float((Y_u - _mm(x_rtn, Vs)).square().mean().clamp_min_(1e-12).item())
 
     def hard(r, g):
         post = discrete_uniform_mmse(r, g, scale_full, zero_full, maxq, W, tau)
@@ -322,9 +359,11 @@ def solve_uniform_rankspace_vamp(W, x_rtn, scale_full, zero_full, maxq, V, Vh, S
     trace["q_vamp"] = best_q.clone()
     if sweeps > 0:
         err_before = rankspace_error(Y_u, x_final, Vs)
-        if polish == "twin":
+        if polish in ("twin", "twin_rowsum", "twin_f64prod"):
             gram = gram_full if gram_full is not None else Vs.matmul(Vs.T)
-            xp, acc = scalar_greedy_cd(x_final, Y_u, Vs, gram, scale_full, zero_full, maxq, sweeps)
+            xp, acc = scalar_greedy_cd(x_final, Y_u, Vs, gram, scale_full, zero_full, maxq, sweeps,
+                                       seq_gain=polish == "twin_rowsum",
+                                       f64_products=polish == "twin_f64prod" or _PRODUCTS["mode"] == "fp64")
         else:
             xp, acc = block_cd_scalar(x_final, Y_u, Vs, scale_full, zero_full, maxq, sweeps)
         qp = nearest_atom_idx(xp, scale_full, zero_full, maxq)
@@ -429,7 +468,7 @@ def run_mpq_quantization(W, H, bits, group_size, module_name, cfg, rotation="non
         sf = torch.repeat_interleave(scale_g[rb], widths, dim=1)
         zf = torch.repeat_interleave(zero_g[rb], widths, dim=1)
         qr = torch.clamp(torch.round(W_work[rb] / sf) + zf, 0, maxq)
-        du = (W_work[rb] - sf * (qr - zf)).matmul(Vs)
+        du = _mm(W_work[rb] - sf * (qr - zf), Vs)
         sum_sq += float(du.square().sum().item())
         count += du.numel()
     obs = 1.0 / max(sum_sq / max(count, 1), 1e-12)

@@ -4,11 +4,10 @@ import pytest
 import torch
 
 from mpq_amd import ops
-from mpq_amd.adapters.gptqmodel import GPTQAdapterConfig, run_mpq_quantization
 from mpq_amd.priors.uniform import discrete_uniform_mmse
 from mpq_amd.solver import UniformVampConfig
 from oracle import uniform as ou
-from tests.uniform_cases import RECIPE, QCfg, make_layer
+from tests.uniform_cases import RECIPE, make_layer
 
 pytestmark = pytest.mark.gpu
 
@@ -214,67 +213,6 @@ def test_cd_polish_x6_products_match_oracle(gpu):
     assert _rel(eb.cpu(), eb32.cpu()) < 1e-4 and _rel(ea.cpu(), ea32.cpu()) < 1e-4
     with pytest.raises(ValueError):
         ops.uniform_cd_polish(*args, block_rows=128, sweeps=3, select=False, S=Sg)
-
-
-@pytest.mark.parametrize("rotation,bits,x6", [("none", 4, False), ("internal_hadamard", 4, False), ("none", 3, False),
-                                              ("internal_hadamard", 3, False), ("internal_hadamard", 4, True),
-                                              ("none", 3, True)])
-def test_adapter_end_to_end_matches_oracle(gpu, rotation, bits, x6, monkeypatch):
-    """Same eigendecomposition on both sides: proxy loss within 0.5%, codes >= 99% equal; x6: the
-    rank-space products on the packed operator (the adapters use them from ops.X6_MIN_N columns;
-    lowered here so the 512-column case takes that path).
-
-    VAMP alone is code-identical (test_vamp_block_matches_oracle); the greedy CD amplifies
-    rounding-order differences through near-tie accept decisions and the shared greedy order, so
-    whole-layer code agreement sits at the level at which the reference's own two CD dispatches
-    disagree with each other (tests/test_oracle_uniform.py::test_reference_cd_dispatches_disagree).
-    """
-    rows, cols, gs = 256, 512, 128
-    monkeypatch.setattr(ops, "X6_MIN_N", 128 if x6 else 1 << 30)
-    W, H = make_layer(rows, cols, tokens=2048, seed_key=f"e2e:{rotation}:{bits}")
-    Hg = 2.0 * H
-    ref = ou.run_mpq_quantization(W, Hg, bits, gs, "model.layers.0.mlp.up_proj", RECIPE, rotation=rotation)
-    lam, V_unrot, _ = ou.hessian_eigen(0.5 * Hg)
-    vcfg = UniformVampConfig(**RECIPE)
-    Q, q, s, z, g_idx, t, st = run_mpq_quantization(W=W.to(gpu), H=Hg.to(gpu), quantizer=None,
-                                                    qcfg=QCfg(bits, gs, rotation),
-                                                    module_name="model.layers.0.mlp.up_proj", vamp_cfg=vcfg,
-                                                    adapter_cfg=GPTQAdapterConfig(block_rows=128),
-                                                    precomputed_eigen=(lam, V_unrot))
-    agree = float((q.cpu() == ref["q_int"]).float().mean())
-    proxy_ref = float(ref["proxy_rows"].sum())
-    print(rotation, bits, "codes agreement", agree, "proxy", st["proxy_loss"], proxy_ref)
-    assert torch.equal(s.cpu(), ref["scale"]) and torch.equal(z.cpu(), ref["zero"])
-    assert agree >= 0.99
-    assert abs(st["proxy_loss"] - proxy_ref) <= 0.005 * proxy_ref
-    assert torch.equal(g_idx.cpu(), torch.arange(cols, dtype=torch.int32) // gs)
-
-
-@pytest.mark.parametrize("rotation", ["none", "internal_hadamard"])
-def test_adapter_device_eigh(gpu, rotation):
-    """With the device eigh (mpq_syevd) the discrete decisions may move; the proxy loss stays close
-    to the CPU path's and well below RTN's."""
-    rows, cols, bits, gs = 256, 512, 4, 128
-    W, H = make_layer(rows, cols, tokens=2048, seed_key=f"e2e:{rotation}:4")
-    Hg = 2.0 * H
-    ref = ou.run_mpq_quantization(W, Hg, bits, gs, "model.layers.0.mlp.up_proj", RECIPE, rotation=rotation)
-    Q, q, s, z, g_idx, t, st = run_mpq_quantization(W=W.to(gpu), H=Hg.to(gpu), quantizer=None,
-                                                    qcfg=QCfg(bits, gs, rotation),
-                                                    module_name="model.layers.0.mlp.up_proj",
-                                                    vamp_cfg=UniformVampConfig(**RECIPE),
-                                                    adapter_cfg=GPTQAdapterConfig(block_rows=128))
-    proxy_ref = float(ref["proxy_rows"].sum())
-    Wr = ref["W_work"]
-    sf = torch.repeat_interleave(ref["scale"], gs, dim=1)
-    zf = torch.repeat_interleave(ref["zero"], gs, dim=1)
-    d = Wr - sf * (torch.clamp(torch.round(Wr / sf) + zf, 0, 2 ** bits - 1) - zf)
-    proxy_rtn = float((d @ ref["H_metric"] * d).sum())
-    agree = float((q.cpu() == ref["q_int"]).float().mean())
-    print(rotation, "device eigh: agreement", agree, "proxy", st["proxy_loss"], proxy_ref, "rtn", proxy_rtn)
-    assert abs(st["proxy_loss"] - proxy_ref) <= 0.05 * proxy_ref
-    assert st["proxy_loss"] < 0.9 * proxy_rtn
-    # Q is the inverse rotation of the dequantised codes
-    assert _rel(Q.cpu(), ref["Q"]) < 0.2
 
 
 def test_postprocess_gptq_polish_matches_oracle(gpu):
