@@ -509,6 +509,26 @@ int mpq_uniform_cd_sweeps(int64_t rows, int64_t n, int maxq, int64_t block_rows,
                           int64_t workspace_bytes, mpq_stream_t stream);
 
 /*
+ * mpq_uniform_cd_sweeps without a workspace argument and without any device
+ * allocation.  No counterpart in the reference: for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The sweeps' scratch is a static device array of
+ * mpq_uniform_cd_sweeps_noalloc_max_bytes() bytes (8 MiB) per GPU, held until
+ * the process ends; a problem whose
+ * mpq_uniform_cd_sweeps_workspace_size(rows, n, block_rows) exceeds it is
+ * rejected with MPQ_INVALID_ARGUMENT.  Runs on the current device (the stream
+ * must belong to it).  Every call on one GPU uses that GPU's array: calls that
+ * overlap on one GPU (other threads, other streams) race.  Results are
+ * bit-identical to mpq_uniform_cd_sweeps.
+ */
+int64_t mpq_uniform_cd_sweeps_noalloc_max_bytes(void);
+int mpq_uniform_cd_sweeps_noalloc(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                                  float accept_tol, float* rhs, float* x, uint8_t* q, float* res_norm,
+                                  int32_t* accepted, const float* scale, const float* zero,
+                                  int64_t group_size, const float* diag, const float* H,
+                                  mpq_stream_t stream);
+
+/*
  * mpq_uniform_cd_polish with the start's product x Vs from the caller (xprod_in, rows x n,
  * contiguous; optional): mpq_uniform_vamp_solve_ex returns it for its codes, so the polish skips
  * that product (the reference recomputes it, mpq/solver.py:283-290).  With S (n singular values,

@@ -96,6 +96,9 @@ SIGNATURES = {
     "mpq_uniform_cd_sweeps_workspace_size": (c_i64, [c_i64, c_i64, c_i64]),
     "mpq_uniform_cd_sweeps": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_float, c_ptr, c_ptr, c_ptr, c_ptr,
                                       c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
+    "mpq_uniform_cd_sweeps_noalloc_max_bytes": (c_i64, []),
+    "mpq_uniform_cd_sweeps_noalloc": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_float, c_ptr, c_ptr, c_ptr,
+                                              c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_ptr]),
 }
 
 

@@ -24,6 +24,7 @@
 // rhs, x, codes and residual norms, a sweep here is bit-identical to the
 // column-at-a-time restatement (mpq_uniform_cd_sweeps).
 #include <algorithm>
+#include <mutex>
 
 #include "cd_common.h"
 #include "mpq_amd.h"
@@ -566,22 +567,23 @@ extern "C" int64_t mpq_uniform_cd_sweeps_workspace_size(int64_t rows, int64_t n,
   return mpq::sweeps_ws_bytes(rows, n, block_rows);
 }
 
-extern "C" int mpq_uniform_cd_sweeps(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
-                                     float accept_tol, float* rhs, float* x, uint8_t* q, float* res_norm,
-                                     int32_t* accepted, const float* scale, const float* zero,
-                                     int64_t group_size, const float* diag, const float* H, void* workspace,
-                                     int64_t workspace_bytes, hipStream_t stream) {
-  using namespace mpq;
-  MPQ_CHECK_ARG(rows > 0 && n > 0, "mpq_uniform_cd_sweeps: empty problem");
-  MPQ_CHECK_ARG(maxq >= 1 && maxq <= 255, "mpq_uniform_cd_sweeps: maxq must be in [1, 255]");
-  MPQ_CHECK_ARG(block_rows >= 1 && sweeps >= 0 && group_size >= 1, "mpq_uniform_cd_sweeps: bad sizes");
-  MPQ_CHECK_ARG(n <= 16384, "mpq_uniform_cd_sweeps: n <= 16384 supported (greedy-order sort in LDS)");
-  MPQ_CHECK_ARG(rows <= 65535 * kRowsPerWG, "mpq_uniform_cd_sweeps: too many rows");
-  MPQ_CHECK_ARG((rows + block_rows - 1) / block_rows <= 65535, "mpq_uniform_cd_sweeps: too many row blocks");
+namespace mpq {
+namespace {
+
+int cd_sweeps_entry(const char* fn, int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                    float accept_tol, float* rhs, float* x, uint8_t* q, float* res_norm, int32_t* accepted,
+                    const float* scale, const float* zero, int64_t group_size, const float* diag, const float* H,
+                    void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  MPQ_CHECK_ARG(rows > 0 && n > 0, "%s: empty problem", fn);
+  MPQ_CHECK_ARG(maxq >= 1 && maxq <= 255, "%s: maxq must be in [1, 255]", fn);
+  MPQ_CHECK_ARG(block_rows >= 1 && sweeps >= 0 && group_size >= 1, "%s: bad sizes", fn);
+  MPQ_CHECK_ARG(n <= 16384, "%s: n <= 16384 supported (greedy-order sort in LDS)", fn);
+  MPQ_CHECK_ARG(rows <= 65535 * kRowsPerWG, "%s: too many rows", fn);
+  MPQ_CHECK_ARG((rows + block_rows - 1) / block_rows <= 65535, "%s: too many row blocks", fn);
   MPQ_CHECK_ARG(rhs && x && q && res_norm && accepted && scale && zero && diag && H && workspace,
-                "mpq_uniform_cd_sweeps: null argument");
+                "%s: null argument", fn);
   const int64_t need = sweeps_ws_bytes(rows, n, block_rows);
-  MPQ_CHECK_ARG(workspace_bytes >= need, "mpq_uniform_cd_sweeps: workspace too small (%lld < %lld bytes)",
+  MPQ_CHECK_ARG(workspace_bytes >= need, "%s: workspace too small (%lld < %lld bytes)", fn,
                 (long long)workspace_bytes, (long long)need);
   const int64_t nblocks = (rows + block_rows - 1) / block_rows;
   const int64_t G = (n + group_size - 1) / group_size;
@@ -591,9 +593,76 @@ extern "C" int mpq_uniform_cd_sweeps(int64_t rows, int64_t n, int maxq, int64_t 
   int32_t* order = (int32_t*)p; p += a64(nblocks * n) * 4;
   float* T = (float*)p; p += a64(nblocks * kWin * kWin) * 4;
   float* delta = (float*)p;
+  // every workspace entry that is read is written first in the same call (diag_inv, gain, order, the
+  // window tiles, and the deltas of the rows that exist), so nothing needs clearing between calls
   hipLaunchKernelGGL(recip_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, n, diag, diag_inv);
   MPQ_LAUNCH_CHECK();
   MPQ_HIP_TRY(run_sweeps(rows, n, maxq, block_rows, nblocks, sweeps, accept_tol, scale, zero, G, group_size, diag,
                          diag_inv, H, rhs, x, q, res_norm, accepted, gain, order, T, delta, stream));
   return kOk;
+}
+
+}  // namespace
+}  // namespace mpq
+
+extern "C" int mpq_uniform_cd_sweeps(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                                     float accept_tol, float* rhs, float* x, uint8_t* q, float* res_norm,
+                                     int32_t* accepted, const float* scale, const float* zero,
+                                     int64_t group_size, const float* diag, const float* H, void* workspace,
+                                     int64_t workspace_bytes, hipStream_t stream) {
+  return mpq::cd_sweeps_entry("mpq_uniform_cd_sweeps", rows, n, maxq, block_rows, sweeps, accept_tol, rhs, x, q,
+                              res_norm, accepted, scale, zero, group_size, diag, H, workspace, workspace_bytes,
+                              stream);
+}
+
+// ---- allocation-free variant ------------------------------------------------------------------
+// The sweeps' workspace lives in a file-scope device array, one copy per GPU, held until the
+// process ends.  Its device address is looked up once per device (hipGetSymbolAddress with that
+// device current) and only that address is handed to kernels; the array's name is a host-side
+// stand-in in host code.  Calls that overlap on one GPU share the array and race.
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = 8ll << 20;  // 8 MiB
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  MPQ_HIP_TRY(hipGetDevice(&dev));
+  MPQ_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "mpq_uniform_cd_sweeps_noalloc: device id %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    MPQ_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    MPQ_CHECK_ARG(p != nullptr, "mpq_uniform_cd_sweeps_noalloc: no device address for the scratch array");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return mpq::kOk;
+}
+
+}  // namespace
+
+extern "C" int64_t mpq_uniform_cd_sweeps_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int mpq_uniform_cd_sweeps_noalloc(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                                             float accept_tol, float* rhs, float* x, uint8_t* q, float* res_norm,
+                                             int32_t* accepted, const float* scale, const float* zero,
+                                             int64_t group_size, const float* diag, const float* H,
+                                             hipStream_t stream) {
+  MPQ_CHECK_ARG(rows > 0 && n > 0 && block_rows >= 1, "mpq_uniform_cd_sweeps_noalloc: empty problem");
+  const int64_t need = mpq::sweeps_ws_bytes(rows, n, block_rows);
+  MPQ_CHECK_ARG(need <= kNoAllocScratchBytes,
+                "mpq_uniform_cd_sweeps_noalloc: needs %lld bytes of scratch, more than the static %lld "
+                "(reduce rows or the number of row blocks, or use mpq_uniform_cd_sweeps with a workspace)",
+                (long long)need, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  const int st = scratch_for_current_device(&ws);
+  if (st != mpq::kOk) return st;
+  return mpq::cd_sweeps_entry("mpq_uniform_cd_sweeps_noalloc", rows, n, maxq, block_rows, sweeps, accept_tol, rhs,
+                              x, q, res_norm, accepted, scale, zero, group_size, diag, H, ws, kNoAllocScratchBytes,
+                              stream);
 }
