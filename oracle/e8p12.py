@@ -418,10 +418,12 @@ def solve_e8p12_rankspace_vamp(Wr, hat_init, V, S, grid, cache, cfg, obs_precisi
     return hat, idx_t, err, stats
 
 
-def refine_codebook(Wr, Hr, grid, cache, cfg, block_rows=128):
+def refine_codebook(Wr, Hr, grid, cache, cfg, block_rows=128, info=None):
     """mpq/adapters/quip_sharp.py:396-878 for solver "vamp", init "rtn": nearest-codeword init,
     fp64 eigh (:33-67), rank-space warm start (:461-475), per row block VAMP + polish with the
-    observation precision carried (:555-586).  Returns (hat, idx, obs_final)."""
+    observation precision carried (:555-586).  Returns (hat, idx, obs_final); ``info`` (a dict,
+    optional) receives the warm-start precision as "obs_initial".  Pinned by the reference's golden
+    vector tests/golden/e8p12_refine.npz."""
     m, n = Wr.shape
     idx0, _ = bruteforce_nearest(Wr.reshape(-1, 8).numpy(), grid.numpy())
     idx0 = torch.from_numpy(np.asarray(idx0)).view(m, n // 8)
@@ -435,6 +437,8 @@ def refine_codebook(Wr, Hr, grid, cache, cfg, block_rows=128):
     S = torch.sqrt(lam)
     Vs = V * S.unsqueeze(0)
     obs = 1.0 / max(float((Wr - hat0).matmul(Vs).square().sum()) / (m * n), 1e-12)
+    if info is not None:
+        info["obs_initial"] = obs
     hat = hat0.clone()
     idx = idx0.clone()
     for r0 in range(0, m, block_rows):

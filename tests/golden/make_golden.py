@@ -124,5 +124,63 @@ def main(ref_root: str) -> None:
     print("e8p12 vamp written; polish updates", est["polish_updates"])
 
 
+def refine_golden(ref_root: str) -> None:
+    """The QUIP# adapter driver (mpq_refine_codebook, solver vamp, init rtn) on the CPU: its glue --
+    the nearest-codeword start, the rank-space warm start of the observation precision and its carry
+    across row blocks -- is pinned by no closed form."""
+    sys.path.insert(0, ROOT)
+    sys.path.insert(0, ref_root)
+    torch.set_num_threads(1)
+    import types
+
+    from mpq.adapters.quip_sharp import mpq_refine_codebook  # reference
+
+    from mpq_amd.codebook import grid_numpy, packed_abs
+    from oracle import e8p12 as oe8
+    from tests.uniform_cases import make_layer
+
+    class E8P12_codebook:  # noqa: N801 - the reference's factor cache requires this class name
+        """CPU stand-in with the build's table: exact nearest codeword by brute force (first index)."""
+        codesz = 8
+        packsz = 1
+        idx_dtype = torch.int64
+
+        def __init__(self):
+            self.grid = torch.from_numpy(grid_numpy())
+            self.grid_packed_abs = torch.from_numpy(packed_abs())
+
+        def quantize(self, X, return_idx=True, **kwargs):
+            shape = X.shape
+            idx, _ = oe8.bruteforce_nearest(X.reshape(-1, 8).numpy(), self.grid.numpy())
+            idx = torch.from_numpy(np.asarray(idx))
+            vals = self.grid[idx].view(shape)
+            return (vals, idx.view(shape[:-1])) if return_idx else vals
+
+        def maybe_pack_idxs(self, idxs):
+            return idxs
+
+        def by_idxs(self, idxs, **kwargs):
+            return self.grid[idxs.long()]
+
+    cb = E8P12_codebook()
+    W, H = make_layer(256, 128, tokens=1024, seed_key="golden:refine", heavy=True)
+    H = H / torch.diagonal(H).mean() + 1e-2 * torch.eye(128)  # QUIP#'s regularised Hessian scale
+    Wr = W / W.square().mean().sqrt()
+    hat0, idx0 = cb.quantize(Wr.reshape(256, 16, 8))
+    hat0 = hat0.reshape(256, 128)
+    args = types.SimpleNamespace(mpq_init="rtn", mpq_iters=16, mpq_prior_tau=0.25, mpq_polish_sweeps=3,
+                                 mpq_compile_prior=False, mpq_block_rows=128)
+    hat, idx, st = mpq_refine_codebook(Wr, H, hat0, idx0, cb, args, module_name="golden.refine")
+    np.savez_compressed(os.path.join(HERE, "e8p12_refine.npz"), **_np({
+        "Wr": Wr, "H": H, "hat": hat, "idx": idx, "obs_initial": float(st["obs_precision_initial"]),
+        "obs_final": float(st["obs_precision_final"])}))
+    print("refine written; obs", st["obs_precision_initial"], "->", st["obs_precision_final"])
+
+
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    if len(sys.argv) > 2 and sys.argv[2] == "refine":
+        refine_golden(ref)
+    else:
+        main(ref)
+        refine_golden(ref)

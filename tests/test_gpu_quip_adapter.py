@@ -155,3 +155,26 @@ def test_solver_api_matches_ops_path(gpu):
     x2, idx2, err2, pst = polish_e8p12_rankspace(x_init=hat, idxs_init=idx, Y_u=Yu.to(gpu), Vs=Vs.to(gpu), cb=cb,
                                                  sweeps=1, polish_mode="block_cd", polish_metric="gram")
     assert bool((err2.cpu() <= err.cpu() * (1 + 1e-5)).all())
+
+
+def test_refine_codebook_against_reference_golden(gpu):
+    """The whole adapter (rtn init, fp64 eigh, warm start, two 128-row blocks with the precision
+    carried, VAMP + 3 gram-CD sweeps) on the input of the reference's golden vector
+    (tests/golden/e8p12_refine.npz, written by the reference's mpq_refine_codebook on the CPU).  The
+    reference's EM drives the precision to its 1e-4 clamp there; the GPU follows it to the clamp."""
+    import os
+
+    d = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "e8p12_refine.npz"))
+    Wr, H = torch.from_numpy(d["Wr"]), torch.from_numpy(d["H"])
+    ref_idx, ref_hat = torch.from_numpy(d["idx"]), torch.from_numpy(d["hat"])
+    cb = codebook.E8P12_codebook(gpu)
+    vals, idx0 = cb.quantize(Wr.to(gpu).reshape(-1, 8))
+    hat, idx, st = mpq_refine_codebook(Wr.to(gpu), H.to(gpu), vals.view(256, 128), idx0.view(256, 16), cb, Args())
+    agree = float((idx.cpu() == ref_idx).float().mean())
+    s_ref, s_got = _surrogate(Wr, ref_hat, H), _surrogate(Wr, hat.cpu(), H)
+    print(f"refine vs reference golden: codes {agree:.5f}, surrogate {s_got:.6g} vs {s_ref:.6g}, obs "
+          f"{st['obs_precision_initial']:.6g} -> {st['obs_precision_final']:.6g} (golden {float(d['obs_initial']):.6g} -> "
+          f"{float(d['obs_final']):.6g})")
+    assert abs(st["obs_precision_initial"] - float(d["obs_initial"])) <= 1e-5 * float(d["obs_initial"])
+    assert st["obs_precision_final"] == float(d["obs_final"])
+    assert abs(s_got - s_ref) <= 5e-3 * s_ref

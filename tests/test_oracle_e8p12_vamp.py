@@ -55,3 +55,23 @@ def test_e8p12_vamp_loop_matches_reference_golden():
     agree = float((idx == g["idx_final"]).float().mean())
     assert agree >= 0.999, agree
     assert torch.allclose(err, g["err_final"], rtol=1e-3)
+
+
+def test_refine_codebook_matches_reference_golden():
+    """The QUIP# adapter driver's glue (nearest-codeword start, rank-space warm start of the
+    observation precision, its carry over two 128-row blocks, per-block VAMP + 3 gram-CD sweeps)
+    against the reference's mpq_refine_codebook run on the CPU (tests/golden/make_golden.py).  On this
+    input the reference's EM drives the precision to its 1e-4 clamp in the first block; the carry
+    hands that value to the second block."""
+    g = _load("e8p12_refine")
+    torch.set_num_threads(1)
+    grid = torch.from_numpy(codebook.grid_numpy())
+    cache = oe8.factor_cache(grid)
+    info = {}
+    hat, idx, obs = oe8.refine_codebook(g["Wr"], g["H"], grid, cache,
+                                        dict(iters=16, damping=0.5, prior_tau=0.25, polish_sweeps=3),
+                                        block_rows=128, info=info)
+    assert torch.equal(idx, g["idx"])
+    assert torch.equal(hat, g["hat"])
+    assert abs(info["obs_initial"] - g["obs_initial"]) <= 1e-6 * g["obs_initial"]
+    assert obs == g["obs_final"]
