@@ -10,8 +10,10 @@ and the CPU baseline (the oracle's torch CPU restatement of the reference's CPU 
 this host on a bounded sample and extrapolated to the layer).
 
 Synthetic data: W ~ 0.02 N(0,1) rounded to bf16; Hessians from 128 x 2048 tokens with lognormal
-channel scales and 1% x20 outlier channels, H = X^T X / T + 0.01 mean(diag) I (config 4).
-AWQ scaling is not applied (the AWQ search is a preprocessing step outside this path).
+channel scales and 1% x20 outlier channels, H = X^T X / T + 0.01 mean(diag) I (config 4).  AWQ
+scaling (config 4) is applied before the timed solve: the scale search over 20 ratios picks s, and
+the solve quantizes W diag(s) under the Hessian of the scaled inputs; the search time is reported
+separately ("awq").  Config 0 is also measured in full on the CPU oracle and the GPU.
 
 It also times one config-3 decoder layer (Llama-3.2-1B-shaped, 2-bit E8P12 via the QUIP# adapter).
 
@@ -56,7 +58,10 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def make_hessian(n: int, tokens: int, seed: int, device, chunk: int = 16384):
+def make_hessian(n: int, tokens: int, seed: int, device, chunk: int = 16384, with_mean: bool = False):
+    """H = X^T X / T + 0.01 mean(diag) I from synthetic tokens (lognormal channel scales, 1% x20 outlier
+    channels); with_mean also returns the undamped X^T X / T and the per-channel mean |X| (the AWQ
+    search's activation statistic)."""
     import torch
 
     g = torch.Generator(device=device)
@@ -65,15 +70,42 @@ def make_hessian(n: int, tokens: int, seed: int, device, chunk: int = 16384):
     out = torch.randperm(n, device=device, generator=g)[: max(1, round(0.01 * n))]
     c[out] *= 20.0
     H = torch.zeros(n, n, device=device, dtype=torch.float32)
+    xabs = torch.zeros(n, device=device, dtype=torch.float64)
     done = 0
     while done < tokens:
         t = min(chunk, tokens - done)
         X = torch.randn(t, n, device=device, generator=g) * c
         H.addmm_(X.T, X)
+        if with_mean:
+            xabs += X.abs().sum(dim=0, dtype=torch.float64)
         done += t
     H /= float(tokens)
+    if with_mean:
+        return H, (xabs / tokens).to(torch.float32)
     H += 0.01 * torch.diagonal(H).mean() * torch.eye(n, device=device)
     return H
+
+
+def awq_scaled(weights, H_raw, x_mean, bits=3, group_size=128):
+    """AWQ-style scaling of linears that share one input (config 4's "AWQ scaling"): the scale search of
+    mpq/awq_scale.py:491-580 over the stacked weights (single-linear output error), then W diag(s) and
+    the Hessian of the scaled inputs diag(1/s) X^T X diag(1/s) / T + 0.01 mean(diag) I.  Returns
+    (scaled weights, damped Hessian, search ms, best ratio)."""
+    import torch
+
+    from mpq_amd import awq
+
+    Wst = torch.cat(list(weights), 0)
+    Hd = H_raw + 0.01 * torch.diagonal(H_raw).mean() * torch.eye(H_raw.shape[0], device=H_raw.device)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    s, _, ratio, _ = awq.search_best_scale_linear(Wst, Hd, x_mean, bits=bits, group_size=group_size)
+    torch.cuda.synchronize()
+    ms = 1e3 * (time.perf_counter() - t0)
+    del Wst, Hd
+    Hs = H_raw / s.view(1, -1) / s.view(-1, 1)
+    Hs += 0.01 * torch.diagonal(Hs).mean() * torch.eye(Hs.shape[0], device=Hs.device)
+    return [w * s.view(1, -1) for w in weights], Hs, ms, ratio
 
 
 def make_weight(rows: int, cols: int, seed: int, device):
@@ -430,12 +462,75 @@ def cpu_baseline(layer, device):
     t_layer = t_eig + sum(t_init + it * t_iter for it in iters) + nblocks * 3 * n * t_cd
     sample_s = t_init + t2 + 256 * t_cd + t_eig / (n / 4096.0) ** 3
     return {"value": 1e3 * t_layer, "unit": "ms", "cores": threads, "kind": "port",
-            "sample": (f"oracle (torch CPU, {threads} threads) on the down_proj layer: one 128-row block's VAMP "
-                       f"setup + {it_done} iterations ({t_iter:.2f} s/iter), 256 columns of rank-space greedy CD "
-                       f"({1e3 * t_cd:.1f} ms/column), eigh at n=4096 scaled by (n/4096)^3; extrapolated to "
-                       f"{nblocks} blocks x logged VAMP iterations + 3 CD sweeps x {n} columns; "
-                       f"{sample_s:.1f} s of CPU work sampled"),
+            "cpu_model": cpu_model(),
+            "sample": (f"extrapolation: oracle (torch CPU, {threads} threads, {cpu_model()}) on the down_proj layer: "
+                       f"one 128-row block's VAMP setup + {it_done} iterations ({t_iter:.2f} s/iter), 256 columns "
+                       f"of rank-space greedy CD ({1e3 * t_cd:.1f} ms/column), eigh at n=4096 scaled by "
+                       f"(n/4096)^3; extrapolated to {nblocks} blocks x logged VAMP iterations + 3 CD sweeps x {n} "
+                       f"columns; {sample_s:.1f} s of CPU work sampled = {100.0 * sample_s / t_layer:.3f}% of the "
+                       f"extrapolated layer"),
+            "sample_fraction": sample_s / t_layer,
             "extrapolated_from": {"t_init_s": t_init, "t_iter_s": t_iter, "t_cd_col_s": t_cd, "t_eigh_s": t_eig}}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def config0_measured(device):
+    """BASELINE config 0 measured in full on both sides: W 1024 x 1024 ~ 0.02 N(0,1), H from 4096
+    synthetic tokens, 4-bit asymmetric, group 128, RTN init, VAMP + 3 CD sweeps, 128-row blocks, no
+    rotation.  CPU: the oracle's restatement of the reference's CPU dispatch (eager denoiser, CPU
+    eigh, rank-space block CD) on all host cores; GPU: the shipped adapter."""
+    import torch
+
+    from mpq_amd.adapters.gptqmodel import GPTQAdapterConfig, clear_eigen_cache, run_mpq_quantization
+    from mpq_amd.solver import UniformVampConfig
+    from oracle import uniform as ou
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    gw = torch.Generator().manual_seed(ou.stable_seed("cfg0:L0:linear:W"))
+    W = 0.02 * torch.randn(1024, 1024, generator=gw)
+    gx = torch.Generator().manual_seed(ou.stable_seed("cfg0:L0:linear:X"))
+    c = torch.exp(torch.randn(1024, generator=gx))
+    c[torch.randperm(1024, generator=gx)[:10]] *= 20.0
+    X = torch.randn(4096, 1024, generator=gx) * c
+    H = X.T @ X / 4096.0
+    H = H + 0.01 * torch.diagonal(H).mean() * torch.eye(1024)
+    Hg = 2.0 * H
+    cfg = dict(iters=16, damping=0.5, prior_tau=0.2, polish_sweeps=3)
+    t0 = time.perf_counter()
+    ref = ou.run_mpq_quantization(W, Hg, 4, 128, "model.layers.0.linear", cfg, polish="block_cd")
+    cpu_s = time.perf_counter() - t0
+    vcfg = UniformVampConfig(iters=16, damping=0.5, prior_tau=0.2, polish_sweeps=3, polish_mode="block_cd")
+    qcfg = QCfg(4, 128, "none")
+    Wg, Hgg = W.to(device), Hg.to(device)
+    times = []
+    res = None
+    for _ in range(3):
+        clear_eigen_cache()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        res = run_mpq_quantization(W=Wg, H=Hgg, quantizer=None, qcfg=qcfg, module_name="model.layers.0.linear",
+                                   vamp_cfg=vcfg, adapter_cfg=GPTQAdapterConfig(block_rows=128))
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    gpu_s = min(times[1:])
+    proxy_cpu = float(ref["proxy_rows"].sum())
+    return {"cpu_ms": round(1e3 * cpu_s, 1), "gpu_ms": round(1e3 * gpu_s, 3), "speedup": round(cpu_s / gpu_s, 1),
+            "cores": threads, "cpu_model": cpu_model(), "kind": "port",
+            "proxy_cpu": proxy_cpu, "proxy_gpu": res[6]["proxy_loss"],
+            "proxy_rel": (res[6]["proxy_loss"] - proxy_cpu) / proxy_cpu,
+            "workload": "BASELINE config 0 in full (1024x1024, 4096 tokens, 4-bit, group 128, VAMP + 3 CD, "
+                        "no rotation); CPU = oracle restatement of the reference's CPU dispatch"}
 
 
 def main():
@@ -473,11 +568,14 @@ def main():
     e8 = e8p12_bench(dev)
     log(json.dumps(e8))
 
-    log("== building down_proj inputs (4096 x 14336)")
+    log("== building down_proj inputs (4096 x 14336), AWQ scaling (outside the timed solve)")
     W = make_weight(4096, 14336, 11, dev)
-    H = make_hessian(14336, args.tokens, 12, dev)
+    H_raw, x_mean = make_hessian(14336, args.tokens, 12, dev, with_mean=True)
+    (W,), H, awq_ms, awq_ratio = awq_scaled([W], H_raw, x_mean)
+    del H_raw
     Hg = 2.0 * H
     del H
+    log(f"AWQ search {awq_ms:.1f} ms, ratio {awq_ratio}")
     log("== timing down_proj")
     down = run_layer(4096, 14336, "model.layers.0.mlp.down_proj", Hg, W, args.steps, args.warmup)
     log(json.dumps({k: v for k, v in down.items() if k in ("ms", "times_ms", "flop")}),
@@ -492,14 +590,21 @@ def main():
         # the attention-input Hessian, gate/up the MLP-input one, o has its own; down is the
         # headline measurement above.  Every linear runs the whole adapter (its own eigh included).
         log("== timing the layer set (q, k, v, o, gate, up, down)")
-        H_attn = 2.0 * make_hessian(4096, args.tokens, 22, dev)
-        H_o = 2.0 * make_hessian(4096, args.tokens, 23, dev)
-        H_mlp = 2.0 * make_hessian(4096, args.tokens, 24, dev)
+        Hr_attn, xm_attn = make_hessian(4096, args.tokens, 22, dev, with_mean=True)
+        Hr_o, xm_o = make_hessian(4096, args.tokens, 23, dev, with_mean=True)
+        Hr_mlp, xm_mlp = make_hessian(4096, args.tokens, 24, dev, with_mean=True)
+        raw = [make_weight(rows, cols, 31 + i, dev) for i, (rows, cols) in
+               enumerate([(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096), (14336, 4096)])]
+        qkv, H_attn, _, _ = awq_scaled(raw[0:3], Hr_attn, xm_attn)
+        (o_w,), H_o, _, _ = awq_scaled(raw[3:4], Hr_o, xm_o)
+        gu, H_mlp, _, _ = awq_scaled(raw[4:6], Hr_mlp, xm_mlp)
+        del raw, Hr_attn, Hr_o, Hr_mlp
+        H_attn, H_o, H_mlp = 2.0 * H_attn, 2.0 * H_o, 2.0 * H_mlp
         specs = [("q_proj", "self_attn", 4096, 4096, H_attn), ("k_proj", "self_attn", 1024, 4096, H_attn),
                  ("v_proj", "self_attn", 1024, 4096, H_attn), ("o_proj", "self_attn", 4096, 4096, H_o),
                  ("gate_proj", "mlp", 14336, 4096, H_mlp), ("up_proj", "mlp", 14336, 4096, H_mlp),
                  ("down_proj", "mlp", 4096, 14336, Hg)]
-        weights = [make_weight(rows, cols, 31 + i, dev) for i, (_, _, rows, cols, _) in enumerate(specs)]
+        weights = [qkv[0], qkv[1], qkv[2], o_w, gu[0], gu[1], W]
         layer_set = set_pass(specs, weights, dev, warmup=True)
         layer_set = set_pass(specs, weights, dev, warmup=False)
         gate = layer_set.pop("gate_run")
@@ -519,6 +624,7 @@ def main():
     down_tflops = down["flop"] / (down["ms"] / 1e3) / 1e12
 
     cpu = None
+    cfg0 = None
     if not args.no_cpu:
         log("== CPU baseline sample")
         # rotated operands for the sample
@@ -537,6 +643,9 @@ def main():
         del lam, Vs, ops
         cpu = cpu_baseline(down, dev)
         log(json.dumps(cpu))
+        log("== config 0 measured in full (CPU oracle and GPU)")
+        cfg0 = config0_measured(dev)
+        log(json.dumps(cfg0))
 
     line = {
         "metric": METRIC,
@@ -592,7 +701,12 @@ def main():
         "e8p12_layer": None if e8l is None else dict(
             e8l, workload="BASELINE config 3: Llama-3.2-1B-shaped decoder layer, 2-bit E8P12, RHT both sides, "
                           "VAMP 16 iterations + 3 gram-metric CD sweeps, 128-row blocks"),
-        "cpu_baseline": cpu if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "cpu_baseline": cpu if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample",
+                                                                       "cpu_model", "sample_fraction")},
+        "config0_measured": cfg0,
+        "awq": {"search_ms": round(awq_ms, 2), "ratio": awq_ratio,
+                "note": "AWQ scale search of the down_proj (20 ratios) before the timed solve; the solve runs on "
+                        "the scaled weight and Hessian"},
     }
     if cpu is not None:
         line["speedup_vs_cpu"] = round(cpu["value"] / down["ms"], 2)

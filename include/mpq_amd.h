@@ -76,6 +76,19 @@ int mpq_e8p12_denoise(const float* r, int64_t rows, int64_t nb, const float* gam
                       const float* center, const float* scale, float tau, float* x1, float* var,
                       int64_t* map_idx, float* map_vals, float* alpha1, mpq_stream_t stream);
 
+/*
+ * Posterior diagnostics of the E8P12 denoiser for rows x nb 8-blocks (any output may be NULL, one
+ * required): logz (rows*nb) = log-partition over the 2^16 codewords, entropy (rows*nb) = entropy of
+ * the posterior (mixture over the 512 components plus their sign entropies), margin (rows*nb) = gap
+ * between the two largest candidate log-scores (each component's best and second-best sign
+ * pattern).  Prior folding as mpq_e8p12_map.  Replaces the need_stats / return_*_blocks outputs of
+ * mpq/priors/e8p12.py:815-968 (vamp_vector_discrete_mmse_e8p12) and the margin of
+ * mpq/priors/e8p12.py:541-631 (vamp_vector_map_e8p12), per-branch terms mpq/priors/e8p12.py:276-305.
+ */
+int mpq_e8p12_posterior_stats(const float* r, int64_t rows, int64_t nb, const float* gamma,
+                              const float* center, const float* scale, float tau, float* logz,
+                              float* entropy, float* margin, mpq_stream_t stream);
+
 /* Mirrors E8P12VampConfig (mpq/solver.py:59-82) without the polish fields. */
 typedef struct MpqE8P12VampConfig {
   int iters;

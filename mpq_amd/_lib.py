@@ -99,6 +99,8 @@ SIGNATURES = {
     "mpq_uniform_cd_sweeps_noalloc_max_bytes": (c_i64, []),
     "mpq_uniform_cd_sweeps_noalloc": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_float, c_ptr, c_ptr, c_ptr,
                                               c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_ptr]),
+    "mpq_e8p12_posterior_stats": (c_int, [c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_float, c_ptr, c_ptr, c_ptr,
+                                          c_ptr]),
 }
 
 

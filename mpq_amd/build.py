@@ -82,6 +82,7 @@ def _run(cmd):
 
 def generate_sources() -> None:
     subprocess.run([sys.executable, os.path.join(CSRC, "gen_e8p12_search.py")], check=True)
+    subprocess.run([sys.executable, os.path.join(CSRC, "gen_e8p12_posterior.py")], check=True)
 
 
 def build(verbose: bool = False, jobs: int = 8) -> str:

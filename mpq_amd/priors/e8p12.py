@@ -106,6 +106,27 @@ def e8p12_map_flat(
 
 
 @torch.inference_mode()
+def posterior_stats(r_flat: torch.Tensor, rows: int, n_blocks: int, gamma1: torch.Tensor, *,
+                    center: Optional[torch.Tensor], scale: Optional[torch.Tensor], tau: float,
+                    want_logz: bool = True, want_entropy: bool = True, want_margin: bool = True
+                    ) -> Dict[str, Optional[torch.Tensor]]:
+    """Per-block posterior diagnostics (``mpq_e8p12_posterior_stats``): logZ, entropy, margin,
+    each (rows, n_blocks) fp32 or None when not requested."""
+    dev = r_flat.device
+    out: Dict[str, Optional[torch.Tensor]] = {}
+    for key, want in (("logz", want_logz), ("entropy", want_entropy), ("margin", want_margin)):
+        out[key] = torch.empty(rows, n_blocks, dtype=torch.float32, device=dev) if want else None
+    if rows * n_blocks:
+        _lib.call("mpq_e8p12_posterior_stats", _lib.ptr(r_flat.to(torch.float32).contiguous()), int(rows),
+                  int(n_blocks), _lib.ptr(gamma1.to(device=dev, dtype=torch.float32).contiguous()),
+                  _lib.ptr(None if center is None else center.to(device=dev, dtype=torch.float32).contiguous()),
+                  _lib.ptr(None if scale is None else scale.to(device=dev, dtype=torch.float32).contiguous()),
+                  float(tau), _lib.ptr(out["logz"]), _lib.ptr(out["entropy"]), _lib.ptr(out["margin"]),
+                  _lib.stream_handle(dev))
+    return out
+
+
+@torch.inference_mode()
 def e8p12_nearest(x: torch.Tensor, *, return_vals: bool = False) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Exact nearest E8P12 codeword of each row of ``x`` (N, 8); first index on ties."""
     _require_device(x, "x")
@@ -129,14 +150,11 @@ def vamp_vector_map_e8p12(
 ) -> Dict[str, torch.Tensor | float]:
     """Factorized E8P12 MAP per 8-block (reference ``mpq/priors/e8p12.py:541-631``).
 
-    ``blocks_per_chunk`` is accepted for signature compatibility; the kernel has
-    no chunking.  ``need_stats`` (margin diagnostics) is not provided by the HIP
-    backend and raises, as the reference's Triton backend does for diagnostics
-    (``mpq/priors/uniform.py:119-120``).
+    ``blocks_per_chunk`` is accepted for signature compatibility; the kernel has no chunking.
+    ``need_stats`` adds ``margin``, the mean over all blocks of the gap between the two largest
+    candidate log-scores (the reference averages per chunk of blocks).
     """
     del blocks_per_chunk, cb
-    if need_stats:
-        raise ValueError("HIP E8P12 MAP backend does not support posterior diagnostics (need_stats=True).")
     batch, n_blocks, codesz = r1_blocks.shape
     if int(codesz) != 8:
         raise ValueError(f"E8P12 MAP expects codesz=8, got {codesz}.")
@@ -157,6 +175,14 @@ def vamp_vector_map_e8p12(
         r1_blocks.reshape(-1, 8), gamma1.reshape(-1), gamma_div=max(int(n_blocks), 1),
         center=center, scale=scale, tau=tau, want_vals=True,
     )
+    if need_stats:
+        st = posterior_stats(r1_blocks.reshape(-1, 8), int(batch), int(n_blocks), gamma1, center=center,
+                             scale=scale, tau=tau, want_logz=False, want_entropy=False)
+        return {
+            "map_idxs": out["idx"].view(batch, n_blocks),
+            "map_vals": out["vals"].view(batch, n_blocks, 8).to(dtype=r1_blocks.dtype),
+            "margin": float(st["margin"].double().mean().item()) if st["margin"].numel() else 0.0,
+        }
     return {
         "map_idxs": out["idx"].view(batch, n_blocks),
         "map_vals": out["vals"].view(batch, n_blocks, 8).to(dtype=r1_blocks.dtype),
@@ -176,17 +202,21 @@ def vamp_vector_discrete_mmse_e8p12(
     prior_tau: float = 0.0,
     prior_tau_scale_mode: str = "absmax",
     compile_prior: bool = True,
+    return_logZ_blocks: bool = False,
+    return_margin_blocks: bool = False,
+    return_entropy_blocks: bool = False,
 ) -> Dict[str, torch.Tensor | float]:
     """Posterior mean/variance over the 2^16 codewords (reference ``mpq/priors/e8p12.py:815-968``).
 
     Returns ``x1_blocks`` (B, n_blocks, 8), ``var1`` (B, n_blocks), ``alpha1`` (B, 1),
-    ``map_idxs`` (B, n_blocks) and ``map_vals`` (B, n_blocks, 8).  ``blocks_per_chunk`` and
-    ``compile_prior`` are accepted for signature compatibility (the kernel streams all
-    blocks in one launch); ``need_stats`` raises as in :func:`vamp_vector_map_e8p12`.
+    ``map_idxs`` (B, n_blocks), ``map_vals`` (B, n_blocks, 8), ``entropy`` and ``margin`` (means over
+    all blocks when ``need_stats`` or a per-block diagnostic is requested, else 0.0; the reference
+    averages per chunk of blocks) and, on request, ``logZ_blocks``, ``margin_blocks`` and
+    ``entropy_blocks`` (B, n_blocks).  ``blocks_per_chunk`` and ``compile_prior`` are accepted for
+    signature compatibility (the kernel streams all blocks in one launch).
     """
     del blocks_per_chunk, cb, compile_prior
-    if need_stats:
-        raise ValueError("HIP E8P12 posterior backend does not support posterior diagnostics (need_stats=True).")
+    need_stats = bool(need_stats) or bool(return_margin_blocks) or bool(return_entropy_blocks)
     _require_device(r1_blocks, "r1_blocks")
     batch, n_blocks, codesz = r1_blocks.shape
     if int(codesz) != 8:
@@ -220,4 +250,18 @@ def vamp_vector_discrete_mmse_e8p12(
             _lib.ptr(x1), _lib.ptr(var), _lib.ptr(idx), _lib.ptr(vals), _lib.ptr(alpha1),
             _lib.stream_handle(dev),
         )
-    return {"x1_blocks": x1, "var1": var, "alpha1": alpha1, "map_idxs": idx, "map_vals": vals}
+    out: Dict[str, torch.Tensor | float] = {"x1_blocks": x1, "var1": var, "alpha1": alpha1, "map_idxs": idx,
+                                            "map_vals": vals, "entropy": 0.0, "margin": 0.0}
+    if need_stats or return_logZ_blocks:
+        st = posterior_stats(r, int(batch), int(n_blocks), g, center=center, scale=scale, tau=tau,
+                             want_logz=bool(return_logZ_blocks), want_entropy=need_stats, want_margin=need_stats)
+        if need_stats:
+            out["entropy"] = float(st["entropy"].double().mean().item()) if nblk else 0.0
+            out["margin"] = float(st["margin"].double().mean().item()) if nblk else 0.0
+        if return_logZ_blocks:
+            out["logZ_blocks"] = st["logz"]
+        if return_margin_blocks:
+            out["margin_blocks"] = st["margin"]
+        if return_entropy_blocks:
+            out["entropy_blocks"] = st["entropy"]
+    return out

@@ -10,6 +10,9 @@
                           (vamp_vector_discrete_mmse_e8p12) with torch CPU ops in the
                           reference's order.
 * ``posterior_bruteforce``  fp64 softmax over all 65536 codewords (pins ``posterior``).
+* ``posterior_stats_bruteforce``  fp64 logZ / entropy / margin over all codewords (the
+                          diagnostics of mpq/priors/e8p12.py:276-305, 885-953; its logZ is pinned by
+                          the reference's golden logZ_blocks).
 """
 from __future__ import annotations
 
@@ -138,8 +141,9 @@ def _log1mexp(x: torch.Tensor) -> torch.Tensor:
     return torch.where(x < cutoff, torch.log1p(-torch.exp(x)), torch.log(-torch.expm1(x)))
 
 
-def _branch_stats(y: torch.Tensor, g: torch.Tensor, offset: float, branch: int, cache) -> Dict[str, torch.Tensor]:
-    """mpq/priors/e8p12.py:169-308 (_branch_factorized_stats_impl), need_stats=False."""
+def _branch_stats(y: torch.Tensor, g: torch.Tensor, offset: float, branch: int, cache,
+                  need_stats: bool = False) -> Dict[str, torch.Tensor]:
+    """mpq/priors/e8p12.py:169-308 (_branch_factorized_stats_impl)."""
     base_abs = cache["base_abs"].view(1, 256, 8)
     sq = cache["base_sqnorm"].view(1, 256)
     parity_even = (cache["base_parity"] == 0).view(1, 256)
@@ -183,12 +187,31 @@ def _branch_stats(y: torch.Tensor, g: torch.Tensor, offset: float, branch: int, 
     mu = mu_core + float(offset)
     second = sq + 8 * float(offset) * float(offset) + 2.0 * float(offset) * mu_core.sum(dim=-1)
     del bits
-    return {"log_component": const + logZ_sign, "mu_component": mu, "second_component": second}
+    out = {"log_component": const + logZ_sign, "mu_component": mu, "second_component": second}
+    if need_stats:  # mpq/priors/e8p12.py:276-305
+        abs_a = a.abs()
+        sum_abs = abs_a.sum(dim=-1)
+        best_parity = (a < 0).long().sum(dim=-1) & 1
+        min_pos = abs_a.argmin(dim=-1)
+        min_abs = abs_a.gather(-1, min_pos.unsqueeze(-1)).squeeze(-1)
+        mismatch = best_parity != cache["base_parity"].view(1, 256)
+        out["best_logscore"] = const + (sum_abs - 2.0 * mismatch.to(torch.float32) * min_abs)
+        second_abs = abs_a.clone()
+        second_abs.scatter_(-1, min_pos.unsqueeze(-1), float("inf"))
+        second_min = second_abs.min(dim=-1).values
+        second_lin = torch.where(mismatch, sum_abs - 2.0 * second_min, sum_abs - 2.0 * (min_abs + second_min))
+        out["second_logscore"] = const + second_lin
+        out["sign_entropy"] = torch.where(torch.isfinite(logZ_sign),
+                                          (logZ_sign - (a * sign_mean).sum(dim=-1)).clamp_min_(0.0),
+                                          torch.zeros_like(logZ_sign))
+    return out
 
 
 def posterior(r1_blocks: torch.Tensor, gamma1: torch.Tensor, cache, *, prior_center_blocks=None,
-              prior_scale_blocks=None, prior_tau: float = 0.0, map_idx: Optional[np.ndarray] = None):
-    """mpq/priors/e8p12.py:815-968 without diagnostics: x1 blocks, var1, alpha1.
+              prior_scale_blocks=None, prior_tau: float = 0.0, map_idx: Optional[np.ndarray] = None,
+              need_stats: bool = False):
+    """mpq/priors/e8p12.py:815-968: x1 blocks, var1, alpha1, logZ per block and, with ``need_stats``,
+    the per-block entropy and margin (:938-953).
 
     MAP (idx/vals) comes from ``map_search`` (same arithmetic as the reference's
     per-branch MAP, :411-412 and :933-936).  High-precision snap at gamma >= 1e3
@@ -212,10 +235,20 @@ def posterior(r1_blocks: torch.Tensor, gamma1: torch.Tensor, cache, *, prior_cen
     g_flat = g_work.reshape(B * nb, 1)
     outs = []
     for bi, off in enumerate((0.25, -0.25)):
-        outs.append(_branch_stats(r_flat - off, g_flat, off, bi, cache))
+        outs.append(_branch_stats(r_flat - off, g_flat, off, bi, cache, need_stats=need_stats))
     log_comp = torch.stack([o["log_component"] for o in outs], dim=1)
     logZ = torch.logsumexp(log_comp.reshape(B * nb, -1), dim=-1)
-    w = torch.exp(log_comp - logZ.view(-1, 1, 1))
+    log_w = log_comp - logZ.view(-1, 1, 1)
+    w = torch.exp(log_w)
+    stats = {}
+    if need_stats:
+        sent = torch.stack([o["sign_entropy"] for o in outs], dim=1)
+        wl = torch.where(torch.isfinite(log_w), w * log_w, torch.zeros_like(log_w))
+        stats["entropy"] = (-(wl.sum(dim=(1, 2))) + (w * sent).sum(dim=(1, 2))).view(B, nb)
+        best = torch.stack([o["best_logscore"] for o in outs], dim=1).reshape(B * nb, -1)
+        sec = torch.stack([o["second_logscore"] for o in outs], dim=1).reshape(B * nb, -1)
+        top2 = torch.topk(torch.cat([best, sec], dim=1), k=2, dim=1).values
+        stats["margin"] = (top2[:, 0] - top2[:, 1]).view(B, nb)
     mu = torch.zeros((B * nb, 8), dtype=torch.float32)
     second = torch.zeros((B * nb,), dtype=torch.float32)
     for bi in range(2):
@@ -236,8 +269,8 @@ def posterior(r1_blocks: torch.Tensor, gamma1: torch.Tensor, cache, *, prior_cen
         var[hi] = 0.0
     var1 = var.view(B, nb)
     alpha1 = gamma1.to(torch.float32) * var1.mean(dim=1, keepdim=True)
-    return {"x1_blocks": mu.view(B, nb, 8), "var1": var1, "alpha1": alpha1,
-            "map_idxs": torch.as_tensor(np.asarray(map_idx)).view(B, nb), "logZ": logZ.view(B, nb)}
+    return dict({"x1_blocks": mu.view(B, nb, 8), "var1": var1, "alpha1": alpha1,
+                 "map_idxs": torch.as_tensor(np.asarray(map_idx)).view(B, nb), "logZ": logZ.view(B, nb)}, **stats)
 
 
 def posterior_bruteforce(r: np.ndarray, g: np.ndarray, grid: np.ndarray):
@@ -260,6 +293,32 @@ def posterior_bruteforce(r: np.ndarray, g: np.ndarray, grid: np.ndarray):
         var[i] = ((p * gn).sum() - means[i] @ means[i]) / 8.0
         logz[i] = m + math.log(Z)
     return means, var, logz
+
+
+def posterior_stats_bruteforce(r: np.ndarray, g: np.ndarray, grid: np.ndarray):
+    """fp64 diagnostics of p(c) ∝ exp(-g/2 ||c - r||^2) over all codewords: logZ, the entropy
+    -sum p log p, and the margin between the two largest log-scores -g/2 ||c - r||^2.  These are
+    the quantities the reference's factorized diagnostics sum to (mpq/priors/e8p12.py:276-305,
+    885-953): the mixture entropy plus the weighted sign entropies is the entropy over codewords, and
+    the top two of every component's best and second-best sign pattern are the top two codewords."""
+    r = np.asarray(r, dtype=np.float64).reshape(-1, 8)
+    g = np.asarray(g, dtype=np.float64).reshape(-1)
+    G = np.asarray(grid, dtype=np.float64)
+    gn = (G * G).sum(axis=1)
+    logz = np.empty(r.shape[0])
+    ent = np.empty(r.shape[0])
+    margin = np.empty(r.shape[0])
+    for i in range(r.shape[0]):
+        s = -0.5 * g[i] * (gn - 2.0 * G @ r[i] + r[i] @ r[i])
+        m = s.max()
+        w = np.exp(s - m)
+        Z = w.sum()
+        p = w / Z
+        logz[i] = m + math.log(Z)
+        ent[i] = logz[i] - (p * s).sum()
+        top = np.partition(s, -2)[-2:]
+        margin[i] = top.max() - top.min()
+    return logz, ent, margin
 
 
 # ---------------------------------------------------------------------------

@@ -34,20 +34,34 @@ _PRODUCTS = {"mode": "fp32"}
 
 def _mm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     if _PRODUCTS["mode"] == "fp64":
-        return a.double().matmul(b.double()).float()
+        out = a.double().matmul(b.double()).float()
+        gen = _PRODUCTS.get("jitter")
+        if gen is not None:  # move each entry to a random neighbouring float (or keep it)
+            step = torch.randint(-1, 2, out.shape, generator=gen).to(torch.float32)
+            up = torch.nextafter(out, torch.full_like(out, float("inf")))
+            dn = torch.nextafter(out, torch.full_like(out, float("-inf")))
+            out = torch.where(step > 0, up, torch.where(step < 0, dn, out))
+        return out
     return a.matmul(b)
 
 
 class products_in_fp64:
-    """Context manager: the solve's products rounded from fp64 (see ``_PRODUCTS``)."""
+    """Context manager: the solve's products rounded from fp64 (see ``_PRODUCTS``); with ``jitter_seed``
+    every entry of every product then moves to a random one of its two neighbouring floats or stays:
+    a random valid fp32 rounding of the same products (errors well inside an fp32 GEMM's)."""
+
+    def __init__(self, jitter_seed=None):
+        self._seed = jitter_seed
 
     def __enter__(self):
-        self._prev = _PRODUCTS["mode"]
+        self._prev = dict(_PRODUCTS)
         _PRODUCTS["mode"] = "fp64"
+        _PRODUCTS["jitter"] = None if self._seed is None else torch.Generator().manual_seed(int(self._seed))
         return self
 
     def __exit__(self, *exc):
-        _PRODUCTS["mode"] = self._prev
+        _PRODUCTS.clear()
+        _PRODUCTS.update(self._prev)
         return False
 
 
@@ -161,6 +175,12 @@ def scalar_greedy_cd(x, Y_u, Vs, gram, scale, zero, maxq, sweeps, accept_tol=0.0
         rhs = ru.matmul(V64.T).float()
         res = ru.square().sum(dim=1).float()
         diag = V64.square().sum(dim=1).float().clamp_min_(1e-12)
+        gen = _PRODUCTS.get("jitter")
+        if gen is not None:
+            step = torch.randint(-1, 2, rhs.shape, generator=gen).to(torch.float32)
+            up = torch.nextafter(rhs, torch.full_like(rhs, float("inf")))
+            dn = torch.nextafter(rhs, torch.full_like(rhs, float("-inf")))
+            rhs = torch.where(step > 0, up, torch.where(step < 0, dn, rhs))
     else:
         res_u = Y_u - x.matmul(Vs)
         rhs = res_u.matmul(Vs.T.contiguous())

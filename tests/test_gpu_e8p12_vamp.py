@@ -160,3 +160,36 @@ def test_vamp_best_iterate_never_worse_than_its_start(gpu):
     if st["stop_iter"] >= 0:
         assert st["iters"] == st["stop_iter"] + 1
         assert st["best_iter"] < st["stop_iter"]
+
+
+@pytest.mark.parametrize("gscale", [0.3, 3.0, 30.0])
+def test_posterior_diagnostics_match_oracle(gpu, gscale):
+    """logZ, entropy and margin per block (mpq_e8p12_posterior_stats, behind need_stats and the
+    return_*_blocks options) against the oracle's restatement of the reference's factorized
+    diagnostics, with the prior folded.  At high precision the factorized formulas themselves drift
+    from the exact values (the oracle's pin in tests/test_oracle_e8p12_vamp.py stops at moderate
+    precisions); the kernel follows the factorized ones."""
+    from mpq_amd.priors.e8p12 import vamp_vector_map_e8p12
+
+    g = torch.Generator().manual_seed(77)
+    rows, nb = 8, 12
+    r1 = torch.randn(rows, nb, 8, generator=g) * 0.8
+    center = r1 + 0.3 * torch.randn(rows, nb, 8, generator=g)
+    gam = torch.exp(torch.randn(rows, 1, generator=g)) * gscale
+    post = vamp_vector_discrete_mmse_e8p12(r1_blocks=r1.to(gpu), gamma1=gam.to(gpu), cb=None,
+                                           prior_center_blocks=center.to(gpu), prior_tau=0.25,
+                                           return_logZ_blocks=True, return_margin_blocks=True,
+                                           return_entropy_blocks=True)
+    mp = vamp_vector_map_e8p12(r1_blocks=r1.to(gpu), gamma1=gam.to(gpu), cb=None, need_stats=True,
+                               prior_center_blocks=center.to(gpu), prior_tau=0.25)
+    _, cache = _grid_cache()
+    ref = oe8.posterior(r1, gam, cache, prior_center_blocks=center, prior_tau=0.25, need_stats=True)
+    got_lz = post["logZ_blocks"].cpu().double()
+    got_ent = post["entropy_blocks"].cpu().double()
+    got_mg = post["margin_blocks"].cpu().double()
+    assert torch.allclose(got_lz, ref["logZ"].double(), rtol=1e-5, atol=1e-4)
+    assert torch.allclose(got_ent, ref["entropy"].double(), rtol=1e-3, atol=1e-3)
+    assert torch.allclose(got_mg, ref["margin"].double(), rtol=1e-5, atol=1e-4)
+    assert abs(post["entropy"] - float(ref["entropy"].double().mean())) <= 1e-3 * (1 + float(ref["entropy"].abs().mean()))
+    assert abs(post["margin"] - float(ref["margin"].double().mean())) <= 1e-4 * (1 + float(ref["margin"].abs().mean()))
+    assert abs(mp["margin"] - post["margin"]) <= 1e-6 * (1 + abs(post["margin"]))

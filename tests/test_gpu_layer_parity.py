@@ -8,9 +8,9 @@ of a seed comes from the agreements the reference shows with itself on that inpu
 
 * its two CD dispatches (the CUDA sweep and the CPU block CD, mpq/solver.py:299-366);
 * the CUDA-order solve with the greedy gain summed in row order instead of torch's reduction order;
-* the same solve with every product rounded from fp64 (``oracle.uniform.products_in_fp64``), with
-  torch's and with the row-order gain: other valid fp32 roundings of the same algorithm, the kind
-  of difference the GPU's products have.
+* that solve with every product rounded from fp64, and three times with every product entry then
+  moved at random to a neighbouring float (``oracle.uniform.products_in_fp64``): other valid fp32
+  roundings of the same algorithm, the kind of difference the GPU's products have.
 
 The floor of a seed is the lowest of these agreements.
 
@@ -68,7 +68,10 @@ def test_config0_layer_matches_oracle(gpu, rotation, seed):
     if agree < 0.999:
         variants = [_oracle(W, Hg, rotation, polish="block_cd"), _oracle(W, Hg, rotation, polish="twin_rowsum")]
         with ou.products_in_fp64():
-            variants += [_oracle(W, Hg, rotation), _oracle(W, Hg, rotation, polish="twin_rowsum")]
+            variants.append(_oracle(W, Hg, rotation, polish="twin_rowsum"))
+        for js in (1, 2, 3):
+            with ou.products_in_fp64(jitter_seed=js):
+                variants.append(_oracle(W, Hg, rotation, polish="twin_rowsum"))
         floor = min(_agree(v["q_int"], ref["q_int"]) for v in variants)
     _RESULTS[(rotation, seed)] = (agree, floor)
     print(f"seed {seed} {rotation}: codes {agree:.5f} (reference floor {floor:.5f}), proxy {rel:+.5f}")

@@ -75,3 +75,45 @@ def test_refine_codebook_matches_reference_golden():
     assert torch.equal(hat, g["hat"])
     assert abs(info["obs_initial"] - g["obs_initial"]) <= 1e-6 * g["obs_initial"]
     assert obs == g["obs_final"]
+
+
+def test_posterior_stats_bruteforce_pinned():
+    """The brute-force diagnostics: logZ equals the reference's golden logZ_blocks; the entropy lies in
+    [0, log 65536] and tends to log 65536 as gamma -> 0 (uniform posterior); a lone codeword far
+    ahead gives entropy ~0 and the closed-form margin g/2 (d2 - d1)."""
+    g = _load("e8p12_posterior")
+    grid = codebook.grid_numpy()
+    r, c = g["r1"].reshape(-1, 8), g["center"].reshape(-1, 8)
+    gam = g["gamma1"].repeat_interleave(g["r1"].shape[1], 0).reshape(-1)
+    s = c.abs().amax(-1).clamp_min(1e-12)
+    pp = 1.0 / (0.25 * s) ** 2
+    gw = gam + pp
+    rw = (gam[:, None] * r + pp[:, None] * c) / gw[:, None]
+    sel = slice(0, 48)
+    logz, ent, margin = oe8.posterior_stats_bruteforce(rw[sel].numpy(), gw[sel].numpy(), grid)
+    assert np.allclose(logz, g["logZ"].reshape(-1)[sel].numpy(), rtol=1e-5, atol=1e-4)
+    assert np.all(ent >= -1e-9) and np.all(ent <= np.log(65536) + 1e-9) and np.all(margin >= 0)
+    lz0, ent0, m0 = oe8.posterior_stats_bruteforce(np.zeros((1, 8)), np.array([1e-9]), grid)
+    assert abs(ent0[0] - np.log(65536)) < 1e-6 and m0[0] < 1e-8
+    x = grid[1234].astype(np.float64)
+    d = ((grid.astype(np.float64) - x) ** 2).sum(1)
+    d2 = np.partition(d, 1)[1]
+    _, ent1, m1 = oe8.posterior_stats_bruteforce(x[None], np.array([50.0]), grid)
+    assert ent1[0] < 1e-6 and abs(m1[0] - 25.0 * d2) < 1e-9 * 25.0 * d2
+
+
+def test_factorized_diagnostics_match_bruteforce():
+    """The oracle's restatement of the reference's factorized diagnostics (need_stats) equals the
+    exact codeword-level logZ, entropy and margin at moderate precisions."""
+    grid = torch.from_numpy(codebook.grid_numpy())
+    cache = oe8.factor_cache(grid)
+    for gs in (0.3, 3.0):
+        g = torch.Generator().manual_seed(77)
+        r1 = torch.randn(8, 12, 8, generator=g) * 0.8
+        gam = torch.exp(torch.randn(8, 1, generator=g)) * gs
+        post = oe8.posterior(r1, gam, cache, need_stats=True)
+        lz, ent, mg = oe8.posterior_stats_bruteforce(r1.reshape(-1, 8).numpy(),
+                                                     gam.repeat_interleave(12, 0).reshape(-1).numpy(), grid.numpy())
+        assert np.allclose(post["logZ"].reshape(-1).numpy(), lz, rtol=1e-6, atol=1e-5)
+        assert np.allclose(post["entropy"].reshape(-1).numpy(), ent, rtol=1e-5, atol=1e-4)
+        assert np.allclose(post["margin"].reshape(-1).numpy(), mg, rtol=1e-5, atol=1e-4)
