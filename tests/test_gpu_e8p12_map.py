@@ -105,5 +105,13 @@ def test_codebook_quantize_and_reference_signature(gpu, cache):
     ref_idx, _ = oe8.map_search(W.reshape(-1, 8).cpu().numpy(), np.full(32, 2.0, np.float32), 8, cache,
                                 center=(W * 0.9).reshape(-1, 8).cpu().numpy(), tau=0.25)
     assert np.array_equal(out["map_idxs"].reshape(-1).cpu().numpy(), ref_idx)
+    # need_stats adds the mean margin between the two best candidate log-scores (:541-631 with
+    # need_stats): against the oracle's per-block margins
+    st = ke8.vamp_vector_map_e8p12(r1_blocks=W.view(32, 8, 8), gamma1=gamma, cb=cb, need_stats=True)
+    assert torch.equal(st["map_idxs"], ke8.vamp_vector_map_e8p12(r1_blocks=W.view(32, 8, 8), gamma1=gamma,
+                                                                  cb=cb)["map_idxs"])
+    ref = oe8.posterior(W.view(32, 8, 8).cpu(), gamma.cpu(), cache, need_stats=True)
+    ref_margin = float(ref["margin"].double().mean())
+    assert abs(st["margin"] - ref_margin) <= 1e-4 * (1.0 + abs(ref_margin))
     with pytest.raises(ValueError):
-        ke8.vamp_vector_map_e8p12(r1_blocks=W.view(32, 8, 8), gamma1=gamma, cb=cb, need_stats=True)
+        ke8.vamp_vector_map_e8p12(r1_blocks=W.view(32, 8, 8), gamma1=gamma[:4], cb=cb)
