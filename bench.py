@@ -327,6 +327,56 @@ def e8p12_bench(device, nvec=1 << 24, reps=10):
             "mean_sqerr": float(out["err"].double().mean().item())}
 
 
+def micro_bench(name, device, reps=50):
+    """One kernel alone, for rocprofv3 counter runs and kernel timing (``--micro NAME``):
+
+    * ``e8p12_posterior``: the E8P12 denoiser (``mpq_e8p12_denoise``) on one config-3 row block,
+      128 rows x 2048 columns (32768 8-blocks), with the recipe's prior (centre = the block's
+      weights, tau 0.2 absmax) and a VAMP-like message r1 = W + N(0, 1/gamma), gamma = 16;
+    * ``e8p12_map``: the nearest-codeword search on the 2^24 vectors of config 1.
+
+    Prints one JSON line with the average per-call time (HIP events on the launch stream)."""
+    import torch
+
+    from mpq_amd import codebook
+    from mpq_amd.priors import e8p12 as ke8
+
+    g = torch.Generator(device=device)
+    g.manual_seed(5)
+    stream = torch.cuda.current_stream(device)
+    if name == "e8p12_posterior":
+        rows, n, gam = 128, 2048, 16.0
+        W = torch.randn(rows, n // 8, 8, device=device, generator=g)
+        r1 = W + torch.randn(rows, n // 8, 8, device=device, generator=g) / gam ** 0.5
+        gamma = torch.full((rows, 1), gam, device=device)
+        cb = codebook.E8P12_codebook(device=device)
+
+        def go():
+            return ke8.vamp_vector_discrete_mmse_e8p12(r1_blocks=r1, gamma1=gamma, cb=cb, prior_center_blocks=W,
+                                                       prior_tau=0.2)
+        unit, per = "blocks", rows * n // 8
+    elif name == "e8p12_map":
+        x = torch.randn(1 << 24, 8, device=device, generator=g)
+        one = torch.ones(1, device=device)
+
+        def go():
+            return ke8.e8p12_map_flat(x, one, gamma_div=1 << 24, want_idx64=False, want_idx16=True, want_err=True)
+        unit, per = "vectors", 1 << 24
+    else:
+        raise SystemExit(f"unknown --micro {name!r}; choose e8p12_posterior or e8p12_map")
+    for _ in range(5):
+        go()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for _ in range(reps):
+        go()
+    e.record(stream)
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / reps
+    return {"micro": name, "ms_per_call": ms, "reps": reps, unit: per, f"{unit}_per_s": per / ms * 1e3}
+
+
 def make_student_hessian(n: int, tokens: int, seed: int, device, chunk: int = 16384):
     """H = X^T X / T + 0.01 mean(diag) I with Student-t (nu = 4) tokens (config 3)."""
     import torch
@@ -544,6 +594,8 @@ def main():
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant-kernel timing plus a 1 GiB device copy (the PMC scaling reference)")
     ap.add_argument("--tokens", type=int, default=128 * 2048)
+    ap.add_argument("--micro", default=None,
+                    help="time one kernel alone (e8p12_posterior | e8p12_map) and exit; for profiler runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the per-layer solve on a single MI355X; "
@@ -555,6 +607,9 @@ def main():
 
     _lib.load()
     dev = torch.device("cuda:0")
+    if args.micro:
+        print(json.dumps(micro_bench(args.micro, dev)), flush=True)
+        return
     if args.roofline_only:
         rf = gemm_roofline(14336, dev, reps=3)
         src = torch.ones(256 * 1024 * 1024, device=dev)

@@ -6,9 +6,9 @@ Drop-in for the reference's ``mpq/adapters/gptqmodel.py``:
 * ``run_mpq_quantization``       reference :650-1163 (``solver="vamp"`` path)
 
 Pipeline (all on the ROCm device):
-  H <- hessian_scale * H; eigh of the unrotated H (``mpq_syevd``: rocSOLVER
-  tridiagonalisation and divide and conquer, compact-WY back-transformation on
-  the library's MFMA GEMM) -> ``mpq_eigh_postprocess`` (floor, descending order,
+  H <- hessian_scale * H; eigh of the unrotated H (``mpq_syevd``: the library's own
+  tridiagonalisation, divide and conquer on the tridiagonal matrix and compact-WY
+  back-transformation on its MFMA GEMM) -> ``mpq_eigh_postprocess`` (floor, descending order,
   S, Vs); internal block-Hadamard rotation of W, H (both sides) and V
   (``mpq_block_hadamard``); GPTQ group parameters (``quantizer.find_params`` if a
   quantizer is given, else ``mpq_gptq_find_params``); RTN (``mpq_uniform_rtn``);

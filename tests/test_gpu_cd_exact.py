@@ -86,3 +86,39 @@ def test_cd_sweeps_rejects_bad_arguments(gpu):
         ops.uniform_cd_sweeps(rhs, x, q, res, acc, s, s, 8, 0, d, H, block_rows=4, sweeps=1)
     with pytest.raises(ValueError):
         ops.uniform_cd_sweeps(rhs, x, q.float(), res, acc, s, s, 8, 3, d, H, block_rows=4, sweeps=1)
+
+
+def test_reference_signature_scalar_cd_matches_oracle(gpu):
+    """mpq_amd.polish.uniform_scalar_diag_greedy_cd (reference mpq/polish/triton_scalar_cd.py:164-307):
+    expanded scale/zero, one greedy order over all rows, per-sweep trace.  The oracle's sweeps run from
+    the start state the wrapper forms on the device (the same deterministic products), so x and the
+    accept counts must be identical."""
+    from mpq_amd.polish import uniform_scalar_diag_greedy_cd
+
+    rows, n, bits, gs = 96, 256, 4, 128
+    H, sg, zg, sf, zf, maxq, q0, x0, rhs0, res0, diag = _state(rows, n, bits, gs, "ref-sig", 1024)
+    lam, V, _ = ou.hessian_eigen(H)
+    Vs = V * torch.sqrt(lam).unsqueeze(0)
+    W, _ = make_layer(rows, n, tokens=1024, seed_key="ref-sig")
+    Yu = W.matmul(Vs)
+    xg, Vsg = x0.to(gpu), Vs.to(gpu)
+    res_u = Yu.to(gpu) - ops.gemm(xg, Vsg)
+    rhs_dev = ops.gemm(res_u, Vsg, trans_b=True).cpu()
+    res_dev = res_u.square().sum(dim=1).cpu()
+    diag_dev = Vsg.square().sum(dim=1).clamp_min_(1e-12).cpu()
+    x_out, st = uniform_scalar_diag_greedy_cd(x=xg, Y_u=Yu.to(gpu), Vs=Vsg, gram_full=H.to(gpu), scale=sf.to(gpu),
+                                              zero=zf.to(gpu), maxq=maxq, sweeps=3, raw_target=W.to(gpu),
+                                              raw_gram=H.to(gpu))
+    x_ref, _, res_ref, acc_ref = ou.greedy_cd_sweeps(x0, rhs_dev, res_dev, H, diag_dev, sf, zf, maxq, 3,
+                                                     seq_gain=True)
+    assert torch.equal(x_out.cpu(), x_ref)
+    assert st["accepted_updates"] == float(acc_ref.sum()) > 0
+    tr = st["cd_trace"]
+    assert [t["budget"] for t in tr] == [0, 1, 2, 3]
+    assert sum(t["accepted_updates_sweep"] for t in tr) == int(acc_ref.sum())
+    assert abs(tr[-1]["stabilized_objective_mean"] - float(res_ref.mean())) <= 1e-6 * float(res_ref.mean())
+    objs = [t["raw_objective_mean"] for t in tr]
+    assert all(b <= a * (1 + 1e-5) for a, b in zip(objs, objs[1:]))
+    with pytest.raises(ValueError, match="update_backend"):
+        uniform_scalar_diag_greedy_cd(x=xg, Y_u=Yu.to(gpu), Vs=Vsg, gram_full=H.to(gpu), scale=sf.to(gpu),
+                                      zero=zf.to(gpu), maxq=maxq, sweeps=1, update_backend="cuda")

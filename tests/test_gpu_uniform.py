@@ -256,3 +256,33 @@ def test_postprocess_gptq_polish_matches_oracle(gpu):
     assert agree >= 0.98, agree
     assert not st["module_fail_closed"] and st["polish_updates"] > 0
     assert torch.equal(got, sf * (qf.cpu().float() - zf))
+
+
+def test_vamp_early_stop_then_call_on_another_stream(gpu):
+    """Status mailbox (two slots, one per pending publish): a block that stops at the best iterate
+    leaves the look-ahead pass's status publish queued; the driver waits for it before returning, so
+    a second call from the same thread on another stream, started right away, reads only its own
+    statuses.  Both results must equal the same solves run alone on the default stream."""
+    cases = []
+    for key in ("mb0", "mb3"):  # oracle: best-iterate stops at 7 and 9 of 16 iterations
+        W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq = _setup_block(128, 512, 4, 128, key, rotate=True)
+        cases.append([t.to(gpu) for t in (W, xr, sg, zg)] + [maxq] + [t.to(gpu) for t in (V, S, Vs)])
+    vcfg = UniformVampConfig(**{k: v for k, v in RECIPE.items()})
+
+    def solve(c):
+        W, xr, sg, zg, maxq, V, S, Vs = c
+        return ops.uniform_vamp_solve(W, xr, sg, zg, 128, maxq, V, S, Vs, vcfg)
+
+    alone = [solve(c) for c in cases]
+    torch.cuda.synchronize()
+    assert all(r[4]["stop_iter"] < 15 for r in alone), [r[4]["stop_iter"] for r in alone]
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(sa):
+        ra = solve(cases[0])
+    with torch.cuda.stream(sb):
+        rb = solve(cases[1])
+    torch.cuda.synchronize()
+    for got, ref in ((ra, alone[0]), (rb, alone[1])):
+        assert torch.equal(got[0], ref[0])
+        assert torch.equal(got[2], ref[2])
+        assert got[4]["stop_iter"] == ref[4]["stop_iter"] and got[4]["best_iter"] == ref[4]["best_iter"]
