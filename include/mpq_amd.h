@@ -287,6 +287,20 @@ int mpq_syevd(int64_t n, const float* H, float* lam, float* V, void* workspace, 
               mpq_stream_t stream);
 
 /*
+ * mpq_syevd with the reduction chosen by the caller (no counterpart in the reference, whose eigh
+ * is torch.linalg.eigh): method 0 = automatic (what mpq_syevd does), 1 = the one-stage blocked
+ * Householder tridiagonalisation above, 2 = the two-stage reduction (3 <= n <= 16416): dense to
+ * a band of half-bandwidth 32 (panels by shifted Cholesky QR with a tall-skinny Householder QR
+ * fallback, Householder vectors reconstructed from the orthogonal factor, trailing updates on the
+ * MFMA GEMM), band to tridiagonal by bulge chasing (a cooperative pipeline of one wave per sweep),
+ * then the chase's reflectors as explicit 64 x 64 blocks and the band reduction's reflectors as
+ * compact-WY blocks applied to the tridiagonal eigenvectors.  Same output contract and workspace
+ * size as mpq_syevd; the two-stage path synchronises `stream` once more (bulge-chasing status).
+ */
+int mpq_syevd_method(int64_t n, const float* H, float* lam, float* V, void* workspace, int64_t workspace_bytes,
+                     int method, mpq_stream_t stream);
+
+/*
  * The same decomposition in fp64 (the torch.linalg.eigh of the float64 Hessian in
  * mpq/adapters/quip_sharp.py:33-67): the same kernels in double (divide-and-conquer tolerances
  * at fp64 unit roundoff), with the trailing updates, merge products and back-transformation on

@@ -63,6 +63,7 @@ SIGNATURES = {
     "mpq_transpose": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr]),
     "mpq_syevd_workspace_size": (c_i64, [c_i64]),
     "mpq_syevd": (c_int, [c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
+    "mpq_syevd_method": (c_int, [c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_int, c_ptr]),
     "mpq_syevd_f64_workspace_size": (c_i64, [c_i64]),
     "mpq_syevd_f64": (c_int, [c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
     "mpq_scale_columns": (c_int, [c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_ptr]),

@@ -41,6 +41,7 @@ HIP_SOURCES = [
     "hessian.hip",
     "awq.hip",
     "eigh.hip",
+    "eigh_band.hip",
     "stedc.hip",
 ]
 CXX_SOURCES = [

@@ -21,11 +21,17 @@
 // is formed.
 // Reflector i (LAPACK's H(i) = I - tau_i v_i v_i^T, v_i[0..i] = 0, v_i[i+1] = 1) is stored in
 // row i, entries i+2..n-1 -- by symmetry the same entries LAPACK's lower storage keeps in column i.
+//
+// fp32 with 2048 <= n <= band::kMaxN takes the two-stage reduction instead (eigh_band.hip: dense ->
+// band of half-bandwidth 32 on the MFMA GEMM, band -> tridiagonal by bulge chasing); its stage-1
+// reflectors sit in the rows of A the same way with v_i[i + 32] = 1, and the same compact-WY
+// back-transformation applies them after the bulge-chasing reflectors.
 #include <rocblas/rocblas.h>
 
 #include <algorithm>
 
 #include "common.h"
+#include "eigh_band.h"
 #include "gemm.h"
 #include "kernels.h"
 #include "stedc.h"
@@ -520,7 +526,7 @@ __global__ __launch_bounds__(kThr) void finish_kernel(T* __restrict__ A, int64_t
 // of the block size) keeps the GEMM operands 16-byte aligned.
 template <typename T>
 __global__ __launch_bounds__(256) void extract_y_kernel(const T* __restrict__ A, int64_t lda, int64_t n,
-                                                        int64_t i0, int nb, T* __restrict__ Y) {
+                                                        int64_t i0, int nb, int64_t off, T* __restrict__ Y) {
   const int64_t m = n - i0;
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= m * nb) return;
@@ -529,8 +535,8 @@ __global__ __launch_bounds__(256) void extract_y_kernel(const T* __restrict__ A,
   const int64_t r = i0 + rp;
   const int64_t i = i0 + c;
   T v = 0.f;
-  if (r == i + 1) v = 1.f;
-  else if (r > i + 1) v = A[i * lda + r];
+  if (r == i + off) v = 1.f;
+  else if (r > i + off) v = A[i * lda + r];
   Y[e] = v;
 }
 
@@ -786,19 +792,15 @@ int sytrd(int64_t n, const SyevdLayout& L, T* base, rocblas_handle h, hipStream_
   return kOk;
 }
 
+// Zb (row-major, row k = eigenvector k of the reduced matrix) <- Zb Q^T for the nrefl reflectors
+// kept in the rows of A (reflector i: v_i[i + off] = 1, entries past it in row i, tau[i]), applied
+// as compact-WY blocks of NB reflectors, last block first:
+//    Zb[:, i0:] <- Zb[:, i0:] - ((Zb[:, i0:] Y) Tb^T) Y^T
+// The grams Y^T Y of all blocks come first, then one larft launch forms every Tb.
 template <typename T>
-int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+int back_transform(int64_t n, int64_t off, int64_t nrefl, const SyevdLayout& L, T* base, rocblas_handle h,
+                   hipStream_t stream) {
   using namespace mpq;
-  MPQ_CHECK_ARG(n > 0 && n <= 46336, "mpq_syevd: n must be in [1, 46336]");
-  static_assert(kDotWG % 4 == 0 && 2 * kPB <= 64 && kPB % kSub == 0, "tridiagonalisation constants");
-  MPQ_CHECK_ARG(H && lam && V && workspace, "mpq_syevd: null pointer");
-  MPQ_CHECK_ARG((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "mpq_syevd: workspace must be 256-byte aligned");
-  const SyevdLayout L = syevd_layout<T>(n);
-  MPQ_CHECK_ARG(workspace_bytes >= L.total * (int64_t)sizeof(T), "mpq_syevd: workspace too small (%lld < %lld)",
-                (long long)workspace_bytes, (long long)(L.total * (int64_t)sizeof(T)));
-  rocblas_handle h = get_handle(stream);
-  MPQ_CHECK_ARG(h != nullptr, "mpq_syevd: rocBLAS handle unavailable");
-  T* base = static_cast<T*>(workspace);
   T* A = base + L.A;
   T* Z = base + L.Z;
   T* Y = base + L.Y;
@@ -808,32 +810,10 @@ int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t wor
   T* G = base + L.G;
   T* Tb = base + L.Tb;
   T* P = base + L.P;
-  T* D = base + L.D;
-  T* E = base + L.E;
   T* tau = base + L.tau;
   const int64_t lda = L.lda;
   const int64_t pfl = L.splits > 1 ? a64(n * L.nb) * L.splits : 0;
   const int NB = (int)L.nb;
-
-  // 1. tridiagonalise (zero-padded copy, leading dimension lda)
-  MPQ_HIP_TRY(hipMemsetAsync(A, 0, (size_t)(lda * lda) * sizeof(T), stream));
-  MPQ_HIP_TRY(hipMemcpy2DAsync(A, lda * sizeof(T), H, n * sizeof(T), n * sizeof(T), n, hipMemcpyDeviceToDevice,
-                               stream));
-  if (n == 1) {
-    MPQ_HIP_TRY(hipMemcpyAsync(D, A, sizeof(T), hipMemcpyDeviceToDevice, stream));
-  } else {
-    const int rc = sytrd<T>(n, L, base, h, stream);
-    if (rc != kOk) return rc;
-  }
-  // 2. tridiagonal eigenproblem
-  {
-    const int rc = tridiag_dc(n, D, E, lam, Z, base + L.dc, (L.total - L.dc) * (int64_t)sizeof(T), h, stream);
-    if (rc != kOk) return rc;
-  }
-  // 3. Z column-major = row-major Zb with Zb = Z^T.  V^T = Zb Q^T, applied block by block:
-  //    Zb[:, i0:] <- Zb[:, i0:] - ((Zb[:, i0:] Y) Tb^T) Y^T
-  //    The grams Y^T Y of all blocks come first, then one larft launch forms every Tb.
-  const int64_t nrefl = n - 1;
   const int64_t nblocks = nrefl > 0 ? (nrefl + NB - 1) / NB : 0;
   int rc;
   for (int64_t b = 0; b < nblocks; ++b) {
@@ -842,7 +822,7 @@ int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t wor
     const int64_t m = n - i0;
     const int64_t cnt = m * nb;
     hipLaunchKernelGGL(extract_y_kernel<T>, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, stream, A, lda, n,
-                       i0, nb, Y);
+                       i0, nb, off, Y);
     MPQ_LAUNCH_CHECK();
     MPQ_HIP_TRY(transpose_t(Y, m, nb, nb, Yt, m, stream));
     if ((rc = gemm_rm(h, Yt, m, Y, nb, false, G + b * NB * NB, nb, nb, nb, m, T(1), T(0), P, pfl, stream)) != kOk)
@@ -859,12 +839,100 @@ int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t wor
     const int64_t cnt = m * nb;
     const T* Tbb = Tb + b * NB * NB;
     hipLaunchKernelGGL(extract_y_kernel<T>, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, stream, A, lda, n,
-                       i0, nb, Y);
+                       i0, nb, off, Y);
     MPQ_LAUNCH_CHECK();
     if ((rc = gemm_rm(h, Z + i0, n, Y, nb, false, W, nb, n, nb, m, T(1), T(0), P, pfl, stream)) != kOk) return rc;
     if ((rc = gemm_rm(h, W, nb, Tbb, nb, true, W2, nb, n, nb, nb, T(1), T(0), nullptr, 0, stream)) != kOk) return rc;
     if ((rc = gemm_rm(h, W2, nb, Y, nb, true, Z + i0, n, n, m, nb, T(-1), T(1), nullptr, 0, stream)) != kOk)
       return rc;
+  }
+  return kOk;
+}
+
+// Two-stage path (fp32): stage 1 to a band of half-bandwidth 32, bulge chasing to tridiagonal
+// form, divide and conquer, then the bulge-chasing reflectors and the stage-1 reflectors applied
+// to the tridiagonal eigenvectors.  The band workspace follows the one-stage layout.
+// Sizes the two-stage path handles, and those where it is the faster path on MI355X (measured:
+// n = 4096 one-stage 73 ms vs two-stage 90 ms; n = 14336 640 ms vs 624 ms).
+bool two_stage_ok(int64_t n) { return n >= 3 && n <= mpq::band::kMaxN; }
+bool use_two_stage(int64_t n, int elem) { return elem == 4 && n >= 8192 && two_stage_ok(n); }
+
+int syevd_two_stage(int64_t n, const float* H, float* lam, float* V, float* base, const SyevdLayout& L,
+                    rocblas_handle h, hipStream_t stream) {
+  using namespace mpq;
+  const band::Layout BL = band::layout(n);
+  float* bws = base + L.total;
+  float* A = base + L.A;
+  float* Z = base + L.Z;
+  const int64_t lda = L.lda;
+  MPQ_HIP_TRY(hipMemsetAsync(A, 0, (size_t)(lda * lda) * sizeof(float), stream));
+  MPQ_HIP_TRY(hipMemcpy2DAsync(A, lda * sizeof(float), H, n * sizeof(float), n * sizeof(float), n,
+                               hipMemcpyDeviceToDevice, stream));
+  int rc;
+  if ((rc = band::sy2sb(n, A, lda, base + L.tau, bws, BL, stream)) != kOk) return rc;
+  if ((rc = band::sb2st(n, A, lda, base + L.D, base + L.E, bws, BL, stream)) != kOk) return rc;
+  if ((rc = tridiag_dc(n, base + L.D, base + L.E, lam, Z, base + L.dc, (L.total - L.dc) * (int64_t)sizeof(float), h,
+                       stream)) != kOk)
+    return rc;
+  if ((rc = band::q2_apply(n, Z, bws, BL, stream)) != kOk) return rc;
+  if ((rc = back_transform<float>(n, band::kBW, n - band::kBW, L, base, h, stream)) != kOk) return rc;
+  MPQ_HIP_TRY(transpose_t(Z, n, n, n, V, n, stream));
+  MPQ_HIP_TRY(hipStreamSynchronize(stream));
+  return kOk;
+}
+
+template <typename T>
+int64_t syevd_workspace_elems(int64_t n) {
+  const SyevdLayout L = syevd_layout<T>(n);
+  return L.total + (sizeof(T) == 4 && two_stage_ok(n) ? mpq::band::layout(n).total : 0);
+}
+
+template <typename T>
+int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t workspace_bytes, hipStream_t stream,
+               int method = 0) {
+  using namespace mpq;
+  MPQ_CHECK_ARG(n > 0 && n <= 46336, "mpq_syevd: n must be in [1, 46336]");
+  static_assert(kDotWG % 4 == 0 && 2 * kPB <= 64 && kPB % kSub == 0, "tridiagonalisation constants");
+  MPQ_CHECK_ARG(H && lam && V && workspace, "mpq_syevd: null pointer");
+  MPQ_CHECK_ARG((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "mpq_syevd: workspace must be 256-byte aligned");
+  const SyevdLayout L = syevd_layout<T>(n);
+  const int64_t need = syevd_workspace_elems<T>(n) * (int64_t)sizeof(T);
+  MPQ_CHECK_ARG(workspace_bytes >= need, "mpq_syevd: workspace too small (%lld < %lld)",
+                (long long)workspace_bytes, (long long)need);
+  rocblas_handle h = get_handle(stream);
+  MPQ_CHECK_ARG(h != nullptr, "mpq_syevd: rocBLAS handle unavailable");
+  T* base = static_cast<T*>(workspace);
+  if constexpr (sizeof(T) == 4) {
+    MPQ_CHECK_ARG(method >= 0 && method <= 2, "mpq_syevd_method: method must be 0 (auto), 1 or 2");
+    MPQ_CHECK_ARG(method != 2 || two_stage_ok(n), "mpq_syevd_method: the two-stage path needs 3 <= n <= %lld",
+                  (long long)mpq::band::kMaxN);
+    if (method == 2 || (method == 0 && use_two_stage(n, 4))) return syevd_two_stage(n, H, lam, V, base, L, h, stream);
+  }
+  T* A = base + L.A;
+  T* Z = base + L.Z;
+  T* D = base + L.D;
+  T* E = base + L.E;
+  const int64_t lda = L.lda;
+
+  // 1. tridiagonalise (zero-padded copy, leading dimension lda)
+  MPQ_HIP_TRY(hipMemsetAsync(A, 0, (size_t)(lda * lda) * sizeof(T), stream));
+  MPQ_HIP_TRY(hipMemcpy2DAsync(A, lda * sizeof(T), H, n * sizeof(T), n * sizeof(T), n, hipMemcpyDeviceToDevice,
+                               stream));
+  if (n == 1) {
+    MPQ_HIP_TRY(hipMemcpyAsync(D, A, sizeof(T), hipMemcpyDeviceToDevice, stream));
+  } else {
+    const int rc = sytrd<T>(n, L, base, h, stream);
+    if (rc != kOk) return rc;
+  }
+  // 2. tridiagonal eigenproblem
+  {
+    const int rc = tridiag_dc(n, D, E, lam, Z, base + L.dc, (L.total - L.dc) * (int64_t)sizeof(T), h, stream);
+    if (rc != kOk) return rc;
+  }
+  // 3. Z column-major = row-major Zb with Zb = Z^T; V^T = Zb Q^T
+  {
+    const int rc = back_transform<T>(n, 1, n - 1, L, base, h, stream);
+    if (rc != kOk) return rc;
   }
   // V (row-major, columns = eigenvectors) = (Zb)^T
   MPQ_HIP_TRY(transpose_t(Z, n, n, n, V, n, stream));
@@ -876,7 +944,7 @@ int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t wor
 
 extern "C" int64_t mpq_syevd_workspace_size(int64_t n) {
   if (n <= 0) return 0;
-  return syevd_layout<float>(n).total * 4;
+  return syevd_workspace_elems<float>(n) * 4;
 }
 
 extern "C" int mpq_syevd(int64_t n, const float* H, float* lam, float* V, void* workspace, int64_t workspace_bytes,
@@ -884,9 +952,14 @@ extern "C" int mpq_syevd(int64_t n, const float* H, float* lam, float* V, void* 
   return syevd_impl<float>(n, H, lam, V, workspace, workspace_bytes, stream);
 }
 
+extern "C" int mpq_syevd_method(int64_t n, const float* H, float* lam, float* V, void* workspace,
+                                int64_t workspace_bytes, int method, hipStream_t stream) {
+  return syevd_impl<float>(n, H, lam, V, workspace, workspace_bytes, stream, method);
+}
+
 extern "C" int64_t mpq_syevd_f64_workspace_size(int64_t n) {
   if (n <= 0) return 0;
-  return syevd_layout<double>(n).total * 8;
+  return syevd_workspace_elems<double>(n) * 8;
 }
 
 extern "C" int mpq_syevd_f64(int64_t n, const double* H, double* lam, double* V, void* workspace,

@@ -1,0 +1,1282 @@
+// Two-stage tridiagonalisation for mpq_syevd (fp32, gfx950): dense -> band -> tridiagonal.
+//
+// The one-stage reduction (eigh.hip) reads the whole trailing matrix once per reflector, a
+// symmetric matrix-vector product per column (2 n^3 / 3 bytes in total), and is bound by HBM.
+// This file reduces to a band first with matrix-core products, then chases the band down to
+// tridiagonal form with small cache-resident tasks:
+//
+// Stage 1 (dense -> band of half-bandwidth kBW = 32), one panel of 32 columns at a time:
+//   * the panel below the band, P = A[r0:, c0:c0+32] (m x 32), is factorised as a tall-skinny
+//     QR: Householder QR of row blocks of kLeaf rows in LDS (one work-group each), Householder QR
+//     of the stacked 32 x 32 R factors in one work-group, the explicit first 32 columns Q1 of the
+//     orthogonal factor (LAPACK org2r on the root, then each leaf's reflectors), and Householder
+//     vectors reconstructed from Q1 (Ballard, Demmel, Grigori, Jacquelin, Nguyen, Solomonik,
+//     "Reconstructing Householder vectors from tall-skinny QR", 2014): Q1 - S = L U with the
+//     diagonal sign matrix S chosen during the elimination (|U_ii| >= 1, no pivoting), Y = L,
+//     T = -U S Y1^-T, R = S R_tsqr, so P = (I - Y T Y^T) [R; 0];
+//   * the trailing matrix takes A22 <- Q^T A22 Q as X = A22 (Y T), W = X - 1/2 Y (T^T Y^T X),
+//     A22 -= Y W^T + W Y^T (the library's fp32 MFMA GEMM; LAPACK sytrd's update).
+// Stage 2 (band -> tridiagonal): bulge chasing (Schwarz 1968; Lang 1993; the task split of Haidar,
+//   Ltaief and Dongarra, SC 2011).  Sweep s annihilates column s below the subdiagonal with one
+//   reflector (task 0, two-sided on the 32 x 32 diagonal block below); task k >= 1 applies the
+//   previous reflector from the right to the 32 x 32 block O below the band (this fills O: the
+//   bulge), builds a reflector from O's first column, applies it from the left to O and
+//   two-sided to the next diagonal block.  Task (s, k) touches elements of sweep s - 1 only in
+//   its tasks k' <= k + 1, so the sweeps run as a pipeline: one wave per sweep, each task started
+//   once the previous sweep has finished two more tasks.  A work-group's waves take consecutive
+//   sweeps and hand over through LDS counters; work-groups hand over through progress counters in
+//   global memory (agent-scope release / acquire), once per NW sweeps.  Every wait is bounded.
+// Back-transformation of stage 2: the reflectors of the 32 sweeps of group g at chase step k act
+//   on the 63 rows 32 g + 1 + 32 k .. + 62; their product is formed once as an explicit 64 x 64
+//   matrix, and the eigenvector matrix takes the blocks in an order that keeps every reflector's
+//   position relative to those it overlaps (groups last to first, steps in increasing order), one
+//   64 x 64 x 64 MFMA product per block and 64-eigenvector slab.
+//
+// Band storage: AB[j * kABld + d] = A[j + d][j] for d < 64 (d <= 32 the band, d > 32 the room the
+// bulges need), with zero columns past n - 1 so the last tasks read and write zeros there.
+#include "eigh_band.h"
+#include "gemm.h"
+
+namespace mpq {
+namespace band {
+namespace {
+
+constexpr int kThr = 256;
+constexpr int kProgStride = 4096;  // progress value = sweep * 4096 + tasks done (4095: finished)
+constexpr int kNW = 8;             // waves (sweeps) per bulge-chasing work-group
+
+inline int64_t al64(int64_t v) { return (v + 63) / 64 * 64; }
+
+// ---- stage 1: tall-skinny QR of a panel -------------------------------------------------------
+
+// Panel kernels: 1024 threads; thread (c = t % 32, s = t / 32) holds column c of rows s + 32 q
+// (q < R) in registers.  The 32 threads of one row phase s are one half of a wave, so a value of
+// column j reaches them by a 32-lane shuffle; the column sums over the 32 row phases are one
+// reduction through LDS (double-buffered by step parity: one barrier per reflector).
+constexpr int kPThr = 1024;
+
+// Orders one wave's LDS accesses (a compiler barrier plus the wave-scope fences).
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+struct PanelLds {
+  float red[2][16][32];
+  float rowj[2][32];
+  float tau[32];
+};
+
+// Sum over the 32 row phases of every thread's `acc` (column c), into red[buf]; returns after the
+// barrier with the column totals readable by every thread.
+__device__ __forceinline__ void phase_reduce(PanelLds& L, int buf, float acc) {
+  const int t = threadIdx.x;
+  acc += __shfl_xor(acc, 32);
+  if (((t >> 5) & 1) == 0) L.red[buf][t >> 6][t & 31] = acc;
+  __syncthreads();
+}
+__device__ __forceinline__ float phase_total(const PanelLds& L, int buf, int c) {
+  float v = 0.f;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) v += L.red[buf][w][c];
+  return v;
+}
+
+// Householder QR (LAPACK geqr2) of the rows x 32 matrix held in x, k = min(rows, 32) reflectors:
+// R on and above the diagonal, v below it (v_j = 1 implied), tau in L.tau.  One reduction per
+// reflector gives the norm of column j and every v^T P[:, c] at once (from the unscaled column).
+template <int R>
+__device__ void reg_geqr2(float (&x)[R], int rows, int k, PanelLds& L) {
+  const int t = threadIdx.x, c = t & 31, s = t >> 5;
+  for (int j = 0; j < k; ++j) {
+    const int buf = j & 1;
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      const float xj = __shfl(x[q], j, 32);
+      if (s + 32 * q > j) acc = fmaf(xj, x[q], acc);
+    }
+    if (s == j) L.rowj[buf][c] = x[0];  // row j of column c (j < 32: phase j, q = 0)
+    phase_reduce(L, buf, acc);
+    const float dc = phase_total(L, buf, c);
+    const float xn2 = phase_total(L, buf, j);
+    const float alpha = L.rowj[buf][j];
+    float tj = 0.f, beta = alpha, scal = 0.f;
+    if (xn2 > 0.f) {
+      beta = -copysignf(sqrtf(fmaf(alpha, alpha, xn2)), alpha);
+      tj = (beta - alpha) / beta;
+      scal = 1.f / (alpha - beta);
+    }
+    const float w = (c > j) ? tj * (L.rowj[buf][c] + scal * dc) : 0.f;  // tau v^T P[:, c]
+    // the shuffle reads column j before its own lanes rescale it (one instruction per q for all lanes)
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      const float xj = __shfl(x[q], j, 32);
+      const int i = s + 32 * q;
+      if (c > j) {
+        if (i >= j) x[q] = fmaf(-(i == j ? 1.f : xj * scal), w, x[q]);
+      } else if (c == j) {
+        if (i > j) x[q] *= scal;
+        else if (i == j) x[q] = beta;
+      }
+    }
+    if (t == 0) L.tau[j] = tj;
+  }
+  __syncthreads();
+}
+
+// Leaf l of the panel: rows l kLeaf .. of P = A[r0:r0+m, c0:c0+32].  Writes its reflectors (Yl,
+// rows of the panel), tau (taul[l * 32 ..], zero past k) and R (Rs rows 32 l .. 32 l + k - 1).
+__global__ __launch_bounds__(kPThr) void leaf_qr_kernel(const float* __restrict__ A, int64_t lda, int64_t r0,
+                                                        int64_t c0, int64_t m, float* __restrict__ Yl,
+                                                        float* __restrict__ taul, float* __restrict__ Rs,
+                                                        const int* __restrict__ fallback) {
+  if (*fallback == 0) return;  // the Cholesky QR path produced Q1 and R
+  constexpr int R = kLeaf / 32;
+  __shared__ PanelLds L;
+  const int t = threadIdx.x, c = t & 31, s = t >> 5;
+  const int64_t row0 = (int64_t)blockIdx.x * kLeaf;
+  const int rows = (int)min((int64_t)kLeaf, m - row0);
+  const int k = min(rows, 32);
+  float x[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+    const int i = s + 32 * q;
+    x[q] = i < rows ? A[(r0 + row0 + i) * lda + c0 + c] : 0.f;
+  }
+  if (t < 32) L.tau[t] = 0.f;
+  __syncthreads();
+  reg_geqr2<R>(x, rows, k, L);
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+    const int i = s + 32 * q;
+    if (i < rows) Yl[(row0 + i) * 32 + c] = x[q];
+    if (i < k) Rs[((int64_t)blockIdx.x * 32 + i) * 32 + c] = c >= i ? x[q] : 0.f;
+  }
+  if (t < 32) taul[blockIdx.x * 32 + t] = L.tau[t];
+}
+
+// Root of the TSQR: Householder QR of the stacked R factors (root_rows x 32, root_rows <= 1024),
+// R (k x 32, zero below) to Rroot, and E = the first k columns of its orthogonal factor (LAPACK
+// org2r; columns k..31 zero) to E (root_rows x 32).
+__global__ __launch_bounds__(kPThr) void root_qr_kernel(const float* __restrict__ Rs, int root_rows,
+                                                        float* __restrict__ Rroot, float* __restrict__ E,
+                                                        const int* __restrict__ fallback) {
+  if (*fallback == 0) return;
+  constexpr int R = 32;
+  __shared__ PanelLds L;
+  const int t = threadIdx.x, c = t & 31, s = t >> 5;
+  const int rows = root_rows;
+  const int k = min(rows, 32);
+  float x[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+    const int i = s + 32 * q;
+    x[q] = i < rows ? Rs[i * 32 + c] : 0.f;
+  }
+  if (t < 32) L.tau[t] = 0.f;
+  __syncthreads();
+  reg_geqr2<R>(x, rows, k, L);
+  if (s < 32) Rroot[s * 32 + c] = (s < k && c >= s) ? x[0] : 0.f;  // rows 0..31 are q = 0
+  // org2r: for j = k-1 .. 0, apply H_j to columns j+1 .. k-1 (rows >= j; their row j is zero, set
+  // when they were finished), then column j becomes -tau_j v below the diagonal, 1 - tau_j on it
+  // and zero above.
+  for (int j = k - 1; j >= 0; --j) {
+    const int buf = j & 1;
+    const float tj = L.tau[j];
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      const float vj = __shfl(x[q], j, 32);
+      if (s + 32 * q > j) acc = fmaf(vj, x[q], acc);
+    }
+    phase_reduce(L, buf, acc);
+    const float w = (c > j && c < k) ? tj * phase_total(L, buf, c) : 0.f;
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      const float vj = __shfl(x[q], j, 32);
+      const int i = s + 32 * q;
+      if (c > j && c < k) {
+        if (i >= j) x[q] = fmaf(-(i == j ? 1.f : vj), w, x[q]);
+      } else if (c == j) {
+        x[q] = i > j ? -tj * x[q] : (i == j ? 1.f - tj : 0.f);
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+    const int i = s + 32 * q;
+    if (i < rows) E[i * 32 + c] = c < k ? x[q] : 0.f;
+  }
+}
+
+// Q1 rows of leaf l: Q_leaf [E_l; 0] with E_l = E rows 32 l .. 32 l + k_l - 1 (the leaf's
+// reflectors applied last to first).
+__global__ __launch_bounds__(kPThr) void leaf_q_kernel(const float* __restrict__ Yl, const float* __restrict__ taul,
+                                                       const float* __restrict__ E, int64_t m,
+                                                       float* __restrict__ Q1, const int* __restrict__ fallback) {
+  if (*fallback == 0) return;
+  constexpr int R = kLeaf / 32;
+  __shared__ PanelLds L;
+  const int t = threadIdx.x, c = t & 31, s = t >> 5;
+  const int64_t row0 = (int64_t)blockIdx.x * kLeaf;
+  const int rows = (int)min((int64_t)kLeaf, m - row0);
+  const int k = min(rows, 32);
+  float v[R], b[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+    const int i = s + 32 * q;
+    v[q] = i < rows ? Yl[(row0 + i) * 32 + c] : 0.f;
+    b[q] = i < k ? E[((int64_t)blockIdx.x * 32 + i) * 32 + c] : 0.f;
+  }
+  for (int j = k - 1; j >= 0; --j) {
+    const float tj = taul[blockIdx.x * 32 + j];
+    if (tj == 0.f) continue;  // uniform
+    const int buf = j & 1;
+    float vj[R];
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      const int i = s + 32 * q;
+      const float sh = __shfl(v[q], j, 32);
+      vj[q] = i == j ? 1.f : (i > j ? sh : 0.f);
+      acc = fmaf(vj[q], b[q], acc);
+    }
+    phase_reduce(L, buf, acc);
+    const float w = tj * phase_total(L, buf, c);
+#pragma unroll
+    for (int q = 0; q < R; ++q) b[q] = fmaf(-vj[q], w, b[q]);
+  }
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+    const int i = s + 32 * q;
+    if (i < rows) Q1[(row0 + i) * 32 + c] = b[q];
+  }
+}
+
+// ---- stage 1 fast path: shifted Cholesky QR, three passes ----------------------------------------
+// Q1 R = P by Cholesky factorisations of 32 x 32 Gram matrices formed in fp64 (Fukaya, Kannan,
+// Nakatsukasa, Yamamoto, Yanagisawa, "Shifted Cholesky QR for computing the QR factorization of
+// ill-conditioned matrices", SIAM J. Sci. Comput. 2020): pass 1 factors P^T P + s I with
+// s = 11 (32 m + 32 * 33) 2^-53 |P|_F^2, passes 2 and 3 refactor the Gram matrix of the current Q
+// (Cholesky QR2).  R = R3 R2 R1.  A pass whose Cholesky factorisation meets a pivot <= 0, or a last
+// pass whose Gram matrix is not close to the identity, sets the panel's fallback flag: then the
+// tall-skinny Householder QR above runs instead (rank-deficient panels, e.g. zero panels).
+constexpr int kCqTile = 256;
+
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const unsigned long long u = __double_as_longlong(v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)u, l);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(u >> 32), l);
+  return __longlong_as_double(((unsigned long long)hi << 32) | lo);
+}
+
+// Cholesky G = L L^T of the 32 x 32 Gram matrix in G (fp64 LDS) by wave 0, with the pass's checks
+// (pass 1 adds the shift first).  Lane t holds row t in registers; pivots and the pivot column come
+// by readlane (loops unrolled, register indices static).  On success the lower triangle of G holds
+// L; on failure *bad = 1.
+__device__ void cq_cholesky(double (*G)[33], int pass, int64_t m, int* bad) {
+  const int t = threadIdx.x;
+  if (t >= 64) return;  // caller checks *bad after a block barrier
+  double row[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) row[c] = t < 32 ? G[t][c] : 0.0;
+  if (pass == 1) {
+    double tr = 0.0;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) tr += readlane_f64(row[c], c);
+    const double shift = 11.0 * (32.0 * (double)m + 32.0 * 33.0) * 0x1p-53 * tr;
+#pragma unroll
+    for (int c = 0; c < 32; ++c)
+      if (t == c) row[c] += shift;
+  }
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const double d = readlane_f64(row[i], i);
+    ok = ok && d > 0.0 && (pass != 3 || (d > 0.5 && d < 2.0));
+    const double lii = sqrt(ok ? d : 1.0);
+    const double inv = 1.0 / lii;
+    const double lti = row[i] * inv;  // L[t][i] for t > i
+    if (t == i) row[i] = lii;
+    else if (t > i) row[i] = lti;
+#pragma unroll
+    for (int c = i + 1; c < 32; ++c) {
+      const double lci = readlane_f64(lti, c);  // L[c][i]
+      if (t >= c) row[c] = fma(-lti, lci, row[c]);
+    }
+  }
+  if (!ok) {
+    if (t == 0) *bad = 1;
+    return;
+  }
+  if (t < 32)
+#pragma unroll
+    for (int c = 0; c < 32; ++c) G[t][c] = row[c];
+}
+
+// Rows of the work-group's chunk: y = p R^-1 (R upper triangular, fp64; none in pass 1) stored to
+// Qout, and, for chol_pass > 0, the partial Gram sum y^T y in fp64.  The last work-group to finish
+// (atomic counter) sums the partials in work-group order, factors them (pass chol_pass), writes R
+// to Rcur for the next launch and R_tot <- R R_tot (pass 3: R_tot to Rroot in fp32), or raises
+// the fallback flag.  Every work-group reads Rcur before it counts itself in, so rewriting it is safe.
+__global__ __launch_bounds__(kThr) void cq_pass_kernel(const float* __restrict__ src, int64_t ld, int64_t m,
+                                                       int64_t chunk, double* __restrict__ Rcur,
+                                                       int use_rcur, float* __restrict__ Qout,
+                                                       double* __restrict__ Gp, int chol_pass,
+                                                       double* __restrict__ Rtot, float* __restrict__ Rroot,
+                                                       int* __restrict__ fallback, unsigned* __restrict__ counter) {
+  if (*fallback != 0) return;
+  __shared__ double sR[32][33];
+  __shared__ float tile[kCqTile][33];
+  __shared__ double G[32][33];
+  __shared__ int bad, last;
+  const int t = threadIdx.x;
+  __shared__ double sRinv[32];
+  if (use_rcur) {
+    for (int e = t; e < 1024; e += kThr) sR[e >> 5][e & 31] = Rcur[e];
+    if (t < 32) sRinv[t] = 1.0 / Rcur[t * 33];
+  }
+  __syncthreads();
+  const int64_t rbeg = (int64_t)blockIdx.x * chunk;
+  const int64_t rend = min(m, rbeg + chunk);
+  // Gram entries (i0 + a, j0 + b), a, b < 2, of this thread
+  const int i0g = 2 * (t >> 4), j0g = 2 * (t & 15);
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  for (int64_t r0 = rbeg; r0 < rend; r0 += kCqTile) {
+    const int64_t r = r0 + t;
+    float y[32];
+    if (r < rend) {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) y[j] = src[r * ld + j];
+      if (use_rcur) {
+        double yd[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+          double a = (double)y[j];
+#pragma unroll
+          for (int i = 0; i < j; ++i) a = fma(-yd[i], sR[i][j], a);
+          yd[j] = a * sRinv[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+          y[j] = (float)yd[j];
+          Qout[r * 32 + j] = y[j];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) y[j] = 0.f;
+    }
+    if (chol_pass > 0) {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) tile[t][j] = y[j];
+      __syncthreads();
+      const int rows = (int)min((int64_t)kCqTile, rend - r0);
+      for (int rr = 0; rr < rows; ++rr) {
+        const double yi0 = (double)tile[rr][i0g], yi1 = (double)tile[rr][i0g + 1];
+        const double yj0 = (double)tile[rr][j0g], yj1 = (double)tile[rr][j0g + 1];
+        acc[0] = fma(yi0, yj0, acc[0]);
+        acc[1] = fma(yi0, yj1, acc[1]);
+        acc[2] = fma(yi1, yj0, acc[2]);
+        acc[3] = fma(yi1, yj1, acc[3]);
+      }
+      __syncthreads();
+    }
+  }
+  if (chol_pass == 0) return;
+  {
+    double* gp = Gp + (int64_t)blockIdx.x * 1024;
+    gp[i0g * 32 + j0g] = acc[0];
+    gp[i0g * 32 + j0g + 1] = acc[1];
+    gp[(i0g + 1) * 32 + j0g] = acc[2];
+    gp[(i0g + 1) * 32 + j0g + 1] = acc[3];
+  }
+  // the last work-group to finish reduces and factors
+  __threadfence();
+  __syncthreads();
+  if (t == 0) {
+    const unsigned prev = atomicAdd(counter, 1u);
+    last = prev == gridDim.x - 1;
+    bad = 0;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  for (int e = t; e < 1024; e += kThr) {
+    double a = 0.0;
+    for (int g = 0; g < (int)gridDim.x; ++g) a += __hip_atomic_load(&Gp[(int64_t)g * 1024 + e], __ATOMIC_RELAXED,
+                                                                     __HIP_MEMORY_SCOPE_AGENT);
+    G[e >> 5][e & 31] = a;
+  }
+  if (t == 0) *counter = 0u;  // ready for the next launch
+  __syncthreads();
+  cq_cholesky(G, chol_pass, m, &bad);
+  __syncthreads();
+  if (bad) {
+    if (t == 0) *fallback = 1;
+    return;
+  }
+  // R = L^T (upper); R_tot <- R R_tot
+  for (int e = t; e < 1024; e += kThr) {
+    const int i = e >> 5, j = e & 31;
+    Rcur[e] = j >= i ? G[j][i] : 0.0;
+  }
+  if (chol_pass == 1) {
+    for (int e = t; e < 1024; e += kThr) {
+      const int i = e >> 5, j = e & 31;
+      Rtot[e] = j >= i ? G[j][i] : 0.0;
+    }
+    return;
+  }
+  for (int e = t; e < 1024; e += kThr) sR[e >> 5][e & 31] = Rtot[e];
+  __syncthreads();
+  for (int e = t; e < 1024; e += kThr) {
+    const int i = e >> 5, j = e & 31;
+    double a = 0.0;
+    for (int l = i; l <= j; ++l) a = fma(G[l][i], sR[l][j], a);  // R[i][l] = L[l][i]
+    Rtot[e] = j >= i ? a : 0.0;
+    if (chol_pass == 3) Rroot[e] = j >= i ? (float)a : 0.f;
+  }
+}
+
+// Householder reconstruction from Q1 (m x 32, kk = min(m, 32) columns used) and the panel's
+// results.  Every work-group factors the kk x kk top block redundantly (cheap) and then handles
+// 256 panel rows: Y row = L row (top block) or Q1 row U^-1, YT row = Y row T; the reflectors go
+// to the rows of A (row c0 + j holds Y[r][j] at column r0 + r, r > j).  Work-group 0 also
+// writes T, tau and the band block A[r0 + i][c0 + j] = (S R)[i][j] (j >= i, zero below).
+__global__ __launch_bounds__(kThr) void hr_kernel(const float* __restrict__ Q1, const float* __restrict__ Rroot,
+                                                  int64_t m, float* __restrict__ A, int64_t lda, int64_t r0,
+                                                  int64_t c0, float* __restrict__ Y, float* __restrict__ YT,
+                                                  float* __restrict__ Tout, float* __restrict__ tau) {
+  __shared__ float LU[32][33];
+  __shared__ float Xi[32][33];  // L1^-T
+  __shared__ float Ts[32][33];
+  __shared__ float S[32];
+  const int kk = (int)min<int64_t>(m, 32);
+  const int t = threadIdx.x;
+  for (int e = t; e < 32 * 32; e += kThr) {
+    const int i = e / 32, j = e & 31;
+    LU[i][j] = (i < kk && j < kk) ? Q1[i * 32 + j] : 0.f;
+  }
+  __syncthreads();
+  // LU without pivoting of Q1 - S, S_i = -sign of the current pivot (|U_ii| >= 1): wave 0, lane r
+  // holds row r in registers, pivot rows by readlane (loops unrolled: register indices are static)
+  if (t < 64) {
+    float row[32];
+#pragma unroll
+    for (int c = 0; c < 32; ++c) row[c] = t < 32 ? LU[t][c] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      if (i < kk) {
+        // pivot row i, read by every lane before any lane changes its registers
+        float prow[32];
+#pragma unroll
+        for (int c = i; c < 32; ++c) prow[c] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(row[c]), i));
+        const float si = prow[i] >= 0.f ? -1.f : 1.f;
+        const float p = prow[i] - si;
+        if (t == i) row[i] = p;
+        if (t > i && t < kk) {
+          const float l = row[i] / p;
+          row[i] = l;
+#pragma unroll
+          for (int c = i + 1; c < 32; ++c) row[c] = fmaf(-l, prow[c], row[c]);
+        }
+        if (t == 0) S[i] = si;
+      }
+    }
+    if (t < 32) {
+#pragma unroll
+      for (int c = 0; c < 32; ++c) LU[t][c] = row[c];
+    }
+  }
+  __syncthreads();
+  // Xi = L1^-T (unit upper): column j by back substitution, Xi[i][j] = -sum_{l=i+1..j} L1[l][i] Xi[l][j]
+  if (t < 32) {
+    const int j = t;
+    for (int i = 0; i < 32; ++i) Xi[i][j] = i == j && j < kk ? 1.f : 0.f;
+    if (j < kk)
+      for (int i = j - 1; i >= 0; --i) {
+        float acc = 0.f;
+        for (int l = i + 1; l <= j; ++l) acc = fmaf(LU[l][i], Xi[l][j], acc);
+        Xi[i][j] = -acc;
+      }
+  }
+  __syncthreads();
+  // T = -U S Xi (upper)
+  for (int e = t; e < 32 * 32; e += kThr) {
+    const int i = e / 32, j = e & 31;
+    float acc = 0.f;
+    if (i <= j && j < kk)
+      for (int l = i; l <= j; ++l) acc = fmaf(LU[i][l] * S[l], Xi[l][j], acc);
+    Ts[i][j] = -acc;
+  }
+  __syncthreads();
+  const int64_t r = (int64_t)blockIdx.x * kThr + t;
+  if (r < m) {
+    float y[32];
+    if (r < kk) {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) y[j] = j < r ? LU[r][j] : (j == r ? 1.f : 0.f);
+    } else {
+      const float* q = Q1 + r * 32;
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        float acc = j < kk ? q[j] : 0.f;
+        for (int i = 0; i < j; ++i) acc = fmaf(-y[i], LU[i][j], acc);
+        y[j] = j < kk ? acc / LU[j][j] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) Y[r * 32 + j] = y[j];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      float acc = 0.f;
+      for (int i = 0; i <= j; ++i) acc = fmaf(y[i], Ts[i][j], acc);
+      YT[r * 32 + j] = acc;
+    }
+    for (int j = 0; j < kk && j < r; ++j) A[(c0 + j) * lda + r0 + r] = y[j];
+  }
+  if (blockIdx.x == 0) {
+    for (int e = t; e < 32 * 32; e += kThr) Tout[e] = Ts[e / 32][e & 31];
+    if (t < 32) tau[c0 + t] = t < kk ? Ts[t][t] : 0.f;
+    const int rows = kk;
+    for (int e = t; e < rows * 32; e += kThr) {
+      const int i = e / 32, j = e & 31;
+      A[(r0 + i) * lda + c0 + j] = j >= i ? S[i] * Rroot[i * 32 + j] : 0.f;
+    }
+  }
+}
+
+// Partial grams Gp[g] = Y^T X over the rows of chunk g (64-row tiles staged in LDS).
+__global__ __launch_bounds__(kThr) void gram_partial_kernel(const float* __restrict__ Y, const float* __restrict__ X,
+                                                            int64_t m, int64_t chunk, float* __restrict__ Gp) {
+  __shared__ float sY[64][33];
+  __shared__ float sX[64][33];
+  const int t = threadIdx.x;
+  const int64_t rbeg = (int64_t)blockIdx.x * chunk;
+  const int64_t rend = min(m, rbeg + chunk);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t r0 = rbeg; r0 < rend; r0 += 64) {
+    for (int e = t; e < 64 * 32; e += kThr) {
+      const int64_t r = r0 + e / 32;
+      sY[e / 32][e & 31] = r < rend ? Y[r * 32 + (e & 31)] : 0.f;
+      sX[e / 32][e & 31] = r < rend ? X[r * 32 + (e & 31)] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = t + q * kThr, i = e / 32, j = e & 31;
+      float a = acc[q];
+      for (int rr = 0; rr < 64; ++rr) a = fmaf(sY[rr][i], sX[rr][j], a);
+      acc[q] = a;
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) Gp[(int64_t)blockIdx.x * 1024 + t + q * kThr] = acc[q];
+}
+
+// M = T^T (sum_g Gp[g]) (32 x 32): one work-group of 1024 threads, one entry each.
+__global__ __launch_bounds__(1024) void m_kernel(const float* __restrict__ Gp, int ng, const float* __restrict__ T,
+                                                 float* __restrict__ Mout) {
+  __shared__ float G[32][33];
+  const int e = threadIdx.x, i = e >> 5, j = e & 31;
+  float a = 0.f;
+  for (int g = 0; g < ng; ++g) a += Gp[(int64_t)g * 1024 + e];
+  G[i][j] = a;
+  __syncthreads();
+  float mv = 0.f;
+  for (int l = 0; l < 32; ++l) mv = fmaf(T[l * 32 + i], G[l][j], mv);
+  Mout[e] = mv;
+}
+
+// W = X - 1/2 Y M and the update operands Xop = [Y W], Yop = [W Y] (m x 64 each).
+__global__ __launch_bounds__(kThr) void w_kernel(const float* __restrict__ Mg, const float* __restrict__ Y,
+                                                 const float* __restrict__ X, int64_t m, float* __restrict__ Xop,
+                                                 float* __restrict__ Yop) {
+  __shared__ float M[32][33];
+  const int t = threadIdx.x;
+  for (int e = t; e < 1024; e += kThr) M[e >> 5][e & 31] = Mg[e];
+  __syncthreads();
+  const int64_t r = (int64_t)blockIdx.x * kThr + t;
+  if (r >= m) return;
+  float y[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) y[j] = Y[r * 32 + j];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    float a = 0.f;
+    for (int l = 0; l < 32; ++l) a = fmaf(y[l], M[l][j], a);
+    const float w = fmaf(-0.5f, a, X[r * 32 + j]);
+    Xop[r * 64 + j] = y[j];
+    Xop[r * 64 + 32 + j] = w;
+    Yop[r * 64 + j] = w;
+    Yop[r * 64 + 32 + j] = y[j];
+  }
+}
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// Split-K partials of X = A22 B with B = Y T (m x 32), from the lower triangle of A22 only (the
+// trailing update keeps the lower triangle and the 32 x 32 diagonal blocks current):
+//   pass 0 (row strips):    P0[ks][r][:] = sum_{k in split ks, k < 32 (r / 32 + 1)} A22[r][k] B[k][:]
+//   pass 1 (column strips): P1[ks][r][:] = sum_{i in split ks, i >= 32 (r / 32 + 1)} A22[i][r] B[i][:]
+// X = the sum of all partials.  Wave w of a work-group owns output rows 128 bx + 32 w .. + 31 (one
+// 32 x 32 MFMA tile).  Pass 0: in each 64-k step lane (row, h) feeds k = kt + 32 h + j to MFMA j, so
+// it streams 32 consecutive floats of its row; pass 1: lane (c, h) feeds i = it + 32 h + j, and for
+// each j the 32 lanes of a half read one contiguous row segment A22[i][32 J .. 32 J + 31].
+constexpr int kXKC = 512;  // k per split
+template <int kPass>
+__global__ __launch_bounds__(kThr) void xprod_kernel(const float* __restrict__ A, int64_t lda,
+                                                     const float* __restrict__ B, int64_t m, float* __restrict__ P) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = lane & 31, h = lane >> 5;
+  const int64_t rbase = (int64_t)blockIdx.x * 128 + wave * 32;  // this wave's 32 output rows
+  const int64_t r = rbase + row;
+  const int64_t rc = r < m ? r : m - 1;
+  const int64_t lim = rbase + 32;  // pass 0: k < lim; pass 1: i >= lim
+  int64_t k0 = (int64_t)blockIdx.y * kXKC, k1 = min(m, k0 + kXKC);
+  if (kPass == 0) k1 = min(k1, lim);
+  else k0 = max(k0, lim);
+  floatx16 acc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[v] = 0.f;
+  if (rbase < m) {
+    for (int64_t kt = k0; kt < k1; kt += 64) {
+      const int64_t kb = kt + 32 * h;
+      float av[32], bv[32];
+      if (kPass == 0 && kt + 64 <= k1 && (kb & 3) == 0) {
+        const float4* ap = reinterpret_cast<const float4*>(A + rc * lda + kb);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const float4 f = ap[q];
+          av[4 * q] = f.x;
+          av[4 * q + 1] = f.y;
+          av[4 * q + 2] = f.z;
+          av[4 * q + 3] = f.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 32; ++j) bv[j] = B[(kb + j) * 32 + row];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+          const int64_t kk = kb + j;
+          const bool in = kk < k1;
+          const int64_t kc = in ? kk : k0;
+          av[j] = in ? (kPass == 0 ? A[rc * lda + kc] : A[kc * lda + rc]) : 0.f;
+          bv[j] = in ? B[kc * 32 + row] : 0.f;
+        }
+      }
+      if (r >= m) {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) av[j] = 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 32; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[j], bv[j], acc, 0, 0, 0);
+    }
+  }
+  float* Ps = P + ((int64_t)kPass * gridDim.y + blockIdx.y) * m * 32;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int64_t rr = rbase + 8 * (v >> 2) + 4 * h + (v & 3);
+    if (rr < m) Ps[rr * 32 + row] = acc[v];
+  }
+}
+
+// X = sum of the partials in split order.
+__global__ __launch_bounds__(kThr) void xsum_kernel(const float* __restrict__ P, int splits, int64_t cnt,
+                                                    float* __restrict__ X) {
+  const int64_t e = (int64_t)blockIdx.x * kThr + threadIdx.x;
+  if (e >= cnt) return;
+  float a = P[e];
+  for (int s2 = 1; s2 < splits; ++s2) a += P[(int64_t)s2 * cnt + e];
+  X[e] = a;
+}
+
+// ---- stage 2: bulge chasing ------------------------------------------------------------------
+
+// AB[j][d] = A[j + d][j] for d <= kBW inside the matrix, zero elsewhere (columns up to n + kABpad).
+__global__ __launch_bounds__(kThr) void band_extract_kernel(const float* __restrict__ A, int64_t lda, int64_t n,
+                                                            float* __restrict__ AB) {
+  const int64_t e = (int64_t)blockIdx.x * kThr + threadIdx.x;
+  if (e >= (n + kABpad) * kABld) return;
+  const int64_t j = e / kABld;
+  const int d = (int)(e % kABld);
+  AB[e] = (d <= kBW && j + d < n) ? A[(j + d) * lda + j] : 0.f;
+}
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Wave sums without LDS: rotate-and-add inside each 16-lane row (DPP row_ror 8, 4, 2, 1), then the
+// row pairs and the two halves through v_permlane16_swap / v_permlane32_swap, whose two results
+// hold the even/odd row (lower/upper half) of each pair, so their sum is own + partner.  Every lane
+// adds the same operands (only commuted), so every lane holds the same bits.
+template <int kCtrl>
+__device__ __forceinline__ float ror_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float half_pair_sum(float v) {  // v + (lane ^ 32)'s v
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float wave_sum64(float v) {
+  v = ror_add<0x128>(v);
+  v = ror_add<0x124>(v);
+  v = ror_add<0x122>(v);
+  v = ror_add<0x121>(v);
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  return half_pair_sum(v);
+}
+
+// Reflector of x (32 entries, lane a of each half holds x[a]): returns tau, beta and v (v_0 = 1).
+struct Refl {
+  float tau, beta, scal;
+};
+__device__ __forceinline__ Refl make_refl(float x, int a, int h) {
+  const float sq = (h == 0 && a >= 1) ? x * x : 0.f;
+  const float xn2 = wave_sum64(sq);
+  const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  Refl r{0.f, alpha, 0.f};
+  if (xn2 > 0.f) {
+    r.beta = -copysignf(sqrtf(fmaf(alpha, alpha, xn2)), alpha);
+    r.tau = (r.beta - alpha) / r.beta;
+    r.scal = 1.f / (alpha - r.beta);
+  }
+  return r;
+}
+
+// Two-sided D <- H D H (D symmetric, full 32 x 32 in LDS), H = I - tau v v^T, v in sv.
+__device__ __forceinline__ void two_sided(float (*D)[33], const float* sv, float* sy, float tau, int a, int h) {
+  const float va = sv[a];
+  float w = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int c = 16 * h + q;
+    w = fmaf(D[a][c], sv[c], w);
+  }
+  w = half_pair_sum(w);
+  const float vw = wave_sum64(h == 0 ? va * w : 0.f);
+  const float y = tau * w - 0.5f * tau * tau * vw * va;
+  if (h == 0) sy[a] = y;
+  wave_sync();
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int c = 16 * h + q;
+    D[a][c] = D[a][c] - (va * sy[c] + y * sv[c]);
+  }
+  wave_sync();
+}
+
+struct BulgeArgs {
+  float* AB;
+  int64_t n;
+  float* V2;    // stage-2 reflectors: block (g, k) at (boff(g) + k) * 1024, sweep 32 g + i at row i
+  float* tau2;  // (boff(g) + k) * 32 + i
+  int* gprog;   // progress of the last sweep of every NW-sweep group (global)
+  int* status;  // 0 ok, 1 a wait ran out
+  int64_t spin_limit;
+};
+
+__device__ __forceinline__ int64_t boff(int64_t g, int64_t K0) { return g * (K0 + 1) - g * (g - 1) / 2; }
+
+// One wave per sweep; the NW waves of a work-group take sweeps grp NW .. grp NW + NW - 1 for
+// grp = blockIdx.x, blockIdx.x + gridDim.x, ...  Cooperative launch (all work-groups resident).
+__global__ __launch_bounds__(64 * kNW) void bulge_kernel(BulgeArgs args) {
+  __shared__ float sD[kNW][32][33];
+  __shared__ float sO[kNW][32][33];
+  __shared__ float sv[kNW][2][32];
+  __shared__ float sy[kNW][32];
+  __shared__ int lprog[kNW];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, a = lane & 31, h = lane >> 5;
+  float* __restrict__ AB = args.AB;
+  const int64_t n = args.n;
+  const int64_t K0 = (n - 2) / kBW;
+  float(*D)[33] = sD[w];
+  float(*O)[33] = sO[w];
+  if (lane == 0) lprog[w] = -1;
+  __syncthreads();
+  const int64_t nsweeps = n - 1;
+  const int64_t ngroups = (nsweeps + kNW - 1) / kNW;
+  for (int64_t grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {
+    const int64_t s = grp * kNW + w;
+    if (s >= nsweeps) break;
+    const int64_t K = (n - 2 - s) / kBW;                    // last chase step of this sweep
+    const int64_t Kp = s > 0 ? (n - 1 - s) / kBW : 0;       // last chase step of sweep s - 1
+    int seen = -1;
+    int cur = 0;       // which sv buffer holds the current reflector
+    float tau_prev = 0.f;
+    for (int64_t k = 0; k <= K; ++k) {
+      // wait until sweep s - 1 has finished its tasks up to k + 1
+      if (s > 0) {
+        const int need = (int)((s - 1) * kProgStride + min(k + 2, Kp + 1));
+        if (seen < need) {
+          int64_t it = 0;
+          for (;;) {
+            // relaxed polls; the acquire (for the other work-group: an L2 invalidation) only once the
+            // condition holds
+            int v;
+            if (w > 0) {
+              v = __hip_atomic_load(&lprog[w - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            } else {
+              v = __hip_atomic_load(&args.gprog[grp - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (v >= need) {
+              if (w > 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+              else __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+              seen = v;
+              break;
+            }
+            if (++it > args.spin_limit ||
+                ((it & 255) == 0 &&
+                 __hip_atomic_load(args.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)) {
+              if (lane == 0) __hip_atomic_store(args.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              return;
+            }
+            __builtin_amdgcn_s_sleep(2);
+          }
+        }
+      }
+      const int64_t g = s / kBW, bid = boff(g, K0) + k;
+      float* vcur = sv[w][cur];
+      const float* vprev = sv[w][cur ^ 1];
+      Refl rf;
+      int64_t r0;
+      // every load of the task is issued before the first use (one memory round trip): the lane
+      // reads D[a][cc] for its 16 columns cc = h, h + 2, ... from the stored lower triangle (the
+      // upper entries through their mirror) and, for k >= 1, the same entries of O
+      r0 = k == 0 ? s + 1 : s + 1 + k * kBW;
+      const int64_t p0 = r0 - kBW;
+      // wave-uniform bases, 32-bit lane offsets (few live registers across the loads)
+      float* __restrict__ ABr = AB + r0 * kABld;
+      float* __restrict__ ABp = AB + p0 * kABld;
+      float dv[16], ov[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int cc = h + 2 * q;
+        dv[q] = ABr[a >= cc ? cc * kABld + (a - cc) : a * kABld + (cc - a)];
+      }
+      if (k > 0) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int cc = h + 2 * q;
+          ov[q] = ABp[cc * kABld + (a + 32 - cc)];
+        }
+      }
+      const float x0 = k == 0 ? AB[s * kABld + 1 + a] : 0.f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) D[a][h + 2 * q] = dv[q];
+      if (k == 0) {
+        // column s below the subdiagonal: AB[s][1 .. 32]
+        rf = make_refl(x0, a, h);
+        if (h == 0) {
+          vcur[a] = a == 0 ? 1.f : x0 * rf.scal;
+          AB[s * kABld + 1 + a] = a == 0 ? rf.beta : 0.f;
+        }
+        wave_sync();
+      } else {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) O[a][h + 2 * q] = ov[q];
+        wave_sync();
+        // O <- O H_prev (rows: lane's row a, columns in its half)
+        float u = 0.f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) u = fmaf(O[a][16 * h + q], vprev[16 * h + q], u);
+        u = half_pair_sum(u);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) O[a][16 * h + q] = fmaf(-tau_prev * u, vprev[16 * h + q], O[a][16 * h + q]);
+        wave_sync();
+        const float x = O[a][0];
+        rf = make_refl(x, a, h);
+        if (h == 0) vcur[a] = a == 0 ? 1.f : x * rf.scal;
+        wave_sync();
+        // O <- H O (column a of the lane, rows in its half); column 0 becomes (beta, 0, ...)
+        float z = 0.f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) z = fmaf(vcur[16 * h + q], O[16 * h + q][a], z);
+        z = half_pair_sum(z);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int i = 16 * h + q;
+          O[i][a] = a == 0 ? (i == 0 ? rf.beta : 0.f) : fmaf(-rf.tau * z, vcur[i], O[i][a]);
+        }
+        wave_sync();
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int cc = h + 2 * q;
+          ABp[cc * kABld + (a + 32 - cc)] = O[a][cc];
+        }
+      }
+      two_sided(D, vcur, sy[w], rf.tau, a, h);
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int cc = h + 2 * q;
+        if (a >= cc) ABr[cc * kABld + (a - cc)] = D[a][cc];
+      }
+      if (h == 0) args.V2[(bid * 32 + (s % kBW)) * 32 + a] = vcur[a];
+      if (lane == 0) args.tau2[bid * 32 + (s % kBW)] = rf.tau;
+      tau_prev = rf.tau;
+      cur ^= 1;
+      // publish
+      const int val = (int)(s * kProgStride + (k == K ? kProgStride - 1 : k + 1));
+      if (w == kNW - 1) {
+        if (lane == 0) __hip_atomic_store(&args.gprog[grp], val, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        if (lane == 0) __hip_atomic_store(&lprog[w], val, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThr) void fill_int_kernel(int* __restrict__ p, int64_t count, int v) {
+  const int64_t e = (int64_t)blockIdx.x * kThr + threadIdx.x;
+  if (e < count) p[e] = v;
+}
+
+__global__ __launch_bounds__(kThr) void tridiag_out_kernel(const float* __restrict__ AB, int64_t n,
+                                                           float* __restrict__ D, float* __restrict__ E) {
+  const int64_t j = (int64_t)blockIdx.x * kThr + threadIdx.x;
+  if (j >= n) return;
+  D[j] = AB[j * kABld];
+  if (j + 1 < n) E[j] = AB[j * kABld + 1];
+}
+
+// ---- back-transformation of stage 2 ----------------------------------------------------------
+
+// Block (g, k): Pt = H_31 ... H_0 over the window rows 32 g + 1 + 32 k .. + 63, H_i the reflector
+// of sweep 32 g + i at step k (acting on window rows i .. i + 31; identity where it does not
+// exist).  One work-group per block; thread (c = t % 64, q = t / 64) owns column c, rows q (mod 4).
+__global__ __launch_bounds__(kThr) void q2_build_kernel(const float* __restrict__ V2, const float* __restrict__ tau2,
+                                                        int64_t n, float* __restrict__ Pt) {
+  __shared__ float M[64][65];
+  __shared__ float sv[32];
+  __shared__ float red[4][64];
+  const int64_t K0 = (n - 2) / kBW;
+  // block index -> (g, k): boff(g) <= bid < boff(g + 1)
+  const int64_t bid = blockIdx.x;
+  int64_t g = 0;
+  {
+    int64_t lo = 0, hi = K0;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) / 2;
+      if (boff(mid, K0) <= bid) lo = mid;
+      else hi = mid - 1;
+    }
+    g = lo;
+  }
+  const int64_t k = bid - boff(g, K0);
+  const int t = threadIdx.x, c = t & 63, q = t >> 6;
+  for (int e = t; e < 64 * 64; e += kThr) M[e / 64][e & 63] = (e / 64) == (e & 63) ? 1.f : 0.f;
+  __syncthreads();
+  for (int i = 0; i < 32; ++i) {
+    const int64_t s = g * kBW + i;
+    const bool exists = s <= n - 2 && k <= (n - 2 - s) / kBW;
+    const float tau = exists ? tau2[bid * 32 + i] : 0.f;
+    if (tau == 0.f) continue;  // uniform
+    if (t < 32) sv[t] = V2[(bid * 32 + i) * 32 + t];
+    __syncthreads();
+    float z = 0.f;
+    for (int aa = q; aa < 32; aa += 4) z = fmaf(sv[aa], M[i + aa][c], z);
+    red[q][c] = z;
+    __syncthreads();
+    const float zc = tau * ((red[0][c] + red[1][c]) + (red[2][c] + red[3][c]));
+    for (int aa = q; aa < 32; aa += 4) M[i + aa][c] = fmaf(-sv[aa], zc, M[i + aa][c]);
+    __syncthreads();
+  }
+  float* out = Pt + bid * 4096;
+  for (int e = t; e < 64 * 64; e += kThr) out[e] = M[e / 64][e & 63];
+}
+
+
+// Zb[z0 .. z0 + 63][:] <- Zb[...] Q2^T: groups last to first, steps in increasing order, each block
+// Zb[:, lo .. lo + 63] <- Zb[:, lo .. lo + 63] Pt(g, k).  Consecutive steps overlap by 32 columns:
+// the right half of a block's result stays in LDS as the left half of the next block's input.
+// Two groups run at once: waves 0-3 take group g (the lead), waves 4-7 group g - 1 three steps
+// behind (block k of group g - 1 reads only columns the lead's blocks <= k have finished; its
+// prefetch, two blocks ahead, reads the lead's left halves of the previous step).  Each half has
+// its own LDS window and matrix and keeps the matrices and new columns of its next two blocks in
+// registers while it runs on the matrix cores.  One 32 x 32 output tile per wave
+// (v_mfma_f32_32x32x2f32, K = 64), two accumulator chains.
+struct Q2Pref {
+  float m[16], z[8];
+};
+
+__device__ __forceinline__ void q2_prefetch(Q2Pref& p, const float* __restrict__ Pt, const float* __restrict__ Zb,
+                                            int64_t bidx, int64_t col0, int64_t z0, int rows, int64_t n, int lt) {
+  const float* M = Pt + bidx * 4096;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) p.m[q] = M[lt + q * 256];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int e = lt + q * 256, r = e >> 5, cc = e & 31;
+    p.z[q] = (r < rows && col0 + cc < n) ? Zb[(z0 + r) * n + col0 + cc] : 0.f;
+  }
+}
+
+__global__ __launch_bounds__(512) void q2_apply_kernel(const float* __restrict__ Pt, float* __restrict__ Zb,
+                                                       int64_t n) {
+  __shared__ float sM[2][64][65];
+  __shared__ float sZ[2][64][65];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int half = wave >> 2, lt = t & 255;
+  const int tm = (wave >> 1) & 1, tn = wave & 1;
+  const int64_t z0 = (int64_t)blockIdx.x * 64;
+  const int rows = (int)min((int64_t)64, n - z0);
+  const int64_t K0 = (n - 2) / kBW;
+  const int kl = lane >> 5, ml = lane & 31;
+  float(*Z)[65] = sZ[half];
+  float(*M)[65] = sM[half];
+  Q2Pref pa, pb;
+  for (int64_t gl = K0; gl >= 0; gl -= 2) {
+    const int64_t g = gl - half;                 // this half's group (< 0: idle)
+    const int64_t nk = g >= 0 ? K0 + 1 - g : 0;
+    const int64_t nk_lag = gl >= 1 ? K0 + 2 - gl : 0;
+    const int64_t steps = max(K0 + 1 - gl, nk_lag > 0 ? 3 + nk_lag : (int64_t)0);
+    const int64_t S = 3 * half;
+    const int64_t base = g >= 0 ? boff(g, K0) : 0;
+    int64_t lo = g * kBW + 1;
+    for (int64_t T = 0; T < steps; ++T) {
+      const int64_t k = T - S;
+      const bool active = k >= 0 && k < nk;
+      if (active && k == 0) {
+        // first block of the group: window and matrix straight into LDS
+        for (int e = lt; e < 64 * 64; e += 256) {
+          const int r = e >> 6, cc = e & 63;
+          Z[r][cc] = (r < rows && lo + cc < n) ? Zb[(z0 + r) * n + lo + cc] : 0.f;
+          M[r][cc] = Pt[base * 4096 + e];
+        }
+        // block j's new columns are lo_j + 32 .. lo_j + 63 with lo_j = lo + 32 j
+        if (nk > 1) q2_prefetch(pa, Pt, Zb, base + 1, lo + 64, z0, rows, n, lt);
+      }
+      __syncthreads();
+      floatx16 acc0, acc1;
+      if (active) {
+        if (k + 2 < nk) q2_prefetch(pb, Pt, Zb, base + k + 2, lo + 96, z0, rows, n, lt);
+        // every operand first (one LDS wait), then two independent accumulator chains
+        float av[32], bv[32];
+#pragma unroll
+        for (int q = 0; q < 32; ++q) {
+          av[q] = Z[tm * 32 + ml][2 * q + kl];
+          bv[q] = M[2 * q + kl][tn * 32 + ml];
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          acc0[v] = 0.f;
+          acc1[v] = 0.f;
+        }
+#pragma unroll
+        for (int q = 0; q < 32; q += 2) {
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q], bv[q], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q + 1], bv[q + 1], acc1, 0, 0, 0);
+        }
+      }
+      __syncthreads();
+      if (active) {
+        // left half (tn == 0) is final for this group; the right half becomes the next block's
+        // left half (or is final too after the group's last block)
+        const int col = ml, rb = kl * 4;
+        const bool more = k + 1 < nk;
+        if (tn == 0 || !more) {
+          const int64_t c = lo + 32 * tn + col;
+          const bool cok = c < n;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int r = tm * 32 + 8 * (v >> 2) + rb + (v & 3);
+            if (cok && r < rows) Zb[(z0 + r) * n + c] = acc0[v] + acc1[v];
+          }
+        } else {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) Z[tm * 32 + 8 * (v >> 2) + rb + (v & 3)][col] = acc0[v] + acc1[v];
+        }
+        if (more) {
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            const int e = lt + q * 256;
+            M[e >> 6][e & 63] = pa.m[q];
+          }
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const int e = lt + q * 256;
+            Z[e >> 5][32 + (e & 31)] = pa.z[q];
+          }
+          pa = pb;
+        }
+        lo += kBW;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace
+
+Layout layout(int64_t n) {
+  Layout L{};
+  int64_t o = 0;
+  auto take = [&](int64_t elems) {
+    const int64_t at = o;
+    o += al64(elems);
+    return at;
+  };
+  const int64_t nleaf = (n + kLeaf - 1) / kLeaf;
+  L.Yl = take(n * 32);
+  L.taul = take(nleaf * 32);
+  L.Rs = take(nleaf * 32 * 32);
+  L.E = take(nleaf * 32 * 32);
+  L.Rroot = take(32 * 32);
+  L.Q1 = take(n * 32);
+  L.Y = take(n * 32);
+  L.YT = take(n * 32);
+  L.X = take(n * 32);
+  L.T = take(32 * 32);
+  L.Gp = take(64 * 1024);
+  L.Xop = take(n * 64);
+  L.Yop = take(n * 64);
+  L.M = take(32 * 32);
+  L.px_floats = 2 * ((n + kXKC - 1) / kXKC) * n * 32;  // split-K partials of X = A22 (Y T), two passes
+  L.Px = take(L.px_floats);
+  L.Gd = take(2 * 64 * 1024);   // fp64 Gram partials
+  L.Rc = take(2 * 1024);        // fp64 R of the current pass
+  L.Rt = take(2 * 1024);        // fp64 R_tot
+  L.flags = take(n / kBW + 64); // per-panel fallback flags (int)
+  L.AB = take((n + kABpad) * kABld);
+  const int64_t nb = q2_blocks(n);
+  L.V2 = take(nb * 32 * 32);
+  L.tau2 = take(nb * 32);
+  L.Pt = take(nb * 64 * 64);
+  L.prog = take((n + kNW) / kNW + 64);  // int progress slots + status
+  L.total = o;
+  return L;
+}
+
+int sy2sb(int64_t n, float* A, int64_t lda, float* tau, float* ws, const Layout& L, hipStream_t stream) {
+  // one fallback flag per panel (0: the Cholesky QR path holds), cleared up front
+  int* flags = reinterpret_cast<int*>(ws + L.flags);
+  const int64_t npanels = n > kBW ? (n - kBW + kBW - 1) / kBW : 0;
+  if (npanels > 0) {
+    hipLaunchKernelGGL(fill_int_kernel, dim3((unsigned)((npanels + 2 + kThr - 1) / kThr)), dim3(kThr), 0, stream,
+                       flags, npanels + 2, 0);
+    MPQ_LAUNCH_CHECK();
+  }
+  for (int64_t c0 = 0; c0 + kBW < n; c0 += kBW) {
+    const int64_t pidx = c0 / kBW;
+    const int64_t r0 = c0 + kBW, m = n - r0;
+    const int64_t nleaf = (m + kLeaf - 1) / kLeaf;
+    const int root_rows = (int)(32 * (nleaf - 1) + std::min<int64_t>(32, m - kLeaf * (nleaf - 1)));
+    // Q1 R = P: Cholesky QR (three passes), or the tall-skinny Householder QR when it fails
+    const int* fb = flags + pidx;
+    int* fbw = flags + pidx;
+    const float* P = A + r0 * lda + c0;
+    const int64_t cq_ng = std::min<int64_t>(64, (m + kCqTile - 1) / kCqTile);
+    const int64_t cq_chunk = (m + cq_ng - 1) / cq_ng;
+    double* Gp = reinterpret_cast<double*>(ws + L.Gd);
+    double* Rc = reinterpret_cast<double*>(ws + L.Rc);
+    double* Rt = reinterpret_cast<double*>(ws + L.Rt);
+    unsigned* counter = reinterpret_cast<unsigned*>(flags + npanels + 1);
+    // pass p's launch solves with R_{p-1} and factors the Gram matrix of the result (R_p); the
+    // fourth launch applies R_3 only
+    for (int pass = 1; pass <= 4; ++pass) {
+      hipLaunchKernelGGL(cq_pass_kernel, dim3((unsigned)cq_ng), dim3(kThr), 0, stream, pass <= 2 ? P : ws + L.Q1,
+                         pass <= 2 ? lda : (int64_t)32, m, cq_chunk, Rc, pass > 1 ? 1 : 0, ws + L.Q1, Gp,
+                         pass <= 3 ? pass : 0, Rt, ws + L.Rroot, fbw, counter);
+      MPQ_LAUNCH_CHECK();
+    }
+    hipLaunchKernelGGL(leaf_qr_kernel, dim3((unsigned)nleaf), dim3(kPThr), 0, stream, A, lda, r0, c0, m, ws + L.Yl,
+                       ws + L.taul, ws + L.Rs, fb);
+    MPQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(root_qr_kernel, dim3(1), dim3(kPThr), 0, stream, ws + L.Rs, root_rows, ws + L.Rroot,
+                       ws + L.E, fb);
+    MPQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(leaf_q_kernel, dim3((unsigned)nleaf), dim3(kPThr), 0, stream, ws + L.Yl, ws + L.taul,
+                       ws + L.E, m, ws + L.Q1, fb);
+    MPQ_LAUNCH_CHECK();
+    const unsigned rblocks = (unsigned)((m + kThr - 1) / kThr);
+    hipLaunchKernelGGL(hr_kernel, dim3(rblocks), dim3(kThr), 0, stream, ws + L.Q1, ws + L.Rroot, m, A, lda, r0, c0,
+                       ws + L.Y, ws + L.YT, ws + L.T, tau);
+    MPQ_LAUNCH_CHECK();
+    float* A22 = A + r0 * lda + r0;
+    // X = A22 (Y T): split-K partials, summed in split order
+    const int xsplits = (int)((m + kXKC - 1) / kXKC);
+    hipLaunchKernelGGL(xprod_kernel<0>, dim3((unsigned)((m + 127) / 128), (unsigned)xsplits), dim3(kThr), 0, stream,
+                       A22, lda, ws + L.YT, m, ws + L.Px);
+    MPQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(xprod_kernel<1>, dim3((unsigned)((m + 127) / 128), (unsigned)xsplits), dim3(kThr), 0, stream,
+                       A22, lda, ws + L.YT, m, ws + L.Px);
+    MPQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(xsum_kernel, dim3((unsigned)((m * 32 + kThr - 1) / kThr)), dim3(kThr), 0, stream, ws + L.Px,
+                       2 * xsplits, m * 32, ws + L.X);
+    MPQ_LAUNCH_CHECK();
+    const int64_t ng = std::min<int64_t>(64, (m + 63) / 64);
+    const int64_t chunk = ((m + ng - 1) / ng + 63) / 64 * 64;
+    const int64_t ngu = (m + chunk - 1) / chunk;
+    hipLaunchKernelGGL(gram_partial_kernel, dim3((unsigned)ngu), dim3(kThr), 0, stream, ws + L.Y, ws + L.X, m, chunk,
+                       ws + L.Gp);
+    MPQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(m_kernel, dim3(1), dim3(1024), 0, stream, ws + L.Gp, (int)ngu, ws + L.T, ws + L.M);
+    MPQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(w_kernel, dim3(rblocks), dim3(kThr), 0, stream, ws + L.M, ws + L.Y, ws + L.X, m, ws + L.Xop,
+                       ws + L.Yop);
+    MPQ_LAUNCH_CHECK();
+    // A22 -= Y W^T + W Y^T on the lower triangle and the 32 x 32 diagonal blocks (whole tiles)
+    MPQ_HIP_TRY(gemm_lower(ws + L.Xop, 64, ws + L.Yop, 64, true, A22, lda, m, 64, -1.f, 1.f, kBW - 1, stream));
+  }
+  return kOk;
+}
+
+int sb2st(int64_t n, const float* A, int64_t lda, float* D, float* E, float* ws, const Layout& L,
+          hipStream_t stream) {
+  float* AB = ws + L.AB;
+  const int64_t cnt = (n + kABpad) * kABld;
+  hipLaunchKernelGGL(band_extract_kernel, dim3((unsigned)((cnt + kThr - 1) / kThr)), dim3(kThr), 0, stream, A, lda, n,
+                     AB);
+  MPQ_LAUNCH_CHECK();
+  if (n >= 3) {
+    const int64_t ngroups = (n - 1 + kNW - 1) / kNW;
+    int* prog = reinterpret_cast<int*>(ws + L.prog);
+    int* status = prog + ngroups;
+    hipLaunchKernelGGL(fill_int_kernel, dim3((unsigned)((ngroups + 1 + kThr - 1) / kThr)), dim3(kThr), 0, stream,
+                       prog, ngroups + 1, -1);
+    MPQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(fill_int_kernel, dim3(1), dim3(kThr), 0, stream, status, 1, 0);
+    MPQ_LAUNCH_CHECK();
+    BulgeArgs args{AB, n, ws + L.V2, ws + L.tau2, prog, status, (int64_t)1 << 24};
+    // enough work-groups that every group of sweeps has one when the pipeline is full (about
+    // n / 64 tasks per sweep in flight, two tasks apart), at most one per CU
+    const int64_t want = std::max<int64_t>(1, std::min<int64_t>(ngroups, (n / kBW) / (2 * kNW) + 2));
+    const unsigned G = (unsigned)std::min<int64_t>(want, 128);
+    void* kargs[] = {&args};
+    MPQ_HIP_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(bulge_kernel), dim3(G), dim3(64 * kNW),
+                                           kargs, 0, stream));
+    int st = 0;
+    MPQ_HIP_TRY(hipMemcpyAsync(&st, status, sizeof(int), hipMemcpyDeviceToHost, stream));
+    MPQ_HIP_TRY(hipStreamSynchronize(stream));
+    if (st != 0) {
+      set_error("mpq_syevd: band reduction pipeline stalled (a wait exceeded its bound)");
+      set_error_code(kHipError);
+      return kHipError;
+    }
+  }
+  hipLaunchKernelGGL(tridiag_out_kernel, dim3((unsigned)((n + kThr - 1) / kThr)), dim3(kThr), 0, stream, AB, n, D, E);
+  MPQ_LAUNCH_CHECK();
+  return kOk;
+}
+
+int q2_apply(int64_t n, float* Zb, float* ws, const Layout& L, hipStream_t stream) {
+  if (n < 3) return kOk;
+  const int64_t nb = q2_blocks(n);
+  hipLaunchKernelGGL(q2_build_kernel, dim3((unsigned)nb), dim3(kThr), 0, stream, ws + L.V2, ws + L.tau2, n,
+                     ws + L.Pt);
+  MPQ_LAUNCH_CHECK();
+  hipLaunchKernelGGL(q2_apply_kernel, dim3((unsigned)((n + 63) / 64)), dim3(512), 0, stream, ws + L.Pt, Zb, n);
+  MPQ_LAUNCH_CHECK();
+  return kOk;
+}
+
+}  // namespace band
+}  // namespace mpq

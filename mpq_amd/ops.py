@@ -256,9 +256,10 @@ def scale_columns(X: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def syevd(H: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+def syevd(H: torch.Tensor, method: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
     """Eigendecomposition of a symmetric matrix: (lam ascending, V with eigenvectors as columns).
-    float64 input runs in fp64 (mpq_syevd_f64), anything else in fp32 (mpq_syevd)."""
+    float64 input runs in fp64 (mpq_syevd_f64), anything else in fp32 (mpq_syevd_method; method 0
+    = automatic, 1 = one-stage tridiagonalisation, 2 = two-stage band reduction)."""
     dev = _dev(H)
     f64 = H.dtype == torch.float64
     H = H.contiguous() if f64 else _f32c(H)
@@ -270,7 +271,13 @@ def syevd(H: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     ws = workspace(int(getattr(lib, name + "_workspace_size")(n)), dev)
     lam = torch.empty(n, dtype=H.dtype, device=dev)
     V = torch.empty(n, n, dtype=H.dtype, device=dev)
-    _lib.call(name, n, _lib.ptr(H), _lib.ptr(lam), _lib.ptr(V), _lib.ptr(ws), int(ws.numel()), _stream(dev))
+    if f64:
+        if method not in (0, 1):
+            raise ValueError("the fp64 eigensolver has the one-stage reduction only")
+        _lib.call(name, n, _lib.ptr(H), _lib.ptr(lam), _lib.ptr(V), _lib.ptr(ws), int(ws.numel()), _stream(dev))
+    else:
+        _lib.call("mpq_syevd_method", n, _lib.ptr(H), _lib.ptr(lam), _lib.ptr(V), _lib.ptr(ws), int(ws.numel()),
+                  int(method), _stream(dev))
     return lam, V
 
 

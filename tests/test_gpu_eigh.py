@@ -1,6 +1,8 @@
-"""GPU: symmetric eigendecomposition (mpq_syevd: tridiagonalisation, divide and conquer on the
-tridiagonal matrix, back-transformation on this library's MFMA GEMM) against fp64 LAPACK on the CPU, with the fp32 accuracy of
-torch.linalg.eigh on the same GPU as the yardstick for residual and orthogonality."""
+"""GPU: symmetric eigendecomposition (mpq_syevd: one-stage tridiagonalisation or the two-stage band
+reduction with bulge chasing, divide and conquer on the tridiagonal matrix, back-transformation on
+this library's MFMA GEMM) against fp64 LAPACK on the CPU, with the fp32 accuracy of
+torch.linalg.eigh on the same GPU as the yardstick for residual and orthogonality.  Both reductions
+are tested explicitly (mpq_syevd_method 1 and 2) at the sizes the automatic choice does not pick."""
 import pytest
 import torch
 
@@ -18,11 +20,12 @@ def _quality(H, lam, V):
     return resid, orth
 
 
-@pytest.mark.parametrize("n", [256, 1000, 2048])
-def test_syevd_matches_fp64(gpu, n):
+@pytest.mark.parametrize("method", [1, 2])
+@pytest.mark.parametrize("n", [256, 1000, 2048, 4100])
+def test_syevd_matches_fp64(gpu, n, method):
     _, H = make_layer(8, n, tokens=2 * n, seed_key=f"eigh:{n}")
     Hg = H.to(gpu)
-    lam, V = ops.syevd(Hg)
+    lam, V = ops.syevd(Hg, method=method)
     ref = torch.linalg.eigvalsh(H.double())
     scale = float(ref.abs().max())
     assert float((lam.cpu().double() - ref).abs().max()) <= 2e-5 * scale
@@ -60,11 +63,42 @@ def test_syevd_small_and_diagonal(gpu):
     # n = 1, 2 (no or one reflector), a diagonal matrix (all reflectors trivial), repeated eigenvalues
     for H in (torch.tensor([[3.0]]), torch.tensor([[2.0, 1.0], [1.0, 2.0]]),
               torch.diag(torch.arange(300, dtype=torch.float32)), torch.eye(129) * 5.0):
-        lam, V = ops.syevd(H.to(gpu))
+        lam, V = ops.syevd(H.to(gpu), method=1)
         ref = torch.linalg.eigvalsh(H.double())
         assert float((lam.cpu().double() - ref).abs().max()) <= 1e-5 * max(1.0, float(ref.abs().max()))
         resid, orth = _quality(H, lam, V)
         assert resid < 1e-5 and orth < 1e-5, (H.shape, resid, orth)
+
+
+def test_syevd_two_stage_edge_cases(gpu):
+    """Two-stage path: no panel (n <= 32: already a band), one panel of one row (n = 33), ragged
+    sizes; zero panels (a diagonal matrix, 5 I: the Cholesky QR fails and the tall-skinny
+    Householder QR runs; every bulge reflector trivial); a matrix whose panels have zero columns."""
+    g = torch.Generator().manual_seed(7)
+    cases = []
+    for n in (3, 32, 33, 64, 65, 100, 300):
+        X = torch.randn(2 * n, n, generator=g) * torch.exp(torch.randn(n, generator=g))
+        cases.append(X.T @ X / (2 * n))
+    cases += [torch.diag(torch.arange(300, dtype=torch.float32)), torch.eye(129) * 5.0]
+    X = torch.randn(600, 300, generator=g)
+    X[:, 40:70] = 0.0  # dead channels: zero rows and columns in H, zero columns in the panels
+    cases.append(X.T @ X / 600 + torch.diag((torch.arange(300) % 7).float()))
+    for H in cases:
+        H = 0.5 * (H + H.T)
+        lam, V = ops.syevd(H.to(gpu), method=2)
+        ref = torch.linalg.eigvalsh(H.double())
+        scale = max(1.0, float(ref.abs().max()))
+        assert float((lam.cpu().double() - ref).abs().max()) <= 2e-5 * scale, H.shape
+        assert bool((lam[1:] >= lam[:-1]).all())
+        resid, orth = _quality(H, lam, V)
+        assert resid < 2e-5 and orth < 2e-5, (H.shape, resid, orth)
+
+
+def test_syevd_method_rejects_bad_arguments(gpu):
+    with pytest.raises(ValueError, match="method"):
+        ops.syevd(torch.eye(4, device=gpu), method=3)
+    with pytest.raises(ValueError, match="two-stage"):
+        ops.syevd(torch.eye(2, device=gpu), method=2)
 
 
 @pytest.mark.parametrize("n", [200, 1000, 2048])
