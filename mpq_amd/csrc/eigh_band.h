@@ -40,9 +40,9 @@ int sy2sb(int64_t n, float* A, int64_t lda, float* tau, float* ws, const Layout&
 int sb2st(int64_t n, const float* A, int64_t lda, float* D, float* E, float* ws, const Layout& L,
           hipStream_t stream);
 
-// Zb (n x n, row-major, row k = eigenvector k of the tridiagonal matrix) <- Zb Q2^T: the rows
+// Zt (n x n, row-major, column k = eigenvector k of the tridiagonal matrix) <- Q2 Zt: the columns
 // become eigenvectors of the band matrix.
-int q2_apply(int64_t n, float* Zb, float* ws, const Layout& L, hipStream_t stream);
+int q2_apply(int64_t n, float* Zt, float* ws, const Layout& L, hipStream_t stream);
 
 }  // namespace band
 }  // namespace mpq

@@ -36,6 +36,7 @@
 // bulges need), with zero columns past n - 1 so the last tasks read and write zeros there.
 #include "eigh_band.h"
 #include "gemm.h"
+#include "x6_split.h"
 
 namespace mpq {
 namespace band {
@@ -949,11 +950,18 @@ __global__ __launch_bounds__(kThr) void tridiag_out_kernel(const float* __restri
 
 // ---- back-transformation of stage 2 ----------------------------------------------------------
 
-// Block (g, k): Pt = H_31 ... H_0 over the window rows 32 g + 1 + 32 k .. + 63, H_i the reflector
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+constexpr int kPtChunks = 3 * 512;  // uint4 per block: 3 bf16 planes x (2 row tiles x 4 k-steps x 64 lanes)
+constexpr int kZs = 9;              // uint4 per LDS window row: 64 bf16 + 16 bytes of padding
+
+// Block (g, k): P = (H_31 ... H_0)^T over the window rows 32 g + 1 + 32 k .. + 63, H_i the reflector
 // of sweep 32 g + i at step k (acting on window rows i .. i + 31; identity where it does not
-// exist).  One work-group per block; thread (c = t % 64, q = t / 64) owns column c, rows q (mod 4).
+// exist).  One work-group per block; thread (c = t % 64, q = t / 64) owns column c, rows q (mod 4)
+// of M = H_31 ... H_0, then P = M^T leaves as three bf16 planes (P = P0 + P1 + P2 to 2^-24) in the
+// left-operand order of v_mfma_f32_32x32x16_bf16: chunk (plane, tile, step, lane) holds the 8
+// entries P[32 tile + lane % 32][16 step + 8 (lane / 32) + 0 .. 7].
 __global__ __launch_bounds__(kThr) void q2_build_kernel(const float* __restrict__ V2, const float* __restrict__ tau2,
-                                                        int64_t n, float* __restrict__ Pt) {
+                                                        int64_t n, uint4* __restrict__ Pt) {
   __shared__ float M[64][65];
   __shared__ float sv[32];
   __shared__ float red[4][64];
@@ -989,126 +997,225 @@ __global__ __launch_bounds__(kThr) void q2_build_kernel(const float* __restrict_
     for (int aa = q; aa < 32; aa += 4) M[i + aa][c] = fmaf(-sv[aa], zc, M[i + aa][c]);
     __syncthreads();
   }
-  float* out = Pt + bid * 4096;
-  for (int e = t; e < 64 * 64; e += kThr) out[e] = M[e / 64][e & 63];
-}
-
-
-// Zb[z0 .. z0 + 63][:] <- Zb[...] Q2^T: groups last to first, steps in increasing order, each block
-// Zb[:, lo .. lo + 63] <- Zb[:, lo .. lo + 63] Pt(g, k).  Consecutive steps overlap by 32 columns:
-// the right half of a block's result stays in LDS as the left half of the next block's input.
-// Two groups run at once: waves 0-3 take group g (the lead), waves 4-7 group g - 1 three steps
-// behind (block k of group g - 1 reads only columns the lead's blocks <= k have finished; its
-// prefetch, two blocks ahead, reads the lead's left halves of the previous step).  Each half has
-// its own LDS window and matrix and keeps the matrices and new columns of its next two blocks in
-// registers while it runs on the matrix cores.  One 32 x 32 output tile per wave
-// (v_mfma_f32_32x32x2f32, K = 64), two accumulator chains.
-struct Q2Pref {
-  float m[16], z[8];
-};
-
-__device__ __forceinline__ void q2_prefetch(Q2Pref& p, const float* __restrict__ Pt, const float* __restrict__ Zb,
-                                            int64_t bidx, int64_t col0, int64_t z0, int rows, int64_t n, int lt) {
-  const float* M = Pt + bidx * 4096;
+  uint4* out = Pt + bid * kPtChunks;
+  for (int ci = t; ci < 512; ci += kThr) {
+    const int l = ci & 63, ts = ci >> 6;
+    const int cc = 32 * (ts >> 2) + (l & 31), k0 = 16 * (ts & 3) + 8 * (l >> 5);
+    uint32_t h[4], m[4], lo[4];
 #pragma unroll
-  for (int q = 0; q < 16; ++q) p.m[q] = M[lt + q * 256];
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int e = lt + q * 256, r = e >> 5, cc = e & 31;
-    p.z[q] = (r < rows && col0 + cc < n) ? Zb[(z0 + r) * n + col0 + cc] : 0.f;
+    for (int j = 0; j < 4; ++j) split3(M[k0 + 2 * j][cc], M[k0 + 2 * j + 1][cc], h[j], m[j], lo[j]);
+    out[ci] = make_uint4(h[0], h[1], h[2], h[3]);
+    out[512 + ci] = make_uint4(m[0], m[1], m[2], m[3]);
+    out[1024 + ci] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
   }
 }
 
-__global__ __launch_bounds__(512) void q2_apply_kernel(const float* __restrict__ Pt, float* __restrict__ Zb,
-                                                       int64_t n) {
-  __shared__ float sM[2][64][65];
-  __shared__ float sZ[2][64][65];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int half = wave >> 2, lt = t & 255;
-  const int tm = (wave >> 1) & 1, tn = wave & 1;
-  const int64_t z0 = (int64_t)blockIdx.x * 64;
-  const int rows = (int)min((int64_t)64, n - z0);
-  const int64_t K0 = (n - 2) / kBW;
-  const int kl = lane >> 5, ml = lane & 31;
-  float(*Z)[65] = sZ[half];
-  float(*M)[65] = sM[half];
-  Q2Pref pa, pb;
-  for (int64_t gl = K0; gl >= 0; gl -= 2) {
-    const int64_t g = gl - half;                 // this half's group (< 0: idle)
-    const int64_t nk = g >= 0 ? K0 + 1 - g : 0;
-    const int64_t nk_lag = gl >= 1 ? K0 + 2 - gl : 0;
-    const int64_t steps = max(K0 + 1 - gl, nk_lag > 0 ? 3 + nk_lag : (int64_t)0);
-    const int64_t S = 3 * half;
-    const int64_t base = g >= 0 ? boff(g, K0) : 0;
-    int64_t lo = g * kBW + 1;
-    for (int64_t T = 0; T < steps; ++T) {
-      const int64_t k = T - S;
-      const bool active = k >= 0 && k < nk;
-      if (active && k == 0) {
-        // first block of the group: window and matrix straight into LDS
-        for (int e = lt; e < 64 * 64; e += 256) {
-          const int r = e >> 6, cc = e & 63;
-          Z[r][cc] = (r < rows && lo + cc < n) ? Zb[(z0 + r) * n + lo + cc] : 0.f;
-          M[r][cc] = Pt[base * 4096 + e];
-        }
-        // block j's new columns are lo_j + 32 .. lo_j + 63 with lo_j = lo + 32 j
-        if (nk > 1) q2_prefetch(pa, Pt, Zb, base + 1, lo + 64, z0, rows, n, lt);
-      }
-      __syncthreads();
-      floatx16 acc0, acc1;
-      if (active) {
-        if (k + 2 < nk) q2_prefetch(pb, Pt, Zb, base + k + 2, lo + 96, z0, rows, n, lt);
-        // every operand first (one LDS wait), then two independent accumulator chains
-        float av[32], bv[32];
+
+// Zt (n x n, row-major, column k = eigenvector k of the tridiagonal matrix) <- Q2 Zt: groups last
+// to first, steps in increasing order, each block Zt[lo .. lo + 63][:] <- P(g, k) Zt[lo .. lo + 63][:].
+// One work-group per 64 columns.  Consecutive steps overlap by 32 rows: the lower half of a block's
+// result stays in LDS as the upper half of the next block's window.  Four groups run at once, one
+// per pair of waves: group gl - q (quarter q) runs kQ2Lag steps behind group gl - q + 1, so block
+// k of group g - 1 reads only rows the blocks <= k - 2 of group g have finished, and its prefetch
+// two blocks ahead reads the rows of block k - 1 of group g.  Each quarter keeps its window in LDS
+// as three bf16 planes (row-contiguous per column: the right-operand order of
+// v_mfma_f32_32x32x16_bf16); the planes of P come from global memory straight into registers, one
+// block ahead.  A wave owns 32 output rows x 64 columns (two 32 x 32 tiles, K = 64): six plane
+// products per tile and 16-k step (every pair with plane indices summing to <= 2).
+constexpr int kQ2Lag = 3;
+
+struct Q2Frag {
+  uint4 a[12];  // [plane * 4 + k-step]
+};
+
+__device__ __forceinline__ void q2_load_frag(Q2Frag& f, const uint4* __restrict__ Pt, int64_t bidx, int tc,
+                                             int lane) {
+  const uint4* src = Pt + bidx * kPtChunks + tc * 256 + lane;
 #pragma unroll
-        for (int q = 0; q < 32; ++q) {
-          av[q] = Z[tm * 32 + ml][2 * q + kl];
-          bv[q] = M[2 * q + kl][tn * 32 + ml];
-        }
+  for (int p = 0; p < 3; ++p)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) f.a[p * 4 + s] = src[p * 512 + s * 64];
+}
+
+// rows row0 .. row0 + 7 of column col, each row index clamped to n - 1 (always a valid address;
+// q2_put_rows zeroes what lies outside the matrix).  row0 is wave-uniform: the row pointers are
+// scalar.  No branch and no use of the values here, so the loads stay in flight.
+__device__ __forceinline__ void q2_load_rows(float (&z)[8], const float* __restrict__ Zt, int row0, int col, int n) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) z[j] = (Zt + (int64_t)min(row0 + j, n - 1) * n)[col];
+}
+
+// the three planes of 8 consecutive window rows of column r at chunk (rows 8 chunk .. 8 chunk + 7);
+// row j counts as zero unless cok and row0 + j < n
+__device__ __forceinline__ void q2_put_rows(uint4* __restrict__ Zp, int r, int chunk, const float (&zin)[8], int row0,
+                                            int n, bool cok) {
+  float z[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) z[j] = (cok && row0 + j < n) ? zin[j] : 0.f;
+  uint4 h, m, l;
+  split3(z[0], z[1], h.x, m.x, l.x);
+  split3(z[2], z[3], h.y, m.y, l.y);
+  split3(z[4], z[5], h.z, m.z, l.z);
+  split3(z[6], z[7], h.w, m.w, l.w);
+  Zp[r * kZs + chunk] = h;
+  Zp[(64 + r) * kZs + chunk] = m;
+  Zp[(128 + r) * kZs + chunk] = l;
+}
+
+struct Q2Ctx {
+  const uint4* Pt;
+  float* Zt;
+  uint4* Zp;
+  int n, z0, lane, wq, tc, lcol, lcl;  // lcl: lcol clamped to n - 1
+  bool colfull, cok;                   // cok: lcol < n
+};
+
+// one step of one quarter: block k = T - S of its group (lo = first window row, base = the group's
+// first block); cur holds block k's planes, the next block's go to nxt; zA holds block k + 1's new
+// rows, block k + 2's go to zB
+__device__ __forceinline__ void q2_step(const Q2Ctx& c, int k, int nk, int lo, int64_t base, Q2Frag& cur,
+                                        Q2Frag& nxt, float (&zA)[2][8], float (&zB)[2][8]) {
+  const bool active = k >= 0 && k < nk;
+  const bool more = k + 1 < nk;
+  if (active && k == 0) {
+    // first block of the group: window into LDS, matrix and block 1's new rows into registers
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      float z[8];
+      const int chunk = 4 * c.wq + h;
+      q2_load_rows(z, c.Zt, lo + 8 * chunk, c.lcl, c.n);
+      q2_put_rows(c.Zp, c.lane, chunk, z, lo + 8 * chunk, c.n, c.cok);
+    }
+    q2_load_frag(cur, c.Pt, base, c.tc, c.lane);
+    q2_load_rows(zA[0], c.Zt, lo + 64 + 16 * c.wq, c.lcl, c.n);
+    q2_load_rows(zA[1], c.Zt, lo + 72 + 16 * c.wq, c.lcl, c.n);
+  }
+  __syncthreads();
+  floatx16 acc0, acc1;
+  if (active) {
+    // unconditional loads (last block: its own matrix again; rows clamped), so that nothing
+    // between them and the matrix cores waits for them
+    q2_load_frag(nxt, c.Pt, base + min(k + 1, nk - 1), c.tc, c.lane);
+    // new rows of block k + 2: lo_{k+2} + 32 .. + 63 with lo_j = lo + 32 j
+    q2_load_rows(zB[0], c.Zt, lo + 96 + 16 * c.wq, c.lcl, c.n);
+    q2_load_rows(zB[1], c.Zt, lo + 104 + 16 * c.wq, c.lcl, c.n);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      acc0[v] = 0.f;
+      acc1[v] = 0.f;
+    }
+    const uint4* Zr = c.Zp + (c.lane & 31) * kZs + (c.lane >> 5);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const bf16x8 a0 = __builtin_bit_cast(bf16x8, cur.a[s]);
+      const bf16x8 a1 = __builtin_bit_cast(bf16x8, cur.a[4 + s]);
+      const bf16x8 a2 = __builtin_bit_cast(bf16x8, cur.a[8 + s]);
+      const bf16x8 b0 = __builtin_bit_cast(bf16x8, Zr[2 * s]);
+      const bf16x8 b1 = __builtin_bit_cast(bf16x8, Zr[64 * kZs + 2 * s]);
+      const bf16x8 b2 = __builtin_bit_cast(bf16x8, Zr[128 * kZs + 2 * s]);
+      const bf16x8 d0 = __builtin_bit_cast(bf16x8, Zr[32 * kZs + 2 * s]);
+      const bf16x8 d1 = __builtin_bit_cast(bf16x8, Zr[96 * kZs + 2 * s]);
+      const bf16x8 d2 = __builtin_bit_cast(bf16x8, Zr[160 * kZs + 2 * s]);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, d0, acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, d1, acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, d0, acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b2, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, d2, acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, d1, acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, d0, acc1, 0, 0, 0);
+      // one k-step of window operands in registers at a time
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __syncthreads();
+  if (active) {
+    // upper output half (tc == 0) is final for this group; the lower half becomes the next
+    // block's upper half (or is final too after the group's last block)
+    if (c.tc == 0 || !more) {
+      const int row0 = lo + 32 * c.tc + 4 * (c.lane >> 5);
+      const int col = c.z0 + (c.lane & 31);
+      if (c.colfull && lo + 64 <= c.n) {
+        const int rw = lo + 32 * c.tc;  // wave-uniform: scalar row pointers
+        const int lo4 = 4 * (c.lane >> 5) * c.n + (c.lane & 31) + c.z0;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          acc0[v] = 0.f;
-          acc1[v] = 0.f;
+          float* dst = c.Zt + (int64_t)(rw + 8 * (v >> 2) + (v & 3)) * c.n;
+          dst[lo4] = acc0[v];
+          dst[lo4 + 32] = acc1[v];
         }
+      } else {
 #pragma unroll
-        for (int q = 0; q < 32; q += 2) {
-          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q], bv[q], acc0, 0, 0, 0);
-          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q + 1], bv[q + 1], acc1, 0, 0, 0);
+        for (int v = 0; v < 16; ++v) {
+          const int row = row0 + 8 * (v >> 2) + (v & 3);
+          if (row < c.n) {
+            if (col < c.n) c.Zt[row * c.n + col] = acc0[v];
+            if (col + 32 < c.n) c.Zt[row * c.n + col + 32] = acc1[v];
+          }
         }
       }
-      __syncthreads();
-      if (active) {
-        // left half (tn == 0) is final for this group; the right half becomes the next block's
-        // left half (or is final too after the group's last block)
-        const int col = ml, rb = kl * 4;
-        const bool more = k + 1 < nk;
-        if (tn == 0 || !more) {
-          const int64_t c = lo + 32 * tn + col;
-          const bool cok = c < n;
+    } else {
+      uint2* Zq = reinterpret_cast<uint2*>(c.Zp) + (c.lane & 31) * (2 * kZs) + (c.lane >> 5);
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int r = tm * 32 + 8 * (v >> 2) + rb + (v & 3);
-            if (cok && r < rows) Zb[(z0 + r) * n + c] = acc0[v] + acc1[v];
-          }
-        } else {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) Z[tm * 32 + 8 * (v >> 2) + rb + (v & 3)][col] = acc0[v] + acc1[v];
-        }
-        if (more) {
-#pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            const int e = lt + q * 256;
-            M[e >> 6][e & 63] = pa.m[q];
-          }
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const int e = lt + q * 256;
-            Z[e >> 5][32 + (e & 31)] = pa.z[q];
-          }
-          pa = pb;
-        }
-        lo += kBW;
+      for (int a = 0; a < 4; ++a) {
+        // rows 8 a + 4 (lane / 32) .. + 3 of the next window, columns lane % 32 and + 32
+        uint2 h, m, l;
+        split3(acc0[4 * a], acc0[4 * a + 1], h.x, m.x, l.x);
+        split3(acc0[4 * a + 2], acc0[4 * a + 3], h.y, m.y, l.y);
+        Zq[2 * a] = h;
+        Zq[64 * 2 * kZs + 2 * a] = m;
+        Zq[128 * 2 * kZs + 2 * a] = l;
+        split3(acc1[4 * a], acc1[4 * a + 1], h.x, m.x, l.x);
+        split3(acc1[4 * a + 2], acc1[4 * a + 3], h.y, m.y, l.y);
+        Zq[32 * 2 * kZs + 2 * a] = h;
+        Zq[96 * 2 * kZs + 2 * a] = m;
+        Zq[160 * 2 * kZs + 2 * a] = l;
       }
+    }
+    if (more) {
+      q2_put_rows(c.Zp, c.lane, 4 + 2 * c.wq, zA[0], lo + 64 + 16 * c.wq, c.n, c.cok);
+      q2_put_rows(c.Zp, c.lane, 5 + 2 * c.wq, zA[1], lo + 72 + 16 * c.wq, c.n, c.cok);
+    }
+  }
+}
+
+__global__ __launch_bounds__(512) void q2_apply_kernel(const uint4* __restrict__ Pt, float* __restrict__ Zt,
+                                                       int64_t n64) {
+  __shared__ uint4 sZ[4][3 * 64 * kZs];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: row indices stay scalar
+  const int qt = wave >> 1;  // quarter: group slot of this pair of waves
+  Q2Ctx c;
+  c.Pt = Pt;
+  c.Zt = Zt;
+  c.Zp = sZ[qt];
+  c.n = (int)n64;
+  c.z0 = (int)blockIdx.x * 64;
+  c.lane = lane;
+  c.wq = wave & 1;
+  // output row tile; swapped in quarters 2 and 3 so each SIMD holds one wave of each kind
+  c.tc = (wave & 1) ^ (qt >> 1);
+  c.lcol = c.z0 + lane;
+  c.lcl = min(c.lcol, c.n - 1);
+  c.cok = c.lcol < c.n;
+  c.colfull = c.z0 + 64 <= c.n;
+  const int K0 = (c.n - 2) / kBW;
+  Q2Frag fa, fb;
+  float za[2][8], zb[2][8];
+  for (int gl = K0; gl >= 0; gl -= 4) {
+    const int g = gl - qt;  // this quarter's group (< 0: idle)
+    const int nk = g >= 0 ? K0 + 1 - g : 0;
+    const int steps = K0 + 1 - gl + (kQ2Lag + 1) * min(3, gl);
+    const int S = kQ2Lag * qt;
+    const int64_t base = g >= 0 ? boff(g, K0) : 0;
+    const int lo0 = g * kBW + 1;
+    for (int T = 0; T < steps; T += 2) {
+      q2_step(c, T - S, nk, lo0 + kBW * (T - S), base, fa, fb, za, zb);
+      if (T + 1 < steps) q2_step(c, T + 1 - S, nk, lo0 + kBW * (T + 1 - S), base, fb, fa, zb, za);
     }
     __syncthreads();
   }
@@ -1149,7 +1256,7 @@ Layout layout(int64_t n) {
   const int64_t nb = q2_blocks(n);
   L.V2 = take(nb * 32 * 32);
   L.tau2 = take(nb * 32);
-  L.Pt = take(nb * 64 * 64);
+  L.Pt = take(nb * kPtChunks * 4);
   L.prog = take((n + kNW) / kNW + 64);  // int progress slots + status
   L.total = o;
   return L;
@@ -1267,13 +1374,13 @@ int sb2st(int64_t n, const float* A, int64_t lda, float* D, float* E, float* ws,
   return kOk;
 }
 
-int q2_apply(int64_t n, float* Zb, float* ws, const Layout& L, hipStream_t stream) {
+int q2_apply(int64_t n, float* Zt, float* ws, const Layout& L, hipStream_t stream) {
   if (n < 3) return kOk;
   const int64_t nb = q2_blocks(n);
-  hipLaunchKernelGGL(q2_build_kernel, dim3((unsigned)nb), dim3(kThr), 0, stream, ws + L.V2, ws + L.tau2, n,
-                     ws + L.Pt);
+  uint4* Pt = reinterpret_cast<uint4*>(ws + L.Pt);
+  hipLaunchKernelGGL(q2_build_kernel, dim3((unsigned)nb), dim3(kThr), 0, stream, ws + L.V2, ws + L.tau2, n, Pt);
   MPQ_LAUNCH_CHECK();
-  hipLaunchKernelGGL(q2_apply_kernel, dim3((unsigned)((n + 63) / 64)), dim3(512), 0, stream, ws + L.Pt, Zb, n);
+  hipLaunchKernelGGL(q2_apply_kernel, dim3((unsigned)((n + 63) / 64)), dim3(512), 0, stream, Pt, Zt, n);
   MPQ_LAUNCH_CHECK();
   return kOk;
 }
