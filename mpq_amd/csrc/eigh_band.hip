@@ -43,6 +43,14 @@ namespace band {
 namespace {
 
 constexpr int kThr = 256;
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 constexpr int kProgStride = 4096;  // progress value = sweep * 4096 + tasks done (4095: finished)
 constexpr int kNW = 8;             // waves (sweeps) per bulge-chasing work-group
 
@@ -133,7 +141,7 @@ __global__ __launch_bounds__(kPThr) void leaf_qr_kernel(const float* __restrict_
                                                         int64_t c0, int64_t m, float* __restrict__ Yl,
                                                         float* __restrict__ taul, float* __restrict__ Rs,
                                                         const int* __restrict__ fallback) {
-  if (*fallback == 0) return;  // the Cholesky QR path produced Q1 and R
+  if (*fallback != 1) return;  // the Cholesky QR path produced Q1 and R
   constexpr int R = kLeaf / 32;
   __shared__ PanelLds L;
   const int t = threadIdx.x, c = t & 31, s = t >> 5;
@@ -164,7 +172,7 @@ __global__ __launch_bounds__(kPThr) void leaf_qr_kernel(const float* __restrict_
 __global__ __launch_bounds__(kPThr) void root_qr_kernel(const float* __restrict__ Rs, int root_rows,
                                                         float* __restrict__ Rroot, float* __restrict__ E,
                                                         const int* __restrict__ fallback) {
-  if (*fallback == 0) return;
+  if (*fallback != 1) return;
   constexpr int R = 32;
   __shared__ PanelLds L;
   const int t = threadIdx.x, c = t & 31, s = t >> 5;
@@ -217,7 +225,7 @@ __global__ __launch_bounds__(kPThr) void root_qr_kernel(const float* __restrict_
 __global__ __launch_bounds__(kPThr) void leaf_q_kernel(const float* __restrict__ Yl, const float* __restrict__ taul,
                                                        const float* __restrict__ E, int64_t m,
                                                        float* __restrict__ Q1, const int* __restrict__ fallback) {
-  if (*fallback == 0) return;
+  if (*fallback != 1) return;
   constexpr int R = kLeaf / 32;
   __shared__ PanelLds L;
   const int t = threadIdx.x, c = t & 31, s = t >> 5;
@@ -261,9 +269,11 @@ __global__ __launch_bounds__(kPThr) void leaf_q_kernel(const float* __restrict__
 // Nakatsukasa, Yamamoto, Yanagisawa, "Shifted Cholesky QR for computing the QR factorization of
 // ill-conditioned matrices", SIAM J. Sci. Comput. 2020): pass 1 factors P^T P + s I with
 // s = 11 (32 m + 32 * 33) 2^-53 |P|_F^2, passes 2 and 3 refactor the Gram matrix of the current Q
-// (Cholesky QR2).  R = R3 R2 R1.  A pass whose Cholesky factorisation meets a pivot <= 0, or a last
-// pass whose Gram matrix is not close to the identity, sets the panel's fallback flag: then the
-// tall-skinny Householder QR above runs instead (rank-deficient panels, e.g. zero panels).
+// (Cholesky QR2).  R = R3 R2 R1.  When the Gram matrix of pass 2 is already within 2e-4 of I, the
+// pass-2 factor is orthonormal to working precision and pass 3 is skipped (flag 2, R = R2 R1).  A
+// pass whose Cholesky factorisation meets a pivot <= 0, or a last pass whose Gram matrix is not
+// close to the identity, sets the panel's fallback flag to 1: then the tall-skinny Householder QR
+// above runs instead (rank-deficient panels, e.g. zero panels).
 constexpr int kCqTile = 256;
 
 __device__ __forceinline__ double readlane_f64(double v, int l) {
@@ -318,10 +328,13 @@ __device__ void cq_cholesky(double (*G)[33], int pass, int64_t m, int* bad) {
 }
 
 // Rows of the work-group's chunk: y = p R^-1 (R upper triangular, fp64; none in pass 1) stored to
-// Qout, and, for chol_pass > 0, the partial Gram sum y^T y in fp64.  The last work-group to finish
-// (atomic counter) sums the partials in work-group order, factors them (pass chol_pass), writes R
-// to Rcur for the next launch and R_tot <- R R_tot (pass 3: R_tot to Rroot in fp32), or raises
-// the fallback flag.  Every work-group reads Rcur before it counts itself in, so rewriting it is safe.
+// Qout, and the partial Gram sum y^T y in fp64 (rows staged in LDS as fp64; thread (g, bi, bj)
+// sums the 4 x 4 block (4 bi.., 4 bj..) over rows g (mod 4) of a tile, the four row groups are
+// added in order at the end).  The last work-group to finish (atomic counter) sums the partials in
+// work-group order, factors them (pass chol_pass), writes R to Rcur for the next launch and
+// R_tot <- R R_tot (last pass: R_tot to Rroot in fp32), or raises the fallback flag.  Every
+// work-group reads Rcur before it counts itself in, so rewriting it is safe.
+constexpr int kCqLd = 34;  // fp64 row stride of the staged tile (16-byte aligned rows)
 __global__ __launch_bounds__(kThr) void cq_pass_kernel(const float* __restrict__ src, int64_t ld, int64_t m,
                                                        int64_t chunk, double* __restrict__ Rcur,
                                                        int use_rcur, float* __restrict__ Qout,
@@ -330,7 +343,7 @@ __global__ __launch_bounds__(kThr) void cq_pass_kernel(const float* __restrict__
                                                        int* __restrict__ fallback, unsigned* __restrict__ counter) {
   if (*fallback != 0) return;
   __shared__ double sR[32][33];
-  __shared__ float tile[kCqTile][33];
+  __shared__ __align__(16) double tile[kCqTile * kCqLd];
   __shared__ double G[32][33];
   __shared__ int bad, last;
   const int t = threadIdx.x;
@@ -342,17 +355,18 @@ __global__ __launch_bounds__(kThr) void cq_pass_kernel(const float* __restrict__
   __syncthreads();
   const int64_t rbeg = (int64_t)blockIdx.x * chunk;
   const int64_t rend = min(m, rbeg + chunk);
-  // Gram entries (i0 + a, j0 + b), a, b < 2, of this thread
-  const int i0g = 2 * (t >> 4), j0g = 2 * (t & 15);
-  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  const int grp = t >> 6, bi = (t >> 3) & 7, bj = t & 7;
+  double acc[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) acc[q] = 0.0;
   for (int64_t r0 = rbeg; r0 < rend; r0 += kCqTile) {
     const int64_t r = r0 + t;
-    float y[32];
+    double yd[32];
     if (r < rend) {
+      float y[32];
 #pragma unroll
       for (int j = 0; j < 32; ++j) y[j] = src[r * ld + j];
       if (use_rcur) {
-        double yd[32];
 #pragma unroll
         for (int j = 0; j < 32; ++j) {
           double a = (double)y[j];
@@ -366,33 +380,44 @@ __global__ __launch_bounds__(kThr) void cq_pass_kernel(const float* __restrict__
           Qout[r * 32 + j] = y[j];
         }
       }
+#pragma unroll
+      for (int j = 0; j < 32; ++j) yd[j] = (double)y[j];
     } else {
 #pragma unroll
-      for (int j = 0; j < 32; ++j) y[j] = 0.f;
+      for (int j = 0; j < 32; ++j) yd[j] = 0.0;
     }
     if (chol_pass > 0) {
 #pragma unroll
-      for (int j = 0; j < 32; ++j) tile[t][j] = y[j];
+      for (int j = 0; j < 32; j += 2)
+        *reinterpret_cast<double2*>(&tile[t * kCqLd + j]) = make_double2(yd[j], yd[j + 1]);
       __syncthreads();
       const int rows = (int)min((int64_t)kCqTile, rend - r0);
-      for (int rr = 0; rr < rows; ++rr) {
-        const double yi0 = (double)tile[rr][i0g], yi1 = (double)tile[rr][i0g + 1];
-        const double yj0 = (double)tile[rr][j0g], yj1 = (double)tile[rr][j0g + 1];
-        acc[0] = fma(yi0, yj0, acc[0]);
-        acc[1] = fma(yi0, yj1, acc[1]);
-        acc[2] = fma(yi1, yj0, acc[2]);
-        acc[3] = fma(yi1, yj1, acc[3]);
+      for (int rr = grp; rr < rows; rr += 4) {
+        const double* row = &tile[rr * kCqLd];
+        const double2 i01 = *reinterpret_cast<const double2*>(row + 4 * bi);
+        const double2 i23 = *reinterpret_cast<const double2*>(row + 4 * bi + 2);
+        const double2 j01 = *reinterpret_cast<const double2*>(row + 4 * bj);
+        const double2 j23 = *reinterpret_cast<const double2*>(row + 4 * bj + 2);
+        const double yi[4] = {i01.x, i01.y, i23.x, i23.y};
+        const double yj[4] = {j01.x, j01.y, j23.x, j23.y};
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) acc[a * 4 + b] = fma(yi[a], yj[b], acc[a * 4 + b]);
       }
       __syncthreads();
     }
   }
   if (chol_pass == 0) return;
   {
+    // the four row groups' blocks, added in group order
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) tile[grp * 1024 + (4 * bi + a) * 32 + 4 * bj + b] = acc[a * 4 + b];
+    __syncthreads();
     double* gp = Gp + (int64_t)blockIdx.x * 1024;
-    gp[i0g * 32 + j0g] = acc[0];
-    gp[i0g * 32 + j0g + 1] = acc[1];
-    gp[(i0g + 1) * 32 + j0g] = acc[2];
-    gp[(i0g + 1) * 32 + j0g + 1] = acc[3];
+    for (int e = t; e < 1024; e += kThr) gp[e] = ((tile[e] + tile[1024 + e]) + tile[2048 + e]) + tile[3072 + e];
   }
   // the last work-group to finish reduces and factors
   __threadfence();
@@ -404,21 +429,54 @@ __global__ __launch_bounds__(kThr) void cq_pass_kernel(const float* __restrict__
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();
-  for (int e = t; e < 1024; e += kThr) {
-    double a = 0.0;
-    for (int g = 0; g < (int)gridDim.x; ++g) a += __hip_atomic_load(&Gp[(int64_t)g * 1024 + e], __ATOMIC_RELAXED,
-                                                                     __HIP_MEMORY_SCOPE_AGENT);
-    G[e >> 5][e & 31] = a;
+  __threadfence();  // acquire: the partials of every work-group are visible to plain loads
+  // lower triangle only (the factorisation reads no other entry), partials added in work-group
+  // order, 16 of them in flight per entry
+  const int ng = (int)gridDim.x;
+  {
+    double a4[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int g0 = 0; g0 < ng; g0 += 16) {
+      double v[4][16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = t + q * kThr;
+        const bool low = (e >> 5) >= (e & 31);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[q][u] = (low && g0 + u < ng) ? Gp[(int64_t)(g0 + u) * 1024 + e] : 0.0;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int u = 0; u < 16; ++u) a4[q] += v[q][u];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = t + q * kThr;
+      G[e >> 5][e & 31] = a4[q];
+    }
   }
   if (t == 0) *counter = 0u;  // ready for the next launch
   __syncthreads();
+  // pass 2: the Gram matrix of the pass-1 factor measures how far it is from orthonormal; within
+  // 2e-4 of I, the pass-2 factor is orthonormal to working precision and pass 3 is skipped
+  if (chol_pass == 2) {
+    double dev = 0.0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = t + q * kThr, i = e >> 5, j = e & 31;
+      if (i >= j) dev = fmax(dev, fabs(G[i][j] - (i == j ? 1.0 : 0.0)));
+    }
+    for (int off = 32; off >= 1; off >>= 1) dev = fmax(dev, __shfl_xor(dev, off));
+    if ((t & 63) == 0) sRinv[t >> 6] = dev;  // scratch (sRinv is not used after the rows)
+  }
   cq_cholesky(G, chol_pass, m, &bad);
   __syncthreads();
   if (bad) {
     if (t == 0) *fallback = 1;
     return;
   }
+  const bool converged =
+      chol_pass == 2 && fmax(fmax(sRinv[0], sRinv[1]), fmax(sRinv[2], sRinv[3])) < 2e-4;
   // R = L^T (upper); R_tot <- R R_tot
   for (int e = t; e < 1024; e += kThr) {
     const int i = e >> 5, j = e & 31;
@@ -438,16 +496,38 @@ __global__ __launch_bounds__(kThr) void cq_pass_kernel(const float* __restrict__
     double a = 0.0;
     for (int l = i; l <= j; ++l) a = fma(G[l][i], sR[l][j], a);  // R[i][l] = L[l][i]
     Rtot[e] = j >= i ? a : 0.0;
-    if (chol_pass == 3) Rroot[e] = j >= i ? (float)a : 0.f;
+    if (chol_pass == 3 || converged) Rroot[e] = j >= i ? (float)a : 0.f;
   }
+  if (converged && t == 0) *fallback = 2;  // pass 3 returns at once; hr_kernel applies R2
 }
 
 // Householder reconstruction from Q1 (m x 32, kk = min(m, 32) columns used) and the panel's
-// results.  Every work-group factors the kk x kk top block redundantly (cheap) and then handles
-// 256 panel rows: Y row = L row (top block) or Q1 row U^-1, YT row = Y row T; the reflectors go
-// to the rows of A (row c0 + j holds Y[r][j] at column r0 + r, r > j).  Work-group 0 also
-// writes T, tau and the band block A[r0 + i][c0 + j] = (S R)[i][j] (j >= i, zero below).
-__global__ __launch_bounds__(kThr) void hr_kernel(const float* __restrict__ Q1, const float* __restrict__ Rroot,
+// results.  On the Cholesky QR path Q1 still lacks the last factor (Rc, fp64): every row is first
+// solved with it; after the tall-skinny fallback (flag 1) Q1 is final.  Every work-group factors
+// the kk x kk top block redundantly and then handles 256 panel rows: Y row = L row (top block) or
+// Q1 row U^-1, YT row = Y row T; the reflectors go to the rows of A (row c0 + j holds Y[r][j] at
+// column r0 + r, r > j).  Work-group 0 also writes T, tau and the band block
+// A[r0 + i][c0 + j] = (S R)[i][j] (j >= i, zero below).
+__device__ __forceinline__ void hr_q1_row(const float* __restrict__ q, const double (*sR)[33], const double* sRinv,
+                                          bool apply, float (&out)[32]) {
+  if (!apply) {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) out[j] = q[j];
+    return;
+  }
+  double yd[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    double a = (double)q[j];
+#pragma unroll
+    for (int i = 0; i < j; ++i) a = fma(-yd[i], sR[i][j], a);
+    yd[j] = a * sRinv[j];
+    out[j] = (float)yd[j];
+  }
+}
+
+__global__ __launch_bounds__(kThr) void hr_kernel(const float* __restrict__ Q1, const double* __restrict__ Rc,
+                                                  const int* __restrict__ fallback, const float* __restrict__ Rroot,
                                                   int64_t m, float* __restrict__ A, int64_t lda, int64_t r0,
                                                   int64_t c0, float* __restrict__ Y, float* __restrict__ YT,
                                                   float* __restrict__ Tout, float* __restrict__ tau) {
@@ -455,15 +535,26 @@ __global__ __launch_bounds__(kThr) void hr_kernel(const float* __restrict__ Q1, 
   __shared__ float Xi[32][33];  // L1^-T
   __shared__ float Ts[32][33];
   __shared__ float S[32];
+  __shared__ double sR[32][33];
+  __shared__ double sRinv[32];
   const int kk = (int)min<int64_t>(m, 32);
   const int t = threadIdx.x;
-  for (int e = t; e < 32 * 32; e += kThr) {
-    const int i = e / 32, j = e & 31;
-    LU[i][j] = (i < kk && j < kk) ? Q1[i * 32 + j] : 0.f;
+  const bool apply = *fallback != 1;
+  if (apply) {
+    for (int e = t; e < 1024; e += kThr) sR[e >> 5][e & 31] = Rc[e];
+    if (t < 32) sRinv[t] = 1.0 / Rc[t * 33];
   }
   __syncthreads();
-  // LU without pivoting of Q1 - S, S_i = -sign of the current pivot (|U_ii| >= 1): wave 0, lane r
-  // holds row r in registers, pivot rows by readlane (loops unrolled: register indices are static)
+  if (t < 32) {
+    float q[32];
+    if (t < kk) hr_q1_row(Q1 + t * 32, sR, sRinv, apply, q);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) LU[t][j] = (t < kk && j < kk) ? q[j] : 0.f;
+  }
+  __syncthreads();
+  // LU without pivoting of Q1 - S, S_i = -sign of the current pivot (|U_ii| >= 1), then L1^-1:
+  // wave 0, lane r holds row r in registers, pivot rows by readlane (loops unrolled: register
+  // indices are static)
   if (t < 64) {
     float row[32];
 #pragma unroll
@@ -487,22 +578,28 @@ __global__ __launch_bounds__(kThr) void hr_kernel(const float* __restrict__ Q1, 
         if (t == 0) S[i] = si;
       }
     }
+    // L1^-1 (unit lower): row t = e_t - sum_{c < t} L1[t][c] (row c), rows in increasing order
+    float inv[32];
+#pragma unroll
+    for (int c = 0; c < 32; ++c) inv[c] = t == c ? 1.f : 0.f;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+      if (c < kk) {
+        float ic[32];
+#pragma unroll
+        for (int k = 0; k <= c; ++k) ic[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv[k]), c));
+        const float l = (t > c && t < kk) ? row[c] : 0.f;
+#pragma unroll
+        for (int k = 0; k <= c; ++k) inv[k] = fmaf(-l, ic[k], inv[k]);
+      }
+    }
     if (t < 32) {
 #pragma unroll
-      for (int c = 0; c < 32; ++c) LU[t][c] = row[c];
-    }
-  }
-  __syncthreads();
-  // Xi = L1^-T (unit upper): column j by back substitution, Xi[i][j] = -sum_{l=i+1..j} L1[l][i] Xi[l][j]
-  if (t < 32) {
-    const int j = t;
-    for (int i = 0; i < 32; ++i) Xi[i][j] = i == j && j < kk ? 1.f : 0.f;
-    if (j < kk)
-      for (int i = j - 1; i >= 0; --i) {
-        float acc = 0.f;
-        for (int l = i + 1; l <= j; ++l) acc = fmaf(LU[l][i], Xi[l][j], acc);
-        Xi[i][j] = -acc;
+      for (int c = 0; c < 32; ++c) {
+        LU[t][c] = row[c];
+        Xi[c][t] = t < kk ? inv[c] : 0.f;  // Xi = (L1^-1)^T
       }
+    }
   }
   __syncthreads();
   // T = -U S Xi (upper)
@@ -521,7 +618,8 @@ __global__ __launch_bounds__(kThr) void hr_kernel(const float* __restrict__ Q1, 
 #pragma unroll
       for (int j = 0; j < 32; ++j) y[j] = j < r ? LU[r][j] : (j == r ? 1.f : 0.f);
     } else {
-      const float* q = Q1 + r * 32;
+      float q[32];
+      hr_q1_row(Q1 + r * 32, sR, sRinv, apply, q);
 #pragma unroll
       for (int j = 0; j < 32; ++j) {
         float acc = j < kk ? q[j] : 0.f;
@@ -618,8 +716,6 @@ __global__ __launch_bounds__(kThr) void w_kernel(const float* __restrict__ Mg, c
   }
 }
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-
 // Split-K partials of X = A22 B with B = Y T (m x 32), from the lower triangle of A22 only (the
 // trailing update keeps the lower triangle and the 32 x 32 diagonal blocks current):
 //   pass 0 (row strips):    P0[ks][r][:] = sum_{k in split ks, k < 32 (r / 32 + 1)} A22[r][k] B[k][:]
@@ -706,12 +802,6 @@ __global__ __launch_bounds__(kThr) void band_extract_kernel(const float* __restr
   const int64_t j = e / kABld;
   const int d = (int)(e % kABld);
   AB[e] = (d <= kBW && j + d < n) ? A[(j + d) * lda + j] : 0.f;
-}
-
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Wave sums without LDS: rotate-and-add inside each 16-lane row (DPP row_ror 8, 4, 2, 1), then the
@@ -1276,7 +1366,8 @@ int sy2sb(int64_t n, float* A, int64_t lda, float* tau, float* ws, const Layout&
     const int64_t r0 = c0 + kBW, m = n - r0;
     const int64_t nleaf = (m + kLeaf - 1) / kLeaf;
     const int root_rows = (int)(32 * (nleaf - 1) + std::min<int64_t>(32, m - kLeaf * (nleaf - 1)));
-    // Q1 R = P: Cholesky QR (three passes), or the tall-skinny Householder QR when it fails
+    // Q1 R = P: Cholesky QR (three passes; hr_kernel applies the last factor), or the tall-skinny
+    // Householder QR when it fails
     const int* fb = flags + pidx;
     int* fbw = flags + pidx;
     const float* P = A + r0 * lda + c0;
@@ -1286,12 +1377,11 @@ int sy2sb(int64_t n, float* A, int64_t lda, float* tau, float* ws, const Layout&
     double* Rc = reinterpret_cast<double*>(ws + L.Rc);
     double* Rt = reinterpret_cast<double*>(ws + L.Rt);
     unsigned* counter = reinterpret_cast<unsigned*>(flags + npanels + 1);
-    // pass p's launch solves with R_{p-1} and factors the Gram matrix of the result (R_p); the
-    // fourth launch applies R_3 only
-    for (int pass = 1; pass <= 4; ++pass) {
+    // pass p's launch solves with R_{p-1} and factors the Gram matrix of the result (R_p)
+    for (int pass = 1; pass <= 3; ++pass) {
       hipLaunchKernelGGL(cq_pass_kernel, dim3((unsigned)cq_ng), dim3(kThr), 0, stream, pass <= 2 ? P : ws + L.Q1,
-                         pass <= 2 ? lda : (int64_t)32, m, cq_chunk, Rc, pass > 1 ? 1 : 0, ws + L.Q1, Gp,
-                         pass <= 3 ? pass : 0, Rt, ws + L.Rroot, fbw, counter);
+                         pass <= 2 ? lda : (int64_t)32, m, cq_chunk, Rc, pass > 1 ? 1 : 0, ws + L.Q1, Gp, pass, Rt,
+                         ws + L.Rroot, fbw, counter);
       MPQ_LAUNCH_CHECK();
     }
     hipLaunchKernelGGL(leaf_qr_kernel, dim3((unsigned)nleaf), dim3(kPThr), 0, stream, A, lda, r0, c0, m, ws + L.Yl,
@@ -1304,8 +1394,8 @@ int sy2sb(int64_t n, float* A, int64_t lda, float* tau, float* ws, const Layout&
                        ws + L.E, m, ws + L.Q1, fb);
     MPQ_LAUNCH_CHECK();
     const unsigned rblocks = (unsigned)((m + kThr - 1) / kThr);
-    hipLaunchKernelGGL(hr_kernel, dim3(rblocks), dim3(kThr), 0, stream, ws + L.Q1, ws + L.Rroot, m, A, lda, r0, c0,
-                       ws + L.Y, ws + L.YT, ws + L.T, tau);
+    hipLaunchKernelGGL(hr_kernel, dim3(rblocks), dim3(kThr), 0, stream, ws + L.Q1, Rc, fb, ws + L.Rroot, m, A, lda,
+                       r0, c0, ws + L.Y, ws + L.YT, ws + L.T, tau);
     MPQ_LAUNCH_CHECK();
     float* A22 = A + r0 * lda + r0;
     // X = A22 (Y T): split-K partials, summed in split order
