@@ -843,28 +843,6 @@ __device__ __forceinline__ Refl make_refl(float x, int a, int h) {
   return r;
 }
 
-// Two-sided D <- H D H (D symmetric, full 32 x 32 in LDS), H = I - tau v v^T, v in sv.
-__device__ __forceinline__ void two_sided(float (*D)[33], const float* sv, float* sy, float tau, int a, int h) {
-  const float va = sv[a];
-  float w = 0.f;
-#pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const int c = 16 * h + q;
-    w = fmaf(D[a][c], sv[c], w);
-  }
-  w = half_pair_sum(w);
-  const float vw = wave_sum64(h == 0 ? va * w : 0.f);
-  const float y = tau * w - 0.5f * tau * tau * vw * va;
-  if (h == 0) sy[a] = y;
-  wave_sync();
-#pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const int c = 16 * h + q;
-    D[a][c] = D[a][c] - (va * sy[c] + y * sv[c]);
-  }
-  wave_sync();
-}
-
 struct BulgeArgs {
   float* AB;
   int64_t n;
@@ -879,18 +857,24 @@ __device__ __forceinline__ int64_t boff(int64_t g, int64_t K0) { return g * (K0 
 
 // One wave per sweep; the NW waves of a work-group take sweeps grp NW .. grp NW + NW - 1 for
 // grp = blockIdx.x, blockIdx.x + gridDim.x, ...  Cooperative launch (all work-groups resident).
+// A task keeps its blocks in registers, lane (a, h) holding row a, columns cc = h + 2 q (q < 16),
+// of the diagonal block D (full, mirrored from the stored lower triangle) and of the off-diagonal
+// block O, and the previous reflector at the same columns.  O H_prev and D's products with v are
+// row dot products (two-lane sums); H O needs columns, so O and v go through LDS (the lane then
+// owns column a, rows 16 h .. 16 h + 15) and O comes back to rows for coalesced stores; y of the
+// two-sided update goes through LDS as well.
 __global__ __launch_bounds__(64 * kNW) void bulge_kernel(BulgeArgs args) {
-  __shared__ float sD[kNW][32][33];
   __shared__ float sO[kNW][32][33];
-  __shared__ float sv[kNW][2][32];
+  __shared__ float sv[kNW][32];
   __shared__ float sy[kNW][32];
   __shared__ int lprog[kNW];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, a = lane & 31, h = lane >> 5;
   float* __restrict__ AB = args.AB;
   const int64_t n = args.n;
   const int64_t K0 = (n - 2) / kBW;
-  float(*D)[33] = sD[w];
   float(*O)[33] = sO[w];
+  float* vs = sv[w];
+  float* ys = sy[w];
   if (lane == 0) lprog[w] = -1;
   __syncthreads();
   const int64_t nsweeps = n - 1;
@@ -901,8 +885,10 @@ __global__ __launch_bounds__(64 * kNW) void bulge_kernel(BulgeArgs args) {
     const int64_t K = (n - 2 - s) / kBW;                    // last chase step of this sweep
     const int64_t Kp = s > 0 ? (n - 1 - s) / kBW : 0;       // last chase step of sweep s - 1
     int seen = -1;
-    int cur = 0;       // which sv buffer holds the current reflector
     float tau_prev = 0.f;
+    float vp[16];  // previous reflector at this lane's columns
+#pragma unroll
+    for (int q = 0; q < 16; ++q) vp[q] = 0.f;
     for (int64_t k = 0; k <= K; ++k) {
       // wait until sweep s - 1 has finished its tasks up to k + 1
       if (s > 0) {
@@ -935,14 +921,8 @@ __global__ __launch_bounds__(64 * kNW) void bulge_kernel(BulgeArgs args) {
         }
       }
       const int64_t g = s / kBW, bid = boff(g, K0) + k;
-      float* vcur = sv[w][cur];
-      const float* vprev = sv[w][cur ^ 1];
-      Refl rf;
-      int64_t r0;
-      // every load of the task is issued before the first use (one memory round trip): the lane
-      // reads D[a][cc] for its 16 columns cc = h, h + 2, ... from the stored lower triangle (the
-      // upper entries through their mirror) and, for k >= 1, the same entries of O
-      r0 = k == 0 ? s + 1 : s + 1 + k * kBW;
+      // every load of the task is issued before the first use (one memory round trip)
+      const int64_t r0 = k == 0 ? s + 1 : s + 1 + k * kBW;
       const int64_t p0 = r0 - kBW;
       // wave-uniform bases, 32-bit lane offsets (few live registers across the loads)
       float* __restrict__ ABr = AB + r0 * kABld;
@@ -961,59 +941,87 @@ __global__ __launch_bounds__(64 * kNW) void bulge_kernel(BulgeArgs args) {
         }
       }
       const float x0 = k == 0 ? AB[s * kABld + 1 + a] : 0.f;
-#pragma unroll
-      for (int q = 0; q < 16; ++q) D[a][h + 2 * q] = dv[q];
+      Refl rf;
+      float va;  // v[a]
       if (k == 0) {
         // column s below the subdiagonal: AB[s][1 .. 32]
         rf = make_refl(x0, a, h);
+        va = a == 0 ? 1.f : x0 * rf.scal;
         if (h == 0) {
-          vcur[a] = a == 0 ? 1.f : x0 * rf.scal;
+          vs[a] = va;
           AB[s * kABld + 1 + a] = a == 0 ? rf.beta : 0.f;
         }
         wave_sync();
       } else {
-#pragma unroll
-        for (int q = 0; q < 16; ++q) O[a][h + 2 * q] = ov[q];
-        wave_sync();
-        // O <- O H_prev (rows: lane's row a, columns in its half)
+        // O <- O H_prev: row a dotted with v_prev
         float u = 0.f;
 #pragma unroll
-        for (int q = 0; q < 16; ++q) u = fmaf(O[a][16 * h + q], vprev[16 * h + q], u);
+        for (int q = 0; q < 16; ++q) u = fmaf(ov[q], vp[q], u);
         u = half_pair_sum(u);
 #pragma unroll
-        for (int q = 0; q < 16; ++q) O[a][16 * h + q] = fmaf(-tau_prev * u, vprev[16 * h + q], O[a][16 * h + q]);
-        wave_sync();
-        const float x = O[a][0];
+        for (int q = 0; q < 16; ++q) ov[q] = fmaf(-tau_prev * u, vp[q], ov[q]);
+        // reflector from column 0 (held by the h = 0 lane of row a as ov[0]); both halves take x[a]
+        const float xh = __uint_as_float(
+            __builtin_amdgcn_permlane32_swap(__float_as_uint(ov[0]), __float_as_uint(ov[0]), false, false)[0]);
+        const float x = h == 0 ? ov[0] : xh;
         rf = make_refl(x, a, h);
-        if (h == 0) vcur[a] = a == 0 ? 1.f : x * rf.scal;
+        va = a == 0 ? 1.f : x * rf.scal;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) O[a][h + 2 * q] = ov[q];
+        if (h == 0) vs[a] = va;
         wave_sync();
-        // O <- H O (column a of the lane, rows in its half); column 0 becomes (beta, 0, ...)
+        // O <- H O on column a, rows 16 h .. 16 h + 15; column 0 becomes (beta, 0, ...)
+        float oc[16], vv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          oc[j] = O[16 * h + j][a];
+          vv[j] = vs[16 * h + j];
+        }
         float z = 0.f;
 #pragma unroll
-        for (int q = 0; q < 16; ++q) z = fmaf(vcur[16 * h + q], O[16 * h + q][a], z);
+        for (int j = 0; j < 16; ++j) z = fmaf(vv[j], oc[j], z);
         z = half_pair_sum(z);
+        wave_sync();  // every column read before the result overwrites it
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const int i = 16 * h + q;
-          O[i][a] = a == 0 ? (i == 0 ? rf.beta : 0.f) : fmaf(-rf.tau * z, vcur[i], O[i][a]);
+        for (int j = 0; j < 16; ++j) {
+          const int i = 16 * h + j;
+          O[i][a] = a == 0 ? (i == 0 ? rf.beta : 0.f) : fmaf(-rf.tau * z, vv[j], oc[j]);
         }
         wave_sync();
+        // row layout again for coalesced stores (row a, columns cc: consecutive lanes, consecutive
+        // addresses)
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
           const int cc = h + 2 * q;
           ABp[cc * kABld + (a + 32 - cc)] = O[a][cc];
         }
       }
-      two_sided(D, vcur, sy[w], rf.tau, a, h);
+      // D <- H D H: w = D v (rows), y = tau w - tau^2 (v.w) v / 2, D -= v y^T + y v^T
+      float vr[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) vr[q] = vs[h + 2 * q];
+      float wr = 0.f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) wr = fmaf(dv[q], vr[q], wr);
+      wr = half_pair_sum(wr);
+      const float vw = wave_sum64(h == 0 ? va * wr : 0.f);
+      const float y = rf.tau * wr - 0.5f * rf.tau * rf.tau * vw * va;
+      if (h == 0) ys[a] = y;
+      wave_sync();
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         const int cc = h + 2 * q;
-        if (a >= cc) ABr[cc * kABld + (a - cc)] = D[a][cc];
+        const float d = dv[q] - (va * ys[cc] + y * vr[q]);
+        if (a >= cc) ABr[cc * kABld + (a - cc)] = d;
       }
-      if (h == 0) args.V2[(bid * 32 + (s % kBW)) * 32 + a] = vcur[a];
+      if (h == 0) args.V2[(bid * 32 + (s % kBW)) * 32 + a] = va;
       if (lane == 0) args.tau2[bid * 32 + (s % kBW)] = rf.tau;
       tau_prev = rf.tau;
-      cur ^= 1;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) vp[q] = vr[q];
+      // the next task rewrites O, v and y in LDS only after its loads and its own barrier; order
+      // this task's LDS reads before those writes
+      wave_sync();
       // publish
       const int val = (int)(s * kProgStride + (k == K ? kProgStride - 1 : k + 1));
       if (w == kNW - 1) {
