@@ -44,6 +44,7 @@ namespace {
 
 constexpr int kThr = 256;
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -648,6 +649,22 @@ __global__ __launch_bounds__(kThr) void hr_kernel(const float* __restrict__ Q1, 
   }
 }
 
+// X = the split-K partials of X = A22 (Y T) added in split order (8 loads in flight per element).
+__global__ __launch_bounds__(kThr) void xsum_kernel(const float* __restrict__ P, int splits, int64_t cnt,
+                                                    float* __restrict__ X) {
+  const int64_t e = (int64_t)blockIdx.x * kThr + threadIdx.x;
+  if (e >= cnt) return;
+  float a = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = s0 + u < splits ? P[(int64_t)(s0 + u) * cnt + e] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a += v[u];
+  }
+  X[e] = a;
+}
+
 // Partial grams Gp[g] = Y^T X over the rows of chunk g (64-row tiles staged in LDS).
 __global__ __launch_bounds__(kThr) void gram_partial_kernel(const float* __restrict__ Y, const float* __restrict__ X,
                                                             int64_t m, int64_t chunk, float* __restrict__ Gp) {
@@ -691,29 +708,126 @@ __global__ __launch_bounds__(1024) void m_kernel(const float* __restrict__ Gp, i
   Mout[e] = mv;
 }
 
-// W = X - 1/2 Y M and the update operands Xop = [Y W], Yop = [W Y] (m x 64 each).
+// W = X - 1/2 Y M and the operands of the rank-64 update A22 -= [Y W] [W Y]^T as three bf16 planes
+// (exact split, see x6_split.h): Xp holds -[Y W], Yp holds [W Y], both in the operand order of
+// v_mfma_f32_32x32x16_bf16, per 32-row tile T chunk (plane p, k-step s, lane l) at
+// T * 768 + (p * 4 + s) * 64 + l = row 32 T + l % 32, k = 16 s + 8 (l / 32) + 0 .. 7.  Rows m ..
+// (a multiple of 128) are zero.
+constexpr int kUpdTile = 768;  // uint4 per 32-row tile of a packed update operand
 __global__ __launch_bounds__(kThr) void w_kernel(const float* __restrict__ Mg, const float* __restrict__ Y,
-                                                 const float* __restrict__ X, int64_t m, float* __restrict__ Xop,
-                                                 float* __restrict__ Yop) {
+                                                 const float* __restrict__ X, int64_t m, uint4* __restrict__ Xp,
+                                                 uint4* __restrict__ Yp) {
   __shared__ float M[32][33];
   const int t = threadIdx.x;
   for (int e = t; e < 1024; e += kThr) M[e >> 5][e & 31] = Mg[e];
   __syncthreads();
   const int64_t r = (int64_t)blockIdx.x * kThr + t;
-  if (r >= m) return;
-  float y[32];
+  if (r >= (m + 127) / 128 * 128) return;  // packed rows: m rounded up to 128
+  float y[32], w[32];
+  if (r < m) {
 #pragma unroll
-  for (int j = 0; j < 32; ++j) y[j] = Y[r * 32 + j];
+    for (int j = 0; j < 32; ++j) y[j] = Y[r * 32 + j];
 #pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    float a = 0.f;
-    for (int l = 0; l < 32; ++l) a = fmaf(y[l], M[l][j], a);
-    const float w = fmaf(-0.5f, a, X[r * 32 + j]);
-    Xop[r * 64 + j] = y[j];
-    Xop[r * 64 + 32 + j] = w;
-    Yop[r * 64 + j] = w;
-    Yop[r * 64 + 32 + j] = y[j];
+    for (int j = 0; j < 32; ++j) {
+      float a = 0.f;
+      for (int l = 0; l < 32; ++l) a = fmaf(y[l], M[l][j], a);
+      w[j] = fmaf(-0.5f, a, X[r * 32 + j]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      y[j] = 0.f;
+      w[j] = 0.f;
+    }
   }
+  uint4* xo = Xp + (r >> 5) * kUpdTile + (r & 31);
+  uint4* yo = Yp + (r >> 5) * kUpdTile + (r & 31);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {  // chunk c: k = 8 c .. 8 c + 7 (s = c / 2, half = c % 2)
+    const float* src = c < 4 ? &y[8 * c] : &w[8 * (c - 4)];    // [Y W]
+    const float* srb = c < 4 ? &w[8 * c] : &y[8 * (c - 4)];    // [W Y]
+    uint4 h, mm, l, hb, mb, lb;
+    split3(-src[0], -src[1], h.x, mm.x, l.x);
+    split3(-src[2], -src[3], h.y, mm.y, l.y);
+    split3(-src[4], -src[5], h.z, mm.z, l.z);
+    split3(-src[6], -src[7], h.w, mm.w, l.w);
+    split3(srb[0], srb[1], hb.x, mb.x, lb.x);
+    split3(srb[2], srb[3], hb.y, mb.y, lb.y);
+    split3(srb[4], srb[5], hb.z, mb.z, lb.z);
+    split3(srb[6], srb[7], hb.w, mb.w, lb.w);
+    const int off = (c >> 1) * 64 + (c & 1) * 32;
+    xo[off] = h;
+    xo[256 + off] = mm;
+    xo[512 + off] = l;
+    yo[off] = hb;
+    yo[256 + off] = mb;
+    yo[512 + off] = lb;
+  }
+}
+
+// A22 += (-[Y W]) [W Y]^T on every 128 x 128 tile (ti, tj) with tj <= ti (the lower triangle and
+// whole diagonal tiles; entries above the diagonal are never read).  One work-group per tile
+// (triangular index), wave (wr, wc) owns the 64 x 64 quarter (two by two 32 x 32 MFMA tiles): the
+// fp32 tile is loaded straight into the accumulators, then K = 64 in four 16-k steps of six bf16
+// plane products, then stored.
+__global__ __launch_bounds__(kThr) void syr2k_x6_kernel(const uint4* __restrict__ Xp, const uint4* __restrict__ Yp,
+                                                        float* __restrict__ A, int64_t lda, int64_t m) {
+  const int64_t b = blockIdx.x;
+  int64_t ti = (int64_t)((sqrt(8.0 * (double)b + 1.0) - 1.0) * 0.5);
+  while ((ti + 1) * (ti + 2) / 2 <= b) ++ti;
+  while (ti * (ti + 1) / 2 > b) --ti;
+  const int64_t tj = b - ti * (ti + 1) / 2;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int64_t R0 = 128 * ti + 64 * wr, C0 = 128 * tj + 64 * wc;
+  const int col = lane & 31, rq = 4 * (lane >> 5);
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int64_t c = C0 + 32 * y + col;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t r = R0 + 32 * x + 8 * (v >> 2) + rq + (v & 3);
+        acc[x][y][v] = (r < m && c < m) ? A[r * lda + c] : 0.f;
+      }
+    }
+  const uint4* xa = Xp + (R0 >> 5) * kUpdTile + lane;
+  const uint4* yb = Yp + (C0 >> 5) * kUpdTile + lane;
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    bf16x8 av[2][3], bv[2][3];
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        av[x][p] = __builtin_bit_cast(bf16x8, xa[x * kUpdTile + (p * 4 + st) * 64]);
+        bv[x][p] = __builtin_bit_cast(bf16x8, yb[x * kUpdTile + (p * 4 + st) * 64]);
+      }
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y) {
+        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[x][0], bv[y][0], acc[x][y], 0, 0, 0);
+        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[x][0], bv[y][1], acc[x][y], 0, 0, 0);
+        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[x][1], bv[y][0], acc[x][y], 0, 0, 0);
+        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[x][0], bv[y][2], acc[x][y], 0, 0, 0);
+        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[x][1], bv[y][1], acc[x][y], 0, 0, 0);
+        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[x][2], bv[y][0], acc[x][y], 0, 0, 0);
+      }
+  }
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int64_t c = C0 + 32 * y + col;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t r = R0 + 32 * x + 8 * (v >> 2) + rq + (v & 3);
+        if (r < m && c < m) A[r * lda + c] = acc[x][y][v];
+      }
+    }
 }
 
 // Split-K partials of X = A22 B with B = Y T (m x 32), from the lower triangle of A22 only (the
@@ -727,14 +841,15 @@ __global__ __launch_bounds__(kThr) void w_kernel(const float* __restrict__ Mg, c
 constexpr int kXKC = 512;  // k per split
 template <int kPass>
 __global__ __launch_bounds__(kThr) void xprod_kernel(const float* __restrict__ A, int64_t lda,
-                                                     const float* __restrict__ B, int64_t m, float* __restrict__ P) {
+                                                     const float* __restrict__ B, int64_t m, int64_t kxkc,
+                                                     float* __restrict__ P) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = lane & 31, h = lane >> 5;
   const int64_t rbase = (int64_t)blockIdx.x * 128 + wave * 32;  // this wave's 32 output rows
   const int64_t r = rbase + row;
   const int64_t rc = r < m ? r : m - 1;
   const int64_t lim = rbase + 32;  // pass 0: k < lim; pass 1: i >= lim
-  int64_t k0 = (int64_t)blockIdx.y * kXKC, k1 = min(m, k0 + kXKC);
+  int64_t k0 = (int64_t)blockIdx.y * kxkc, k1 = min(m, k0 + kxkc);
   if (kPass == 0) k1 = min(k1, lim);
   else k0 = max(k0, lim);
   floatx16 acc;
@@ -780,16 +895,6 @@ __global__ __launch_bounds__(kThr) void xprod_kernel(const float* __restrict__ A
     const int64_t rr = rbase + 8 * (v >> 2) + 4 * h + (v & 3);
     if (rr < m) Ps[rr * 32 + row] = acc[v];
   }
-}
-
-// X = sum of the partials in split order.
-__global__ __launch_bounds__(kThr) void xsum_kernel(const float* __restrict__ P, int splits, int64_t cnt,
-                                                    float* __restrict__ X) {
-  const int64_t e = (int64_t)blockIdx.x * kThr + threadIdx.x;
-  if (e >= cnt) return;
-  float a = P[e];
-  for (int s2 = 1; s2 < splits; ++s2) a += P[(int64_t)s2 * cnt + e];
-  X[e] = a;
 }
 
 // ---- stage 2: bulge chasing ------------------------------------------------------------------
@@ -1048,7 +1153,6 @@ __global__ __launch_bounds__(kThr) void tridiag_out_kernel(const float* __restri
 
 // ---- back-transformation of stage 2 ----------------------------------------------------------
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int kPtChunks = 3 * 512;  // uint4 per block: 3 bf16 planes x (2 row tiles x 4 k-steps x 64 lanes)
 constexpr int kZs = 9;              // uint4 per LDS window row: 64 bf16 + 16 bytes of padding
 
@@ -1341,8 +1445,8 @@ Layout layout(int64_t n) {
   L.X = take(n * 32);
   L.T = take(32 * 32);
   L.Gp = take(64 * 1024);
-  L.Xop = take(n * 64);
-  L.Yop = take(n * 64);
+  L.Xop = take((n + 127) / 128 * 4 * kUpdTile * 4);  // packed update operands (uint4 = 4 floats)
+  L.Yop = take((n + 127) / 128 * 4 * kUpdTile * 4);
   L.M = take(32 * 32);
   L.px_floats = 2 * ((n + kXKC - 1) / kXKC) * n * 32;  // split-K partials of X = A22 (Y T), two passes
   L.Px = take(L.px_floats);
@@ -1406,16 +1510,17 @@ int sy2sb(int64_t n, float* A, int64_t lda, float* tau, float* ws, const Layout&
                        r0, c0, ws + L.Y, ws + L.YT, ws + L.T, tau);
     MPQ_LAUNCH_CHECK();
     float* A22 = A + r0 * lda + r0;
-    // X = A22 (Y T): split-K partials, summed in split order
-    const int xsplits = (int)((m + kXKC - 1) / kXKC);
-    hipLaunchKernelGGL(xprod_kernel<0>, dim3((unsigned)((m + 127) / 128), (unsigned)xsplits), dim3(kThr), 0, stream,
-                       A22, lda, ws + L.YT, m, ws + L.Px);
+    // X = A22 (Y T): split-K partials, summed in split order; then Y^T X and M = T^T Y^T X
+    const int64_t mtiles = (m + 127) / 128;
+    const int64_t xsplits = (m + kXKC - 1) / kXKC;
+    hipLaunchKernelGGL(xprod_kernel<0>, dim3((unsigned)mtiles, (unsigned)xsplits), dim3(kThr), 0, stream, A22, lda,
+                       ws + L.YT, m, (int64_t)kXKC, ws + L.Px);
     MPQ_LAUNCH_CHECK();
-    hipLaunchKernelGGL(xprod_kernel<1>, dim3((unsigned)((m + 127) / 128), (unsigned)xsplits), dim3(kThr), 0, stream,
-                       A22, lda, ws + L.YT, m, ws + L.Px);
+    hipLaunchKernelGGL(xprod_kernel<1>, dim3((unsigned)mtiles, (unsigned)xsplits), dim3(kThr), 0, stream, A22, lda,
+                       ws + L.YT, m, (int64_t)kXKC, ws + L.Px);
     MPQ_LAUNCH_CHECK();
     hipLaunchKernelGGL(xsum_kernel, dim3((unsigned)((m * 32 + kThr - 1) / kThr)), dim3(kThr), 0, stream, ws + L.Px,
-                       2 * xsplits, m * 32, ws + L.X);
+                       (int)(2 * xsplits), m * 32, ws + L.X);
     MPQ_LAUNCH_CHECK();
     const int64_t ng = std::min<int64_t>(64, (m + 63) / 64);
     const int64_t chunk = ((m + ng - 1) / ng + 63) / 64 * 64;
@@ -1425,11 +1530,17 @@ int sy2sb(int64_t n, float* A, int64_t lda, float* tau, float* ws, const Layout&
     MPQ_LAUNCH_CHECK();
     hipLaunchKernelGGL(m_kernel, dim3(1), dim3(1024), 0, stream, ws + L.Gp, (int)ngu, ws + L.T, ws + L.M);
     MPQ_LAUNCH_CHECK();
-    hipLaunchKernelGGL(w_kernel, dim3(rblocks), dim3(kThr), 0, stream, ws + L.M, ws + L.Y, ws + L.X, m, ws + L.Xop,
-                       ws + L.Yop);
+    const int64_t m128 = (m + 127) / 128 * 128;
+    uint4* Xp = reinterpret_cast<uint4*>(ws + L.Xop);
+    uint4* Yp = reinterpret_cast<uint4*>(ws + L.Yop);
+    hipLaunchKernelGGL(w_kernel, dim3((unsigned)(m128 / kThr + (m128 % kThr ? 1 : 0))), dim3(kThr), 0, stream,
+                       ws + L.M, ws + L.Y, ws + L.X, m, Xp, Yp);
     MPQ_LAUNCH_CHECK();
-    // A22 -= Y W^T + W Y^T on the lower triangle and the 32 x 32 diagonal blocks (whole tiles)
-    MPQ_HIP_TRY(gemm_lower(ws + L.Xop, 64, ws + L.Yop, 64, true, A22, lda, m, 64, -1.f, 1.f, kBW - 1, stream));
+    // A22 -= Y W^T + W Y^T on the lower triangle and whole diagonal tiles
+    const int64_t nt = m128 / 128;
+    hipLaunchKernelGGL(syr2k_x6_kernel, dim3((unsigned)(nt * (nt + 1) / 2)), dim3(kThr), 0, stream, Xp, Yp, A22,
+                       lda, m);
+    MPQ_LAUNCH_CHECK();
   }
   return kOk;
 }
