@@ -42,6 +42,7 @@ HIP_SOURCES = [
     "awq.hip",
     "eigh.hip",
     "eigh_band.hip",
+    "wy_x6.hip",
     "stedc.hip",
 ]
 CXX_SOURCES = [

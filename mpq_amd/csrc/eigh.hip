@@ -35,6 +35,7 @@
 #include "gemm.h"
 #include "kernels.h"
 #include "stedc.h"
+#include "wy_x6.h"
 
 namespace mpq {
 namespace {
@@ -670,7 +671,7 @@ hipError_t transpose_t(const T* in, int64_t rows, int64_t cols, int64_t ld_in, T
 // Workspace layout of mpq_syevd / mpq_syevd_f64 (element offsets, each region 64 elements aligned).
 struct SyevdLayout {
   int64_t lda, nblk, ch_alloc, pn_stride, splits, nb;
-  int64_t A, Z, Y, Yt, W, W2, G, Tb, P, D, E, tau, alph, Pn, Wb, X, Yb, Pr, Pc, Pvv, Ppq, dc, total;
+  int64_t A, Z, Y, Yt, W, W2, G, Tb, P, D, E, tau, alph, Pn, Wb, X, Yb, Pr, Pc, Pvv, Ppq, dc, wy1, wy3, wyw, total;
 };
 
 template <typename T>
@@ -715,6 +716,11 @@ SyevdLayout syevd_layout(int64_t n) {
   L.Pvv = take(L.nblk * L.ch_alloc);
   L.Ppq = take(kDotWG * 64);
   L.dc = take((tridiag_dc_workspace_bytes(n, (int)sizeof(T)) + (int64_t)sizeof(T) - 1) / (int64_t)sizeof(T));
+  // packed operands of the fp32 back-transformation on the bf16 matrix cores
+  const int64_t wyf = sizeof(T) == 4 ? wy_x6_buffer_floats(n) : 0;
+  L.wy1 = take(wyf);
+  L.wy3 = take(wyf);
+  L.wyw = take(wyf);
   L.total = o;
   return L;
 }
@@ -831,6 +837,29 @@ int back_transform(int64_t n, int64_t off, int64_t nrefl, const SyevdLayout& L, 
   if (nblocks > 0) {
     hipLaunchKernelGGL(larft_kernel<T>, dim3((unsigned)nblocks), dim3(256), 0, stream, G, tau, nrefl, Tb);
     MPQ_LAUNCH_CHECK();
+  }
+  if constexpr (sizeof(T) == 4) {
+    // the blocks' products on the bf16 matrix cores (x6 planes)
+    static_assert(NbOf<T>::value == kWyNB, "block size of the x6 back-transformation");
+    struct Extract : WyExtractY {
+      const float* A;
+      int64_t lda, n, off;
+      hipStream_t stream;
+      int operator()(int64_t i0, int nb, float* Yo) const override {
+        const int64_t cnt = (n - i0) * nb;
+        hipLaunchKernelGGL(extract_y_kernel<float>, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, stream, A,
+                           lda, n, i0, nb, off, Yo);
+        MPQ_LAUNCH_CHECK();
+        return kOk;
+      }
+    } ex;
+    ex.A = A;
+    ex.lda = lda;
+    ex.n = n;
+    ex.off = off;
+    ex.stream = stream;
+    return wy_apply_x6(n, nrefl, Tb, Z, Y, Yt, P, (int)L.splits, base + L.wy1, base + L.wy3, base + L.wyw, ex,
+                       stream);
   }
   for (int64_t b = nblocks - 1; b >= 0; --b) {
     const int64_t i0 = b * NB;
