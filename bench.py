@@ -333,7 +333,10 @@ def micro_bench(name, device, reps=50):
     * ``e8p12_posterior``: the E8P12 denoiser (``mpq_e8p12_denoise``) on one config-3 row block,
       128 rows x 2048 columns (32768 8-blocks), with the recipe's prior (centre = the block's
       weights, tau 0.2 absmax) and a VAMP-like message r1 = W + N(0, 1/gamma), gamma = 16;
-    * ``e8p12_map``: the nearest-codeword search on the 2^24 vectors of config 1.
+    * ``e8p12_map``: the nearest-codeword search on the 2^24 vectors of config 1;
+    * ``eigh``: the eigendecomposition (``mpq_syevd``, automatic method: two-stage at this size) of
+      a config-4-sized Hessian, n = 14336, H = X^T X / T with 2n Gaussian tokens of log-normal
+      channel scales.
 
     Prints one JSON line with the average per-call time (HIP events on the launch stream)."""
     import torch
@@ -362,8 +365,22 @@ def micro_bench(name, device, reps=50):
         def go():
             return ke8.e8p12_map_flat(x, one, gamma_div=1 << 24, want_idx64=False, want_idx16=True, want_err=True)
         unit, per = "vectors", 1 << 24
+    elif name == "eigh":
+        from mpq_amd import ops
+
+        n = 14336
+        c = torch.exp(torch.randn(n, device=device, generator=g))
+        X = torch.randn(2 * n, n, device=device, generator=g) * c
+        H = X.T.matmul(X) / (2 * n)
+        del X
+        H = 0.5 * (H + H.T)
+        reps = min(reps, 3)
+
+        def go():
+            return ops.syevd(H)
+        unit, per = "matrices", 1
     else:
-        raise SystemExit(f"unknown --micro {name!r}; choose e8p12_posterior or e8p12_map")
+        raise SystemExit(f"unknown --micro {name!r}; choose e8p12_posterior, e8p12_map or eigh")
     for _ in range(5):
         go()
     torch.cuda.synchronize()
