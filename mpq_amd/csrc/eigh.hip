@@ -903,10 +903,7 @@ int syevd_two_stage(int64_t n, const float* H, float* lam, float* V, float* base
   if ((rc = tridiag_dc(n, base + L.D, base + L.E, lam, Z, base + L.dc, (L.total - L.dc) * (int64_t)sizeof(float), h,
                        stream)) != kOk)
     return rc;
-  // Q2 runs on the columns of Zb^T, held in the output buffer meanwhile
-  MPQ_HIP_TRY(transpose_t(Z, n, n, n, V, n, stream));
-  if ((rc = band::q2_apply(n, V, bws, BL, stream)) != kOk) return rc;
-  MPQ_HIP_TRY(transpose_t(V, n, n, n, Z, n, stream));
+  if ((rc = band::q2_apply(n, Z, bws, BL, stream)) != kOk) return rc;
   if ((rc = back_transform<float>(n, band::kBW, n - band::kBW, L, base, h, stream)) != kOk) return rc;
   MPQ_HIP_TRY(transpose_t(Z, n, n, n, V, n, stream));
   MPQ_HIP_TRY(hipStreamSynchronize(stream));

@@ -24,7 +24,8 @@ inline int64_t q2_blocks(int64_t n) {
 
 // Element offsets (floats) of the two-stage workspace, each region 64 floats aligned.
 struct Layout {
-  int64_t Yl, taul, Rs, E, Rroot, Q1, Y, YT, X, T, Gp, M, Xop, Yop, Px, Gd, Rc, Rt, flags, AB, V2, tau2, Pt, prog, total;
+  int64_t Yl, taul, Rs, E, Rroot, Q1, Y, YT, X, T, Gp, M, Xop, Yop, Px, Gd, Rc, Rt, flags, AB, V2, tau2, Pt, prog, Zq, total;
+  int64_t ldq;  // leading dimension of Zq (n rounded up to 64)
   int64_t px_floats;
 };
 Layout layout(int64_t n);
@@ -40,9 +41,9 @@ int sy2sb(int64_t n, float* A, int64_t lda, float* tau, float* ws, const Layout&
 int sb2st(int64_t n, const float* A, int64_t lda, float* D, float* E, float* ws, const Layout& L,
           hipStream_t stream);
 
-// Zt (n x n, row-major, column k = eigenvector k of the tridiagonal matrix) <- Q2 Zt: the columns
-// become eigenvectors of the band matrix.
-int q2_apply(int64_t n, float* Zt, float* ws, const Layout& L, hipStream_t stream);
+// Z (n x n, row-major, row j = eigenvector j of the tridiagonal matrix) <- Z Q2^T: the rows become
+// eigenvectors of the band matrix.  Synchronises the stream once (pipeline status).
+int q2_apply(int64_t n, float* Z, float* ws, const Layout& L, hipStream_t stream);
 
 }  // namespace band
 }  // namespace mpq

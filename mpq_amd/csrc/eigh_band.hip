@@ -1154,14 +1154,14 @@ __global__ __launch_bounds__(kThr) void tridiag_out_kernel(const float* __restri
 // ---- back-transformation of stage 2 ----------------------------------------------------------
 
 constexpr int kPtChunks = 3 * 512;  // uint4 per block: 3 bf16 planes x (2 row tiles x 4 k-steps x 64 lanes)
-constexpr int kZs = 9;              // uint4 per LDS window row: 64 bf16 + 16 bytes of padding
 
 // Block (g, k): P = (H_31 ... H_0)^T over the window rows 32 g + 1 + 32 k .. + 63, H_i the reflector
 // of sweep 32 g + i at step k (acting on window rows i .. i + 31; identity where it does not
 // exist).  One work-group per block; thread (c = t % 64, q = t / 64) owns column c, rows q (mod 4)
 // of M = H_31 ... H_0, then P = M^T leaves as three bf16 planes (P = P0 + P1 + P2 to 2^-24) in the
-// left-operand order of v_mfma_f32_32x32x16_bf16: chunk (plane, tile, step, lane) holds the 8
-// entries P[32 tile + lane % 32][16 step + 8 (lane / 32) + 0 .. 7].
+// left-operand order of v_mfma_f32_32x32x16_bf16 with the k index permuted: chunk (plane, tile,
+// step, lane) holds the 8 entries P[32 tile + lane % 32][16 step + 8 (j / 4) + 4 (lane / 32) + j % 4],
+// j = 0 .. 7 (the window row that k slot j of the lane stands for in q2_apply_kernel).
 __global__ __launch_bounds__(kThr) void q2_build_kernel(const float* __restrict__ V2, const float* __restrict__ tau2,
                                                         int64_t n, uint4* __restrict__ Pt) {
   __shared__ float M[64][65];
@@ -1202,10 +1202,13 @@ __global__ __launch_bounds__(kThr) void q2_build_kernel(const float* __restrict_
   uint4* out = Pt + bid * kPtChunks;
   for (int ci = t; ci < 512; ci += kThr) {
     const int l = ci & 63, ts = ci >> 6;
-    const int cc = 32 * (ts >> 2) + (l & 31), k0 = 16 * (ts & 3) + 8 * (l >> 5);
+    const int cc = 32 * (ts >> 2) + (l & 31), k0 = 16 * (ts & 3) + 4 * (l >> 5);
     uint32_t h[4], m[4], lo[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) split3(M[k0 + 2 * j][cc], M[k0 + 2 * j + 1][cc], h[j], m[j], lo[j]);
+    for (int j = 0; j < 4; ++j) {
+      const int kk = k0 + 2 * (j & 1) + 8 * (j >> 1);  // slots 2 j, 2 j + 1
+      split3(M[kk][cc], M[kk + 1][cc], h[j], m[j], lo[j]);
+    }
     out[ci] = make_uint4(h[0], h[1], h[2], h[3]);
     out[512 + ci] = make_uint4(m[0], m[1], m[2], m[3]);
     out[1024 + ci] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
@@ -1213,213 +1216,322 @@ __global__ __launch_bounds__(kThr) void q2_build_kernel(const float* __restrict_
 }
 
 
-// Zt (n x n, row-major, column k = eigenvector k of the tridiagonal matrix) <- Q2 Zt: groups last
-// to first, steps in increasing order, each block Zt[lo .. lo + 63][:] <- P(g, k) Zt[lo .. lo + 63][:].
-// One work-group per 64 columns.  Consecutive steps overlap by 32 rows: the lower half of a block's
-// result stays in LDS as the upper half of the next block's window.  Four groups run at once, one
-// per pair of waves: group gl - q (quarter q) runs kQ2Lag steps behind group gl - q + 1, so block
-// k of group g - 1 reads only rows the blocks <= k - 2 of group g have finished, and its prefetch
-// two blocks ahead reads the rows of block k - 1 of group g.  Each quarter keeps its window in LDS
-// as three bf16 planes (row-contiguous per column: the right-operand order of
-// v_mfma_f32_32x32x16_bf16); the planes of P come from global memory straight into registers, one
-// block ahead.  A wave owns 32 output rows x 64 columns (two 32 x 32 tiles, K = 64): six plane
-// products per tile and 16-k step (every pair with plane indices summing to <= 2).
-constexpr int kQ2Lag = 3;
+// Zq ((n + kQ2Pad) x ldq, row-major, zero outside the n x n matrix; column j = eigenvector j of
+// the tridiagonal matrix) <- Q2 Zq: groups last to first, blocks in increasing order, each block
+// Zq[lo .. lo + 63][:] <- P(g, k) Zq[lo .. lo + 63][:].  One work-group per 64 columns and one wave
+// per group: four groups at once, group gl - q on wave q.  Block k of group g reads rows that
+// block k - 1 of group g + 1 (wave q - 1) finishes, and its prefetch two blocks ahead the rows of
+// block k + 1 of group g + 1: each wave publishes its last finished block in LDS and waits for
+// its predecessor's before loading rows.  A wave keeps the whole 64 x 64 block result in
+// registers (four 32 x 32 tiles; K = 64 as four 16-k steps; six bf16 plane products each): the
+// finished upper half goes to memory, while the lower half, split into bf16 planes in registers,
+// is the next block's upper window as it stands, because P's columns are packed in the order that
+// lines each result register up with the right-operand slot holding the same row: k slot (s, h, j)
+// of lane l (h = l / 32) is window row 16 s + 8 (j / 4) + 4 h + j % 4.  The window's new rows load
+// from memory straight into that order.  No data passes through LDS and waves do not wait on one
+// another except for rows.
+constexpr int kQ2Pad = 128;  // zero rows below the matrix (prefetches past a group's end read them)
+static_assert((kMaxN + kQ2Pad) * ((kMaxN + 63) / 64 * 64) * 4 < ((int64_t)1 << 31), "Zq byte offsets are int32");
 
-struct Q2Frag {
-  uint4 a[12];  // [plane * 4 + k-step]
+struct Q2Ops {
+  uint4 a01[1][2][2][3];  // P planes, k steps 0, 1 [-][row tile][k step][plane]
+  uint4 a23[2][2][3];     // P planes, k steps 2, 3 [row tile][k step - 2][plane]
+  uint4 b[2][4][3];    // window planes [column tile][k step][plane]
+  floatx16 acc[2][2];  // block result [row tile][column tile]
+  float raw[2][2][8];  // window rows (32 + 16 s' .. of a later block) [column tile][s'][slot]
 };
 
-__device__ __forceinline__ void q2_load_frag(Q2Frag& f, const uint4* __restrict__ Pt, int64_t bidx, int tc,
-                                             int lane) {
-  const uint4* src = Pt + bidx * kPtChunks + tc * 256 + lane;
-#pragma unroll
-  for (int p = 0; p < 3; ++p)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) f.a[p * 4 + s] = src[p * 512 + s * 64];
-}
-
-// rows row0 .. row0 + 7 of column col, each row index clamped to n - 1 (always a valid address;
-// q2_put_rows zeroes what lies outside the matrix).  row0 is wave-uniform: the row pointers are
-// scalar.  No branch and no use of the values here, so the loads stay in flight.
-__device__ __forceinline__ void q2_load_rows(float (&z)[8], const float* __restrict__ Zt, int row0, int col, int n) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) z[j] = (Zt + (int64_t)min(row0 + j, n - 1) * n)[col];
-}
-
-// the three planes of 8 consecutive window rows of column r at chunk (rows 8 chunk .. 8 chunk + 7);
-// row j counts as zero unless cok and row0 + j < n
-__device__ __forceinline__ void q2_put_rows(uint4* __restrict__ Zp, int r, int chunk, const float (&zin)[8], int row0,
-                                            int n, bool cok) {
-  float z[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) z[j] = (cok && row0 + j < n) ? zin[j] : 0.f;
-  uint4 h, m, l;
-  split3(z[0], z[1], h.x, m.x, l.x);
-  split3(z[2], z[3], h.y, m.y, l.y);
-  split3(z[4], z[5], h.z, m.z, l.z);
-  split3(z[6], z[7], h.w, m.w, l.w);
-  Zp[r * kZs + chunk] = h;
-  Zp[(64 + r) * kZs + chunk] = m;
-  Zp[(128 + r) * kZs + chunk] = l;
-}
-
-struct Q2Ctx {
+// Zq and Pt go through buffer instructions: a lane's byte offset in a VGPR (fixed for the
+// kernel), the row's or chunk's byte offset in an SGPR, no 64-bit address arithmetic per access
+struct Q2Wave {
   const uint4* Pt;
-  float* Zt;
-  uint4* Zp;
-  int n, z0, lane, wq, tc, lcol, lcl;  // lcl: lcol clamped to n - 1
-  bool colfull, cok;                   // cok: lcol < n
+  __amdgpu_buffer_rsrc_t rz;  // Zq
+  int vz[2];                  // lane byte offset, column tile ct: row 4 (lane / 32), column z0 + 32 ct + lane % 32
+  int ldq4;                   // bytes per row of Zq
+  int roff[16];               // byte offset of row 8 (i / 4) + i % 4 (k slots 8 s + j, result registers v)
+  int lane;
+  int* prog;                  // LDS: last finished block of each wave in this pass
+  int* status;                // global: a wait ran past its bound
+  int q;
+  bool failed;
 };
 
-// one step of one quarter: block k = T - S of its group (lo = first window row, base = the group's
-// first block); cur holds block k's planes, the next block's go to nxt; zA holds block k + 1's new
-// rows, block k + 2's go to zB
-__device__ __forceinline__ void q2_step(const Q2Ctx& c, int k, int nk, int lo, int64_t base, Q2Frag& cur,
-                                        Q2Frag& nxt, float (&zA)[2][8], float (&zB)[2][8]) {
-  const bool active = k >= 0 && k < nk;
-  const bool more = k + 1 < nk;
-  if (active && k == 0) {
-    // first block of the group: window into LDS, matrix and block 1's new rows into registers
+// k steps S0, S0 + 1 of block bid's P planes (k steps 0, 1 into set SET)
+template <int SET, int S0>
+__device__ __forceinline__ void q2w_load_a(Q2Ops& o, const Q2Wave& w, int64_t bid) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint4*>(w.Pt + bid * kPtChunks), (short)0, kPtChunks * 16, 0x00020000);
+  const int vo = w.lane * 16;
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      float z[8];
-      const int chunk = 4 * c.wq + h;
-      q2_load_rows(z, c.Zt, lo + 8 * chunk, c.lcl, c.n);
-      q2_put_rows(c.Zp, c.lane, chunk, z, lo + 8 * chunk, c.n, c.cok);
-    }
-    q2_load_frag(cur, c.Pt, base, c.tc, c.lane);
-    q2_load_rows(zA[0], c.Zt, lo + 64 + 16 * c.wq, c.lcl, c.n);
-    q2_load_rows(zA[1], c.Zt, lo + 72 + 16 * c.wq, c.lcl, c.n);
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int s = S0; s < S0 + 2; ++s)
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      r, vo, (p * 512 + (rt * 4 + s) * 64) * 16, 0));
+        if (S0 == 0) o.a01[SET][rt][s][p] = v;
+        else o.a23[rt][s - 2][p] = v;
+      }
+}
+
+// window rows row0 + 16 s' + 8 (j / 4) + j % 4 + 4 h (the slots of two k steps)
+__device__ __forceinline__ void q2w_load_rows(Q2Ops& o, const Q2Wave& w, int row0) {
+  const int rb = row0 * w.ldq4;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int so = rb + w.roff[i];
+    o.raw[0][i >> 3][i & 7] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(w.rz, w.vz[0], so, 0));
+    o.raw[1][i >> 3][i & 7] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(w.rz, w.vz[1], so, 0));
   }
-  __syncthreads();
-  floatx16 acc0, acc1;
-  if (active) {
-    // unconditional loads (last block: its own matrix again; rows clamped), so that nothing
-    // between them and the matrix cores waits for them
-    q2_load_frag(nxt, c.Pt, base + min(k + 1, nk - 1), c.tc, c.lane);
-    // new rows of block k + 2: lo_{k+2} + 32 .. + 63 with lo_j = lo + 32 j
-    q2_load_rows(zB[0], c.Zt, lo + 96 + 16 * c.wq, c.lcl, c.n);
-    q2_load_rows(zB[1], c.Zt, lo + 104 + 16 * c.wq, c.lcl, c.n);
+}
+
+__device__ __forceinline__ void q2w_split8(const float* x, uint4& h, uint4& m, uint4& l) {
+  split3(x[0], x[1], h.x, m.x, l.x);
+  split3(x[2], x[3], h.y, m.y, l.y);
+  split3(x[4], x[5], h.z, m.z, l.z);
+  split3(x[6], x[7], h.w, m.w, l.w);
+}
+
+// k steps SB, SB + 1 of the window from the loaded rows
+template <int SB>
+__device__ __forceinline__ void q2w_split_rows(Q2Ops& o) {
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) q2w_split8(o.raw[ct][s], o.b[ct][SB + s][0], o.b[ct][SB + s][1], o.b[ct][SB + s][2]);
+}
+
+// k steps 0, 1 of the next window from the lower result tile: result register 8 s + j of the lane
+// is window row 16 s + 8 (j / 4) + 4 h + j % 4 of the next block
+__device__ __forceinline__ void q2w_split_lower(Q2Ops& o) {
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = o.acc[1][ct][8 * s + j];
+      q2w_split8(x, o.b[ct][s][0], o.b[ct][s][1], o.b[ct][s][2]);
+    }
+}
+
+// row tile RT, k step S: six plane products into both column tiles (FRESH: the first k step)
+template <int SET, int RT, int S, bool FRESH>
+__device__ __forceinline__ void q2w_mfma(Q2Ops& o) {
+  const uint4* pa = S < 2 ? o.a01[SET][RT][S] : o.a23[RT][S - 2];
+  const bf16x8 a0 = __builtin_bit_cast(bf16x8, pa[0]);
+  const bf16x8 a1 = __builtin_bit_cast(bf16x8, pa[1]);
+  const bf16x8 a2 = __builtin_bit_cast(bf16x8, pa[2]);
+  const bf16x8 b0 = __builtin_bit_cast(bf16x8, o.b[0][S][0]);
+  const bf16x8 b1 = __builtin_bit_cast(bf16x8, o.b[0][S][1]);
+  const bf16x8 b2 = __builtin_bit_cast(bf16x8, o.b[0][S][2]);
+  const bf16x8 d0 = __builtin_bit_cast(bf16x8, o.b[1][S][0]);
+  const bf16x8 d1 = __builtin_bit_cast(bf16x8, o.b[1][S][1]);
+  const bf16x8 d2 = __builtin_bit_cast(bf16x8, o.b[1][S][2]);
+  floatx16 c0, c1;
+  if (FRESH) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      acc0[v] = 0.f;
-      acc1[v] = 0.f;
+      c0[v] = 0.f;
+      c1[v] = 0.f;
     }
-    const uint4* Zr = c.Zp + (c.lane & 31) * kZs + (c.lane >> 5);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const bf16x8 a0 = __builtin_bit_cast(bf16x8, cur.a[s]);
-      const bf16x8 a1 = __builtin_bit_cast(bf16x8, cur.a[4 + s]);
-      const bf16x8 a2 = __builtin_bit_cast(bf16x8, cur.a[8 + s]);
-      const bf16x8 b0 = __builtin_bit_cast(bf16x8, Zr[2 * s]);
-      const bf16x8 b1 = __builtin_bit_cast(bf16x8, Zr[64 * kZs + 2 * s]);
-      const bf16x8 b2 = __builtin_bit_cast(bf16x8, Zr[128 * kZs + 2 * s]);
-      const bf16x8 d0 = __builtin_bit_cast(bf16x8, Zr[32 * kZs + 2 * s]);
-      const bf16x8 d1 = __builtin_bit_cast(bf16x8, Zr[96 * kZs + 2 * s]);
-      const bf16x8 d2 = __builtin_bit_cast(bf16x8, Zr[160 * kZs + 2 * s]);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, d0, acc1, 0, 0, 0);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, d1, acc1, 0, 0, 0);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, d0, acc1, 0, 0, 0);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b2, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, d2, acc1, 0, 0, 0);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, d1, acc1, 0, 0, 0);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b0, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, d0, acc1, 0, 0, 0);
-      // one k-step of window operands in registers at a time
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  } else {
+    c0 = o.acc[RT][0];
+    c1 = o.acc[RT][1];
   }
-  __syncthreads();
-  if (active) {
-    // upper output half (tc == 0) is final for this group; the lower half becomes the next
-    // block's upper half (or is final too after the group's last block)
-    if (c.tc == 0 || !more) {
-      const int row0 = lo + 32 * c.tc + 4 * (c.lane >> 5);
-      const int col = c.z0 + (c.lane & 31);
-      if (c.colfull && lo + 64 <= c.n) {
-        const int rw = lo + 32 * c.tc;  // wave-uniform: scalar row pointers
-        const int lo4 = 4 * (c.lane >> 5) * c.n + (c.lane & 31) + c.z0;
+  c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, c0, 0, 0, 0);
+  c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, d0, c1, 0, 0, 0);
+  c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, c0, 0, 0, 0);
+  c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, d1, c1, 0, 0, 0);
+  c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, c0, 0, 0, 0);
+  c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, d0, c1, 0, 0, 0);
+  c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b2, c0, 0, 0, 0);
+  c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, d2, c1, 0, 0, 0);
+  c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, c0, 0, 0, 0);
+  c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, d1, c1, 0, 0, 0);
+  c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b0, c0, 0, 0, 0);
+  c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, d0, c1, 0, 0, 0);
+  o.acc[RT][0] = c0;
+  o.acc[RT][1] = c1;
+}
+
+// result tile (both column tiles) -> rows row0 .. row0 + 31: register v is row 8 (v / 4) + 4 h + v % 4
+__device__ __forceinline__ void q2w_store(const floatx16 (&c)[2], const Q2Wave& w, int row0) {
+  const int rb = row0 * w.ldq4;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          float* dst = c.Zt + (int64_t)(rw + 8 * (v >> 2) + (v & 3)) * c.n;
-          dst[lo4] = acc0[v];
-          dst[lo4 + 32] = acc1[v];
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = row0 + 8 * (v >> 2) + (v & 3);
-          if (row < c.n) {
-            if (col < c.n) c.Zt[row * c.n + col] = acc0[v];
-            if (col + 32 < c.n) c.Zt[row * c.n + col + 32] = acc1[v];
-          }
-        }
-      }
-    } else {
-      uint2* Zq = reinterpret_cast<uint2*>(c.Zp) + (c.lane & 31) * (2 * kZs) + (c.lane >> 5);
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        // rows 8 a + 4 (lane / 32) .. + 3 of the next window, columns lane % 32 and + 32
-        uint2 h, m, l;
-        split3(acc0[4 * a], acc0[4 * a + 1], h.x, m.x, l.x);
-        split3(acc0[4 * a + 2], acc0[4 * a + 3], h.y, m.y, l.y);
-        Zq[2 * a] = h;
-        Zq[64 * 2 * kZs + 2 * a] = m;
-        Zq[128 * 2 * kZs + 2 * a] = l;
-        split3(acc1[4 * a], acc1[4 * a + 1], h.x, m.x, l.x);
-        split3(acc1[4 * a + 2], acc1[4 * a + 3], h.y, m.y, l.y);
-        Zq[32 * 2 * kZs + 2 * a] = h;
-        Zq[96 * 2 * kZs + 2 * a] = m;
-        Zq[160 * 2 * kZs + 2 * a] = l;
-      }
-    }
-    if (more) {
-      q2_put_rows(c.Zp, c.lane, 4 + 2 * c.wq, zA[0], lo + 64 + 16 * c.wq, c.n, c.cok);
-      q2_put_rows(c.Zp, c.lane, 5 + 2 * c.wq, zA[1], lo + 72 + 16 * c.wq, c.n, c.cok);
-    }
+  for (int v = 0; v < 16; ++v) {
+    const int so = rb + w.roff[v];
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(c[0][v]), w.rz, w.vz[0], so, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(c[1][v]), w.rz, w.vz[1], so, 0);
   }
 }
 
-__global__ __launch_bounds__(512) void q2_apply_kernel(const uint4* __restrict__ Pt, float* __restrict__ Zt,
-                                                       int64_t n64) {
-  __shared__ uint4 sZ[4][3 * 64 * kZs];
-  const int t = threadIdx.x, lane = t & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: row indices stay scalar
-  const int qt = wave >> 1;  // quarter: group slot of this pair of waves
-  Q2Ctx c;
-  c.Pt = Pt;
-  c.Zt = Zt;
-  c.Zp = sZ[qt];
-  c.n = (int)n64;
-  c.z0 = (int)blockIdx.x * 64;
-  c.lane = lane;
-  c.wq = wave & 1;
-  // output row tile; swapped in quarters 2 and 3 so each SIMD holds one wave of each kind
-  c.tc = (wave & 1) ^ (qt >> 1);
-  c.lcol = c.z0 + lane;
-  c.lcl = min(c.lcol, c.n - 1);
-  c.cok = c.lcol < c.n;
-  c.colfull = c.z0 + 64 <= c.n;
-  const int K0 = (c.n - 2) / kBW;
-  Q2Frag fa, fb;
-  float za[2][8], zb[2][8];
-  for (int gl = K0; gl >= 0; gl -= 4) {
-    const int g = gl - qt;  // this quarter's group (< 0: idle)
-    const int nk = g >= 0 ? K0 + 1 - g : 0;
-    const int steps = K0 + 1 - gl + (kQ2Lag + 1) * min(3, gl);
-    const int S = kQ2Lag * qt;
-    const int64_t base = g >= 0 ? boff(g, K0) : 0;
-    const int lo0 = g * kBW + 1;
-    for (int T = 0; T < steps; T += 2) {
-      q2_step(c, T - S, nk, lo0 + kBW * (T - S), base, fa, fb, za, zb);
-      if (T + 1 < steps) q2_step(c, T + 1 - S, nk, lo0 + kBW * (T + 1 - S), base, fb, fa, zb, za);
+// wave q waits until wave q - 1 has finished its block `target` of this pass
+__device__ __forceinline__ void q2w_wait(Q2Wave& w, int target) {
+  if (w.q == 0 || w.failed) return;
+  for (int it = 0;; ++it) {
+    if (__hip_atomic_load(&w.prog[w.q - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+    if (it > (1 << 22)) {
+      __hip_atomic_store(w.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      w.failed = true;
+      break;
     }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// every lane stores the same value: no branch, so a block's work stays one scheduling region
+__device__ __forceinline__ void q2w_publish(const Q2Wave& w, int k) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __hip_atomic_store(&w.prog[w.q], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// instruction classes of __builtin_amdgcn_sched_group_barrier
+constexpr int kSgMfma = 0x008, kSgValu = 0x002, kSgVmemRd = 0x020;
+
+// block k of the wave's group (window rows lo0 + 32 k ..), k-step 0, 1 planes in set SET = k % 2.
+// On entry: block k's P planes and block k + 1's for k steps 0, 1 (loaded or in flight), the
+// window's k steps 2, 3, the rows of block k + 1's k steps 2, 3 in raw, and (k > 0) block k - 1's
+// result, whose lower tile becomes this window's k steps 0, 1.  Block k + 1's k-step 2, 3 planes
+// and block k + 2's k-step 0, 1 planes replace block k's as they are used.
+template <bool FIRST, int SET>
+__device__ __forceinline__ void q2w_block(Q2Ops& o, Q2Wave& w, int k, int nk, int lo0, int64_t base) {
+  const int lo = lo0 + kBW * k;
+  // One wave per SIMD issues in order, so the matrix cores stay busy only if the splits and the
+  // loads sit between the products in the instruction stream: k steps 2, 3 of the upper tile
+  // with the lower tile's split, k steps 2, 3 of the lower tile with block k + 1's k-step 2, 3
+  // loads, k step 0 with the new rows' split (one scheduling region each).
+  if (!FIRST) {
+    q2w_store(o.acc[0], w, lo - kBW);  // block k - 1's upper tile is final
+    q2w_publish(w, k - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    q2w_mfma<SET, 0, 2, true>(o);
+    q2w_split_lower(o);
+    q2w_mfma<SET, 0, 3, false>(o);
+#pragma unroll
+    for (int i = 0; i < 24; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSgValu, 10, 0);
+    }
+  } else {
+    q2w_mfma<SET, 0, 2, true>(o);
+    q2w_mfma<SET, 0, 3, false>(o);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  q2w_mfma<SET, 1, 2, true>(o);
+  q2w_mfma<SET, 1, 3, false>(o);
+  q2w_load_a<SET, 2>(o, w, base + min(k + 1, nk - 1));
+#pragma unroll
+  for (int i = 0; i < 12; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(kSgVmemRd, 1, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  q2w_mfma<SET, 0, 0, false>(o);
+  q2w_mfma<SET, 1, 0, false>(o);
+  q2w_split_rows<2>(o);  // block k + 1's k steps 2, 3
+#pragma unroll
+  for (int i = 0; i < 24; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSgValu, 8, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // rows of block k + 2's k steps 2, 3 (block k + 1 of wave q - 1; clamped past the group's end)
+  q2w_wait(w, min(k + 2, nk - 2));
+  q2w_load_rows(o, w, lo0 + kBW * min(k + 2, nk - 1) + 32);
+  q2w_mfma<SET, 0, 1, false>(o);
+  q2w_mfma<SET, 1, 1, false>(o);
+  q2w_load_a<0, 0>(o, w, base + min(k + 1, nk - 1));
+#pragma unroll
+  for (int i = 0; i < 22; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSgVmemRd, 2, 0);
+  }
+}
+
+__global__ __launch_bounds__(256) void q2_apply_kernel(const uint4* __restrict__ Pt, float* __restrict__ Zq,
+                                                       int64_t n64, int64_t ldq, int* __restrict__ status) {
+  __shared__ int sprog[4];
+  const int t = threadIdx.x, lane = t & 63;
+  const int q = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int n = (int)n64;
+  const int z0 = (int)blockIdx.x * 64;
+  Q2Wave w;
+  w.Pt = Pt;
+  // every byte offset fits in 32 bits: (n + kQ2Pad) ldq 4 < 2^31 for n <= kMaxN
+  w.rz = __builtin_amdgcn_make_buffer_rsrc(Zq, (short)0, (int)((n64 + kQ2Pad) * ldq * 4), 0x00020000);
+  w.ldq4 = (int)ldq * 4;
+  w.vz[0] = (4 * (lane >> 5) * (int)ldq + z0 + (lane & 31)) * 4;
+  w.vz[1] = w.vz[0] + 32 * 4;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) w.roff[i] = (8 * (i >> 2) + (i & 3)) * w.ldq4;
+  w.lane = lane;
+  w.prog = sprog;
+  w.status = status;
+  w.q = q;
+  w.failed = false;
+  const int K0 = (n - 2) / kBW;
+  Q2Ops o;
+  for (int gl = K0; gl >= 0; gl -= 4) {
+    if (t < 4) sprog[t] = -1;
     __syncthreads();
+    const int g = gl - q;
+    if (g >= 0) {
+      const int nk = K0 + 1 - g;
+      const int64_t base = boff(g, K0);
+      const int lo0 = g * kBW + 1;
+      // block 0's window and block 1's new rows: rows wave q - 1 finishes by its block 1
+      q2w_wait(w, min(1, nk - 2));
+      q2w_load_rows(o, w, lo0);
+      q2w_split_rows<0>(o);
+      q2w_load_rows(o, w, lo0 + 32);
+      q2w_split_rows<2>(o);
+      q2w_load_a<0, 0>(o, w, base);
+      q2w_load_a<0, 2>(o, w, base);
+      q2w_load_rows(o, w, lo0 + 32 + kBW * min(1, nk - 1));
+      q2w_block<true, 0>(o, w, 0, nk, lo0, base);
+      for (int k = 1; k < nk; ++k) q2w_block<false, 0>(o, w, k, nk, lo0, base);
+      // the last block: both halves are final
+      const int lol = lo0 + kBW * (nk - 1);
+      q2w_store(o.acc[0], w, lol);
+      q2w_store(o.acc[1], w, lol + 32);
+      // the last blocks' prefetches are never used: wait for them here, once per pass
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    q2w_publish(w, 1 << 30);
+    __syncthreads();
+  }
+}
+
+// Z (n x n, row j = eigenvector j) -> Zq (row i = coordinate i, zero outside n x n) and back
+__global__ __launch_bounds__(256) void q2_gather_kernel(const float* __restrict__ Z, int64_t n, float* __restrict__ Zq,
+                                                        int64_t ldq) {
+  __shared__ float tile[32][33];
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;  // Zq tile
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t j = c0 + i, r = r0 + tx;  // Z[j][r]
+    tile[i][tx] = (j < n && r < n) ? Z[j * n + r] : 0.f;
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) Zq[(r0 + i) * ldq + c0 + tx] = tile[tx][i];
+}
+
+__global__ __launch_bounds__(256) void q2_scatter_kernel(const float* __restrict__ Zq, int64_t ldq, int64_t n,
+                                                         float* __restrict__ Z) {
+  __shared__ float tile[32][33];
+  const int64_t j0 = (int64_t)blockIdx.y * 32, r0 = (int64_t)blockIdx.x * 32;  // Z tile
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t r = r0 + i, j = j0 + tx;  // Zq[r][j]
+    tile[i][tx] = (r < n && j < n) ? Zq[r * ldq + j] : 0.f;
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t j = j0 + i, r = r0 + tx;
+    if (j < n && r < n) Z[j * n + r] = tile[tx][i];
   }
 }
 
@@ -1460,6 +1572,8 @@ Layout layout(int64_t n) {
   L.tau2 = take(nb * 32);
   L.Pt = take(nb * kPtChunks * 4);
   L.prog = take((n + kNW) / kNW + 64);  // int progress slots + status
+  L.ldq = (n + 63) / 64 * 64;
+  L.Zq = take((n + kQ2Pad) * L.ldq);
   L.total = o;
   return L;
 }
@@ -1583,14 +1697,32 @@ int sb2st(int64_t n, const float* A, int64_t lda, float* D, float* E, float* ws,
   return kOk;
 }
 
-int q2_apply(int64_t n, float* Zt, float* ws, const Layout& L, hipStream_t stream) {
+int q2_apply(int64_t n, float* Z, float* ws, const Layout& L, hipStream_t stream) {
   if (n < 3) return kOk;
   const int64_t nb = q2_blocks(n);
   uint4* Pt = reinterpret_cast<uint4*>(ws + L.Pt);
+  float* Zq = ws + L.Zq;
   hipLaunchKernelGGL(q2_build_kernel, dim3((unsigned)nb), dim3(kThr), 0, stream, ws + L.V2, ws + L.tau2, n, Pt);
   MPQ_LAUNCH_CHECK();
-  hipLaunchKernelGGL(q2_apply_kernel, dim3((unsigned)((n + 63) / 64)), dim3(512), 0, stream, Pt, Zt, n);
+  hipLaunchKernelGGL(q2_gather_kernel, dim3((unsigned)(L.ldq / 32), (unsigned)((n + kQ2Pad) / 32)), dim3(kThr), 0,
+                     stream, Z, n, Zq, L.ldq);
   MPQ_LAUNCH_CHECK();
+  int* status = reinterpret_cast<int*>(ws + L.prog) + (n - 1 + kNW - 1) / kNW + 1;
+  hipLaunchKernelGGL(fill_int_kernel, dim3(1), dim3(kThr), 0, stream, status, 1, 0);
+  MPQ_LAUNCH_CHECK();
+  hipLaunchKernelGGL(q2_apply_kernel, dim3((unsigned)(L.ldq / 64)), dim3(kThr), 0, stream, Pt, Zq, n, L.ldq, status);
+  MPQ_LAUNCH_CHECK();
+  hipLaunchKernelGGL(q2_scatter_kernel, dim3((unsigned)((n + 31) / 32), (unsigned)((n + 31) / 32)), dim3(kThr), 0,
+                     stream, Zq, L.ldq, n, Z);
+  MPQ_LAUNCH_CHECK();
+  int st = 0;
+  MPQ_HIP_TRY(hipMemcpyAsync(&st, status, sizeof(int), hipMemcpyDeviceToHost, stream));
+  MPQ_HIP_TRY(hipStreamSynchronize(stream));
+  if (st != 0) {
+    set_error("mpq_syevd: band back-transformation pipeline stalled (a wait exceeded its bound)");
+    set_error_code(kHipError);
+    return kHipError;
+  }
   return kOk;
 }
 
