@@ -15,7 +15,8 @@
 //     diagonal sign matrix S chosen during the elimination (|U_ii| >= 1, no pivoting), Y = L,
 //     T = -U S Y1^-T, R = S R_tsqr, so P = (I - Y T Y^T) [R; 0];
 //   * the trailing matrix takes A22 <- Q^T A22 Q as X = A22 (Y T), W = X - 1/2 Y (T^T Y^T X),
-//     A22 -= Y W^T + W Y^T (the library's fp32 MFMA GEMM; LAPACK sytrd's update).
+//     A22 -= Y W^T + W Y^T (LAPACK sytrd's update): X from one read of A22's lower triangle on
+//     the fp32 matrix cores, the rank-64 update as bf16 x6 products.
 // Stage 2 (band -> tridiagonal): bulge chasing (Schwarz 1968; Lang 1993; the task split of Haidar,
 //   Ltaief and Dongarra, SC 2011).  Sweep s annihilates column s below the subdiagonal with one
 //   reflector (task 0, two-sided on the 32 x 32 diagonal block below); task k >= 1 applies the
@@ -506,7 +507,7 @@ __global__ __launch_bounds__(kThr) void cq_pass_kernel(const float* __restrict__
 // results.  On the Cholesky QR path Q1 still lacks the last factor (Rc, fp64): every row is first
 // solved with it; after the tall-skinny fallback (flag 1) Q1 is final.  Every work-group factors
 // the kk x kk top block redundantly and then handles 256 panel rows: Y row = L row (top block) or
-// Q1 row U^-1, YT row = Y row T; the reflectors go to the rows of A (row c0 + j holds Y[r][j] at
+// Q1 row U^-1, B row = Y row T (packed into BP); the reflectors go to the rows of A (row c0 + j holds Y[r][j] at
 // column r0 + r, r > j).  Work-group 0 also writes T, tau and the band block
 // A[r0 + i][c0 + j] = (S R)[i][j] (j >= i, zero below).
 __device__ __forceinline__ void hr_q1_row(const float* __restrict__ q, const double (*sR)[33], const double* sRinv,
@@ -530,7 +531,7 @@ __device__ __forceinline__ void hr_q1_row(const float* __restrict__ q, const dou
 __global__ __launch_bounds__(kThr) void hr_kernel(const float* __restrict__ Q1, const double* __restrict__ Rc,
                                                   const int* __restrict__ fallback, const float* __restrict__ Rroot,
                                                   int64_t m, float* __restrict__ A, int64_t lda, int64_t r0,
-                                                  int64_t c0, float* __restrict__ Y, float* __restrict__ YT,
+                                                  int64_t c0, float* __restrict__ Y, float* __restrict__ BP,
                                                   float* __restrict__ Tout, float* __restrict__ tau) {
   __shared__ float LU[32][33];
   __shared__ float Xi[32][33];  // L1^-T
@@ -630,13 +631,19 @@ __global__ __launch_bounds__(kThr) void hr_kernel(const float* __restrict__ Q1, 
     }
 #pragma unroll
     for (int j = 0; j < 32; ++j) Y[r * 32 + j] = y[j];
+    // B = Y T, packed for xsym_kernel: BP[r / 32][lane (j, h = r / 16 % 2)][r % 16]
+    float* bp = BP + (r >> 5) * 1024 + 512 * ((r >> 4) & 1) + (r & 15);
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
       float acc = 0.f;
       for (int i = 0; i <= j; ++i) acc = fmaf(y[i], Ts[i][j], acc);
-      YT[r * 32 + j] = acc;
+      bp[16 * j] = acc;
     }
     for (int j = 0; j < kk && j < r; ++j) A[(c0 + j) * lda + r0 + r] = y[j];
+  } else {  // rows m .. of the last 256-row block: zero operand rows
+    float* bp = BP + (r >> 5) * 1024 + 512 * ((r >> 4) & 1) + (r & 15);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) bp[16 * j] = 0.f;
   }
   if (blockIdx.x == 0) {
     for (int e = t; e < 32 * 32; e += kThr) Tout[e] = Ts[e / 32][e & 31];
@@ -830,70 +837,194 @@ __global__ __launch_bounds__(kThr) void syr2k_x6_kernel(const uint4* __restrict_
     }
 }
 
-// Split-K partials of X = A22 B with B = Y T (m x 32), from the lower triangle of A22 only (the
-// trailing update keeps the lower triangle and the 32 x 32 diagonal blocks current):
-//   pass 0 (row strips):    P0[ks][r][:] = sum_{k in split ks, k < 32 (r / 32 + 1)} A22[r][k] B[k][:]
-//   pass 1 (column strips): P1[ks][r][:] = sum_{i in split ks, i >= 32 (r / 32 + 1)} A22[i][r] B[i][:]
-// X = the sum of all partials.  Wave w of a work-group owns output rows 128 bx + 32 w .. + 31 (one
-// 32 x 32 MFMA tile).  Pass 0: in each 64-k step lane (row, h) feeds k = kt + 32 h + j to MFMA j, so
-// it streams 32 consecutive floats of its row; pass 1: lane (c, h) feeds i = it + 32 h + j, and for
-// each j the 32 lanes of a half read one contiguous row segment A22[i][32 J .. 32 J + 31].
-constexpr int kXKC = 512;  // k per split
-template <int kPass>
-__global__ __launch_bounds__(kThr) void xprod_kernel(const float* __restrict__ A, int64_t lda,
-                                                     const float* __restrict__ B, int64_t m, int64_t kxkc,
-                                                     float* __restrict__ P) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row = lane & 31, h = lane >> 5;
-  const int64_t rbase = (int64_t)blockIdx.x * 128 + wave * 32;  // this wave's 32 output rows
-  const int64_t r = rbase + row;
-  const int64_t rc = r < m ? r : m - 1;
-  const int64_t lim = rbase + 32;  // pass 0: k < lim; pass 1: i >= lim
-  int64_t k0 = (int64_t)blockIdx.y * kxkc, k1 = min(m, k0 + kxkc);
-  if (kPass == 0) k1 = min(k1, lim);
-  else k0 = max(k0, lim);
-  floatx16 acc;
+// X = A22 B (B = Y T, m x 32) from the lower triangle of A22 (the trailing update keeps the lower
+// triangle and the 32 x 32 diagonal blocks current), reading that triangle once.  Work-group t owns
+// the lower tile (I, J), I >= J, of kTile = 64 R rows and columns and adds both of its products:
+//   rows of block I: A_IJ B_J      -> partial slot J of block I,
+//   rows of block J: A_IJ^T B_I    -> partial slot I of block J (I > J),
+// and a diagonal tile (I = J) puts the sum of both over its lower 32 x 32 blocks (the diagonal blocks
+// counted once, as stored) into slot I of block I.  Every (slot s, block K) is written by exactly one
+// work-group -- tile (K, s) for s <= K, tile (s, K) for s > K -- so X = the sum over the slots in
+// slot order, as xsum_kernel adds them.
+//
+// The four waves split the tile into 2 x 2 sub-blocks of 32 R rows.  A wave walks its sub-block in
+// 32 x 32 blocks: lane (r, h) loads A[r][16 h .. 16 h + 15] (four float4) and feeds the row product
+// with k = 16 h + s on MFMA step s; the same block, transposed through the wave's own LDS buffer,
+// feeds the column product (lane (c, h): A[16 h + s][c]).  Both B operands come packed by hr_kernel
+// (BP[32-row block][lane (j, h)][s] = B[32 blk + 16 h + s][j]).  The two waves that share a row half
+// or a column half of the tile add their partials through LDS at the end.
+constexpr int kXsLd = 36;  // row stride (floats) of a wave's 32 x 32 transpose buffer
+
+struct XsBlock {
+  float a[16];  // lane (r, h): A[r][16 h + s]
+  float4 bi[4], bj[4];
+};
+
+template <int R>
+__device__ __forceinline__ void xs_load(const float* __restrict__ A, int64_t lda, const float4* __restrict__ BP,
+                                        int64_t m, int64_t R0, int64_t C0, int lane, XsBlock& x) {
+  const int r = lane & 31, h = lane >> 5;
+  if (R0 >= m || C0 >= m) {  // outside the matrix (the last tile row or column only)
 #pragma unroll
-  for (int v = 0; v < 16; ++v) acc[v] = 0.f;
-  if (rbase < m) {
-    for (int64_t kt = k0; kt < k1; kt += 64) {
-      const int64_t kb = kt + 32 * h;
-      float av[32], bv[32];
-      if (kPass == 0 && kt + 64 <= k1 && (kb & 3) == 0) {
-        const float4* ap = reinterpret_cast<const float4*>(A + rc * lda + kb);
+    for (int s = 0; s < 16; ++s) x.a[s] = 0.f;
+  } else {
+    const int64_t row = min(R0 + r, m - 1);
+    const float4* p = reinterpret_cast<const float4*>(A + row * lda + C0 + 16 * h);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const float4 f = ap[q];
-          av[4 * q] = f.x;
-          av[4 * q + 1] = f.y;
-          av[4 * q + 2] = f.z;
-          av[4 * q + 3] = f.w;
-        }
+    for (int q = 0; q < 4; ++q) {
+      const float4 f = p[q];
+      x.a[4 * q] = f.x;
+      x.a[4 * q + 1] = f.y;
+      x.a[4 * q + 2] = f.z;
+      x.a[4 * q + 3] = f.w;
+    }
+    if (R0 + 32 > m || C0 + 32 > m) {  // crosses the edge: rows and columns >= m are zero
 #pragma unroll
-        for (int j = 0; j < 32; ++j) bv[j] = B[(kb + j) * 32 + row];
-      } else {
-#pragma unroll
-        for (int j = 0; j < 32; ++j) {
-          const int64_t kk = kb + j;
-          const bool in = kk < k1;
-          const int64_t kc = in ? kk : k0;
-          av[j] = in ? (kPass == 0 ? A[rc * lda + kc] : A[kc * lda + rc]) : 0.f;
-          bv[j] = in ? B[kc * 32 + row] : 0.f;
-        }
-      }
-      if (r >= m) {
-#pragma unroll
-        for (int j = 0; j < 32; ++j) av[j] = 0.f;
-      }
-#pragma unroll
-      for (int j = 0; j < 32; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[j], bv[j], acc, 0, 0, 0);
+      for (int s = 0; s < 16; ++s)
+        if (R0 + r >= m || C0 + 16 * h + s >= m) x.a[s] = 0.f;
     }
   }
-  float* Ps = P + ((int64_t)kPass * gridDim.y + blockIdx.y) * m * 32;
+  const float4* bi = BP + (R0 >> 5) * 256 + lane * 4;
+  const float4* bj = BP + (C0 >> 5) * 256 + lane * 4;
 #pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int64_t rr = rbase + 8 * (v >> 2) + 4 * h + (v & 3);
-    if (rr < m) Ps[rr * 32 + row] = acc[v];
+  for (int q = 0; q < 4; ++q) {
+    x.bi[q] = bi[q];
+    x.bj[q] = bj[q];
+  }
+}
+
+__device__ __forceinline__ float f4e(const float4* v, int s) {
+  const float4 f = v[s >> 2];
+  return (s & 3) == 0 ? f.x : (s & 3) == 1 ? f.y : (s & 3) == 2 ? f.z : f.w;
+}
+
+// One wave's sub-block: 32 x 32 blocks (a, b), b outer; DIAG: a sub-block on the tile's diagonal
+// (blocks above its diagonal skipped, diagonal blocks feed the row product only).
+template <int R, bool DIAG>
+__device__ __forceinline__ void xs_walk(const float* __restrict__ A, int64_t lda, const float4* __restrict__ BP,
+                                        int64_t m, int64_t rowbase, int64_t colbase, float* tb, int lane,
+                                        floatx16 (&c1)[R], floatx16 (&c2)[R]) {
+  const int r = lane & 31, h = lane >> 5;
+  XsBlock cur, nxt;
+  xs_load<R>(A, lda, BP, m, rowbase, colbase, lane, cur);  // block (0, 0)
+#pragma unroll
+  for (int b = 0; b < R; ++b)
+#pragma unroll
+    for (int a = DIAG ? b : 0; a < R; ++a) {
+      // the next block in walk order, loaded before this one's products
+      const int na = a + 1 < R ? a + 1 : (DIAG ? b + 1 : 0), nb = a + 1 < R ? b : b + 1;
+      if (nb < R) xs_load<R>(A, lda, BP, m, rowbase + 32 * na, colbase + 32 * nb, lane, nxt);
+      const bool dblk = DIAG && a == b;
+      float at[16];
+      if (!dblk) {
+        float4* w = reinterpret_cast<float4*>(tb + r * kXsLd + 16 * h);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) w[q] = make_float4(cur.a[4 * q], cur.a[4 * q + 1], cur.a[4 * q + 2], cur.a[4 * q + 3]);
+#pragma unroll
+        for (int s = 0; s < 16; ++s) at[s] = tb[(16 * h + s) * kXsLd + r];
+      }
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        c1[a] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[s], f4e(cur.bj, s), c1[a], 0, 0, 0);
+        if (!dblk) c2[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(at[s], f4e(cur.bi, s), c2[b], 0, 0, 0);
+      }
+      if (nb < R) cur = nxt;
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void xs_put(float* reg, const floatx16 (&c)[R], int lane) {
+#pragma unroll
+  for (int a = 0; a < R; ++a)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) reg[(a * 16 + v) * 64 + lane] = c[a][v];
+}
+
+// out[slot][rows base .. base + 32 R) = c (+ the partial in reg)
+template <int R>
+__device__ __forceinline__ void xs_store(float* __restrict__ P, int64_t m, int64_t slot, int64_t base,
+                                         const floatx16 (&c)[R], const float* reg, int lane) {
+  const int j = lane & 31, h = lane >> 5;
+  float* out = P + slot * m * 32;
+#pragma unroll
+  for (int a = 0; a < R; ++a)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t row = base + 32 * a + 8 * (v >> 2) + 4 * h + (v & 3);
+      if (row < m) out[row * 32 + j] = c[a][v] + reg[(a * 16 + v) * 64 + lane];
+    }
+}
+
+template <int R>
+__global__ __launch_bounds__(kThr, 2) void xsym_kernel(const float* __restrict__ A, int64_t lda,
+                                                       const float4* __restrict__ BP, int64_t m,
+                                                       float* __restrict__ P) {
+  constexpr int SB = 32 * R, kTile = 2 * SB, kReg = R * 16 * 64;
+  __shared__ float lds[4 * kReg];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int t = (int)blockIdx.x;
+  int I = (int)((sqrtf(8.f * (float)t + 1.f) - 1.f) * 0.5f);
+  while ((I + 1) * (I + 2) / 2 <= t) ++I;
+  while (I * (I + 1) / 2 > t) --I;
+  const int J = t - I * (I + 1) / 2;
+  const bool diag = I == J;
+  const int64_t rowbase = (int64_t)I * kTile + SB * wr, colbase = (int64_t)J * kTile + SB * wc;
+  floatx16 c1[R], c2[R];
+#pragma unroll
+  for (int a = 0; a < R; ++a)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      c1[a][v] = 0.f;
+      c2[a][v] = 0.f;
+    }
+  float* tb = lds + wave * kReg;
+  if (!diag)
+    xs_walk<R, false>(A, lda, BP, m, rowbase, colbase, tb, lane, c1, c2);
+  else if (wr == wc)
+    xs_walk<R, true>(A, lda, BP, m, rowbase, colbase, tb, lane, c1, c2);
+  else if (wr > wc)
+    xs_walk<R, false>(A, lda, BP, m, rowbase, colbase, tb, lane, c1, c2);
+  __syncthreads();
+  float* L0 = lds;
+  float* L1 = lds + kReg;
+  float* L2 = lds + 2 * kReg;
+  float* L3 = lds + 3 * kReg;
+  if (!diag) {
+    // row half wr: (wr, 0) + (wr, 1); column half wc: (0, wc) + (1, wc)
+    if (wave == 1) {
+      xs_put<R>(L0, c1, lane);
+      xs_put<R>(L3, c2, lane);
+    } else if (wave == 3) {
+      xs_put<R>(L1, c1, lane);
+    } else if (wave == 0) {
+      xs_put<R>(L2, c2, lane);
+    }
+    __syncthreads();
+    const int64_t bI = (int64_t)I * kTile, bJ = (int64_t)J * kTile;
+    if (wave == 0) {
+      xs_store<R>(P, m, J, bI, c1, L0, lane);
+    } else if (wave == 2) {
+      xs_store<R>(P, m, J, bI + SB, c1, L1, lane);
+      xs_store<R>(P, m, I, bJ, c2, L2, lane);
+    } else if (wave == 3) {
+      xs_store<R>(P, m, I, bJ + SB, c2, L3, lane);
+    }
+  } else {
+    // rows 0 .. SB: (0, 0)'s both products + (1, 0)'s column product; rows SB ..: (1, 0)'s row
+    // product + (1, 1)'s both products
+    if (wave == 2) {
+      xs_put<R>(L2, c2, lane);
+      xs_put<R>(L1, c1, lane);
+    }
+    __syncthreads();
+    const int64_t bI = (int64_t)I * kTile;
+    if (wave == 0 || wave == 3) {
+      floatx16 s[R];
+#pragma unroll
+      for (int a = 0; a < R; ++a) s[a] = c1[a] + c2[a];
+      xs_store<R>(P, m, I, bI + (wave == 3 ? SB : 0), s, wave == 3 ? L1 : L2, lane);
+    }
   }
 }
 
@@ -1553,14 +1684,14 @@ Layout layout(int64_t n) {
   L.Rroot = take(32 * 32);
   L.Q1 = take(n * 32);
   L.Y = take(n * 32);
-  L.YT = take(n * 32);
+  L.BP = take((n + 255) / 256 * 256 * 32);  // B = Y T packed for xsym_kernel, zero rows to 256
   L.X = take(n * 32);
   L.T = take(32 * 32);
   L.Gp = take(64 * 1024);
   L.Xop = take((n + 127) / 128 * 4 * kUpdTile * 4);  // packed update operands (uint4 = 4 floats)
   L.Yop = take((n + 127) / 128 * 4 * kUpdTile * 4);
   L.M = take(32 * 32);
-  L.px_floats = 2 * ((n + kXKC - 1) / kXKC) * n * 32;  // split-K partials of X = A22 (Y T), two passes
+  L.px_floats = (n + 255) / 256 * n * 32;  // partial slots of X = A22 (Y T): one per tile row
   L.Px = take(L.px_floats);
   L.Gd = take(2 * 64 * 1024);   // fp64 Gram partials
   L.Rc = take(2 * 1024);        // fp64 R of the current pass
@@ -1621,20 +1752,28 @@ int sy2sb(int64_t n, float* A, int64_t lda, float* tau, float* ws, const Layout&
     MPQ_LAUNCH_CHECK();
     const unsigned rblocks = (unsigned)((m + kThr - 1) / kThr);
     hipLaunchKernelGGL(hr_kernel, dim3(rblocks), dim3(kThr), 0, stream, ws + L.Q1, Rc, fb, ws + L.Rroot, m, A, lda,
-                       r0, c0, ws + L.Y, ws + L.YT, ws + L.T, tau);
+                       r0, c0, ws + L.Y, ws + L.BP, ws + L.T, tau);
     MPQ_LAUNCH_CHECK();
     float* A22 = A + r0 * lda + r0;
-    // X = A22 (Y T): split-K partials, summed in split order; then Y^T X and M = T^T Y^T X
-    const int64_t mtiles = (m + 127) / 128;
-    const int64_t xsplits = (m + kXKC - 1) / kXKC;
-    hipLaunchKernelGGL(xprod_kernel<0>, dim3((unsigned)mtiles, (unsigned)xsplits), dim3(kThr), 0, stream, A22, lda,
-                       ws + L.YT, m, (int64_t)kXKC, ws + L.Px);
-    MPQ_LAUNCH_CHECK();
-    hipLaunchKernelGGL(xprod_kernel<1>, dim3((unsigned)mtiles, (unsigned)xsplits), dim3(kThr), 0, stream, A22, lda,
-                       ws + L.YT, m, (int64_t)kXKC, ws + L.Px);
+    // X = A22 (Y T): one partial slot per tile of the lower triangle's tile row / column, summed in
+    // slot order; 128-wide tiles while they keep the slots within the buffer (m <= n / 2)
+    const bool small = 2 * m <= n;
+    const int64_t tile = small ? 128 : 256;
+    const int64_t nbt = (m + tile - 1) / tile;
+    if (nbt * m * 32 > L.px_floats) {
+      set_error("sy2sb: %lld partial slots of %lld rows exceed the workspace", (long long)nbt, (long long)m);
+      return kUnsupported;
+    }
+    const unsigned ntiles = (unsigned)(nbt * (nbt + 1) / 2);
+    if (small)
+      hipLaunchKernelGGL(xsym_kernel<2>, dim3(ntiles), dim3(kThr), 0, stream, A22, lda,
+                         reinterpret_cast<const float4*>(ws + L.BP), m, ws + L.Px);
+    else
+      hipLaunchKernelGGL(xsym_kernel<4>, dim3(ntiles), dim3(kThr), 0, stream, A22, lda,
+                         reinterpret_cast<const float4*>(ws + L.BP), m, ws + L.Px);
     MPQ_LAUNCH_CHECK();
     hipLaunchKernelGGL(xsum_kernel, dim3((unsigned)((m * 32 + kThr - 1) / kThr)), dim3(kThr), 0, stream, ws + L.Px,
-                       (int)(2 * xsplits), m * 32, ws + L.X);
+                       (int)nbt, m * 32, ws + L.X);
     MPQ_LAUNCH_CHECK();
     const int64_t ng = std::min<int64_t>(64, (m + 63) / 64);
     const int64_t chunk = ((m + ng - 1) / ng + 63) / 64 * 64;
