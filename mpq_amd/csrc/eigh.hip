@@ -858,8 +858,10 @@ int back_transform(int64_t n, int64_t off, int64_t nrefl, const SyevdLayout& L, 
     ex.n = n;
     ex.off = off;
     ex.stream = stream;
-    return wy_apply_x6(n, nrefl, Tb, Z, Y, Yt, P, (int)L.splits, base + L.wy1, base + L.wy3, base + L.wyw, ex,
-                       stream);
+    // the grams are consumed by larft: their area is the pairs' scratch; W and W2 hold the second block
+    const int64_t g_floats = std::max<int64_t>((n - 1 + L.nb - 1) / L.nb, 1) * L.nb * L.nb;
+    return wy_apply_x6(n, nrefl, Tb, Z, Y, Yt, W, W2, P, (int)L.splits, G, g_floats, base + L.wy1, base + L.wy3,
+                       base + L.wyw, ex, stream);
   }
   for (int64_t b = nblocks - 1; b >= 0; --b) {
     const int64_t i0 = b * NB;

@@ -37,13 +37,14 @@ __device__ __forceinline__ void put3(uint4* __restrict__ dst, const float* v, fl
   dst[128] = l;
 }
 
-// Yb3: Y by rows (K = kWyNB reflectors), the right operand of Z += (-W2) Y^T;
-// Yb1: Yt^T by rows (K = mpad), the right operand of W2 = Z Yt.  Y and Yt are m x nb (leading
-// dimension nb); entries past m rows or nb columns are zero.
+// Yb3: Y by rows, the right operand of Z += (-W2) Y^T: its kWyNB reflectors fill the 16-k steps
+// soff .. soff + 7 of ks3 per 32-row tile (ks3 = 16 when two blocks are applied together; Y null:
+// Yb3 untouched); Yb1: Yt^T by rows (K = mpad), the right operand of W2 = Z Yt (Yt null: untouched).
+// Y and Yt are m x nb (leading dimension nb); entries past m rows or nb columns are zero.
 __global__ __launch_bounds__(kThr) void wy_pack_y_kernel(const float* __restrict__ Y, const float* __restrict__ Yt,
                                                          int nb, int64_t m, int64_t mpad, uint4* __restrict__ Yb1,
-                                                         uint4* __restrict__ Yb3) {
-  const int64_t n3 = mpad * 16, q1 = mpad / 8, n1 = q1 * kWyNB;
+                                                         uint4* __restrict__ Yb3, int ks3, int soff) {
+  const int64_t n3 = Y ? mpad * 16 : 0, q1 = mpad / 8, n1 = Yt ? q1 * kWyNB : 0;
   for (int64_t it = (int64_t)blockIdx.x * kThr + threadIdx.x; it < n3 + n1; it += (int64_t)gridDim.x * kThr) {
     float v[8];
     if (it < n3) {
@@ -56,7 +57,7 @@ __global__ __launch_bounds__(kThr) void wy_pack_y_kernel(const float* __restrict
       }
       const int64_t T = j >> 5;
       const int lane = (c8 & 1) * 32 + (int)(j & 31);
-      put3(Yb3 + ((T * 8 + (c8 >> 1)) * 3) * 64 + lane, v, 1.f);
+      put3(Yb3 + ((T * ks3 + soff + (c8 >> 1)) * 3) * 64 + lane, v, 1.f);
     } else {
       const int64_t i2 = it - n3;
       const int c = (int)(i2 % kWyNB);
@@ -181,7 +182,7 @@ __global__ __launch_bounds__(kThr) void wy_w_kernel(const float* __restrict__ Z,
 // W2 = the sum of the split partials (split order), stored as the planes of -W2 (the left operand
 // of the update; rows past n are zero).  Thread: row 32 bx + t / 8, columns 16 (t % 8) .. + 15.
 __global__ __launch_bounds__(kThr) void wy_w2_kernel(const float* __restrict__ P, int splits, int64_t n,
-                                                     uint4* __restrict__ Wp) {
+                                                     uint4* __restrict__ Wp, int ks, int soff) {
   const int t = threadIdx.x;
   const int r = t >> 3, q = t & 7;
   const int64_t row = (int64_t)blockIdx.x * 32 + r;
@@ -201,15 +202,16 @@ __global__ __launch_bounds__(kThr) void wy_w2_kernel(const float* __restrict__ P
       }
     }
   }
-  uint4* dst = Wp + (((int64_t)blockIdx.x * 8 + q) * 3) * 64 + r;
+  uint4* dst = Wp + (((int64_t)blockIdx.x * ks + soff + q) * 3) * 64 + r;
   put3(dst, o, -1.f);
   put3(dst + 32, o + 8, -1.f);
 }
 
 // Z[r][i0 + c] += sum_k (-W2)[r][k] Y[c][k] on the 128 x 128 tile (ti, tj) (rows r < n, columns
-// c < m); wave (wr, wc) owns a 64 x 64 quarter, loaded into the accumulators, K = kWyNB in eight
-// 16-k steps of six plane products.  The 24 fragments of a step (4 row tiles and 4 column tiles x
+// c < m); wave (wr, wc) owns a 64 x 64 quarter, loaded into the accumulators, K = 16 KSU (one or two
+// blocks of kWyNB reflectors) in KSU 16-k steps of six plane products.  The 24 fragments of a step (4 row tiles and 4 column tiles x
 // 3 planes, 24 KB) are loaded once per work-group into a double-buffered LDS slot.
+template <int KSU>
 __global__ __launch_bounds__(kThr, 2) void wy_upd_kernel(const uint4* __restrict__ Wp, const uint4* __restrict__ Yb3,
                                                       float* __restrict__ Z, int64_t n, int64_t i0, int64_t m,
                                                       int64_t tiles_m) {
@@ -223,13 +225,13 @@ __global__ __launch_bounds__(kThr, 2) void wy_upd_kernel(const uint4* __restrict
   const int nn = (int)n;
   // thread t moves chunks e = t + 256 q (q < 6) of a step: q < 3 from the row side, q >= 3 from the
   // column side (chunk f = e / 64 = side * 12 + tile * 3 + plane)
-  const uint4* srow = Wp + (4 * ti) * (8 * 3 * 64);
-  const uint4* scol = Yb3 + (4 * tj) * (8 * 3 * 64);
+  const uint4* srow = Wp + (4 * ti) * (KSU * 3 * 64);
+  const uint4* scol = Yb3 + (4 * tj) * (KSU * 3 * 64);
   int foff[6];
 #pragma unroll
   for (int q = 0; q < 6; ++q) {
     const int e = t + 256 * q, f = (e >> 6) % 12, l = e & 63;
-    foff[q] = (f / 3) * (8 * 3 * 64) + (f % 3) * 64 + l;
+    foff[q] = (f / 3) * (KSU * 3 * 64) + (f % 3) * 64 + l;
   }
 #pragma unroll
   for (int q = 0; q < 6; ++q) sF[0][t + 256 * q] = (q < 3 ? srow : scol)[foff[q]];
@@ -247,10 +249,10 @@ __global__ __launch_bounds__(kThr, 2) void wy_upd_kernel(const uint4* __restrict
       }
     }
   __syncthreads();
-  for (int ks = 0; ks < 8; ++ks) {
+  for (int ks = 0; ks < KSU; ++ks) {
     const int buf = ks & 1;
     uint4 nf[6];
-    if (ks + 1 < 8) {
+    if (ks + 1 < KSU) {
 #pragma unroll
       for (int q = 0; q < 6; ++q) nf[q] = (q < 3 ? srow : scol)[foff[q] + (ks + 1) * 3 * 64];
     }
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(kThr, 2) void wy_upd_kernel(const uint4* __restrict
         acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[x][1], bv[y][1], acc[x][y], 0, 0, 0);
         acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[x][2], bv[y][0], acc[x][y], 0, 0, 0);
       }
-    if (ks + 1 < 8) {
+    if (ks + 1 < KSU) {
 #pragma unroll
       for (int q = 0; q < 6; ++q) sF[buf ^ 1][t + 256 * q] = nf[q];
     }
@@ -293,34 +295,53 @@ __global__ __launch_bounds__(kThr, 2) void wy_upd_kernel(const uint4* __restrict
     }
 }
 
+// out (cols x rows, leading dimension rows) = in^T for in (rows x cols, leading dimension cols),
+// 32 x 32 tiles through LDS
+__global__ __launch_bounds__(kThr) void wy_transpose_kernel(const float* __restrict__ in, int64_t rows, int cols,
+                                                            float* __restrict__ out) {
+  __shared__ float tile[32][33];
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const int64_t r0 = (int64_t)blockIdx.x * 32;
+  const int c0 = blockIdx.y * 32;
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = r0 + k;
+    tile[k][tx] = (r < rows && c0 + tx < cols) ? in[r * cols + c0 + tx] : 0.f;
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int c = c0 + k;
+    const int64_t r = r0 + tx;
+    if (c < cols && r < rows) out[(int64_t)c * rows + r] = tile[tx][k];
+  }
+}
+
+inline int64_t a64f(int64_t v) { return (v + 63) / 64 * 64; }
+
 }  // namespace
 
-int64_t wy_x6_buffer_floats(int64_t n) { return (n + 127) / 128 * 128 * 192 + 256; }
+int64_t wy_x6_buffer_floats(int64_t n) { return (n + 127) / 128 * 128 * 384 + 256; }
 
-int wy_apply_x6(int64_t n, int64_t nrefl, const float* Tb, float* Z, float* Y, float* Yt, float* P, int p_splits,
-                void* Yb1v, void* Yb3v, void* Wpv, const WyExtractY& extract, hipStream_t stream) {
+int wy_apply_x6(int64_t n, int64_t nrefl, const float* Tb, float* Z, float* Y, float* Yt, float* Y2, float* Yt2,
+                float* P, int p_splits, float* scratch, int64_t scratch_floats, void* Yb1v, void* Yb3v, void* Wpv,
+                const WyExtractY& extract, hipStream_t stream) {
   uint4* Yb1 = static_cast<uint4*>(Yb1v);
   uint4* Yb3 = static_cast<uint4*>(Yb3v);
   uint4* Wp = static_cast<uint4*>(Wpv);
   const int64_t nblocks = nrefl > 0 ? (nrefl + kWyNB - 1) / kWyNB : 0;
   const int64_t rows_wg = (n + 127) / 128;
-  for (int64_t b = nblocks - 1; b >= 0; --b) {
-    const int64_t i0 = b * kWyNB;
-    const int nb = (int)std::min<int64_t>(kWyNB, nrefl - i0);
-    const int64_t m = n - i0;
-    const int64_t mpad = (m + 127) / 128 * 128;
-    const int64_t KS1 = mpad / 16;
-    int rc = extract(i0, nb, Y);
+  auto pack = [&](const float* Yr, const float* Ytr, int nb, int64_t m, int64_t mpad, int ks, int soff) -> int {
+    const int64_t items = (Yr ? mpad * 16 : 0) + (Ytr ? mpad / 8 * kWyNB : 0);
+    const int64_t g = std::min<int64_t>((items + kThr - 1) / kThr, 16384);
+    hipLaunchKernelGGL(wy_pack_y_kernel, dim3((unsigned)g), dim3(kThr), 0, stream, Yr, Ytr, nb, m, mpad, Yb1, Yb3,
+                       ks, soff);
+    MPQ_LAUNCH_CHECK();
+    return kOk;
+  };
+  // the planes of -(Z[:, i0:] Ytr) (m x nb) at the 16-k steps soff .. soff + 7 of ks (Yb1 from Ytr)
+  auto w_pass = [&](const float* Ytr, int nb, int64_t i0, int64_t m, int64_t mpad, int ks, int soff) -> int {
+    int rc = pack(nullptr, Ytr, nb, m, mpad, ks, soff);
     if (rc != kOk) return rc;
-    // Yt = Y Tb^T (m x nb)
-    MPQ_HIP_TRY(gemm(Y, nb, Tb + b * kWyNB * kWyNB, nb, true, nullptr, Yt, nb, m, nb, nb, 1.f, 0.f, nullptr, 0,
-                     stream));
-    {
-      const int64_t items = mpad * 16 + mpad / 8 * kWyNB;
-      const int64_t g = std::min<int64_t>((items + kThr - 1) / kThr, 16384);
-      hipLaunchKernelGGL(wy_pack_y_kernel, dim3((unsigned)g), dim3(kThr), 0, stream, Y, Yt, nb, m, mpad, Yb1, Yb3);
-      MPQ_LAUNCH_CHECK();
-    }
+    const int64_t KS1 = mpad / 16;
     // split K so that about 1024 work-groups run, each slice a multiple of 64
     int64_t S = std::max<int64_t>(1, std::min<int64_t>({(int64_t)p_splits, mpad / 64, (1024 + rows_wg - 1) / rows_wg}));
     const int64_t kps = (mpad / S + 63) / 64 * 64;
@@ -332,12 +353,74 @@ int wy_apply_x6(int64_t n, int64_t nrefl, const float* Tb, float* Z, float* Y, f
       hipLaunchKernelGGL(wy_w_kernel<false>, dim3((unsigned)rows_wg, (unsigned)S), dim3(kThr), 0, stream, Z, n, i0, m,
                          Yb1, KS1, kps, P);
     MPQ_LAUNCH_CHECK();
-    hipLaunchKernelGGL(wy_w2_kernel, dim3((unsigned)(rows_wg * 4)), dim3(kThr), 0, stream, P, (int)S, n, Wp);
+    hipLaunchKernelGGL(wy_w2_kernel, dim3((unsigned)(rows_wg * 4)), dim3(kThr), 0, stream, P, (int)S, n, Wp, ks, soff);
     MPQ_LAUNCH_CHECK();
+    return kOk;
+  };
+  auto update = [&](int ks, int64_t i0, int64_t m, int64_t mpad) -> int {
     const int64_t tiles_m = mpad / 128;
-    hipLaunchKernelGGL(wy_upd_kernel, dim3((unsigned)(rows_wg * tiles_m)), dim3(kThr), 0, stream, Wp, Yb3, Z, n, i0,
-                       m, tiles_m);
+    if (ks == 16)
+      hipLaunchKernelGGL(wy_upd_kernel<16>, dim3((unsigned)(rows_wg * tiles_m)), dim3(kThr), 0, stream, Wp, Yb3, Z, n,
+                         i0, m, tiles_m);
+    else
+      hipLaunchKernelGGL(wy_upd_kernel<8>, dim3((unsigned)(rows_wg * tiles_m)), dim3(kThr), 0, stream, Wp, Yb3, Z, n,
+                         i0, m, tiles_m);
     MPQ_LAUNCH_CHECK();
+    return kOk;
+  };
+  int rc;
+  int64_t b = nblocks - 1;
+  while (b >= 0) {
+    if (b >= 1) {
+      // Blocks B = b and A = b - 1 in one update: with W_B = Z Yt_B and W_A' = Z Yt_A from the same Z,
+      // applying B then A is Z - W_B Y_B^T - (W_A' - W_B C) Y_A^T, C = Y_B^T Yt_A, i.e.
+      // Z - W_B (Y_B - Y_A C^T)^T - W_A' Y_A^T: one pass over Z with K = 2 kWyNB.
+      const int64_t i0 = (b - 1) * kWyNB, i0B = b * kWyNB;
+      const int nbA = kWyNB;
+      const int nbB = (int)std::min<int64_t>(kWyNB, nrefl - i0B);
+      const int64_t m = n - i0;
+      const int64_t mpad = (m + 127) / 128 * 128;
+      if (scratch_floats < (int64_t)nbB * nbA + 64 || a64f(n * kWyNB) * p_splits < (int64_t)nbB * m) {
+        set_error("wy_apply_x6: scratch too small");
+        return kInvalidArgument;
+      }
+      if ((rc = extract(i0, nbA, Y)) != kOk) return rc;
+      MPQ_HIP_TRY(gemm(Y, nbA, Tb + (b - 1) * kWyNB * kWyNB, nbA, true, nullptr, Yt, nbA, m, nbA, nbA, 1.f, 0.f,
+                       nullptr, 0, stream));
+      // Y_B as m x nbB with its first kWyNB rows zero (its reflectors start kWyNB columns later)
+      MPQ_HIP_TRY(hipMemsetAsync(Y2, 0, (size_t)kWyNB * nbB * sizeof(float), stream));
+      if ((rc = extract(i0B, nbB, Y2 + (int64_t)kWyNB * nbB)) != kOk) return rc;
+      MPQ_HIP_TRY(gemm(Y2, nbB, Tb + b * kWyNB * kWyNB, nbB, true, nullptr, Yt2, nbB, m, nbB, nbB, 1.f, 0.f, nullptr,
+                       0, stream));
+      if ((rc = w_pass(Yt2, nbB, i0, m, mpad, 16, 0)) != kOk) return rc;
+      if ((rc = w_pass(Yt, nbA, i0, m, mpad, 16, 8)) != kOk) return rc;
+      // C (nbB x nbA, in scratch) = Y_B^T Yt_A through Y_B^T in P (free again); Y_B -= Y_A C^T
+      hipLaunchKernelGGL(wy_transpose_kernel, dim3((unsigned)((m + 31) / 32), (unsigned)((nbB + 31) / 32)),
+                         dim3(kThr), 0, stream, Y2, m, nbB, P);
+      MPQ_LAUNCH_CHECK();
+      float* C = scratch;
+      float* gws = scratch + ((int64_t)nbB * nbA + 63) / 64 * 64;
+      const int64_t gws_floats = scratch_floats - (gws - scratch);
+      MPQ_HIP_TRY(gemm(P, m, Yt, nbA, false, nullptr, C, nbA, nbB, nbA, m, 1.f, 0.f, gws, gws_floats, stream));
+      MPQ_HIP_TRY(gemm(Y, nbA, C, nbA, true, nullptr, Y2, nbB, m, nbB, nbA, -1.f, 1.f, gws, gws_floats, stream));
+      if ((rc = pack(Y2, nullptr, nbB, m, mpad, 16, 0)) != kOk) return rc;
+      if ((rc = pack(Y, nullptr, nbA, m, mpad, 16, 8)) != kOk) return rc;
+      if ((rc = update(16, i0, m, mpad)) != kOk) return rc;
+      b -= 2;
+    } else {
+      const int64_t i0 = b * kWyNB;
+      const int nb = (int)std::min<int64_t>(kWyNB, nrefl - i0);
+      const int64_t m = n - i0;
+      const int64_t mpad = (m + 127) / 128 * 128;
+      if ((rc = extract(i0, nb, Y)) != kOk) return rc;
+      // Yt = Y Tb^T (m x nb)
+      MPQ_HIP_TRY(gemm(Y, nb, Tb + b * kWyNB * kWyNB, nb, true, nullptr, Yt, nb, m, nb, nb, 1.f, 0.f, nullptr, 0,
+                       stream));
+      if ((rc = pack(Y, nullptr, nb, m, mpad, 8, 0)) != kOk) return rc;
+      if ((rc = w_pass(Yt, nb, i0, m, mpad, 8, 0)) != kOk) return rc;
+      if ((rc = update(8, i0, m, mpad)) != kOk) return rc;
+      b -= 1;
+    }
   }
   return kOk;
 }
