@@ -43,7 +43,7 @@ __device__ __forceinline__ void put3(uint4* __restrict__ dst, const float* v, fl
 // Y and Yt are m x nb (leading dimension nb); entries past m rows or nb columns are zero.
 __global__ __launch_bounds__(kThr) void wy_pack_y_kernel(const float* __restrict__ Y, const float* __restrict__ Yt,
                                                          int nb, int64_t m, int64_t mpad, uint4* __restrict__ Yb1,
-                                                         uint4* __restrict__ Yb3, int ks3, int soff) {
+                                                         uint4* __restrict__ Yb3, int ks3, int soff, int tc0) {
   const int64_t n3 = Y ? mpad * 16 : 0, q1 = mpad / 8, n1 = Yt ? q1 * kWyNB : 0;
   for (int64_t it = (int64_t)blockIdx.x * kThr + threadIdx.x; it < n3 + n1; it += (int64_t)gridDim.x * kThr) {
     float v[8];
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(kThr) void wy_pack_y_kernel(const float* __restrict
       }
       const int64_t KS1 = mpad / 16;
       const int lane = (int)(q & 1) * 32 + (c & 31);
-      put3(Yb1 + (((int64_t)(c >> 5) * KS1 + (q >> 1)) * 3) * 64 + lane, v, 1.f);
+      put3(Yb1 + (((int64_t)(tc0 + (c >> 5)) * KS1 + (q >> 1)) * 3) * 64 + lane, v, 1.f);
     }
   }
 }
@@ -107,35 +107,38 @@ __device__ __forceinline__ const uint4* wy_bsrc(const uint4* __restrict__ Yb1, i
   return Yb1 + ((tc * KS1 + s) * 3 + p) * 64 + l;
 }
 
-template <bool VEC>
+template <bool VEC, int NT>
 __global__ __launch_bounds__(kThr) void wy_w_kernel(const float* __restrict__ Z, int64_t n, int64_t i0, int64_t m,
                                                     const uint4* __restrict__ Yb1, int64_t KS1, int64_t kps,
                                                     float* __restrict__ P) {
-  __shared__ uint4 sB[2][12 * 64];
+  constexpr int NF = NT * 3 * 64;  // right-operand chunks of a 16-k step
+  __shared__ uint4 sB[2][NF];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, hh = lane >> 5;
   const int64_t R0 = (int64_t)blockIdx.x * 128 + 32 * wave;
   const int64_t row = R0 + (lane & 31);
   const bool rok = row < n;
   const float* __restrict__ zr = Z + (rok ? row : n - 1) * n + i0;
   const int64_t s0 = (int64_t)blockIdx.y * kps / 16, s1 = min(KS1, ((int64_t)blockIdx.y * kps + kps) / 16);
-  floatx16 acc[4];
+  floatx16 acc[NT];
 #pragma unroll
-  for (int tc = 0; tc < 4; ++tc)
+  for (int tc = 0; tc < NT; ++tc)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[tc][v] = 0.f;
   if (s0 < s1) {
 #pragma unroll
-    for (int q = 0; q < 3; ++q) sB[0][t + 256 * q] = *wy_bsrc(Yb1, KS1, s0, t + 256 * q);
+    for (int q = 0; q < NF / 256; ++q) sB[0][t + 256 * q] = *wy_bsrc(Yb1, KS1, s0, t + 256 * q);
     Z8 zc = wy_zload<VEC>(zr, 16 * s0 + 8 * hh, m);
     __syncthreads();
     for (int64_t s = s0; s < s1; ++s) {
       const int buf = (int)((s - s0) & 1);
       const bool more = s + 1 < s1;
-      uint4 nb[3] = {zc4(), zc4(), zc4()};
+      uint4 nb[NF / 256];
+#pragma unroll
+      for (int q = 0; q < NF / 256; ++q) nb[q] = zc4();
       Z8 zn = zc;
       if (more) {
 #pragma unroll
-        for (int q = 0; q < 3; ++q) nb[q] = *wy_bsrc(Yb1, KS1, s + 1, t + 256 * q);
+        for (int q = 0; q < NF / 256; ++q) nb[q] = *wy_bsrc(Yb1, KS1, s + 1, t + 256 * q);
         zn = wy_zload<VEC>(zr, 16 * (s + 1) + 8 * hh, m);
       }
       float v[8];
@@ -150,7 +153,7 @@ __global__ __launch_bounds__(kThr) void wy_w_kernel(const float* __restrict__ Z,
                    a2 = __builtin_bit_cast(bf16x8, pl);
       const uint4* sb = sB[buf] + lane;
 #pragma unroll
-      for (int tc = 0; tc < 4; ++tc) {
+      for (int tc = 0; tc < NT; ++tc) {
         const bf16x8 b0 = __builtin_bit_cast(bf16x8, sb[(tc * 3 + 0) * 64]);
         const bf16x8 b1 = __builtin_bit_cast(bf16x8, sb[(tc * 3 + 1) * 64]);
         const bf16x8 b2 = __builtin_bit_cast(bf16x8, sb[(tc * 3 + 2) * 64]);
@@ -163,26 +166,26 @@ __global__ __launch_bounds__(kThr) void wy_w_kernel(const float* __restrict__ Z,
       }
       if (more) {
 #pragma unroll
-        for (int q = 0; q < 3; ++q) sB[buf ^ 1][t + 256 * q] = nb[q];
+        for (int q = 0; q < NF / 256; ++q) sB[buf ^ 1][t + 256 * q] = nb[q];
         zc = zn;
       }
       __syncthreads();  // uniform: s, s1 are the same for the whole work-group
     }
   }
-  float* Ps = P + (int64_t)blockIdx.y * n * kWyNB;
+  float* Ps = P + (int64_t)blockIdx.y * n * (32 * NT);
 #pragma unroll
-  for (int tc = 0; tc < 4; ++tc)
+  for (int tc = 0; tc < NT; ++tc)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int64_t r = R0 + 8 * (v >> 2) + 4 * hh + (v & 3);
-      if (r < n) Ps[r * kWyNB + 32 * tc + (lane & 31)] = acc[tc][v];
+      if (r < n) Ps[r * (32 * NT) + 32 * tc + (lane & 31)] = acc[tc][v];
     }
 }
 
 // W2 = the sum of the split partials (split order), stored as the planes of -W2 (the left operand
 // of the update; rows past n are zero).  Thread: row 32 bx + t / 8, columns 16 (t % 8) .. + 15.
 __global__ __launch_bounds__(kThr) void wy_w2_kernel(const float* __restrict__ P, int splits, int64_t n,
-                                                     uint4* __restrict__ Wp, int ks, int soff) {
+                                                     uint4* __restrict__ Wp, int ks, int soff, int pw, int pc0) {
   const int t = threadIdx.x;
   const int r = t >> 3, q = t & 7;
   const int64_t row = (int64_t)blockIdx.x * 32 + r;
@@ -191,7 +194,7 @@ __global__ __launch_bounds__(kThr) void wy_w2_kernel(const float* __restrict__ P
   for (int j = 0; j < 16; ++j) o[j] = 0.f;
   if (row < n) {
     for (int sp = 0; sp < splits; ++sp) {
-      const float4* src = reinterpret_cast<const float4*>(P + ((int64_t)sp * n + row) * kWyNB + 16 * q);
+      const float4* src = reinterpret_cast<const float4*>(P + ((int64_t)sp * n + row) * pw + pc0 + 16 * q);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float4 f = src[j];
@@ -329,33 +332,53 @@ int wy_apply_x6(int64_t n, int64_t nrefl, const float* Tb, float* Z, float* Y, f
   uint4* Wp = static_cast<uint4*>(Wpv);
   const int64_t nblocks = nrefl > 0 ? (nrefl + kWyNB - 1) / kWyNB : 0;
   const int64_t rows_wg = (n + 127) / 128;
-  auto pack = [&](const float* Yr, const float* Ytr, int nb, int64_t m, int64_t mpad, int ks, int soff) -> int {
+  auto pack = [&](const float* Yr, const float* Ytr, int nb, int64_t m, int64_t mpad, int ks, int soff,
+                  int tc0) -> int {
     const int64_t items = (Yr ? mpad * 16 : 0) + (Ytr ? mpad / 8 * kWyNB : 0);
     const int64_t g = std::min<int64_t>((items + kThr - 1) / kThr, 16384);
     hipLaunchKernelGGL(wy_pack_y_kernel, dim3((unsigned)g), dim3(kThr), 0, stream, Yr, Ytr, nb, m, mpad, Yb1, Yb3,
-                       ks, soff);
+                       ks, soff, tc0);
+    MPQ_LAUNCH_CHECK();
+    return kOk;
+  };
+  // P (S splits x n x 32 NT) = Z[:, i0:] times the NT column tiles packed in Yb1
+  auto w_prod = [&](int NT, int64_t i0, int64_t m, int64_t mpad, int64_t smax) -> int64_t {
+    const int64_t KS1 = mpad / 16;
+    // split K so that about 1024 work-groups run, each slice a multiple of 64
+    int64_t S = std::max<int64_t>(1, std::min<int64_t>({smax, mpad / 64, (1024 + rows_wg - 1) / rows_wg}));
+    const int64_t kps = (mpad / S + 63) / 64 * 64;
+    S = (mpad + kps - 1) / kps;
+    const dim3 grid((unsigned)rows_wg, (unsigned)S);
+    if (NT == 8) {
+      if ((n & 3) == 0)
+        hipLaunchKernelGGL((wy_w_kernel<true, 8>), grid, dim3(kThr), 0, stream, Z, n, i0, m, Yb1, KS1, kps, P);
+      else
+        hipLaunchKernelGGL((wy_w_kernel<false, 8>), grid, dim3(kThr), 0, stream, Z, n, i0, m, Yb1, KS1, kps, P);
+    } else {
+      if ((n & 3) == 0)
+        hipLaunchKernelGGL((wy_w_kernel<true, 4>), grid, dim3(kThr), 0, stream, Z, n, i0, m, Yb1, KS1, kps, P);
+      else
+        hipLaunchKernelGGL((wy_w_kernel<false, 4>), grid, dim3(kThr), 0, stream, Z, n, i0, m, Yb1, KS1, kps, P);
+    }
+    return hipGetLastError() == hipSuccess ? S : -1;
+  };
+  // planes of -W (columns pc0 .. pc0 + 127 of the partials' pw) at the 16-k steps soff .. soff + 7 of ks
+  auto w_planes = [&](int64_t S, int pw, int pc0, int ks, int soff) -> int {
+    hipLaunchKernelGGL(wy_w2_kernel, dim3((unsigned)(rows_wg * 4)), dim3(kThr), 0, stream, P, (int)S, n, Wp, ks, soff,
+                       pw, pc0);
     MPQ_LAUNCH_CHECK();
     return kOk;
   };
   // the planes of -(Z[:, i0:] Ytr) (m x nb) at the 16-k steps soff .. soff + 7 of ks (Yb1 from Ytr)
   auto w_pass = [&](const float* Ytr, int nb, int64_t i0, int64_t m, int64_t mpad, int ks, int soff) -> int {
-    int rc = pack(nullptr, Ytr, nb, m, mpad, ks, soff);
+    int rc = pack(nullptr, Ytr, nb, m, mpad, ks, soff, 0);
     if (rc != kOk) return rc;
-    const int64_t KS1 = mpad / 16;
-    // split K so that about 1024 work-groups run, each slice a multiple of 64
-    int64_t S = std::max<int64_t>(1, std::min<int64_t>({(int64_t)p_splits, mpad / 64, (1024 + rows_wg - 1) / rows_wg}));
-    const int64_t kps = (mpad / S + 63) / 64 * 64;
-    S = (mpad + kps - 1) / kps;
-    if ((n & 3) == 0)
-      hipLaunchKernelGGL(wy_w_kernel<true>, dim3((unsigned)rows_wg, (unsigned)S), dim3(kThr), 0, stream, Z, n, i0, m,
-                         Yb1, KS1, kps, P);
-    else
-      hipLaunchKernelGGL(wy_w_kernel<false>, dim3((unsigned)rows_wg, (unsigned)S), dim3(kThr), 0, stream, Z, n, i0, m,
-                         Yb1, KS1, kps, P);
-    MPQ_LAUNCH_CHECK();
-    hipLaunchKernelGGL(wy_w2_kernel, dim3((unsigned)(rows_wg * 4)), dim3(kThr), 0, stream, P, (int)S, n, Wp, ks, soff);
-    MPQ_LAUNCH_CHECK();
-    return kOk;
+    const int64_t S = w_prod(4, i0, m, mpad, p_splits);
+    if (S < 0) {
+      set_error("wy_apply_x6: launch failed");
+      return kHipError;
+    }
+    return w_planes(S, kWyNB, 0, ks, soff);
   };
   auto update = [&](int ks, int64_t i0, int64_t m, int64_t mpad) -> int {
     const int64_t tiles_m = mpad / 128;
@@ -392,8 +415,21 @@ int wy_apply_x6(int64_t n, int64_t nrefl, const float* Tb, float* Z, float* Y, f
       if ((rc = extract(i0B, nbB, Y2 + (int64_t)kWyNB * nbB)) != kOk) return rc;
       MPQ_HIP_TRY(gemm(Y2, nbB, Tb + b * kWyNB * kWyNB, nbB, true, nullptr, Yt2, nbB, m, nbB, nbB, 1.f, 0.f, nullptr,
                        0, stream));
-      if ((rc = w_pass(Yt2, nbB, i0, m, mpad, 16, 0)) != kOk) return rc;
-      if ((rc = w_pass(Yt, nbA, i0, m, mpad, 16, 8)) != kOk) return rc;
+      if (p_splits >= 2) {
+        // W_B and W_A' from one read of Z: the 8 column tiles of [Yt_B Yt_A]
+        if ((rc = pack(nullptr, Yt2, nbB, m, mpad, 16, 0, 0)) != kOk) return rc;
+        if ((rc = pack(nullptr, Yt, nbA, m, mpad, 16, 0, 4)) != kOk) return rc;
+        const int64_t S = w_prod(8, i0, m, mpad, p_splits / 2);
+        if (S < 0) {
+          set_error("wy_apply_x6: launch failed");
+          return kHipError;
+        }
+        if ((rc = w_planes(S, 2 * kWyNB, 0, 16, 0)) != kOk) return rc;
+        if ((rc = w_planes(S, 2 * kWyNB, kWyNB, 16, 8)) != kOk) return rc;
+      } else {
+        if ((rc = w_pass(Yt2, nbB, i0, m, mpad, 16, 0)) != kOk) return rc;
+        if ((rc = w_pass(Yt, nbA, i0, m, mpad, 16, 8)) != kOk) return rc;
+      }
       // C (nbB x nbA, in scratch) = Y_B^T Yt_A through Y_B^T in P (free again); Y_B -= Y_A C^T
       hipLaunchKernelGGL(wy_transpose_kernel, dim3((unsigned)((m + 31) / 32), (unsigned)((nbB + 31) / 32)),
                          dim3(kThr), 0, stream, Y2, m, nbB, P);
@@ -403,8 +439,8 @@ int wy_apply_x6(int64_t n, int64_t nrefl, const float* Tb, float* Z, float* Y, f
       const int64_t gws_floats = scratch_floats - (gws - scratch);
       MPQ_HIP_TRY(gemm(P, m, Yt, nbA, false, nullptr, C, nbA, nbB, nbA, m, 1.f, 0.f, gws, gws_floats, stream));
       MPQ_HIP_TRY(gemm(Y, nbA, C, nbA, true, nullptr, Y2, nbB, m, nbB, nbA, -1.f, 1.f, gws, gws_floats, stream));
-      if ((rc = pack(Y2, nullptr, nbB, m, mpad, 16, 0)) != kOk) return rc;
-      if ((rc = pack(Y, nullptr, nbA, m, mpad, 16, 8)) != kOk) return rc;
+      if ((rc = pack(Y2, nullptr, nbB, m, mpad, 16, 0, 0)) != kOk) return rc;
+      if ((rc = pack(Y, nullptr, nbA, m, mpad, 16, 8, 0)) != kOk) return rc;
       if ((rc = update(16, i0, m, mpad)) != kOk) return rc;
       b -= 2;
     } else {
@@ -416,7 +452,7 @@ int wy_apply_x6(int64_t n, int64_t nrefl, const float* Tb, float* Z, float* Y, f
       // Yt = Y Tb^T (m x nb)
       MPQ_HIP_TRY(gemm(Y, nb, Tb + b * kWyNB * kWyNB, nb, true, nullptr, Yt, nb, m, nb, nb, 1.f, 0.f, nullptr, 0,
                        stream));
-      if ((rc = pack(Y, nullptr, nb, m, mpad, 8, 0)) != kOk) return rc;
+      if ((rc = pack(Y, nullptr, nb, m, mpad, 8, 0, 0)) != kOk) return rc;
       if ((rc = w_pass(Yt, nb, i0, m, mpad, 8, 0)) != kOk) return rc;
       if ((rc = update(8, i0, m, mpad)) != kOk) return rc;
       b -= 1;
