@@ -24,7 +24,7 @@ inline int64_t q2_blocks(int64_t n) {
 
 // Element offsets (floats) of the two-stage workspace, each region 64 floats aligned.
 struct Layout {
-  int64_t Yl, taul, Rs, E, Rroot, Q1, Y, BP, X, T, Gp, M, Xop, Yop, Px, Gd, Rc, Rt, flags, AB, V2, tau2, Pt, prog, Zq, total;
+  int64_t Yl, taul, Rs, E, Rroot, Q1, Y, BP, X, T, Gp, M, Xop, Yop, Y2, Wf, G12, Px, Gd, Rc, Rt, flags, AB, V2, tau2, Pt, prog, Zq, total;
   int64_t ldq;  // leading dimension of Zq (n rounded up to 64)
   int64_t px_floats;
 };

@@ -672,87 +672,186 @@ __global__ __launch_bounds__(kThr) void xsum_kernel(const float* __restrict__ P,
   X[e] = a;
 }
 
-// Partial grams Gp[g] = Y^T X over the rows of chunk g (64-row tiles staged in LDS).
+// Partial grams over the rows of chunk g on the fp32 matrix cores: Gp[g][0] = Y^T X, and when the
+// panel is the second of a pair also Gp[g][1] = Y^T Yh and Gp[g][2] = Y^T Wh (Yh, Wh: the first
+// panel's Y and W from the row where this panel's rows start); np = 1 or 3 products per chunk.  Wave
+// w takes rows 8 t + 2 w + h of the chunk (lane (i, h) feeds Y[row][i] and X[row][i] to MFMA step t);
+// the four waves' 32 x 32 results are added through LDS in wave order.
 __global__ __launch_bounds__(kThr) void gram_partial_kernel(const float* __restrict__ Y, const float* __restrict__ X,
-                                                            int64_t m, int64_t chunk, float* __restrict__ Gp) {
-  __shared__ float sY[64][33];
-  __shared__ float sX[64][33];
-  const int t = threadIdx.x;
+                                                            int64_t m, int64_t chunk, float* __restrict__ Gp,
+                                                            const float* __restrict__ Yh,
+                                                            const float* __restrict__ Wh) {
+  __shared__ float red[4][3][1024];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, i = lane & 31, h = lane >> 5;
+  const bool three = Yh != nullptr;
+  const int np = three ? 3 : 1;
   const int64_t rbeg = (int64_t)blockIdx.x * chunk;
   const int64_t rend = min(m, rbeg + chunk);
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int64_t r0 = rbeg; r0 < rend; r0 += 64) {
-    for (int e = t; e < 64 * 32; e += kThr) {
-      const int64_t r = r0 + e / 32;
-      sY[e / 32][e & 31] = r < rend ? Y[r * 32 + (e & 31)] : 0.f;
-      sX[e / 32][e & 31] = r < rend ? X[r * 32 + (e & 31)] : 0.f;
-    }
-    __syncthreads();
+  floatx16 acc[3];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int e = t + q * kThr, i = e / 32, j = e & 31;
-      float a = acc[q];
-      for (int rr = 0; rr < 64; ++rr) a = fmaf(sY[rr][i], sX[rr][j], a);
-      acc[q] = a;
+  for (int q = 0; q < 3; ++q)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[q][v] = 0.f;
+  for (int64_t k0 = rbeg; k0 < rend; k0 += 64) {  // 8 steps of 8 rows, loads first
+    float ya[8], xa[8], ha[8], wa[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t k = k0 + 8 * u + 2 * w + h;
+      const bool in = k < rend;
+      const int64_t kc = in ? k : rbeg;
+      ya[u] = in ? Y[kc * 32 + i] : 0.f;
+      xa[u] = in ? X[kc * 32 + i] : 0.f;
+      if (three) {
+        ha[u] = in ? Yh[kc * 32 + i] : 0.f;
+        wa[u] = in ? Wh[kc * 32 + i] : 0.f;
+      }
     }
-    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ya[u], xa[u], acc[0], 0, 0, 0);
+      if (three) {
+        acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(ya[u], ha[u], acc[1], 0, 0, 0);
+        acc[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(ya[u], wa[u], acc[2], 0, 0, 0);
+      }
+    }
   }
+  for (int q = 0; q < np; ++q)
 #pragma unroll
-  for (int q = 0; q < 4; ++q) Gp[(int64_t)blockIdx.x * 1024 + t + q * kThr] = acc[q];
+    for (int v = 0; v < 16; ++v) red[w][q][(8 * (v >> 2) + 4 * h + (v & 3)) * 32 + i] = acc[q][v];
+  __syncthreads();
+  for (int q = 0; q < np; ++q)
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+      const int e = t + e4 * kThr;
+      Gp[((int64_t)blockIdx.x * np + q) * 1024 + e] = ((red[0][q][e] + red[1][q][e]) + red[2][q][e]) + red[3][q][e];
+    }
 }
 
-// M = T^T (sum_g Gp[g]) (32 x 32): one work-group of 1024 threads, one entry each.
-__global__ __launch_bounds__(1024) void m_kernel(const float* __restrict__ Gp, int ng, const float* __restrict__ T,
-                                                 float* __restrict__ Mout) {
-  __shared__ float G[32][33];
+// M = T^T (sum_g Gp[g]) (32 x 32): one work-group of 1024 threads, one entry each.  For the second
+// panel of a pair (np = 3) X is the product of the not yet updated matrix, X = X^ - Yh G1 - Wh G2
+// with G1 = (Y^T Wh)^T T and G2 = (Y^T Yh)^T T (Yh G1 + Wh G2 is the first panel's update applied to
+// this panel's B = Y T); then Y^T X = S1 - S2 G1 - S3 G2 (S1 = Y^T X^, S2 = Y^T Yh, S3 = Y^T Wh), and
+// G1, G2 go to Gout for w_kernel.
+__global__ __launch_bounds__(1024) void m_kernel(const float* __restrict__ Gp, int ng, int np,
+                                                 const float* __restrict__ T, float* __restrict__ Mout,
+                                                 float* __restrict__ Gout) {
+  __shared__ float S[3][32][33];
+  __shared__ float Gc[2][32][33];
+  __shared__ float sT[32][33];
   const int e = threadIdx.x, i = e >> 5, j = e & 31;
-  float a = 0.f;
-  for (int g = 0; g < ng; ++g) a += Gp[(int64_t)g * 1024 + e];
-  G[i][j] = a;
+  sT[i][j] = T[e];
+  for (int pr = 0; pr < np; ++pr) {
+    float a = 0.f;
+    for (int g0 = 0; g0 < ng; g0 += 16) {  // 16 loads in flight, added in partial order
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = g0 + u < ng ? Gp[((int64_t)(g0 + u) * np + pr) * 1024 + e] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) a += v[u];
+    }
+    S[pr][i][j] = a;
+  }
   __syncthreads();
+  if (np == 3) {
+    float g1 = 0.f, g2 = 0.f;
+    for (int l = 0; l < 32; ++l) {
+      g1 = fmaf(S[2][l][i], sT[l][j], g1);
+      g2 = fmaf(S[1][l][i], sT[l][j], g2);
+    }
+    Gc[0][i][j] = g1;
+    Gc[1][i][j] = g2;
+    Gout[e] = g1;
+    Gout[1024 + e] = g2;
+    __syncthreads();
+    float c = S[0][i][j];
+    for (int l = 0; l < 32; ++l) c -= S[1][i][l] * Gc[0][l][j] + S[2][i][l] * Gc[1][l][j];
+    __syncthreads();
+    S[0][i][j] = c;
+    __syncthreads();
+  }
   float mv = 0.f;
-  for (int l = 0; l < 32; ++l) mv = fmaf(T[l * 32 + i], G[l][j], mv);
+  for (int l = 0; l < 32; ++l) mv = fmaf(sT[l][i], S[0][l][j], mv);
   Mout[e] = mv;
 }
 
-// W = X - 1/2 Y M and the operands of the rank-64 update A22 -= [Y W] [W Y]^T as three bf16 planes
+// W = X - 1/2 Y M and the operands of the trailing update A22 -= [Y W] [W Y]^T as three bf16 planes
 // (exact split, see x6_split.h): Xp holds -[Y W], Yp holds [W Y], both in the operand order of
-// v_mfma_f32_32x32x16_bf16, per 32-row tile T chunk (plane p, k-step s, lane l) at
-// T * 768 + (p * 4 + s) * 64 + l = row 32 T + l % 32, k = 16 s + 8 (l / 32) + 0 .. 7.  Rows m ..
-// (a multiple of 128) are zero.
-constexpr int kUpdTile = 768;  // uint4 per 32-row tile of a packed update operand
+// v_mfma_f32_32x32x16_bf16 with ks 16-k steps (K = 16 ks), per 32-row tile T chunk (plane p, step s,
+// lane l) at T * 3 ks 64 + (p ks + s) * 64 + l = row 32 T + l % 32, k = 16 s + 8 (l / 32) + 0 .. 7.
+// This panel's Y fills the 8-k chunks cy .. cy + 3 of Xp (W those of Yp) and W the chunks cw .. cw + 3
+// (Y those of Yp): a lone panel takes K = 64 (cy 0, cw 4); a pair of panels shares K = 128.  Row r
+// goes to packed row r - row_off (the first panel of a pair packs its rows from the second panel's
+// origin, row_off = 32); packed rows past m are zero, up to a multiple of 128.  Wout (optional) gets
+// W in fp32.  With Gc (the second panel of a pair), X is the product of the not yet updated matrix
+// and W -= Yh G1 + Wh G2 (see m_kernel).
 __global__ __launch_bounds__(kThr) void w_kernel(const float* __restrict__ Mg, const float* __restrict__ Y,
                                                  const float* __restrict__ X, int64_t m, uint4* __restrict__ Xp,
-                                                 uint4* __restrict__ Yp) {
-  __shared__ float M[32][33];
+                                                 uint4* __restrict__ Yp, int ks, int cy, int cw, int row_off,
+                                                 float* __restrict__ Wout, const float* __restrict__ Yh,
+                                                 const float* __restrict__ Wh, const float* __restrict__ Gc) {
+  __shared__ float M[3][32][33];
   const int t = threadIdx.x;
-  for (int e = t; e < 1024; e += kThr) M[e >> 5][e & 31] = Mg[e];
+  for (int e = t; e < 1024; e += kThr) M[0][e >> 5][e & 31] = Mg[e];
+  if (Gc) {
+    for (int e = t; e < 1024; e += kThr) {
+      M[1][e >> 5][e & 31] = Gc[e];
+      M[2][e >> 5][e & 31] = Gc[1024 + e];
+    }
+  }
   __syncthreads();
-  const int64_t r = (int64_t)blockIdx.x * kThr + t;
-  if (r >= (m + 127) / 128 * 128) return;  // packed rows: m rounded up to 128
-  float y[32], w[32];
+  // four threads per row: quarter q computes W's columns 8 q .. 8 q + 7 and packs chunk q of Y and W
+  const int q = t & 3;
+  const int64_t r = (int64_t)blockIdx.x * (kThr / 4) + (t >> 2);
+  if (r >= row_off + (m - row_off + 127) / 128 * 128) return;  // packed rows: rounded up to 128
+  float yq[8], wq[8];
   if (r < m) {
+    float y[32];
 #pragma unroll
     for (int j = 0; j < 32; ++j) y[j] = Y[r * 32 + j];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
+    for (int jj = 0; jj < 8; ++jj) {
+      const int j = 8 * q + jj;
       float a = 0.f;
-      for (int l = 0; l < 32; ++l) a = fmaf(y[l], M[l][j], a);
-      w[j] = fmaf(-0.5f, a, X[r * 32 + j]);
+      for (int l = 0; l < 32; ++l) a = fmaf(y[l], M[0][l][j], a);
+      wq[jj] = fmaf(-0.5f, a, X[r * 32 + j]);
+      yq[jj] = y[j];
+    }
+    if (Gc) {
+      float yh[32], wh[32];
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        yh[j] = Yh[r * 32 + j];
+        wh[j] = Wh[r * 32 + j];
+      }
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int j = 8 * q + jj;
+        float c = 0.f;
+        for (int l = 0; l < 32; ++l) c = fmaf(yh[l], M[1][l][j], fmaf(wh[l], M[2][l][j], c));
+        wq[jj] -= c;
+      }
+    }
+    if (Wout) {
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) Wout[r * 32 + 8 * q + jj] = wq[jj];
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      y[j] = 0.f;
-      w[j] = 0.f;
+    for (int jj = 0; jj < 8; ++jj) {
+      yq[jj] = 0.f;
+      wq[jj] = 0.f;
     }
   }
-  uint4* xo = Xp + (r >> 5) * kUpdTile + (r & 31);
-  uint4* yo = Yp + (r >> 5) * kUpdTile + (r & 31);
+  if (r < row_off) return;
+  const int64_t pr = r - row_off;
+  const int tile = 3 * ks * 64;
+  uint4* xo = Xp + (pr >> 5) * tile + (pr & 31);
+  uint4* yo = Yp + (pr >> 5) * tile + (pr & 31);
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {  // chunk c: k = 8 c .. 8 c + 7 (s = c / 2, half = c % 2)
-    const float* src = c < 4 ? &y[8 * c] : &w[8 * (c - 4)];    // [Y W]
-    const float* srb = c < 4 ? &w[8 * c] : &y[8 * (c - 4)];    // [W Y]
+  for (int part = 0; part < 2; ++part) {  // chunk q of Y (part 0) and of W (part 1)
+    const float* src = part == 0 ? yq : wq;  // [Y W]
+    const float* srb = part == 0 ? wq : yq;  // [W Y]
+    const int cc = part == 0 ? cy + q : cw + q;
     uint4 h, mm, l, hb, mb, lb;
     split3(-src[0], -src[1], h.x, mm.x, l.x);
     split3(-src[2], -src[3], h.y, mm.y, l.y);
@@ -762,23 +861,52 @@ __global__ __launch_bounds__(kThr) void w_kernel(const float* __restrict__ Mg, c
     split3(srb[2], srb[3], hb.y, mb.y, lb.y);
     split3(srb[4], srb[5], hb.z, mb.z, lb.z);
     split3(srb[6], srb[7], hb.w, mb.w, lb.w);
-    const int off = (c >> 1) * 64 + (c & 1) * 32;
+    const int off = (cc >> 1) * 64 + (cc & 1) * 32;
     xo[off] = h;
-    xo[256 + off] = mm;
-    xo[512 + off] = l;
+    xo[ks * 64 + off] = mm;
+    xo[2 * ks * 64 + off] = l;
     yo[off] = hb;
-    yo[256 + off] = mb;
-    yo[512 + off] = lb;
+    yo[ks * 64 + off] = mb;
+    yo[2 * ks * 64 + off] = lb;
   }
+}
+
+// The first panel of a pair updates the second panel's columns before that panel is factorised:
+// A22[r][c] -= sum_k Y[r][k] W[c][k] + W[r][k] Y[c][k] for rows r < m, columns c < 32 (fp32; the rest
+// of A22 takes this panel's update together with the second panel's).  8 rows per work-group.
+__global__ __launch_bounds__(kThr) void colblock_kernel(float* __restrict__ A22, int64_t lda, int64_t m,
+                                                        const float* __restrict__ Y, const float* __restrict__ W) {
+  __shared__ float sYc[32][33], sWc[32][33], sYr[8][33], sWr[8][33];
+  const int t = threadIdx.x, rr = t >> 5, c = t & 31;
+  const int64_t r0 = (int64_t)blockIdx.x * 8;
+  for (int e = t; e < 1024; e += kThr) {
+    const int i = e >> 5, j = e & 31;
+    sYc[i][j] = i < m ? Y[i * 32 + j] : 0.f;
+    sWc[i][j] = i < m ? W[i * 32 + j] : 0.f;
+  }
+  {
+    const int64_t r = r0 + rr;
+    sYr[rr][c] = r < m ? Y[r * 32 + c] : 0.f;
+    sWr[rr][c] = r < m ? W[r * 32 + c] : 0.f;
+  }
+  __syncthreads();
+  const int64_t r = r0 + rr;
+  if (r >= m || c >= m) return;
+  float a = 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) a = fmaf(sYr[rr][k], sWc[c][k], fmaf(sWr[rr][k], sYc[c][k], a));
+  A22[r * lda + c] -= a;
 }
 
 // A22 += (-[Y W]) [W Y]^T on every 128 x 128 tile (ti, tj) with tj <= ti (the lower triangle and
 // whole diagonal tiles; entries above the diagonal are never read).  One work-group per tile
 // (triangular index), wave (wr, wc) owns the 64 x 64 quarter (two by two 32 x 32 MFMA tiles): the
-// fp32 tile is loaded straight into the accumulators, then K = 64 in four 16-k steps of six bf16
-// plane products, then stored.
+// fp32 tile is loaded straight into the accumulators, then K = 16 KS (64 for one panel, 128 for a
+// pair) in 16-k steps of six bf16 plane products, then stored.
+template <int KS>
 __global__ __launch_bounds__(kThr) void syr2k_x6_kernel(const uint4* __restrict__ Xp, const uint4* __restrict__ Yp,
                                                         float* __restrict__ A, int64_t lda, int64_t m) {
+  constexpr int kTile = 3 * KS * 64;  // uint4 per 32-row tile of a packed operand
   const int64_t b = blockIdx.x;
   int64_t ti = (int64_t)((sqrt(8.0 * (double)b + 1.0) - 1.0) * 0.5);
   while ((ti + 1) * (ti + 2) / 2 <= b) ++ti;
@@ -800,17 +928,17 @@ __global__ __launch_bounds__(kThr) void syr2k_x6_kernel(const uint4* __restrict_
         acc[x][y][v] = (r < m && c < m) ? A[r * lda + c] : 0.f;
       }
     }
-  const uint4* xa = Xp + (R0 >> 5) * kUpdTile + lane;
-  const uint4* yb = Yp + (C0 >> 5) * kUpdTile + lane;
+  const uint4* xa = Xp + (R0 >> 5) * kTile + lane;
+  const uint4* yb = Yp + (C0 >> 5) * kTile + lane;
 #pragma unroll
-  for (int st = 0; st < 4; ++st) {
+  for (int st = 0; st < KS; ++st) {
     bf16x8 av[2][3], bv[2][3];
 #pragma unroll
     for (int x = 0; x < 2; ++x)
 #pragma unroll
       for (int p = 0; p < 3; ++p) {
-        av[x][p] = __builtin_bit_cast(bf16x8, xa[x * kUpdTile + (p * 4 + st) * 64]);
-        bv[x][p] = __builtin_bit_cast(bf16x8, yb[x * kUpdTile + (p * 4 + st) * 64]);
+        av[x][p] = __builtin_bit_cast(bf16x8, xa[x * kTile + (p * KS + st) * 64]);
+        bv[x][p] = __builtin_bit_cast(bf16x8, yb[x * kTile + (p * KS + st) * 64]);
       }
 #pragma unroll
     for (int x = 0; x < 2; ++x)
@@ -1687,9 +1815,12 @@ Layout layout(int64_t n) {
   L.BP = take((n + 255) / 256 * 256 * 32);  // B = Y T packed for xsym_kernel, zero rows to 256
   L.X = take(n * 32);
   L.T = take(32 * 32);
-  L.Gp = take(64 * 1024);
-  L.Xop = take((n + 127) / 128 * 4 * kUpdTile * 4);  // packed update operands (uint4 = 4 floats)
-  L.Yop = take((n + 127) / 128 * 4 * kUpdTile * 4);
+  L.Gp = take(64 * 1024 * 3);
+  L.Xop = take((n + 127) / 128 * 4 * (3 * 8 * 64) * 4);  // packed update operands, K <= 128 (uint4 = 4 floats)
+  L.Yop = take((n + 127) / 128 * 4 * (3 * 8 * 64) * 4);
+  L.Y2 = take(n * 32);   // Y of the odd panels (the first panel's Y of a pair stays in Y)
+  L.Wf = take(n * 32);   // W of the first panel of a pair (fp32)
+  L.G12 = take(2048);    // the pair correction's G1, G2
   L.M = take(32 * 32);
   L.px_floats = (n + 255) / 256 * n * 32;  // partial slots of X = A22 (Y T): one per tile row
   L.Px = take(L.px_floats);
@@ -1751,8 +1882,12 @@ int sy2sb(int64_t n, float* A, int64_t lda, float* tau, float* ws, const Layout&
                        ws + L.E, m, ws + L.Q1, fb);
     MPQ_LAUNCH_CHECK();
     const unsigned rblocks = (unsigned)((m + kThr - 1) / kThr);
+    // panels go in pairs (even panel first) sharing one trailing update; a last even panel goes alone
+    const bool second = (pidx & 1) != 0;
+    const bool first = !second && c0 + 2 * kBW < n;
+    float* Ycur = second ? ws + L.Y2 : ws + L.Y;
     hipLaunchKernelGGL(hr_kernel, dim3(rblocks), dim3(kThr), 0, stream, ws + L.Q1, Rc, fb, ws + L.Rroot, m, A, lda,
-                       r0, c0, ws + L.Y, ws + L.BP, ws + L.T, tau);
+                       r0, c0, Ycur, ws + L.BP, ws + L.T, tau);
     MPQ_LAUNCH_CHECK();
     float* A22 = A + r0 * lda + r0;
     // X = A22 (Y T): one partial slot per tile of the lower triangle's tile row / column, summed in
@@ -1778,22 +1913,43 @@ int sy2sb(int64_t n, float* A, int64_t lda, float* tau, float* ws, const Layout&
     const int64_t ng = std::min<int64_t>(64, (m + 63) / 64);
     const int64_t chunk = ((m + ng - 1) / ng + 63) / 64 * 64;
     const int64_t ngu = (m + chunk - 1) / chunk;
-    hipLaunchKernelGGL(gram_partial_kernel, dim3((unsigned)ngu), dim3(kThr), 0, stream, ws + L.Y, ws + L.X, m, chunk,
-                       ws + L.Gp);
+    // the first panel's Y and W from this panel's first row (the second panel of a pair)
+    const float* Yh = second ? ws + L.Y + 32 * 32 : nullptr;
+    const float* Wh = second ? ws + L.Wf + 32 * 32 : nullptr;
+    hipLaunchKernelGGL(gram_partial_kernel, dim3((unsigned)ngu), dim3(kThr), 0, stream, Ycur, ws + L.X, m, chunk,
+                       ws + L.Gp, Yh, Wh);
     MPQ_LAUNCH_CHECK();
-    hipLaunchKernelGGL(m_kernel, dim3(1), dim3(1024), 0, stream, ws + L.Gp, (int)ngu, ws + L.T, ws + L.M);
+    hipLaunchKernelGGL(m_kernel, dim3(1), dim3(1024), 0, stream, ws + L.Gp, (int)ngu, second ? 3 : 1, ws + L.T,
+                       ws + L.M, ws + L.G12);
     MPQ_LAUNCH_CHECK();
-    const int64_t m128 = (m + 127) / 128 * 128;
     uint4* Xp = reinterpret_cast<uint4*>(ws + L.Xop);
     uint4* Yp = reinterpret_cast<uint4*>(ws + L.Yop);
-    hipLaunchKernelGGL(w_kernel, dim3((unsigned)(m128 / kThr + (m128 % kThr ? 1 : 0))), dim3(kThr), 0, stream,
-                       ws + L.M, ws + L.Y, ws + L.X, m, Xp, Yp);
+    const int ks = (first || second) ? 8 : 4;
+    const int cy = second ? 4 : 0, cw = first ? 8 : (second ? 12 : 4);
+    const int row_off = first ? 32 : 0;
+    const int64_t wrows = row_off + (m - row_off + 127) / 128 * 128;
+    hipLaunchKernelGGL(w_kernel, dim3((unsigned)((4 * wrows + kThr - 1) / kThr)), dim3(kThr), 0, stream, ws + L.M, Ycur,
+                       ws + L.X, m, Xp, Yp, ks, cy, cw, row_off, first ? ws + L.Wf : nullptr, Yh, Wh,
+                       second ? ws + L.G12 : nullptr);
     MPQ_LAUNCH_CHECK();
-    // A22 -= Y W^T + W Y^T on the lower triangle and whole diagonal tiles
-    const int64_t nt = m128 / 128;
-    hipLaunchKernelGGL(syr2k_x6_kernel, dim3((unsigned)(nt * (nt + 1) / 2)), dim3(kThr), 0, stream, Xp, Yp, A22,
-                       lda, m);
-    MPQ_LAUNCH_CHECK();
+    if (first) {
+      // the second panel's columns now; the rest of A22 with the second panel's update
+      hipLaunchKernelGGL(colblock_kernel, dim3((unsigned)((m + 7) / 8)), dim3(kThr), 0, stream, A22, lda, m, Ycur,
+                         ws + L.Wf);
+      MPQ_LAUNCH_CHECK();
+    } else {
+      // A22 -= Y W^T + W Y^T on the lower triangle and whole diagonal tiles (with the first panel's
+      // part for the second panel of a pair)
+      const int64_t m128 = (m + 127) / 128 * 128;
+      const int64_t nt = m128 / 128;
+      if (second)
+        hipLaunchKernelGGL(syr2k_x6_kernel<8>, dim3((unsigned)(nt * (nt + 1) / 2)), dim3(kThr), 0, stream, Xp, Yp,
+                           A22, lda, m);
+      else
+        hipLaunchKernelGGL(syr2k_x6_kernel<4>, dim3((unsigned)(nt * (nt + 1) / 2)), dim3(kThr), 0, stream, Xp, Yp,
+                           A22, lda, m);
+      MPQ_LAUNCH_CHECK();
+    }
   }
   return kOk;
 }
