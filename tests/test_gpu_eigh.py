@@ -37,6 +37,37 @@ def test_syevd_matches_fp64(gpu, n, method):
     assert orth <= max(2.0 * orth_t, 2e-5), (orth, orth_t)
 
 
+def test_syevd_two_stage_8192(gpu):
+    """Two-stage path (the automatic choice from n = 8192) at a size where stage 1 runs in panel pairs
+    with 256-row X tiles (255 panels: 127 pairs and a last panel alone) and Q1 in block pairs (64
+    blocks of 128 reflectors): eigenvalues against fp64 eigvalsh, residual and orthogonality against
+    torch's fp32 eigh, all on the GPU (H = X^T X / 2n with log-normal channel scales)."""
+    n = 8192
+    g = torch.Generator(device=gpu).manual_seed(8192)
+    c = torch.exp(torch.randn(n, generator=g, device=gpu))
+    X = torch.randn(2 * n, n, generator=g, device=gpu) * c
+    H = X.T @ X / (2 * n)
+    del X
+    H = 0.5 * (H + H.T)
+    lam, V = ops.syevd(H)
+    ref = torch.linalg.eigvalsh(H.double())
+    scale = float(ref.abs().max())
+    assert float((lam.double() - ref).abs().max()) <= 2e-5 * scale
+    assert bool((lam[1:] >= lam[:-1]).all())
+
+    def quality(lv, Vv):
+        Hd, Vd = H.double(), Vv.double()
+        resid = float((Hd @ Vd - Vd * lv.double().unsqueeze(0)).norm() / Hd.norm())
+        orth = float((Vd.T @ Vd - torch.eye(n, dtype=torch.float64, device=gpu)).abs().max())
+        return resid, orth
+
+    resid, orth = quality(lam, V)
+    lt, Vt = torch.linalg.eigh(H)
+    resid_t, orth_t = quality(lt, Vt)
+    assert resid <= max(2.0 * resid_t, 1e-5), (resid, resid_t)
+    assert orth <= max(2.0 * orth_t, 2e-5), (orth, orth_t)
+
+
 def test_syevd_large_remainder_paths(gpu):
     # n = 17000: the first trailing matrices exceed the tridiagonalisation kernels' fixed load
     # batches (over 512 norm partials, 8192 symv partials and 256 column strips), so their
