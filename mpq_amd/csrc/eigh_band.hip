@@ -309,8 +309,13 @@ __device__ void cq_cholesky(double (*G)[33], int pass, int64_t m, int* bad) {
   for (int i = 0; i < 32; ++i) {
     const double d = readlane_f64(row[i], i);
     ok = ok && d > 0.0 && (pass != 3 || (d > 0.5 && d < 2.0));
-    const double lii = sqrt(ok ? d : 1.0);
-    const double inv = 1.0 / lii;
+    // 1 / sqrt by the hardware estimate (v_rsq_f64, ~2^-28) and two Newton steps (full precision),
+    // a shorter latency chain than sqrt followed by a division
+    const double dd = ok ? d : 1.0;
+    double inv = __builtin_amdgcn_rsq(dd);
+    inv = inv * fma(-0.5 * dd, inv * inv, 1.5);
+    inv = inv * fma(-0.5 * dd, inv * inv, 1.5);
+    const double lii = dd * inv;
     const double lti = row[i] * inv;  // L[t][i] for t > i
     if (t == i) row[i] = lii;
     else if (t > i) row[i] = lti;
@@ -537,6 +542,7 @@ __global__ __launch_bounds__(kThr) void hr_kernel(const float* __restrict__ Q1, 
   __shared__ float Xi[32][33];  // L1^-T
   __shared__ float Ts[32][33];
   __shared__ float S[32];
+  __shared__ float Uinv[32];  // 1 / U[j][j]
   __shared__ double sR[32][33];
   __shared__ double sRinv[32];
   const int kk = (int)min<int64_t>(m, 32);
@@ -612,6 +618,7 @@ __global__ __launch_bounds__(kThr) void hr_kernel(const float* __restrict__ Q1, 
       for (int l = i; l <= j; ++l) acc = fmaf(LU[i][l] * S[l], Xi[l][j], acc);
     Ts[i][j] = -acc;
   }
+  if (t < 32) Uinv[t] = t < kk ? 1.0f / LU[t][t] : 0.f;
   __syncthreads();
   const int64_t r = (int64_t)blockIdx.x * kThr + t;
   if (r < m) {
@@ -626,7 +633,7 @@ __global__ __launch_bounds__(kThr) void hr_kernel(const float* __restrict__ Q1, 
       for (int j = 0; j < 32; ++j) {
         float acc = j < kk ? q[j] : 0.f;
         for (int i = 0; i < j; ++i) acc = fmaf(-y[i], LU[i][j], acc);
-        y[j] = j < kk ? acc / LU[j][j] : 0.f;
+        y[j] = j < kk ? acc * Uinv[j] : 0.f;
       }
     }
 #pragma unroll
