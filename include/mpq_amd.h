@@ -38,6 +38,15 @@ const char* mpq_last_error(void);
 int mpq_last_error_code(void);
 void mpq_clear_error(void);
 
+/*
+ * Frees the calling thread's pinned host buffers (the VAMP drivers' status mailboxes and the
+ * eigensolver's staging buffers); a later call that needs one allocates it again.  Waits for the
+ * device to finish first.  No counterpart in the reference (its torch calls keep no such state);
+ * the Python binding calls it at interpreter exit so that no library allocation outlives the
+ * HIP runtime's teardown.
+ */
+int mpq_release_thread_resources(void);
+
 /* ------------------------------------------------------------------------ */
 /* E8P12 lattice codebook                                                   */
 /* ------------------------------------------------------------------------ */
@@ -211,6 +220,18 @@ int mpq_gemm_f32(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, c
                  mpq_stream_t stream);
 
 /*
+ * C = alpha * A op(B) + beta * C in fp64 on the fp64 matrix cores (v_mfma_f64_16x16x4_f64, 128 x 64
+ * tiles, split-K partials summed in a fixed order when `workspace` holds
+ * mpq_gemm_f64_workspace_size(M, N, K) bytes; NULL runs the product unsplit).  The products of
+ * mpq_syevd_f64, i.e. of the float64 torch.linalg.eigh in mpq/adapters/quip_sharp.py:54; exported
+ * for testing the kernel on its own.
+ */
+int64_t mpq_gemm_f64_workspace_size(int64_t M, int64_t N, int64_t K);
+int mpq_gemm_f64(int64_t M, int64_t N, int64_t K, const double* A, int64_t lda, const double* B, int64_t ldb,
+                 int trans_b, double* C, int64_t ldc, double alpha, double beta, double* workspace,
+                 int64_t workspace_bytes, mpq_stream_t stream);
+
+/*
  * Split-K partial products P[s] = A[:, Ks] op(B)[Ks, :], s = 0..splits-1, written to
  * `partials` (splits x M x N, M*N apart): the kernel the VAMP drivers run for their rank-space
  * products, whose epilogues sum the partials in split order (callers that fuse their own
@@ -278,8 +299,8 @@ int mpq_eigh_postprocess(const float* lam_asc, const float* V_asc, int64_t n, fl
  * Blocked Householder tridiagonalisation, divide and conquer on the tridiagonal matrix (fp64
  * secular equations and Loewner vectors, merge products on the fp32 MFMA GEMM), then the
  * back-transformation V = Q Z as blocked compact-WY updates on the same GEMM; all on this
- * library's kernels.  workspace: mpq_syevd_workspace_size(n) bytes (about 24 n^2; rocBLAS may
- * also use its handle's device memory).  Synchronises `stream` once per tridiagonal merge of more
+ * library's kernels.  workspace: mpq_syevd_workspace_size(n) bytes (about 24 n^2 below n = 8192,
+ * about 40 n^2 from there).  Synchronises `stream` once per tridiagonal merge of more
  * than 512 rows and once at the end.
  */
 int64_t mpq_syevd_workspace_size(int64_t n);
@@ -302,9 +323,9 @@ int mpq_syevd_method(int64_t n, const float* H, float* lam, float* V, void* work
 
 /*
  * The same decomposition in fp64 (the torch.linalg.eigh of the float64 Hessian in
- * mpq/adapters/quip_sharp.py:33-67): the same kernels in double (divide-and-conquer tolerances
- * at fp64 unit roundoff), with the trailing updates, merge products and back-transformation on
- * rocBLAS dgemm.
+ * mpq/adapters/quip_sharp.py:33-67): the one-stage kernels in double (divide-and-conquer
+ * tolerances at fp64 unit roundoff), with the trailing updates, merge products and
+ * back-transformation on the fp64 matrix cores (mpq_gemm_f64's kernel).
  * workspace: mpq_syevd_f64_workspace_size(n) bytes.
  */
 int64_t mpq_syevd_f64_workspace_size(int64_t n);
@@ -534,6 +555,71 @@ int mpq_uniform_cd_sweeps(int64_t rows, int64_t n, int maxq, int64_t block_rows,
                           int32_t* accepted, const float* scale, const float* zero,
                           int64_t group_size, const float* diag, const float* H, void* workspace,
                           int64_t workspace_bytes, mpq_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Generic rank-space block coordinate descent                              */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * The device steps of mpq/polish/block_cd.py:332-625 (block_coordinate_descent_rankspace) for a
+ * caller-driven block loop with any candidate provider; blocks of 1 <= block_size <= 16 columns.
+ * mpq_bcd_prepare: per block b of the n x R matrix Vs, the gram G_b = Vs_b Vs_b^T (gram, nb x bs x
+ * bs), for metric_gram the Cholesky factor with the reference's diagonal-jitter retries
+ * (stabilize_cholesky, mpq/linear.py:121-141; chol, lower) and (L L^T)^-1 (ginv), otherwise ginv[b]
+ * holds 1 / max(G_ii, 1e-12); importance[b] = trace(G_b) (:398-420); status[b] = 1 where every
+ * Cholesky retry failed.
+ * mpq_bcd_gain: the greedy gain of every block from rhs = residual_u Vs^T (rows x n)
+ * (_batched_greedy_gain, :286-306).
+ * mpq_bcd_target: target = x_blk + rhs G^-1 (gram) or x_blk + rhs diag_inv (diag) (:581-585).
+ * mpq_bcd_accept: the accept test and state update of one block (_cd_accept_step_impl :28-42 and
+ * :600-611): x, res_norm, accepted, the block's column of idx (when given) in place; delta gets the
+ * accepted moves for residual_u -= delta Vs_blk.
+ */
+int mpq_bcd_prepare(int64_t n, int64_t R, int block_size, int metric_gram, const float* Vs, float* gram,
+                    float* chol, float* ginv, float* importance, int32_t* status, mpq_stream_t stream);
+int mpq_bcd_gain(int64_t rows, int64_t n, int block_size, int metric_gram, const float* rhs, const float* ginv,
+                 float* gain, mpq_stream_t stream);
+int mpq_bcd_target(int64_t rows, int64_t n, int block_size, int64_t block, int metric_gram, const float* x,
+                   const float* rhs, const float* ginv, float* target, mpq_stream_t stream);
+int mpq_bcd_accept(int64_t rows, int64_t n, int block_size, int64_t block, const float* cand, const float* rhs,
+                   const float* gram, float accept_tol, const int64_t* cand_idx, float* x, float* res_norm,
+                   int64_t* idx, int32_t* accepted, float* delta, mpq_stream_t stream);
+
+/*
+ * Candidate providers of mpq/polish/block_cd.py:628-861 on the device.
+ * mpq_bcd_uniform_propose: UniformScalarProvider (:628-653), column `col` of the expanded
+ * scale / zero (rows x n): q = clamp(round(target / s + z), 0, maxq), value s (q - z).
+ * mpq_bcd_topk_scalar_propose: UniformTopKProvider (:656-682): the nearest of the k candidates
+ * vals_k[r, col, :] (rows x n x k; first on ties) and its level from q_k (nullable; -1 then).
+ * mpq_e8p12_metric_argmin: E8P12Provider with the gram metric (_metric_map_assign, :702-739): per
+ * row of target (rows x 8) the codeword minimising |(t - c) L|^2 over all 65536 codewords of the
+ * build's table, first index on ties; workspace mpq_e8p12_metric_argmin_workspace_size(rows) bytes.
+ * mpq_bcd_e8_topk_propose: E8P12TopKProvider (:778-861): the nearest of topk_idx[r, block, :]
+ * (rows x nb x k codeword indices) to the target, whitened by chol (8 x 8, nullable: plain distance).
+ */
+int mpq_bcd_uniform_propose(int64_t rows, int64_t n, int64_t col, int maxq, const float* target,
+                            const float* scale, const float* zero, float* vals, int64_t* q, mpq_stream_t stream);
+int mpq_bcd_topk_scalar_propose(int64_t rows, int64_t n, int64_t col, int64_t k, const float* target,
+                                const float* vals_k, const int64_t* q_k, float* vals, int64_t* q,
+                                mpq_stream_t stream);
+int64_t mpq_e8p12_metric_argmin_workspace_size(int64_t rows);
+int mpq_e8p12_metric_argmin(int64_t rows, const float* target, const float* chol, float* vals, int64_t* idx,
+                            void* workspace, int64_t workspace_bytes, mpq_stream_t stream);
+int mpq_bcd_e8_topk_propose(int64_t rows, int64_t nb, int64_t block, int64_t k, const int64_t* topk_idx,
+                            const float* target, const float* chol, float* vals, int64_t* idx,
+                            mpq_stream_t stream);
+
+/*
+ * mpq_uniform_cd_sweeps with the RTN target formed as x + rhs * (1 / diag), the rule of the
+ * reference's torch update loop (mpq/polish/triton_scalar_cd.py:258-288, target at :266, the
+ * default update_backend="torch"); mpq_uniform_cd_sweeps forms x + rhs / diag like its sweep kernel
+ * (:73).  Same arguments and workspace as mpq_uniform_cd_sweeps.
+ */
+int mpq_uniform_cd_sweeps_recip(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                                float accept_tol, float* rhs, float* x, uint8_t* q, float* res_norm,
+                                int32_t* accepted, const float* scale, const float* zero,
+                                int64_t group_size, const float* diag, const float* H, void* workspace,
+                                int64_t workspace_bytes, mpq_stream_t stream);
 
 /*
  * mpq_uniform_cd_sweeps without a workspace argument and without any device

@@ -7,6 +7,7 @@ call is asynchronous on the given HIP stream (default: torch's current stream).
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 import os
 import threading
@@ -46,6 +47,20 @@ SIGNATURES = {
     "mpq_gemm_f32": (c_int, [c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_int, c_ptr,
                              c_ptr, c_i64, c_float, c_float, c_ptr, c_i64, c_ptr]),
     "mpq_gemm_f32_split_count": (c_int, [c_i64, c_i64, c_i64]),
+    "mpq_gemm_f64_workspace_size": (c_i64, [c_i64, c_i64, c_i64]),
+    "mpq_gemm_f64": (c_int, [c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_int, c_ptr, c_i64, c_double,
+                             c_double, c_ptr, c_i64, c_ptr]),
+    "mpq_release_thread_resources": (c_int, []),
+    "mpq_bcd_prepare": (c_int, [c_i64, c_i64, c_int, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "mpq_bcd_gain": (c_int, [c_i64, c_i64, c_int, c_int, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "mpq_bcd_target": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "mpq_bcd_accept": (c_int, [c_i64, c_i64, c_int, c_i64, c_ptr, c_ptr, c_ptr, c_float, c_ptr, c_ptr, c_ptr,
+                               c_ptr, c_ptr, c_ptr, c_ptr]),
+    "mpq_bcd_uniform_propose": (c_int, [c_i64, c_i64, c_i64, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "mpq_bcd_topk_scalar_propose": (c_int, [c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "mpq_e8p12_metric_argmin_workspace_size": (c_i64, [c_i64]),
+    "mpq_e8p12_metric_argmin": (c_int, [c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
+    "mpq_bcd_e8_topk_propose": (c_int, [c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
     "mpq_gemm_f32_splitk": (c_int, [c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_int, c_ptr, c_int, c_ptr]),
     "mpq_gptq_find_params": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_ptr, c_ptr]),
     "mpq_uniform_rtn": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_int, c_ptr, c_ptr,
@@ -97,6 +112,8 @@ SIGNATURES = {
     "mpq_uniform_cd_sweeps_workspace_size": (c_i64, [c_i64, c_i64, c_i64]),
     "mpq_uniform_cd_sweeps": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_float, c_ptr, c_ptr, c_ptr, c_ptr,
                                       c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
+    "mpq_uniform_cd_sweeps_recip": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_float, c_ptr, c_ptr, c_ptr, c_ptr,
+                                            c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
     "mpq_uniform_cd_sweeps_noalloc_max_bytes": (c_i64, []),
     "mpq_uniform_cd_sweeps_noalloc": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_float, c_ptr, c_ptr, c_ptr,
                                               c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_ptr]),
@@ -205,7 +222,20 @@ def load() -> ctypes.CDLL:
             fn.restype = restype
             fn.argtypes = argtypes
         _lib = lib
+        atexit.register(_release_at_exit)
         return lib
+
+
+def _release_at_exit() -> None:
+    """Free this thread's pinned host buffers (status mailboxes, staging) while the HIP runtime is
+    still up: the library's thread-lifetime allocations are not left to process teardown."""
+    lib = _lib
+    if lib is None:
+        return
+    try:
+        lib.mpq_release_thread_resources()
+    except Exception:  # the interpreter is shutting down; nothing to report to
+        pass
 
 
 def exported_symbols() -> list:

@@ -15,9 +15,10 @@ Drop-in for the reference's ``mpq/adapters/quip_sharp.py`` entry point
 * the exact surrogate audits ``(Wr - hat) Hr (Wr - hat)^T`` per row block against the
   LDLQ result (:70-117, :805-818).
 
-Supported solver combinations: ``vamp`` (polish ``block_cd`` or ``none``) and ``ldlq``
-(polish ``block_cd`` or ``none``).  The reference's baseline solvers (cdquant, quantease,
-ojbkq) and the top-k polish are outside this build and raise ``ValueError``.
+Supported solver combinations: ``vamp`` (polish ``block_cd`` or ``none``, metric ``gram`` or
+``diag``) and ``ldlq`` (polish ``block_cd`` or ``none``).  The reference's baseline solvers (cdquant,
+quantease, ojbkq) and the top-k polish (whose candidates come from the solver's top-k posterior) are
+outside this build and raise ``ValueError``.
 """
 from __future__ import annotations
 
@@ -299,16 +300,30 @@ def mpq_refine_codebook(
     _resolve_e8p12_polish_metric(str(getattr(args, "mpq_polish_metric", vamp_cfg.polish_metric)))
     polish_updates = 0.0
     changed = 0
-    if polish_mode == "block_cd":
-        if _resolve_e8p12_polish_metric(str(getattr(args, "mpq_polish_metric", "gram"))) != "gram":
-            raise ValueError("mpq_amd implements polish_metric='gram' (the recipe default); 'diag' is not provided.")
+    max_blocks = int(getattr(args, "mpq_polish_max_blocks", vamp_cfg.polish_max_blocks) or 0)
+    if polish_mode == "block_cd" and _resolve_e8p12_polish_metric(
+            str(getattr(args, "mpq_polish_metric", "gram"))) == "gram":
         ctx = ops.e8p12_cd_prepare(Vs)
-        x_p, idx_p, _, _, acc = ops.e8p12_cd_polish(
-            final_hat, final_idx, Vs, ctx, sweeps=sweeps, block_rows=block_rows, W=Wr,
-            max_blocks=int(getattr(args, "mpq_polish_max_blocks", vamp_cfg.polish_max_blocks) or 0))
+        x_p, idx_p, _, _, acc = ops.e8p12_cd_polish(final_hat, final_idx, Vs, ctx, sweeps=sweeps,
+                                                    block_rows=block_rows, W=Wr, max_blocks=max_blocks)
         changed = int((idx_p != final_idx).sum().item())
         final_hat, final_idx = x_p, idx_p
         polish_updates = float(acc.sum().item())
+    elif polish_mode == "block_cd":
+        # the diag metric: the generic block CD with the codebook's nearest codeword, per row block
+        from ..solver import polish_e8p12_rankspace
+
+        before = final_idx.clone()
+        for r0 in range(0, m, block_rows):
+            r1 = min(m, r0 + block_rows)
+            Yu_b = ops.gemm(Wr[r0:r1].contiguous(), Vs)
+            x_b, i_b, _, st_b = polish_e8p12_rankspace(
+                x_init=final_hat[r0:r1].contiguous(), idxs_init=final_idx[r0:r1].contiguous(), Y_u=Yu_b, Vs=Vs,
+                cb=cb, sweeps=sweeps, polish_mode="block_cd", polish_metric="diag", polish_max_blocks=max_blocks)
+            final_hat[r0:r1] = x_b
+            final_idx[r0:r1] = i_b
+            polish_updates += float(st_b.get("accepted_updates", 0.0))
+        changed = int((final_idx != before).sum().item())
     torch.cuda.synchronize(device)
     timings["polish_s"] = time.time() - t0
 

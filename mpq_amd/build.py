@@ -26,17 +26,18 @@ BUILD_DIR = os.path.join(HERE, "_build")
 LIB_NAME = "libmpq_amd.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
-ROCM_LIB = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
 
 HIP_SOURCES = [
     "e8p12_map.hip",
     "e8p12_posterior.hip",
     "gemm.hip",
+    "gemm_f64.hip",
     "elementwise.hip",
     "uniform_vamp.hip",
     "e8p12_vamp.hip",
     "cd_uniform.hip",
     "e8p12_cd.hip",
+    "block_cd.hip",
     "gptq_pack.hip",
     "hessian.hip",
     "awq.hip",
@@ -47,6 +48,7 @@ HIP_SOURCES = [
 ]
 CXX_SOURCES = [
     "errors.cpp",
+    "resources.cpp",
 ]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -107,8 +109,7 @@ def build(verbose: bool = False, jobs: int = 8) -> str:
             if verbose and out:
                 print(out)
     tmp = LIB_PATH + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-L", ROCM_LIB,
-          "-Wl,-rpath," + ROCM_LIB, "-lrocblas"])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     shutil.move(tmp, LIB_PATH)
     return LIB_PATH
 

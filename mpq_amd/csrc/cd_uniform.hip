@@ -7,7 +7,8 @@
 // Semantics per row block (block_rows rows sharing one greedy order):
 //   residual_u = Yu - x Vs, rhs = residual_u Vs^T, diag_j = |Vs_j|^2 (>= 1e-12)
 //   per sweep: gain_j = mean_rows(rhs_j^2 / diag_j), order = stable argsort(-gain)
-//   per column (in order): target = x + rhs/diag, q = clamp(rint(target/s + z)),
+//   per column (in order): target = x + rhs/diag (the sweep kernel's rule; mpq_uniform_cd_sweeps_recip
+//     takes the torch loop's x + rhs * (1/diag), :266), q = clamp(rint(target/s + z)),
 //     accept iff res + d^2 diag - 2 rhs d + 1e-12 < res (1 + tol),
 //     rhs -= d * H[col, :]
 // Blocking: columns are taken in windows of 128 consecutive positions of the
@@ -18,7 +19,8 @@
 // order, runs on the VALU as a sequential multiply-then-subtract chain per
 // entry (schur_valu_kernel), which is exactly the per-column update order and
 // rounding of the reference's sweep (its torch twin,
-// mpq/polish/triton_scalar_cd.py:258-288).  Steps whose delta is zero for
+// mpq/polish/triton_scalar_cd.py:258-288; that loop forms the target with the reciprocal of diag,
+// which the _recip entry point reproduces).  Steps whose delta is zero for
 // every row of a 16-row tile are skipped (subtracting 0 * h leaves rhs as is).
 // The greedy gain is summed over the block's rows in row order.  From the same
 // rhs, x, codes and residual norms, a sweep here is bit-identical to the
@@ -80,8 +82,8 @@ __global__ __launch_bounds__(64 * kRowsPerWG) void window_kernel(
     int64_t rows, int64_t n, int64_t block_rows, int maxq, float accept_tol,
     const int32_t* __restrict__ order, int64_t w0, int wn, const float* __restrict__ T,
     const float* __restrict__ scale, const float* __restrict__ zero, int64_t G, int64_t gs,
-    const float* __restrict__ diag, float* __restrict__ rhs, float* __restrict__ x,
-    uint8_t* __restrict__ q, float* __restrict__ res_norm, float* __restrict__ delta,
+    const float* __restrict__ diag, const float* __restrict__ diag_inv, int recip, float* __restrict__ rhs,
+    float* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ res_norm, float* __restrict__ delta,
     int* __restrict__ accepted) {
   __shared__ float Ts[kWin * kWin];
   const int64_t blk = blockIdx.y;
@@ -107,6 +109,7 @@ __global__ __launch_bounds__(64 * kRowsPerWG) void window_kernel(
   s1 = s1 < 1e-12f ? 1e-12f : s1;
   const float z0 = v0 ? zero[row * G + c0 / gs] : 0.f, z1 = v1 ? zero[row * G + c1 / gs] : 0.f;
   const float dg0 = v0 ? diag[c0] : 1.f, dg1 = v1 ? diag[c1] : 1.f;
+  const float di0 = v0 ? diag_inv[c0] : 1.f, di1 = v1 ? diag_inv[c1] : 1.f;
   int q0 = -1, q1 = -1;
   float d0 = 0.f, d1 = 0.f;
   float res = res_norm[row];
@@ -121,7 +124,8 @@ __global__ __launch_bounds__(64 * kRowsPerWG) void window_kernel(
     const float sp = bcast(hi ? s1 : s0, src);
     const float zp = bcast(hi ? z1 : z0, src);
     const float dp = bcast(hi ? dg1 : dg0, src);
-    const float target = xp + rp / dp;
+    // the sweep kernel's rule x + rhs / diag, or the torch loop's x + rhs * (1 / diag)
+    const float target = recip ? xp + rp * bcast(hi ? di1 : di0, src) : xp + rp / dp;
     float qf = rintf(target / sp + zp);
     qf = fmaxf(fminf(qf, (float)maxq), 0.f);
     const float xq = sp * (qf - zp);
@@ -313,7 +317,7 @@ hipError_t run_sweeps(int64_t rows, int64_t n, int maxq, int64_t block_rows, int
                       float accept_tol, const float* scale, const float* zero, int64_t G, int64_t gs,
                       const float* diag, const float* diag_inv, const float* H, float* rhs, float* x,
                       uint8_t* qw, float* res_norm, int* acc, float* gain, int32_t* order, float* T,
-                      float* delta, hipStream_t stream) {
+                      float* delta, hipStream_t stream, int recip = 0) {
   const int64_t rtiles = (block_rows + kSRows - 1) / kSRows;
   const int64_t ctiles = (n + kSCols - 1) / kSCols;
   const int64_t wgs = nblocks * rtiles * ctiles;
@@ -332,7 +336,7 @@ hipError_t run_sweeps(int64_t rows, int64_t n, int maxq, int64_t block_rows, int
       hipLaunchKernelGGL(window_kernel, dim3((unsigned)((block_rows + kRowsPerWG - 1) / kRowsPerWG),
                                              (unsigned)nblocks),
                          dim3(64 * kRowsPerWG), 0, stream, rows, n, block_rows, maxq, accept_tol, order, w0,
-                         wn, T, scale, zero, G, gs, diag, rhs, x, qw, res_norm, delta, acc);
+                         wn, T, scale, zero, G, gs, diag, diag_inv, recip, rhs, x, qw, res_norm, delta, acc);
       if (n % 4 == 0)
         hipLaunchKernelGGL(schur_valu_kernel<true>, dim3((unsigned)wgs), dim3(256), 0, stream, rows, n, block_rows,
                            rtiles, ctiles, order, w0, wn, delta, H, rhs);
@@ -573,7 +577,7 @@ namespace {
 int cd_sweeps_entry(const char* fn, int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
                     float accept_tol, float* rhs, float* x, uint8_t* q, float* res_norm, int32_t* accepted,
                     const float* scale, const float* zero, int64_t group_size, const float* diag, const float* H,
-                    void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+                    void* workspace, int64_t workspace_bytes, hipStream_t stream, int recip = 0) {
   MPQ_CHECK_ARG(rows > 0 && n > 0, "%s: empty problem", fn);
   MPQ_CHECK_ARG(maxq >= 1 && maxq <= 255, "%s: maxq must be in [1, 255]", fn);
   MPQ_CHECK_ARG(block_rows >= 1 && sweeps >= 0 && group_size >= 1, "%s: bad sizes", fn);
@@ -598,7 +602,7 @@ int cd_sweeps_entry(const char* fn, int64_t rows, int64_t n, int maxq, int64_t b
   hipLaunchKernelGGL(recip_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, n, diag, diag_inv);
   MPQ_LAUNCH_CHECK();
   MPQ_HIP_TRY(run_sweeps(rows, n, maxq, block_rows, nblocks, sweeps, accept_tol, scale, zero, G, group_size, diag,
-                         diag_inv, H, rhs, x, q, res_norm, accepted, gain, order, T, delta, stream));
+                         diag_inv, H, rhs, x, q, res_norm, accepted, gain, order, T, delta, stream, recip));
   return kOk;
 }
 
@@ -613,6 +617,16 @@ extern "C" int mpq_uniform_cd_sweeps(int64_t rows, int64_t n, int maxq, int64_t 
   return mpq::cd_sweeps_entry("mpq_uniform_cd_sweeps", rows, n, maxq, block_rows, sweeps, accept_tol, rhs, x, q,
                               res_norm, accepted, scale, zero, group_size, diag, H, workspace, workspace_bytes,
                               stream);
+}
+
+extern "C" int mpq_uniform_cd_sweeps_recip(int64_t rows, int64_t n, int maxq, int64_t block_rows, int sweeps,
+                                           float accept_tol, float* rhs, float* x, uint8_t* q, float* res_norm,
+                                           int32_t* accepted, const float* scale, const float* zero,
+                                           int64_t group_size, const float* diag, const float* H, void* workspace,
+                                           int64_t workspace_bytes, hipStream_t stream) {
+  return mpq::cd_sweeps_entry("mpq_uniform_cd_sweeps_recip", rows, n, maxq, block_rows, sweeps, accept_tol, rhs, x,
+                              q, res_norm, accepted, scale, zero, group_size, diag, H, workspace, workspace_bytes,
+                              stream, 1);
 }
 
 // ---- allocation-free variant ------------------------------------------------------------------

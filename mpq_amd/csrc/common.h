@@ -25,6 +25,11 @@ const char* last_error();
 int last_error_code();
 void set_error_code(int code);
 
+// Registers a per-thread pinned host buffer (its host pointer slot, optionally the slot of its
+// device view and of its capacity) so that mpq_release_thread_resources() frees it and clears the
+// slots; registering the same slot again is a no-op.
+void track_pinned(void** host, void** dev, size_t* cap);
+
 }  // namespace mpq
 
 #define MPQ_CHECK_ARG(cond, ...)                 \

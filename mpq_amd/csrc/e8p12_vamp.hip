@@ -69,7 +69,10 @@ E8Plan e8_plan(int64_t rows, int64_t n) {
 
 VampStatus* host_status_e8() {
   static thread_local VampStatus* h = nullptr;
-  if (!h && hipHostMalloc((void**)&h, sizeof(VampStatus), hipHostMallocDefault) != hipSuccess) h = nullptr;
+  if (!h) {
+    if (hipHostMalloc((void**)&h, sizeof(VampStatus), hipHostMallocDefault) != hipSuccess) h = nullptr;
+    else track_pinned(reinterpret_cast<void**>(&h), nullptr, nullptr);
+  }
   return h;
 }
 

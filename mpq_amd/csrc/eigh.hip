@@ -10,9 +10,10 @@
 //      trailing matrix takes the rank-64 update A -= V W^T + W V^T on the MFMA GEMM;
 //   2. divide and conquer on the tridiagonal matrix (stedc.hip): T = Z^T diag(lam) Z, eigenvalues
 //      ascending, Z row-major with row k = eigenvector k;
-//   3. back-transformation V = Q Z on fp32 MFMA GEMMs: the reflectors are applied in blocks of
-//      kNB as compact-WY factors I - Y Tb Y^T (Tb from the block's gram Y^T Y, LAPACK larft
-//      forward/columnwise), last block first.
+//   3. back-transformation V = Q Z: the reflectors are applied in blocks of kNB (fp64: kNB / 2) as
+//      compact-WY factors I - Y Tb Y^T (Tb from the block's gram Y^T Y, LAPACK larft
+//      forward/columnwise), last block first; fp32 on bf16-plane products (wy_x6.hip), fp64 on the
+//      fp64 matrix cores (gemm_f64.hip).
 // Output: lam ascending (n), V (n x n, row-major, column k = eigenvector k), as torch.linalg.eigh.
 //
 // Storage: the symmetric matrix sits in a zero-padded row-major buffer with leading dimension
@@ -22,17 +23,17 @@
 // Reflector i (LAPACK's H(i) = I - tau_i v_i v_i^T, v_i[0..i] = 0, v_i[i+1] = 1) is stored in
 // row i, entries i+2..n-1 -- by symmetry the same entries LAPACK's lower storage keeps in column i.
 //
-// fp32 with 2048 <= n <= band::kMaxN takes the two-stage reduction instead (eigh_band.hip: dense ->
+// fp32 with 8192 <= n <= band::kMaxN (use_two_stage) takes the two-stage reduction instead (eigh_band.hip: dense ->
 // band of half-bandwidth 32 on the MFMA GEMM, band -> tridiagonal by bulge chasing); its stage-1
 // reflectors sit in the rows of A the same way with v_i[i + 32] = 1, and the same compact-WY
 // back-transformation applies them after the bulge-chasing reflectors.
-#include <rocblas/rocblas.h>
 
 #include <algorithm>
 
 #include "common.h"
 #include "eigh_band.h"
 #include "gemm.h"
+#include "gemm_f64.h"
 #include "kernels.h"
 #include "stedc.h"
 #include "wy_x6.h"
@@ -612,52 +613,32 @@ namespace {
 
 using mpq::a64;
 
-rocblas_handle get_handle(hipStream_t stream) {
-  static thread_local rocblas_handle hs[16] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return nullptr;
-  if (!hs[dev] && rocblas_create_handle(&hs[dev]) != rocblas_status_success) return nullptr;
-  if (rocblas_set_stream(hs[dev], stream) != rocblas_status_success) return nullptr;
-  return hs[dev];
+// Row-major C (M x N) = alpha A (M x K) op(B) + beta C, op(B) = B (K x N) or B^T (B: N x K), on this
+// library's MFMA GEMMs (split-K partials in P when given).
+int gemm_rm(const float* A, int64_t lda, const float* B, int64_t ldb, bool trans_b, float* C, int64_t ldc, int64_t M,
+            int64_t N, int64_t K, float alpha, float beta, float* P, int64_t p_elems, hipStream_t stream) {
+  MPQ_HIP_TRY(mpq::gemm(A, lda, B, ldb, trans_b, nullptr, C, ldc, M, N, K, alpha, beta, P, p_elems, stream));
+  return mpq::kOk;
 }
-
-int rocblas_fail(const char* what) {
-  mpq::set_error("mpq_syevd: %s failed", what);
-  mpq::set_error_code(mpq::kHipError);
-  return mpq::kHipError;
-}
-
-// Row-major C (M x N) = alpha A (M x K) op(B) + beta C, op(B) = B (K x N) or B^T (B: N x K).
-// fp32: this library's MFMA GEMM (split-K partials in P when given); fp64: rocBLAS dgemm on the
-// column-major view, C^T = op(B)^T A^T.
-int gemm_rm(rocblas_handle, const float* A, int64_t lda, const float* B, int64_t ldb, bool trans_b, float* C,
-            int64_t ldc, int64_t M, int64_t N, int64_t K, float alpha, float beta, float* P, int64_t p_floats,
+int gemm_rm(const double* A, int64_t lda, const double* B, int64_t ldb, bool trans_b, double* C, int64_t ldc,
+            int64_t M, int64_t N, int64_t K, double alpha, double beta, double* P, int64_t p_elems,
             hipStream_t stream) {
-  MPQ_HIP_TRY(mpq::gemm(A, lda, B, ldb, trans_b, nullptr, C, ldc, M, N, K, alpha, beta, P, p_floats, stream));
-  return mpq::kOk;
-}
-int gemm_rm(rocblas_handle h, const double* A, int64_t lda, const double* B, int64_t ldb, bool trans_b, double* C,
-            int64_t ldc, int64_t M, int64_t N, int64_t K, double alpha, double beta, double*, int64_t, hipStream_t) {
-  if (rocblas_dgemm(h, trans_b ? rocblas_operation_transpose : rocblas_operation_none, rocblas_operation_none,
-                    (rocblas_int)N, (rocblas_int)M, (rocblas_int)K, &alpha, B, (rocblas_int)ldb, A,
-                    (rocblas_int)lda, &beta, C, (rocblas_int)ldc) != rocblas_status_success)
-    return rocblas_fail("rocblas_dgemm");
+  MPQ_HIP_TRY(mpq::gemm_f64(A, lda, B, ldb, trans_b, C, ldc, M, N, K, alpha, beta, P, p_elems, stream));
   return mpq::kOk;
 }
 
-// Trailing update A[s0:, s0:] -= [V W] [W V]^T (m x m, K = 2 kPB).  fp32: only the tiles that
-// symv and the column reads use (lower triangle plus a band of kTB - 1 above the diagonal, so the
-// 64 x 64 diagonal tiles are whole); fp64: the whole square on rocBLAS.
-int trailing_update(rocblas_handle, const float* X, const float* Yb, float* C, int64_t ldc, int64_t m,
-                    hipStream_t stream) {
+// Trailing update A[s0:, s0:] -= [V W] [W V]^T (m x m, K = 2 kPB) on the tiles that symv and the
+// column reads use: the lower triangle plus a band of kTB - 1 above the diagonal, so the 64 x 64
+// diagonal tiles are whole.
+int trailing_update(const float* X, const float* Yb, float* C, int64_t ldc, int64_t m, hipStream_t stream) {
   using namespace mpq;
   MPQ_HIP_TRY(gemm_lower(X, 2 * kPB, Yb, 2 * kPB, true, C, ldc, m, 2 * kPB, -1.f, 1.f, kTB - 1, stream));
   return kOk;
 }
-int trailing_update(rocblas_handle h, const double* X, const double* Yb, double* C, int64_t ldc, int64_t m,
-                    hipStream_t stream) {
+int trailing_update(const double* X, const double* Yb, double* C, int64_t ldc, int64_t m, hipStream_t stream) {
   using namespace mpq;
-  return gemm_rm(h, X, 2 * kPB, Yb, 2 * kPB, true, C, ldc, m, m, 2 * kPB, -1.0, 1.0, nullptr, 0, stream);
+  MPQ_HIP_TRY(gemm_f64_lower(X, 2 * kPB, Yb, 2 * kPB, true, C, ldc, m, 2 * kPB, -1.0, 1.0, kTB - 1, stream));
+  return kOk;
 }
 
 template <typename T>
@@ -670,7 +651,7 @@ hipError_t transpose_t(const T* in, int64_t rows, int64_t cols, int64_t ld_in, T
 
 // Workspace layout of mpq_syevd / mpq_syevd_f64 (element offsets, each region 64 elements aligned).
 struct SyevdLayout {
-  int64_t lda, nblk, ch_alloc, pn_stride, splits, nb;
+  int64_t lda, nblk, ch_alloc, pn_stride, splits, nb, Pcap;
   int64_t A, Z, Y, Yt, W, W2, G, Tb, P, D, E, tau, alph, Pn, Wb, X, Yb, Pr, Pc, Pvv, Ppq, dc, wy1, wy3, wyw, total;
 };
 
@@ -684,7 +665,8 @@ SyevdLayout syevd_layout(int64_t n) {
   L.pn_stride = a64(L.lda / kRowsPB + 2);
   L.nb = NbOf<T>::value;
   int bn = 64;
-  // split-K partials of the fp32 back-transformation GEMMs (rocBLAS needs none)
+  // split-K partials of the back-transformation GEMMs: W = Z Y (n x nb, K up to n) and, in fp64,
+  // the grams Y^T Y (nb x nb, K up to n)
   L.splits = sizeof(T) == 4 ? std::max(choose_splits(n, L.nb, n, (int64_t)1 << 62, &bn), 1) : 1;
   int64_t o = 0;
   auto take = [&](int64_t elems) {
@@ -702,7 +684,10 @@ SyevdLayout syevd_layout(int64_t n) {
   const int64_t nblocks = std::max<int64_t>((n - 1 + L.nb - 1) / L.nb, 1);
   L.G = take(nblocks * L.nb * L.nb);
   L.Tb = take(nblocks * L.nb * L.nb);
-  L.P = take(sizeof(T) == 4 ? a64(n * L.nb) * L.splits : 64);
+  L.Pcap = sizeof(T) == 4 ? a64(n * L.nb) * L.splits
+                          : std::max<int64_t>(n * L.nb * f64_choose_splits(n, L.nb, n, (int64_t)1 << 62),
+                                              L.nb * L.nb * f64_choose_splits(L.nb, L.nb, n, (int64_t)1 << 62));
+  L.P = take(L.Pcap);
   L.D = take(n);
   L.E = take(n);
   L.tau = take(n);
@@ -728,7 +713,7 @@ SyevdLayout syevd_layout(int64_t n) {
 // A = Q T Q^T for the symmetric A (lda x lda buffer, zero padded): D, E, tau and the reflectors
 // in the rows of A.  n >= 2.
 template <typename T>
-int sytrd(int64_t n, const SyevdLayout& L, T* base, rocblas_handle h, hipStream_t stream) {
+int sytrd(int64_t n, const SyevdLayout& L, T* base, hipStream_t stream) {
   using namespace mpq;
   const int64_t lda = L.lda;
   T* A = base + L.A;
@@ -791,7 +776,7 @@ int sytrd(int64_t n, const SyevdLayout& L, T* base, rocblas_handle h, hipStream_
       hipLaunchKernelGGL(panel_operands_kernel<T>, dim3((unsigned)((m + 31) / 32)), dim3(256), 0, stream, Vp, Wp,
                          m, s0 - sa, lda, X, Yb);
       MPQ_LAUNCH_CHECK();
-      const int rc = trailing_update(h, X, Yb, A + sa * lda + sa, lda, m, stream);
+      const int rc = trailing_update(X, Yb, A + sa * lda + sa, lda, m, stream);
       if (rc != kOk) return rc;
     }
   }
@@ -804,8 +789,7 @@ int sytrd(int64_t n, const SyevdLayout& L, T* base, rocblas_handle h, hipStream_
 //    Zb[:, i0:] <- Zb[:, i0:] - ((Zb[:, i0:] Y) Tb^T) Y^T
 // The grams Y^T Y of all blocks come first, then one larft launch forms every Tb.
 template <typename T>
-int back_transform(int64_t n, int64_t off, int64_t nrefl, const SyevdLayout& L, T* base, rocblas_handle h,
-                   hipStream_t stream) {
+int back_transform(int64_t n, int64_t off, int64_t nrefl, const SyevdLayout& L, T* base, hipStream_t stream) {
   using namespace mpq;
   T* A = base + L.A;
   T* Z = base + L.Z;
@@ -818,7 +802,7 @@ int back_transform(int64_t n, int64_t off, int64_t nrefl, const SyevdLayout& L, 
   T* P = base + L.P;
   T* tau = base + L.tau;
   const int64_t lda = L.lda;
-  const int64_t pfl = L.splits > 1 ? a64(n * L.nb) * L.splits : 0;
+  const int64_t pfl = sizeof(T) == 4 ? (L.splits > 1 ? a64(n * L.nb) * L.splits : 0) : L.Pcap;
   const int NB = (int)L.nb;
   const int64_t nblocks = nrefl > 0 ? (nrefl + NB - 1) / NB : 0;
   int rc;
@@ -831,7 +815,7 @@ int back_transform(int64_t n, int64_t off, int64_t nrefl, const SyevdLayout& L, 
                        i0, nb, off, Y);
     MPQ_LAUNCH_CHECK();
     MPQ_HIP_TRY(transpose_t(Y, m, nb, nb, Yt, m, stream));
-    if ((rc = gemm_rm(h, Yt, m, Y, nb, false, G + b * NB * NB, nb, nb, nb, m, T(1), T(0), P, pfl, stream)) != kOk)
+    if ((rc = gemm_rm(Yt, m, Y, nb, false, G + b * NB * NB, nb, nb, nb, m, T(1), T(0), P, pfl, stream)) != kOk)
       return rc;
   }
   if (nblocks > 0) {
@@ -872,9 +856,9 @@ int back_transform(int64_t n, int64_t off, int64_t nrefl, const SyevdLayout& L, 
     hipLaunchKernelGGL(extract_y_kernel<T>, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, stream, A, lda, n,
                        i0, nb, off, Y);
     MPQ_LAUNCH_CHECK();
-    if ((rc = gemm_rm(h, Z + i0, n, Y, nb, false, W, nb, n, nb, m, T(1), T(0), P, pfl, stream)) != kOk) return rc;
-    if ((rc = gemm_rm(h, W, nb, Tbb, nb, true, W2, nb, n, nb, nb, T(1), T(0), nullptr, 0, stream)) != kOk) return rc;
-    if ((rc = gemm_rm(h, W2, nb, Y, nb, true, Z + i0, n, n, m, nb, T(-1), T(1), nullptr, 0, stream)) != kOk)
+    if ((rc = gemm_rm(Z + i0, n, Y, nb, false, W, nb, n, nb, m, T(1), T(0), P, pfl, stream)) != kOk) return rc;
+    if ((rc = gemm_rm(W, nb, Tbb, nb, true, W2, nb, n, nb, nb, T(1), T(0), nullptr, 0, stream)) != kOk) return rc;
+    if ((rc = gemm_rm(W2, nb, Y, nb, true, Z + i0, n, n, m, nb, T(-1), T(1), nullptr, 0, stream)) != kOk)
       return rc;
   }
   return kOk;
@@ -889,7 +873,7 @@ bool two_stage_ok(int64_t n) { return n >= 3 && n <= mpq::band::kMaxN; }
 bool use_two_stage(int64_t n, int elem) { return elem == 4 && n >= 8192 && two_stage_ok(n); }
 
 int syevd_two_stage(int64_t n, const float* H, float* lam, float* V, float* base, const SyevdLayout& L,
-                    rocblas_handle h, hipStream_t stream) {
+                    hipStream_t stream) {
   using namespace mpq;
   const band::Layout BL = band::layout(n);
   float* bws = base + L.total;
@@ -902,11 +886,11 @@ int syevd_two_stage(int64_t n, const float* H, float* lam, float* V, float* base
   int rc;
   if ((rc = band::sy2sb(n, A, lda, base + L.tau, bws, BL, stream)) != kOk) return rc;
   if ((rc = band::sb2st(n, A, lda, base + L.D, base + L.E, bws, BL, stream)) != kOk) return rc;
-  if ((rc = tridiag_dc(n, base + L.D, base + L.E, lam, Z, base + L.dc, (L.total - L.dc) * (int64_t)sizeof(float), h,
+  if ((rc = tridiag_dc(n, base + L.D, base + L.E, lam, Z, base + L.dc, (L.total - L.dc) * (int64_t)sizeof(float),
                        stream)) != kOk)
     return rc;
   if ((rc = band::q2_apply(n, Z, bws, BL, stream)) != kOk) return rc;
-  if ((rc = back_transform<float>(n, band::kBW, n - band::kBW, L, base, h, stream)) != kOk) return rc;
+  if ((rc = back_transform<float>(n, band::kBW, n - band::kBW, L, base, stream)) != kOk) return rc;
   MPQ_HIP_TRY(transpose_t(Z, n, n, n, V, n, stream));
   MPQ_HIP_TRY(hipStreamSynchronize(stream));
   return kOk;
@@ -930,14 +914,12 @@ int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t wor
   const int64_t need = syevd_workspace_elems<T>(n) * (int64_t)sizeof(T);
   MPQ_CHECK_ARG(workspace_bytes >= need, "mpq_syevd: workspace too small (%lld < %lld)",
                 (long long)workspace_bytes, (long long)need);
-  rocblas_handle h = get_handle(stream);
-  MPQ_CHECK_ARG(h != nullptr, "mpq_syevd: rocBLAS handle unavailable");
   T* base = static_cast<T*>(workspace);
   if constexpr (sizeof(T) == 4) {
     MPQ_CHECK_ARG(method >= 0 && method <= 2, "mpq_syevd_method: method must be 0 (auto), 1 or 2");
     MPQ_CHECK_ARG(method != 2 || two_stage_ok(n), "mpq_syevd_method: the two-stage path needs 3 <= n <= %lld",
                   (long long)mpq::band::kMaxN);
-    if (method == 2 || (method == 0 && use_two_stage(n, 4))) return syevd_two_stage(n, H, lam, V, base, L, h, stream);
+    if (method == 2 || (method == 0 && use_two_stage(n, 4))) return syevd_two_stage(n, H, lam, V, base, L, stream);
   }
   T* A = base + L.A;
   T* Z = base + L.Z;
@@ -952,17 +934,17 @@ int syevd_impl(int64_t n, const T* H, T* lam, T* V, void* workspace, int64_t wor
   if (n == 1) {
     MPQ_HIP_TRY(hipMemcpyAsync(D, A, sizeof(T), hipMemcpyDeviceToDevice, stream));
   } else {
-    const int rc = sytrd<T>(n, L, base, h, stream);
+    const int rc = sytrd<T>(n, L, base, stream);
     if (rc != kOk) return rc;
   }
   // 2. tridiagonal eigenproblem
   {
-    const int rc = tridiag_dc(n, D, E, lam, Z, base + L.dc, (L.total - L.dc) * (int64_t)sizeof(T), h, stream);
+    const int rc = tridiag_dc(n, D, E, lam, Z, base + L.dc, (L.total - L.dc) * (int64_t)sizeof(T), stream);
     if (rc != kOk) return rc;
   }
   // 3. Z column-major = row-major Zb with Zb = Z^T; V^T = Zb Q^T
   {
-    const int rc = back_transform<T>(n, 1, n - 1, L, base, h, stream);
+    const int rc = back_transform<T>(n, 1, n - 1, L, base, stream);
     if (rc != kOk) return rc;
   }
   // V (row-major, columns = eigenvectors) = (Zb)^T

@@ -3,7 +3,6 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
 
 #include <cstdint>
 
@@ -17,10 +16,10 @@ int64_t tridiag_dc_workspace_bytes(int64_t n, int elem_size);
 // aligned, `ws_bytes` >= tridiag_dc_workspace_bytes(n, sizeof(T)).  Synchronises `stream` once per
 // merge of more than 512 rows (the host sizes that merge's GEMMs); the caller synchronises `stream`
 // before its next call on the same host thread (the node lists are staged in a per-thread pinned
-// buffer).  fp64 products go through rocBLAS on `h`.
+// buffer).  The merge products run on this library's MFMA GEMMs (fp32 or fp64).
 int tridiag_dc(int64_t n, const float* d, const float* e, float* lam, float* Z, void* ws, int64_t ws_bytes,
-               rocblas_handle h, hipStream_t stream);
+               hipStream_t stream);
 int tridiag_dc(int64_t n, const double* d, const double* e, double* lam, double* Z, void* ws,
-               int64_t ws_bytes, rocblas_handle h, hipStream_t stream);
+               int64_t ws_bytes, hipStream_t stream);
 
 }  // namespace mpq

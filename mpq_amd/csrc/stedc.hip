@@ -17,7 +17,7 @@
 // Merges of at most 512 rows run in one work-group each (all merges of a tree level in one launch).
 // Larger merges run one at a time with the GPU-wide kernels below: the kept rows are gathered in
 // three groups (rows from the first half only, from both halves after a rotation, from the second
-// half only), so the product is two MFMA GEMMs over the nonzero halves (fp64: rocBLAS dgemm).
+// half only), so the product is two MFMA GEMMs over the nonzero halves (fp32 or fp64 matrix cores).
 // Eigenvalues stay in fp64 through the tree.  Storage: Z row-major n x n, row k = eigenvector k;
 // a merge of rows [s, s+m) reads and writes only the diagonal block Z[s:s+m, s:s+m].
 #include "stedc.h"
@@ -27,6 +27,7 @@
 
 #include "common.h"
 #include "gemm.h"
+#include "gemm_f64.h"
 
 namespace mpq {
 namespace {
@@ -1136,7 +1137,8 @@ DcLayout dc_layout(int64_t n, int es) {
 }
 
 // Pinned staging of the node lists (grown as needed; every caller synchronises its stream before
-// returning, so no copy from it is pending when it is reused).
+// returning, so no copy from it is pending when it is reused; freed by
+// mpq_release_thread_resources).
 int* host_nodes_buf(size_t count) {
   static thread_local int* p = nullptr;
   static thread_local size_t cap = 0;
@@ -1146,34 +1148,29 @@ int* host_nodes_buf(size_t count) {
     cap = 0;
     if (hipHostMalloc((void**)&p, count * sizeof(int), hipHostMallocDefault) != hipSuccess) return nullptr;
     cap = count;
+    track_pinned(reinterpret_cast<void**>(&p), nullptr, &cap);
   }
   return p;
 }
 
 int* host_info_buf() {
   static thread_local int* p = nullptr;
-  if (!p && hipHostMalloc((void**)&p, 64 * sizeof(int), hipHostMallocDefault) != hipSuccess) p = nullptr;
+  if (!p) {
+    if (hipHostMalloc((void**)&p, 64 * sizeof(int), hipHostMallocDefault) != hipSuccess) p = nullptr;
+    else track_pinned(reinterpret_cast<void**>(&p), nullptr, nullptr);
+  }
   return p;
 }
 
-int large_gemm(rocblas_handle, const float* A, int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc,
-               int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+int large_gemm(const float* A, int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc, int64_t M, int64_t N,
+               int64_t K, hipStream_t stream) {
   MPQ_HIP_TRY(gemm(A, lda, B, ldb, false, nullptr, C, ldc, M, N, K, 1.f, 0.f, nullptr, 0, stream));
   return kOk;
 }
 
-int large_gemm(rocblas_handle h, const double* A, int64_t lda, const double* B, int64_t ldb, double* C, int64_t ldc,
-               int64_t M, int64_t N, int64_t K, hipStream_t stream) {
-  (void)stream;  // h is bound to the stream
-  const double one = 1.0, zero = 0.0;
-  // row-major C = A B  <=>  column-major C^T = B^T A^T
-  if (rocblas_dgemm(h, rocblas_operation_none, rocblas_operation_none, (rocblas_int)N, (rocblas_int)M,
-                    (rocblas_int)K, &one, B, (rocblas_int)ldb, A, (rocblas_int)lda, &zero, C,
-                    (rocblas_int)ldc) != rocblas_status_success) {
-    set_error("tridiagonal divide and conquer: rocblas_dgemm failed");
-    set_error_code(kHipError);
-    return kHipError;
-  }
+int large_gemm(const double* A, int64_t lda, const double* B, int64_t ldb, double* C, int64_t ldc, int64_t M,
+               int64_t N, int64_t K, hipStream_t stream) {
+  MPQ_HIP_TRY(gemm_f64(A, lda, B, ldb, false, C, ldc, M, N, K, 1.0, 0.0, nullptr, 0, stream));
   return kOk;
 }
 
@@ -1199,7 +1196,7 @@ int small_level(int64_t n, const int* nl, int count, const T* e, double* lam, T*
 
 template <typename T>
 int tridiag_dc_impl(int64_t n, const T* d, const T* e, T* lam_out, T* Z, void* ws, int64_t ws_bytes,
-                    rocblas_handle h, hipStream_t stream) {
+                    hipStream_t stream) {
   MPQ_CHECK_ARG(n >= 1 && n <= (int64_t)1 << 30, "tridiagonal divide and conquer: bad order %lld", (long long)n);
   const DcLayout L = dc_layout(n, (int)sizeof(T));
   MPQ_CHECK_ARG(ws_bytes >= L.total, "tridiagonal divide and conquer: workspace too small");
@@ -1347,14 +1344,14 @@ int tridiag_dc_impl(int64_t n, const T* d, const T* e, T* lam_out, T* Z, void* w
           int rc;
           // first half of the columns: groups 1 and 2; second half: groups 2 and 3
           if (n1p + n2p > 0) {
-            if ((rc = large_gemm(h, Ut, Kc, Bbuf, mp, Cb, mp, Kr, hh, n1p + n2p, stream)) != kOk) return rc;
+            if ((rc = large_gemm(Ut, Kc, Bbuf, mp, Cb, mp, Kr, hh, n1p + n2p, stream)) != kOk) return rc;
           } else {
             hipLaunchKernelGGL(dc_zero_cols_kernel<T>, dim3((unsigned)Kr), dim3(256), 0, stream, (int64_t)Kr,
                                (int64_t)hh, mp, Cb);
             MPQ_LAUNCH_CHECK();
           }
           if (n2p + n3p > 0) {
-            if ((rc = large_gemm(h, Ut + n1p, Kc, Bbuf + (int64_t)n1p * mp + hh, mp, Cb + hh, mp, Kr, m - hh,
+            if ((rc = large_gemm(Ut + n1p, Kc, Bbuf + (int64_t)n1p * mp + hh, mp, Cb + hh, mp, Kr, m - hh,
                                  n2p + n3p, stream)) != kOk)
               return rc;
           } else {
@@ -1382,13 +1379,13 @@ int64_t tridiag_dc_workspace_bytes(int64_t n, int elem_size) {
 }
 
 int tridiag_dc(int64_t n, const float* d, const float* e, float* lam, float* Z, void* ws, int64_t ws_bytes,
-               rocblas_handle h, hipStream_t stream) {
-  return tridiag_dc_impl<float>(n, d, e, lam, Z, ws, ws_bytes, h, stream);
+               hipStream_t stream) {
+  return tridiag_dc_impl<float>(n, d, e, lam, Z, ws, ws_bytes, stream);
 }
 
 int tridiag_dc(int64_t n, const double* d, const double* e, double* lam, double* Z, void* ws, int64_t ws_bytes,
-               rocblas_handle h, hipStream_t stream) {
-  return tridiag_dc_impl<double>(n, d, e, lam, Z, ws, ws_bytes, h, stream);
+               hipStream_t stream) {
+  return tridiag_dc_impl<double>(n, d, e, lam, Z, ws, ws_bytes, stream);
 }
 
 }  // namespace mpq

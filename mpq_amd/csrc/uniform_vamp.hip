@@ -244,11 +244,13 @@ Workspace carve(void* base, const Sizes& s) {
   return w;
 }
 
-// Pinned host mirror of the device status (allocated once per process).
+// Pinned host mirror of the device status (one per host thread, freed by
+// mpq_release_thread_resources).
 VampStatus* host_status() {
   static thread_local VampStatus* h = nullptr;
   if (!h) {
     if (hipHostMalloc((void**)&h, sizeof(VampStatus), hipHostMallocDefault) != hipSuccess) h = nullptr;
+    else track_pinned(reinterpret_cast<void**>(&h), nullptr, nullptr);
   }
   return h;
 }

@@ -83,7 +83,7 @@ struct HostMailbox {
   StatusMailbox* dev(unsigned s) const { return d + (s & 1u); }
 };
 
-// One mailbox per host thread (allocated once, kept for the thread's lifetime).
+// One mailbox per host thread (allocated on first use, freed by mpq_release_thread_resources).
 inline HostMailbox* host_mailbox() {
   static thread_local HostMailbox mb;
   if (mb.h == nullptr) {
@@ -99,6 +99,7 @@ inline HostMailbox* host_mailbox() {
     }
     mb.h = h;
     mb.d = d;
+    track_pinned(reinterpret_cast<void**>(&mb.h), reinterpret_cast<void**>(&mb.d), nullptr);
   }
   return &mb;
 }

@@ -80,6 +80,30 @@ def gemm(A: torch.Tensor, B: torch.Tensor, *, trans_b: bool = False, b_rows: Opt
     return out
 
 
+def gemm_f64(A: torch.Tensor, B: torch.Tensor, *, trans_b: bool = False, out: Optional[torch.Tensor] = None,
+             alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
+    """C = alpha * A @ op(B) + beta * C in fp64 on the fp64 matrix cores (the eigensolver's kernel)."""
+    dev = _dev(A, B)
+    A = A.to(dtype=torch.float64).contiguous()
+    B = B.to(dtype=torch.float64).contiguous()
+    M, K = A.shape
+    N = int(B.shape[0]) if trans_b else int(B.shape[1])
+    if int(B.shape[1] if trans_b else B.shape[0]) != K:
+        raise ValueError(f"shape mismatch: A {tuple(A.shape)} vs op(B) of {tuple(B.shape)}")
+    if out is None:
+        if beta != 0.0:
+            raise ValueError("beta != 0 needs out")
+        out = torch.empty(M, N, dtype=torch.float64, device=dev)
+    elif out.dtype != torch.float64 or not out.is_contiguous() or tuple(out.shape) != (M, N):
+        raise ValueError("out must be a contiguous fp64 (M, N) tensor")
+    lib = _lib.load()
+    wsb = int(lib.mpq_gemm_f64_workspace_size(M, N, K))
+    ws = workspace(wsb, dev) if wsb > 0 else None
+    _lib.call("mpq_gemm_f64", M, N, K, _lib.ptr(A), K, _lib.ptr(B), int(B.shape[1]), int(bool(trans_b)),
+              _lib.ptr(out), N, float(alpha), float(beta), _lib.ptr(ws), wsb, _stream(dev))
+    return out
+
+
 def gemm_x6_pack_b(B: torch.Tensor, *, trans_b: bool = False) -> torch.Tensor:
     """op(B) (K x N; N % 128 == 0, K % 32 == 0) packed for :func:`gemm_x6` (K * N floats)."""
     dev = _dev(B)
@@ -406,9 +430,13 @@ def uniform_cd_polish(W, q_in, scale, zero, group_size, maxq, Vs, H, *, block_ro
 
 
 def uniform_cd_sweeps(rhs, x, q, res_norm, accepted, scale, zero, group_size, maxq, diag, H, *,
-                      block_rows: int, sweeps: int, accept_tol: float = 0.0):
+                      block_rows: int, sweeps: int, accept_tol: float = 0.0, target_rule: str = "div"):
     """The greedy sweeps in place on (rhs, x, q, res_norm, accepted): the state the reference's
-    persistent sweep kernel takes (mpq/polish/triton_scalar_cd.py:113-161)."""
+    persistent sweep kernel takes (mpq/polish/triton_scalar_cd.py:113-161).  ``target_rule`` "div"
+    forms the RTN target x + rhs / diag (the sweep kernel, :73), "recip" x + rhs * (1 / diag) (the
+    torch update loop, :266)."""
+    if target_rule not in ("div", "recip"):
+        raise ValueError(f"target_rule must be 'div' or 'recip', got {target_rule!r}")
     dev = _dev(rhs, x, q, res_norm, accepted, scale, zero, diag, H)
     rows, n = rhs.shape
     for name, t, dt, shape in (("rhs", rhs, F32, (rows, n)), ("x", x, F32, (rows, n)),
@@ -419,7 +447,8 @@ def uniform_cd_sweeps(rhs, x, q, res_norm, accepted, scale, zero, group_size, ma
     lib = _lib.load()
     need = int(lib.mpq_uniform_cd_sweeps_workspace_size(rows, n, int(block_rows)))
     ws = workspace(need, dev)
-    _lib.call("mpq_uniform_cd_sweeps", rows, n, int(maxq), int(block_rows), int(sweeps), float(accept_tol),
+    entry = "mpq_uniform_cd_sweeps" if target_rule == "div" else "mpq_uniform_cd_sweeps_recip"
+    _lib.call(entry, rows, n, int(maxq), int(block_rows), int(sweeps), float(accept_tol),
               _lib.ptr(rhs), _lib.ptr(x), _lib.ptr(q), _lib.ptr(res_norm), _lib.ptr(accepted),
               _lib.ptr(_f32c(scale)), _lib.ptr(_f32c(zero)), int(group_size), _lib.ptr(_f32c(diag)),
               _lib.ptr(_f32c(H)), _lib.ptr(ws), int(ws.numel()), _stream(dev))

@@ -2,9 +2,13 @@
 
 Drop-in for the reference's ``mpq/polish/triton_scalar_cd.py:164-307``
 (``uniform_scalar_diag_greedy_cd``): same keyword signature, start state, per-sweep greedy order,
-accept test, return value and ``cd_trace`` items.  Both ``update_backend`` values run
-``mpq_uniform_cd_sweeps`` (one launch sequence per sweep; 128 decisions per window with the
-deferred rank-1 updates applied in the per-column order of the reference's torch twin).
+accept test, return value and ``cd_trace`` items.  Both ``update_backend`` values run the HIP sweeps
+(one launch sequence per sweep; 128 decisions per window with the deferred rank-1 updates applied in
+the per-column order of the reference's torch loop), each with its backend's RTN target:
+``"torch"`` forms ``x + rhs * (1 / diag)`` as the torch loop does (:266,
+``mpq_uniform_cd_sweeps_recip``), ``"triton"`` forms ``x + rhs / diag`` as the sweep kernel does
+(:73, ``mpq_uniform_cd_sweeps``).  ``assignment_changes_from_cd0`` re-rounds the current values as
+the reference does (:292-296).
 
 Differences from the reference, both documented there as free choices:
 * the greedy order is a stable descending sort of the gain (ties by column index; the reference's
@@ -74,12 +78,13 @@ def uniform_scalar_diag_greedy_cd(
     accepted = torch.zeros(rows, dtype=torch.int32, device=x_work.device)
 
     def trace_item(budget: int, swept: int, total: int) -> Dict[str, float | int]:
+        q_current = torch.round(x_work / scale_f.clamp_min(1e-12) + zero_f).clamp_(0, int(maxq)).to(torch.int32)
         item: Dict[str, float | int] = {
             "budget": int(budget),
             "stabilized_objective_mean": float(res_norm.mean().item()),
             "accepted_updates_sweep": int(swept),
             "accepted_updates_cumulative": int(total),
-            "assignment_changes_from_cd0": int((q.to(torch.int32) != q_initial).sum().item()),
+            "assignment_changes_from_cd0": int((q_current != q_initial).sum().item()),
             "assignments_total": int(q_initial.numel()),
         }
         if raw_target is not None and raw_gram is not None:
@@ -93,7 +98,8 @@ def uniform_scalar_diag_greedy_cd(
             trace.append(trace_item(sweep + 1, 0, total))
             continue
         ops.uniform_cd_sweeps(rhs, x_work, q, res_norm, accepted, scale_f, zero_f, 1, int(maxq), diag, gram,
-                              block_rows=rows, sweeps=1, accept_tol=float(accept_tol))
+                              block_rows=rows, sweeps=1, accept_tol=float(accept_tol),
+                              target_rule="recip" if backend == "torch" else "div")
         now = int(accepted.sum().item())
         trace.append(trace_item(sweep + 1, now - total, now))
         total = now

@@ -14,6 +14,8 @@ always floor the eigenvalues, so this holds on the reference's own path).
 """
 from __future__ import annotations
 
+import weakref
+
 from dataclasses import dataclass
 from typing import Any, Dict, Optional, Tuple
 
@@ -130,8 +132,13 @@ def polish_uniform_rankspace(
     raw_target: Optional[torch.Tensor] = None,
     raw_gram: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, Dict[str, float]]:
-    """Greedy scalar CD polish (reference :260-366); returns (q int32, x, err, stats)."""
-    del topk_values, topk_q, compile_block_cd, raw_target, raw_gram
+    """Greedy scalar CD polish (reference :260-366); returns (q int32, x, err, stats).
+
+    The recipe case (block_cd, greedy order) runs the fused sweeps (``mpq_uniform_cd_polish``);
+    ``topk_block_cd`` (with ``topk_values``) and the static / cyclic orders run the generic block CD
+    (``mpq_amd.polish.block_cd``) with the reference's providers, as its CPU dispatch does (:334-366).
+    """
+    del compile_block_cd
     mode = _resolve_polish_mode(sweeps=int(sweeps), mode=str(polish_mode))
     _resolve_backend(block_cd_backend, field="block_cd_backend")
     rows, n = x_init.shape
@@ -141,10 +148,31 @@ def polish_uniform_rankspace(
         x_out = dequant_from_q(q_int=q0, scale_full=scale_full, zero_full=zero_full)
         err = (Y_u - ops.gemm(x_out, Vs)).square().sum(dim=1)
         return q0, x_out, err, {"accepted_updates": 0.0}
-    if mode == "topk_block_cd":
-        raise ValueError("mpq_amd implements polish_mode='block_cd' (the recipe default); topk_block_cd is not provided.")
-    if str(order_mode or "greedy_gain").strip().lower() != "greedy_gain":
-        raise ValueError("mpq_amd's CD polish implements order_mode='greedy_gain' only.")
+    order = str(order_mode or "greedy_gain").strip().lower()
+    if mode == "topk_block_cd" or order != "greedy_gain":
+        from .polish.block_cd import (BlockCDConfig, UniformScalarProvider, UniformTopKProvider,
+                                      block_coordinate_descent_rankspace)
+
+        if mode == "topk_block_cd":
+            if topk_values is None:
+                raise ValueError("topk_block_cd requires topk_values for uniform polish.")
+            provider = UniformTopKProvider(topk_values=topk_values, topk_q=topk_q)
+        else:
+            provider = UniformScalarProvider(scale=scale_full, zero=zero_full, maxq=maxq)
+        x_pol, q_pol, st = block_coordinate_descent_rankspace(
+            x=x_work, Y_u=Y_u, Vs=Vs, block_size=1, provider=provider,
+            cfg=BlockCDConfig(sweeps=int(sweeps), metric="diag", accept_tol=0.0, order_mode=order),
+            idxs_init=q0, raw_target=raw_target, raw_gram=raw_gram)
+        if q_pol is not None and bool((q_pol >= 0).all().item()):
+            q_out = q_pol.to(torch.int32)
+        else:
+            q_out = nearest_atom_idx(x=x_pol, scale_full=scale_full, zero_full=zero_full, maxq=maxq)
+        x_out = dequant_from_q(q_int=q_out, scale_full=scale_full, zero_full=zero_full)
+        err = (Y_u - ops.gemm(x_out, Vs)).square().sum(dim=1)
+        st = dict(st)
+        st["block_cd_backend"] = "hip"
+        return q_out, x_out, err, st
+    del topk_values, topk_q, raw_target, raw_gram
     gram = gram_full if gram_full is not None else ops.gemm(Vs, Vs, trans_b=True)
     q, eb, ea, _imp, acc = ops.uniform_cd_polish(
         None, q0.to(torch.uint8), scale_full, zero_full, 1, maxq, Vs, gram, block_rows=rows,
@@ -252,18 +280,40 @@ def solve_uniform_rankspace_vamp(
 _CD_CTX: Dict[str, Any] = {}
 
 
+def _tensor_version(t: torch.Tensor) -> Optional[int]:
+    """torch's in-place modification counter of ``t`` (None for inference tensors, which keep none)."""
+    try:
+        return int(t._version)
+    except RuntimeError:
+        return None
+
+
 def _e8p12_cd_context(Vs: torch.Tensor) -> torch.Tensor:
     """Per-layer polish context for the last Vs seen (the reference-signature solvers call the
-    polish once per row block with the same Vs).  A hit requires the same shape and device and
-    every element equal to the stored copy of Vs; anything else rebuilds the context."""
-    held = _CD_CTX.get("Vs")
-    if held is not None and held.shape == Vs.shape and held.device == Vs.device and torch.equal(held, Vs):
+    polish once per row block with the same Vs).  A hit requires the very same tensor object and an
+    unchanged in-place modification counter; anything else rebuilds the context.  Inference tensors
+    keep no such counter, so for them an in-place change between calls is not seen: callers that
+    modify Vs in place pass ``cd_context`` explicitly.  Only a weak reference to Vs is kept, and the
+    context is dropped when Vs is freed."""
+    ref = _CD_CTX.get("ref")
+    if ref is not None and ref() is Vs and _CD_CTX.get("version") == _tensor_version(Vs):
         return _CD_CTX["ctx"]
     _CD_CTX.clear()
     ctx = ops.e8p12_cd_prepare(Vs)
-    _CD_CTX["Vs"] = Vs.detach().clone()
+    _CD_CTX["ref"] = weakref.ref(Vs, _drop_cd_context)
+    _CD_CTX["version"] = _tensor_version(Vs)
     _CD_CTX["ctx"] = ctx
     return ctx
+
+
+def _drop_cd_context(dead_ref) -> None:
+    if _CD_CTX.get("ref") is dead_ref:
+        _CD_CTX.clear()
+
+
+def clear_e8p12_cd_context() -> None:
+    """Drop the cached polish context (called when a layer's solve finishes)."""
+    _CD_CTX.clear()
 
 
 @torch.inference_mode()
@@ -295,22 +345,34 @@ def polish_e8p12_rankspace(
     Returns (x, idxs, err, stats).
     """
     require_standin_table(cb, "polish_e8p12_rankspace")
-    del cb, metric_rows_per_chunk, topk_idxs
     mode = _resolve_polish_mode(sweeps=int(sweeps), mode=str(polish_mode))
     metric = _resolve_e8p12_polish_metric(str(polish_metric))
     x_work = x_init.to(dtype=torch.float32)
     if mode == "none" or Vs.numel() == 0:
         err = (Y_u - ops.gemm(x_work, Vs)).square().sum(dim=1)
         return x_work, idxs_init, err, {"accepted_updates": 0.0}
-    if mode == "topk_block_cd":
-        raise ValueError("mpq_amd implements polish_mode='block_cd' (the recipe default); topk_block_cd is not provided.")
-    if metric != "gram":
-        raise ValueError("mpq_amd implements polish_metric='gram' (the recipe default); 'diag' is not provided.")
-    if str(order_mode or "greedy_gain").strip().lower() != "greedy_gain":
-        raise ValueError("mpq_amd implements order_mode='greedy_gain' (the recipe default).")
-    if snapshot_budgets:
-        raise ValueError("CD snapshots are not provided by the HIP polish.")
-    del snapshots_out
+    order = str(order_mode or "greedy_gain").strip().lower()
+    if mode == "topk_block_cd" or metric != "gram" or order != "greedy_gain" or snapshot_budgets:
+        # the reference's generic dispatch (:402-423) with its providers, one greedy group for all rows
+        from .polish.block_cd import BlockCDConfig, E8P12Provider, E8P12TopKProvider, block_coordinate_descent_rankspace
+
+        if mode == "topk_block_cd":
+            if topk_idxs is None:
+                raise ValueError("topk_block_cd requires topk_idxs for E8P12 polish.")
+            provider = E8P12TopKProvider(cb=cb, topk_idxs=topk_idxs)
+        else:
+            provider = E8P12Provider(cb=cb, metric_rows_per_chunk=int(metric_rows_per_chunk))
+        x_out, idx_out, st = block_coordinate_descent_rankspace(
+            x=x_work.contiguous(), Y_u=Y_u, Vs=Vs, block_size=int(getattr(cb, "codesz", 8)), provider=provider,
+            cfg=BlockCDConfig(sweeps=int(sweeps), metric="gram" if metric == "gram" else "diag", accept_tol=0.0,
+                              metric_rows_per_chunk=int(metric_rows_per_chunk),
+                              max_blocks_per_sweep=int(polish_max_blocks), order_mode=order),
+            idxs_init=idxs_init, snapshot_budgets=snapshot_budgets, snapshots_out=snapshots_out)
+        if idx_out is None:
+            raise RuntimeError("E8P12 polish must return block indices.")
+        err = (Y_u - ops.gemm(x_out.contiguous(), Vs)).square().sum(dim=1)
+        return x_out, idx_out, err, st
+    del cb, metric_rows_per_chunk, topk_idxs, snapshots_out
     rows = int(x_work.shape[0])
     ctx = cd_context if cd_context is not None else _e8p12_cd_context(Vs.to(dtype=torch.float32).contiguous())
     x, idx, eb, ea, acc = ops.e8p12_cd_polish(x_work, idxs_init, Vs, ctx, sweeps=int(sweeps),

@@ -338,9 +338,12 @@ def stabilize_cholesky(gram: torch.Tensor, jitter: float = 1e-6, max_tries: int 
     return torch.linalg.cholesky(out)
 
 
-def gram_block_cd(x, idxs, Y_u, Vs, grid, sweeps, accept_tol=0.0, max_blocks=0):
-    """mpq/polish/block_cd.py:332-625 with E8P12Provider, metric "gram", greedy_gain order and the
-    compiled step _cd_gram_step_impl (:212-246): whitened brute-force argmin over all codewords."""
+def gram_block_cd(x, idxs, Y_u, Vs, grid, sweeps, accept_tol=0.0, max_blocks=0, metric="gram",
+                  order_mode="greedy_gain"):
+    """mpq/polish/block_cd.py:332-625 with E8P12Provider, greedy_gain order and, for metric "gram", the
+    compiled step _cd_gram_step_impl (:212-246): whitened brute-force argmin over all codewords.
+    metric "diag": target x + rhs * (1 / diag G) and the nearest codeword (cb.quantize, :740-745);
+    order_mode static (trace G descending) or cyclic (:505-511); stable sorts."""
     B, n = x.shape
     nb = n // 8
     x = x.to(torch.float32).clone()
@@ -356,21 +359,36 @@ def gram_block_cd(x, idxs, Y_u, Vs, grid, sweeps, accept_tol=0.0, max_blocks=0):
         Gi = torch.cholesky_inverse(L).contiguous()
         meta.append((Vb.T.contiguous(), Vb.contiguous(), G, L, Gi))
     gi_stack = torch.stack([m[4] for m in meta], 0)
+    dinv_stack = torch.stack([torch.diag(m[2]).clamp_min(1e-12).reciprocal() for m in meta], 0)
+    static = torch.argsort(torch.stack([torch.diag(m[2]).sum() for m in meta]), descending=True, stable=True).tolist()
     accepted = 0
     for _ in range(sweeps):
-        rhs_all = res_u.matmul(Vs_t).reshape(B, nb, 8).permute(1, 0, 2).contiguous()
-        gain = (rhs_all * torch.bmm(rhs_all, gi_stack)).sum(dim=2).mean(dim=1)
-        order = torch.argsort(gain, descending=True, stable=True).tolist()
+        if order_mode == "greedy_gain":
+            rhs_all = res_u.matmul(Vs_t).reshape(B, nb, 8).permute(1, 0, 2).contiguous()
+            if metric == "gram":
+                gain = (rhs_all * torch.bmm(rhs_all, gi_stack)).sum(dim=2).mean(dim=1)
+            else:
+                gain = (rhs_all.square() * dinv_stack.unsqueeze(1)).sum(dim=2).mean(dim=1)
+            order = torch.argsort(gain, descending=True, stable=True).tolist()
+        elif order_mode == "static":
+            order = list(static)
+        else:
+            order = list(range(nb))
         if max_blocks > 0:
             order = order[:max_blocks]  # mpq/polish/block_cd.py:510-511
         for b in order:
             Vbt, Vb, G, L, Gi = meta[b]
             xb = x[:, 8 * b:8 * b + 8]
             rhs = res_u.matmul(Vbt)
-            target = xb + rhs.matmul(Gi)
-            tm = target.matmul(L)
-            mg = grid.matmul(L)
-            scores = tm.square().sum(dim=1, keepdim=True) + mg.square().sum(dim=-1).unsqueeze(0) - 2.0 * tm.matmul(mg.T)
+            if metric == "gram":
+                target = xb + rhs.matmul(Gi)
+                tm = target.matmul(L)
+                mg = grid.matmul(L)
+                scores = (tm.square().sum(dim=1, keepdim=True) + mg.square().sum(dim=-1).unsqueeze(0)
+                          - 2.0 * tm.matmul(mg.T))
+            else:
+                target = xb + rhs * dinv_stack[b].unsqueeze(0)
+                scores = (target.unsqueeze(1) - grid.unsqueeze(0)).square().sum(dim=-1)
             best = torch.argmin(scores, dim=1)
             cand = grid.index_select(0, best)
             delta = cand - xb
@@ -477,12 +495,23 @@ def solve_e8p12_rankspace_vamp(Wr, hat_init, V, S, grid, cache, cfg, obs_precisi
     return hat, idx_t, err, stats
 
 
-def refine_codebook(Wr, Hr, grid, cache, cfg, block_rows=128, info=None):
+def _jitter_last_bit(V: torch.Tensor, seed: int) -> torch.Tensor:
+    """Every entry moved to a random one of its two neighbouring floats or kept (seeded)."""
+    g = torch.Generator().manual_seed(int(seed))
+    step = torch.randint(-1, 2, V.shape, generator=g)
+    up = torch.nextafter(V, torch.full_like(V, float("inf")))
+    dn = torch.nextafter(V, torch.full_like(V, float("-inf")))
+    return torch.where(step > 0, up, torch.where(step < 0, dn, V))
+
+
+def refine_codebook(Wr, Hr, grid, cache, cfg, block_rows=128, info=None, v_jitter_seed=None):
     """mpq/adapters/quip_sharp.py:396-878 for solver "vamp", init "rtn": nearest-codeword init,
     fp64 eigh (:33-67), rank-space warm start (:461-475), per row block VAMP + polish with the
     observation precision carried (:555-586).  Returns (hat, idx, obs_final); ``info`` (a dict,
-    optional) receives the warm-start precision as "obs_initial".  Pinned by the reference's golden
-    vector tests/golden/e8p12_refine.npz."""
+    optional) receives the warm-start precision as "obs_initial".  ``v_jitter_seed`` moves every entry
+    of the fp32 eigenvectors to a random neighbouring float (another valid fp32 rounding of the fp64
+    decomposition, for noise floors).  Pinned by the reference's golden vector
+    tests/golden/e8p12_refine.npz."""
     m, n = Wr.shape
     idx0, _ = bruteforce_nearest(Wr.reshape(-1, 8).numpy(), grid.numpy())
     idx0 = torch.from_numpy(np.asarray(idx0)).view(m, n // 8)
@@ -490,6 +519,8 @@ def refine_codebook(Wr, Hr, grid, cache, cfg, block_rows=128, info=None):
     H64 = 0.5 * (Hr.double() + Hr.double().T)
     lam, V = torch.linalg.eigh(H64)
     lam, V = lam.float(), V.float()
+    if v_jitter_seed is not None:
+        V = _jitter_last_bit(V, v_jitter_seed)
     floor = max(1e-6, 1e-6 * max(float(torch.diagonal(H64).mean().abs()), float(lam.max()), 1e-12))
     lam = lam.clamp_min(floor).flip(0).contiguous()
     V = V.flip(1).contiguous()

@@ -240,8 +240,10 @@ def greedy_cd_sweeps(x, rhs, res, gram, diag, scale, zero, maxq, sweeps, accept_
     return x, rhs, res, acc_rows
 
 
-def block_cd_scalar(x, Y_u, Vs, scale, zero, maxq, sweeps, accept_tol=0.0, max_cols=0):
-    """mpq/polish/block_cd.py:332-625, block_size=1, metric diag, greedy_gain order (CPU dispatch).
+def block_cd_scalar(x, Y_u, Vs, scale, zero, maxq, sweeps, accept_tol=0.0, max_cols=0, order_mode="greedy_gain"):
+    """mpq/polish/block_cd.py:332-625, block_size=1, metric diag (CPU dispatch); ``order_mode``
+    greedy_gain (per sweep, :505-507), static (trace of each column's gram, descending, :418-420) or
+    cyclic (:508-509), stable sorts.
 
     ``max_cols`` > 0 stops each sweep after that many columns (a bounded sample for timing).
     """
@@ -253,10 +255,16 @@ def block_cd_scalar(x, Y_u, Vs, scale, zero, maxq, sweeps, accept_tol=0.0, max_c
     gram_diag = Vs.square().sum(dim=1)
     dinv_all = gram_diag.clamp_min(1e-12).reciprocal()
     accepted = 0
+    static = torch.argsort(gram_diag, descending=True, stable=True).tolist()
     for _ in range(sweeps):
-        rhs_all = res_u.matmul(Vs_t)
-        gain = (rhs_all.square() * dinv_all.unsqueeze(0)).mean(dim=0)
-        order = torch.argsort(gain, descending=True, stable=True).tolist()
+        if order_mode == "greedy_gain":
+            rhs_all = res_u.matmul(Vs_t)
+            gain = (rhs_all.square() * dinv_all.unsqueeze(0)).mean(dim=0)
+            order = torch.argsort(gain, descending=True, stable=True).tolist()
+        elif order_mode == "static":
+            order = list(static)
+        else:
+            order = list(range(n))
         if max_cols > 0:
             order = order[:max_cols]
         for j in order:

@@ -8,7 +8,7 @@ posterior (torch's reduction orders).  The reference runs on its CPU dispatch (e
 The E8P12 functions need a codebook object of class ``E8P12_codebook``; the build's own table
 (mpq_amd/codebook.py) is passed in.
 
-Usage:  python tests/golden/make_golden.py /root/reference
+Usage:  python tests/golden/make_golden.py /root/reference [all|refine|udriver]
 Output: tests/golden/*.npz (inputs and outputs only; no reference code is stored).
 """
 from __future__ import annotations
@@ -177,10 +177,77 @@ def refine_golden(ref_root: str) -> None:
     print("refine written; obs", st["obs_precision_initial"], "->", st["obs_precision_final"])
 
 
+def udriver_golden(ref_root: str) -> None:
+    """The GPTQ adapter's per-linear driver (run_mpq_quantization, solver vamp) on the CPU: its glue --
+    the rotation signs, the eigenvalue floor of the unrotated Hessian, the rotated eigenbasis, the
+    group parameters, the rank-space warm start summed over row blocks and the observation precision
+    carried across row blocks -- is pinned by no closed form.  GPTQModel's quantizer is not vendored;
+    the stand-in is the min-max formula the oracle uses (oracle/uniform.py gptq_find_params)."""
+    sys.path.insert(0, ROOT)
+    sys.path.insert(0, ref_root)
+    torch.set_num_threads(1)
+    import types
+
+    from mpq.adapters.gptqmodel import GPTQAdapterConfig, run_mpq_quantization  # reference
+    from mpq.rotation import sample_rademacher_signs  # reference
+    from mpq.solver import UniformVampConfig as RefUCfg  # reference
+
+    from oracle import uniform as ou
+    from tests.uniform_cases import make_layer
+
+    class MinMaxQuantizer:
+        """GPTQModel's Quantizer interface (find_params sets .scale / .zero per row)."""
+
+        def __init__(self, maxq):
+            self.maxq = maxq
+
+        def find_params(self, x, weight=True):
+            self.scale, self.zero = ou.gptq_find_params(x.to(torch.float32), self.maxq)
+
+    out = {}
+    for key in ("model.layers.0.mlp.up_proj", "model.layers.3.self_attn.q_proj", "golden.udriver"):
+        for width in (512, 1024):
+            out[f"signs:{key}:{width}"] = sample_rademacher_signs(width=width, key=f"{key}:full", seed=0,
+                                                                  device=torch.device("cpu"))
+    np.savez_compressed(os.path.join(HERE, "rademacher_signs.npz"),
+                        **{k.replace(":", "|"): v.numpy() for k, v in out.items()})
+    print("rademacher signs written")
+
+    rows, cols = 384, 256
+    for rotation, bits in (("none", 4), ("internal_hadamard", 3)):
+        name = "model.layers.0.mlp.up_proj"
+        W, H = make_layer(rows, cols, tokens=1024, seed_key=f"golden:udriver:{rotation}")
+        Hg = 2.0 * H  # GPTQModel convention: the adapter halves it (mpq/adapters/gptqmodel.py:702)
+        qcfg = types.SimpleNamespace(bits=bits, group_size=128, desc_act=False,
+                                     mpq=types.SimpleNamespace(rotation_mode=rotation, solver="vamp"))
+        vcfg = RefUCfg(iters=16, damping=0.5, prior_tau=0.2, polish_sweeps=3, polish_mode="block_cd",
+                       vamp_backend="eager", block_cd_backend="eager")
+        Q, q, sc, zr, g_idx, _, st = run_mpq_quantization(W=W, H=Hg, quantizer=MinMaxQuantizer(2 ** bits - 1),
+                                                          qcfg=qcfg, module_name=name, vamp_cfg=vcfg,
+                                                          adapter_cfg=GPTQAdapterConfig(block_rows=128))
+        bst = st["block_stats"]
+        # W is rebuilt from its seed by the test (a draw from torch's CPU generator); H is stored
+        # (X^T X on the CPU rounds by the BLAS partition)
+        np.savez_compressed(os.path.join(HERE, f"udriver_{rotation}.npz"), **_np({
+            "bits": bits, "H": Hg, "Q": Q, "q_int": q, "scale": sc, "zero": zr, "g_idx": g_idx,
+            "obs_initial": float(st["obs_precision_initial"]), "obs_final": float(st["obs_precision_final"]),
+            "eigen_floor": float(st["eigen_floor"]), "layer_error_sum": float(st["layer_error_sum"]),
+            "block_obs_final": torch.tensor([float(b["obs_precision_final"]) for b in bst], dtype=torch.float64),
+            "block_best_iter": torch.tensor([int(b["best_iter"]) for b in bst]),
+            "block_stop_iter": torch.tensor([int(b["stop_iter"]) for b in bst]),
+            "polish_updates": torch.tensor([float(b.get("polish_updates", 0.0)) for b in bst], dtype=torch.float64)}))
+        print("udriver", rotation, "obs", st["obs_precision_initial"], "->", st["obs_precision_final"],
+              "stops", [b["stop_iter"] for b in bst])
+
+
 if __name__ == "__main__":
     ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
-    if len(sys.argv) > 2 and sys.argv[2] == "refine":
+    part = sys.argv[2] if len(sys.argv) > 2 else "all"
+    if part == "refine":
         refine_golden(ref)
+    elif part == "udriver":
+        udriver_golden(ref)
     else:
         main(ref)
         refine_golden(ref)
+        udriver_golden(ref)

@@ -1,5 +1,6 @@
-"""The GPU greedy sweeps (mpq_uniform_cd_sweeps) against the oracle's column-at-a-time sweeps from the
-same state: bit-identical codes, values, residual norms, rhs and accept counts.
+"""The GPU greedy sweeps (mpq_uniform_cd_sweeps, mpq_uniform_cd_sweeps_recip) against the oracle's
+column-at-a-time sweeps from the same state: bit-identical codes, values, residual norms, rhs and accept
+counts.
 
 The GPU runs 128 decisions per window with the window's rank-1 updates in registers and applies the
 deferred update of every other column as a sequential multiply-then-subtract chain in window order,
@@ -73,6 +74,39 @@ def test_cd_sweeps_bit_identical_to_oracle(gpu, rows, n, bits, gs, block_rows, t
     assert torch.equal(rhs.cpu(), rhs_ref)
 
 
+@pytest.mark.parametrize("rows,n,bits,gs,block_rows,tokens,key", [
+    (1024, 1024, 4, 128, 128, 4096, "cfg0:2"),
+    (300, 260, 4, 128, 100, 1024, "ragged-r"),
+])
+def test_cd_sweeps_recip_rule_bit_identical_to_oracle(gpu, rows, n, bits, gs, block_rows, tokens, key):
+    """mpq_uniform_cd_sweeps_recip: the RTN target x + rhs * (1 / diag) of the reference's torch update
+    loop (mpq/polish/triton_scalar_cd.py:266) against the oracle with ``target_div=False``."""
+    H, sg, zg, sf, zf, maxq, q0, x0, rhs0, res0, diag = _state(rows, n, bits, gs, key, tokens)
+    rhs, x, q = rhs0.to(gpu), x0.to(gpu), q0.to(gpu)
+    res = res0.to(gpu)
+    acc = torch.zeros(rows, dtype=torch.int32, device=gpu)
+    ops.uniform_cd_sweeps(rhs, x, q, res, acc, sg.to(gpu), zg.to(gpu), gs, maxq, diag.to(gpu), H.to(gpu),
+                          block_rows=block_rows, sweeps=3, target_rule="recip")
+    xs, rhss, ress, accs = [], [], [], []
+    for r0 in range(0, rows, block_rows):
+        rb = slice(r0, min(r0 + block_rows, rows))
+        xr, rr, er, ar = ou.greedy_cd_sweeps(x0[rb], rhs0[rb], res0[rb], H, diag, sf[rb], zf[rb], maxq, 3,
+                                             target_div=False, seq_gain=True)
+        xs.append(xr)
+        rhss.append(rr)
+        ress.append(er)
+        accs.append(ar)
+    x_ref, rhs_ref, res_ref, acc_ref = torch.cat(xs), torch.cat(rhss), torch.cat(ress), torch.cat(accs)
+    assert int(acc_ref.sum()) > 0
+    assert torch.equal(acc.cpu().long(), acc_ref)
+    assert torch.equal(x.cpu(), x_ref)
+    assert torch.equal(res.cpu(), res_ref)
+    assert torch.equal(rhs.cpu(), rhs_ref)
+    with pytest.raises(ValueError, match="target_rule"):
+        ops.uniform_cd_sweeps(rhs, x, q, res, acc, sg.to(gpu), zg.to(gpu), gs, maxq, diag.to(gpu), H.to(gpu),
+                              block_rows=block_rows, sweeps=1, target_rule="exact")
+
+
 def test_cd_sweeps_rejects_bad_arguments(gpu):
     rhs = torch.zeros(4, 8, device=gpu)
     x = torch.zeros(4, 8, device=gpu)
@@ -88,11 +122,13 @@ def test_cd_sweeps_rejects_bad_arguments(gpu):
         ops.uniform_cd_sweeps(rhs, x, q.float(), res, acc, s, s, 8, 3, d, H, block_rows=4, sweeps=1)
 
 
-def test_reference_signature_scalar_cd_matches_oracle(gpu):
+@pytest.mark.parametrize("backend", ["torch", "triton"])
+def test_reference_signature_scalar_cd_matches_oracle(gpu, backend):
     """mpq_amd.polish.uniform_scalar_diag_greedy_cd (reference mpq/polish/triton_scalar_cd.py:164-307):
     expanded scale/zero, one greedy order over all rows, per-sweep trace.  The oracle's sweeps run from
     the start state the wrapper forms on the device (the same deterministic products), so x and the
-    accept counts must be identical."""
+    accept counts must be identical; each backend with its RTN target rule (torch: x + rhs * (1/diag),
+    :266; triton: x + rhs / diag, :73)."""
     from mpq_amd.polish import uniform_scalar_diag_greedy_cd
 
     rows, n, bits, gs = 96, 256, 4, 128
@@ -108,15 +144,17 @@ def test_reference_signature_scalar_cd_matches_oracle(gpu):
     diag_dev = Vsg.square().sum(dim=1).clamp_min_(1e-12).cpu()
     x_out, st = uniform_scalar_diag_greedy_cd(x=xg, Y_u=Yu.to(gpu), Vs=Vsg, gram_full=H.to(gpu), scale=sf.to(gpu),
                                               zero=zf.to(gpu), maxq=maxq, sweeps=3, raw_target=W.to(gpu),
-                                              raw_gram=H.to(gpu))
+                                              raw_gram=H.to(gpu), update_backend=backend)
     x_ref, _, res_ref, acc_ref = ou.greedy_cd_sweeps(x0, rhs_dev, res_dev, H, diag_dev, sf, zf, maxq, 3,
-                                                     seq_gain=True)
+                                                     target_div=backend == "triton", seq_gain=True)
     assert torch.equal(x_out.cpu(), x_ref)
     assert st["accepted_updates"] == float(acc_ref.sum()) > 0
     tr = st["cd_trace"]
     assert [t["budget"] for t in tr] == [0, 1, 2, 3]
     assert sum(t["accepted_updates_sweep"] for t in tr) == int(acc_ref.sum())
     assert abs(tr[-1]["stabilized_objective_mean"] - float(res_ref.mean())) <= 1e-6 * float(res_ref.mean())
+    q_ref = ou.nearest_atom_idx(x_ref, sf, zf, maxq)
+    assert tr[-1]["assignment_changes_from_cd0"] == int((q_ref.long() != q0.long()).sum())
     objs = [t["raw_objective_mean"] for t in tr]
     assert all(b <= a * (1 + 1e-5) for a, b in zip(objs, objs[1:]))
     with pytest.raises(ValueError, match="update_backend"):

@@ -71,10 +71,20 @@ def test_config2_awq_solve_pack_chain(gpu):
     proxy_ref = float(ref["proxy_rows"].sum())
     rel = (st["proxy_loss"] - proxy_ref) / proxy_ref
     agree = float((q.cpu() == ref["q_int"]).float().mean())
-    print(f"config 2 chain: awq ratio {r}, codes {agree:.5f}, proxy {rel:+.5f}")
+    floor = 1.0
+    if agree < 0.999:
+        # the reference's agreement with itself on this input: its CPU dispatch of the polish
+        # (mpq/solver.py:336-366) and its solve with every product rounded from fp64
+        alt = [ou.run_mpq_quantization(Ws, Hg, bits, gs, name, RECIPE, rotation="internal_hadamard",
+                                       polish="block_cd")]
+        with ou.products_in_fp64():
+            alt.append(ou.run_mpq_quantization(Ws, Hg, bits, gs, name, RECIPE, rotation="internal_hadamard",
+                                               polish="twin_rowsum"))
+        floor = min(float((a["q_int"] == ref["q_int"]).float().mean()) for a in alt)
+    print(f"config 2 chain: awq ratio {r}, codes {agree:.5f} (reference floor {floor:.5f}), proxy {rel:+.5f}")
     assert torch.equal(sc.cpu(), ref["scale"]) and torch.equal(zr.cpu(), ref["zero"])
     assert abs(rel) <= 0.005
-    assert agree >= 0.98
+    assert agree >= min(0.999, floor), (agree, floor)
     # GPTQ packing of the solve's codes: bit-exact against the bit-stream oracle, and it unpacks to them
     packed = pack_gptq(q, sc, zr, bits=bits, group_size=gs)
     ref_pack = og.pack_gptq(q.cpu().numpy(), sc.cpu().numpy(), zr.cpu().numpy(), bits, gs, "v2")

@@ -78,10 +78,11 @@ def _oracle_blocks(Wr, Vs, x0, idx0, grid, block_rows, sweeps, max_blocks=0):
 @pytest.mark.parametrize("rows,n,block_rows,max_blocks", [(64, 256, 64, 0), (200, 128, 64, 0),
                                                            (256, 256, 128, 0), (96, 512, 96, 7)])
 def test_polish_matches_oracle(gpu, rows, n, block_rows, max_blocks):
-    """Codes agree with the oracle on >= 99 % of the blocks, or on at least as many as the oracle
-    agrees with itself when only the rounding of its input factorisation changes (an fp64
-    factorisation rounded to fp32, and two random last-bit roundings of Vs): greedy block CD turns
-    last-bit differences of the gains into different decisions that cascade along a row."""
+    """Codes agree with the oracle on >= 99.9 % of the blocks, or on at least as many as the oracle
+    agrees with itself when only the rounding of its input factorisation changes (the lowest
+    agreement over an fp64 factorisation rounded to fp32 and two random last-bit roundings of Vs):
+    greedy block CD turns last-bit differences of the gains into different decisions that cascade
+    along a row."""
     Wr, Vs, x0, idx0, grid, H = _case(rows, n, f"e8cd:{rows}:{n}", jitter=0.15, with_h=True)
     ref_x, ref_idx, ref_err = _oracle_blocks(Wr, Vs, x0, idx0, grid, block_rows, 3, max_blocks)
     ctx = ops.e8p12_cd_prepare(Vs.to(gpu))
@@ -98,12 +99,11 @@ def test_polish_matches_oracle(gpu, rows, n, block_rows, max_blocks):
     assert bool((ea <= eb * (1 + 1e-5)).all())
     agree = float((idx == ref_idx).float().mean())
     floor = 1.0
-    if agree < 0.99:
-        for alt in (_vs_fp64_rounding(H, Vs), _vs_jitter(Vs, 1), _vs_jitter(Vs, 2)):
-            _, alt_idx, _ = _oracle_blocks(Wr, alt, x0, idx0, grid, block_rows, 3, max_blocks)
-            floor = min(floor, float((alt_idx == ref_idx).float().mean()))
+    for alt in (_vs_fp64_rounding(H, Vs), _vs_jitter(Vs, 1), _vs_jitter(Vs, 2)):
+        _, alt_idx, _ = _oracle_blocks(Wr, alt, x0, idx0, grid, block_rows, 3, max_blocks)
+        floor = min(floor, float((alt_idx == ref_idx).float().mean()))
     print(f"codes agree {agree:.5f} (reference floor {floor:.5f})")
-    assert agree >= min(0.99, floor), (agree, floor)
+    assert agree >= min(0.999, floor), (agree, floor)
     rel = abs(float(ea.mean()) - float(ref_err.mean())) / float(ref_err.mean())
     assert rel <= 5e-3, rel
     assert int(acc.sum()) > 0

@@ -8,11 +8,15 @@ of a seed comes from the agreements the reference shows with itself on that inpu
 
 * its two CD dispatches (the CUDA sweep and the CPU block CD, mpq/solver.py:299-366);
 * the CUDA-order solve with the greedy gain summed in row order instead of torch's reduction order;
-* that solve with every product rounded from fp64, and three times with every product entry then
-  moved at random to a neighbouring float (``oracle.uniform.products_in_fp64``): other valid fp32
-  roundings of the same algorithm, the kind of difference the GPU's products have.
+* that solve with every product rounded from fp64 (``oracle.uniform.products_in_fp64``): another
+  valid fp32 rounding of the same algorithm, the kind of difference the GPU's products have;
+* the unchanged oracle with another BLAS thread count: its products' sums partitioned differently.
+  On these layers that alone moves whole row blocks (one block's best-iterate stop moves from
+  iteration 3 to 11 on seed 4 with internal Hadamard): the oracle agrees with itself on only ~94.6 %
+  of the codes between 8, 4 and 1 threads there.
 
-The floor of a seed is the lowest of these agreements.
+The floor of a seed is the lowest of these agreements.  Two further variants, with every product
+entry then moved at random to a neighbouring float, are printed for information only.
 
 Codes must agree with the oracle on >= 99.9 % of entries or, averaged over the five seeds, on at least
 as many entries as the reference's floor.  The proxy loss tr((W-Q)H(W-Q)^T) must be within 0.5 % of
@@ -64,17 +68,26 @@ def test_config0_layer_matches_oracle(gpu, rotation, seed):
     agree = _agree(q.cpu(), ref["q_int"])
     proxy_ref = float(ref["proxy_rows"].sum())
     rel = (st["proxy_loss"] - proxy_ref) / proxy_ref
-    floor = 1.0
+    floor, jit = 1.0, []
     if agree < 0.999:
         variants = [_oracle(W, Hg, rotation, polish="block_cd"), _oracle(W, Hg, rotation, polish="twin_rowsum")]
         with ou.products_in_fp64():
             variants.append(_oracle(W, Hg, rotation, polish="twin_rowsum"))
-        for js in (1, 2, 3):
-            with ou.products_in_fp64(jitter_seed=js):
-                variants.append(_oracle(W, Hg, rotation, polish="twin_rowsum"))
+        # the same oracle code with another BLAS thread count (another partition of every product's sums)
+        prev = torch.get_num_threads()
+        torch.set_num_threads(4 if prev != 4 else 2)
+        try:
+            variants.append(_oracle(W, Hg, rotation))
+        finally:
+            torch.set_num_threads(prev)
         floor = min(_agree(v["q_int"], ref["q_int"]) for v in variants)
+        # reported only: the fp64 products moved at random to a neighbouring float
+        for js in (1, 2):
+            with ou.products_in_fp64(jitter_seed=js):
+                jit.append(_agree(_oracle(W, Hg, rotation, polish="twin_rowsum")["q_int"], ref["q_int"]))
     _RESULTS[(rotation, seed)] = (agree, floor)
-    print(f"seed {seed} {rotation}: codes {agree:.5f} (reference floor {floor:.5f}), proxy {rel:+.5f}")
+    print(f"seed {seed} {rotation}: codes {agree:.5f} (reference floor {floor:.5f}; last-bit jitter variants "
+          f"{' '.join(f'{j:.5f}' for j in jit) or '-'}), proxy {rel:+.5f}")
     assert torch.equal(s.cpu(), ref["scale"]) and torch.equal(z.cpu(), ref["zero"])
     assert torch.equal(g_idx.cpu(), torch.arange(1024, dtype=torch.int32) // 128)
     assert abs(rel) <= 0.005
@@ -150,4 +163,7 @@ def test_config0_layer_device_eigh(gpu, rotation, seed):
     print(f"seed {seed} {rotation} device eigh: proxy {rel:+.5f} vs LAPACK oracle, {rel_same:+.5f} vs oracle on "
           f"the device eigenbasis (oracle's own shift {shift:+.5f}); codes {_agree(q.cpu(), ref['q_int']):.5f}")
     assert torch.equal(s.cpu(), ref["scale"]) and torch.equal(z.cpu(), ref["zero"])
-    assert abs(rel) <= 0.005 or abs(rel_same) <= 0.005 <= abs(shift)
+    # within 0.5 % of the LAPACK-based oracle, or -- when the oracle itself moves by more than that on
+    # the device eigenbasis -- within 0.5 % of the moved oracle and no further from the LAPACK-based
+    # one than that move plus 0.5 %
+    assert abs(rel) <= 0.005 or (abs(rel_same) <= 0.005 <= abs(shift) and abs(rel) <= abs(shift) + 0.005)

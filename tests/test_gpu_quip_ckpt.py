@@ -24,11 +24,16 @@ def test_rht_matches_closed_form(gpu, m, n):
     H = X.T @ X / (2 * n)
     SU = torch.randint(0, 2, (n,), generator=g).float() * 2 - 1
     SV = torch.randint(0, 2, (m,), generator=g).float() * 2 - 1
-    Hr, Wr, lr, rr = quip_ckpt.incoherence_preprocess(H.to(gpu), W.to(gpu), SU.to(gpu), SV.to(gpu))
+    pow2 = (m & (m - 1)) == 0
+    if not pow2:  # quip-sharp's had-K transform is not provided: refused unless the block fallback is asked for
+        with pytest.raises(ValueError, match="not a power of two"):
+            quip_ckpt.incoherence_preprocess(H.to(gpu), W.to(gpu), SU.to(gpu), SV.to(gpu))
+    Hr, Wr, lr, rr = quip_ckpt.incoherence_preprocess(H.to(gpu), W.to(gpu), SU.to(gpu), SV.to(gpu),
+                                                      allow_block=not pow2)
     assert _rel(Hr.cpu(), rht.rht_h(H, SU)) < 1e-6
     assert _rel(Wr.cpu(), rht.rht_w(W, SU, SV)) < 1e-6
-    assert lr == "" and (rr == "") == ((m & (m - 1)) == 0)
-    back = quip_ckpt.incoherence_process(Wr, SU.to(gpu), SV.to(gpu))
+    assert rr == "" and (lr == "") == pow2
+    back = quip_ckpt.incoherence_process(Wr, SU.to(gpu), SV.to(gpu), allow_block=not pow2)
     assert _rel(back.cpu(), W) < 1e-6
     assert _rel(back.cpu(), rht.incoherence_process(Wr.cpu(), SU, SV)) < 1e-6
 
@@ -57,8 +62,12 @@ def test_layer_ckpt_layout_and_round_trip(gpu, tmp_path):
         "up": ([w(inter, hidden), w(inter, hidden)], H_attn),
         "down": ([w(hidden, inter)], H_down),
     }
+    # the fused qkv has 384 rows (not a power of two): refused without the block-Hadamard opt-in
+    with pytest.raises(ValueError, match="not a power of two"):
+        quip_ckpt.quantize_layer_to_ckpt(save_dir=str(tmp_path / "refused"), idx=3, linears={"qkv": linears["qkv"]},
+                                         cb=cb, args=_args(), device=gpu)
     errs = quip_ckpt.quantize_layer_to_ckpt(save_dir=str(tmp_path), idx=3, linears=linears, cb=cb, args=_args(),
-                                            device=gpu)
+                                            device=gpu, allow_block_hadamard=True)
     for name, (weights, H) in linears.items():
         path = tmp_path / f"3_{name}.pt"
         saved = torch.load(path, map_location="cpu", weights_only=True)
@@ -74,7 +83,12 @@ def test_layer_ckpt_layout_and_round_trip(gpu, tmp_path):
         if len(weights) == 1:
             assert saved["scales"] == [1.0]
         assert saved["input_fingerprint"]["w_shape"] == [m, n]
-        assert saved["rotation_family"] == "had" and saved["scaleWH"] is None
+        assert saved["scaleWH"] is None
+        pow2 = (m & (m - 1)) == 0
+        assert saved["rotation_family"] == ("had" if pow2 else "block_had")
+        assert saved["left_rotation_family"] == ("had" if pow2 else "block_had")
+        assert saved["left_had_dim"] == (m & -m) and saved["right_had_dim"] == n
+        assert saved["right_rotation_family"] == "had"
         assert saved["mpq_stats"]["solver"] == "vamp"
         # round trip: the decoded weights equal the writer's hatW up to the fp16 rounding of SV, and
         # approximate the original weights as a 2-bit code does
@@ -90,6 +104,10 @@ def test_layer_ckpt_layout_and_round_trip(gpu, tmp_path):
         back = rht.incoherence_process(hatWr, saved["SU"].float(), saved["SV"].float())
         dec_full = quip_ckpt.decompress_saved_quip(saved, cb, device=gpu).cpu()
         assert _rel(dec_full, back) < 1e-6
+        if not pow2:  # a block-Hadamard side recorded as plain 'had' is refused, not decoded another way
+            bad = dict(saved, left_rotation_family="had")
+            with pytest.raises(ValueError, match="had-K"):
+                quip_ckpt.decompress_saved_quip(bad, cb, device=gpu)
 
 
 def test_refuses_foreign_codebook_and_unsupported_modes(gpu):

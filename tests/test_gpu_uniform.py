@@ -253,7 +253,15 @@ def test_postprocess_gptq_polish_matches_oracle(gpu):
     assert float(e_got.mean()) <= float(e0.mean()) + 1e-6
     assert abs(float(e_got.mean()) - float(e_ref.mean())) <= 5e-3 * float(e_ref.mean())
     agree = float((got == ref).float().mean())
-    assert agree >= 0.98, agree
+    floor = 1.0
+    if agree < 0.999:
+        # the reference's other dispatch of the same polish (its CPU block CD, mpq/solver.py:336-366)
+        x_blk, _ = ou.block_cd_scalar(Q0, Yu, Vs, sf, zf, maxq, 3)
+        e_blk = ou.rankspace_error(Yu, x_blk, Vs)
+        ref_blk = torch.where((e_blk + 1e-12 < e0).unsqueeze(1), x_blk, Q0)
+        floor = float((ref_blk == ref).float().mean())
+    print(f"postprocess polish: codes {agree:.5f} (reference floor {floor:.5f})")
+    assert agree >= min(0.999, floor), (agree, floor)
     assert not st["module_fail_closed"] and st["polish_updates"] > 0
     assert torch.equal(got, sf * (qf.cpu().float() - zf))
 
