@@ -556,6 +556,18 @@ int mpq_uniform_cd_sweeps(int64_t rows, int64_t n, int maxq, int64_t block_rows,
                           int64_t group_size, const float* diag, const float* H, void* workspace,
                           int64_t workspace_bytes, mpq_stream_t stream);
 
+/*
+ * Column permutations of the activation-order path (desc_act, mpq/adapters/gptqmodel.py:733-740 and
+ * the inverse at :1090-1095, where the reference uses index_select): mpq_permute_columns gives
+ * out[:, c] = in[:, perm[c]] for a rows x cols row-major matrix of 1-byte (codes) or 4-byte (fp32)
+ * elements; mpq_permute_symmetric gives out[i][j] = in[perm[i]][perm[j]] (n x n fp32).  The kernels
+ * read through perm unchecked: every entry must lie in [0, cols) (resp. [0, n)), and out must not
+ * overlap in.
+ */
+int mpq_permute_columns(const void* in, int64_t rows, int64_t cols, const int32_t* perm, void* out, int elem_bytes,
+                        mpq_stream_t stream);
+int mpq_permute_symmetric(const float* in, int64_t n, const int32_t* perm, float* out, mpq_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Generic rank-space block coordinate descent                              */
 /* ------------------------------------------------------------------------ */

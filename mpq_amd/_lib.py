@@ -51,6 +51,8 @@ SIGNATURES = {
     "mpq_gemm_f64": (c_int, [c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_int, c_ptr, c_i64, c_double,
                              c_double, c_ptr, c_i64, c_ptr]),
     "mpq_release_thread_resources": (c_int, []),
+    "mpq_permute_columns": (c_int, [c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_int, c_ptr]),
+    "mpq_permute_symmetric": (c_int, [c_ptr, c_i64, c_ptr, c_ptr, c_ptr]),
     "mpq_bcd_prepare": (c_int, [c_i64, c_i64, c_int, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
     "mpq_bcd_gain": (c_int, [c_i64, c_i64, c_int, c_int, c_ptr, c_ptr, c_ptr, c_ptr]),
     "mpq_bcd_target": (c_int, [c_i64, c_i64, c_int, c_i64, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),

@@ -158,8 +158,9 @@ def run_mpq_quantization(
     Returns (Q fp32 rows x cols in the original basis, q_int uint8 (solver basis),
     scale_groups, zero_groups, g_idx int32, quant_time_s, stats) as the reference.
     ``precomputed_eigen`` = (floored descending eigenvalues, eigenvectors) of the
-    unrotated ``hessian_scale * H`` replaces the device ``eigh`` (used to compare
-    against another eigensolver's output on identical inputs).
+    unrotated ``hessian_scale * H`` -- with ``qcfg.desc_act``, of the rotated and
+    column-permuted Hessian the solver works on -- replaces the device ``eigh`` (used to
+    compare against another eigensolver's output on identical inputs).
     """
     start = time.time()
     device = W.device
@@ -177,8 +178,7 @@ def run_mpq_quantization(
     solver_name = str(getattr(mpq_cfg, "dispatch_solver", getattr(mpq_cfg, "solver", "vamp")) or "vamp").strip().lower()
     if solver_name != "vamp":
         raise ValueError(f"mpq_amd implements solver='vamp'; got {solver_name!r}.")
-    if bool(getattr(qcfg, "desc_act", False)):
-        raise ValueError("mpq_amd implements desc_act=False (the recipe default).")
+    use_activation_order = bool(getattr(qcfg, "desc_act", False))
     rotation = resolve_internal_rotation(
         requested=str(getattr(mpq_cfg, "rotation_mode", getattr(qcfg, "rotation", None) or "none")),
         cols=int(cols), module_name=str(module_name), seed=int(adapter_cfg.rotation_seed), device=device)
@@ -186,7 +186,12 @@ def run_mpq_quantization(
 
     H_work = float(adapter_cfg.hessian_scale) * H
     t0 = time.time()
-    if precomputed_eigen is not None:
+    if use_activation_order:
+        # the reference decomposes the rotated, permuted Hessian in the solver basis (:716-722 take the
+        # unrotated decomposition only without activation order); formed below
+        lam = S = V = Vs = None
+        eigen_floor = 0.0
+    elif precomputed_eigen is not None:
         lam = precomputed_eigen[0].to(device=device, dtype=torch.float32).contiguous()
         V = precomputed_eigen[1].to(device=device, dtype=torch.float32).contiguous()
         S = torch.sqrt(lam)
@@ -204,13 +209,41 @@ def run_mpq_quantization(
         W_work = apply_right_block_hadamard(W, signs=signs, had_dim=had)
         H_metric = apply_right_block_hadamard(apply_left_block_hadamard(H_work, signs=signs, had_dim=had),
                                               signs=signs, had_dim=had)
-        V = apply_left_block_hadamard(V, signs=signs, had_dim=had)
-        Vs = ops.scale_columns(V, S)  # Vs = V * S after the rotation (reference :887-890)
+        if V is not None:
+            V = apply_left_block_hadamard(V, signs=signs, had_dim=had)
+            Vs = ops.scale_columns(V, S)  # Vs = V * S after the rotation (reference :887-890)
     else:
         W_work = W.contiguous()
         H_metric = H_work.contiguous()
+    perm = invperm = None
+    if use_activation_order:
+        # columns by descending diagonal of the solver-basis Hessian (reference :733-740; a stable sort,
+        # ties by column index, where the reference's argsort is unstable)
+        diag = torch.diagonal(H_metric).to("cpu", torch.float64).tolist()
+        order = sorted(range(cols), key=lambda j: -diag[j])
+        perm = torch.tensor(order, dtype=torch.int32, device=device)
+        inv = [0] * cols
+        for pos, j in enumerate(order):
+            inv[j] = pos
+        invperm = torch.tensor(inv, dtype=torch.int32, device=device)
+        W_work = ops.permute_columns(W_work.to(torch.float32), perm)
+        H_metric = ops.permute_symmetric(H_metric, perm)
     dead = torch.diagonal(H_metric) == 0
     has_dead = bool(dead.any().item())
+    if use_activation_order and not has_dead:
+        t0 = time.time()
+        if precomputed_eigen is not None:
+            lam = precomputed_eigen[0].to(device=device, dtype=torch.float32).contiguous()
+            V = precomputed_eigen[1].to(device=device, dtype=torch.float32).contiguous()
+            S = torch.sqrt(lam)
+            Vs = ops.scale_columns(V, S)
+            eigen_floor = float(lam.min().item())
+        else:
+            lam, S, V, Vs, eigen_floor = vamp_hessian_eigen(H_metric, jitter_base=adapter_cfg.jitter_base,
+                                                            floor_scale=adapter_cfg.eigen_floor_scale,
+                                                            use_cache=bool(adapter_cfg.eigen_cache))
+        torch.cuda.synchronize(device)
+        timings["eigh_s"] += time.time() - t0
     if has_dead:
         H_metric = H_metric.clone()
         W_work = W_work.clone()
@@ -304,6 +337,11 @@ def run_mpq_quantization(
     delta = W_work - Q_work
     raw_rows = (ops.gemm(delta, H_metric) * delta).sum(dim=1)
     g_idx = torch.arange(cols, device=device, dtype=torch.int32) // int(group_size)
+    if invperm is not None:
+        # back to the column order of the solver basis (reference :1090-1095)
+        Q_work = ops.permute_columns(Q_work, invperm)
+        q_int = ops.permute_columns(q_int, invperm)
+        g_idx = g_idx.index_select(0, invperm.long())
     if rotation["mode"] == "block":
         Q = apply_right_block_hadamard_inverse(Q_work, signs=signs, had_dim=had)
     else:
@@ -332,7 +370,7 @@ def run_mpq_quantization(
         "rotation_internal": bool(rotation["internal"]),
         "rotation_block_dim": had,
         "rotation_fallback_reason": str(rotation["fallback_reason"]),
-        "desc_act": False,
+        "desc_act": bool(use_activation_order),
         "rows": int(rows),
         "cols": int(cols),
         "rank": int(S.numel()),

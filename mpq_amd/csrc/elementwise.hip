@@ -362,3 +362,55 @@ extern "C" int mpq_scale_columns(const float* in, int64_t rows, int64_t cols, co
   MPQ_LAUNCH_CHECK();
   return kOk;
 }
+
+// ---- column permutations (activation order, mpq/adapters/gptqmodel.py:733-740, :1090-1095) ------
+
+namespace {
+
+template <typename T>
+__global__ void permute_cols_kernel(const T* __restrict__ in, int64_t rows, int64_t cols,
+                                    const int32_t* __restrict__ perm, T* __restrict__ out) {
+  const int64_t total = rows * cols;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / cols, c = e - r * cols;
+    out[e] = in[r * cols + perm[c]];
+  }
+}
+
+__global__ void permute_sym_kernel(const float* __restrict__ in, int64_t n, const int32_t* __restrict__ perm,
+                                   float* __restrict__ out) {
+  const int64_t total = n * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = e / n, j = e - i * n;
+    out[e] = in[(int64_t)perm[i] * n + perm[j]];
+  }
+}
+
+}  // namespace
+
+// out[:, c] = in[:, perm[c]] for a rows x cols row-major matrix of 1- or 4-byte elements.
+extern "C" int mpq_permute_columns(const void* in, int64_t rows, int64_t cols, const int32_t* perm, void* out,
+                                   int elem_bytes, hipStream_t stream) {
+  MPQ_CHECK_ARG(rows >= 0 && cols >= 0 && (elem_bytes == 1 || elem_bytes == 4), "mpq_permute_columns: bad shape");
+  if (rows == 0 || cols == 0) return kOk;
+  MPQ_CHECK_ARG(in && perm && out && in != out, "mpq_permute_columns: null or aliased pointer");
+  if (elem_bytes == 4)
+    hipLaunchKernelGGL(permute_cols_kernel<float>, dim3(grid_for(rows * cols)), dim3(256), 0, stream,
+                       static_cast<const float*>(in), rows, cols, perm, static_cast<float*>(out));
+  else
+    hipLaunchKernelGGL(permute_cols_kernel<uint8_t>, dim3(grid_for(rows * cols)), dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(in), rows, cols, perm, static_cast<uint8_t*>(out));
+  MPQ_LAUNCH_CHECK();
+  return kOk;
+}
+
+// out[i][j] = in[perm[i]][perm[j]] (n x n).
+extern "C" int mpq_permute_symmetric(const float* in, int64_t n, const int32_t* perm, float* out,
+                                     hipStream_t stream) {
+  MPQ_CHECK_ARG(n >= 0, "mpq_permute_symmetric: bad shape");
+  if (n == 0) return kOk;
+  MPQ_CHECK_ARG(in && perm && out && in != out, "mpq_permute_symmetric: null or aliased pointer");
+  hipLaunchKernelGGL(permute_sym_kernel, dim3(grid_for(n * n)), dim3(256), 0, stream, in, n, perm, out);
+  MPQ_LAUNCH_CHECK();
+  return kOk;
+}

@@ -80,6 +80,43 @@ def gemm(A: torch.Tensor, B: torch.Tensor, *, trans_b: bool = False, b_rows: Opt
     return out
 
 
+def _check_index_range(idx: torch.Tensor, bound: int) -> None:
+    """The kernels read through ``idx`` unchecked: every entry must lie in [0, bound)."""
+    if idx.numel() and (int(idx.min().item()) < 0 or int(idx.max().item()) >= bound):
+        raise ValueError(f"index entries must lie in [0, {bound})")
+
+
+def permute_columns(X: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
+    """out[:, c] = X[:, perm[c]] (fp32 or uint8 rows x cols)."""
+    dev = _dev(X, perm)
+    if X.dtype not in (F32, torch.uint8) or X.dim() != 2:
+        raise ValueError("permute_columns takes a 2-D float32 or uint8 tensor")
+    X = X.contiguous()
+    rows, cols = X.shape
+    perm = perm.to(device=dev, dtype=torch.int32).contiguous()
+    if int(perm.numel()) != cols:
+        raise ValueError("perm must hold one entry per column")
+    _check_index_range(perm, cols)
+    out = torch.empty_like(X)
+    _lib.call("mpq_permute_columns", _lib.ptr(X), rows, cols, _lib.ptr(perm), _lib.ptr(out),
+              1 if X.dtype == torch.uint8 else 4, _stream(dev))
+    return out
+
+
+def permute_symmetric(H: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
+    """out[i][j] = H[perm[i]][perm[j]] (fp32 n x n)."""
+    dev = _dev(H, perm)
+    H = _f32c(H)
+    n = int(H.shape[0])
+    perm = perm.to(device=dev, dtype=torch.int32).contiguous()
+    if tuple(H.shape) != (n, n) or int(perm.numel()) != n:
+        raise ValueError("permute_symmetric takes an n x n matrix and n entries")
+    _check_index_range(perm, n)
+    out = torch.empty_like(H)
+    _lib.call("mpq_permute_symmetric", _lib.ptr(H), n, _lib.ptr(perm), _lib.ptr(out), _stream(dev))
+    return out
+
+
 def gemm_f64(A: torch.Tensor, B: torch.Tensor, *, trans_b: bool = False, out: Optional[torch.Tensor] = None,
              alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
     """C = alpha * A @ op(B) + beta * C in fp64 on the fp64 matrix cores (the eigensolver's kernel)."""

@@ -15,7 +15,7 @@ torch CPU ops in the reference's operation order:
 * ``solve_uniform_rankspace_vamp``  mpq/solver.py:426-830
 * ``gptq_find_params``           GPTQ asymmetric min-max quantizer (GPTQModel Quantizer.find_params,
                                  un-vendored: parity unpinned, standard published GPTQ formula)
-* ``run_mpq_quantization``       mpq/adapters/gptqmodel.py:650-1163 (vamp solver, no desc_act)
+* ``run_mpq_quantization``       mpq/adapters/gptqmodel.py:650-1163 (vamp solver, desc_act optional)
 """
 from __future__ import annotations
 
@@ -461,22 +461,34 @@ def rotation_plan(n: int, module_name: str, seed: int = 0):
 
 
 def run_mpq_quantization(W, H, bits, group_size, module_name, cfg, rotation="none", block_rows=128,
-                         polish: str = "twin", hessian_scale=0.5):
-    """CPU restatement of the per-linear scalar driver; returns dict with Q, q_int, scale, zero, stats."""
+                         polish: str = "twin", hessian_scale=0.5, desc_act: bool = False):
+    """CPU restatement of the per-linear scalar driver; returns dict with Q, q_int, scale, zero, stats.
+    ``desc_act``: columns in descending order of the solver-basis Hessian's diagonal (stable sort;
+    mpq/adapters/gptqmodel.py:733-740), the decomposition of that permuted Hessian (:716-722 apply
+    only without it), the results permuted back (:1090-1095)."""
     W = W.to(torch.float32)
     rows, cols = W.shape
     maxq = 2 ** bits - 1
     H_work = float(hessian_scale) * H.to(torch.float32)
-    lam, V, floor = hessian_eigen(H_work)
+    if not desc_act:
+        lam, V, floor = hessian_eigen(H_work)
     plan = rotation_plan(cols, module_name) if rotation == "internal_hadamard" else None
     if plan is not None:
         signs, had = plan
         W_work = hadamard_rows(W * signs.view(1, -1), had)
         Hm = hadamard_rows(H_work.T.contiguous() * signs.view(1, -1), had).T.contiguous()
         Hm = hadamard_rows(Hm * signs.view(1, -1), had)
-        V = hadamard_rows(V.T.contiguous() * signs.view(1, -1), had).T.contiguous()
+        if not desc_act:
+            V = hadamard_rows(V.T.contiguous() * signs.view(1, -1), had).T.contiguous()
     else:
         W_work, Hm = W, H_work
+    invperm = None
+    if desc_act:
+        perm = torch.argsort(torch.diagonal(Hm), descending=True, stable=True)
+        invperm = torch.argsort(perm)
+        W_work = W_work.index_select(1, perm).contiguous()
+        Hm = Hm.index_select(0, perm).index_select(1, perm).contiguous()
+        lam, V, floor = hessian_eigen(Hm)
     S = torch.sqrt(lam)
     Vs = V * S.unsqueeze(0)
     Vh = V.T.contiguous()
@@ -519,11 +531,16 @@ def run_mpq_quantization(W, H, bits, group_size, module_name, cfg, rotation="non
         traces.append(tr)
     delta = W_work - Q_work
     proxy = (delta.matmul(Hm) * delta).sum(dim=1)
+    g_idx = torch.arange(cols, dtype=torch.int32) // int(group_size)
+    if invperm is not None:
+        Q_work = Q_work.index_select(1, invperm)
+        q_int = q_int.index_select(1, invperm)
+        g_idx = g_idx.index_select(0, invperm)
     if plan is not None:
         signs, had = plan
         Q = hadamard_rows(Q_work, had) * signs.view(1, -1)
     else:
         Q = Q_work
-    return {"Q": Q, "Q_work": Q_work, "q_int": q_int, "scale": scale_g, "zero": zero_g, "obs_initial": obs,
+    return {"Q": Q, "Q_work": Q_work, "q_int": q_int, "scale": scale_g, "zero": zero_g, "g_idx": g_idx, "obs_initial": obs,
             "obs_final": obs_block, "proxy_rows": proxy, "traces": traces, "W_work": W_work, "H_metric": Hm,
-            "V": V, "S": S}
+            "V": V, "S": S, "eigen_floor": floor}

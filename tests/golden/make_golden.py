@@ -214,11 +214,13 @@ def udriver_golden(ref_root: str) -> None:
     print("rademacher signs written")
 
     rows, cols = 384, 256
-    for rotation, bits in (("none", 4), ("internal_hadamard", 3)):
+    for rotation, bits, desc_act in (("none", 4, False), ("internal_hadamard", 3, False),
+                                     ("internal_hadamard", 4, True)):
         name = "model.layers.0.mlp.up_proj"
-        W, H = make_layer(rows, cols, tokens=1024, seed_key=f"golden:udriver:{rotation}")
+        tag = rotation + ("_desc_act" if desc_act else "")
+        W, H = make_layer(rows, cols, tokens=1024, seed_key=f"golden:udriver:{tag}")
         Hg = 2.0 * H  # GPTQModel convention: the adapter halves it (mpq/adapters/gptqmodel.py:702)
-        qcfg = types.SimpleNamespace(bits=bits, group_size=128, desc_act=False,
+        qcfg = types.SimpleNamespace(bits=bits, group_size=128, desc_act=desc_act,
                                      mpq=types.SimpleNamespace(rotation_mode=rotation, solver="vamp"))
         vcfg = RefUCfg(iters=16, damping=0.5, prior_tau=0.2, polish_sweeps=3, polish_mode="block_cd",
                        vamp_backend="eager", block_cd_backend="eager")
@@ -228,7 +230,7 @@ def udriver_golden(ref_root: str) -> None:
         bst = st["block_stats"]
         # W is rebuilt from its seed by the test (a draw from torch's CPU generator); H is stored
         # (X^T X on the CPU rounds by the BLAS partition)
-        np.savez_compressed(os.path.join(HERE, f"udriver_{rotation}.npz"), **_np({
+        np.savez_compressed(os.path.join(HERE, f"udriver_{tag}.npz"), **_np({
             "bits": bits, "H": Hg, "Q": Q, "q_int": q, "scale": sc, "zero": zr, "g_idx": g_idx,
             "obs_initial": float(st["obs_precision_initial"]), "obs_final": float(st["obs_precision_final"]),
             "eigen_floor": float(st["eigen_floor"]), "layer_error_sum": float(st["layer_error_sum"]),
@@ -236,7 +238,7 @@ def udriver_golden(ref_root: str) -> None:
             "block_best_iter": torch.tensor([int(b["best_iter"]) for b in bst]),
             "block_stop_iter": torch.tensor([int(b["stop_iter"]) for b in bst]),
             "polish_updates": torch.tensor([float(b.get("polish_updates", 0.0)) for b in bst], dtype=torch.float64)}))
-        print("udriver", rotation, "obs", st["obs_precision_initial"], "->", st["obs_precision_final"],
+        print("udriver", tag, "obs", st["obs_precision_initial"], "->", st["obs_precision_final"],
               "stops", [b["stop_iter"] for b in bst])
 
 

@@ -180,14 +180,12 @@ def test_refine_codebook_against_reference_golden(gpu):
     assert abs(s_got - s_ref) <= 5e-3 * s_ref
     # codes: >= 99.9 % of the golden's, or as many as the oracle (which reproduces the golden exactly)
     # keeps when only the fp32 rounding of its fp64 eigenvectors changes -- the one input the GPU forms
-    # differently (its own fp64 eigensolver); at the precision clamp these roundings decide codes
-    floor = 1.0
-    if agree < 0.999:
-        grid = torch.from_numpy(codebook.grid_numpy())
-        cache = oe8.factor_cache(grid)
-        cfg = dict(iters=16, damping=0.5, prior_tau=0.25, polish_sweeps=3)
-        for seed in (1, 2, 3):
-            _, alt_idx, _ = oe8.refine_codebook(Wr, H, grid, cache, cfg, block_rows=128, v_jitter_seed=seed)
-            floor = min(floor, float((alt_idx == ref_idx).float().mean()))
+    # differently (its own fp64 eigensolver); at the precision clamp such roundings decide codes.  The
+    # floor is recorded by tests/golden/make_refine_floor.py (two of eight one-ulp perturbations move
+    # the oracle to 97.95 %).
+    import json
+
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "e8p12_refine_floor.json")) as fh:
+        floor = float(json.load(fh)["floor"])
     print(f"refine golden codes {agree:.5f} (oracle floor {floor:.5f})")
     assert agree >= min(0.999, floor), (agree, floor)

@@ -30,21 +30,27 @@ def test_rotation_plan_reproduces_reference_signs():
         assert np.array_equal(signs.numpy(), d[k]), k
 
 
-@pytest.mark.parametrize("rotation", ["none", "internal_hadamard"])
-def test_driver_reproduces_reference(rotation):
-    d = np.load(os.path.join(HERE, f"udriver_{rotation}.npz"))
+@pytest.mark.parametrize("rotation,desc_act", [("none", False), ("internal_hadamard", False),
+                                               ("internal_hadamard", True)])
+def test_driver_reproduces_reference(rotation, desc_act):
+    tag = rotation + ("_desc_act" if desc_act else "")
+    d = np.load(os.path.join(HERE, f"udriver_{tag}.npz"))
     bits = int(d["bits"])
-    W, _ = make_layer(384, 256, tokens=1024, seed_key=f"golden:udriver:{rotation}")
+    W, _ = make_layer(384, 256, tokens=1024, seed_key=f"golden:udriver:{tag}")
     H = torch.from_numpy(d["H"])
     prev = torch.get_num_threads()
     torch.set_num_threads(1)  # the reference's vectors were written on one thread
     try:
-        r = ou.run_mpq_quantization(W, H, bits, 128, NAME, dict(RECIPE), rotation=rotation, polish="block_cd")
+        r = ou.run_mpq_quantization(W, H, bits, 128, NAME, dict(RECIPE), rotation=rotation, polish="block_cd",
+                                    desc_act=desc_act)
         _, _, floor = ou.hessian_eigen(0.5 * H)
     finally:
         torch.set_num_threads(prev)
+    if desc_act:  # decomposed after the rotation and the column order (mpq/adapters/gptqmodel.py:716-722, :886-892)
+        floor = r["eigen_floor"]
     assert np.array_equal(r["scale"].numpy(), d["scale"])
     assert np.array_equal(r["zero"].numpy(), d["zero"])
+    assert np.array_equal(r["g_idx"].numpy(), d["g_idx"])
     assert r["obs_initial"] == float(d["obs_initial"])
     assert [t["best_iter"] for t in r["traces"]] == d["block_best_iter"].tolist()
     assert [t["stop_iter"] for t in r["traces"]] == d["block_stop_iter"].tolist()
