@@ -515,8 +515,9 @@ def postprocess_gptq_quantization(
 
     The codes ``round(Q_init / s + z)`` are polished in the rank space of ``hessian_scale * H`` with
     one greedy order over all rows, each row keeps the polished codes only if its error drops, and
-    the module falls back to ``Q_init`` when the mean error would rise (fail-closed).  Only the
-    contiguous group layout (``g_idx[i] = i // group_size``, no act-order) is provided.
+    the module falls back to ``Q_init`` when the mean error would rise (fail-closed).  Column c
+    takes group ``g_idx[c]``'s scale and zero (the reference's ``_expand_group_params_from_gidx``):
+    with GPTQModel's act-order layout the parameters are expanded to one per column.
     Returns ``(Q, q_int, scale_groups, zero_groups, g_idx, time_s, stats)``.
     """
     start = time.time()
@@ -535,14 +536,25 @@ def postprocess_gptq_quantization(
     group_size = int(getattr(qcfg, "group_size", cols) or cols)
     if group_size <= 0:
         group_size = cols
+    if int(g_idx.numel()) != cols:
+        raise ValueError(f"g_idx must hold one group per column ({cols}), got {int(g_idx.numel())}")
+    n_groups = int(scale_groups.shape[1])
+    if tuple(scale_groups.shape) != (rows, n_groups) or tuple(zero_groups.shape) != (rows, n_groups):
+        raise ValueError("scale_groups and zero_groups must be rows x groups")
+    if int(g_idx.min().item()) < 0 or int(g_idx.max().item()) >= n_groups:
+        raise ValueError(f"g_idx entries must lie in [0, {n_groups})")
     expected = torch.arange(cols, device=device, dtype=torch.int32) // group_size
-    if int(g_idx.numel()) != cols or not bool(torch.equal(g_idx, expected)):
-        raise ValueError("mpq_amd postprocess supports the contiguous group layout (g_idx = i // group_size) only.")
+    if n_groups == (cols + group_size - 1) // group_size and bool(torch.equal(g_idx, expected)):
+        sg_w, zg_w, gs_w = scale_groups, zero_groups, group_size
+    else:  # act-order (or any other) layout: one scale and zero per column
+        sg_w = scale_groups.index_select(1, g_idx.long()).contiguous()
+        zg_w = zero_groups.index_select(1, g_idx.long()).contiguous()
+        gs_w = 1
     mpq_cfg = getattr(qcfg, "mpq", None)
     H_work = float(adapter_cfg.hessian_scale) * H
     _, S, V, Vs, eigen_floor = vamp_hessian_eigen(H_work, jitter_base=adapter_cfg.jitter_base,
                                                   floor_scale=adapter_cfg.eigen_floor_scale)
-    q_init, _ = ops.uniform_rtn(Q_init, scale_groups.clamp_min(1e-12), zero_groups, group_size, maxq, want_x=False)
+    q_init, _ = ops.uniform_rtn(Q_init, sg_w.clamp_min(1e-12), zg_w, gs_w, maxq, want_x=False)
     polish_mode = str(getattr(mpq_cfg, "polish_mode", "none") or "none").strip().lower()
     polish_sweeps = int(getattr(mpq_cfg, "polish_sweeps", 0) or 0)
     mode = _resolve_polish_mode(sweeps=polish_sweeps, mode=polish_mode)
@@ -558,14 +570,13 @@ def postprocess_gptq_quantization(
     raw_before = (ops.gemm(delta0, H_work) * delta0).sum(dim=1)
     polish_updates = 0.0
     if mode == "block_cd":
-        q_pol, eb, ea, imp, acc = ops.uniform_cd_polish(None, q_init, scale_groups, zero_groups, group_size, maxq,
+        q_pol, eb, ea, imp, acc = ops.uniform_cd_polish(None, q_init, sg_w, zg_w, gs_w, maxq,
                                                         Vs, H_work, block_rows=rows, sweeps=polish_sweeps,
                                                         select=True, Yu=Yu, x_in=Q_init)
         err_after = ea
         polish_updates = float(acc.sum().item())
         q_final = q_pol
-        Q_final = torch.where(imp.bool().unsqueeze(1), ops.dequant(q_pol, scale_groups, zero_groups, group_size),
-                              Q_init)
+        Q_final = torch.where(imp.bool().unsqueeze(1), ops.dequant(q_pol, sg_w, zg_w, gs_w), Q_init)
     else:
         err_after = err_before
         q_final = q_init

@@ -215,17 +215,27 @@ def test_cd_polish_x6_products_match_oracle(gpu):
         ops.uniform_cd_polish(*args, block_rows=128, sweeps=3, select=False, S=Sg)
 
 
-def test_postprocess_gptq_polish_matches_oracle(gpu):
+@pytest.mark.parametrize("layout", ["contiguous", "act_order"])
+def test_postprocess_gptq_polish_matches_oracle(gpu, layout):
     """postprocess_gptq_quantization (mpq/adapters/gptqmodel.py:1250-1470): one greedy order over all
-    rows, keep-if-better per row, module fail-closed; against the oracle's scalar CD."""
+    rows, keep-if-better per row, module fail-closed; against the oracle's scalar CD.  ``act_order``:
+    GPTQModel's desc_act layout, groups formed over the columns in descending order of diag(H) and
+    column c taking group g_idx[c] (the reference's _expand_group_params_from_gidx)."""
     from mpq_amd.adapters.gptqmodel import postprocess_gptq_quantization
 
     rows, n, gs, bits = 96, 256, 128, 3
     maxq = 2 ** bits - 1
     W, H = make_layer(rows, n, tokens=1024, seed_key="post:gptq")
-    sg, zg = ou.gptq_find_params(W.reshape(-1, gs), maxq)
+    if layout == "act_order":
+        perm = torch.argsort(torch.diagonal(H), descending=True, stable=True)
+        g_idx = (torch.argsort(perm) // gs).to(torch.int32)
+        Wp = W[:, perm]
+    else:
+        g_idx = torch.arange(n, dtype=torch.int32) // gs
+        Wp = W
+    sg, zg = ou.gptq_find_params(Wp.reshape(-1, gs), maxq)
     sg, zg = sg.reshape(rows, n // gs), zg.reshape(rows, n // gs)
-    sf, zf = sg.repeat_interleave(gs, 1), zg.repeat_interleave(gs, 1)
+    sf, zf = sg[:, g_idx.long()], zg[:, g_idx.long()]
     Q0 = sf * (torch.clamp(torch.round(W / sf) + zf, 0, maxq) - zf)
 
     class Q:
@@ -235,7 +245,6 @@ def test_postprocess_gptq_polish_matches_oracle(gpu):
     qcfg.bits, qcfg.group_size = bits, gs
     qcfg.mpq = Q()
     qcfg.mpq.polish_mode, qcfg.mpq.polish_sweeps = "block_cd", 3
-    g_idx = torch.arange(n, dtype=torch.int32) // gs
     Qf, qf, _, _, _, _, st = postprocess_gptq_quantization(W=W.to(gpu), H=(2.0 * H).to(gpu), Q_init=Q0.to(gpu),
                                                            scale_groups=sg.to(gpu), zero_groups=zg.to(gpu),
                                                            g_idx=g_idx.to(gpu), qcfg=qcfg, module_name="m")
@@ -260,7 +269,7 @@ def test_postprocess_gptq_polish_matches_oracle(gpu):
         e_blk = ou.rankspace_error(Yu, x_blk, Vs)
         ref_blk = torch.where((e_blk + 1e-12 < e0).unsqueeze(1), x_blk, Q0)
         floor = float((ref_blk == ref).float().mean())
-    print(f"postprocess polish: codes {agree:.5f} (reference floor {floor:.5f})")
+    print(f"postprocess polish ({layout}): codes {agree:.5f} (reference floor {floor:.5f})")
     assert agree >= min(0.999, floor), (agree, floor)
     assert not st["module_fail_closed"] and st["polish_updates"] > 0
     assert torch.equal(got, sf * (qf.cpu().float() - zf))
