@@ -336,7 +336,10 @@ def micro_bench(name, device, reps=50):
     * ``e8p12_map``: the nearest-codeword search on the 2^24 vectors of config 1;
     * ``eigh``: the eigendecomposition (``mpq_syevd``, automatic method: two-stage at this size) of
       a config-4-sized Hessian, n = 14336, H = X^T X / T with 2n Gaussian tokens of log-normal
-      channel scales.
+      channel scales;
+    * ``e8p12_cd``: one gram-metric CD sweep (``mpq_e8p12_cd_polish``) over a config-3 linear of the
+      up/gate shape's width, 2048 rows x 2048 columns (256 greedy steps of ``e8_cd_step_kernel``),
+      from the nearest-codeword start, Vs from the eigendecomposition of a Student-t Hessian.
 
     Prints one JSON line with the average per-call time (HIP events on the launch stream)."""
     import torch
@@ -379,8 +382,25 @@ def micro_bench(name, device, reps=50):
         def go():
             return ops.syevd(H)
         unit, per = "matrices", 1
+    elif name == "e8p12_cd":
+        from mpq_amd import ops
+
+        rows, n = 2048, 2048
+        H = make_student_hessian(n, 8192, 300 + n, device)
+        lam, V = ops.syevd(H)
+        Vs = V * lam.clamp_min(1e-6 * float(lam.max())).sqrt().unsqueeze(0)
+        cb = codebook.E8P12_codebook(device=device)
+        Wr = torch.randn(rows, n, device=device, generator=g)
+        x0, idx0 = cb.quantize(Wr.reshape(-1, 8))
+        x0, idx0 = x0.view(rows, n), idx0.view(rows, n // 8)
+        ctx = ops.e8p12_cd_prepare(Vs)
+        reps = min(reps, 5)
+
+        def go():
+            return ops.e8p12_cd_polish(x0, idx0, Vs, ctx, sweeps=1, block_rows=128, W=Wr)
+        unit, per = "row_blocks", rows * n // 8
     else:
-        raise SystemExit(f"unknown --micro {name!r}; choose e8p12_posterior, e8p12_map or eigh")
+        raise SystemExit(f"unknown --micro {name!r}; choose e8p12_posterior, e8p12_map, eigh or e8p12_cd")
     for _ in range(5):
         go()
     torch.cuda.synchronize()
@@ -612,7 +632,7 @@ def main():
                     help="only the dominant-kernel timing plus a 1 GiB device copy (the PMC scaling reference)")
     ap.add_argument("--tokens", type=int, default=128 * 2048)
     ap.add_argument("--micro", default=None,
-                    help="time one kernel alone (e8p12_posterior | e8p12_map) and exit; for profiler runs")
+                    help="time one kernel alone (e8p12_posterior | e8p12_map | eigh | e8p12_cd) and exit; for profiler runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the per-layer solve on a single MI355X; "

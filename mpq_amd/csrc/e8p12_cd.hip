@@ -41,6 +41,7 @@
 #include "gemm.h"
 #include "kernels.h"
 #include "mpq_amd.h"
+#include "x6_split.h"
 
 namespace mpq {
 namespace {
@@ -48,11 +49,13 @@ namespace {
 constexpr int kRT = 32;        // rows per tile
 constexpr int kWS = 16;        // greedy steps per window
 constexpr int kDS = 8 * kWS;   // delta row stride
-constexpr int kMaxCS = 16384;  // codewords per chunk (LDS table of |L^T c|^2)
+constexpr int kNChunk = 16;    // codeword chunks per greedy step (work-groups per row tile)
+constexpr int kCS = 65536 / kNChunk;  // codewords per chunk (LDS table of |L^T c|^2, 16 KB)
 constexpr int kMeta = 192;     // G, L, Gi (8x8 each) per block
 constexpr int kCodes = 65536;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 inline int64_t a64(int64_t v) { return (v + 63) / 64 * 64; }
 
@@ -68,7 +71,8 @@ __device__ __forceinline__ float sum8(float v) {
 // preparation (per layer): codebook grid, per-block G/L/Gi, |L^T c|^2 tables
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void grid_kernel(float* __restrict__ grid) {
+// grid (65536 x 8) and the abs-pattern table (256 x 8: |coordinate| - 1/4 magnitudes a of pattern k)
+__global__ __launch_bounds__(256) void grid_kernel(float* __restrict__ grid, float* __restrict__ abs_tab) {
   const int idx = blockIdx.x * 256 + threadIdx.x;
   const int k = idx >> 8;
   const int s = idx & 255;
@@ -79,6 +83,7 @@ __global__ __launch_bounds__(256) void grid_kernel(float* __restrict__ grid) {
   for (int d = 0; d < 8; ++d) {
     const float a = 0.5f * (float)kE8Abs2[k][d];
     grid[(int64_t)idx * 8 + d] = sh + (((signs >> d) & 1) ? -a : a);
+    if (s == 0) abs_tab[k * 8 + d] = a;
   }
 }
 
@@ -239,6 +244,7 @@ struct StepArgs {
   const float* cgc;      // nb x 65536
   const float* H;        // n x n
   const float* grid;     // 65536 x 8
+  const float* abs_tab;  // 256 x 8 abs-pattern magnitudes
   const float* rhs;      // rows x n, current at the window start
   float* x;              // rows x n
   int64_t* idx;          // rows x nb
@@ -246,14 +252,20 @@ struct StepArgs {
   float* D;              // rows x kDS
   float* Rt;             // 2 x rows x 8: rhs of the step
   float* Xt;             // 2 x rows x 8: x block of the step before the decision
-  float* ps;             // rows x 16 partial scores
-  int32_t* pi;           // rows x 16 partial indices
+  float* ps;             // 2 x rows x 16 partial scores (by step parity)
+  int32_t* pi;           // 2 x rows x 16 partial indices (by step parity)
   int32_t* accepted;     // rows
 };
 
 __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
-  __shared__ float s_cgc[kMaxCS];
-  __shared__ float s_abs[256 * 8];
+  // s_cgc: the chunk's |L^T c|^2 for the argmin; before it, the same space holds s_D, the window's
+  // deltas of the tile's rows (row r, step s, coordinate d at 8 kWS r + 8 s + d)
+  __shared__ __align__(16) float s_cgc[kCS];
+  static_assert(kCS >= kRT * 8 * kWS, "s_D does not fit in s_cgc");
+  float* const s_D = s_cgc;
+  __shared__ __align__(16) float s_abs[(kCS / 256) * 8];  // magnitudes of the chunk's kCS / 256 abs patterns
+  __shared__ __align__(16) float s_H[kWS * 64];  // H[8 j_s + d][8 j + e] of the window's steps s, entry 64 s + 8 e + d
+  __shared__ float s_M[128];       // block j's L (64) and Gi (64)
   __shared__ float s_u[kRT][8];
   __shared__ float s_bs[4][kRT];
   __shared__ int s_bi[4][kRT];
@@ -272,34 +284,97 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
   const int32_t* ord = a.order + rb * a.nb;
   const int64_t rows = a.rows, n = a.n;
 
-  float dl = 0.f;  // accepted delta of the finalized step, coordinate e
+  // ---- finalize, part 1 (loads): the previous step's decision needs, per row, the best of all
+  // chunks' partials (in the buffer of that launch's parity: this launch's work-groups write the
+  // other one, so a work-group that finishes early cannot overwrite what a later one still reads),
+  // its codeword, the step's x block and rhs, the residual norm and the block's gram G.
+  int jp = 0, bi = 0;
+  float cand = 0.f, fx = 0.f, fr = 0.f, r0 = 0.f;
+  float gm[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) gm[d] = 0.f;
   if (a.finalize) {
-    const int jp = ord[a.fin_t];
+    jp = ord[a.fin_t];
     const float* Gm = a.meta + (int64_t)jp * kMeta;
-    float bs = a.ps[row * 16];
-    int bi = a.pi[row * 16];
-    for (int c = 1; c < a.nparts; ++c) {
-      const float s = a.ps[row * 16 + c];
-      if (s < bs) {
-        bs = s;
-        bi = a.pi[row * 16 + c];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) gm[d] = Gm[d * 8 + e];
+    fx = a.Xt[(int64_t)a.fin_par * rows * 8 + row * 8 + e];
+    fr = a.Rt[(int64_t)a.fin_par * rows * 8 + row * 8 + e];
+    r0 = a.res[(int64_t)a.fin_par * rows + row];
+    const float4* fps = reinterpret_cast<const float4*>(a.ps + (int64_t)a.fin_par * rows * 16 + row * 16);
+    const int4* fpi = reinterpret_cast<const int4*>(a.pi + (int64_t)a.fin_par * rows * 16 + row * 16);
+    float ps[16];
+    int pi[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 v = fps[q];
+      const int4 w = fpi[q];
+      ps[4 * q] = v.x; ps[4 * q + 1] = v.y; ps[4 * q + 2] = v.z; ps[4 * q + 3] = v.w;
+      pi[4 * q] = w.x; pi[4 * q + 1] = w.y; pi[4 * q + 2] = w.z; pi[4 * q + 3] = w.w;
+    }
+    // earlier chunk wins ties
+    float bs = ps[0];
+    bi = pi[0];
+#pragma unroll
+    for (int c = 1; c < kNChunk; ++c) {
+      if (ps[c] < bs) {
+        bs = ps[c];
+        bi = pi[c];
       }
     }
-    const float cand = a.grid[(int64_t)bi * 8 + e];
-    const float xb = a.Xt[(int64_t)a.fin_par * rows * 8 + row * 8 + e];
-    const float rh = a.Rt[(int64_t)a.fin_par * rows * 8 + row * 8 + e];
-    const float dv = cand - xb;
+    cand = a.grid[(int64_t)bi * 8 + e];
+  }
+
+  // Loads of the compute phase, issued before the finalize's arithmetic so that they overlap it:
+  // none of them reads what the finalize writes (block j is not the finalized block; D slots
+  // s < p - 1 were written by earlier launches)
+  static_assert(kCS / 4 / 256 == 4 && kWS * 64 / 256 == 4, "staging assumes 4 loads per thread");
+  const int j = a.compute ? ord[a.t] : 0;
+  const int c0 = blockIdx.y * kCS;
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 cg0 = z4, cg1 = z4, cg2 = z4, cg3 = z4;
+  float hv0 = 0.f, hv1 = 0.f, hv2 = 0.f, hv3 = 0.f;
+  float dv[kWS - 1];
+#pragma unroll
+  for (int s = 0; s < kWS - 1; ++s) dv[s] = 0.f;
+  float mv = 0.f, rh = 0.f, xb = 0.f;
+  float4 ab0 = z4;
+  if (a.compute) {
+    const float4* src = reinterpret_cast<const float4*>(a.cgc + (int64_t)j * kCodes + c0) + tid;
+    cg0 = src[0];
+    cg1 = src[256];
+    cg2 = src[512];
+    cg3 = src[768];
+    if (tid < kCS / 256 * 2) ab0 = reinterpret_cast<const float4*>(a.abs_tab)[c0 / 256 * 2 + tid];
+    // H block entry (s, d, e) = i = 64 s + 8 d + e, i = tid + 256 q; s = wave + 4 q is wave-uniform
+    const int64_t hcol = 8 * (int64_t)j + (tid & 7);
+    const int hd = (tid >> 3) & 7, hs = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int32_t* wo = ord + a.w0 + hs;
+    if (hs < a.p) hv0 = a.H[(8 * (int64_t)wo[0] + hd) * n + hcol];
+    if (hs + 4 < a.p) hv1 = a.H[(8 * (int64_t)wo[4] + hd) * n + hcol];
+    if (hs + 8 < a.p) hv2 = a.H[(8 * (int64_t)wo[8] + hd) * n + hcol];
+    if (hs + 12 < a.p) hv3 = a.H[(8 * (int64_t)wo[12] + hd) * n + hcol];
+    mv = tid < 128 ? a.meta[(int64_t)j * kMeta + 64 + tid] : 0.f;
+#pragma unroll
+    for (int s = 0; s < kWS - 1; ++s) dv[s] = s + 1 < a.p ? a.D[row * kDS + 8 * s + e] : 0.f;
+    rh = a.rhs[row * n + 8 * (int64_t)j + e];
+    xb = a.x[row * n + 8 * (int64_t)j + e];
+  }
+
+  // ---- finalize, part 2: accept test and (chunk 0) the state updates
+  float dl = 0.f;  // accepted delta of the finalized step, coordinate e
+  if (a.finalize) {
+    const float fd = cand - fx;
     float dg = 0.f;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) dg = dg + __shfl(dv, gbase + d) * Gm[d * 8 + e];
-    const float cross = sum8(rh * dv);
-    float dn = sum8(dg * dv);
+    for (int d = 0; d < 8; ++d) dg = dg + __shfl(fd, gbase + d) * gm[d];
+    const float cross = sum8(fr * fd);
+    float dn = sum8(dg * fd);
     dn = dn > 0.f ? dn : 0.f;
-    const float r0 = a.res[(int64_t)a.fin_par * rows + row];
     float ce = (r0 + dn) - 2.0f * cross;
     ce = ce > 0.f ? ce : 0.f;
     const bool acc = ce + 1e-12f < r0 * (1.0f + a.accept_tol);
-    dl = acc ? dv : 0.f;
+    dl = acc ? fd : 0.f;
     if (writer && valid) {
       a.D[row * kDS + 8 * a.fin_slot + e] = dl;
       if (acc) a.x[row * n + 8 * (int64_t)jp + e] = cand;
@@ -314,75 +389,112 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
   }
   if (!a.compute) return;
 
-  // ---- target of order position t (block j) for the tile's rows
-  const int j = ord[a.t];
-  const float* M = a.meta + (int64_t)j * kMeta;
-  float rh = a.rhs[row * n + 8 * (int64_t)j + e];
-  for (int s = 0; s < a.p; ++s) {
-    const int64_t js = ord[a.w0 + s];
-    const float* Hb = a.H + (8 * js) * n + 8 * (int64_t)j + e;
-    if (s + 1 < a.p) {
-      const float* Dr = a.D + row * kDS + 8 * s;
+  // ---- target of order position t (block j) for the tile's rows, from operands staged in LDS by
+  // the whole work-group (loaded above): block j's L and Gi, the 8 x 8 blocks H[8 j_s.., 8 j..] of
+  // the window's earlier steps, and the tile's window deltas (lane e brings D[row][8 s + e]).
+  {
+    if (tid < kCS / 256 * 2) reinterpret_cast<float4*>(s_abs)[tid] = ab0;
+    // H entry (s, d, e) of hv_q (i = tid + 256 q = 64 s + 8 d + e) goes to 64 s + 8 e + d
+    const int ht = (tid & ~63) + 8 * (tid & 7) + ((tid >> 3) & 7);
+    s_H[ht] = hv0;
+    s_H[ht + 256] = hv1;
+    s_H[ht + 512] = hv2;
+    s_H[ht + 768] = hv3;
+    if (tid < 128) s_M[tid] = mv;
+    // the tile's window deltas; the last one is the delta finalized above (chunk 0 writes it to D in
+    // this launch)
+    float* dr = s_D + 8 * kWS * r + e;
 #pragma unroll
-      for (int d = 0; d < 8; ++d) rh = rh - Dr[d] * Hb[d * n];
-    } else {
-#pragma unroll
-      for (int d = 0; d < 8; ++d) rh = rh - __shfl(dl, gbase + d) * Hb[d * n];
+    for (int s = 0; s < kWS - 1; ++s)
+      if (s + 1 < a.p) dr[8 * s] = dv[s];
+    if (a.p > 0) dr[8 * (a.p - 1)] = dl;
+  }
+  __syncthreads();
+  // rhs of the step: window-start rhs minus the window's deltas times H blocks, in step order
+  {
+    const float4* dr4 = reinterpret_cast<const float4*>(s_D + 8 * kWS * r);
+    const float4* hr4 = reinterpret_cast<const float4*>(s_H + 8 * e);
+    for (int s = 0; s < a.p; ++s) {
+      const float4 d0 = dr4[2 * s], d1 = dr4[2 * s + 1];
+      const float4 h0 = hr4[16 * s], h1 = hr4[16 * s + 1];
+      rh = rh - d0.x * h0.x;
+      rh = rh - d0.y * h0.y;
+      rh = rh - d0.z * h0.z;
+      rh = rh - d0.w * h0.w;
+      rh = rh - d1.x * h1.x;
+      rh = rh - d1.y * h1.y;
+      rh = rh - d1.z * h1.z;
+      rh = rh - d1.w * h1.w;
     }
   }
-  const float xb = a.x[row * n + 8 * (int64_t)j + e];
   if (writer && valid) {
     a.Xt[(int64_t)a.cur_par * rows * 8 + row * 8 + e] = xb;
     a.Rt[(int64_t)a.cur_par * rows * 8 + row * 8 + e] = rh;
   }
   float tg = xb;
 #pragma unroll
-  for (int d = 0; d < 8; ++d) tg = tg + __shfl(rh, gbase + d) * M[128 + d * 8 + e];
+  for (int d = 0; d < 8; ++d) tg = tg + __shfl(rh, gbase + d) * s_M[64 + d * 8 + e];
   float tm = 0.f;  // (target L)_e
 #pragma unroll
-  for (int d = 0; d < 8; ++d) tm = tm + __shfl(tg, gbase + d) * M[64 + d * 8 + e];
+  for (int d = 0; d < 8; ++d) tm = tm + __shfl(tg, gbase + d) * s_M[d * 8 + e];
   float u = 0.f;  // (L tm)_e = (L L^T target)_e
 #pragma unroll
-  for (int f = 0; f < 8; ++f) u = u + M[64 + e * 8 + f] * __shfl(tm, gbase + f);
+  for (int f = 0; f < 8; ++f) u = u + s_M[e * 8 + f] * __shfl(tm, gbase + f);
   s_u[r][e] = -2.0f * u;
-
-  // ---- stage this chunk's |L^T c|^2 and the abs table
-  const int cs = kCodes / a.nchunk;
-  const int c0 = blockIdx.y * cs;
+  __syncthreads();  // every wave is past the window loop: s_D's space takes the chunk's table
   {
-    const float4* src = reinterpret_cast<const float4*>(a.cgc + (int64_t)j * kCodes + c0);
-    float4* dst = reinterpret_cast<float4*>(s_cgc);
-    for (int i = tid; i < cs / 4; i += 256) dst[i] = src[i];
-    for (int i = tid; i < 256 * 8; i += 256) s_abs[i] = 0.5f * (float)kE8Abs2[i >> 3][i & 7];
+    float4* dst = reinterpret_cast<float4*>(s_cgc) + tid;
+    dst[0] = cg0;
+    dst[256] = cg1;
+    dst[512] = cg2;
+    dst[768] = cg3;
   }
   __syncthreads();
 
-  // ---- argmin over the chunk: wave w takes a quarter, 32 codewords per MFMA tile
+  // ---- argmin over the chunk: wave w takes a quarter, 32 codewords per MFMA tile.
+  // The product u . c runs on v_mfma_f32_32x32x16_bf16: codewords (multiples of 1/4 below 4, exact
+  // in bf16) on the M side, the rows' u = -2 L L^T target on the N side as three exact bf16 planes
+  // (u = hi + mid + lo), K = 16 holding (hi | mid) in one product and (lo | 0) in the other, each
+  // k slot pairing coordinate d with plane (k / 8): every product is exact, summed in fp32.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5;
   const int i = lane & 31;
-  const float b0 = s_u[i][h], b1 = s_u[i][2 + h], b2 = s_u[i][4 + h], b3 = s_u[i][6 + h];
+  bf16x8_t bu1, bu2;
+  {
+    uint32_t ph[4], pm[4], plo[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) split3(s_u[i][2 * q], s_u[i][2 * q + 1], ph[q], pm[q], plo[q]);
+    const uint4 u1 = h ? make_uint4(pm[0], pm[1], pm[2], pm[3]) : make_uint4(ph[0], ph[1], ph[2], ph[3]);
+    const uint4 u2 = h ? make_uint4(0u, 0u, 0u, 0u) : make_uint4(plo[0], plo[1], plo[2], plo[3]);
+    bu1 = __builtin_bit_cast(bf16x8_t, u1);
+    bu2 = __builtin_bit_cast(bf16x8_t, u2);
+  }
   const int pl = __builtin_popcount(i) & 1;
-  const int wq = cs / 4;
+  const int wq = kCS / 4;
   const int wbeg = c0 + wave * wq;
   float best = INFINITY;
   int bidx = wbeg;
   for (int kb = wbeg; kb < wbeg + wq; kb += 256) {
     const int k = kb >> 8;
     const int bp = (int)kE8Parity[k];
-    const float a0 = s_abs[k * 8 + h], a1 = s_abs[k * 8 + 2 + h];
-    const float a2 = s_abs[k * 8 + 4 + h], a3 = s_abs[k * 8 + 6 + h];
+    // lane half h generates coordinates 4 h .. 4 h + 3 of its codeword
+    const float* ak = s_abs + (k - c0 / 256) * 8 + 4 * h;
+    const float a0 = ak[0], a1 = ak[1], a2 = ak[2], a3 = ak[3];
 #pragma unroll 2
     for (int th = 0; th < 8; ++th) {
       const int shi = th * 32;
       const int s8 = shi | i;
       const int branch = (__builtin_popcount(shi) & 1) ^ pl;
-      const int sg = s8 ^ (((branch ^ bp) & 1) << 7);
+      const int sg = (s8 ^ (((branch ^ bp) & 1) << 7)) >> (4 * h);
       const float sh = branch ? -0.25f : 0.25f;
-      const float A0 = sh + (((sg >> h) & 1) ? -a0 : a0);
-      const float A1 = sh + (((sg >> (2 + h)) & 1) ? -a1 : a1);
-      const float A2 = sh + (((sg >> (4 + h)) & 1) ? -a2 : a2);
-      const float A3 = sh + (((sg >> (6 + h)) & 1) ? -a3 : a3);
+      const float c0v = sh + ((sg & 1) ? -a0 : a0);
+      const float c1v = sh + ((sg & 2) ? -a1 : a1);
+      const float c2v = sh + ((sg & 4) ? -a2 : a2);
+      const float c3v = sh + ((sg & 8) ? -a3 : a3);
+      // exact bf16 pairs; the two lane halves exchange theirs so every lane holds all 8 coordinates
+      const auto px = __builtin_amdgcn_permlane32_swap(pk_bf16(c0v, c1v), pk_bf16(c0v, c1v), false, false);
+      const auto py = __builtin_amdgcn_permlane32_swap(pk_bf16(c2v, c3v), pk_bf16(c2v, c3v), false, false);
+      const bf16x8_t cw = __builtin_bit_cast(bf16x8_t, make_uint4(px[0], py[0], px[1], py[1]));
       const int idx0 = kb + shi;
       const float* cp = s_cgc + (idx0 - c0) + 4 * h;
       floatx16 acc;
@@ -394,10 +506,8 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
         acc[4 * g + 2] = q.z;
         acc[4 * g + 3] = q.w;
       }
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(A0, b0, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(A1, b1, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(A2, b2, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(A3, b3, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cw, bu1, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cw, bu2, acc, 0, 0, 0);
       float m01 = fminf(acc[0], acc[1]), m23 = fminf(acc[2], acc[3]);
       float m45 = fminf(acc[4], acc[5]), m67 = fminf(acc[6], acc[7]);
       float m89 = fminf(acc[8], acc[9]), mab = fminf(acc[10], acc[11]);
@@ -439,8 +549,8 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
     const int64_t rl = (int64_t)(blockIdx.x % a.tiles_per_rb) * kRT + tid;
     const int64_t rr = rb * a.block_rows + rl;
     if (rl < a.block_rows && rr < a.rows) {
-      a.ps[rr * 16 + blockIdx.y] = bsv;
-      a.pi[rr * 16 + blockIdx.y] = biv;
+      a.ps[(int64_t)a.cur_par * rows * 16 + rr * 16 + blockIdx.y] = bsv;
+      a.pi[(int64_t)a.cur_par * rows * 16 + rr * 16 + blockIdx.y] = biv;
     }
   }
 }
@@ -466,7 +576,7 @@ CdPlan e8_cd_plan(int64_t rows, int64_t n, int64_t block_rows) {
   b += a64(rows * kDS) * 4;                    // deltas
   b += 2 * a64(rows * 8) * 4 * 2;              // Rt, Xt
   b += 2 * a64(rows) * 4;                      // res
-  b += a64(rows * 16) * 4 * 2;                 // partial scores / indices
+  b += 2 * a64(rows * 16) * 4 * 2;             // partial scores / indices, two parities
   b += 3 * a64(rows) * 4;                      // accepted, err_b, err_a
   b += a64(rows * c.nchunks) * 4;              // row partials
   c.bytes = b;
@@ -485,7 +595,7 @@ hipError_t product_splits(const float* A, const float* B, bool trans_b, int64_t 
 
 int64_t ctx_bytes(int64_t n) {
   const int64_t nb = n / 8;
-  return a64(n * n) * 4 + a64(nb * kMeta) * 4 + nb * kCodes * 4 + (int64_t)kCodes * 8 * 4 + 256;
+  return a64(n * n) * 4 + a64(nb * kMeta) * 4 + nb * kCodes * 4 + (int64_t)kCodes * 8 * 4 + 256 * 8 * 4 + 256;
 }
 
 struct Ctx {
@@ -493,6 +603,7 @@ struct Ctx {
   float* meta;
   float* cgc;
   float* grid;
+  float* abs_tab;
   int* fail;
 };
 
@@ -504,6 +615,7 @@ Ctx carve_ctx(void* p, int64_t n) {
   x.meta = (float*)c; c += a64(nb * kMeta) * 4;
   x.cgc = (float*)c; c += nb * kCodes * 4;
   x.grid = (float*)c; c += (int64_t)kCodes * 8 * 4;
+  x.abs_tab = (float*)c; c += 256 * 8 * 4;
   x.fail = (int*)c;
   return x;
 }
@@ -529,7 +641,7 @@ extern "C" int mpq_e8p12_cd_prepare(int64_t n, const float* Vs, void* ctx, int64
   // H = Vs Vs^T (the per-block grams are its 8x8 diagonal blocks)
   MPQ_HIP_TRY(gemm(Vs, n, Vs, n, true, nullptr, c.H, n, n, n, n, 1.f, 0.f, nullptr, 0, stream));
   MPQ_HIP_TRY(hipMemsetAsync(c.fail, 0, sizeof(int), stream));
-  hipLaunchKernelGGL(grid_kernel, dim3(kCodes / 256), dim3(256), 0, stream, c.grid);
+  hipLaunchKernelGGL(grid_kernel, dim3(kCodes / 256), dim3(256), 0, stream, c.grid, c.abs_tab);
   hipLaunchKernelGGL(meta_kernel, dim3((unsigned)((nb + 63) / 64)), dim3(64), 0, stream, n, nb, c.H, c.meta,
                      c.fail);
   hipLaunchKernelGGL(cgc_kernel, dim3(kCodes / 256, (unsigned)nb), dim3(256), 0, stream, c.grid, c.meta, c.cgc);
@@ -583,8 +695,8 @@ extern "C" int mpq_e8p12_cd_polish(int64_t rows, int64_t n, int64_t block_rows, 
   float* Rt = (float*)p; p += 2 * a64(rows * 8) * 4;
   float* Xt = (float*)p; p += 2 * a64(rows * 8) * 4;
   float* res = (float*)p; p += 2 * a64(rows) * 4;
-  float* ps = (float*)p; p += a64(rows * 16) * 4;
-  int32_t* pi = (int32_t*)p; p += a64(rows * 16) * 4;
+  float* ps = (float*)p; p += 2 * a64(rows * 16) * 4;   // double-buffered by step parity
+  int32_t* pi = (int32_t*)p; p += 2 * a64(rows * 16) * 4;
   int32_t* acc = (int32_t*)p; p += a64(rows) * 4;
   float* err_b = (float*)p; p += a64(rows) * 4;
   float* err_a = (float*)p; p += a64(rows) * 4;
@@ -615,14 +727,14 @@ extern "C" int mpq_e8p12_cd_polish(int64_t rows, int64_t n, int64_t block_rows, 
 
   const int64_t nsteps = (max_blocks > 0 && max_blocks < nb) ? max_blocks : nb;
   const int64_t row_tiles = pl.nrb * tiles_per_rb;
-  int nchunk = 4;
-  while (nchunk < 16 && row_tiles * nchunk < 1024) nchunk *= 2;
+  // kNChunk chunks: the chunk's table takes 16 KB of LDS, so occupancy is set by registers, not LDS
+  const int nchunk = kNChunk;
   const bool grouped_gemm = (block_rows % 128 == 0) || pl.nrb == 1;
 
   StepArgs sa{};
   sa.rows = rows; sa.n = n; sa.nb = nb; sa.block_rows = block_rows;
   sa.tiles_per_rb = (int)tiles_per_rb; sa.accept_tol = accept_tol;
-  sa.order = order; sa.meta = cx.meta; sa.cgc = cx.cgc; sa.H = cx.H; sa.grid = cx.grid;
+  sa.order = order; sa.meta = cx.meta; sa.cgc = cx.cgc; sa.H = cx.H; sa.grid = cx.grid; sa.abs_tab = cx.abs_tab;
   sa.rhs = rhs; sa.x = x_out; sa.idx = idx_out; sa.res = res; sa.D = D; sa.Rt = Rt; sa.Xt = Xt;
   sa.ps = ps; sa.pi = pi; sa.accepted = acc;
   int64_t g = 0;  // global step counter: parity of the double buffers

@@ -339,11 +339,13 @@ def stabilize_cholesky(gram: torch.Tensor, jitter: float = 1e-6, max_tries: int 
 
 
 def gram_block_cd(x, idxs, Y_u, Vs, grid, sweeps, accept_tol=0.0, max_blocks=0, metric="gram",
-                  order_mode="greedy_gain"):
+                  order_mode="greedy_gain", scores_fp64=False):
     """mpq/polish/block_cd.py:332-625 with E8P12Provider, greedy_gain order and, for metric "gram", the
     compiled step _cd_gram_step_impl (:212-246): whitened brute-force argmin over all codewords.
     metric "diag": target x + rhs * (1 / diag G) and the nearest codeword (cb.quantize, :740-745);
-    order_mode static (trace G descending) or cyclic (:505-511); stable sorts."""
+    order_mode static (trace G descending) or cyclic (:505-511); stable sorts.  ``scores_fp64``: the
+    gram step's scores evaluated in fp64 from the same fp32 target and factor (another rounding of
+    the reference's fp32 scores, used to measure how far that rounding moves the greedy decisions)."""
     B, n = x.shape
     nb = n // 8
     x = x.to(torch.float32).clone()
@@ -382,8 +384,12 @@ def gram_block_cd(x, idxs, Y_u, Vs, grid, sweeps, accept_tol=0.0, max_blocks=0, 
             rhs = res_u.matmul(Vbt)
             if metric == "gram":
                 target = xb + rhs.matmul(Gi)
-                tm = target.matmul(L)
-                mg = grid.matmul(L)
+                if scores_fp64:
+                    tm = target.double().matmul(L.double())
+                    mg = grid.double().matmul(L.double())
+                else:
+                    tm = target.matmul(L)
+                    mg = grid.matmul(L)
                 scores = (tm.square().sum(dim=1, keepdim=True) + mg.square().sum(dim=-1).unsqueeze(0)
                           - 2.0 * tm.matmul(mg.T))
             else:
@@ -486,7 +492,8 @@ def solve_e8p12_rankspace_vamp(Wr, hat_init, V, S, grid, cache, cfg, obs_precisi
     stats["idx_vamp"] = idx_t.clone()
     stats["err_vamp"] = ou.rankspace_error(Y_u, hat, Vs)
     if sweeps > 0:
-        hat, idx_t, acc = gram_block_cd(hat, idx_t, Y_u, Vs, grid, sweeps)
+        hat, idx_t, acc = gram_block_cd(hat, idx_t, Y_u, Vs, grid, sweeps,
+                                        scores_fp64=bool(cfg.get("scores_fp64", False)))
         stats["polish_accepted"] = acc
     err = ou.rankspace_error(Y_u, hat, Vs)
     stats["obs_final"] = obs
@@ -504,21 +511,25 @@ def _jitter_last_bit(V: torch.Tensor, seed: int) -> torch.Tensor:
     return torch.where(step > 0, up, torch.where(step < 0, dn, V))
 
 
-def refine_codebook(Wr, Hr, grid, cache, cfg, block_rows=128, info=None, v_jitter_seed=None):
+def refine_codebook(Wr, Hr, grid, cache, cfg, block_rows=128, info=None, v_jitter_seed=None, decomposition=None):
     """mpq/adapters/quip_sharp.py:396-878 for solver "vamp", init "rtn": nearest-codeword init,
     fp64 eigh (:33-67), rank-space warm start (:461-475), per row block VAMP + polish with the
     observation precision carried (:555-586).  Returns (hat, idx, obs_final); ``info`` (a dict,
     optional) receives the warm-start precision as "obs_initial".  ``v_jitter_seed`` moves every entry
     of the fp32 eigenvectors to a random neighbouring float (another valid fp32 rounding of the fp64
-    decomposition, for noise floors).  Pinned by the reference's golden vector
-    tests/golden/e8p12_refine.npz."""
+    decomposition, for noise floors); ``decomposition`` = (ascending eigenvalues, eigenvectors), fp64
+    results of another eigensolver rounded to fp32, replaces LAPACK's.  Pinned by the reference's
+    golden vector tests/golden/e8p12_refine.npz."""
     m, n = Wr.shape
     idx0, _ = bruteforce_nearest(Wr.reshape(-1, 8).numpy(), grid.numpy())
     idx0 = torch.from_numpy(np.asarray(idx0)).view(m, n // 8)
     hat0 = grid[idx0.reshape(-1)].view(m, n)
     H64 = 0.5 * (Hr.double() + Hr.double().T)
-    lam, V = torch.linalg.eigh(H64)
-    lam, V = lam.float(), V.float()
+    if decomposition is None:
+        lam, V = torch.linalg.eigh(H64)
+        lam, V = lam.float(), V.float()
+    else:
+        lam, V = decomposition[0].float(), decomposition[1].float()
     if v_jitter_seed is not None:
         V = _jitter_last_bit(V, v_jitter_seed)
     floor = max(1e-6, 1e-6 * max(float(torch.diagonal(H64).mean().abs()), float(lam.max()), 1e-12))

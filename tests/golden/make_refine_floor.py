@@ -1,15 +1,20 @@
 """Noise floor of the QUIP# adapter golden (tests/golden/e8p12_refine.npz): the oracle's code agreement
-with the reference's vector when only the fp32 rounding of the fp64 eigenvectors changes (every entry
-moved at random to a neighbouring float, seeds 1-8; oracle/e8p12.py refine_codebook(v_jitter_seed)).
+with the reference's vector when only roundings change --
+
+* the fp32 rounding of the fp64 eigenvectors (every entry moved at random to a neighbouring float,
+  seeds 1-32; oracle/e8p12.py refine_codebook(v_jitter_seed)),
+* the polish's argmin scores evaluated in fp64 (cfg "scores_fp64"), alone and with seeds 1-8,
+* the VAMP's products rounded from fp64 (oracle.uniform.products_in_fp64), with fp32 and fp64 scores,
+* the unchanged oracle on 2, 4 and 8 BLAS threads (the golden was written on one).
 
 On this input the reference's EM drives the observation precision to its 1e-4 clamp, where fp32
-near-ties decide codes.  The oracle reproduces the golden exactly with the unperturbed decomposition
-(tests/test_oracle_e8p12_vamp.py), so the lowest agreement over the perturbed runs is the reference's
-own sensitivity to a last-bit change of its eigenvectors -- the input the GPU forms with its own fp64
-eigensolver.  Recorded in the build container (the sensitivity is chaotic: another CPU's BLAS can
-move which seeds flip codes).
+near-ties decide the VAMP's decisions for a few rows; the greedy CD, whose order each 128-row block
+shares, turns one such row into a cascade over the block.  The oracle reproduces the golden exactly
+with the unperturbed decomposition (tests/test_oracle_e8p12_vamp.py), so the lowest agreement over the
+perturbed runs is the reference's own sensitivity.  Recorded in the build container, each perturbed
+run on one thread (the sensitivity is chaotic: another CPU's BLAS can move which seeds flip codes).
 
-Usage:  python tests/golden/make_refine_floor.py
+Usage:  python tests/golden/make_refine_floor.py       (about 5 minutes with 8 worker processes)
 Output: tests/golden/e8p12_refine_floor.json
 """
 from __future__ import annotations
@@ -17,6 +22,7 @@ from __future__ import annotations
 import json
 import os
 import sys
+from concurrent.futures import ProcessPoolExecutor
 
 import numpy as np
 import torch
@@ -26,24 +32,51 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
+CFG = dict(iters=16, damping=0.5, prior_tau=0.25, polish_sweeps=3)
 
-def main() -> None:
+
+def _run(variant):
+    """Agreement of one oracle variant (jitter seed or None, fp64 scores, fp64 products, thread count)
+    with the golden."""
+    seed, scores_fp64, products_fp64, threads = variant
     from mpq_amd import codebook
     from oracle import e8p12 as oe8
+    from oracle import uniform as ou
 
-    torch.set_num_threads(1)
+    torch.set_num_threads(threads)
     d = np.load(os.path.join(HERE, "e8p12_refine.npz"))
     Wr, H = torch.from_numpy(d["Wr"]), torch.from_numpy(d["H"])
     grid = torch.from_numpy(codebook.grid_numpy())
     cache = oe8.factor_cache(grid)
-    cfg = dict(iters=16, damping=0.5, prior_tau=0.25, polish_sweeps=3)
-    agree = {}
-    for seed in range(1, 9):
+    cfg = dict(CFG, scores_fp64=scores_fp64)
+    if products_fp64:
+        with ou.products_in_fp64():
+            _, idx, _ = oe8.refine_codebook(Wr, H, grid, cache, cfg, block_rows=128, v_jitter_seed=seed)
+    else:
         _, idx, _ = oe8.refine_codebook(Wr, H, grid, cache, cfg, block_rows=128, v_jitter_seed=seed)
-        agree[seed] = float((idx.numpy() == d["idx"]).mean())
-        print(seed, agree[seed], flush=True)
-    out = {"v_jitter_agreement": agree, "floor": min(agree.values()),
-           "note": "oracle vs the reference golden with the fp32 eigenvectors moved by one ulp at random"}
+    return float((idx.numpy() == d["idx"]).mean())
+
+
+def main() -> None:
+    variants = ([(s, False, False, 1) for s in range(1, 33)] + [(None, True, False, 1)]
+                + [(s, True, False, 1) for s in range(1, 9)] + [(None, False, True, 1), (None, True, True, 1)])
+    with ProcessPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as pool:
+        res = list(pool.map(_run, variants))
+    # the unchanged oracle on more threads (its BLAS partitions every product's sums differently):
+    # one run at a time, each with the whole machine's share of threads it asks for
+    thr = {str(t): _run((None, False, False, t)) for t in (2, 4, 8)}
+    got = dict(zip(variants, res))
+    jitter = {str(s): got[(s, False, False, 1)] for s in range(1, 33)}
+    scores = {str(s or 0): got[(s, True, False, 1)] for s in [None] + list(range(1, 9))}
+    prods = {"fp32_scores": got[(None, False, True, 1)], "fp64_scores": got[(None, True, True, 1)]}
+    for k, v in list(jitter.items()) + list(scores.items()) + list(prods.items()) + list(thr.items()):
+        print(k, v)
+    out = {"v_jitter_agreement": jitter, "fp64_scores_agreement": scores, "fp64_products_agreement": prods,
+           "threads_agreement": thr, "floor": min(min(res), min(thr.values())),
+           "note": "oracle vs the reference golden with the fp32 eigenvectors moved by one ulp at random "
+                   "(seeds 1-32), with the polish's argmin scores evaluated in fp64 (key 0: no jitter; "
+                   "1-8: with that seed's jitter), with the VAMP's products rounded from fp64, and on "
+                   "2, 4 and 8 BLAS threads"}
     with open(os.path.join(HERE, "e8p12_refine_floor.json"), "w") as fh:
         json.dump(out, fh, indent=1)
 
