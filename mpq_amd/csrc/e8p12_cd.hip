@@ -71,8 +71,9 @@ __device__ __forceinline__ float sum8(float v) {
 // preparation (per layer): codebook grid, per-block G/L/Gi, |L^T c|^2 tables
 // ---------------------------------------------------------------------------
 
-// grid (65536 x 8) and the abs-pattern table (256 x 8: |coordinate| - 1/4 magnitudes a of pattern k)
-__global__ __launch_bounds__(256) void grid_kernel(float* __restrict__ grid, float* __restrict__ abs_tab) {
+// grid (65536 x 8) and the pattern table: the magnitudes a of abs pattern k (256 x 8), then the
+// 256 pattern parities as int bits
+__global__ __launch_bounds__(256) void grid_kernel(float* __restrict__ grid, float* __restrict__ pat) {
   const int idx = blockIdx.x * 256 + threadIdx.x;
   const int k = idx >> 8;
   const int s = idx & 255;
@@ -83,8 +84,9 @@ __global__ __launch_bounds__(256) void grid_kernel(float* __restrict__ grid, flo
   for (int d = 0; d < 8; ++d) {
     const float a = 0.5f * (float)kE8Abs2[k][d];
     grid[(int64_t)idx * 8 + d] = sh + (((signs >> d) & 1) ? -a : a);
-    if (s == 0) abs_tab[k * 8 + d] = a;
+    if (s == 0) pat[k * 8 + d] = a;
   }
+  if (s == 0) pat[256 * 8 + k] = __int_as_float((int)kE8Parity[k]);
 }
 
 __device__ bool chol8(const float (&A)[8][8], float (&L)[8][8]) {
@@ -92,7 +94,8 @@ __device__ bool chol8(const float (&A)[8][8], float (&L)[8][8]) {
   for (int j = 0; j < 8; ++j) {
     float s = A[j][j];
     for (int k = 0; k < j; ++k) s = s - L[j][k] * L[j][k];
-    if (!(s > 0.f) || !isfinite(s)) return false;
+    // finiteness from the bits: this file is compiled without NaN semantics (-fno-honor-nans)
+    if ((__float_as_uint(s) & 0x7f800000u) == 0x7f800000u || !(s > 0.f)) return false;
     const float d = sqrtf(s);
     L[j][j] = d;
     for (int i = j + 1; i < 8; ++i) {
@@ -244,7 +247,7 @@ struct StepArgs {
   const float* cgc;      // nb x 65536
   const float* H;        // n x n
   const float* grid;     // 65536 x 8
-  const float* abs_tab;  // 256 x 8 abs-pattern magnitudes
+  const float* pat;      // 256 x 8 abs-pattern magnitudes, then 256 parities (int bits)
   const float* rhs;      // rows x n, current at the window start
   float* x;              // rows x n
   int64_t* idx;          // rows x nb
@@ -263,7 +266,7 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
   __shared__ __align__(16) float s_cgc[kCS];
   static_assert(kCS >= kRT * 8 * kWS, "s_D does not fit in s_cgc");
   float* const s_D = s_cgc;
-  __shared__ __align__(16) float s_abs[(kCS / 256) * 8];  // magnitudes of the chunk's kCS / 256 abs patterns
+  __shared__ __align__(16) float s_pat[256 * 8 + 256];  // abs-pattern magnitudes, then parities (int bits)
   __shared__ __align__(16) float s_H[kWS * 64];  // H[8 j_s + d][8 j + e] of the window's steps s, entry 64 s + 8 e + d
   __shared__ float s_M[128];       // block j's L (64) and Gi (64)
   __shared__ float s_u[kRT][8];
@@ -284,27 +287,24 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
   const int32_t* ord = a.order + rb * a.nb;
   const int64_t rows = a.rows, n = a.n;
 
-  // ---- finalize, part 1 (loads): the previous step's decision needs, per row, the best of all
-  // chunks' partials (in the buffer of that launch's parity: this launch's work-groups write the
-  // other one, so a work-group that finishes early cannot overwrite what a later one still reads),
-  // its codeword, the step's x block and rhs, the residual norm and the block's gram G.
-  int jp = 0, bi = 0;
-  float cand = 0.f, fx = 0.f, fr = 0.f, r0 = 0.f;
+  // ---- loads.  Finalize: the previous step's decision needs, per row, the best of all chunks'
+  // partials (in the buffer of that launch's parity: this launch's work-groups write the other one,
+  // so a work-group that finishes early cannot overwrite what a later one still reads), the step's
+  // x block and rhs, the residual norm and the block's gram G.  Compute: the chunk's |L^T c|^2,
+  // block j's L and Gi, the window's H blocks and deltas, rhs and x of block j.  None of them reads
+  // what this launch writes (block j is not the finalized block; D slots s < p - 1 were written by
+  // earlier launches).  All of them are issued before the first use.
+  static_assert(kCS / 4 / 256 == 4 && kWS * 64 / 256 == 4, "staging assumes 4 loads per thread");
+  int jp = 0;
+  float fx = 0.f, fr = 0.f, r0 = 0.f;
   float gm[8];
+  float ps[16];
+  int pi[16];
 #pragma unroll
   for (int d = 0; d < 8; ++d) gm[d] = 0.f;
   if (a.finalize) {
-    jp = ord[a.fin_t];
-    const float* Gm = a.meta + (int64_t)jp * kMeta;
-#pragma unroll
-    for (int d = 0; d < 8; ++d) gm[d] = Gm[d * 8 + e];
-    fx = a.Xt[(int64_t)a.fin_par * rows * 8 + row * 8 + e];
-    fr = a.Rt[(int64_t)a.fin_par * rows * 8 + row * 8 + e];
-    r0 = a.res[(int64_t)a.fin_par * rows + row];
     const float4* fps = reinterpret_cast<const float4*>(a.ps + (int64_t)a.fin_par * rows * 16 + row * 16);
     const int4* fpi = reinterpret_cast<const int4*>(a.pi + (int64_t)a.fin_par * rows * 16 + row * 16);
-    float ps[16];
-    int pi[16];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float4 v = fps[q];
@@ -312,40 +312,33 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
       ps[4 * q] = v.x; ps[4 * q + 1] = v.y; ps[4 * q + 2] = v.z; ps[4 * q + 3] = v.w;
       pi[4 * q] = w.x; pi[4 * q + 1] = w.y; pi[4 * q + 2] = w.z; pi[4 * q + 3] = w.w;
     }
-    // earlier chunk wins ties
-    float bs = ps[0];
-    bi = pi[0];
+    jp = ord[a.fin_t];
+    const float* Gm = a.meta + (int64_t)jp * kMeta;
 #pragma unroll
-    for (int c = 1; c < kNChunk; ++c) {
-      if (ps[c] < bs) {
-        bs = ps[c];
-        bi = pi[c];
-      }
-    }
-    cand = a.grid[(int64_t)bi * 8 + e];
+    for (int d = 0; d < 8; ++d) gm[d] = Gm[d * 8 + e];
+    fx = a.Xt[(int64_t)a.fin_par * rows * 8 + row * 8 + e];
+    fr = a.Rt[(int64_t)a.fin_par * rows * 8 + row * 8 + e];
+    r0 = a.res[(int64_t)a.fin_par * rows + row];
   }
-
-  // Loads of the compute phase, issued before the finalize's arithmetic so that they overlap it:
-  // none of them reads what the finalize writes (block j is not the finalized block; D slots
-  // s < p - 1 were written by earlier launches)
-  static_assert(kCS / 4 / 256 == 4 && kWS * 64 / 256 == 4, "staging assumes 4 loads per thread");
+  // the abs-pattern magnitudes (256 x 8) and parities: codewords are formed from their index
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float4 pt0 = reinterpret_cast<const float4*>(a.pat)[tid];
+  const float4 pt1 = reinterpret_cast<const float4*>(a.pat)[tid + 256];
+  const float pt2 = tid < 256 ? a.pat[2048 + tid] : 0.f;
   const int j = a.compute ? ord[a.t] : 0;
   const int c0 = blockIdx.y * kCS;
-  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
   float4 cg0 = z4, cg1 = z4, cg2 = z4, cg3 = z4;
   float hv0 = 0.f, hv1 = 0.f, hv2 = 0.f, hv3 = 0.f;
   float dv[kWS - 1];
 #pragma unroll
   for (int s = 0; s < kWS - 1; ++s) dv[s] = 0.f;
   float mv = 0.f, rh = 0.f, xb = 0.f;
-  float4 ab0 = z4;
   if (a.compute) {
     const float4* src = reinterpret_cast<const float4*>(a.cgc + (int64_t)j * kCodes + c0) + tid;
     cg0 = src[0];
     cg1 = src[256];
     cg2 = src[512];
     cg3 = src[768];
-    if (tid < kCS / 256 * 2) ab0 = reinterpret_cast<const float4*>(a.abs_tab)[c0 / 256 * 2 + tid];
     // H block entry (s, d, e) = i = 64 s + 8 d + e, i = tid + 256 q; s = wave + 4 q is wave-uniform
     const int64_t hcol = 8 * (int64_t)j + (tid & 7);
     const int hd = (tid >> 3) & 7, hs = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -361,9 +354,67 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
     xb = a.x[row * n + 8 * (int64_t)j + e];
   }
 
-  // ---- finalize, part 2: accept test and (chunk 0) the state updates
+  // ---- the previous step's candidate per row: earlier chunk wins ties
+  int bi = 0;
+  if (a.finalize) {
+    float bs = ps[0];
+    bi = pi[0];
+#pragma unroll
+    for (int c = 1; c < kNChunk; ++c) {
+      if (ps[c] < bs) {
+        bs = ps[c];
+        bi = pi[c];
+      }
+    }
+  }
+
+  // ---- stage in LDS what the tile's rows share (and each row's window deltas s < p - 1)
+  reinterpret_cast<float4*>(s_pat)[tid] = pt0;
+  reinterpret_cast<float4*>(s_pat)[tid + 256] = pt1;
+  if (tid < 256) s_pat[2048 + tid] = pt2;
+  if (a.compute) {
+    // H entry (s, d, e) of hv_q (i = tid + 256 q = 64 s + 8 d + e) goes to 64 s + 8 e + d
+    const int ht = (tid & ~63) + 8 * (tid & 7) + ((tid >> 3) & 7);
+    s_H[ht] = hv0;
+    s_H[ht + 256] = hv1;
+    s_H[ht + 512] = hv2;
+    s_H[ht + 768] = hv3;
+    if (tid < 128) s_M[tid] = mv;
+    float* dr = s_D + 8 * kWS * r + e;
+#pragma unroll
+    for (int s = 0; s < kWS - 1; ++s)
+      if (s + 1 < a.p) dr[8 * s] = dv[s];
+  }
+  __syncthreads();
+
+  // ---- rhs of the step, part 1: window-start rhs minus the window's deltas s < p - 1 times H
+  // blocks, in step order (the last delta is the one finalized below)
+  if (a.compute) {
+    const float4* dr4 = reinterpret_cast<const float4*>(s_D + 8 * kWS * r);
+    const float4* hr4 = reinterpret_cast<const float4*>(s_H + 8 * e);
+    for (int s = 0; s + 1 < a.p; ++s) {
+      const float4 d0 = dr4[2 * s], d1 = dr4[2 * s + 1];
+      const float4 h0 = hr4[16 * s], h1 = hr4[16 * s + 1];
+      rh = rh - d0.x * h0.x;
+      rh = rh - d0.y * h0.y;
+      rh = rh - d0.z * h0.z;
+      rh = rh - d0.w * h0.w;
+      rh = rh - d1.x * h1.x;
+      rh = rh - d1.y * h1.y;
+      rh = rh - d1.z * h1.z;
+      rh = rh - d1.w * h1.w;
+    }
+  }
+
+  // ---- finalize: the candidate's coordinate e from its index (as grid_kernel forms the grid),
+  // accept test and (chunk 0) the state updates
   float dl = 0.f;  // accepted delta of the finalized step, coordinate e
   if (a.finalize) {
+    const int k = bi >> 8, sb = bi & 255;
+    const int branch = __builtin_popcount(sb) & 1;
+    const int signs = sb ^ (((branch ^ __float_as_int(s_pat[2048 + k])) & 1) << 7);
+    const float av = s_pat[8 * k + e];
+    const float cand = (branch ? -0.25f : 0.25f) + (((signs >> e) & 1) ? -av : av);
     const float fd = cand - fx;
     float dg = 0.f;
 #pragma unroll
@@ -389,43 +440,12 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
   }
   if (!a.compute) return;
 
-  // ---- target of order position t (block j) for the tile's rows, from operands staged in LDS by
-  // the whole work-group (loaded above): block j's L and Gi, the 8 x 8 blocks H[8 j_s.., 8 j..] of
-  // the window's earlier steps, and the tile's window deltas (lane e brings D[row][8 s + e]).
-  {
-    if (tid < kCS / 256 * 2) reinterpret_cast<float4*>(s_abs)[tid] = ab0;
-    // H entry (s, d, e) of hv_q (i = tid + 256 q = 64 s + 8 d + e) goes to 64 s + 8 e + d
-    const int ht = (tid & ~63) + 8 * (tid & 7) + ((tid >> 3) & 7);
-    s_H[ht] = hv0;
-    s_H[ht + 256] = hv1;
-    s_H[ht + 512] = hv2;
-    s_H[ht + 768] = hv3;
-    if (tid < 128) s_M[tid] = mv;
-    // the tile's window deltas; the last one is the delta finalized above (chunk 0 writes it to D in
-    // this launch)
-    float* dr = s_D + 8 * kWS * r + e;
+  // ---- rhs of the step, part 2: the finalized delta (step p - 1 of the window), then the target
+  // of order position t (block j) from block j's L and Gi
+  if (a.p > 0) {
+    const float* hl = s_H + 64 * (a.p - 1) + 8 * e;
 #pragma unroll
-    for (int s = 0; s < kWS - 1; ++s)
-      if (s + 1 < a.p) dr[8 * s] = dv[s];
-    if (a.p > 0) dr[8 * (a.p - 1)] = dl;
-  }
-  __syncthreads();
-  // rhs of the step: window-start rhs minus the window's deltas times H blocks, in step order
-  {
-    const float4* dr4 = reinterpret_cast<const float4*>(s_D + 8 * kWS * r);
-    const float4* hr4 = reinterpret_cast<const float4*>(s_H + 8 * e);
-    for (int s = 0; s < a.p; ++s) {
-      const float4 d0 = dr4[2 * s], d1 = dr4[2 * s + 1];
-      const float4 h0 = hr4[16 * s], h1 = hr4[16 * s + 1];
-      rh = rh - d0.x * h0.x;
-      rh = rh - d0.y * h0.y;
-      rh = rh - d0.z * h0.z;
-      rh = rh - d0.w * h0.w;
-      rh = rh - d1.x * h1.x;
-      rh = rh - d1.y * h1.y;
-      rh = rh - d1.z * h1.z;
-      rh = rh - d1.w * h1.w;
-    }
+    for (int d = 0; d < 8; ++d) rh = rh - __shfl(dl, gbase + d) * hl[d];
   }
   if (writer && valid) {
     a.Xt[(int64_t)a.cur_par * rows * 8 + row * 8 + e] = xb;
@@ -473,15 +493,18 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
   const int wq = kCS / 4;
   const int wbeg = c0 + wave * wq;
   float best = INFINITY;
-  int bidx = wbeg;
+  int btile = wbeg;
+  floatx16 snap;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) snap[v] = INFINITY;
   for (int kb = wbeg; kb < wbeg + wq; kb += 256) {
     const int k = kb >> 8;
     const int bp = (int)kE8Parity[k];
     // lane half h generates coordinates 4 h .. 4 h + 3 of its codeword
-    const float* ak = s_abs + (k - c0 / 256) * 8 + 4 * h;
+    const float* ak = s_pat + k * 8 + 4 * h;
     const float a0 = ak[0], a1 = ak[1], a2 = ak[2], a3 = ak[3];
-#pragma unroll 2
-    for (int th = 0; th < 8; ++th) {
+    // the codeword operand of tile th (32 codewords kb + 32 th + i)
+    auto codewords = [&](int th) {
       const int shi = th * 32;
       const int s8 = shi | i;
       const int branch = (__builtin_popcount(shi) & 1) ^ pl;
@@ -494,9 +517,10 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
       // exact bf16 pairs; the two lane halves exchange theirs so every lane holds all 8 coordinates
       const auto px = __builtin_amdgcn_permlane32_swap(pk_bf16(c0v, c1v), pk_bf16(c0v, c1v), false, false);
       const auto py = __builtin_amdgcn_permlane32_swap(pk_bf16(c2v, c3v), pk_bf16(c2v, c3v), false, false);
-      const bf16x8_t cw = __builtin_bit_cast(bf16x8_t, make_uint4(px[0], py[0], px[1], py[1]));
-      const int idx0 = kb + shi;
-      const float* cp = s_cgc + (idx0 - c0) + 4 * h;
+      return __builtin_bit_cast(bf16x8_t, make_uint4(px[0], py[0], px[1], py[1]));
+    };
+    auto table = [&](int th) {  // |L^T c|^2 of the tile's codewords at the lane's accumulator slots
+      const float* cp = s_cgc + (kb + 32 * th - c0) + 4 * h;
       floatx16 acc;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -506,21 +530,42 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
         acc[4 * g + 2] = q.z;
         acc[4 * g + 3] = q.w;
       }
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cw, bu1, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cw, bu2, acc, 0, 0, 0);
-      float m01 = fminf(acc[0], acc[1]), m23 = fminf(acc[2], acc[3]);
-      float m45 = fminf(acc[4], acc[5]), m67 = fminf(acc[6], acc[7]);
-      float m89 = fminf(acc[8], acc[9]), mab = fminf(acc[10], acc[11]);
-      float mcd = fminf(acc[12], acc[13]), mef = fminf(acc[14], acc[15]);
+      return acc;
+    };
+    // the lane's best tile so far: its minimum, its first codeword and a copy of its 16 scores,
+    // kept with selects (no branch); the index inside the tile is resolved once, after the loop.
+    // First index on ties: a later tile replaces only a strictly smaller minimum.
+    auto keep_min = [&](const floatx16& acc, int th) {
+      const float m01 = fminf(acc[0], acc[1]), m23 = fminf(acc[2], acc[3]);
+      const float m45 = fminf(acc[4], acc[5]), m67 = fminf(acc[6], acc[7]);
+      const float m89 = fminf(acc[8], acc[9]), mab = fminf(acc[10], acc[11]);
+      const float mcd = fminf(acc[12], acc[13]), mef = fminf(acc[14], acc[15]);
       const float m = fminf(fminf(fminf(m01, m23), fminf(m45, m67)), fminf(fminf(m89, mab), fminf(mcd, mef)));
-      if (m < best) {
-        int vv = 15;
+      const bool better = m < best;
+      best = better ? m : best;
+      btile = better ? kb + 32 * th : btile;
 #pragma unroll
-        for (int v = 14; v >= 0; --v) vv = acc[v] == m ? v : vv;
-        best = m;
-        bidx = idx0 + 8 * (vv >> 2) + 4 * h + (vv & 3);
-      }
+      for (int v = 0; v < 16; ++v) snap[v] = better ? acc[v] : snap[v];
+    };
+    // two tiles at a time with their own accumulators: one tile's products run on the matrix core
+    // while the other's minimum runs on the vector unit
+    for (int th = 0; th < 8; th += 2) {
+      const bf16x8_t cwa = codewords(th), cwb = codewords(th + 1);
+      floatx16 acca = table(th), accb = table(th + 1);
+      acca = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cwa, bu1, acca, 0, 0, 0);
+      accb = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cwb, bu1, accb, 0, 0, 0);
+      acca = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cwa, bu2, acca, 0, 0, 0);
+      accb = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cwb, bu2, accb, 0, 0, 0);
+      keep_min(acca, th);
+      keep_min(accb, th + 1);
     }
+  }
+  int bidx;
+  {
+    int vv = 15;
+#pragma unroll
+    for (int v = 14; v >= 0; --v) vv = snap[v] == best ? v : vv;
+    bidx = btile + 8 * (vv >> 2) + 4 * h + (vv & 3);
   }
   // combine the two lane halves (same row, interleaved codewords), then the 4 waves
   {
@@ -595,7 +640,7 @@ hipError_t product_splits(const float* A, const float* B, bool trans_b, int64_t 
 
 int64_t ctx_bytes(int64_t n) {
   const int64_t nb = n / 8;
-  return a64(n * n) * 4 + a64(nb * kMeta) * 4 + nb * kCodes * 4 + (int64_t)kCodes * 8 * 4 + 256 * 8 * 4 + 256;
+  return a64(n * n) * 4 + a64(nb * kMeta) * 4 + nb * kCodes * 4 + (int64_t)kCodes * 8 * 4 + (256 * 8 + 256) * 4 + 256;
 }
 
 struct Ctx {
@@ -603,7 +648,7 @@ struct Ctx {
   float* meta;
   float* cgc;
   float* grid;
-  float* abs_tab;
+  float* pat;
   int* fail;
 };
 
@@ -615,7 +660,7 @@ Ctx carve_ctx(void* p, int64_t n) {
   x.meta = (float*)c; c += a64(nb * kMeta) * 4;
   x.cgc = (float*)c; c += nb * kCodes * 4;
   x.grid = (float*)c; c += (int64_t)kCodes * 8 * 4;
-  x.abs_tab = (float*)c; c += 256 * 8 * 4;
+  x.pat = (float*)c; c += (256 * 8 + 256) * 4;
   x.fail = (int*)c;
   return x;
 }
@@ -641,7 +686,7 @@ extern "C" int mpq_e8p12_cd_prepare(int64_t n, const float* Vs, void* ctx, int64
   // H = Vs Vs^T (the per-block grams are its 8x8 diagonal blocks)
   MPQ_HIP_TRY(gemm(Vs, n, Vs, n, true, nullptr, c.H, n, n, n, n, 1.f, 0.f, nullptr, 0, stream));
   MPQ_HIP_TRY(hipMemsetAsync(c.fail, 0, sizeof(int), stream));
-  hipLaunchKernelGGL(grid_kernel, dim3(kCodes / 256), dim3(256), 0, stream, c.grid, c.abs_tab);
+  hipLaunchKernelGGL(grid_kernel, dim3(kCodes / 256), dim3(256), 0, stream, c.grid, c.pat);
   hipLaunchKernelGGL(meta_kernel, dim3((unsigned)((nb + 63) / 64)), dim3(64), 0, stream, n, nb, c.H, c.meta,
                      c.fail);
   hipLaunchKernelGGL(cgc_kernel, dim3(kCodes / 256, (unsigned)nb), dim3(256), 0, stream, c.grid, c.meta, c.cgc);
@@ -734,7 +779,7 @@ extern "C" int mpq_e8p12_cd_polish(int64_t rows, int64_t n, int64_t block_rows, 
   StepArgs sa{};
   sa.rows = rows; sa.n = n; sa.nb = nb; sa.block_rows = block_rows;
   sa.tiles_per_rb = (int)tiles_per_rb; sa.accept_tol = accept_tol;
-  sa.order = order; sa.meta = cx.meta; sa.cgc = cx.cgc; sa.H = cx.H; sa.grid = cx.grid; sa.abs_tab = cx.abs_tab;
+  sa.order = order; sa.meta = cx.meta; sa.cgc = cx.cgc; sa.H = cx.H; sa.grid = cx.grid; sa.pat = cx.pat;
   sa.rhs = rhs; sa.x = x_out; sa.idx = idx_out; sa.res = res; sa.D = D; sa.Rt = Rt; sa.Xt = Xt;
   sa.ps = ps; sa.pi = pi; sa.accepted = acc;
   int64_t g = 0;  // global step counter: parity of the double buffers
