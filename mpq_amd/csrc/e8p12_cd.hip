@@ -266,7 +266,7 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
   __shared__ __align__(16) float s_cgc[kCS];
   static_assert(kCS >= kRT * 8 * kWS, "s_D does not fit in s_cgc");
   float* const s_D = s_cgc;
-  __shared__ __align__(16) float s_pat[256 * 8 + 256];  // abs-pattern magnitudes, then parities (int bits)
+  __shared__ __align__(16) float s_abs[(kCS / 256) * 8];  // magnitudes of the chunk's kCS / 256 abs patterns
   __shared__ __align__(16) float s_H[kWS * 64];  // H[8 j_s + d][8 j + e] of the window's steps s, entry 64 s + 8 e + d
   __shared__ float s_M[128];       // block j's L (64) and Gi (64)
   __shared__ float s_u[kRT][8];
@@ -320,13 +320,12 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
     fr = a.Rt[(int64_t)a.fin_par * rows * 8 + row * 8 + e];
     r0 = a.res[(int64_t)a.fin_par * rows + row];
   }
-  // the abs-pattern magnitudes (256 x 8) and parities: codewords are formed from their index
   const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  const float4 pt0 = reinterpret_cast<const float4*>(a.pat)[tid];
-  const float4 pt1 = reinterpret_cast<const float4*>(a.pat)[tid + 256];
-  const float pt2 = tid < 256 ? a.pat[2048 + tid] : 0.f;
   const int j = a.compute ? ord[a.t] : 0;
   const int c0 = blockIdx.y * kCS;
+  // the magnitudes of the chunk's abs patterns (codewords are formed from their index)
+  float4 ab0 = z4;
+  if (tid < kCS / 256 * 2) ab0 = reinterpret_cast<const float4*>(a.pat)[c0 / 256 * 2 + tid];
   float4 cg0 = z4, cg1 = z4, cg2 = z4, cg3 = z4;
   float hv0 = 0.f, hv1 = 0.f, hv2 = 0.f, hv3 = 0.f;
   float dv[kWS - 1];
@@ -354,8 +353,11 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
     xb = a.x[row * n + 8 * (int64_t)j + e];
   }
 
-  // ---- the previous step's candidate per row: earlier chunk wins ties
+  // ---- the previous step's candidate per row (earlier chunk wins ties) and its pattern's magnitude
+  // and parity, loaded here and used after the window's first part
   int bi = 0;
+  float cav = 0.f;
+  int cpar = 0;
   if (a.finalize) {
     float bs = ps[0];
     bi = pi[0];
@@ -366,12 +368,12 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
         bi = pi[c];
       }
     }
+    cav = a.pat[8 * (bi >> 8) + e];
+    cpar = __float_as_int(a.pat[2048 + (bi >> 8)]);
   }
 
   // ---- stage in LDS what the tile's rows share (and each row's window deltas s < p - 1)
-  reinterpret_cast<float4*>(s_pat)[tid] = pt0;
-  reinterpret_cast<float4*>(s_pat)[tid + 256] = pt1;
-  if (tid < 256) s_pat[2048 + tid] = pt2;
+  if (tid < kCS / 256 * 2) reinterpret_cast<float4*>(s_abs)[tid] = ab0;
   if (a.compute) {
     // H entry (s, d, e) of hv_q (i = tid + 256 q = 64 s + 8 d + e) goes to 64 s + 8 e + d
     const int ht = (tid & ~63) + 8 * (tid & 7) + ((tid >> 3) & 7);
@@ -410,11 +412,10 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
   // accept test and (chunk 0) the state updates
   float dl = 0.f;  // accepted delta of the finalized step, coordinate e
   if (a.finalize) {
-    const int k = bi >> 8, sb = bi & 255;
+    const int sb = bi & 255;
     const int branch = __builtin_popcount(sb) & 1;
-    const int signs = sb ^ (((branch ^ __float_as_int(s_pat[2048 + k])) & 1) << 7);
-    const float av = s_pat[8 * k + e];
-    const float cand = (branch ? -0.25f : 0.25f) + (((signs >> e) & 1) ? -av : av);
+    const int signs = sb ^ (((branch ^ cpar) & 1) << 7);
+    const float cand = (branch ? -0.25f : 0.25f) + (((signs >> e) & 1) ? -cav : cav);
     const float fd = cand - fx;
     float dg = 0.f;
 #pragma unroll
@@ -501,7 +502,7 @@ __global__ __launch_bounds__(256) void e8_cd_step_kernel(StepArgs a) {
     const int k = kb >> 8;
     const int bp = (int)kE8Parity[k];
     // lane half h generates coordinates 4 h .. 4 h + 3 of its codeword
-    const float* ak = s_pat + k * 8 + 4 * h;
+    const float* ak = s_abs + (k - c0 / 256) * 8 + 4 * h;
     const float a0 = ak[0], a1 = ak[1], a2 = ak[2], a3 = ak[3];
     // the codeword operand of tile th (32 codewords kb + 32 th + i)
     auto codewords = [&](int th) {
