@@ -87,6 +87,30 @@ def test_posterior_matches_oracle(gpu, prior):
     _check_post(got, ref["x1_blocks"], ref["var1"], ref["alpha1"], ref["map_idxs"])
 
 
+def test_posterior_without_usable_map_score(gpu):
+    """Rows where the MAP codeword's score cannot serve as the weights' reference: gamma <= 0 (the
+    nearest codeword is then the worst-scoring one) and a diverged message (|r| in the hundreds at
+    gamma 500, scores ~1e8 whose fp32 differences are rounding).  The kernel switches to the bound over
+    its components there; the first rows must still match the oracle, the diverged rows stay finite."""
+    gen = torch.Generator().manual_seed(29)
+    rows, nb = 6, 64
+    r1 = torch.randn(rows, nb, 8, generator=gen) * 0.8
+    gam = torch.tensor([[-0.3], [-2.0], [1e-12], [0.7], [500.0], [500.0]])
+    r1[4:] *= 300.0
+    _, cache = _grid_cache()
+    ref = oe8.posterior(r1, gam, cache)
+    got = vamp_vector_discrete_mmse_e8p12(r1_blocks=r1.to(gpu), gamma1=gam.to(gpu), cb=None)
+    x1, v = got["x1_blocks"].cpu(), got["var1"].cpu()
+    assert bool(torch.isfinite(x1).all()) and bool(torch.isfinite(v).all()) and bool((v >= 0).all())
+    # every coordinate of a codeword lies in [-3, 3], so does every mean
+    assert float(x1.abs().max()) <= 3.0
+    err = (x1[:4] - ref["x1_blocks"][:4]).norm(dim=-1) / ref["x1_blocks"][:4].norm(dim=-1).clamp_min(1e-3)
+    assert float(err.max()) <= POST_RTOL, float(err.max())
+    rv = ref["var1"][:4]
+    second = ref["x1_blocks"][:4].square().sum(-1) / 8 + rv
+    assert float(((v[:4] - rv).abs() / (2e-4 * rv + 256 * 2.0 ** -23 * second)).max()) <= 1.0
+
+
 def _e8_case(rows, n, seed_key):
     W, H = make_layer(rows, n, tokens=1024, seed_key=seed_key, heavy=True)
     Wr = W / W.square().mean().sqrt()
