@@ -62,14 +62,25 @@ __device__ __forceinline__ BaseEval eval_base(const float t[8], float cst_yn, fl
   return out;
 }
 
-template <bool kPrior, bool kVec4>
+// kSplit = false: one lane per vector, 256 vectors per work-group.  kSplit = true (few vectors): 64
+// vectors per work-group, one per lane, and the four waves split each vector's search -- wave p walks
+// shift branch p / 2, bases 128 (p % 2) .. + 127 -- then wave 0 combines the four (best score, first
+// group) pairs in index order, which is the order the one-lane search visits them in, and finishes.
+template <bool kPrior, bool kVec4, bool kSplit>
 __global__ __launch_bounds__(256) void e8p12_map_kernel(
     const float* __restrict__ r, int64_t n, const float* __restrict__ gamma, int64_t gamma_div,
     const float* __restrict__ center, const float* __restrict__ scale, float tau,
     int64_t* __restrict__ idx64, uint16_t* __restrict__ idx16, float* __restrict__ vals,
     float* __restrict__ err, float* __restrict__ score_out) {
-  const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (v >= n) return;
+  const int part = kSplit ? (int)(threadIdx.x >> 6) : 0;
+  const int64_t v0 = kSplit ? (int64_t)blockIdx.x * 64 + (threadIdx.x & 63)
+                            : (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if constexpr (!kSplit) {
+    if (v0 >= n) return;
+  }
+  // split: the four waves hold the same vectors, so a lane past the end stays (on the last vector)
+  // until the combine; every wave reaches the barrier
+  const int64_t v = v0 < n ? v0 : n - 1;
 
   float x[8];
   if constexpr (kVec4) {
@@ -114,7 +125,7 @@ __global__ __launch_bounds__(256) void e8p12_map_kernel(
   int best_g = 0;  // first group of MPQ_E8_GROUP bases (flattened branch*256 + k) holding `best`
   bool slow = false;
 
-  for (int br = 0; br < 2; ++br) {
+  for (int br = kSplit ? part >> 1 : 0; br < (kSplit ? (part >> 1) + 1 : 2); ++br) {
     const float off = br == 0 ? 0.25f : -0.25f;
     float y[8], t[8], u[8];
     unsigned neg = 0;
@@ -149,7 +160,34 @@ __global__ __launch_bounds__(256) void e8p12_map_kernel(
     const float p6_0 = u[6] * 0.5f, p6_1 = u[6] * 1.5f, p6_2 = u[6] * 2.5f;
     const float p7_0 = u[7] * 0.5f, p7_1 = u[7] * 1.5f, p7_2 = u[7] * 2.5f;
     const int br_group = br * (256 / MPQ_E8_GROUP);
+    if constexpr (!kSplit) {
 #include "e8p12_search.inc"
+    } else if ((part & 1) == 0) {
+#include "e8p12_search_h0.inc"
+    } else {
+#include "e8p12_search_h1.inc"
+    }
+  }
+  if constexpr (kSplit) {
+    __shared__ float s_best[4][64];
+    __shared__ int s_bg[4][64];
+    __shared__ int s_slow[4][64];
+    const int lane = threadIdx.x & 63;
+    s_best[part][lane] = best;
+    s_bg[part][lane] = best_g;
+    s_slow[part][lane] = slow ? 1 : 0;
+    __syncthreads();
+    if (part != 0 || v0 >= n) return;
+    // index order: (branch 0, bases 0..127), (0, 128..255), (1, 0..127), (1, 128..255); a later part
+    // replaces the running choice only with a strictly larger score, as the one-lane walk does
+    slow = s_slow[0][lane] | s_slow[2][lane];  // per branch: the same in both of its halves
+#pragma unroll
+    for (int p = 1; p < 4; ++p) {
+      if (s_best[p][lane] > best) {
+        best = s_best[p][lane];
+        best_g = s_bg[p][lane];
+      }
+    }
   }
 
   int br, k;
@@ -254,18 +292,24 @@ extern "C" int mpq_e8p12_map(const float* r, int64_t n, const float* gamma, int6
   const bool prior = center != nullptr && tau > 0.0f;
   MPQ_CHECK_ARG(idx64 || idx16 || vals || err || score, "mpq_e8p12_map: no output requested");
   const bool vec4 = (reinterpret_cast<uintptr_t>(r) & 15u) == 0;
+  // Below 2^19 vectors one lane per vector leaves SIMDs idle (2^19 / 64 lanes = 8 waves per SIMD on
+  // 256 CUs): four waves per vector then, 64 vectors per work-group.
+  const bool split = n < (int64_t(1) << 19);
   const int threads = 256;
-  const int64_t blocks = mpq_cdiv(n, threads);
+  const int64_t blocks = mpq_cdiv(n, split ? 64 : threads);
   MPQ_CHECK_ARG(blocks <= 0x7fffffff, "mpq_e8p12_map: n too large");
   dim3 grid((unsigned)blocks), block(threads);
-#define MPQ_E8_LAUNCH(P, V)                                                                  \
-  hipLaunchKernelGGL((e8p12_map_kernel<P, V>), grid, block, 0, stream, r, n, gamma, gamma_div, \
+#define MPQ_E8_LAUNCH(P, V, S)                                                                  \
+  hipLaunchKernelGGL((e8p12_map_kernel<P, V, S>), grid, block, 0, stream, r, n, gamma, gamma_div, \
                      center, scale, tau, idx64, idx16, vals, err, score)
+#define MPQ_E8_LAUNCH2(P, V) \
+  if (split) MPQ_E8_LAUNCH(P, V, true); else MPQ_E8_LAUNCH(P, V, false)
   if (prior) {
-    if (vec4) MPQ_E8_LAUNCH(true, true); else MPQ_E8_LAUNCH(true, false);
+    if (vec4) { MPQ_E8_LAUNCH2(true, true); } else { MPQ_E8_LAUNCH2(true, false); }
   } else {
-    if (vec4) MPQ_E8_LAUNCH(false, true); else MPQ_E8_LAUNCH(false, false);
+    if (vec4) { MPQ_E8_LAUNCH2(false, true); } else { MPQ_E8_LAUNCH2(false, false); }
   }
+#undef MPQ_E8_LAUNCH2
 #undef MPQ_E8_LAUNCH
   MPQ_LAUNCH_CHECK();
   return mpq::kOk;

@@ -42,6 +42,19 @@ def test_unit_precision_bit_exact(gpu, cache, scale):
     assert np.array_equal(out["err"].view(np.uint32), oe8.sqerr(x, idx, GRID).view(np.uint32))
 
 
+def test_one_lane_path_bit_exact(gpu, cache):
+    """From 2^19 vectors the kernel searches one vector per lane; below, four waves split each
+    vector's search (every other test here).  Both must give the oracle's results bit for bit."""
+    rng = np.random.default_rng(14)
+    n = (1 << 19) + 77
+    x = (rng.standard_normal((n, 8)) * 1.3).astype(np.float32)
+    out = _run(x, np.ones(1, np.float32), n, gpu)
+    idx, score = oe8.map_search(x, np.ones(1, np.float32), n, cache)
+    assert np.array_equal(out["idx"], idx)
+    assert np.array_equal(out["score"].view(np.uint32), score.view(np.uint32))
+    assert np.array_equal(out["err"].view(np.uint32), oe8.sqerr(x, idx, GRID).view(np.uint32))
+
+
 def test_row_precision_and_prior_bit_exact(gpu, cache):
     rng = np.random.default_rng(11)
     rows, nb = 64, 512
