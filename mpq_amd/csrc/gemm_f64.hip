@@ -68,11 +68,29 @@ __global__ __launch_bounds__(kThreads) void gemm_f64_kernel(F64Params p) {
   const int fr = lane & 15;   // fragment row / column
   const int fk = lane >> 4;   // fragment k
 
+  // C = alpha A B + beta C with alpha = +-1 and beta != 0 (the eigensolvers' updates, K = 64 or 128,
+  // which are bound by this read-modify-write of C): the accumulators start from alpha beta C, read
+  // before the K loop so that its latency hides behind the products (read after them it ran at
+  // 1-2 TB/s), and alpha acc is the result -- the same value as alpha (A B) + beta C up to the
+  // order of the fp64 sum.
+  const bool c_early = p.mode == kModeAxpby && p.beta != 0.0 && (p.alpha == 1.0 || p.alpha == -1.0);
   v4d acc[4][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v4d{0.0, 0.0, 0.0, 0.0};
+    for (int j = 0; j < 2; ++j) {
+      acc[i][j] = v4d{0.0, 0.0, 0.0, 0.0};
+      if (c_early) {
+        const double ab = p.alpha * p.beta;
+        const int64_t col = min(n0 + wn + 16 * j + fr, p.N - 1);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int64_t row = min(m0 + wm + 16 * i + fk + 4 * v, p.M - 1);
+          acc[i][j][v] = ab * p.C[row * p.ldc + col];
+        }
+      }
+    }
+  }
 
   double ra[kALoads], rb[kBLoads];
   // A slab: element e = u * 256 + tid is (row e / 16, k e % 16): 16 lanes read one row's 128 bytes
@@ -165,6 +183,8 @@ __global__ __launch_bounds__(kThreads) void gemm_f64_kernel(F64Params p) {
         if (row >= p.M) continue;
         if (p.mode == kModePartials) {
           p.C[(int64_t)blockIdx.z * p.split_stride + row * p.ldc + col] = acc[i][j][v];
+        } else if (c_early) {
+          p.C[row * p.ldc + col] = p.alpha * acc[i][j][v];
         } else {
           double* c = p.C + row * p.ldc + col;
           const double prod = p.alpha * acc[i][j][v];

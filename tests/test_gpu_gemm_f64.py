@@ -12,15 +12,17 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (17, 33, 5), (128, 64, 16), (130, 70, 200), (64, 64, 8192),
                                    (1000, 64, 1000), (300, 513, 64), (8, 8, 3000)])
 @pytest.mark.parametrize("trans_b", [False, True])
-def test_gemm_f64_matches_cpu(gpu, M, N, K, trans_b):
+@pytest.mark.parametrize("alpha,beta", [(0.75, -0.5), (-1.0, 1.0), (1.0, -0.5)])
+def test_gemm_f64_matches_cpu(gpu, M, N, K, trans_b, alpha, beta):
+    """alpha = +-1 with beta != 0 (the eigensolver's updates) starts the accumulators from C."""
     g = torch.Generator().manual_seed(M * 7919 + N * 31 + K)
     A = torch.randn(M, K, generator=g, dtype=torch.float64)
     B = torch.randn(N, K, generator=g, dtype=torch.float64) if trans_b else torch.randn(K, N, generator=g,
                                                                                           dtype=torch.float64)
     C0 = torch.randn(M, N, generator=g, dtype=torch.float64)
-    ref = 0.75 * (A @ (B.T if trans_b else B)) - 0.5 * C0
+    ref = alpha * (A @ (B.T if trans_b else B)) + beta * C0
     out = C0.to(gpu)
-    ops.gemm_f64(A.to(gpu), B.to(gpu), trans_b=trans_b, out=out, alpha=0.75, beta=-0.5)
+    ops.gemm_f64(A.to(gpu), B.to(gpu), trans_b=trans_b, out=out, alpha=alpha, beta=beta)
     scale = float((A.abs() @ (B.abs().T if trans_b else B.abs())).max()) + 1.0
     err = float((out.cpu() - ref).abs().max())
     assert err <= 64 * K * 2.0 ** -53 * scale + 1e-300, (err, scale)
