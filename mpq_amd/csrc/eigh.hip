@@ -44,7 +44,11 @@ namespace {
 constexpr int kNB = 128;  // reflectors per compact-WY block of the back-transformation
 constexpr int kPB = 32;   // reflectors per tridiagonalisation panel (latrd block)
 constexpr int kTB = 64;   // symv tile edge
-constexpr int kCH = 8;    // most symv tiles per work-group (one chunk of a column strip)
+// most symv tiles per work-group (one chunk of a column strip): 4 in fp32, 8 in fp64 (measured: fp32
+// n = 4096 67.6 ms per solve at 4 against 71.1 at 8 and 83.8 at 16; fp64 n = 8192 336 ms at 8, 340
+// at 4, 350 at 16)
+template <typename T>
+constexpr int ch_max() { return sizeof(T) == 4 ? 4 : 8; }
 constexpr int kThr = 256;
 constexpr int kSub = 8;               // finish_kernel lanes per matrix row
 constexpr int kRowsPB = kThr / kSub;  // finish_kernel rows per work-group
@@ -224,7 +228,7 @@ __global__ __launch_bounds__(kThr) void symv_kernel(const T* __restrict__ A, int
   if (bi_first >= nblk) return;  // uniform over the work-group, before any barrier
   const int bi_end = min(bi_first + chl, nblk);
   __shared__ T red[kThr / 64];
-  __shared__ T sv[(kCH + 1) * kTB];
+  __shared__ T sv[(ch_max<T>() + 1) * kTB];
   __shared__ T scol[16][kTB + 1];
   const int cq = threadIdx.x & 15, r0 = threadIdx.x >> 4;
   const T* colbase = A + (int64_t)bj * kTB + 4 * cq;
@@ -740,9 +744,9 @@ int sytrd(int64_t n, const SyevdLayout& L, T* base, hipStream_t stream) {
     for (int i = 0; i < nbl; ++i) {
       const int64_t c = i0 + i;
       const int ns = (int)L.nblk - (int)((c + 1) / kTB);
-      // chunk length: kCH tiles (fewest partials) except on small trailing matrices, where more
+      // chunk length: ch_max tiles (fewest partials) except on small trailing matrices, where more
       // and shorter work-groups shorten the kernel
-      const int chl = ns > 32 ? kCH : 1;
+      const int chl = ns > 32 ? ch_max<T>() : 1;
       const int chy = (ns + chl - 1) / chl;
       if (chy >= kThr - 1) {
         set_error("mpq_syevd: internal chunk count %d too large", chy);
