@@ -18,7 +18,7 @@ namespace mpq {
 
 hipError_t e8p12_posterior(const float* r, int64_t n, const float* gamma, int64_t gamma_div,
                            const float* center, const float* scale, float tau, const float* map_vals,
-                           float* x1, float* var, hipStream_t stream);
+                           float* x1, float* var, hipStream_t stream, float* var_wg);
 
 namespace {
 
@@ -62,6 +62,7 @@ E8Plan e8_plan(int64_t rows, int64_t n) {
   b += a64(rows * p.nb) * 8;                    // map idx
   b += a64(16 * rows) * 4;                      // row arrays
   b += a64(3 * rows * p.nchunks) * 4;           // chunk partials
+  b += a64(rows * ((p.nb + 63) / 64)) * 4;      // per-work-group variance sums of the posterior
   b += 256;                                     // status
   p.bytes = b;
   return p;
@@ -143,6 +144,7 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
   int64_t* midx = (int64_t*)p; p += a64(rows * nb) * 8;
   float* rowbuf = (float*)p; p += a64(16 * rows) * 4;
   float* part = (float*)p; p += a64(3 * rows * nchunks) * 4;
+  float* var_wg = (float*)p; p += a64(rows * ((nb + 63) / 64)) * 4;
   VampStatus* status = (VampStatus*)p;
   float* g1 = rowbuf + 0 * rows;
   float* g1w = rowbuf + 1 * rows;
@@ -250,10 +252,15 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
     int e = mpq_e8p12_map(r1, rows * nb, g1w, nb, center, prior_scale, tau, nullptr, nullptr, mvals, nullptr, nullptr,
                           stream);
     if (e != kOk) return e;
-    MPQ_HIP_TRY(e8p12_posterior(r1, rows * nb, g1w, nb, center, prior_scale, tau, mvals, x1, var1, stream));
-    hipLaunchKernelGGL(row_sum_kernel, dim3((unsigned)rows), eb, 0, stream, nb, var1, varsum);
+    // a row's variances: whole work-groups of the posterior (nb % 64 == 0), summed in the row kernel,
+    // else a reduction launch of its own
+    const bool wg_rows = nb % 64 == 0;
+    MPQ_HIP_TRY(e8p12_posterior(r1, rows * nb, g1w, nb, center, prior_scale, tau, mvals, x1, var1, stream,
+                                wg_rows ? var_wg : nullptr));
+    if (!wg_rows) hipLaunchKernelGGL(row_sum_kernel, dim3((unsigned)rows), eb, 0, stream, nb, var1, varsum);
     *seq = ++mb->seq;
-    hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, nb, 1, varsum, g1w, has_prev ? 1 : 0,
+    hipLaunchKernelGGL(rows_alpha1_kernel, dim3(1), eb, 0, stream, rows, nb, wg_rows ? (int)(nb / 64) : 1,
+                       wg_rows ? var_wg : varsum, g1w, has_prev ? 1 : 0,
                        damping, g2prev, a1raw, a1, eta1, g2new, g2, status, mb->dev(*seq), *seq);
     MPQ_LAUNCH_CHECK();
     return kOk;
@@ -291,19 +298,19 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
     MPQ_HIP_TRY(prod(r2, V, false, 0, planes != nullptr));
     hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, Yu, S, g2, obs_f, x1, part,
                        planes);
+    // without best-iterate tracking the row kernel publishes this iteration's status (its EM statistic
+    // and alpha2 clips are all the host reads); with it the hard state's row kernel does, after it
+    const unsigned st_seq = best_iterate ? 0u : ++mb->seq;
     hipLaunchKernelGGL(rows_lmmse_kernel, dim3(1), eb, 0, stream, rows, n, n, nchunks, part, g2, damping, eta2,
-                       g1new, g1, nullptr, status);
+                       g1new, g1, nullptr, status, best_iterate ? nullptr : mb->dev(st_seq), st_seq);
     MPQ_LAUNCH_CHECK();
     MPQ_HIP_TRY(prod(x1, V, true, 1, planes != nullptr));
     hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, r2, eta2, g2, g1new, damping,
                        r1);
     MPQ_LAUNCH_CHECK();
-    const unsigned st_seq = ++mb->seq;
+    const unsigned wait_seq = best_iterate ? ++mb->seq : st_seq;
     if (best_iterate) {
-      if ((rc = map_state(r1, g1, st_seq)) != kOk) return rc;
-    } else {
-      hipLaunchKernelGGL(publish_status_kernel, dim3(1), dim3(64), 0, stream, status, mb->dev(st_seq), st_seq);
-      MPQ_LAUNCH_CHECK();
+      if ((rc = map_state(r1, g1, wait_seq)) != kOk) return rc;
     }
     std::swap(r2, r2prev);
     std::swap(g2, g2prev);
@@ -316,7 +323,7 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
       MPQ_HIP_TRY(copy_rows(g1w, 0, g1, 0, 1, rows * 4, stream));
       if ((rc = launch_alpha1(&ahead_seq)) != kOk) return rc;
     }
-    if ((rc = wait_status(mb, st_seq, hs, stream)) != kOk) return rc;
+    if ((rc = wait_status(mb, wait_seq, hs, stream)) != kOk) return rc;
     a2_clip += hs->a2_clip;
     if (em_active) {
       const float den = hs->em_mean < 1e-12f ? 1e-12f : hs->em_mean;

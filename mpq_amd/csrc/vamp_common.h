@@ -306,7 +306,8 @@ __global__ __launch_bounds__(kEW) void lmmse_epi1_kernel(
 __global__ __launch_bounds__(kEW) void rows_lmmse_kernel(
     int64_t rows, int64_t n, int64_t rank, int nchunks, const float* __restrict__ part3,
     const float* __restrict__ g2, float damping, float* __restrict__ eta2,
-    float* __restrict__ g1new, float* __restrict__ g1, float* __restrict__ g1w, VampStatus* __restrict__ st) {
+    float* __restrict__ g1new, float* __restrict__ g1, float* __restrict__ g1w, VampStatus* __restrict__ st,
+    StatusMailbox* box = nullptr, unsigned seq = 0u) {
   __shared__ float red[kEW / 64];
   const float hi = one_minus_alpha_eps();
   const float c0 = (float)(1.0 - (double)rank / (double)n);
@@ -356,6 +357,7 @@ __global__ __launch_bounds__(kEW) void rows_lmmse_kernel(
     st->a2_clip = (int)s_clip;
     st->em_mean = em / (float)rows;
     st->a2_mean = a2s / (float)rows;
+    if (box) publish_to(st, box, seq);  // saves the launch of publish_status_kernel
   }
 }
 
