@@ -79,15 +79,34 @@ def test_refine_codebook_matches_oracle(gpu, m, n, key, heavy, x6, monkeypatch):
     floor = max(1e-6, 1e-6 * max(float(torch.diagonal(Hd).mean().abs()), float(lam.max()), 1e-12))
     Vs = V.flip(1) * torch.sqrt(lam.clamp_min(floor).flip(0)).unsqueeze(0)
     Yu = Wr.matmul(Vs)
-    ref_x, ref_i = [], []
-    for r0 in range(0, m, 128):
-        sl = slice(r0, min(m, r0 + 128))
-        x_b, i_b, _ = oe8.gram_block_cd(hat0.cpu()[sl], idx0.cpu()[sl], Yu[sl], Vs, grid, 3)
-        ref_x.append(x_b)
-        ref_i.append(i_b)
-    ref_x, ref_i = torch.cat(ref_x), torch.cat(ref_i)
+    def polish(Vs_, scores_fp64=False):
+        Yu_ = Wr.matmul(Vs_)
+        xs, ids = [], []
+        for r0 in range(0, m, 128):
+            sl = slice(r0, min(m, r0 + 128))
+            x_b, i_b, _ = oe8.gram_block_cd(hat0.cpu()[sl], idx0.cpu()[sl], Yu_[sl], Vs_, grid, 3,
+                                            scores_fp64=scores_fp64)
+            xs.append(x_b)
+            ids.append(i_b)
+        return torch.cat(xs), torch.cat(ids)
+
+    ref_x, ref_i = polish(Vs)
     agree = float((idx == ref_i).float().mean())
-    assert agree >= 0.99, agree
+    # the adapter polishes in its own device decomposition; the greedy block CD turns last-bit
+    # differences of Vs into different decisions, so the bar is 99.9 % or the oracle's agreement with
+    # itself under such roundings (Vs moved by one ulp at random, the argmin scores in fp64)
+    floor = 1.0
+    if agree < 0.999:
+        for seed in (1, 2):
+            gen = torch.Generator().manual_seed(seed)
+            step = torch.randint(-1, 2, Vs.shape, generator=gen)
+            alt = torch.where(step > 0, torch.nextafter(Vs, torch.full_like(Vs, float("inf"))),
+                              torch.where(step < 0, torch.nextafter(Vs, torch.full_like(Vs, float("-inf"))), Vs))
+            floor = min(floor, float((polish(alt)[1] == ref_i).float().mean()))
+        floor = min(floor, float((polish(Vs, scores_fp64=True)[1] == ref_i).float().mean()))
+    print(f"refine {m}x{n} x6={x6}: VAMP codes {agree0:.5f}, polished codes {agree:.5f} (reference floor "
+          f"{floor:.5f})")
+    assert agree >= min(0.999, floor), (agree, floor)
     s_ref, s_got = _surrogate(Wr, ref_x, H), _surrogate(Wr, hat, H)
     assert abs(s_got - s_ref) <= 5e-3 * s_ref, (s_got, s_ref)
 
