@@ -265,13 +265,32 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
     MPQ_LAUNCH_CHECK();
     return kOk;
   };
+  // r2 message and the first LMMSE product: they write only the message, the product's partials, the
+  // LMMSE mean (in x1) and its row partials, which a gamma retry recomputes (the retried posterior
+  // rewrites x1), so they are queued behind the first denoiser pass before its status is read
+  auto launch_lmmse_head = [&](float obs_f) -> int {
+    hipLaunchKernelGGL(msg_r2_kernel, eg, eb, 0, stream, n, x1, r1, eta1, g1w, g2new, has_prev ? 1 : 0, damping,
+                       r2prev, r2, planes);
+    MPQ_LAUNCH_CHECK();
+    MPQ_HIP_TRY(prod(r2, V, false, 0, planes != nullptr));
+    hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, Yu, S, g2, obs_f, x1, part,
+                       planes);
+    MPQ_LAUNCH_CHECK();
+    return kOk;
+  };
   unsigned ahead_seq = 0;  // the iteration's first denoiser pass, launched at the end of the one before
   for (int it = 0; it < iters; ++it) {
     if (ahead_seq == 0) MPQ_HIP_TRY(copy_rows(g1w, 0, g1, 0, 1, rows * 4, stream));
+    const float obs_f = (float)obs;
+    bool head_queued = false;  // the LMMSE head of the pass whose status is read last
     for (int attempt = 0; attempt <= retry_steps; ++attempt) {
       unsigned a1_seq = ahead_seq;
       ahead_seq = 0;
       if (a1_seq == 0 && (rc = launch_alpha1(&a1_seq)) != kOk) return rc;
+      if (attempt == 0) {
+        if ((rc = launch_lmmse_head(obs_f)) != kOk) return rc;
+        head_queued = true;
+      }
       if ((rc = wait_status(mb, a1_seq, hs, stream)) != kOk) return rc;
       if (hs->a1_invalid == 0) break;
       if (attempt >= retry_steps) {
@@ -280,24 +299,19 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
           set_error_code(kNumerical);
           return kNumerical;
         }
-        break;
+        break;  // clamped alpha1 already in place (before the queued head read it)
       }
       a1_retry += hs->a1_invalid;
       hipLaunchKernelGGL(rows_retry_kernel, dim3(1), eb, 0, stream, rows, a1raw, retry_factor, g1w);
+      head_queued = false;
       MPQ_LAUNCH_CHECK();
     }
     if (hs->g2new_invalid || hs->g2_invalid) {
       ++g2_invalid;
-      continue;
+      continue;  // the queued head's results are never read
     }
     const float a1_mean_it = hs->a1_mean;
-    const float obs_f = (float)obs;
-    hipLaunchKernelGGL(msg_r2_kernel, eg, eb, 0, stream, n, x1, r1, eta1, g1w, g2new, has_prev ? 1 : 0, damping,
-                       r2prev, r2, planes);
-    MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(prod(r2, V, false, 0, planes != nullptr));
-    hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, Yu, S, g2, obs_f, x1, part,
-                       planes);
+    if (!head_queued && (rc = launch_lmmse_head(obs_f)) != kOk) return rc;
     // without best-iterate tracking the row kernel publishes this iteration's status (its EM statistic
     // and alpha2 clips are all the host reads); with it the hard state's row kernel does, after it
     const unsigned st_seq = best_iterate ? 0u : ++mb->seq;

@@ -432,6 +432,21 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
                        has_prev ? 1 : 0, damping, g2prev, a1raw, a1, eta1, g2new, g2, w.status, mb->dev(seq), seq);
     return seq;
   };
+  // r2 message and the first LMMSE product (obs as used by this iteration).  They write only the
+  // message, the product's partials, the LMMSE mean (in x1) and its row partials, which a gamma retry
+  // recomputes from scratch (the retried denoiser rewrites x1), so the loop queues them behind the
+  // first denoiser pass before that pass's status is read, and the GPU has work while the host
+  // waits; after a retry (g1w rescaled) they run again from the retried pass.
+  auto launch_lmmse_head = [&](float obs_f) -> int {
+    hipLaunchKernelGGL(msg_r2_kernel, eg, eb, 0, stream, n, w.x1, w.r1, eta1, g1w, g2new,
+                       has_prev ? 1 : 0, damping, w.r2prev, w.r2, planes);
+    MPQ_LAUNCH_CHECK();
+    MPQ_HIP_TRY(product(w, w.r2, pr.V, false, kOpV, rows, n, stream, planes != nullptr));
+    hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, pr.S, g2,
+                       obs_f, w.x1, w.part, planes);
+    MPQ_LAUNCH_CHECK();
+    return kOk;
+  };
   unsigned ahead_seq = 0;  // the iteration's first denoiser pass, launched at the end of the one before
   for (int it = 0; it < iters; ++it) {
     // ---- denoiser with gamma retries (mpq/solver.py:559-596), from g1w = g1
@@ -439,12 +454,18 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
       if (!g1w_current) MPQ_HIP_TRY(copy_rows(g1w, 0, g1, 0, 1, rows * 4, stream));
       g1w_current = true;
     }
+    const float obs_f = (float)obs;
+    bool head_queued = false;  // the LMMSE head of the pass whose status is read last
     for (int attempt = 0; attempt <= retry_steps; ++attempt) {
       unsigned a1_seq = ahead_seq;
       ahead_seq = 0;
       if (a1_seq == 0) {
         a1_seq = launch_alpha1();
         MPQ_LAUNCH_CHECK();
+      }
+      if (attempt == 0) {
+        if ((rc = launch_lmmse_head(obs_f)) != kOk) return rc;
+        head_queued = true;
       }
       if ((rc = wait_status(mb, a1_seq, hs, stream)) != kOk) return rc;
       if (hs->a1_invalid == 0) break;
@@ -454,26 +475,21 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
           set_error_code(kNumerical);
           return kNumerical;
         }
-        break;  // clamped alpha1 already in place
+        break;  // clamped alpha1 already in place (before the queued head read it)
       }
       a1_retry += hs->a1_invalid;
       hipLaunchKernelGGL(rows_retry_kernel, dim3(1), eb, 0, stream, rows, a1raw, retry_factor, g1w);
       g1w_current = false;
+      head_queued = false;
       MPQ_LAUNCH_CHECK();
     }
     if (hs->g2new_invalid || hs->g2_invalid) {  // mpq/solver.py:602-604, 613-615
       ++g2_invalid;
-      continue;
+      continue;  // the queued head's results are never read
     }
     const float a1_mean_it = hs->a1_mean;
-    // ---- r2 message, LMMSE (obs as used by this iteration)
-    const float obs_f = (float)obs;
-    hipLaunchKernelGGL(msg_r2_kernel, eg, eb, 0, stream, n, w.x1, w.r1, eta1, g1w, g2new,
-                       has_prev ? 1 : 0, damping, w.r2prev, w.r2, planes);
-    MPQ_LAUNCH_CHECK();
-    MPQ_HIP_TRY(product(w, w.r2, pr.V, false, kOpV, rows, n, stream, planes != nullptr));
-    hipLaunchKernelGGL(lmmse_epi1_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, Yu, pr.S, g2,
-                       obs_f, w.x1, w.part, planes);
+    // ---- LMMSE
+    if (!head_queued && (rc = launch_lmmse_head(obs_f)) != kOk) return rc;
     hipLaunchKernelGGL(rows_lmmse_kernel, dim3(1), eb, 0, stream, rows, n, n, nchunks, w.part, g2, damping,
                        eta2, g1new, g1, g1w, w.status);
     MPQ_LAUNCH_CHECK();

@@ -163,6 +163,36 @@ def test_vamp_matches_oracle(gpu, packed):
     assert torch.allclose(g1.cpu(), ref_st["gamma1"], rtol=1e-2)
 
 
+@pytest.mark.parametrize("packed", [False, True])
+def test_vamp_gamma_retries_match_oracle(gpu, packed):
+    """gamma_start 1e-8: the first iteration's alpha1 (4e-9 .. 5.5e-9 in the oracle, far below the
+    1e-7 bound) stays invalid through its three retries and the iteration continues with the clamped
+    alpha1; later iterations are valid (the oracle's posterior runs 19 times in 16 iterations).  The r2
+    message and first LMMSE product, queued before the first pass's status is read, are discarded
+    after the retries and run again from the last pass.  (Large gamma_start values retry where the
+    posterior collapses onto one codeword: there alpha1 = gamma1 var rests on the cancellation in
+    var = E|c|^2 / 8 - |mu|^2 / 8, and fp32 rounding alone decides whether it crosses 1e-7.)"""
+    gamma_start = 1e-8
+    Wr, V, S, hat0 = _e8_case(64, 512, "e8vamp:gpu")
+    grid, cache = _grid_cache()
+    cfg = dict(iters=16, damping=0.5, prior_tau=0.25, polish_sweeps=0, gamma_start=gamma_start)
+    ref_hat, ref_idx, ref_err, ref_st = oe8.solve_e8p12_rankspace_vamp(Wr, hat0, V, S, grid, cache, cfg)
+
+    class Cfg(_Cfg):
+        pass
+
+    Cfg.gamma_start = gamma_start
+    idx, hat, err, r1, g1, st = _gpu_vamp(Wr, hat0, V, S, Cfg, gpu, packed=packed)
+    agree = float((idx.cpu() == ref_idx).float().mean())
+    print("retries", st["alpha1_retry_count"], "agreement", agree)
+    assert st["alpha1_retry_count"] > 0
+    assert agree >= 0.999, agree
+    assert abs(st["obs_precision_final"] - ref_st["obs_final"]) <= 2e-3 * ref_st["obs_final"]
+    assert abs(float(err.mean()) - float(ref_err.mean())) <= 2e-3 * float(ref_err.mean())
+    r1_rel = float((r1.cpu() - ref_st["r1"]).norm() / ref_st["r1"].norm())
+    assert r1_rel <= 1e-3, r1_rel
+
+
 def test_vamp_best_iterate_never_worse_than_its_start(gpu):
     """best_iterate keeps the iterate whose MAP decision has the lowest rank-space error, starting from the
     MAP of the initial state (mpq/solver.py:940-958, 1083-1121)."""

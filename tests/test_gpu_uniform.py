@@ -144,6 +144,28 @@ def test_vamp_block_matches_oracle(gpu, rotate, bits, packed):
     assert abs(float(e.mean()) - float(e_ref.mean())) <= 5e-3 * float(e_ref.mean())
 
 
+@pytest.mark.parametrize("packed", [False, True])
+def test_vamp_block_gamma_retries_match_oracle(gpu, packed):
+    """gamma_start 100: the first denoiser pass finds alpha1 outside (1e-7, 1 - 1e-7) on most rows and
+    the loop retries with rescaled gamma1 twice before alpha1 is valid (the oracle's posterior runs
+    five times).  The r2 message and first LMMSE product, queued before the first pass's status is
+    read, are discarded and run again from the retried pass."""
+    W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq = _setup_block(128, 512, 4, 128, "vb4", rotate=True)
+    cfg = dict(RECIPE, polish_sweeps=0, gamma_start=100.0)
+    q_ref, x_ref, e_ref, rtn_ref, tr = ou.solve_uniform_rankspace_vamp(W, xr, sf, zf, maxq, V, V.T, S, Vs, cfg)
+    vcfg = UniformVampConfig(**{k: v for k, v in cfg.items()})
+    pk = ops.rankspace_pack(V.to(gpu), Vs.to(gpu)) if packed else None
+    q, x, e, rtn, st = ops.uniform_vamp_solve(W.to(gpu), xr.to(gpu), sg.to(gpu), zg.to(gpu), 128, maxq, V.to(gpu),
+                                              S.to(gpu), Vs.to(gpu), vcfg, want_x=True, packed=pk)
+    agree = float((q.cpu().long() == q_ref.long()).float().mean())
+    print("retries", st["alpha1_retry_count"], "agreement", agree, "best/stop", st["best_iter"], st["stop_iter"])
+    assert st["alpha1_retry_count"] > 0
+    assert agree >= 0.999
+    assert st["best_iter"] == tr["best_iter"] and st["stop_iter"] == tr["stop_iter"]
+    assert abs(st["obs_precision_final"] - tr["obs_final"]) <= 1e-4 * tr["obs_final"]
+    assert abs(float(e.mean()) - float(e_ref.mean())) <= 5e-3 * float(e_ref.mean())
+
+
 def test_vamp_block_with_caller_products(gpu):
     # mpq_uniform_vamp_solve_ex: W Vs and x_init Vs from the caller (one product over all rows), and
     # the returned x_best Vs; matches the oracle like the per-block path, and x_best Vs is the
