@@ -285,7 +285,8 @@ def run_mpq_quantization(
         obs_precision = float(vamp_cfg.obs_precision)
     else:
         sq = (Yu_all - XR_all).square().sum(dim=1)
-        sums = [float(sq[r0:r0 + block_rows].sum().item()) for r0 in range(0, rows, block_rows)]
+        # one device sum per block (as the reference's per-block loop forms them), read back at once
+        sums = torch.stack([sq[r0:r0 + block_rows].sum() for r0 in range(0, rows, block_rows)]).tolist()
         mse = max(sum(sums) / max(rows * cols, 1), 1e-12)
         obs_precision = 1.0 / mse
 

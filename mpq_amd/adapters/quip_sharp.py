@@ -266,6 +266,7 @@ def mpq_refine_codebook(
 
     obs_block = float(obs_precision)
     gamma_sum, gamma_count, gamma_min, gamma_max = 0.0, 0, math.inf, -math.inf
+    gamma_blocks = []
     block_stats = []
     t0 = time.time()
     if solver == "vamp":
@@ -283,12 +284,15 @@ def mpq_refine_codebook(
             final_idx[r0:r1] = idx_b
             if bool(vamp_cfg.em_obs_precision) and float(vamp_cfg.obs_precision) <= 0.0:
                 obs_block = float(st["obs_precision_final"])
+            # the block's gamma1 sum (fp64), min and max stay on the device until the loop ends
             g64 = g1_b.double()
-            gamma_sum += float(g64.sum().item())
+            gamma_blocks.append(torch.stack([g64.sum(), g64.min(), g64.max()]))
             gamma_count += int(g64.numel())
-            gamma_min = min(gamma_min, float(g64.min().item()))
-            gamma_max = max(gamma_max, float(g64.max().item()))
             block_stats.append(st)
+        for g_sum, g_min, g_max in (torch.stack(gamma_blocks).tolist() if gamma_blocks else []):
+            gamma_sum += g_sum
+            gamma_min = min(gamma_min, g_min)
+            gamma_max = max(gamma_max, g_max)
         del ws
     del packed
     torch.cuda.synchronize(device)
