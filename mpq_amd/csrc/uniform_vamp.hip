@@ -34,7 +34,83 @@ enum DenoiseMode : int { kPosterior = 0, kHardMap = 1, kHardRoundMean = 2, kFull
 constexpr int kRegAtoms = 16;  // grids up to 4 bits keep their scores in registers
 
 // Per element: posterior of a uniform grid a_q = s(q - z), q = 0..maxq, under the
-// channel N(r1, 1/gamma) and the prior N(W, (tau*s)^2)  (mpq/priors/uniform.py:177-191).
+// channel N(r1, 1/gamma) and the prior N(W, (tau*s)^2)  (mpq/priors/uniform.py:177-191): the
+// first argmax of the atom scores and (MOMENTS) the softmax mean and variance.
+template <bool MOMENTS>
+__device__ __forceinline__ void denoise_element(float r, float c, float s, float z, float mh, float tau, int maxq,
+                                                int& arg_out, float& mean_out, float& var_out) {
+  float st2 = 0.f;
+  if (tau > 0.f) {
+    const float sc = s < 1e-12f ? 1e-12f : s;
+    const float ts = tau * sc;
+    st2 = ts * ts;
+  }
+  // score of atom q (the division is kept as a division: MAP decisions are bit-exact)
+  auto score_of = [&](int q) {
+    const float a = s * ((float)q - z);
+    const float d = a - r;
+    float score = mh * (d * d);
+    if (tau > 0.f) {
+      const float dc = a - c;
+      score = score - (0.5f * (dc * dc)) / st2;
+    }
+    return score;
+  };
+  // pass 1: scores, max, first argmax.  Grids of up to kRegAtoms levels (4-bit) keep the scores
+  // in registers for pass 2, so each score is computed once.
+  float sc_reg[kRegAtoms];
+  const bool in_regs = maxq < kRegAtoms;
+  float mx = -INFINITY;
+  int arg = 0;
+  if (in_regs) {
+#pragma unroll
+    for (int q = 0; q < kRegAtoms; ++q) {
+      sc_reg[q] = q <= maxq ? score_of(q) : -INFINITY;
+      if (q <= maxq && sc_reg[q] > mx) {
+        mx = sc_reg[q];
+        arg = q;
+      }
+    }
+  } else {
+    for (int q = 0; q <= maxq; ++q) {
+      const float score = score_of(q);
+      if (score > mx) {
+        mx = score;
+        arg = q;
+      }
+    }
+  }
+  arg_out = arg;
+  if (MOMENTS) {
+    // pass 2: softmax moments
+    float zsum = 0.f, m1 = 0.f, m2 = 0.f;
+    if (in_regs) {
+#pragma unroll
+      for (int q = 0; q < kRegAtoms; ++q) {
+        if (q > maxq) break;
+        const float a = s * ((float)q - z);
+        const float w = expf(sc_reg[q] - mx);
+        zsum += w;
+        m1 += w * a;
+        m2 += w * (a * a);
+      }
+    } else {
+      for (int q = 0; q <= maxq; ++q) {
+        const float a = s * ((float)q - z);
+        const float w = expf(score_of(q) - mx);
+        zsum += w;
+        m1 += w * a;
+        m2 += w * (a * a);
+      }
+    }
+    const float mean = m1 / zsum;
+    const float second = m2 / zsum;
+    const float var = second - mean * mean;
+    mean_out = mean;
+    var_out = var < 0.f ? 0.f : var;
+  }
+}
+
 template <int MODE>
 __global__ __launch_bounds__(kEW) void uniform_denoise_kernel(
     const float* __restrict__ r1, const float* __restrict__ gamma, const float* __restrict__ W,
@@ -57,84 +133,19 @@ __global__ __launch_bounds__(kEW) void uniform_denoise_kernel(
     const float c = W[b * ldw + j];
     const float s = grp(scale, b, G, gs, j);
     const float z = grp(zero, b, G, gs, j);
-    float st2 = 0.f;
-    if (tau > 0.f) {
-      const float sc = s < 1e-12f ? 1e-12f : s;
-      const float ts = tau * sc;
-      st2 = ts * ts;
+    int arg;
+    float mean = 0.f, var = 0.f;
+    denoise_element<MODE == kPosterior || MODE == kHardRoundMean || MODE == kFull>(r, c, s, z, mh, tau, maxq, arg,
+                                                                                 mean, var);
+    if (MODE == kPosterior) {
+      mean_out[b * n + j] = mean;
+      vsum += var;
     }
-    // score of atom q (the division is kept as a division: MAP decisions are bit-exact)
-    auto score_of = [&](int q) {
-      const float a = s * ((float)q - z);
-      const float d = a - r;
-      float score = mh * (d * d);
-      if (tau > 0.f) {
-        const float dc = a - c;
-        score = score - (0.5f * (dc * dc)) / st2;
-      }
-      return score;
-    };
-    // pass 1: scores, max, first argmax.  Grids of up to kRegAtoms levels (4-bit) keep the scores
-    // in registers for pass 2, so each score is computed once.
-    float sc_reg[kRegAtoms];
-    const bool in_regs = maxq < kRegAtoms;
-    float mx = -INFINITY;
-    int arg = 0;
-    if (in_regs) {
-#pragma unroll
-      for (int q = 0; q < kRegAtoms; ++q) {
-        sc_reg[q] = q <= maxq ? score_of(q) : -INFINITY;
-        if (q <= maxq && sc_reg[q] > mx) {
-          mx = sc_reg[q];
-          arg = q;
-        }
-      }
-    } else {
-      for (int q = 0; q <= maxq; ++q) {
-        const float score = score_of(q);
-        if (score > mx) {
-          mx = score;
-          arg = q;
-        }
-      }
-    }
-    float mean = 0.f;
-    if (MODE == kPosterior || MODE == kHardRoundMean || MODE == kFull) {
-      // pass 2: softmax moments
-      float zsum = 0.f, m1 = 0.f, m2 = 0.f;
-      if (in_regs) {
-#pragma unroll
-        for (int q = 0; q < kRegAtoms; ++q) {
-          if (q > maxq) break;
-          const float a = s * ((float)q - z);
-          const float w = expf(sc_reg[q] - mx);
-          zsum += w;
-          m1 += w * a;
-          m2 += w * (a * a);
-        }
-      } else {
-        for (int q = 0; q <= maxq; ++q) {
-          const float a = s * ((float)q - z);
-          const float w = expf(score_of(q) - mx);
-          zsum += w;
-          m1 += w * a;
-          m2 += w * (a * a);
-        }
-      }
-      mean = m1 / zsum;
-      const float second = m2 / zsum;
-      float var = second - mean * mean;
-      var = var < 0.f ? 0.f : var;
-      if (MODE == kPosterior) {
-        mean_out[b * n + j] = mean;
-        vsum += var;
-      }
-      if (MODE == kFull) {
-        mean_out[b * n + j] = mean;
-        var_part[b * n + j] = var;  // per-element variance in this mode
-        reinterpret_cast<int64_t*>(q_out)[b * n + j] = arg;
-        x_out[b * n + j] = s * ((float)arg - z);
-      }
+    if (MODE == kFull) {
+      mean_out[b * n + j] = mean;
+      var_part[b * n + j] = var;  // per-element variance in this mode
+      reinterpret_cast<int64_t*>(q_out)[b * n + j] = arg;
+      x_out[b * n + j] = s * ((float)arg - z);
     }
     if (MODE == kHardMap || MODE == kHardRoundMean) {
       int q = arg;
@@ -158,6 +169,56 @@ __global__ __launch_bounds__(kEW) void uniform_denoise_kernel(
   if (MODE == kPosterior) {
     const float tot = block_sum(vsum, red);
     if (threadIdx.x == 0) var_part[b * nchunks + blockIdx.x] = tot;
+  }
+}
+
+// LMMSE part 2 and the r1 message as lmmse_epi2_kernel (r1 <- damped), then, from the new r1 in
+// registers, the hard decision of uniform_denoise_kernel<HMODE> with gamma = the damped gamma1 the
+// row kernel wrote: one launch and one pass over r1 instead of two, the same per-element arithmetic.
+template <int HMODE>
+__global__ __launch_bounds__(kEW) void epi2_denoise_kernel(
+    int64_t n, const float* __restrict__ P, int splits, int64_t split_stride, const float* __restrict__ r2,
+    const float* __restrict__ eta2, const float* __restrict__ g2, const float* __restrict__ g1new, float damping,
+    float* __restrict__ r1, const float* __restrict__ gamma, const float* __restrict__ W, int64_t ldw,
+    const float* __restrict__ scale, const float* __restrict__ zero, int64_t G, int64_t gs, int maxq, float tau,
+    uint8_t* __restrict__ q_out, float* __restrict__ x_out, uint4* __restrict__ planes) {
+  static_assert(HMODE == kHardMap || HMODE == kHardRoundMean, "hard decision modes");
+  __shared__ __attribute__((aligned(16))) float s_v[kChunk];
+  const int64_t b = blockIdx.y;
+  const float e2 = eta2[b], gb = g2[b], gn = g1new[b];
+  const float keep = 1.0f - damping;
+  const float mh = -0.5f * gamma[b];
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int64_t j = (int64_t)blockIdx.x * kChunk + e * kEW + threadIdx.x;
+    if (j >= n) continue;
+    const int64_t o = b * n + j;
+    const float d = sum_splits(P, splits, split_stride, o);
+    const float r2v = r2[o];
+    const float x2 = r2v + d;
+    const float rn = (e2 * x2 - gb * r2v) / gn;
+    const float r = damping >= 1.f ? rn : keep * r1[o] + damping * rn;
+    r1[o] = r;
+    const float c = W[b * ldw + j];
+    const float s = grp(scale, b, G, gs, j);
+    const float z = grp(zero, b, G, gs, j);
+    int arg;
+    float mean = 0.f, var = 0.f;
+    denoise_element<HMODE == kHardRoundMean>(r, c, s, z, mh, tau, maxq, arg, mean, var);
+    int q = arg;
+    if (HMODE == kHardRoundMean) {
+      const float sc = s < 1e-12f ? 1e-12f : s;
+      float qf = rintf(mean / sc + z);
+      qf = qf < 0.f ? 0.f : (qf > (float)maxq ? (float)maxq : qf);
+      q = (int)qf;
+    }
+    q_out[o] = (uint8_t)q;
+    x_out[o] = s * ((float)q - z);
+    if (planes) s_v[e * kEW + threadIdx.x] = s * ((float)q - z);
+  }
+  if (planes) {
+    __syncthreads();
+    chunk_planes(planes, n, b, s_v);
   }
 }
 
@@ -329,8 +390,10 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
   int rc;
 
   // hard state + rank-space error of the decision for (r1, g1) -> q_cur, err_cur, status.err_mean
-  auto hard_state = [&](const float* r, const float* g) -> int {
-    if (cfg.final_decision == 1) {
+  // (decided: the denoiser's decision is already in q_cur / xs / planes, from epi2_denoise_kernel)
+  auto hard_state = [&](const float* r, const float* g, bool decided) -> int {
+    if (decided) {
+    } else if (cfg.final_decision == 1) {
       hipLaunchKernelGGL(uniform_denoise_kernel<kHardRoundMean>, eg, eb, 0, stream, r, g, pr.W, pr.ldw,
                          pr.scale, pr.zero, G, pr.group_size, n, pr.maxq, tau, nullptr, nullptr,
                          w.q_cur, w.xs, planes);
@@ -403,7 +466,7 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     MPQ_HIP_TRY(copy_rows(w.r1, n * 4, src, pr.ldw * 4, rows, n * 4, stream));
   }
   // initial hard state = best
-  if ((rc = hard_state(w.r1, g1)) != kOk) return rc;
+  if ((rc = hard_state(w.r1, g1, false)) != kOk) return rc;
   if ((rc = wait_status(mb, hard_seq, hs, stream)) != kOk) return rc;
   double best_err_mean = (double)hs->err_mean;
   std::swap(w.q_cur, w.q_best);
@@ -494,11 +557,18 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
                        eta2, g1new, g1, g1w, w.status);
     MPQ_LAUNCH_CHECK();
     MPQ_HIP_TRY(product(w, w.x1, pr.V, true, kOpVt, rows, n, stream, planes != nullptr));
-    hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.r2, eta2, g2,
-                       g1new, damping, w.r1);
+    // ---- r1 message and the hard state of the new (r1, g1)
+    if (cfg.final_decision == 1) {
+      hipLaunchKernelGGL(epi2_denoise_kernel<kHardRoundMean>, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.r2,
+                         eta2, g2, g1new, damping, w.r1, g1, pr.W, pr.ldw, pr.scale, pr.zero, G, pr.group_size,
+                         pr.maxq, tau, w.q_cur, w.xs, planes);
+    } else {
+      hipLaunchKernelGGL(epi2_denoise_kernel<kHardMap>, eg, eb, 0, stream, n, w.P, w.splits, sstride, w.r2, eta2,
+                         g2, g1new, damping, w.r1, g1, pr.W, pr.ldw, pr.scale, pr.zero, G, pr.group_size, pr.maxq,
+                         tau, w.q_cur, w.xs, planes);
+    }
     MPQ_LAUNCH_CHECK();
-    // ---- hard state of the new (r1, g1)
-    if ((rc = hard_state(w.r1, g1)) != kOk) return rc;
+    if ((rc = hard_state(w.r1, g1, true)) != kOk) return rc;
     std::swap(w.r2, w.r2prev);  // r2_prev <- r2
     std::swap(g2, g2prev);      // gamma2_prev <- gamma2
     has_prev = true;
