@@ -315,8 +315,9 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
     // without best-iterate tracking the row kernel publishes this iteration's status (its EM statistic
     // and alpha2 clips are all the host reads); with it the hard state's row kernel does, after it
     const unsigned st_seq = best_iterate ? 0u : ++mb->seq;
+    // the row kernel also writes the next iteration's working gamma1 (g1w = the damped gamma1)
     hipLaunchKernelGGL(rows_lmmse_kernel, dim3(1), eb, 0, stream, rows, n, n, nchunks, part, g2, damping, eta2,
-                       g1new, g1, nullptr, status, best_iterate ? nullptr : mb->dev(st_seq), st_seq);
+                       g1new, g1, g1w, status, best_iterate ? nullptr : mb->dev(st_seq), st_seq);
     MPQ_LAUNCH_CHECK();
     MPQ_HIP_TRY(prod(x1, V, true, 1, planes != nullptr));
     hipLaunchKernelGGL(lmmse_epi2_kernel, eg, eb, 0, stream, n, P, nsplit, sstride, r2, eta2, g2, g1new, damping,
@@ -334,7 +335,6 @@ extern "C" int mpq_e8p12_vamp_solve_ex(int64_t rows, int64_t n, const float* Wr,
     // r1, gamma1 or the MAP decision the loop keeps, so a stop (which restores the best r1, gamma1
     // and decides again) never reads its results.
     if (it + 1 < iters) {
-      MPQ_HIP_TRY(copy_rows(g1w, 0, g1, 0, 1, rows * 4, stream));
       if ((rc = launch_alpha1(&ahead_seq)) != kOk) return rc;
     }
     if ((rc = wait_status(mb, wait_seq, hs, stream)) != kOk) return rc;
