@@ -852,13 +852,16 @@ hipError_t splitk_reduce(const float* P, int splits, int64_t M, int64_t N, float
 
 bool x6_shape_ok(int64_t N, int64_t K) { return N > 0 && K > 0 && N % 128 == 0 && K % 32 == 0; }
 
-// Split K until the grid holds about two work-groups per CU (512): more splits do not speed the
-// product up and every split is one more partial the epilogues read.  128 x 14336 x 14336: 4 splits,
-// 0.292 ms per product and 8.7 us to read the partials back, against 0.298 ms and 20.7 us with 16.
+// Split K until the grid holds about two work-groups per CU (512) or a K slice would fall below
+// 32 slabs (512): more splits do not speed the product up and every split is one more partial the
+// epilogues read.  128 x 14336 x 14336: 4 splits, 0.292 ms per product and 8.7 us to read the
+// partials back, against 0.298 ms and 20.7 us with 16 (the down_proj layer: 2 splits 1085 ms, 4
+// splits 1053-1062 ms).  128 x 4096 x 4096: 8 splits; a 14336 x 4096 gate_proj layer takes 391 ms
+// against 414 ms with 16 splits, 451 ms with 4 and 619 ms with 2.
 int x6_choose_splits(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = ((M + 127) / 128) * (N / 128);
   int splits = 1;
-  while (splits < 16 && tiles * splits * 2 <= 512 && K % (splits * 2 * 32) == 0 && K / (splits * 2) >= 256)
+  while (splits < 16 && tiles * splits * 2 <= 512 && K % (splits * 2 * 32) == 0 && K / (splits * 2) >= 512)
     splits *= 2;
   return splits;
 }
