@@ -311,9 +311,12 @@ def solve_uniform_rankspace_vamp(W, x_rtn, scale_full, zero_full, maxq, V, Vh, S
     else:
         obs = 1.0 / float((Y_u - _mm(x_rtn, Vs)).square().mean().clamp_min_(1e-12).item())
 
+    # final decision (mpq/solver.py:833-850): the MAP atom, or "round_mean" the posterior mean rounded
+    round_mean = str(cfg.get("final_decision", "map") or "map").strip().lower() == "round_mean"
+
     def hard(r, g):
         post = discrete_uniform_mmse(r, g, scale_full, zero_full, maxq, W, tau)
-        q = nearest_atom_idx(post["map_value"], scale_full, zero_full, maxq)
+        q = nearest_atom_idx(post["mean"] if round_mean else post["map_value"], scale_full, zero_full, maxq)
         xs = dequant_from_q(q, scale_full, zero_full)
         return q, xs, rankspace_error(Y_u, xs, Vs)
 

@@ -145,6 +145,31 @@ def test_vamp_block_matches_oracle(gpu, rotate, bits, packed):
 
 
 @pytest.mark.parametrize("packed", [False, True])
+def test_vamp_block_round_mean_matches_oracle(gpu, packed):
+    """final_decision="round_mean" (mpq/solver.py:833-850): every hard state rounds the posterior mean
+    to the grid instead of taking the MAP atom (the fused LMMSE / hard-decision kernel's second mode).
+    A weak prior (tau 2) and a small gamma1 start keep the posteriors broad, so the two decisions
+    differ (on about 6 % of the codes in the oracle, with other best / stop iterations)."""
+    W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq = _setup_block(128, 512, 4, 128, "vb4", rotate=True)
+    cfg = dict(RECIPE, polish_sweeps=0, final_decision="round_mean", gamma_start=0.01, prior_tau=2.0)
+    q_ref, x_ref, e_ref, rtn_ref, tr = ou.solve_uniform_rankspace_vamp(W, xr, sf, zf, maxq, V, V.T, S, Vs, cfg)
+    cfg_map = dict(cfg, final_decision="map")
+    q_map, _, _, _, _ = ou.solve_uniform_rankspace_vamp(W, xr, sf, zf, maxq, V, V.T, S, Vs, cfg_map)
+    vcfg = UniformVampConfig(**{k: v for k, v in cfg.items()})
+    pk = ops.rankspace_pack(V.to(gpu), Vs.to(gpu)) if packed else None
+    q, x, e, rtn, st = ops.uniform_vamp_solve(W.to(gpu), xr.to(gpu), sg.to(gpu), zg.to(gpu), 128, maxq, V.to(gpu),
+                                              S.to(gpu), Vs.to(gpu), vcfg, want_x=True, packed=pk)
+    agree = float((q.cpu().long() == q_ref.long()).float().mean())
+    differs = float((q_ref.long() != q_map.long()).float().mean())
+    print("round_mean agreement", agree, "oracle codes differing from the MAP decision", differs,
+          "best/stop", st["best_iter"], st["stop_iter"])
+    assert differs > 0  # the two decisions are not the same on this input
+    assert agree >= 0.999
+    assert st["best_iter"] == tr["best_iter"] and st["stop_iter"] == tr["stop_iter"]
+    assert abs(float(e.mean()) - float(e_ref.mean())) <= 5e-3 * float(e_ref.mean())
+
+
+@pytest.mark.parametrize("packed", [False, True])
 def test_vamp_block_gamma_retries_match_oracle(gpu, packed):
     """gamma_start 100: the first denoiser pass finds alpha1 outside (1e-7, 1 - 1e-7) on most rows and
     the loop retries with rescaled gamma1 twice before alpha1 is valid (the oracle's posterior runs
