@@ -303,11 +303,16 @@ def solve_uniform_rankspace_vamp(W, x_rtn, scale_full, zero_full, maxq, V, Vh, S
     em_on = bool(cfg.get("em_obs_precision", True)) and float(cfg.get("obs_precision", 0.0)) <= 0.0
     sweeps = int(cfg.get("polish_sweeps", 3))
     R = S.numel()
-    r1 = x_rtn.clone()
+    # r1 start (mpq/solver.py:472-479): the RTN decision, the float weight or zero
+    init_from = str(cfg.get("init_from", "rtn") or "rtn").strip().lower()
+    r1 = {"rtn": x_rtn, "float": W, "zero": torch.zeros_like(W)}[init_from].clone()
     gamma1 = gamma_start * (0.25 / (W - x_rtn).square().mean(dim=1, keepdim=True).clamp_min_(1e-12))
     Y_u = _mm(W, Vs)
+    requested = float(cfg.get("obs_precision", 0.0))
     if obs_precision_init is not None and obs_precision_init > 0:
         obs = float(obs_precision_init)
+    elif math.isfinite(requested) and requested > 0.0:  # _resolve_obs_precision (mpq/solver.py:147-161)
+        obs = requested
     else:
         obs = 1.0 / float((Y_u - _mm(x_rtn, Vs)).square().mean().clamp_min_(1e-12).item())
 

@@ -144,6 +144,28 @@ def test_vamp_block_matches_oracle(gpu, rotate, bits, packed):
     assert abs(float(e.mean()) - float(e_ref.mean())) <= 5e-3 * float(e_ref.mean())
 
 
+@pytest.mark.parametrize("extra", [dict(init_from="float"), dict(init_from="zero"), dict(em_obs_precision=False),
+                                   dict(obs_precision=50.0), dict(damping=1.0)],
+                         ids=["init_float", "init_zero", "em_off", "obs_fixed", "undamped"])
+def test_vamp_block_config_options_match_oracle(gpu, extra):
+    """The solver's other options (mpq/solver.py:426-830): the r1 start (float weight, zero), EM off,
+    a fixed observation precision, no damping.  Each takes its own trajectory on this input (1-5 %
+    of the codes and the best / stop iterations move against the recipe in the oracle)."""
+    W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq = _setup_block(128, 512, 4, 128, "vb4", rotate=True)
+    cfg = dict(RECIPE, polish_sweeps=0, **extra)
+    q_ref, x_ref, e_ref, rtn_ref, tr = ou.solve_uniform_rankspace_vamp(W, xr, sf, zf, maxq, V, V.T, S, Vs, cfg)
+    vcfg = UniformVampConfig(**{k: v for k, v in cfg.items()})
+    pk = ops.rankspace_pack(V.to(gpu), Vs.to(gpu))
+    q, x, e, rtn, st = ops.uniform_vamp_solve(W.to(gpu), xr.to(gpu), sg.to(gpu), zg.to(gpu), 128, maxq, V.to(gpu),
+                                              S.to(gpu), Vs.to(gpu), vcfg, want_x=True, packed=pk)
+    agree = float((q.cpu().long() == q_ref.long()).float().mean())
+    print(extra, "agreement", agree, "best/stop", st["best_iter"], st["stop_iter"], "obs", st["obs_precision_final"])
+    assert agree >= 0.999
+    assert st["best_iter"] == tr["best_iter"] and st["stop_iter"] == tr["stop_iter"]
+    assert abs(st["obs_precision_final"] - tr["obs_final"]) <= 1e-4 * tr["obs_final"]
+    assert abs(float(e.mean()) - float(e_ref.mean())) <= 5e-3 * float(e_ref.mean())
+
+
 @pytest.mark.parametrize("packed", [False, True])
 def test_vamp_block_round_mean_matches_oracle(gpu, packed):
     """final_decision="round_mean" (mpq/solver.py:833-850): every hard state rounds the posterior mean
