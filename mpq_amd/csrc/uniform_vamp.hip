@@ -448,9 +448,10 @@ int uniform_vamp_solve(const UniformProblem& pr, const float* Vs, const MpqUnifo
     return kNumerical;
   }
   const double rtn_err_mean = (double)hs->err_mean;
+  // the caller's warm start first, then the requested precision (mpq/solver.py:486-489, :147-161)
   double obs;
-  if (cfg.obs_precision > 0.0) obs = cfg.obs_precision;
-  else if (obs_init > 0.0) obs = obs_init;
+  if (obs_init > 0.0) obs = obs_init;
+  else if (cfg.obs_precision > 0.0) obs = cfg.obs_precision;
   else {
     float m = hs->err_sum / (float)(rows * n);  // mean over all rank-space entries
     obs = 1.0 / (double)(m < 1e-12f ? 1e-12f : m);

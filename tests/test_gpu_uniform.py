@@ -145,19 +145,27 @@ def test_vamp_block_matches_oracle(gpu, rotate, bits, packed):
 
 
 @pytest.mark.parametrize("extra", [dict(init_from="float"), dict(init_from="zero"), dict(em_obs_precision=False),
-                                   dict(obs_precision=50.0), dict(damping=1.0)],
-                         ids=["init_float", "init_zero", "em_off", "obs_fixed", "undamped"])
+                                   dict(obs_precision=50.0), dict(obs_precision=50.0, obs_init=200.0),
+                                   dict(damping=1.0)],
+                         ids=["init_float", "init_zero", "em_off", "obs_fixed", "obs_warm_start_first", "undamped"])
 def test_vamp_block_config_options_match_oracle(gpu, extra):
     """The solver's other options (mpq/solver.py:426-830): the r1 start (float weight, zero), EM off,
-    a fixed observation precision, no damping.  Each takes its own trajectory on this input (1-5 %
-    of the codes and the best / stop iterations move against the recipe in the oracle)."""
+    a fixed observation precision (a caller's warm start still comes first, :486-489), no damping.
+    Each takes its own trajectory on this input (1-5 % of the codes and the best / stop iterations
+    move against the recipe in the oracle)."""
     W, Hw, V, S, Vs, sg, zg, sf, zf, xr, maxq = _setup_block(128, 512, 4, 128, "vb4", rotate=True)
+    extra = dict(extra)
+    obs_init = extra.pop("obs_init", None)
     cfg = dict(RECIPE, polish_sweeps=0, **extra)
-    q_ref, x_ref, e_ref, rtn_ref, tr = ou.solve_uniform_rankspace_vamp(W, xr, sf, zf, maxq, V, V.T, S, Vs, cfg)
+    q_ref, x_ref, e_ref, rtn_ref, tr = ou.solve_uniform_rankspace_vamp(W, xr, sf, zf, maxq, V, V.T, S, Vs, cfg,
+                                                                      obs_precision_init=obs_init)
     vcfg = UniformVampConfig(**{k: v for k, v in cfg.items()})
     pk = ops.rankspace_pack(V.to(gpu), Vs.to(gpu))
     q, x, e, rtn, st = ops.uniform_vamp_solve(W.to(gpu), xr.to(gpu), sg.to(gpu), zg.to(gpu), 128, maxq, V.to(gpu),
-                                              S.to(gpu), Vs.to(gpu), vcfg, want_x=True, packed=pk)
+                                              S.to(gpu), Vs.to(gpu), vcfg, want_x=True, packed=pk,
+                                              obs_init=float(obs_init or 0.0))
+    if obs_init:
+        assert st["obs_precision_initial"] == obs_init
     agree = float((q.cpu().long() == q_ref.long()).float().mean())
     print(extra, "agreement", agree, "best/stop", st["best_iter"], st["stop_iter"], "obs", st["obs_precision_final"])
     assert agree >= 0.999
