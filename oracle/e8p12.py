@@ -429,7 +429,11 @@ def solve_e8p12_rankspace_vamp(Wr, hat_init, V, S, grid, cache, cfg, obs_precisi
     Wb = Wr.reshape(B, nb, 8)
     pscale = Wb.abs().amax(dim=-1, keepdim=True).clamp_min(1e-12) if tau > 0 else None
     Y_u = Wr.matmul(Vs)
-    if obs_precision_init is not None and obs_precision_init > 0:
+    # the requested precision first, then the caller's warm start (mpq/solver.py:893-899)
+    requested = float(cfg.get("obs_precision", 0.0))
+    if requested > 0.0:
+        obs = requested
+    elif obs_precision_init is not None and obs_precision_init > 0:
         obs = float(obs_precision_init)
     else:
         obs = 1.0 / float((Y_u - hat_init.matmul(Vs)).square().mean().clamp_min_(1e-12).item())

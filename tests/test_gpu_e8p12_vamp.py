@@ -193,6 +193,37 @@ def test_vamp_gamma_retries_match_oracle(gpu, packed):
     assert r1_rel <= 1e-3, r1_rel
 
 
+@pytest.mark.parametrize("extra", [dict(prior_tau=0.0), dict(em_obs_precision=False), dict(obs_precision=0.1),
+                                   dict(obs_precision=0.1, obs_init=0.5), dict(damping=1.0)],
+                         ids=["no_prior", "em_off", "obs_fixed", "obs_requested_first", "undamped"])
+def test_vamp_config_options_match_oracle(gpu, extra):
+    """The solver's other options (mpq/solver.py:853-1276): no prior, EM off, a fixed observation
+    precision (taken before a caller's warm start in this solver, :893-899), no damping.  Each moves
+    8-49 % of the codes against the recipe in the oracle on this input."""
+    Wr, V, S, hat0 = _e8_case(64, 512, "e8vamp:gpu")
+    grid, cache = _grid_cache()
+    extra = dict(extra)
+    obs_init = extra.pop("obs_init", None)
+    cfg = dict(dict(iters=16, damping=0.5, prior_tau=0.25, polish_sweeps=0), **extra)
+    ref_hat, ref_idx, ref_err, ref_st = oe8.solve_e8p12_rankspace_vamp(Wr, hat0, V, S, grid, cache, cfg,
+                                                                       obs_precision_init=obs_init)
+
+    class Cfg(_Cfg):
+        pass
+
+    for k, v in extra.items():
+        setattr(Cfg, k, v)
+    Vs = V * S.unsqueeze(0)
+    pk = ops.rankspace_pack(V.to(gpu), Vs.to(gpu))
+    idx, hat, err, r1, g1, st = ops.e8p12_vamp_solve(Wr.to(gpu), hat0.to(gpu), V.to(gpu), S.to(gpu), Vs.to(gpu), Cfg,
+                                                     want_state=True, packed=pk, obs_init=float(obs_init or 0.0))
+    agree = float((idx.cpu() == ref_idx).float().mean())
+    print(extra, "agreement", agree, "obs", st["obs_precision_final"], ref_st["obs_final"])
+    assert agree >= 0.999, agree
+    assert abs(st["obs_precision_final"] - ref_st["obs_final"]) <= 2e-3 * ref_st["obs_final"]
+    assert abs(float(err.mean()) - float(ref_err.mean())) <= 2e-3 * float(ref_err.mean())
+
+
 def test_vamp_best_iterate_never_worse_than_its_start(gpu):
     """best_iterate keeps the iterate whose MAP decision has the lowest rank-space error, starting from the
     MAP of the initial state (mpq/solver.py:940-958, 1083-1121)."""
