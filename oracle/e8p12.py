@@ -412,7 +412,8 @@ def gram_block_cd(x, idxs, Y_u, Vs, grid, sweeps, accept_tol=0.0, max_blocks=0, 
 
 
 def solve_e8p12_rankspace_vamp(Wr, hat_init, V, S, grid, cache, cfg, obs_precision_init=None):
-    """mpq/solver.py:853-1276 (best_iterate off, the recipe default); returns (hat, idx, err, stats)."""
+    """mpq/solver.py:853-1276, with best-iterate tracking when cfg["best_iterate"] (off in the recipe);
+    returns (hat, idx, err, stats)."""
     from oracle import uniform as ou
 
     iters = int(cfg.get("iters", 16))
@@ -440,7 +441,23 @@ def solve_e8p12_rankspace_vamp(Wr, hat_init, V, S, grid, cache, cfg, obs_precisi
     r1 = hat_init.clone()
     gamma1 = float(cfg.get("gamma_start", 1.0)) * (0.25 / (Wr - hat_init).square().mean(dim=1, keepdim=True).clamp_min_(1e-12))
     r2_prev = g2_prev = None
-    stats = {"gamma2_invalid": 0, "obs": []}
+    stats = {"gamma2_invalid": 0, "obs": [], "best_iter": -1, "stop_iter": -1}
+    center = Wb.reshape(-1, 8).numpy() if tau > 0 else None
+    scl = pscale.reshape(-1).numpy() if pscale is not None else None
+
+    def map_error_mean(r, g):
+        """mean rank-space error of the MAP decision of (r, g)"""
+        idx_s, _ = map_search(r.reshape(-1, 8).numpy(), g.reshape(-1).numpy(), nb, cache, center=center, scale=scl,
+                              tau=tau)
+        hat_s = grid.index_select(0, torch.from_numpy(idx_s)).view(B, n)
+        return float(ou.rankspace_error(Y_u, hat_s, Vs).mean().item())
+
+    # best iterate (mpq/solver.py:940-958, 1083-1121): keep the state whose MAP decision has the
+    # lowest error, stop at the first iterate that does not improve and restore the best state
+    best_iterate = bool(cfg.get("best_iterate", False))
+    if best_iterate:
+        best_err_mean = map_error_mean(r1, gamma1)
+        best_state = (r1.clone(), gamma1.clone(), None, None, obs)
     for it in range(iters):
         g1w = gamma1
         for attempt in range(retry_steps + 1):
@@ -487,8 +504,16 @@ def solve_e8p12_rankspace_vamp(Wr, hat_init, V, S, grid, cache, cfg, obs_precisi
             r1 = (1.0 - damping) * r1 + damping * r1n
         r2_prev, g2_prev = r2, g2
         stats["obs"].append(obs)
-    center = Wb.reshape(-1, 8).numpy() if tau > 0 else None
-    scl = pscale.reshape(-1).numpy() if pscale is not None else None
+        if best_iterate:
+            cur = map_error_mean(r1, gamma1)
+            if cur + max(1e-10, abs(best_err_mean) * 1e-8) < best_err_mean:
+                best_err_mean = cur
+                best_state = (r1.clone(), gamma1.clone(), r2_prev.clone(), g2_prev.clone(), obs)
+                stats["best_iter"] = it
+            else:
+                r1, gamma1, r2_prev, g2_prev, obs = best_state
+                stats["stop_iter"] = it
+                break
     idx, _ = map_search(r1.reshape(-1, 8).numpy(), gamma1.reshape(-1).numpy(), nb, cache, center=center,
                         scale=scl, tau=tau)
     idx_t = torch.from_numpy(idx).view(B, nb)

@@ -8,7 +8,7 @@ posterior (torch's reduction orders).  The reference runs on its CPU dispatch (e
 The E8P12 functions need a codebook object of class ``E8P12_codebook``; the build's own table
 (mpq_amd/codebook.py) is passed in.
 
-Usage:  python tests/golden/make_golden.py /root/reference [all|refine|udriver]
+Usage:  python tests/golden/make_golden.py /root/reference [all|refine|udriver|options]
 Output: tests/golden/*.npz (inputs and outputs only; no reference code is stored).
 """
 from __future__ import annotations
@@ -242,6 +242,74 @@ def udriver_golden(ref_root: str) -> None:
               "stops", [b["stop_iter"] for b in bst])
 
 
+def options_golden(ref_root: str) -> None:
+    """The VAMP solvers' non-recipe options: the uniform loop with another r1 start, EM off, a fixed
+    observation precision (alone and with a caller's warm start), no damping and the round-mean final
+    decision; the E8P12 loop with best-iterate tracking, without a prior and with a fixed precision."""
+    sys.path.insert(0, ROOT)
+    sys.path.insert(0, ref_root)
+    torch.set_num_threads(1)
+    from mpq.priors.e8p12 import vamp_vector_map_e8p12  # reference
+    from mpq.solver import (  # reference
+        E8P12VampConfig as RefE8Cfg,
+        UniformVampConfig as RefUCfg,
+        solve_e8p12_rankspace_vamp,
+        solve_uniform_rankspace_vamp,
+    )
+
+    from mpq_amd.codebook import E8P12_codebook, grid_numpy
+    from oracle import uniform as ou
+    from tests.uniform_cases import make_layer
+
+    rows, cols, bits = 64, 256, 4
+    W, H = make_layer(rows, cols, tokens=1024, seed_key="golden:options")
+    lam, V, _ = ou.hessian_eigen(H)
+    S = torch.sqrt(lam)
+    Vs = V * S.unsqueeze(0)
+    maxq = 2 ** bits - 1
+    sc, zc = zip(*[ou.gptq_find_params(W[:, g:g + 128], maxq) for g in range(0, cols, 128)])
+    sf = torch.repeat_interleave(torch.cat(sc, 1), 128, dim=1)
+    zf = torch.repeat_interleave(torch.cat(zc, 1), 128, dim=1)
+    xr = sf * (torch.clamp(torch.round(W / sf) + zf, 0, maxq) - zf)
+    out = {"W": W, "H": H, "V": V, "S": S, "scale_full": sf, "zero_full": zf, "x_rtn": xr, "maxq": maxq}
+    variants = {"init_float": (dict(init_from="float"), None), "init_zero": (dict(init_from="zero"), None),
+                "em_off": (dict(em_obs_precision=False), None), "obs_fixed": (dict(obs_precision=50.0), None),
+                "obs_warm_start": (dict(obs_precision=50.0), 200.0), "undamped": (dict(damping=1.0), None),
+                "round_mean": (dict(final_decision="round_mean", gamma_start=0.01, prior_tau=2.0), None)}
+    for name, (extra, obs_init) in variants.items():
+        kw = dict(iters=16, damping=0.5, prior_tau=0.2, polish_sweeps=0, vamp_backend="eager")
+        kw.update(extra)
+        q, x, e, r, st = solve_uniform_rankspace_vamp(W=W, x_rtn=xr, scale_full=sf, zero_full=zf, maxq=maxq, V=V,
+                                                      Vh=V.T.contiguous(), S=S, Vs=Vs, cfg=RefUCfg(**kw),
+                                                      obs_precision_init=obs_init, log_stats=False)
+        out.update({f"u_{name}_q": q, f"u_{name}_best_iter": int(st["best_iter"]),
+                    f"u_{name}_stop_iter": int(st["stop_iter"]),
+                    f"u_{name}_obs_final": float(st["obs_precision_final"])})
+        print("uniform", name, "best/stop", st["best_iter"], st["stop_iter"], "obs", st["obs_precision_final"])
+
+    cb = E8P12_codebook()
+    We, He = make_layer(32, 128, tokens=1024, seed_key="golden:e8options", heavy=True)
+    Wr = We / We.square().mean().sqrt()
+    lamq, Vq, _ = ou.hessian_eigen(He)
+    Sq = torch.sqrt(lamq)
+    Vsq = Vq * Sq.unsqueeze(0)
+    cb_t = torch.from_numpy(grid_numpy())
+    hat0 = cb_t[torch.from_numpy(np.asarray(vamp_vector_map_e8p12(
+        r1_blocks=Wr.view(32, 16, 8), gamma1=torch.ones(32, 1), cb=cb)["map_idxs"]).reshape(-1))].view(32, 128)
+    out.update({"e_Wr": Wr, "e_H": He, "e_V": Vq, "e_S": Sq, "e_hat0": hat0})
+    e_variants = {"best_iterate": dict(best_iterate=True), "no_prior": dict(prior_tau=0.0),
+                  "obs_fixed": dict(obs_precision=0.1)}
+    for name, extra in e_variants.items():
+        ecfg = RefE8Cfg(iters=16, polish_sweeps=0, compile_prior=False, **extra)
+        hat, idx, err, est = solve_e8p12_rankspace_vamp(Wr=Wr, hatWr_init=hat0, cb=cb, V=Vq, Vh=Vq.T.contiguous(),
+                                                        S=Sq, Vs=Vsq, cfg=ecfg, log_stats=False)
+        out.update({f"e_{name}_idx": idx, f"e_{name}_best_iter": int(est["best_iter"]),
+                    f"e_{name}_stop_iter": int(est["stop_iter"]),
+                    f"e_{name}_obs_final": float(est["obs_precision_final"])})
+        print("e8p12", name, "best/stop", est["best_iter"], est["stop_iter"], "obs", est["obs_precision_final"])
+    np.savez_compressed(os.path.join(HERE, "vamp_options.npz"), **_np(out))
+
+
 if __name__ == "__main__":
     ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     part = sys.argv[2] if len(sys.argv) > 2 else "all"
@@ -249,7 +317,10 @@ if __name__ == "__main__":
         refine_golden(ref)
     elif part == "udriver":
         udriver_golden(ref)
+    elif part == "options":
+        options_golden(ref)
     else:
         main(ref)
         refine_golden(ref)
         udriver_golden(ref)
+        options_golden(ref)

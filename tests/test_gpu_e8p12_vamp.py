@@ -194,12 +194,14 @@ def test_vamp_gamma_retries_match_oracle(gpu, packed):
 
 
 @pytest.mark.parametrize("extra", [dict(prior_tau=0.0), dict(em_obs_precision=False), dict(obs_precision=0.1),
-                                   dict(obs_precision=0.1, obs_init=0.5), dict(damping=1.0)],
-                         ids=["no_prior", "em_off", "obs_fixed", "obs_requested_first", "undamped"])
+                                   dict(obs_precision=0.1, obs_init=0.5), dict(damping=1.0),
+                                   dict(best_iterate=True)],
+                         ids=["no_prior", "em_off", "obs_fixed", "obs_requested_first", "undamped", "best_iterate"])
 def test_vamp_config_options_match_oracle(gpu, extra):
     """The solver's other options (mpq/solver.py:853-1276): no prior, EM off, a fixed observation
-    precision (taken before a caller's warm start in this solver, :893-899), no damping.  Each moves
-    8-49 % of the codes against the recipe in the oracle on this input."""
+    precision (taken before a caller's warm start in this solver, :893-899), no damping, and
+    best-iterate tracking (:940-958, 1083-1121: same best / stop iteration as the oracle).  Each
+    moves 8-49 % of the codes against the recipe in the oracle on this input."""
     Wr, V, S, hat0 = _e8_case(64, 512, "e8vamp:gpu")
     grid, cache = _grid_cache()
     extra = dict(extra)
@@ -222,6 +224,8 @@ def test_vamp_config_options_match_oracle(gpu, extra):
     assert agree >= 0.999, agree
     assert abs(st["obs_precision_final"] - ref_st["obs_final"]) <= 2e-3 * ref_st["obs_final"]
     assert abs(float(err.mean()) - float(ref_err.mean())) <= 2e-3 * float(ref_err.mean())
+    if extra.get("best_iterate"):
+        assert st["best_iter"] == ref_st["best_iter"] and st["stop_iter"] == ref_st["stop_iter"]
 
 
 def test_vamp_best_iterate_never_worse_than_its_start(gpu):
