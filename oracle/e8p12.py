@@ -428,7 +428,18 @@ def solve_e8p12_rankspace_vamp(Wr, hat_init, V, S, grid, cache, cfg, obs_precisi
     Vs = V * S.unsqueeze(0)
     Vh = V.T.contiguous()
     Wb = Wr.reshape(B, nb, 8)
-    pscale = Wb.abs().amax(dim=-1, keepdim=True).clamp_min(1e-12) if tau > 0 else None
+    # per-block prior scale (mpq/priors/e8p12.py:48-63): |W|max, rms, mean |W| or 1
+    smode = str(cfg.get("prior_tau_scale_mode", "absmax") or "absmax").strip().lower()
+    if tau <= 0:
+        pscale = None
+    elif smode in ("none", "unit", "legacy"):
+        pscale = torch.ones(Wb.shape[:-1] + (1,), dtype=torch.float32)
+    elif smode in ("rms", "std"):
+        pscale = Wb.square().mean(dim=-1, keepdim=True).sqrt().clamp_min(1e-12)
+    elif smode in ("mean_abs", "l1"):
+        pscale = Wb.abs().mean(dim=-1, keepdim=True).clamp_min(1e-12)
+    else:
+        pscale = Wb.abs().amax(dim=-1, keepdim=True).clamp_min(1e-12)
     Y_u = Wr.matmul(Vs)
     # the requested precision first, then the caller's warm start (mpq/solver.py:893-899)
     requested = float(cfg.get("obs_precision", 0.0))

@@ -245,7 +245,8 @@ def udriver_golden(ref_root: str) -> None:
 def options_golden(ref_root: str) -> None:
     """The VAMP solvers' non-recipe options: the uniform loop with another r1 start, EM off, a fixed
     observation precision (alone and with a caller's warm start), no damping and the round-mean final
-    decision; the E8P12 loop with best-iterate tracking, without a prior and with a fixed precision."""
+    decision; the E8P12 loop with best-iterate tracking, without a prior, with a fixed precision and
+    with the other prior scales (rms, mean |W|, unit)."""
     sys.path.insert(0, ROOT)
     sys.path.insert(0, ref_root)
     torch.set_num_threads(1)
@@ -298,7 +299,9 @@ def options_golden(ref_root: str) -> None:
         r1_blocks=Wr.view(32, 16, 8), gamma1=torch.ones(32, 1), cb=cb)["map_idxs"]).reshape(-1))].view(32, 128)
     out.update({"e_Wr": Wr, "e_H": He, "e_V": Vq, "e_S": Sq, "e_hat0": hat0})
     e_variants = {"best_iterate": dict(best_iterate=True), "no_prior": dict(prior_tau=0.0),
-                  "obs_fixed": dict(obs_precision=0.1)}
+                  "obs_fixed": dict(obs_precision=0.1), "prior_rms": dict(prior_tau_scale_mode="rms"),
+                  "prior_mean_abs": dict(prior_tau_scale_mode="mean_abs"),
+                  "prior_unit": dict(prior_tau_scale_mode="none")}
     for name, extra in e_variants.items():
         ecfg = RefE8Cfg(iters=16, polish_sweeps=0, compile_prior=False, **extra)
         hat, idx, err, est = solve_e8p12_rankspace_vamp(Wr=Wr, hatWr_init=hat0, cb=cb, V=Vq, Vh=Vq.T.contiguous(),

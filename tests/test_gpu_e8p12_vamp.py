@@ -195,8 +195,10 @@ def test_vamp_gamma_retries_match_oracle(gpu, packed):
 
 @pytest.mark.parametrize("extra", [dict(prior_tau=0.0), dict(em_obs_precision=False), dict(obs_precision=0.1),
                                    dict(obs_precision=0.1, obs_init=0.5), dict(damping=1.0),
-                                   dict(best_iterate=True)],
-                         ids=["no_prior", "em_off", "obs_fixed", "obs_requested_first", "undamped", "best_iterate"])
+                                   dict(best_iterate=True), dict(prior_tau_scale_mode="rms"),
+                                   dict(prior_tau_scale_mode="mean_abs"), dict(prior_tau_scale_mode="none")],
+                         ids=["no_prior", "em_off", "obs_fixed", "obs_requested_first", "undamped", "best_iterate",
+                              "prior_rms", "prior_mean_abs", "prior_unit"])
 def test_vamp_config_options_match_oracle(gpu, extra):
     """The solver's other options (mpq/solver.py:853-1276): no prior, EM off, a fixed observation
     precision (taken before a caller's warm start in this solver, :893-899), no damping, and
@@ -217,8 +219,16 @@ def test_vamp_config_options_match_oracle(gpu, extra):
         setattr(Cfg, k, v)
     Vs = V * S.unsqueeze(0)
     pk = ops.rankspace_pack(V.to(gpu), Vs.to(gpu))
+    # the per-block prior scales of the other modes come from the caller, as the solver passes them
+    mode = extra.get("prior_tau_scale_mode")
+    pscale = None
+    if mode is not None:
+        from mpq_amd.priors.e8p12 import prior_scale_from_center
+        rows, n = Wr.shape
+        pscale = prior_scale_from_center(Wr.to(gpu).reshape(rows, n // 8, 8), mode).reshape(-1)
     idx, hat, err, r1, g1, st = ops.e8p12_vamp_solve(Wr.to(gpu), hat0.to(gpu), V.to(gpu), S.to(gpu), Vs.to(gpu), Cfg,
-                                                     want_state=True, packed=pk, obs_init=float(obs_init or 0.0))
+                                                     want_state=True, packed=pk, obs_init=float(obs_init or 0.0),
+                                                     prior_scale=pscale)
     agree = float((idx.cpu() == ref_idx).float().mean())
     print(extra, "agreement", agree, "obs", st["obs_precision_final"], ref_st["obs_final"])
     assert agree >= 0.999, agree

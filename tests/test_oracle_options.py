@@ -6,7 +6,7 @@ Uniform loop (mpq/solver.py:426-830, 64 x 256, 4-bit): r1 started from the float
 (:472-479), EM off, a fixed observation precision alone and with a caller's warm start (the warm
 start wins, :486-489), no damping, and the round-mean final decision (:833-850).  E8P12 loop
 (mpq/solver.py:853-1276, 32 x 128): best-iterate tracking (:940-958, 1083-1121), no prior, a fixed
-observation precision.  Checked: codes, best / stop iteration and the final observation precision."""
+observation precision, the rms / mean |W| / unit prior scales (mpq/priors/e8p12.py:48-63).  Checked: codes, best / stop iteration and the final observation precision."""
 import os
 
 import numpy as np
@@ -23,7 +23,9 @@ UNIFORM = {"init_float": (dict(init_from="float"), None), "init_zero": (dict(ini
            "em_off": (dict(em_obs_precision=False), None), "obs_fixed": (dict(obs_precision=50.0), None),
            "obs_warm_start": (dict(obs_precision=50.0), 200.0), "undamped": (dict(damping=1.0), None),
            "round_mean": (dict(final_decision="round_mean", gamma_start=0.01, prior_tau=2.0), None)}
-E8P12 = {"best_iterate": dict(best_iterate=True), "no_prior": dict(prior_tau=0.0), "obs_fixed": dict(obs_precision=0.1)}
+E8P12 = {"best_iterate": dict(best_iterate=True), "no_prior": dict(prior_tau=0.0), "obs_fixed": dict(obs_precision=0.1),
+         "prior_rms": dict(prior_tau_scale_mode="rms"), "prior_mean_abs": dict(prior_tau_scale_mode="mean_abs"),
+         "prior_unit": dict(prior_tau_scale_mode="none")}
 
 
 def _gold():
