@@ -142,10 +142,14 @@ int64_t mpq_e8p12_vamp_workspace_size(int64_t rows, int64_t n);
  *   prior_scale: rows*n/8 block scales (NULL: absmax of each Wr block)
  *   idx_out: rows x n/8 int64 codeword indices, hat_out rows x n codewords,
  *   err_out (rows), r1_out (rows x n), gamma1_out (rows): optional
- * Waits twice per iteration for `stream` to drain up to a small status block, which a
- * one-thread kernel publishes into mapped pinned host memory (the host spins on a sequence
- * number; after 20 s it falls back to hipStreamSynchronize).  Output copies issued after
- * the last wait stay asynchronous on `stream`.
+ *   obs_init > 0 is the warm start of the observation precision; cfg->obs_precision > 0
+ *   comes before it in this solver (mpq/solver.py:893-899)
+ * Reads two small status blocks per iteration (the denoiser's alpha1 checks, the LMMSE
+ * row statistics), which the row kernels publish into mapped pinned host memory (the host
+ * spins on a sequence number; after 20 s it falls back to hipStreamSynchronize).  The r2
+ * message and first LMMSE product are queued before the first is read, the next
+ * iteration's first denoiser pass before the second.  Output copies issued after the last
+ * wait stay asynchronous on `stream`.
  */
 int mpq_e8p12_vamp_solve(int64_t rows, int64_t n, const float* Wr, const float* hat_init,
                          const float* V, const float* S, const float* Vs, const float* prior_scale,
@@ -476,12 +480,15 @@ int64_t mpq_uniform_vamp_workspace_size(int64_t rows, int64_t n);
  *   W (ldw), x_init: rows x n (x_init = RTN decision, also the gamma1 init)
  *   scale/zero: rows x ceil(n/group_size) group parameters
  *   V, Vs: n x n (full rank), S: n
- *   obs_init > 0 overrides the warm start of the observation precision
+ *   obs_init > 0 is the warm start of the observation precision; it comes before
+ *   cfg->obs_precision (mpq/solver.py:486-489), else the RTN decision's error sets it
  *   q_out (rows x n uint8), x_out (optional), err_out (rows), rtn_err_out (rows, optional)
- * Waits twice per iteration for `stream` to drain up to a small status block, which a
- * one-thread kernel publishes into mapped pinned host memory (the host spins on a sequence
- * number; after 20 s it falls back to hipStreamSynchronize).  Output copies issued after
- * the last wait stay asynchronous on `stream`.
+ * Reads two small status blocks per iteration (the denoiser's alpha1 checks, the hard
+ * state's error), which the row kernels publish into mapped pinned host memory (the host
+ * spins on a sequence number; after 20 s it falls back to hipStreamSynchronize).  The r2
+ * message and first LMMSE product are queued before the first is read, the next
+ * iteration's first denoiser pass before the second.  Output copies issued after the last
+ * wait stay asynchronous on `stream`.
  */
 int mpq_uniform_vamp_solve(int64_t rows, int64_t n, int maxq, const float* W, int64_t ldw,
                            const float* x_init, const float* scale, const float* zero,
