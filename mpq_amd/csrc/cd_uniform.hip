@@ -86,16 +86,22 @@ __global__ __launch_bounds__(64 * kRowsPerWG) void window_kernel(
     float* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ res_norm, float* __restrict__ delta,
     int* __restrict__ accepted) {
   __shared__ float Ts[kWin * kWin];
+  // each wave's per-position constants (x at the window's start, scale, zero, diag), read by the
+  // decision of position p with a wave-uniform LDS address: they do not depend on the decisions
+  // before p, so their reads issue ahead of the sequential chain (a lane broadcast could not)
+  __shared__ float Pc[kRowsPerWG][4][kWin];
   const int64_t blk = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const float* Tb = T + blk * kWin * kWin;
   for (int i = threadIdx.x; i < kWin * kWin; i += blockDim.x) Ts[i] = Tb[i];
-  __syncthreads();
   const int64_t row = blk * block_rows + (int64_t)blockIdx.x * kRowsPerWG + wave;
   int64_t blk_end = (blk + 1) * block_rows;
   if (blk_end > rows) blk_end = rows;
-  if (row >= blk_end) return;
+  if (row >= blk_end) {
+    __syncthreads();  // the tile load's barrier (every wave reaches it)
+    return;
+  }
 
   const int32_t* ord = order + blk * n + w0;
   const bool v0 = lane < wn, v1 = lane + 64 < wn;
@@ -115,15 +121,25 @@ __global__ __launch_bounds__(64 * kRowsPerWG) void window_kernel(
   float res = res_norm[row];
   int acc_count = 0;
   const float one_tol = 1.0f + accept_tol;
+  float (*pc)[kWin] = Pc[wave];
+  pc[0][lane] = x0;
+  pc[0][lane + 64] = x1;
+  pc[1][lane] = s0;
+  pc[1][lane + 64] = s1;
+  pc[2][lane] = z0;
+  pc[2][lane + 64] = z1;
+  pc[3][lane] = dg0;
+  pc[3][lane + 64] = dg1;
+  __syncthreads();  // the tile and the constants
 
   for (int p = 0; p < wn; ++p) {
     const int src = p & 63;
     const bool hi = p >= 64;
     const float rp = bcast(hi ? rhs1 : rhs0, src);
-    const float xp = bcast(hi ? x1 : x0, src);
-    const float sp = bcast(hi ? s1 : s0, src);
-    const float zp = bcast(hi ? z1 : z0, src);
-    const float dp = bcast(hi ? dg1 : dg0, src);
+    const float xp = pc[0][p];
+    const float sp = pc[1][p];
+    const float zp = pc[2][p];
+    const float dp = pc[3][p];
     // the sweep kernel's rule x + rhs / diag, or the torch loop's x + rhs * (1 / diag)
     const float target = recip ? xp + rp * bcast(hi ? di1 : di0, src) : xp + rp / dp;
     float qf = rintf(target / sp + zp);
