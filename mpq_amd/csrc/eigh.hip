@@ -23,7 +23,7 @@
 // Reflector i (LAPACK's H(i) = I - tau_i v_i v_i^T, v_i[0..i] = 0, v_i[i+1] = 1) is stored in
 // row i, entries i+2..n-1 -- by symmetry the same entries LAPACK's lower storage keeps in column i.
 //
-// fp32 with 8192 <= n <= band::kMaxN (use_two_stage) takes the two-stage reduction instead (eigh_band.hip: dense ->
+// fp32 with 1024 <= n <= band::kMaxN (use_two_stage) takes the two-stage reduction instead (eigh_band.hip: dense ->
 // band of half-bandwidth 32 on the MFMA GEMM, band -> tridiagonal by bulge chasing); its stage-1
 // reflectors sit in the rows of A the same way with v_i[i + 32] = 1, and the same compact-WY
 // back-transformation applies them after the bulge-chasing reflectors.
@@ -871,10 +871,11 @@ int back_transform(int64_t n, int64_t off, int64_t nrefl, const SyevdLayout& L, 
 // Two-stage path (fp32): stage 1 to a band of half-bandwidth 32, bulge chasing to tridiagonal
 // form, divide and conquer, then the bulge-chasing reflectors and the stage-1 reflectors applied
 // to the tridiagonal eigenvectors.  The band workspace follows the one-stage layout.
-// Sizes the two-stage path handles, and those where it is the faster path on MI355X (measured:
-// n = 4096 one-stage 73 ms vs two-stage 90 ms; n = 14336 640 ms vs 624 ms).
+// Sizes the two-stage path handles, and those where it is the faster path on MI355X (measured per
+// solve, one-stage vs two-stage: n = 1024 16.3 vs 14.0 ms, 2048 32.1 vs 28.7, 3072 50.0 vs 45.3,
+// 4096 68.9 vs 62.7, 6144 125.3 vs 107.5, 8192 201.8 vs 161.5, 14336 640 vs 402; the same residuals).
 bool two_stage_ok(int64_t n) { return n >= 3 && n <= mpq::band::kMaxN; }
-bool use_two_stage(int64_t n, int elem) { return elem == 4 && n >= 8192 && two_stage_ok(n); }
+bool use_two_stage(int64_t n, int elem) { return elem == 4 && n >= 1024 && two_stage_ok(n); }
 
 int syevd_two_stage(int64_t n, const float* H, float* lam, float* V, float* base, const SyevdLayout& L,
                     hipStream_t stream) {

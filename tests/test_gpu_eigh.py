@@ -38,7 +38,7 @@ def test_syevd_matches_fp64(gpu, n, method):
 
 
 def test_syevd_two_stage_8192(gpu):
-    """Two-stage path (the automatic choice from n = 8192) at a size where stage 1 runs in panel pairs
+    """Two-stage path (the automatic choice from n = 1024) at a size where stage 1 runs in panel pairs
     with 256-row X tiles (255 panels: 127 pairs and a last panel alone) and Q1 in block pairs (64
     blocks of 128 reflectors): eigenvalues against fp64 eigvalsh, residual and orthogonality against
     torch's fp32 eigh, all on the GPU (H = X^T X / 2n with log-normal channel scales)."""
