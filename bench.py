@@ -332,16 +332,16 @@ def e8p12_bench(device, nvec=1 << 24, reps=20, warmup=20):
             "mean_sqerr": float(out["err"].double().mean().item())}
 
 
-def micro_bench(name, device, reps=50):
+def micro_bench(name, device, reps=50, eigh_n=14336):
     """One kernel alone, for rocprofv3 counter runs and kernel timing (``--micro NAME``):
 
     * ``e8p12_posterior``: the E8P12 denoiser (``mpq_e8p12_denoise``) on one config-3 row block,
       128 rows x 2048 columns (32768 8-blocks), with the recipe's prior (centre = the block's
       weights, tau 0.2 absmax) and a VAMP-like message r1 = W + N(0, 1/gamma), gamma = 16;
     * ``e8p12_map``: the nearest-codeword search on the 2^24 vectors of config 1;
-    * ``eigh``: the eigendecomposition (``mpq_syevd``, automatic method: two-stage at this size) of
-      a config-4-sized Hessian, n = 14336, H = X^T X / T with 2n Gaussian tokens of log-normal
-      channel scales;
+    * ``eigh``: the eigendecomposition (``mpq_syevd``, automatic method: two-stage from n = 1024) of
+      a config-4-sized Hessian, n = 14336 (``--micro-n`` for another size, e.g. 4096 for q_proj),
+      H = X^T X / T with 2n Gaussian tokens of log-normal channel scales;
     * ``e8p12_cd``: one gram-metric CD sweep (``mpq_e8p12_cd_polish``) over a config-3 linear of the
       up/gate shape's width, 2048 rows x 2048 columns (256 greedy steps of ``e8_cd_step_kernel``),
       from the nearest-codeword start, Vs from the eigendecomposition of a Student-t Hessian.
@@ -376,7 +376,7 @@ def micro_bench(name, device, reps=50):
     elif name == "eigh":
         from mpq_amd import ops
 
-        n = 14336
+        n = int(eigh_n)
         c = torch.exp(torch.randn(n, device=device, generator=g))
         X = torch.randn(2 * n, n, device=device, generator=g) * c
         H = X.T.matmul(X) / (2 * n)
@@ -638,6 +638,7 @@ def main():
     ap.add_argument("--tokens", type=int, default=128 * 2048)
     ap.add_argument("--micro", default=None,
                     help="time one kernel alone (e8p12_posterior | e8p12_map | eigh | e8p12_cd) and exit; for profiler runs")
+    ap.add_argument("--micro-n", type=int, default=14336, help="matrix size of --micro eigh")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the per-layer solve on a single MI355X; "
@@ -650,7 +651,7 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     if args.micro:
-        print(json.dumps(micro_bench(args.micro, dev)), flush=True)
+        print(json.dumps(micro_bench(args.micro, dev, eigh_n=args.micro_n)), flush=True)
         return
     if args.roofline_only:
         rf = gemm_roofline(14336, dev, reps=3)
